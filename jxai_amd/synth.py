@@ -1,0 +1,236 @@
+"""Seeded synthetic MoE layers and token batches.
+
+One generator feeds the GPU path, the oracle and the golden-vector script, so
+all three see identical bytes.  Everything derives from SplitMix64 streams:
+
+  * sub-seed  = splitmix64(base_seed XOR fnv1a64("<config>/<tensor>"))
+  * uniform   = (u64 >> 11) * 2**-53                      in [0, 1)
+  * normal    = Box-Muller in float64 on (1-u0, u1) pairs, rounded to fp32
+  * fp16 scale= float16(lo + (hi-lo)*u)  (round to nearest even)
+  * bytes     = the little-endian bytes of consecutive u64 outputs
+  * int8      = (byte mod 255) - 127
+
+Weight tensors are produced in the reference's on-disk block layout
+(include/quant.h:10-33), packed over experts the way GGUF stores
+``ffn_{gate,up,down}_exps`` (expert e's slice at e * bytes/E,
+src/transformer.cpp:2166-2185).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import formats as F
+
+BASE_SEED = 20261201
+_GOLD = np.uint64(0x9E3779B97F4A7C15)
+_M1 = np.uint64(0xBF58476D1CE4E5B9)
+_M2 = np.uint64(0x94D049BB133111EB)
+_CHUNK = 1 << 22
+
+
+def splitmix64(seed: int, n: int) -> np.ndarray:
+    """The first ``n`` outputs of SplitMix64 started at ``seed``."""
+    out = np.empty(n, dtype=np.uint64)
+    s = np.uint64(seed & 0xFFFFFFFFFFFFFFFF)
+    tmp = np.empty(min(n, _CHUNK), dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        for lo in range(0, n, _CHUNK):
+            hi = min(n, lo + _CHUNK)
+            z = out[lo:hi]
+            t = tmp[: hi - lo]
+            z[:] = np.arange(lo + 1, hi + 1, dtype=np.uint64)
+            z *= _GOLD
+            z += s
+            np.right_shift(z, np.uint64(30), out=t)
+            z ^= t
+            z *= _M1
+            np.right_shift(z, np.uint64(27), out=t)
+            z ^= t
+            z *= _M2
+            np.right_shift(z, np.uint64(31), out=t)
+            z ^= t
+    return out
+
+
+def _fnv1a64(text: str) -> int:
+    h = 0xCBF29CE484222325
+    for b in text.encode():
+        h ^= b
+        h = (h * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+def sub_seed(config: str, tensor: str, base: int = BASE_SEED) -> int:
+    return int(splitmix64(base ^ _fnv1a64(f"{config}/{tensor}"), 1)[0])
+
+
+def uniform01(seed: int, n: int) -> np.ndarray:
+    return (splitmix64(seed, n) >> np.uint64(11)).astype(np.float64) * (2.0 ** -53)
+
+
+def normal_f32(seed: int, n: int, std: float) -> np.ndarray:
+    m = (n + 1) // 2
+    u = uniform01(seed, 2 * m)
+    r = np.sqrt(-2.0 * np.log(1.0 - u[0::2]))
+    t = 2.0 * math.pi * u[1::2]
+    z = np.empty(2 * m, dtype=np.float64)
+    z[0::2] = r * np.cos(t)
+    z[1::2] = r * np.sin(t)
+    return (std * z[:n]).astype(np.float32)
+
+
+def random_bytes(seed: int, n: int) -> np.ndarray:
+    w = (n + 7) // 8
+    return splitmix64(seed, w).view(np.uint8)[:n].copy()
+
+
+def fp16_uniform(seed: int, n: int, lo: float, hi: float) -> np.ndarray:
+    return (lo + (hi - lo) * uniform01(seed, n)).astype(np.float16)
+
+
+def int8_pm127(seed: int, n: int) -> np.ndarray:
+    """int8 in [-127, 127] as (b mod 255) - 127 of random bytes b, as uint8 bytes."""
+    b = random_bytes(seed, n)
+    np.remainder(b, np.uint8(255), out=b)
+    b += np.uint8(129)  # wraps: t + 129 mod 256 is the two's complement of t - 127
+    return b
+
+
+# ---------------------------------------------------------------------------
+# block-format matrices
+
+
+def quant_matrix(seed: int, qtype: int, rows: int, cols: int,
+                 scale_lo: float = 0.005, scale_hi: float = 0.02) -> np.ndarray:
+    """A [rows][cols] matrix in GGML block layout as raw bytes."""
+    blk, bsz = F.BLOCK[qtype]
+    nb = (cols + blk - 1) // blk
+    nblocks = rows * nb
+    out = np.empty((nblocks, bsz), dtype=np.uint8)
+    if qtype == F.Q4_0:
+        d = fp16_uniform(seed ^ 0x1, nblocks, scale_lo, scale_hi)
+        out[:, 0:2] = d.view(np.uint8).reshape(nblocks, 2)
+        out[:, 2:18] = random_bytes(seed ^ 0x2, nblocks * 16).reshape(nblocks, 16)
+    elif qtype == F.Q8_0:
+        d = fp16_uniform(seed ^ 0x1, nblocks, scale_lo, scale_hi)
+        out[:, 0:2] = d.view(np.uint8).reshape(nblocks, 2)
+        out[:, 2:34] = int8_pm127(seed ^ 0x2, nblocks * 32).reshape(nblocks, 32)
+    elif qtype == F.Q4_K:
+        d = fp16_uniform(seed ^ 0x1, nblocks, scale_lo, scale_hi)
+        dmin = fp16_uniform(seed ^ 0x3, nblocks, scale_lo, scale_hi)
+        out[:, 0:2] = d.view(np.uint8).reshape(nblocks, 2)
+        out[:, 2:4] = dmin.view(np.uint8).reshape(nblocks, 2)
+        out[:, 4:16] = random_bytes(seed ^ 0x4, nblocks * 12).reshape(nblocks, 12)
+        out[:, 16:144] = random_bytes(seed ^ 0x2, nblocks * 128).reshape(nblocks, 128)
+    else:
+        raise ValueError(f"unsupported expert weight type {qtype}")
+    return out.reshape(-1)
+
+
+# ---------------------------------------------------------------------------
+# layer configurations
+
+
+@dataclass(frozen=True)
+class LayerConfig:
+    name: str
+    d_model: int
+    n_experts: int
+    top_k: int
+    d_ff: int
+    wtype: int
+    d_ff_shared: int = 0
+    shared_gate: bool = False
+    zipf_gamma: float = 0.0
+    decode_tokens: tuple = field(default_factory=tuple)
+    describe: str = ""
+
+    @property
+    def has_shared(self) -> bool:
+        return self.d_ff_shared > 0
+
+
+CONFIGS = {
+    "toy": LayerConfig("toy", 512, 8, 2, 1024, F.Q4_0, decode_tokens=(1,),
+                       describe="Toy MoE FFN d512 E8 top-2 F1024 Q4_0"),
+    "qwen15moe": LayerConfig("qwen15moe", 2048, 60, 4, 1408, F.Q4_0, d_ff_shared=5632,
+                             shared_gate=True, decode_tokens=(1, 64),
+                             describe="Qwen1.5-MoE-A2.7B-shaped d2048 E60 top-4 F1408 Q4_0 + shared 5632 (sigmoid gate)"),
+    "mixtral": LayerConfig("mixtral", 4096, 8, 2, 14336, F.Q4_K, decode_tokens=(1, 512, 2048),
+                           describe="Mixtral-8x7B-shaped d4096 E8 top-2 F14336 Q4_K"),
+    "qwen3moe": LayerConfig("qwen3moe", 2048, 128, 8, 768, F.Q8_0, zipf_gamma=0.75,
+                            decode_tokens=(2048,),
+                            describe="Qwen3-30B-A3B-shaped d2048 E128 top-8 F768 Q8_0, Zipf-skewed routing"),
+    "dsv2lite": LayerConfig("dsv2lite", 2048, 64, 6, 1408, F.Q4_K, d_ff_shared=2816,
+                            decode_tokens=(32,),
+                            describe="DeepSeek-V2-Lite-shaped d2048 E64 top-6 F1408 Q4_K + 2x1408 shared"),
+}
+
+
+def zipf_bias(cfg: LayerConfig, seed: int = BASE_SEED) -> np.ndarray:
+    """Per-expert router bias -1.1*gamma*ln(rank_e) with a seeded rank permutation."""
+    keys = splitmix64(sub_seed(cfg.name, "zipf_rank", seed), cfg.n_experts)
+    order = np.argsort(keys, kind="stable")
+    rank = np.empty(cfg.n_experts, dtype=np.int64)
+    rank[order] = np.arange(1, cfg.n_experts + 1)
+    return np.array([-1.1 * cfg.zipf_gamma * math.log(float(r)) for r in rank], dtype=np.float32)
+
+
+@dataclass
+class LayerWeights:
+    cfg: LayerConfig
+    router: np.ndarray              # fp32 [E][d]
+    router_bias: np.ndarray | None  # fp32 [E]
+    gate: np.ndarray                # bytes, [E][F] rows of d
+    up: np.ndarray
+    down: np.ndarray                # bytes, [E][d] rows of F
+    sh_gate: np.ndarray | None = None
+    sh_up: np.ndarray | None = None
+    sh_down: np.ndarray | None = None
+    sh_gate_inp: np.ndarray | None = None  # fp32 [d]
+
+    @property
+    def types(self):
+        t = self.cfg.wtype
+        return t, t, t
+
+
+def make_layer(cfg: LayerConfig, seed: int = BASE_SEED) -> LayerWeights:
+    d, E, Fd = cfg.d_model, cfg.n_experts, cfg.d_ff
+    s = lambda name: sub_seed(cfg.name, name, seed)  # noqa: E731
+    router = normal_f32(s("router"), E * d, 0.02).reshape(E, d)
+    bias = zipf_bias(cfg, seed) if cfg.zipf_gamma > 0 else None
+    gate = quant_matrix(s("gate_exps"), cfg.wtype, E * Fd, d)
+    up = quant_matrix(s("up_exps"), cfg.wtype, E * Fd, d)
+    down = quant_matrix(s("down_exps"), cfg.wtype, E * d, Fd)
+    lw = LayerWeights(cfg, router, bias, gate, up, down)
+    if cfg.has_shared:
+        Fs = cfg.d_ff_shared
+        lw.sh_gate = quant_matrix(s("gate_shexp"), cfg.wtype, Fs, d)
+        lw.sh_up = quant_matrix(s("up_shexp"), cfg.wtype, Fs, d)
+        lw.sh_down = quant_matrix(s("down_shexp"), cfg.wtype, d, Fs)
+        if cfg.shared_gate:
+            lw.sh_gate_inp = normal_f32(s("gate_inp_shexp"), d, 0.02)
+    return lw
+
+
+def make_tokens(cfg: LayerConfig, n: int, seed: int = BASE_SEED) -> np.ndarray:
+    """``n`` post-norm activations ~N(0,1), fp32 [n][d]."""
+    return normal_f32(sub_seed(cfg.name, f"x@{n}", seed), n * cfg.d_model, 1.0).reshape(n, cfg.d_model)
+
+
+def expert_bytes(cfg: LayerConfig) -> int:
+    """gate+up+down bytes of one routed expert."""
+    t = cfg.wtype
+    return 2 * F.matrix_bytes(t, cfg.d_ff, cfg.d_model) + F.matrix_bytes(t, cfg.d_model, cfg.d_ff)
+
+
+def shared_bytes(cfg: LayerConfig) -> int:
+    if not cfg.has_shared:
+        return 0
+    t = cfg.wtype
+    Fs = cfg.d_ff_shared
+    return 2 * F.matrix_bytes(t, Fs, cfg.d_model) + F.matrix_bytes(t, cfg.d_model, Fs)

@@ -1,0 +1,69 @@
+/*
+ * CPU oracle for the MoE expert path -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of the reference engine's CPU arithmetic for the MoE
+ * block (router GEMV, top-k softmax, Q8_0 activation quantization, quantized
+ * gate/up/down dots with SwiGLU, weighted combine, shared expert).  It exists
+ * to check the HIP library: only the test-suite, the smoke check and the
+ * benchmark's CPU-baseline leg may load it.  The product path never calls it.
+ *
+ * Every function names the reference file:line it restates.  fp32 operations
+ * are issued in the reference's order (the AVX2 lane layout of its dot
+ * kernels, or the AVX-512 layout when order == JXO_ORDER_AVX512) with explicit
+ * fmaf(), so results are bit-identical to the reference build.
+ */
+#ifndef JX_MOE_ORACLE_H
+#define JX_MOE_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { JXO_F32 = 0, JXO_Q4_0 = 2, JXO_Q8_0 = 8, JXO_Q4_K = 12 };
+enum { JXO_ORDER_AVX2 = 0, JXO_ORDER_AVX512 = 1 };
+
+typedef struct {
+    int32_t n_experts, top_k, d_model, d_ff;
+    int32_t gate_type, up_type, down_type;
+    const float* router;       /* [E][d] fp32                               */
+    const float* router_bias;  /* [E] fp32 added after the GEMV, or NULL     */
+    const uint8_t* gate;       /* [E][d_ff] rows of d_model, block layout     */
+    const uint8_t* up;
+    const uint8_t* down;       /* [E][d_model] rows of d_ff                  */
+    int32_t d_ff_shared;       /* 0 = no shared expert                       */
+    int32_t sh_gate_type, sh_up_type, sh_down_type;
+    const uint8_t* sh_gate;
+    const uint8_t* sh_up;
+    const uint8_t* sh_down;
+    const float* sh_gate_inp;  /* [d] fp32 sigmoid gate, or NULL             */
+} jxo_moe_desc;
+
+uint16_t jxo_fp32_to_fp16(float f);
+float jxo_fp16_to_fp32(uint16_t h);
+int64_t jxo_row_bytes(int32_t type, int64_t cols);
+void jxo_quantize_row_q8_0(const float* x, uint8_t* blocks, int64_t k);
+void jxo_dequantize_row(int32_t type, const uint8_t* w, float* y, int64_t k);
+float jxo_vec_dot_f32(const float* a, const float* b, int64_t k);
+float jxo_vec_dot_q8(int32_t type, const uint8_t* w, const uint8_t* xq8, int64_t k, int32_t order);
+float jxo_vec_dot_q4_K_f32(const uint8_t* w, const float* y, int64_t k);
+void jxo_matmul_quant_f32(int32_t type, const uint8_t* W, const float* x, float* out,
+                          int64_t rows, int64_t cols, int32_t order);
+void jxo_matmul_swiglu_quant_f32(int32_t gate_type, const uint8_t* Wg, int32_t up_type, const uint8_t* Wu,
+                                 const float* x, float* out, int64_t exp_dim, int64_t cols, int32_t order);
+int32_t jxo_select_experts(const float* logits, int32_t n_experts, int32_t top_k,
+                           int32_t* ids, float* probs);
+/* One MoE block over the tokens listed in token_idx (all n_tok when NULL). */
+int32_t jxo_moe_forward(const jxo_moe_desc* L, const float* x, int32_t n_tok,
+                        const int32_t* token_idx, int32_t n_sel,
+                        float* out, int32_t* topk_ids, float* topk_w, float* logits,
+                        int32_t order);
+void jxo_route(const jxo_moe_desc* L, const float* x, int32_t n_tok,
+               float* logits, int32_t* topk_ids, float* topk_w);
+void jxo_set_threads(int32_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,228 @@
+"""ctypes access to the CPU checkers -- TEST INFRASTRUCTURE ONLY.
+
+``Oracle("port")`` loads oracle/liboracle.so (the C restatement in
+moe_oracle.c); ``Oracle("reference")`` loads oracle/_ref/libjxref.so (the
+reference's own quant.cpp + tier.cpp behind ref_driver.cpp).  Only tests/,
+the smoke check and the benchmark's CPU-baseline leg import this module.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PORT_LIB = os.path.join(HERE, "liboracle.so")
+REF_LIB = os.path.join(HERE, "_ref", "libjxref.so")
+REF_SRC = "/root/reference"
+
+_fp = C.POINTER(C.c_float)
+_u8 = C.POINTER(C.c_uint8)
+_i32 = C.POINTER(C.c_int32)
+
+
+class MoeDesc(C.Structure):
+    _fields_ = [
+        ("n_experts", C.c_int32), ("top_k", C.c_int32), ("d_model", C.c_int32), ("d_ff", C.c_int32),
+        ("gate_type", C.c_int32), ("up_type", C.c_int32), ("down_type", C.c_int32),
+        ("router", _fp), ("router_bias", _fp),
+        ("gate", _u8), ("up", _u8), ("down", _u8),
+        ("d_ff_shared", C.c_int32),
+        ("sh_gate_type", C.c_int32), ("sh_up_type", C.c_int32), ("sh_down_type", C.c_int32),
+        ("sh_gate", _u8), ("sh_up", _u8), ("sh_down", _u8),
+        ("sh_gate_inp", _fp),
+    ]
+
+
+def build(ref: bool = False) -> None:
+    """Compile liboracle.so (and _ref/libjxref.so when the reference tree is present)."""
+    subprocess.run(["make", "-s", "-C", HERE, "liboracle.so"], check=True)
+    if ref and os.path.isdir(os.path.join(REF_SRC, "src")):
+        subprocess.run(["make", "-s", "-C", HERE, "ref", f"REF={REF_SRC}"], check=True)
+
+
+def available(kind: str) -> bool:
+    return os.path.exists(PORT_LIB if kind == "port" else REF_LIB)
+
+
+def _ptr(a, t):
+    return None if a is None else a.ctypes.data_as(t)
+
+
+class Oracle:
+    def __init__(self, kind: str = "port", avx512: bool = False):
+        self.kind = kind
+        path = PORT_LIB if kind == "port" else REF_LIB
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} is not built (make -C oracle{' ref' if kind != 'port' else ''})")
+        self.lib = C.CDLL(path)
+        self.order = 1 if avx512 else 0
+        p = "jxo_" if kind == "port" else "jxr_"
+        self.p = p
+        L = self.lib
+        if kind == "reference":
+            L.jxr_set_avx512.argtypes = [C.c_int32]
+            L.jxr_set_avx512(1 if avx512 else 0)
+        getattr(L, p + "fp32_to_fp16").restype = C.c_uint16
+        getattr(L, p + "fp32_to_fp16").argtypes = [C.c_float]
+        getattr(L, p + "fp16_to_fp32").restype = C.c_float
+        getattr(L, p + "fp16_to_fp32").argtypes = [C.c_uint16]
+        getattr(L, p + "quantize_row_q8_0").argtypes = [_fp, _u8, C.c_int64]
+        getattr(L, p + "dequantize_row").argtypes = [C.c_int32, _u8, _fp, C.c_int64]
+        getattr(L, p + "vec_dot_f32").restype = C.c_float
+        getattr(L, p + "vec_dot_f32").argtypes = [_fp, _fp, C.c_int64]
+        getattr(L, p + "vec_dot_q4_K_f32").restype = C.c_float
+        getattr(L, p + "vec_dot_q4_K_f32").argtypes = [_u8, _fp, C.c_int64]
+        getattr(L, p + "vec_dot_q8").restype = C.c_float
+        getattr(L, p + "select_experts").restype = C.c_int32
+        getattr(L, p + "select_experts").argtypes = [_fp, C.c_int32, C.c_int32, _i32, _fp]
+        getattr(L, p + "moe_forward").restype = C.c_int32
+        if kind == "port":
+            L.jxo_vec_dot_q8.argtypes = [C.c_int32, _u8, _u8, C.c_int64, C.c_int32]
+            L.jxo_matmul_quant_f32.argtypes = [C.c_int32, _u8, _fp, _fp, C.c_int64, C.c_int64, C.c_int32]
+            L.jxo_matmul_swiglu_quant_f32.argtypes = [C.c_int32, _u8, C.c_int32, _u8, _fp, _fp,
+                                                     C.c_int64, C.c_int64, C.c_int32]
+            L.jxo_moe_forward.argtypes = [C.POINTER(MoeDesc), _fp, C.c_int32, _i32, C.c_int32,
+                                          _fp, _i32, _fp, _fp, C.c_int32]
+            L.jxo_route.argtypes = [C.POINTER(MoeDesc), _fp, C.c_int32, _fp, _i32, _fp]
+            L.jxo_set_threads.argtypes = [C.c_int32]
+        else:
+            L.jxr_vec_dot_q8.argtypes = [C.c_int32, _u8, _u8, C.c_int64]
+            L.jxr_matmul_quant_f32.argtypes = [C.c_int32, _u8, _fp, _fp, C.c_int64, C.c_int64]
+            L.jxr_matmul_swiglu_quant_f32.argtypes = [C.c_int32, _u8, C.c_int32, _u8, _fp, _fp,
+                                                     C.c_int64, C.c_int64]
+            L.jxr_moe_forward.argtypes = [C.POINTER(MoeDesc), _fp, C.c_int32, _i32, C.c_int32,
+                                          _fp, _i32, _fp, _fp]
+
+    # -- scalar helpers -------------------------------------------------
+    def fp32_to_fp16(self, f: float) -> int:
+        return getattr(self.lib, self.p + "fp32_to_fp16")(f)
+
+    def fp16_to_fp32(self, h: int) -> float:
+        return getattr(self.lib, self.p + "fp16_to_fp32")(h)
+
+    def quantize_row_q8_0(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros(x.size // 32 * 34, dtype=np.uint8)
+        getattr(self.lib, self.p + "quantize_row_q8_0")(_ptr(x, _fp), _ptr(out, _u8), x.size)
+        return out
+
+    def dequantize_row(self, qtype: int, w: np.ndarray, k: int) -> np.ndarray:
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        out = np.zeros(k, dtype=np.float32)
+        getattr(self.lib, self.p + "dequantize_row")(qtype, _ptr(w, _u8), _ptr(out, _fp), k)
+        return out
+
+    def vec_dot_f32(self, a, b) -> float:
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        b = np.ascontiguousarray(b, dtype=np.float32)
+        return getattr(self.lib, self.p + "vec_dot_f32")(_ptr(a, _fp), _ptr(b, _fp), a.size)
+
+    def vec_dot_q4_K_f32(self, w, y) -> float:
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        y = np.ascontiguousarray(y, dtype=np.float32)
+        return getattr(self.lib, self.p + "vec_dot_q4_K_f32")(_ptr(w, _u8), _ptr(y, _fp), y.size)
+
+    def vec_dot_q8(self, qtype: int, w, xq8, k: int) -> float:
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        xq8 = np.ascontiguousarray(xq8, dtype=np.uint8)
+        if self.kind == "port":
+            return self.lib.jxo_vec_dot_q8(qtype, _ptr(w, _u8), _ptr(xq8, _u8), k, self.order)
+        return self.lib.jxr_vec_dot_q8(qtype, _ptr(w, _u8), _ptr(xq8, _u8), k)
+
+    def matmul_quant_f32(self, qtype: int, W, x, rows: int, cols: int) -> np.ndarray:
+        W = np.ascontiguousarray(W, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros(rows, dtype=np.float32)
+        if self.kind == "port":
+            self.lib.jxo_matmul_quant_f32(qtype, _ptr(W, _u8), _ptr(x, _fp), _ptr(out, _fp), rows, cols, self.order)
+        else:
+            self.lib.jxr_matmul_quant_f32(qtype, _ptr(W, _u8), _ptr(x, _fp), _ptr(out, _fp), rows, cols)
+        return out
+
+    def matmul_swiglu_quant_f32(self, gt: int, Wg, ut: int, Wu, x, exp_dim: int, cols: int) -> np.ndarray:
+        Wg = np.ascontiguousarray(Wg, dtype=np.uint8)
+        Wu = np.ascontiguousarray(Wu, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros(exp_dim, dtype=np.float32)
+        if self.kind == "port":
+            self.lib.jxo_matmul_swiglu_quant_f32(gt, _ptr(Wg, _u8), ut, _ptr(Wu, _u8), _ptr(x, _fp),
+                                                 _ptr(out, _fp), exp_dim, cols, self.order)
+        else:
+            self.lib.jxr_matmul_swiglu_quant_f32(gt, _ptr(Wg, _u8), ut, _ptr(Wu, _u8), _ptr(x, _fp),
+                                                 _ptr(out, _fp), exp_dim, cols)
+        return out
+
+    def select_experts(self, logits, k: int):
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        ids = np.zeros(k, dtype=np.int32)
+        probs = np.zeros(k, dtype=np.float32)
+        r = getattr(self.lib, self.p + "select_experts")(_ptr(logits, _fp), logits.size, k,
+                                                          _ptr(ids, _i32), _ptr(probs, _fp))
+        return ids, probs, r
+
+    # -- MoE block ------------------------------------------------------
+    @staticmethod
+    def desc(lw) -> tuple[MoeDesc, list]:
+        """A MoeDesc over a jxai_amd.synth.LayerWeights (plus the arrays it points into)."""
+        cfg = lw.cfg
+        keep = []
+
+        def P(a, t):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a)
+            keep.append(a)
+            return a.ctypes.data_as(t)
+
+        gt, ut, dt = lw.types
+        D = MoeDesc(cfg.n_experts, cfg.top_k, cfg.d_model, cfg.d_ff, gt, ut, dt,
+                    P(lw.router, _fp), P(lw.router_bias, _fp),
+                    P(lw.gate, _u8), P(lw.up, _u8), P(lw.down, _u8),
+                    cfg.d_ff_shared, gt, ut, dt,
+                    P(lw.sh_gate, _u8), P(lw.sh_up, _u8), P(lw.sh_down, _u8),
+                    P(lw.sh_gate_inp, _fp))
+        return D, keep
+
+    def moe_forward(self, lw, x: np.ndarray, token_idx=None, threads: int = 0):
+        """Run the MoE block for ``token_idx`` (all tokens when None).
+
+        Returns (out [m][d], topk_ids [m][k], topk_w [m][k], logits [m][E])."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        n, d = x.shape
+        cfg = lw.cfg
+        sel = None if token_idx is None else np.ascontiguousarray(token_idx, dtype=np.int32)
+        m = n if sel is None else sel.size
+        out = np.zeros((m, d), dtype=np.float32)
+        ids = np.zeros((m, cfg.top_k), dtype=np.int32)
+        w = np.zeros((m, cfg.top_k), dtype=np.float32)
+        lg = np.zeros((m, cfg.n_experts), dtype=np.float32)
+        D, keep = self.desc(lw)
+        if self.kind == "port":
+            if threads:
+                self.lib.jxo_set_threads(threads)
+            r = self.lib.jxo_moe_forward(C.byref(D), _ptr(x, _fp), n, _ptr(sel, _i32), m,
+                                         _ptr(out, _fp), _ptr(ids, _i32), _ptr(w, _fp), _ptr(lg, _fp), self.order)
+        else:
+            r = self.lib.jxr_moe_forward(C.byref(D), _ptr(x, _fp), n, _ptr(sel, _i32), m,
+                                         _ptr(out, _fp), _ptr(ids, _i32), _ptr(w, _fp), _ptr(lg, _fp))
+        del keep
+        if r != 0:
+            raise RuntimeError(f"{self.kind} moe_forward failed: {r}")
+        return out, ids, w, lg
+
+    def route(self, lw, x: np.ndarray):
+        """Router logits (+bias) and top-k for every token (port only)."""
+        assert self.kind == "port"
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        n = x.shape[0]
+        cfg = lw.cfg
+        lg = np.zeros((n, cfg.n_experts), dtype=np.float32)
+        ids = np.zeros((n, cfg.top_k), dtype=np.int32)
+        w = np.zeros((n, cfg.top_k), dtype=np.float32)
+        D, keep = self.desc(lw)
+        self.lib.jxo_route(C.byref(D), _ptr(x, _fp), n, _ptr(lg, _fp), _ptr(ids, _i32), _ptr(w, _fp))
+        del keep
+        return lg, ids, w

@@ -1,0 +1,146 @@
+"""Write the golden vectors in tests/golden/*.npz.
+
+The expected values come from the reference engine's own arithmetic: its
+src/quant.cpp and src/tier.cpp compiled in place by ``make -C oracle ref``
+(oracle/_ref/libjxref.so), driven through oracle/ref_driver.cpp, which replays
+the MoE block of src/transformer.cpp:2589-2757.  Inputs are the seeded
+synthetics of jxai_amd.synth; each fixture stores SHA-256 digests of its inputs
+so a drift in the generator is reported instead of silently compared.
+
+Run in a container that has the reference tree:
+    python tests/golden/make_golden.py            # AVX2 dot order (MOE_AVX512=0)
+The AVX-512 variant of the toy fixture is produced by a child process, since
+the reference caches MOE_AVX512 on its first dot call.
+"""
+from __future__ import annotations
+
+import hashlib
+import os
+import subprocess
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+
+from jxai_amd import formats as F  # noqa: E402
+from jxai_amd import synth  # noqa: E402
+from oracle.oracle import Oracle, build  # noqa: E402
+
+OUT = os.path.dirname(os.path.abspath(__file__))
+
+# (config, n tokens, tokens whose full output row is stored)
+CASES = [
+    ("toy", 1, [0]),
+    ("qwen15moe", 1, [0]),
+    ("qwen15moe", 64, [0, 17, 63]),
+    ("mixtral", 1, [0]),
+    ("mixtral", 512, [0, 255, 511]),
+    ("mixtral", 2048, [0, 1000, 2047]),
+    ("qwen3moe", 2048, [0, 5, 1024, 2047]),
+    ("dsv2lite", 32, [0, 7, 19, 31]),
+]
+
+
+def digest(*arrays) -> str:
+    h = hashlib.sha256()
+    for a in arrays:
+        if a is not None:
+            h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
+
+
+def layer_digest(lw) -> str:
+    return digest(lw.router, lw.router_bias, lw.gate, lw.up, lw.down,
+                  lw.sh_gate, lw.sh_up, lw.sh_down, lw.sh_gate_inp)
+
+
+def make_case(ref: Oracle, name: str, n: int, rows: list[int], tag: str = "") -> str:
+    cfg = synth.CONFIGS[name]
+    lw = synth.make_layer(cfg)
+    x = synth.make_tokens(cfg, n)
+    # full MoE-block outputs for `rows`, routing for every token (the router is cheap)
+    out, ids_r, w_r, lg_r = ref.moe_forward(lw, x, np.asarray(rows, dtype=np.int32))
+    ids_all = np.zeros((n, cfg.top_k), np.int32)
+    w_all = np.zeros((n, cfg.top_k), np.float32)
+    lg_all = np.zeros((n, cfg.n_experts), np.float32)
+    for t in range(n):
+        logits = ref.matmul_quant_f32(F.F32, lw.router.view(np.uint8).reshape(-1), x[t],
+                                      cfg.n_experts, cfg.d_model)
+        if lw.router_bias is not None:
+            logits = (logits + lw.router_bias).astype(np.float32)
+        i, p, _ = ref.select_experts(logits, cfg.top_k)
+        ids_all[t], w_all[t], lg_all[t] = i, p, logits
+    assert np.array_equal(ids_all[rows], ids_r) and np.array_equal(w_all[rows].view(np.uint32), w_r.view(np.uint32))
+    counts = np.bincount(ids_all.reshape(-1), minlength=cfg.n_experts).astype(np.int32)
+    path = os.path.join(OUT, f"{name}_n{n}{tag}.npz")
+    np.savez_compressed(
+        path,
+        config=name, n=n, rows=np.asarray(rows, np.int32),
+        out=out, topk_ids=ids_all, topk_w=w_all, logits_rows=lg_all[rows], counts=counts,
+        layer_sha256=layer_digest(lw), x_sha256=digest(x),
+    )
+    return path
+
+
+def make_units(ref: Oracle) -> str:
+    """Function-level vectors: fp16 truncation, Q8_0 quantization, block dots."""
+    rng_f = synth.normal_f32(synth.sub_seed("units", "f"), 4096, 3.0)
+    special = np.array([0.0, -0.0, 1.0, -1.0, 65504.0, 65519.99, 65520.0, 1e9, -1e9, 6.1035156e-05,
+                        6.0975552e-05, 5.9604645e-08, 2.9802322e-08, 1e-12, np.inf, -np.inf,
+                        0.33333334, 2.0 / 3.0, 0.1, 1.0009765625, 1.00048828125], np.float32)
+    f = np.concatenate([special, rng_f, rng_f * np.float32(1e-5)]).astype(np.float32)
+    h = np.array([ref.fp32_to_fp16(float(v)) for v in f], np.uint16)
+
+    # Q8_0 activations: random blocks, a zero block, exact .5 ties, one huge block
+    xs = synth.normal_f32(synth.sub_seed("units", "xq"), 32 * 64, 1.0)
+    xs[0:32] = 0.0
+    xs[32:64] = np.arange(32, dtype=np.float32) - 15.5          # amax 15.5 -> ties
+    xs[64:96] = np.linspace(-127.0, 127.0, 32, dtype=np.float32)  # q == x exactly
+    xs[96:128] = xs[96:128] * np.float32(1e4)
+    xq = ref.quantize_row_q8_0(xs)
+
+    dots = {}
+    for qt, cols in ((F.Q4_0, 2048), (F.Q8_0, 2048), (F.Q4_K, 4096), (F.Q4_K, 896)):
+        rows = 16
+        w = synth.quant_matrix(synth.sub_seed("units", f"w{qt}_{cols}"), qt, rows, cols)
+        y = synth.normal_f32(synth.sub_seed("units", f"y{qt}_{cols}"), cols, 1.0)
+        out_q8 = ref.matmul_quant_f32(qt, w, y, rows, cols)
+        yq = ref.quantize_row_q8_0(np.concatenate([y, np.zeros((-cols) % 256, np.float32)]))
+        rb = F.row_bytes(qt, cols)
+        direct = np.array([ref.vec_dot_q8(qt, w[r * rb:(r + 1) * rb], yq, cols) for r in range(rows)], np.float32)
+        dots[f"{qt}_{cols}"] = (w, y, out_q8, direct)
+    # Q4_K fp32-activation dot with a partial super-block (DeepSeek down rows)
+    w14 = synth.quant_matrix(synth.sub_seed("units", "w14"), F.Q4_K, 16, 1408)
+    y14 = synth.normal_f32(synth.sub_seed("units", "y14"), 1408, 1.0)
+    o14 = ref.matmul_quant_f32(F.Q4_K, w14, y14, 16, 1408)
+    sw_g = synth.quant_matrix(synth.sub_seed("units", "swg"), F.Q4_0, 64, 512)
+    sw_u = synth.quant_matrix(synth.sub_seed("units", "swu"), F.Q4_0, 64, 512)
+    sw_x = synth.normal_f32(synth.sub_seed("units", "swx"), 512, 1.0)
+    sw_o = ref.matmul_swiglu_quant_f32(F.Q4_0, sw_g, F.Q4_0, sw_u, sw_x, 64, 512)
+    path = os.path.join(OUT, "units.npz")
+    kw = {}
+    for key, (w, y, o, dd) in dots.items():
+        kw[f"dot_w_{key}"], kw[f"dot_y_{key}"], kw[f"dot_out_{key}"], kw[f"dot_direct_{key}"] = w, y, o, dd
+    np.savez_compressed(path, f=f, h=h, xs=xs, xq=xq, w14=w14, y14=y14, o14=o14,
+                        sw_g=sw_g, sw_u=sw_u, sw_x=sw_x, sw_o=sw_o, **kw)
+    return path
+
+
+def main() -> None:
+    build(ref=True)
+    if "--avx512-child" in sys.argv:
+        ref = Oracle("reference", avx512=True)
+        print(make_case(ref, "toy", 1, [0], tag="_avx512"))
+        print(make_case(ref, "qwen3moe", 2048, [0, 5], tag="_avx512"))
+        return
+    ref = Oracle("reference", avx512=False)
+    print(make_units(ref))
+    for name, n, rows in CASES:
+        print(make_case(ref, name, n, rows))
+    subprocess.run([sys.executable, os.path.abspath(__file__), "--avx512-child"], check=True)
+
+
+if __name__ == "__main__":
+    main()
