@@ -1,0 +1,143 @@
+/*
+ * jxmoe -- MI355X (gfx950) MoE expert path behind a plain C ABI.
+ *
+ * The reference engine runs its MoE block inline in
+ * MoETransformerEngine::forward_token (src/transformer.cpp:2584-2764) on top
+ * of the math API in include/quant.h and the router selection in
+ * include/tier.h.  This header is the boundary that replaces that block:
+ * plain pointers and sizes, integer status codes, a thread-local error
+ * string, no C++ types or exceptions across it.
+ *
+ * Ownership: weights are copied (and repacked) into device memory once by
+ * jx_moe_layer_create; caller buffers are only borrowed for the duration of a
+ * call.  One caller at a time per layer handle (its workspace is reused).
+ */
+#ifndef JXMOE_H
+#define JXMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  Every entry point returns one; JX_OK == 0. */
+enum {
+    JX_OK = 0,
+    JX_ERR_INVALID = 1,      /* bad argument / shape                          */
+    JX_ERR_UNSUPPORTED = 2,  /* tensor type or shape the path does not cover  */
+    JX_ERR_HIP = 3,          /* a HIP runtime call failed                     */
+    JX_ERR_NOMEM = 4,        /* device allocation failed                      */
+    JX_ERR_NODEVICE = 5      /* no gfx950 device / init not done              */
+};
+
+/* GGML tensor type codes, as GGMLType in include/common.h:45-77. */
+enum { JX_TYPE_F32 = 0, JX_TYPE_Q4_0 = 2, JX_TYPE_Q8_0 = 8, JX_TYPE_Q4_K = 12 };
+
+/* jx_moe_forward flags */
+enum {
+    JX_FWD_DEVICE_PTRS = 1u << 0, /* x, out, ids, weights, counts on the device  */
+    JX_FWD_ASYNC = 1u << 1,       /* return after enqueueing (device ptrs only)   */
+    JX_FWD_FORCE_GEMV = 1u << 2,  /* force the decode (dequant-GEMV) regime       */
+    JX_FWD_FORCE_MFMA = 1u << 3   /* force the prefill (int8 MFMA GEMM) regime    */
+};
+
+/* One MoE layer, as bound by bind_tensors (src/transformer.cpp:2142-2186).
+ * Expert tensors are the packed GGUF ffn_{gate,up,down}_exps blocks:
+ * [n_experts][rows][ceil(cols/blk) blocks], expert e at e * bytes / n_experts.
+ * gate/up rows = d_ff, cols = d_model; down rows = d_model, cols = d_ff. */
+typedef struct jx_moe_layer_desc {
+    int32_t n_experts;     /* E        (hp_.n_experts)                          */
+    int32_t top_k;         /* k        (hp_.n_experts_used)                     */
+    int32_t d_model;       /* d        (hp_.dim)                                */
+    int32_t d_ff;          /* F        (hp_.moe_expert_dim)                     */
+    int32_t gate_type, up_type, down_type;  /* Q4_0 / Q8_0 / Q4_K            */
+    const float* router;   /* [E][d] fp32, blk.L.ffn_gate_inp.weight            */
+    const float* router_bias; /* [E] fp32 added to the logits, or NULL          */
+    const void* gate_exps;
+    const void* up_exps;
+    const void* down_exps;
+    int32_t d_ff_shared;   /* 0 = no shared expert (ffn_*_shexp)                */
+    int32_t sh_gate_type, sh_up_type, sh_down_type;
+    const void* sh_gate;
+    const void* sh_up;
+    const void* sh_down;
+    const float* sh_gate_inp; /* [d] fp32 ffn_gate_inp_shexp, or NULL (scale 1) */
+} jx_moe_layer_desc;
+
+typedef struct jx_moe_layer jx_moe_layer;
+
+/* Select and initialise a device.  Replaces nothing in the reference (its
+ * "GPU" init, VulkanComputeBackend::init, src/vulkan_backend.cpp:64-156,
+ * computes nothing).  Fails with JX_ERR_NODEVICE unless the device is gfx950. */
+int jx_moe_init(int32_t device);
+
+/* Upload + repack one layer's router and expert weights (replaces the
+ * per-expert residency of LFRUTierManager::get_resident/admit_expert,
+ * src/tier.cpp:41-122, and PILOT streaming, src/pilot_io.cpp:182-212: every
+ * expert stays resident in HBM). */
+int jx_moe_layer_create(const jx_moe_layer_desc* desc, jx_moe_layer** out);
+void jx_moe_layer_destroy(jx_moe_layer* layer);
+
+/* The MoE block for n_tok tokens (replaces src/transformer.cpp:2589-2757 for
+ * one token at a time; tokens are independent, so a batch is the per-token
+ * block applied to each row):
+ *   x           [n_tok][d] fp32 post-ffn_norm activations
+ *   out         [n_tok][d] fp32 moe_accum (the residual add stays with the caller)
+ *   topk_ids    [n_tok][k] int32 selected experts, descending logit   (or NULL)
+ *   topk_w      [n_tok][k] fp32 softmax weights over the k             (or NULL)
+ *   expert_counts [E] int32 tokens routed to each expert              (or NULL)
+ *   stream      hipStream_t (NULL = default stream)
+ * With CACHE_ROUTE off, ids/order/counts are those of
+ * select_experts_cache_aware (src/tier.cpp:124-198); exact logit ties are
+ * ordered by expert index. */
+int jx_moe_forward(jx_moe_layer* layer, const float* x, int32_t n_tok, float* out, int32_t* topk_ids,
+                   float* topk_w, int32_t* expert_counts, void* stream, uint32_t flags);
+
+/* Router logits of the last forward, [n_tok][E] fp32, copied to host memory
+ * (the reference's router_logits vector, src/transformer.cpp:2589-2594). */
+int jx_moe_last_logits(jx_moe_layer* layer, float* logits_host, int32_t n_tok);
+
+/* Per-kernel-class device time of the forwards run since profiling was
+ * enabled, measured with HIP events on the forward's stream.  names is a
+ * ';'-separated list written into names_buf. */
+int jx_moe_profile(jx_moe_layer* layer, int32_t enable);
+int jx_moe_profile_read(jx_moe_layer* layer, char* names_buf, size_t names_len, double* ms, int64_t* launches,
+                        int32_t max_entries, int32_t* n_entries);
+
+/* ---- math-API drop-ins over a persistent device matrix ------------------ */
+
+/* A single quantized weight matrix [rows][cols] in GGUF block layout, uploaded
+ * and repacked once (the device counterpart of a mapped TensorDescriptor). */
+typedef struct jx_qmatrix jx_qmatrix;
+int jx_qmatrix_create(int32_t type, int64_t rows, int64_t cols, const void* host_blocks, jx_qmatrix** out);
+void jx_qmatrix_destroy(jx_qmatrix* m);
+
+/* out[r] = W[r] . x  (matmul_quant_f32, include/quant.h:336-343;
+ * src/quant.cpp:3895-3922): Q8_0 activations under the reference's rule
+ * (rows >= 8 and supports_q8_activation), fp32 otherwise.  Host pointers. */
+int jx_matmul_quant_f32(jx_qmatrix* W, const float* x, float* out);
+
+/* out[r] = SiLU(Wg[r] . x) * (Wu[r] . x)  (matmul_swiglu_quant_f32,
+ * include/quant.h:354-362; src/quant.cpp:3970-4009).  Host pointers. */
+int jx_matmul_swiglu_quant_f32(jx_qmatrix* Wg, jx_qmatrix* Wu, const float* x, float* out);
+
+/* quantize_row_q8_0 (include/quant.h:112; src/quant.cpp:1029-1045) on the
+ * device: x [k] fp32 -> k/32 blocks of 34 bytes (fp16 d + 32 int8).  Host pointers. */
+int jx_quantize_row_q8_0(const float* x, void* blocks, int64_t k);
+
+/* ---- device buffers (plumbing for callers without their own allocator) -- */
+int jx_dev_alloc(size_t bytes, void** ptr);
+int jx_dev_free(void* ptr);
+int jx_memcpy_htod(void* dst, const void* src, size_t bytes);
+int jx_memcpy_dtoh(void* dst, const void* src, size_t bytes);
+int jx_device_synchronize(void);
+
+/* Last error message of the calling thread ("" if none). */
+const char* jx_moe_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* JXMOE_H */

@@ -1,0 +1,98 @@
+// Device-side helpers shared by the MoE expert-path kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace jx {
+
+enum : int { T_F32 = 0, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12 };
+
+constexpr int WAVE = 64;
+constexpr int ROWS_PER_TILE = 32;   // weight rows per repacked tile (= one MFMA M/N edge)
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// ---------------------------------------------------------------- numerics
+
+// fp32 -> fp16 bits, mantissa truncated (the store rule of the reference's
+// Q8_0 activation scale, src/quant.cpp:909-925): subnormal results shift,
+// results below 2^-24 become signed zero, |f| >= 2^16 (and inf/NaN) become
+// signed infinity.
+__device__ __forceinline__ uint32_t f32_to_f16_trunc(float f) {
+    const uint32_t b = __float_as_uint(f);
+    const uint32_t sign = (b >> 16) & 0x8000u;
+    const int e = (int)((b >> 23) & 0xFFu) - 112;
+    uint32_t m = b & 0x7FFFFFu;
+    if (e <= 0) {
+        if (e < -10) return sign;
+        m |= 0x800000u;
+        return sign | (m >> (uint32_t)(14 - e));
+    }
+    if (e >= 31) return sign | 0x7C00u;
+    return sign | ((uint32_t)e << 10) | (m >> 13);
+}
+
+// Exact fp16 -> fp32 with integer ops only (independent of the fp16
+// denormal mode).
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1Fu;
+    const uint32_t m = h & 0x3FFu;
+    if (e == 0) {
+        const float v = (float)m * 0x1p-24f;
+        return sign ? -v : v;
+    }
+    if (e == 31) return __uint_as_float(sign | 0x7F800000u | (m << 13));
+    return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+// Round half away from zero (C roundf), exact for every finite input.
+__device__ __forceinline__ float round_away(float v) {
+    const float t = __builtin_truncf(v);
+    const float fr = v - t;  // exact
+    return (__builtin_fabsf(fr) >= 0.5f) ? t + __builtin_copysignf(1.0f, v) : t;
+}
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) {
+    return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+// 6-bit (scale, min) j of a Q4_K super-block header (layout of
+// include/quant.h:28-33, unpacking as get_scale_min_k4, quant.cpp:1107-1115).
+__device__ __forceinline__ void q4k_scale_min(int j, const uint8_t* s, int& sc, int& mn) {
+    if (j < 4) {
+        sc = s[j] & 63;
+        mn = s[j + 4] & 63;
+    } else {
+        sc = (s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4);
+        mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+// ---------------------------------------------------------------- wave ops
+__device__ __forceinline__ float wave_max32(float v) {
+    // max over the 32 lanes of each half-wave (order-independent)
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ int wave_sum32i(int v) {
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Non-temporal 16-byte load for weights streamed exactly once.
+__device__ __forceinline__ uint4 ld_stream16(const void* p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+}  // namespace jx

@@ -1,0 +1,100 @@
+// Kernel argument blocks and host-side launchers of the MoE expert path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace jx {
+
+// One projection (gate, up or down) of every expert, repacked in HBM into
+// tiles of 32 rows so a wave's 32 lanes read 32 rows' 16-byte chunks of the
+// same K-block as one contiguous 512-byte run:
+//   Q4_0  qs  [e][rt][b][32 rows][16 B]           sc  [e][rt][b][32] fp16 d
+//   Q8_0  qs  [e][rt][b][2 halves][32 rows][16 B]  sc  [e][rt][b][32] fp16 d
+//   Q4_K  qs  [e][rt][sb][4 pairs][2 halves][32 rows][16 B]
+//         sc  [e][rt][sb][32 rows][16 B]  = (d, dmin, scales[12]) headers
+//         kt  [e][rt][sb][8 sub-blocks][32 rows] float2 (d*sc, dmin*m)
+// Byte totals of qs+sc equal the GGUF tensor (18/34/144 B per block); kt is a
+// decoded copy of the Q4_K scales used only by the MFMA prefill kernels.
+struct QMat {
+    int type = 0;
+    int rows = 0;       // per expert, multiple of 32
+    int cols = 0;       // K
+    int nrt = 0;        // rows / 32
+    int nkb = 0;        // K-units: 32-blocks (Q4_0/Q8_0) or 256-super-blocks (Q4_K)
+    const uint8_t* qs = nullptr;
+    const uint8_t* sc = nullptr;
+    const float2* kt = nullptr;
+    size_t qs_es = 0, sc_es = 0, kt_es = 0;  // per-expert strides (bytes, bytes, float2s)
+    int n_mats = 0;     // experts held
+};
+
+// Q8_0 activations on the device: q [rows][K] int8, s [rows][K/32] = (fp16-truncated
+// scale as fp32, sum of the 32 quants as fp32).
+struct ActQ8 {
+    int8_t* q = nullptr;
+    float2* s = nullptr;
+    int K = 0;
+};
+
+// Token -> expert grouping produced by the dispatch kernel.
+struct Groups {
+    const int* counts = nullptr;  // [E]
+    const int* offs = nullptr;    // [E+1]
+    const int* act = nullptr;     // [E] active experts, increasing id
+    const int* n_act = nullptr;   // [1]
+    const int* pair_f = nullptr;  // [P] sorted pair -> flat index t*k + s
+    const int4* tiles = nullptr;  // [T] (expert, first pair, pair count, 0) MFMA tiles
+    const int* n_tiles = nullptr; // [1]
+    int top_k = 1;
+    int identity = 0;             // shared expert: pair p is token p, one group of n_tok
+    int n_tok = 0;
+};
+
+constexpr int MFMA_BN = 32;  // pairs per MFMA tile
+
+struct RouteArgs {
+    const float* x;        // [n][d]
+    int n, d, E, k;
+    const float* router;   // [E][d]
+    const float* bias;     // [E] or null
+    const float* shgate;   // [d] or null
+    ActQ8 xq;              // out: Q8_0 of x
+    int* ids;              // [n][k]
+    float* probs;          // [n][k]
+    float* shscale;        // [n]
+    float* logits;         // [n][E] or null
+};
+
+void launch_route(const RouteArgs& a, hipStream_t st);
+void launch_dispatch(const int* ids, int nk, int E, int top_k, int* counts, int* offs, int* act, int* n_act,
+                     int* pair_f, int* pos_of, int4* tiles, int* n_tiles, hipStream_t st);
+
+// Decode regime: gate+up dequant-GEMV with SwiGLU and Q8_0 re-quantization.
+// Output rows are sorted pairs (routed) or tokens (shared).
+void launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots,
+                        int tb, ActQ8 hq, float* hf, hipStream_t st);
+// Decode regime: down projection over Q8_0 (hq) or fp32 (hf) activations into
+// y[slice][pair][d]; ksplit slices of K are summed by the combine kernel.
+void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp,
+                      int slots, int tb, int ksplit, float* y, size_t y_slice, hipStream_t st);
+// Prefill regime: int8 MFMA grouped GEMMs over the dispatch tile table.
+void launch_mfma_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int tiles_ub,
+                        ActQ8 hq, float* hf, hipStream_t st);
+void launch_mfma_down(const QMat& dn, const ActQ8& hq, const Groups& grp, int tiles_ub, float* y,
+                      hipStream_t st);
+
+// out[t] = sum_s p[t][s] * y[pos(t,s)] (+ shscale[t] * ysh[t]), fma in selection order.
+void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, int ysl,
+                    size_t y_slice, const float* ysh, int shsl, size_t ysh_slice, const float* shscale,
+                    float* out, hipStream_t st);
+
+// Q8_0 of rows x K fp32 (row-major, K % 32 == 0).
+void launch_quantize_q8(const float* x, int rows, int K, ActQ8 out, hipStream_t st);
+
+// Repack a GGUF block matrix set [n_mats][rows][cols] (already on the device
+// as raw bytes) into the QMat layout.
+void launch_repack(const uint8_t* raw, QMat m, uint8_t* qs, uint8_t* sc, float2* kt, hipStream_t st);
+
+}  // namespace jx

@@ -1,0 +1,328 @@
+// Routing side of the MoE expert path: router GEMV + top-k softmax + Q8_0
+// activation quantization (one fused kernel), token->expert dispatch, the
+// weighted combine, and the one-time weight repack.
+#include "jxmoe_device.h"
+#include "jxmoe_kernels.h"
+
+namespace jx {
+
+constexpr int ROUTE_THREADS = 512;
+constexpr int MAX_E = 512;
+constexpr int MAX_K = 32;
+
+// One block per token.
+//  1. x -> LDS.
+//  2. Q8_0 of x, 32 lanes per block (quantize_row_q8_0, src/quant.cpp:1029-1045):
+//     amax, d = amax/127 (IEEE division), id = 1/d, q = clamp(round-half-away(x*id)),
+//     stored scale = truncated fp16 of d; the block sum of q rides along for the
+//     Q4_0 (-8 offset) and Q4_K (min) terms.
+//  3. Router logits in vec_dot_f32's exact fp32 order (src/quant.cpp:2756-2778):
+//     16 lanes per expert, lane j runs the FMA chain over elements 16i+j (lanes
+//     0-7 are the reference's acc0, 8-15 its acc1), then acc0+acc1, the optional
+//     8-element pass, the sequential sum of 8 lanes and the scalar tail.  Four
+//     experts per 16-lane group run interleaved for ILP.  The shared-expert gate
+//     vector (transformer.cpp:2748-2751) is one more row of the same GEMV.
+//  4. Top-k by rank counting (descending logit, ties by index) and softmax over
+//     the k selected logits (select_experts_cache_aware, src/tier.cpp:144-188).
+__global__ void __launch_bounds__(ROUTE_THREADS) k_route(RouteArgs a) {
+    extern __shared__ float xs[];  // d floats
+    __shared__ float lg[MAX_E];
+    __shared__ int sel[MAX_K];
+    __shared__ float shl;
+    const int t = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int d = a.d;
+    const float* x = a.x + (size_t)t * d;
+    for (int i = tid; i < d; i += ROUTE_THREADS) xs[i] = x[i];
+    // every selection slot holds a valid expert even if NaN logits break the ranking
+    if (tid < a.k) sel[tid] = tid;
+    __syncthreads();
+
+    // -- Q8_0 of x
+    {
+        const int lane = tid & 63, wave = tid >> 6, half = lane >> 5, l32 = lane & 31;
+        const int nb = d / 32;
+        for (int bb = wave * 2; bb < nb; bb += (ROUTE_THREADS / 64) * 2) {
+            const int b = bb + half;
+            const bool ok = b < nb;
+            const float v = ok ? xs[b * 32 + l32] : 0.0f;
+            const float amax = wave_max32(__builtin_fabsf(v));
+            const float dd = amax / 127.0f;
+            const float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
+            float r = round_away(v * id);
+            r = fminf(fmaxf(r, -127.0f), 127.0f);
+            const int q = (int)r;
+            const int s = wave_sum32i(q);
+            if (ok) {
+                a.xq.q[(size_t)t * d + b * 32 + l32] = (int8_t)q;
+                if (l32 == 0) a.xq.s[(size_t)t * nb + b] = make_float2(f16_to_f32(f32_to_f16_trunc(dd)), (float)s);
+            }
+        }
+    }
+
+    // -- router GEMV, exact vec_dot_f32 order
+    {
+        const int grp = tid >> 4, j = tid & 15, ngrp = ROUTE_THREADS / 16;
+        const int nrows = a.E + (a.shgate ? 1 : 0);
+        const int d16 = (d / 16) * 16;
+        const bool has8 = (d - d16) >= 8;
+        for (int base = 0; base < nrows; base += ngrp * 4) {
+            const float* w[4];
+            bool ok[4];
+            float acc[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int e = base + c * ngrp + grp;
+                ok[c] = e < nrows;
+                w[c] = ok[c] ? (e < a.E ? a.router + (size_t)e * d : a.shgate) : a.router;
+                acc[c] = 0.0f;
+            }
+#pragma unroll 4
+            for (int i = 0; i < d16; i += 16) {
+                const float xv = xs[i + j];
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (ok[c]) acc[c] = __builtin_fmaf(w[c][i + j], xv, acc[c]);
+            }
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float hi = __shfl_down(acc[c], 8, 16);
+                float v = acc[c] + hi;  // acc0[j] + acc1[j] for j < 8
+                if (has8 && ok[c] && j < 8) v = __builtin_fmaf(w[c][d16 + j], xs[d16 + j], v);
+                float s = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) s += __shfl(v, q, 16);
+                for (int i = d16 + (has8 ? 8 : 0); i < d; ++i)
+                    if (ok[c]) s = __builtin_fmaf(w[c][i], xs[i], s);
+                const int e = base + c * ngrp + grp;
+                if (j == 0 && ok[c]) {
+                    if (e < a.E) lg[e] = a.bias ? s + a.bias[e] : s;
+                    else shl = s;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // -- top-k by rank
+    for (int e = tid; e < a.E; e += ROUTE_THREADS) {
+        const float le = lg[e];
+        int rank = 0;
+        for (int f = 0; f < a.E; ++f) {
+            const float lf = lg[f];
+            rank += (lf > le) || (lf == le && f < e);
+        }
+        if (rank < a.k) sel[rank] = e;
+        if (a.logits) a.logits[(size_t)t * a.E + e] = le;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const int k = a.k;
+        float p[MAX_K];
+        float mx = lg[sel[0]];
+        for (int i = 1; i < k; ++i) mx = fmaxf(mx, lg[sel[i]]);
+        float sum = 0.0f;
+        for (int i = 0; i < k; ++i) {
+            p[i] = expf(lg[sel[i]] - mx);
+            sum += p[i];
+        }
+        const float inv = (sum > 0.0f) ? 1.0f / sum : 1.0f / (float)k;
+        for (int i = 0; i < k; ++i) {
+            a.ids[(size_t)t * k + i] = sel[i];
+            a.probs[(size_t)t * k + i] = p[i] * inv;
+        }
+        if (a.shscale) a.shscale[t] = a.shgate ? 1.0f / (1.0f + expf(-shl)) : 1.0f;
+    }
+}
+
+void launch_route(const RouteArgs& a, hipStream_t st) {
+    hipLaunchKernelGGL(k_route, dim3(a.n), dim3(ROUTE_THREADS), (size_t)a.d * sizeof(float), st, a);
+}
+
+// One block per expert.  Every block builds the full per-expert histogram in
+// LDS (no global atomics, nothing to clear between calls), derives its pair
+// offset, MFMA tile offset and active-list slot, then writes the positions of
+// its (token, slot) pairs in flat order -- a stable counting sort, so tokens
+// keep their order inside each expert.
+constexpr int DISPATCH_THREADS = 256;
+
+__global__ void __launch_bounds__(DISPATCH_THREADS)
+k_dispatch(const int* ids, int nk, int E, int* counts, int* offs, int* act, int* n_act, int* pair_f, int* pos_of,
+           int4* tiles, int* n_tiles) {
+    extern __shared__ int hist[];
+    __shared__ int wtot[DISPATCH_THREADS / 64];
+    __shared__ int s_off, s_toff;
+    const int e = blockIdx.x;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < E; i += DISPATCH_THREADS) hist[i] = 0;
+    __syncthreads();
+    for (int f = tid; f < nk; f += DISPATCH_THREADS) atomicAdd(&hist[ids[f]], 1);
+    __syncthreads();
+    if (tid == 0) {
+        int off = 0, toff = 0, na = 0;
+        for (int i = 0; i < e; ++i) {
+            off += hist[i];
+            toff += (hist[i] + MFMA_BN - 1) / MFMA_BN;
+            na += hist[i] > 0;
+        }
+        s_off = off;
+        s_toff = toff;
+        const int c = hist[e];
+        counts[e] = c;
+        offs[e] = off;
+        if (c > 0) act[na] = e;
+        if (e == E - 1) {
+            offs[E] = off + c;
+            *n_act = na + (c > 0);
+            *n_tiles = toff + (c + MFMA_BN - 1) / MFMA_BN;
+        }
+    }
+    __syncthreads();
+    const int cnt = hist[e];
+    const int off = s_off;
+    for (int i = tid; i * MFMA_BN < cnt; i += DISPATCH_THREADS)
+        tiles[s_toff + i] = make_int4(e, off + i * MFMA_BN, min(MFMA_BN, cnt - i * MFMA_BN), 0);
+    if (cnt == 0) return;
+    const int lane = tid & 63, wave = tid >> 6;
+    int run = 0;
+    for (int base = 0; base < nk; base += DISPATCH_THREADS) {
+        const int f = base + tid;
+        const bool pred = f < nk && ids[f] == e;
+        const unsigned long long m = __ballot(pred);
+        const int lp = __popcll(m & ((1ull << lane) - 1ull));
+        if (lane == 0) wtot[wave] = __popcll(m);
+        __syncthreads();
+        int woff = 0, tot = 0;
+        for (int w = 0; w < DISPATCH_THREADS / 64; ++w) {
+            woff += (w < wave) ? wtot[w] : 0;
+            tot += wtot[w];
+        }
+        if (pred) {
+            const int p = off + run + woff + lp;
+            pair_f[p] = f;
+            pos_of[f] = p;
+        }
+        run += tot;
+        __syncthreads();
+    }
+}
+
+void launch_dispatch(const int* ids, int nk, int E, int top_k, int* counts, int* offs, int* act, int* n_act,
+                     int* pair_f, int* pos_of, int4* tiles, int* n_tiles, hipStream_t st) {
+    (void)top_k;
+    hipLaunchKernelGGL(k_dispatch, dim3(E), dim3(DISPATCH_THREADS), (size_t)E * sizeof(int), st, ids, nk, E,
+                       counts, offs, act, n_act, pair_f, pos_of, tiles, n_tiles);
+}
+
+// MoE combine (transformer.cpp:2728-2730 and 2752-2754): starting from 0, for
+// each selected expert in descending-logit order acc = fma(p, y, acc), then
+// acc = fma(shared_scale, y_shared, acc).  Split-K slices of y are summed
+// first, in slice order.
+__global__ void __launch_bounds__(256)
+k_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, int ysl, size_t y_slice,
+          const float* ysh, int shsl, size_t ysh_slice, const float* shscale, float* out) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)n * d) return;
+    const int t = (int)(idx / d), i = (int)(idx % d);
+    float acc = 0.0f;
+    for (int s = 0; s < k; ++s) {
+        const size_t p = (size_t)pos_of[(size_t)t * k + s];
+        float v = y[p * d + i];
+        for (int sl = 1; sl < ysl; ++sl) v = v + y[sl * y_slice + p * d + i];
+        acc = __builtin_fmaf(probs[(size_t)t * k + s], v, acc);
+    }
+    if (ysh) {
+        float v = ysh[(size_t)t * d + i];
+        for (int sl = 1; sl < shsl; ++sl) v = v + ysh[sl * ysh_slice + (size_t)t * d + i];
+        acc = __builtin_fmaf(shscale[t], v, acc);
+    }
+    out[idx] = acc;
+}
+
+void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, int ysl,
+                    size_t y_slice, const float* ysh, int shsl, size_t ysh_slice, const float* shscale,
+                    float* out, hipStream_t st) {
+    const size_t tot = (size_t)n * d;
+    hipLaunchKernelGGL(k_combine, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, n, d, k, probs, pos_of, y,
+                       ysl, y_slice, ysh, shsl, ysh_slice, shscale, out);
+}
+
+// Q8_0 of `rows` rows of K fp32 values (quantize_row_q8_0, src/quant.cpp:1029-1045),
+// one 32-block per half-wave.
+__global__ void __launch_bounds__(256) k_quant_q8(const float* x, int rows, int K, ActQ8 out) {
+    const int nb = K / 32;
+    const size_t gid = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int half = (threadIdx.x >> 5) & 1, l32 = threadIdx.x & 31;
+    const size_t blk = gid * 2 + half;
+    const bool ok = blk < (size_t)rows * nb;
+    const float v = ok ? x[blk * 32 + l32] : 0.0f;
+    const float amax = wave_max32(__builtin_fabsf(v));
+    const float dd = amax / 127.0f;
+    const float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
+    float r = round_away(v * id);
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    const int q = (int)r;
+    const int s = wave_sum32i(q);
+    if (ok) {
+        out.q[blk * 32 + l32] = (int8_t)q;
+        if (l32 == 0) out.s[blk] = make_float2(f16_to_f32(f32_to_f16_trunc(dd)), (float)s);
+    }
+}
+
+void launch_quantize_q8(const float* x, int rows, int K, ActQ8 out, hipStream_t st) {
+    const size_t blocks = (size_t)rows * (K / 32);
+    const size_t waves = (blocks + 1) / 2;
+    hipLaunchKernelGGL(k_quant_q8, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, x, rows, K, out);
+}
+
+// One thread per (matrix, row, K-unit): scatter a GGUF block into the tile
+// layout described in jxmoe_kernels.h.
+__global__ void __launch_bounds__(256) k_repack(const uint8_t* raw, QMat m, uint8_t* qs, uint8_t* sc, float2* kt) {
+    const size_t units = (size_t)m.n_mats * m.rows * m.nkb;
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= units) return;
+    const int kb = (int)(idx % m.nkb);
+    const size_t er = idx / m.nkb;  // e*rows + r
+    const int r = (int)(er % m.rows);
+    const int e = (int)(er / m.rows);
+    const int rt = r / ROWS_PER_TILE, mm = r % ROWS_PER_TILE;
+    const size_t tile = ((size_t)e * m.nrt + rt) * m.nkb + kb;
+    if (m.type == T_Q4_0) {
+        const uint8_t* src = raw + idx * 18;
+        uint8_t* dq = qs + (tile * 32 + mm) * 16;
+        for (int i = 0; i < 16; ++i) dq[i] = src[2 + i];
+        sc[(tile * 32 + mm) * 2 + 0] = src[0];
+        sc[(tile * 32 + mm) * 2 + 1] = src[1];
+    } else if (m.type == T_Q8_0) {
+        const uint8_t* src = raw + idx * 34;
+        for (int h = 0; h < 2; ++h) {
+            uint8_t* dq = qs + ((tile * 2 + h) * 32 + mm) * 16;
+            for (int i = 0; i < 16; ++i) dq[i] = src[2 + 16 * h + i];
+        }
+        sc[(tile * 32 + mm) * 2 + 0] = src[0];
+        sc[(tile * 32 + mm) * 2 + 1] = src[1];
+    } else {  // Q4_K
+        const uint8_t* src = raw + idx * 144;
+        uint8_t* dh = sc + (tile * 32 + mm) * 16;
+        for (int i = 0; i < 16; ++i) dh[i] = src[i];
+        for (int p = 0; p < 4; ++p)
+            for (int h = 0; h < 2; ++h) {
+                uint8_t* dq = qs + (((tile * 4 + p) * 2 + h) * 32 + mm) * 16;
+                for (int i = 0; i < 16; ++i) dq[i] = src[16 + 32 * p + 16 * h + i];
+            }
+        const float d = f16_to_f32((uint32_t)src[0] | ((uint32_t)src[1] << 8));
+        const float dmin = f16_to_f32((uint32_t)src[2] | ((uint32_t)src[3] << 8));
+        for (int j = 0; j < 8; ++j) {
+            int s, mn;
+            q4k_scale_min(j, src + 4, s, mn);
+            kt[(tile * 8 + j) * 32 + mm] = make_float2(d * (float)s, dmin * (float)mn);
+        }
+    }
+}
+
+void launch_repack(const uint8_t* raw, QMat m, uint8_t* qs, uint8_t* sc, float2* kt, hipStream_t st) {
+    const size_t units = (size_t)m.n_mats * m.rows * m.nkb;
+    hipLaunchKernelGGL(k_repack, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, st, raw, m, qs, sc, kt);
+}
+
+}  // namespace jx

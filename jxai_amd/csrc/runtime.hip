@@ -1,0 +1,695 @@
+// C-ABI runtime of the MoE expert path: device init, one-time upload and
+// repack of a layer, workspace management, the forward pipeline
+//   route -> dispatch -> {dequant-GEMV | int8-MFMA GEMM} x (gate/up, down) -> combine
+// and the function-level drop-ins of the reference's math API.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/jxmoe.h"
+#include "jxmoe_device.h"
+#include "jxmoe_kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+int g_device = -1;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+#define HIPCHK(expr)                                                                              \
+    do {                                                                                          \
+        hipError_t e_ = (expr);                                                                   \
+        if (e_ != hipSuccess)                                                                     \
+            return fail(e_ == hipErrorOutOfMemory ? JX_ERR_NOMEM : JX_ERR_HIP,                    \
+                        std::string(#expr) + ": " + hipGetErrorString(e_));                       \
+    } while (0)
+
+bool expert_type_ok(int t) { return t == jx::T_Q4_0 || t == jx::T_Q8_0 || t == jx::T_Q4_K; }
+
+size_t row_bytes(int t, int64_t cols) {
+    switch (t) {
+        case jx::T_Q4_0: return (size_t)((cols + 31) / 32) * 18;
+        case jx::T_Q8_0: return (size_t)((cols + 31) / 32) * 34;
+        case jx::T_Q4_K: return (size_t)((cols + 255) / 256) * 144;
+        default: return 0;
+    }
+}
+
+// supports_q8_activation (src/quant.cpp:3881-3893)
+bool q8_activation(int t, int64_t cols) {
+    if (t == jx::T_Q4_0 || t == jx::T_Q8_0) return cols % 32 == 0;
+    if (t == jx::T_Q4_K) return cols % 256 == 0;
+    return false;
+}
+
+struct DevMat {
+    jx::QMat m;
+    uint8_t* qs = nullptr;
+    uint8_t* sc = nullptr;
+    float2* kt = nullptr;
+    void release() {
+        if (qs) (void)hipFree(qs);
+        if (sc) (void)hipFree(sc);
+        if (kt) (void)hipFree(kt);
+        qs = sc = nullptr;
+        kt = nullptr;
+    }
+};
+
+// Upload n_mats [rows][cols] block matrices and repack them on the device.
+int upload_matrix(int type, int n_mats, int rows, int cols, const void* host, DevMat& out, hipStream_t st) {
+    if (!expert_type_ok(type)) return fail(JX_ERR_UNSUPPORTED, "expert weight type must be Q4_0, Q8_0 or Q4_K");
+    if (rows % jx::ROWS_PER_TILE != 0) return fail(JX_ERR_UNSUPPORTED, "matrix rows must be a multiple of 32");
+    if (cols % 32 != 0) return fail(JX_ERR_UNSUPPORTED, "matrix cols must be a multiple of 32");
+    jx::QMat& m = out.m;
+    m.type = type;
+    m.rows = rows;
+    m.cols = cols;
+    m.nrt = rows / jx::ROWS_PER_TILE;
+    m.nkb = type == jx::T_Q4_K ? (cols + 255) / 256 : cols / 32;
+    m.n_mats = n_mats;
+    const size_t units = (size_t)rows * m.nkb;
+    const size_t qs_u = type == jx::T_Q4_0 ? 16 : (type == jx::T_Q8_0 ? 32 : 128);
+    const size_t sc_u = type == jx::T_Q4_K ? 16 : 2;
+    m.qs_es = units * qs_u;
+    m.sc_es = units * sc_u;
+    m.kt_es = type == jx::T_Q4_K ? units * 8 : 0;
+    const size_t raw_bytes = (size_t)n_mats * rows * row_bytes(type, cols);
+    uint8_t* raw = nullptr;
+    HIPCHK(hipMalloc(&out.qs, m.qs_es * n_mats));
+    HIPCHK(hipMalloc(&out.sc, m.sc_es * n_mats));
+    if (m.kt_es) HIPCHK(hipMalloc(&out.kt, m.kt_es * n_mats * sizeof(float2)));
+    HIPCHK(hipMalloc(&raw, raw_bytes));
+    hipError_t e = hipMemcpyAsync(raw, host, raw_bytes, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) {
+        m.qs = out.qs;
+        m.sc = out.sc;
+        m.kt = out.kt;
+        jx::launch_repack(raw, m, out.qs, out.sc, out.kt, st);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    (void)hipFree(raw);
+    if (e != hipSuccess) return fail(JX_ERR_HIP, std::string("weight upload: ") + hipGetErrorString(e));
+    return JX_OK;
+}
+
+template <typename T>
+int dalloc(T*& p, size_t n) {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    if (n == 0) return JX_OK;
+    HIPCHK(hipMalloc(&p, n * sizeof(T)));
+    return JX_OK;
+}
+
+struct Prof {
+    bool on = false;
+    std::vector<hipEvent_t> pool;
+    size_t used = 0;
+    std::vector<std::pair<std::string, size_t>> pending;  // name, event index (start; end = +1)
+    std::map<std::string, std::pair<double, int64_t>> acc;
+};
+
+}  // namespace
+
+struct jx_moe_layer {
+    int device = 0;
+    int E = 0, k = 0, d = 0, F = 0, Fs = 0;
+    bool shared = false, down_f32 = false, sdown_f32 = false;
+    float* router = nullptr;
+    float* bias = nullptr;
+    float* shgate = nullptr;
+    DevMat gate, up, down, sgate, sup, sdown;
+    // workspace
+    int cap = 0;
+    float *x = nullptr, *out = nullptr, *probs = nullptr, *shscale = nullptr, *logits = nullptr;
+    int *ids = nullptr, *counts = nullptr, *offs = nullptr, *act = nullptr, *n_act = nullptr, *pair_f = nullptr,
+        *pos_of = nullptr, *n_tiles = nullptr;
+    int4* tiles = nullptr;
+    jx::ActQ8 xq, hq, hqs;
+    float *hf = nullptr, *hfs = nullptr, *y = nullptr, *ysh = nullptr;
+    int last_n = 0;
+    Prof prof;
+};
+
+struct jx_qmatrix {
+    int device = 0;
+    int type = 0, rows = 0, cols = 0;
+    DevMat w;
+};
+
+namespace {
+
+int ensure_workspace(jx_moe_layer* L, int n) {
+    if (n <= L->cap) return JX_OK;
+    const int cap = std::max(n, L->cap * 2);
+    const size_t nk = (size_t)cap * L->k;
+    int r;
+#define WS(ptr, count)                                 \
+    if ((r = dalloc(ptr, (size_t)(count))) != JX_OK) { \
+        L->cap = 0;                                    \
+        return r;                                      \
+    }
+    WS(L->x, (size_t)cap * L->d);
+    WS(L->out, (size_t)cap * L->d);
+    WS(L->probs, nk);
+    WS(L->ids, nk);
+    WS(L->shscale, cap);
+    WS(L->logits, (size_t)cap * L->E);
+    WS(L->counts, L->E);
+    WS(L->offs, L->E + 1);
+    WS(L->act, L->E);
+    WS(L->n_act, 1);
+    WS(L->pair_f, nk);
+    WS(L->pos_of, nk);
+    WS(L->n_tiles, 1);
+    WS(L->tiles, nk / jx::MFMA_BN + std::min<size_t>(L->E, nk) + 1);
+    WS(L->xq.q, (size_t)cap * L->d);
+    WS(L->xq.s, (size_t)cap * L->d / 32);
+    L->xq.K = L->d;
+    WS(L->hq.q, nk * L->F);
+    WS(L->hq.s, nk * L->F / 32);
+    L->hq.K = L->F;
+    WS(L->y, nk * L->d);
+    const size_t fpad = ((size_t)L->F + 255) / 256 * 256;
+    if (L->down_f32) {
+        WS(L->hf, nk * fpad);
+        HIPCHK(hipMemset(L->hf, 0, nk * fpad * sizeof(float)));
+    }
+    if (L->shared) {
+        WS(L->hqs.q, (size_t)cap * L->Fs);
+        WS(L->hqs.s, (size_t)cap * L->Fs / 32);
+        L->hqs.K = L->Fs;
+        WS(L->ysh, (size_t)cap * L->d);
+        const size_t fspad = ((size_t)L->Fs + 255) / 256 * 256;
+        if (L->sdown_f32) {
+            WS(L->hfs, (size_t)cap * fspad);
+            HIPCHK(hipMemset(L->hfs, 0, (size_t)cap * fspad * sizeof(float)));
+        }
+    }
+#undef WS
+    L->cap = cap;
+    return JX_OK;
+}
+
+void free_layer(jx_moe_layer* L) {
+    (void)hipSetDevice(L->device);
+    for (auto* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown}) m->release();
+    void* ptrs[] = {L->router, L->bias, L->shgate, L->x, L->out, L->probs, L->shscale, L->logits, L->ids,
+                    L->counts, L->offs, L->act, L->n_act, L->pair_f, L->pos_of, L->n_tiles, L->tiles,
+                    L->xq.q, L->xq.s, L->hq.q, L->hq.s, L->hqs.q, L->hqs.s, L->hf, L->hfs, L->y, L->ysh};
+    for (void* p : ptrs)
+        if (p) (void)hipFree(p);
+    for (auto ev : L->prof.pool) (void)hipEventDestroy(ev);
+    delete L;
+}
+
+// Profiling: bracket a launch with two pooled events on the forward's stream.
+struct Launch {
+    jx_moe_layer* L;
+    const char* name;
+    hipStream_t st;
+    size_t idx = (size_t)-1;
+    Launch(jx_moe_layer* L_, const char* n, hipStream_t s) : L(L_), name(n), st(s) {
+        if (!L->prof.on) return;
+        Prof& P = L->prof;
+        while (P.pool.size() < P.used + 2) {
+            hipEvent_t ev;
+            if (hipEventCreate(&ev) != hipSuccess) return;
+            P.pool.push_back(ev);
+        }
+        idx = P.used;
+        P.used += 2;
+        (void)hipEventRecord(P.pool[idx], st);
+    }
+    ~Launch() {
+        if (idx == (size_t)-1) return;
+        (void)hipEventRecord(L->prof.pool[idx + 1], st);
+        L->prof.pending.emplace_back(name, idx);
+    }
+};
+
+int resolve_profile(jx_moe_layer* L) {
+    Prof& P = L->prof;
+    for (auto& pe : P.pending) {
+        HIPCHK(hipEventSynchronize(P.pool[pe.second + 1]));
+        float ms = 0.0f;
+        HIPCHK(hipEventElapsedTime(&ms, P.pool[pe.second], P.pool[pe.second + 1]));
+        auto& a = P.acc[pe.first];
+        a.first += ms;
+        a.second += 1;
+    }
+    P.pending.clear();
+    P.used = 0;
+    return JX_OK;
+}
+
+// MFMA tiles when the average expert sees at least this many pairs.
+constexpr int MFMA_MIN_PAIRS_PER_EXPERT = 16;
+
+int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStream_t st, uint32_t flags) {
+    const int E = L->E, k = L->k, d = L->d;
+    const int nk = n * k;
+    jx::RouteArgs ra{xdev, n, d, E, k, L->router, L->bias, L->shgate, L->xq, L->ids, L->probs, L->shscale, L->logits};
+    {
+        Launch l(L, "route", st);
+        jx::launch_route(ra, st);
+    }
+    {
+        Launch l(L, "dispatch", st);
+        jx::launch_dispatch(L->ids, nk, E, k, L->counts, L->offs, L->act, L->n_act, L->pair_f, L->pos_of, L->tiles,
+                            L->n_tiles, st);
+    }
+    jx::Groups grp;
+    grp.counts = L->counts;
+    grp.offs = L->offs;
+    grp.act = L->act;
+    grp.n_act = L->n_act;
+    grp.pair_f = L->pair_f;
+    grp.tiles = L->tiles;
+    grp.n_tiles = L->n_tiles;
+    grp.top_k = k;
+    grp.n_tok = n;
+    bool mfma = (size_t)nk >= (size_t)MFMA_MIN_PAIRS_PER_EXPERT * E;
+    if (flags & JX_FWD_FORCE_GEMV) mfma = false;
+    if (flags & JX_FWD_FORCE_MFMA) mfma = true;
+    const int slots = std::min(E, nk);
+    const int tb = n == 1 ? 1 : 4;
+    const int tiles_ub = nk / jx::MFMA_BN + slots;
+    const size_t fpad = ((size_t)L->F + 255) / 256 * 256;
+    if (mfma) {
+        {
+            Launch l(L, "gateup_mfma", st);
+            jx::launch_mfma_gateup(L->gate.m, L->up.m, L->xq, grp, tiles_ub, L->hq, L->down_f32 ? L->hf : nullptr, st);
+        }
+        Launch l(L, L->down_f32 ? "down_gemv_f32" : "down_mfma", st);
+        if (L->down_f32)
+            jx::launch_gemv_down(L->down.m, L->hq, L->hf, (int)fpad, grp, slots, 4, 1, L->y, 0, st);
+        else
+            jx::launch_mfma_down(L->down.m, L->hq, grp, tiles_ub, L->y, st);
+    } else {
+        {
+            Launch l(L, "gateup_gemv", st);
+            jx::launch_gemv_gateup(L->gate.m, L->up.m, L->xq, grp, slots, tb, L->hq, L->down_f32 ? L->hf : nullptr, st);
+        }
+        Launch l(L, L->down_f32 ? "down_gemv_f32" : "down_gemv", st);
+        jx::launch_gemv_down(L->down.m, L->hq, L->down_f32 ? L->hf : nullptr, (int)fpad, grp, slots, tb, 1, L->y, 0,
+                             st);
+    }
+    if (L->shared) {
+        jx::Groups sg;
+        sg.identity = 1;
+        sg.n_tok = n;
+        sg.top_k = 1;
+        const size_t fspad = ((size_t)L->Fs + 255) / 256 * 256;
+        const bool smfma = n >= jx::MFMA_BN && !(flags & JX_FWD_FORCE_GEMV);
+        if (smfma) {
+            {
+                Launch l(L, "shared_gateup_mfma", st);
+                jx::launch_mfma_gateup(L->sgate.m, L->sup.m, L->xq, sg, (n + jx::MFMA_BN - 1) / jx::MFMA_BN, L->hqs,
+                                       L->sdown_f32 ? L->hfs : nullptr, st);
+            }
+            Launch l(L, "shared_down", st);
+            if (L->sdown_f32)
+                jx::launch_gemv_down(L->sdown.m, L->hqs, L->hfs, (int)fspad, sg, 1, 4, 1, L->ysh, 0, st);
+            else
+                jx::launch_mfma_down(L->sdown.m, L->hqs, sg, (n + jx::MFMA_BN - 1) / jx::MFMA_BN, L->ysh, st);
+        } else {
+            {
+                Launch l(L, "shared_gateup_gemv", st);
+                jx::launch_gemv_gateup(L->sgate.m, L->sup.m, L->xq, sg, 1, tb, L->hqs, L->sdown_f32 ? L->hfs : nullptr,
+                                       st);
+            }
+            Launch l(L, "shared_down", st);
+            jx::launch_gemv_down(L->sdown.m, L->hqs, L->sdown_f32 ? L->hfs : nullptr, (int)fspad, sg, 1, tb, 1, L->ysh,
+                                 0, st);
+        }
+    }
+    {
+        Launch l(L, "combine", st);
+        jx::launch_combine(n, d, k, L->probs, L->pos_of, L->y, 1, 0, L->shared ? L->ysh : nullptr, 1, 0, L->shscale,
+                           outdev, st);
+    }
+    HIPCHK(hipGetLastError());
+    return JX_OK;
+}
+
+// Scratch for the drop-ins (allocated per call; these are function-level
+// entry points for parity checks and single-matrix callers, not the layer path).
+struct Scratch {
+    std::vector<void*> ptrs;
+    ~Scratch() {
+        for (void* p : ptrs) (void)hipFree(p);
+    }
+    template <typename T>
+    T* get(size_t n) {
+        void* p = nullptr;
+        if (hipMalloc(&p, std::max<size_t>(n, 1) * sizeof(T)) != hipSuccess) return nullptr;
+        ptrs.push_back(p);
+        return static_cast<T*>(p);
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+const char* jx_moe_last_error(void) { return g_err.c_str(); }
+
+int jx_moe_init(int32_t device) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return fail(JX_ERR_NODEVICE, "no HIP device");
+    if (device < 0 || device >= n) return fail(JX_ERR_NODEVICE, "device index out of range");
+    hipDeviceProp_t p;
+    HIPCHK(hipGetDeviceProperties(&p, device));
+    if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return fail(JX_ERR_NODEVICE, std::string("device is ") + p.gcnArchName + ", this build targets gfx950");
+    HIPCHK(hipSetDevice(device));
+    g_device = device;
+    return JX_OK;
+}
+
+int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
+    if (!D || !out) return fail(JX_ERR_INVALID, "null argument");
+    *out = nullptr;
+    if (g_device < 0) return fail(JX_ERR_NODEVICE, "jx_moe_init has not been called");
+    if (D->n_experts < 1 || D->n_experts > 512) return fail(JX_ERR_UNSUPPORTED, "n_experts must be 1..512");
+    if (D->top_k < 1 || D->top_k > 32 || D->top_k > D->n_experts) return fail(JX_ERR_UNSUPPORTED, "top_k must be 1..min(32, E)");
+    if (D->d_model < 32 || D->d_model % 32 != 0 || D->d_model > 8192)
+        return fail(JX_ERR_UNSUPPORTED, "d_model must be a multiple of 32, at most 8192");
+    if (D->d_ff < 32 || D->d_ff % 32 != 0) return fail(JX_ERR_UNSUPPORTED, "d_ff must be a multiple of 32");
+    if (!D->router || !D->gate_exps || !D->up_exps || !D->down_exps) return fail(JX_ERR_INVALID, "missing tensor");
+    if (D->gate_type != D->up_type) return fail(JX_ERR_UNSUPPORTED, "gate and up must share a type");
+    // gate/up consume Q8_0 activations (cols = d_model); the fp32-activation
+    // fallback of the reference is only implemented for Q4_K down projections.
+    if (!q8_activation(D->gate_type, D->d_model))
+        return fail(JX_ERR_UNSUPPORTED, "gate/up need Q8_0 activations (Q4_K requires d_model % 256 == 0)");
+    if (!q8_activation(D->down_type, D->d_ff) && D->down_type != jx::T_Q4_K)
+        return fail(JX_ERR_UNSUPPORTED, "down projection shape not covered");
+    if (D->d_ff_shared > 0) {
+        if (D->d_ff_shared % 32 != 0) return fail(JX_ERR_UNSUPPORTED, "d_ff_shared must be a multiple of 32");
+        if (!D->sh_gate || !D->sh_up || !D->sh_down) return fail(JX_ERR_INVALID, "missing shared expert tensor");
+        if (D->sh_gate_type != D->sh_up_type) return fail(JX_ERR_UNSUPPORTED, "shared gate and up must share a type");
+        if (!q8_activation(D->sh_gate_type, D->d_model))
+            return fail(JX_ERR_UNSUPPORTED, "shared gate/up need Q8_0 activations");
+        if (!q8_activation(D->sh_down_type, D->d_ff_shared) && D->sh_down_type != jx::T_Q4_K)
+            return fail(JX_ERR_UNSUPPORTED, "shared down projection shape not covered");
+    }
+    auto* L = new jx_moe_layer();
+    L->device = g_device;
+    L->E = D->n_experts;
+    L->k = D->top_k;
+    L->d = D->d_model;
+    L->F = D->d_ff;
+    L->Fs = D->d_ff_shared;
+    L->shared = D->d_ff_shared > 0;
+    // rows >= 8 always holds here, so the reference uses Q8_0 down activations
+    // exactly when supports_q8_activation allows (matmul_quant_f32, 3908-3914)
+    L->down_f32 = !q8_activation(D->down_type, D->d_ff);
+    L->sdown_f32 = L->shared && !q8_activation(D->sh_down_type, D->d_ff_shared);
+    hipStream_t st = nullptr;
+    int r = JX_OK;
+    auto bail = [&](int code) {
+        free_layer(L);
+        return code;
+    };
+    if (hipSetDevice(L->device) != hipSuccess) return bail(fail(JX_ERR_HIP, "hipSetDevice"));
+    const size_t E = L->E, d = L->d;
+    if ((r = dalloc(L->router, E * d)) != JX_OK) return bail(r);
+    if (hipMemcpy(L->router, D->router, E * d * 4, hipMemcpyHostToDevice) != hipSuccess)
+        return bail(fail(JX_ERR_HIP, "router upload"));
+    if (D->router_bias) {
+        if ((r = dalloc(L->bias, E)) != JX_OK) return bail(r);
+        if (hipMemcpy(L->bias, D->router_bias, E * 4, hipMemcpyHostToDevice) != hipSuccess)
+            return bail(fail(JX_ERR_HIP, "router bias upload"));
+    }
+    if ((r = upload_matrix(D->gate_type, L->E, L->F, L->d, D->gate_exps, L->gate, st)) != JX_OK) return bail(r);
+    if ((r = upload_matrix(D->up_type, L->E, L->F, L->d, D->up_exps, L->up, st)) != JX_OK) return bail(r);
+    if ((r = upload_matrix(D->down_type, L->E, L->d, L->F, D->down_exps, L->down, st)) != JX_OK) return bail(r);
+    if (L->shared) {
+        if ((r = upload_matrix(D->sh_gate_type, 1, L->Fs, L->d, D->sh_gate, L->sgate, st)) != JX_OK) return bail(r);
+        if ((r = upload_matrix(D->sh_up_type, 1, L->Fs, L->d, D->sh_up, L->sup, st)) != JX_OK) return bail(r);
+        if ((r = upload_matrix(D->sh_down_type, 1, L->d, L->Fs, D->sh_down, L->sdown, st)) != JX_OK) return bail(r);
+        if (D->sh_gate_inp) {
+            if ((r = dalloc(L->shgate, d)) != JX_OK) return bail(r);
+            if (hipMemcpy(L->shgate, D->sh_gate_inp, d * 4, hipMemcpyHostToDevice) != hipSuccess)
+                return bail(fail(JX_ERR_HIP, "shared gate upload"));
+        }
+    }
+    if ((r = ensure_workspace(L, 1)) != JX_OK) return bail(r);
+    *out = L;
+    return JX_OK;
+}
+
+void jx_moe_layer_destroy(jx_moe_layer* L) {
+    if (L) free_layer(L);
+}
+
+int jx_moe_forward(jx_moe_layer* L, const float* x, int32_t n_tok, float* out, int32_t* topk_ids, float* topk_w,
+                   int32_t* expert_counts, void* stream, uint32_t flags) {
+    if (!L || !x || !out) return fail(JX_ERR_INVALID, "null argument");
+    if (n_tok < 1) return fail(JX_ERR_INVALID, "n_tok must be >= 1");
+    if ((flags & JX_FWD_ASYNC) && !(flags & JX_FWD_DEVICE_PTRS))
+        return fail(JX_ERR_INVALID, "JX_FWD_ASYNC needs JX_FWD_DEVICE_PTRS");
+    if ((flags & JX_FWD_FORCE_GEMV) && (flags & JX_FWD_FORCE_MFMA))
+        return fail(JX_ERR_INVALID, "conflicting regime flags");
+    HIPCHK(hipSetDevice(L->device));
+    int r = ensure_workspace(L, n_tok);
+    if (r != JX_OK) return r;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const bool dev = flags & JX_FWD_DEVICE_PTRS;
+    const size_t xd = (size_t)n_tok * L->d;
+    const float* xin = x;
+    float* outp = out;
+    if (!dev) {
+        HIPCHK(hipMemcpyAsync(L->x, x, xd * 4, hipMemcpyHostToDevice, st));
+        xin = L->x;
+        outp = L->out;
+    }
+    if ((r = run_forward(L, xin, n_tok, outp, st, flags)) != JX_OK) return r;
+    L->last_n = n_tok;
+    const size_t nk = (size_t)n_tok * L->k;
+    const hipMemcpyKind k2 = dev ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost;
+    if (!dev) HIPCHK(hipMemcpyAsync(out, L->out, xd * 4, hipMemcpyDeviceToHost, st));
+    if (topk_ids) HIPCHK(hipMemcpyAsync(topk_ids, L->ids, nk * 4, k2, st));
+    if (topk_w) HIPCHK(hipMemcpyAsync(topk_w, L->probs, nk * 4, k2, st));
+    if (expert_counts) HIPCHK(hipMemcpyAsync(expert_counts, L->counts, (size_t)L->E * 4, k2, st));
+    if (!(flags & JX_FWD_ASYNC)) {
+        HIPCHK(hipStreamSynchronize(st));
+        if (L->prof.on && (r = resolve_profile(L)) != JX_OK) return r;
+    }
+    return JX_OK;
+}
+
+int jx_moe_last_logits(jx_moe_layer* L, float* logits_host, int32_t n_tok) {
+    if (!L || !logits_host) return fail(JX_ERR_INVALID, "null argument");
+    if (n_tok < 1 || n_tok > L->last_n) return fail(JX_ERR_INVALID, "n_tok exceeds the last forward");
+    HIPCHK(hipSetDevice(L->device));
+    HIPCHK(hipDeviceSynchronize());
+    HIPCHK(hipMemcpy(logits_host, L->logits, (size_t)n_tok * L->E * 4, hipMemcpyDeviceToHost));
+    return JX_OK;
+}
+
+int jx_moe_profile(jx_moe_layer* L, int32_t enable) {
+    if (!L) return fail(JX_ERR_INVALID, "null layer");
+    L->prof.on = enable != 0;
+    L->prof.acc.clear();
+    L->prof.pending.clear();
+    L->prof.used = 0;
+    return JX_OK;
+}
+
+int jx_moe_profile_read(jx_moe_layer* L, char* names_buf, size_t names_len, double* ms, int64_t* launches,
+                        int32_t max_entries, int32_t* n_entries) {
+    if (!L || !names_buf || !ms || !launches || !n_entries) return fail(JX_ERR_INVALID, "null argument");
+    HIPCHK(hipSetDevice(L->device));
+    int r = resolve_profile(L);
+    if (r != JX_OK) return r;
+    std::string names;
+    int i = 0;
+    for (auto& kv : L->prof.acc) {
+        if (i >= max_entries) break;
+        names += kv.first + ";";
+        ms[i] = kv.second.first;
+        launches[i] = kv.second.second;
+        ++i;
+    }
+    if (names.size() + 1 > names_len) return fail(JX_ERR_INVALID, "names buffer too small");
+    std::memcpy(names_buf, names.c_str(), names.size() + 1);
+    *n_entries = i;
+    return JX_OK;
+}
+
+// ---- math-API drop-ins -----------------------------------------------------
+
+int jx_qmatrix_create(int32_t type, int64_t rows, int64_t cols, const void* host, jx_qmatrix** out) {
+    if (!host || !out) return fail(JX_ERR_INVALID, "null argument");
+    *out = nullptr;
+    if (g_device < 0) return fail(JX_ERR_NODEVICE, "jx_moe_init has not been called");
+    if (rows < 1 || cols < 1 || rows > (1 << 24) || cols > (1 << 20)) return fail(JX_ERR_INVALID, "bad shape");
+    HIPCHK(hipSetDevice(g_device));
+    auto* m = new jx_qmatrix();
+    m->device = g_device;
+    m->type = type;
+    m->rows = (int)rows;
+    m->cols = (int)cols;
+    const int r = upload_matrix(type, 1, (int)rows, (int)cols, host, m->w, nullptr);
+    if (r != JX_OK) {
+        m->w.release();
+        delete m;
+        return r;
+    }
+    *out = m;
+    return JX_OK;
+}
+
+void jx_qmatrix_destroy(jx_qmatrix* m) {
+    if (!m) return;
+    (void)hipSetDevice(m->device);
+    m->w.release();
+    delete m;
+}
+
+int jx_matmul_quant_f32(jx_qmatrix* W, const float* x, float* out) {
+    if (!W || !x || !out) return fail(JX_ERR_INVALID, "null argument");
+    HIPCHK(hipSetDevice(W->device));
+    const int rows = W->rows, cols = W->cols;
+    const bool q8 = rows >= 8 && q8_activation(W->type, cols);
+    if (!q8 && W->type != jx::T_Q4_K)
+        return fail(JX_ERR_UNSUPPORTED, "fp32-activation dot only implemented for Q4_K");
+    Scratch s;
+    const size_t kpad = ((size_t)cols + 255) / 256 * 256;
+    float* xd = s.get<float>(kpad);
+    float* yd = s.get<float>(rows);
+    if (!xd || !yd) return fail(JX_ERR_NOMEM, "scratch allocation");
+    HIPCHK(hipMemset(xd, 0, kpad * 4));
+    HIPCHK(hipMemcpy(xd, x, (size_t)cols * 4, hipMemcpyHostToDevice));
+    jx::Groups g;
+    g.identity = 1;
+    g.n_tok = 1;
+    jx::ActQ8 a;
+    if (q8) {
+        a.q = s.get<int8_t>(cols);
+        a.s = s.get<float2>(cols / 32);
+        a.K = cols;
+        if (!a.q || !a.s) return fail(JX_ERR_NOMEM, "scratch allocation");
+        jx::launch_quantize_q8(xd, 1, cols, a, nullptr);
+        jx::launch_gemv_down(W->w.m, a, nullptr, 0, g, 1, 1, 1, yd, 0, nullptr);
+    } else {
+        a.K = (int)kpad;
+        jx::launch_gemv_down(W->w.m, a, xd, (int)kpad, g, 1, 1, 1, yd, 0, nullptr);
+    }
+    HIPCHK(hipGetLastError());
+    HIPCHK(hipMemcpy(out, yd, (size_t)rows * 4, hipMemcpyDeviceToHost));
+    return JX_OK;
+}
+
+int jx_matmul_swiglu_quant_f32(jx_qmatrix* Wg, jx_qmatrix* Wu, const float* x, float* out) {
+    if (!Wg || !Wu || !x || !out) return fail(JX_ERR_INVALID, "null argument");
+    if (Wg->rows != Wu->rows || Wg->cols != Wu->cols || Wg->type != Wu->type)
+        return fail(JX_ERR_UNSUPPORTED, "gate and up must share shape and type");
+    HIPCHK(hipSetDevice(Wg->device));
+    const int rows = Wg->rows, cols = Wg->cols;
+    if (!(rows >= 8 && cols % 32 == 0 && q8_activation(Wg->type, cols)))
+        return fail(JX_ERR_UNSUPPORTED, "fp32-activation gate/up not implemented");
+    Scratch s;
+    float* xd = s.get<float>(cols);
+    const size_t fpad = ((size_t)rows + 255) / 256 * 256;
+    float* hf = s.get<float>(fpad);
+    jx::ActQ8 a, hq;
+    a.q = s.get<int8_t>(cols);
+    a.s = s.get<float2>(cols / 32);
+    a.K = cols;
+    if (!xd || !hf || !a.q || !a.s) return fail(JX_ERR_NOMEM, "scratch allocation");
+    HIPCHK(hipMemcpy(xd, x, (size_t)cols * 4, hipMemcpyHostToDevice));
+    jx::launch_quantize_q8(xd, 1, cols, a, nullptr);
+    jx::Groups g;
+    g.identity = 1;
+    g.n_tok = 1;
+    hq.K = rows;  // q == nullptr: no Q8_0 output wanted
+    jx::launch_gemv_gateup(Wg->w.m, Wu->w.m, a, g, 1, 1, hq, hf, nullptr);
+    HIPCHK(hipGetLastError());
+    HIPCHK(hipMemcpy(out, hf, (size_t)rows * 4, hipMemcpyDeviceToHost));
+    return JX_OK;
+}
+
+int jx_quantize_row_q8_0(const float* x, void* blocks, int64_t k) {
+    if (!x || !blocks) return fail(JX_ERR_INVALID, "null argument");
+    if (k < 32 || k % 32 != 0) return fail(JX_ERR_INVALID, "k must be a positive multiple of 32");
+    if (g_device < 0) return fail(JX_ERR_NODEVICE, "jx_moe_init has not been called");
+    HIPCHK(hipSetDevice(g_device));
+    Scratch s;
+    float* xd = s.get<float>(k);
+    jx::ActQ8 a;
+    a.q = s.get<int8_t>(k);
+    a.s = s.get<float2>(k / 32);
+    a.K = (int)k;
+    if (!xd || !a.q || !a.s) return fail(JX_ERR_NOMEM, "scratch allocation");
+    HIPCHK(hipMemcpy(xd, x, (size_t)k * 4, hipMemcpyHostToDevice));
+    jx::launch_quantize_q8(xd, 1, (int)k, a, nullptr);
+    HIPCHK(hipGetLastError());
+    std::vector<int8_t> q((size_t)k);
+    std::vector<float2> sc((size_t)k / 32);
+    HIPCHK(hipMemcpy(q.data(), a.q, (size_t)k, hipMemcpyDeviceToHost));
+    HIPCHK(hipMemcpy(sc.data(), a.s, (size_t)k / 32 * sizeof(float2), hipMemcpyDeviceToHost));
+    auto* out = static_cast<uint8_t*>(blocks);
+    for (size_t b = 0; b < (size_t)k / 32; ++b) {
+        // the scale is an fp16 value widened exactly; narrow it back bit for bit
+        const float f = sc[b].x;
+        uint32_t u;
+        std::memcpy(&u, &f, 4);
+        const uint32_t sign = (u >> 16) & 0x8000u;
+        const int e = (int)((u >> 23) & 0xFF) - 112;
+        uint32_t m = u & 0x7FFFFFu;
+        uint16_t h;
+        if (e <= 0) {
+            h = (e < -10) ? (uint16_t)sign : (uint16_t)(sign | ((m | 0x800000u) >> (uint32_t)(14 - e)));
+        } else if (e >= 31) {
+            h = (uint16_t)(sign | 0x7C00u);
+        } else {
+            h = (uint16_t)(sign | ((uint32_t)e << 10) | (m >> 13));
+        }
+        std::memcpy(out + b * 34, &h, 2);
+        std::memcpy(out + b * 34 + 2, q.data() + b * 32, 32);
+    }
+    return JX_OK;
+}
+
+int jx_dev_alloc(size_t bytes, void** ptr) {
+    if (!ptr) return fail(JX_ERR_INVALID, "null argument");
+    if (g_device >= 0) HIPCHK(hipSetDevice(g_device));
+    HIPCHK(hipMalloc(ptr, bytes));
+    return JX_OK;
+}
+
+int jx_dev_free(void* ptr) {
+    HIPCHK(hipFree(ptr));
+    return JX_OK;
+}
+
+int jx_memcpy_htod(void* dst, const void* src, size_t bytes) {
+    HIPCHK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return JX_OK;
+}
+
+int jx_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
+    HIPCHK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return JX_OK;
+}
+
+int jx_device_synchronize(void) {
+    HIPCHK(hipDeviceSynchronize());
+    return JX_OK;
+}
+
+}  // extern "C"

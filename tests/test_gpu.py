@@ -1,0 +1,176 @@
+"""GPU parity of the HIP MoE path against the oracle and the golden vectors.
+
+Bar: expert ids, top-k order and per-expert counts
+bit-exact; Q8_0 activations bit-exact; layer outputs within max relative error
+1e-3 per token (||y_gpu - y_ref||_inf / ||y_ref||_inf) of the reference CPU
+path; softmax weights within 2e-6 relative (the GPU's expf and glibc's may
+differ in the last ulp).
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from jxai_amd import formats as F
+from jxai_amd import synth
+from tests.conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-3
+
+
+def say(msg):
+    print(f"[gpu] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def moe():
+    from jxai_amd import moe as M
+    M.init(0)
+    return M
+
+
+_LAYERS = {}
+
+
+def layer(name):
+    if name not in _LAYERS:
+        cfg = synth.CONFIGS[name]
+        _LAYERS.clear()
+        _LAYERS[name] = (cfg, synth.make_layer(cfg))
+    return _LAYERS[name]
+
+
+def rel_err(a, b):
+    return float((np.abs(a.astype(np.float64) - b).max(axis=1) / np.abs(b).max(axis=1)).max())
+
+
+# ------------------------------------------------------------------ function level
+def test_quantize_row_q8_0_bitexact(moe, port):
+    z = np.load(os.path.join(GOLDEN, "units.npz"))
+    say("quantize_row_q8_0 golden")
+    assert np.array_equal(moe.quantize_row_q8_0(z["xs"]), z["xq"])
+    x = synth.normal_f32(11, 32 * 4096, 3.0)
+    x[:64] = 0.0
+    x[64:96] = np.arange(32, dtype=np.float32) - 15.5
+    assert np.array_equal(moe.quantize_row_q8_0(x), port.quantize_row_q8_0(x))
+
+
+@pytest.mark.parametrize("qt,rows,cols", [(F.Q4_0, 1024, 2048), (F.Q8_0, 768, 2048), (F.Q4_K, 512, 4096),
+                                          (F.Q4_K, 256, 1408), (F.Q4_0, 2048, 1408), (F.Q8_0, 2048, 768)])
+def test_matmul_quant_f32(moe, port, qt, rows, cols):
+    say(f"matmul_quant_f32 type={qt} {rows}x{cols}")
+    W = synth.quant_matrix(synth.sub_seed("gpu", f"mm{qt}_{rows}_{cols}"), qt, rows, cols)
+    x = synth.normal_f32(synth.sub_seed("gpu", f"mx{cols}"), cols, 1.0)
+    got = moe.matmul_quant_f32(qt, W, x, rows, cols)
+    want = port.matmul_quant_f32(qt, W, x, rows, cols)
+    # same integer block sums, different fp32 summation order
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("qt,rows,cols", [(F.Q4_0, 1408, 2048), (F.Q4_K, 1024, 4096), (F.Q8_0, 768, 2048)])
+def test_matmul_swiglu_quant_f32(moe, port, qt, rows, cols):
+    say(f"matmul_swiglu_quant_f32 type={qt} {rows}x{cols}")
+    Wg = synth.quant_matrix(synth.sub_seed("gpu", f"g{qt}"), qt, rows, cols)
+    Wu = synth.quant_matrix(synth.sub_seed("gpu", f"u{qt}"), qt, rows, cols)
+    x = synth.normal_f32(synth.sub_seed("gpu", f"sx{cols}"), cols, 1.0)
+    got = moe.matmul_swiglu_quant_f32(qt, Wg, qt, Wu, x, rows, cols)
+    want = port.matmul_swiglu_quant_f32(qt, Wg, qt, Wu, x, rows, cols)
+    assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max()
+
+
+# ------------------------------------------------------------------ layer vs the golden vectors
+GOLDEN_CASES = ["toy_n1", "qwen15moe_n1", "qwen15moe_n64", "mixtral_n1", "mixtral_n512", "mixtral_n2048",
+                "qwen3moe_n2048", "dsv2lite_n32"]
+
+
+@pytest.mark.parametrize("case", GOLDEN_CASES)
+def test_layer_vs_golden(moe, case):
+    z = np.load(os.path.join(GOLDEN, case + ".npz"))
+    name, n = str(z["config"]), int(z["n"])
+    say(f"layer {case}: building")
+    cfg, lw = layer(name)
+    x = synth.make_tokens(cfg, n)
+    L = moe.MoELayer.from_weights(lw)
+    say(f"layer {case}: forward")
+    out, ids, w, counts = L.forward(x)
+    assert np.array_equal(ids, z["topk_ids"]), "routing differs"
+    assert np.array_equal(counts, z["counts"])
+    np.testing.assert_allclose(w, z["topk_w"], rtol=2e-6, atol=0)
+    assert rel_err(out[z["rows"]], z["out"]) <= REL_TOL
+    lg = L.last_logits(n)
+    assert np.array_equal(lg[z["rows"]].view(np.uint32), z["logits_rows"].view(np.uint32)), "router logits not bit-exact"
+    L.close()
+
+
+# ------------------------------------------------------------------ both regimes vs the oracle
+@pytest.mark.parametrize("name,n,regime", [("toy", 1, "mfma"), ("toy", 40, "gemv"), ("toy", 300, "mfma"),
+                                           ("qwen15moe", 64, "mfma"), ("qwen15moe", 100, "gemv"),
+                                           ("dsv2lite", 32, "mfma"), ("dsv2lite", 7, "gemv"),
+                                           ("qwen3moe", 200, "gemv"), ("qwen3moe", 96, "mfma")])
+def test_layer_regimes_vs_oracle(moe, port, name, n, regime):
+    say(f"{name} n={n} regime={regime}")
+    cfg, lw = layer(name)
+    x = synth.make_tokens(cfg, n, seed=7)
+    L = moe.MoELayer.from_weights(lw)
+    out, ids, w, counts = L.forward(x, regime=regime)
+    lg_o, ids_o, w_o = port.route(lw, x)
+    assert np.array_equal(ids, ids_o)
+    assert np.array_equal(counts, np.bincount(ids_o.reshape(-1), minlength=cfg.n_experts))
+    np.testing.assert_allclose(w, w_o, rtol=2e-6, atol=0)
+    sel = np.unique(np.linspace(0, n - 1, min(n, 6)).astype(np.int32))
+    want = port.moe_forward(lw, x, sel)[0]
+    assert rel_err(out[sel], want) <= REL_TOL
+    L.close()
+
+
+# ------------------------------------------------------------------ properties at full size
+def test_mixtral_prefill_properties(moe):
+    """2048-token Mixtral layer: routing invariants, regime agreement, determinism."""
+    cfg, lw = layer("mixtral")
+    x = synth.make_tokens(cfg, 2048)
+    L = moe.MoELayer.from_weights(lw)
+    say("mixtral 2048 mfma x2")
+    a = L.forward(x, regime="mfma")
+    b = L.forward(x, regime="mfma")
+    assert all(np.array_equal(u, v) for u, v in zip(a, b)), "two runs differ"
+    out, ids, w, counts = a
+    assert counts.sum() == 2048 * cfg.top_k
+    assert np.all(np.diff(L.last_logits(2048)[np.arange(2048)[:, None], ids], axis=1) <= 0), "not descending"
+    np.testing.assert_allclose(w.sum(axis=1), 1.0, rtol=1e-6)
+    say("mixtral 2048 gemv")
+    g = L.forward(x, regime="gemv")
+    assert np.array_equal(g[1], ids)
+    assert rel_err(g[0], out) <= REL_TOL
+    L.close()
+
+
+def test_edge_cases(moe, port):
+    """Zero activations (all logits tie: index order), a single token, an expert that takes every token."""
+    cfg = synth.LayerConfig("edge", 256, 4, 4, 256, F.Q4_K, d_ff_shared=256, shared_gate=True)
+    lw = synth.make_layer(cfg, seed=3)
+    L = moe.MoELayer.from_weights(lw)
+    x = np.zeros((3, 256), np.float32)
+    out, ids, w, counts = L.forward(x)
+    assert np.array_equal(ids, np.tile(np.arange(4, dtype=np.int32), (3, 1)))
+    np.testing.assert_allclose(w, 0.25, rtol=0)
+    want = port.moe_forward(lw, x)[0]
+    assert np.abs(out - want).max() <= 1e-6
+    x1 = synth.make_tokens(cfg, 1, seed=5)
+    o1 = L.forward(x1)[0]
+    assert rel_err(o1, port.moe_forward(lw, x1)[0]) <= REL_TOL
+    L.close()
+    # top_k == n_experts: every expert takes every token, both regimes
+    cfg2 = synth.LayerConfig("edge2", 512, 2, 2, 512, F.Q4_0)
+    lw2 = synth.make_layer(cfg2, seed=4)
+    L2 = moe.MoELayer.from_weights(lw2)
+    x2 = synth.make_tokens(cfg2, 70, seed=4)
+    want2 = port.moe_forward(lw2, x2)[0]
+    for regime in ("gemv", "mfma"):
+        o, i, ww, c = L2.forward(x2, regime=regime)
+        assert np.array_equal(c, [70, 70])
+        assert rel_err(o, want2) <= REL_TOL
+    L2.close()
