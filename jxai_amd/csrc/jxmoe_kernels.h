@@ -75,10 +75,9 @@ void launch_dispatch(const int* ids, int nk, int E, int top_k, int* counts, int*
 // Output rows are sorted pairs (routed) or tokens (shared).
 void launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots,
                         int tb, ActQ8 hq, float* hf, hipStream_t st);
-// Decode regime: down projection over Q8_0 (hq) or fp32 (hf) activations into
-// y[slice][pair][d]; ksplit slices of K are summed by the combine kernel.
+// Decode regime: down projection over Q8_0 (hq) or fp32 (hf) activations into y[pair][d].
 void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp,
-                      int slots, int tb, int ksplit, float* y, size_t y_slice, hipStream_t st);
+                      int slots, int tb, float* y, hipStream_t st);
 // Prefill regime: int8 MFMA grouped GEMMs over the dispatch tile table.
 void launch_mfma_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int tiles_ub,
                         ActQ8 hq, float* hf, hipStream_t st);
@@ -86,9 +85,17 @@ void launch_mfma_down(const QMat& dn, const ActQ8& hq, const Groups& grp, int ti
                       hipStream_t st);
 
 // out[t] = sum_s p[t][s] * y[pos(t,s)] (+ shscale[t] * ysh[t]), fma in selection order.
-void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, int ysl,
-                    size_t y_slice, const float* ysh, int shsl, size_t ysh_slice, const float* shscale,
-                    float* out, hipStream_t st);
+void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
+                    const float* shscale, float* out, hipStream_t st);
+
+// Routing for a few tokens (n <= ROUTE_SMALL_MAX_N): one block per router row
+// with the row staged in LDS; the last block to finish does top-k, softmax and
+// the dispatch (replacing launch_dispatch).  `done` is a zeroed counter the
+// kernel leaves at zero.
+constexpr int ROUTE_SMALL_MAX_N = 2;
+bool route_small_fits(int n, int d, int E);
+void launch_route_small(const RouteArgs& a, int* done, int* counts, int* offs, int* act, int* n_act, int* pair_f,
+                        int* pos_of, int4* tiles, int* n_tiles, hipStream_t st);
 
 // Q8_0 of rows x K fp32 (row-major, K % 32 == 0).
 void launch_quantize_q8(const float* x, int rows, int K, ActQ8 out, hipStream_t st);

@@ -1,6 +1,8 @@
 // Routing side of the MoE expert path: router GEMV + top-k softmax + Q8_0
 // activation quantization (one fused kernel), token->expert dispatch, the
 // weighted combine, and the one-time weight repack.
+#include <algorithm>
+
 #include "jxmoe_device.h"
 #include "jxmoe_kernels.h"
 
@@ -139,6 +141,172 @@ void launch_route(const RouteArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(k_route, dim3(a.n), dim3(ROUTE_THREADS), (size_t)a.d * sizeof(float), st, a);
 }
 
+// ---------------------------------------------------------------- few tokens
+// Decode routing: a one-block-per-token kernel would serialise every router
+// row behind one CU's load latency.  Here block r owns router row r (expert r,
+// or the shared-expert gate vector as row E): it stages that row and the n
+// tokens in LDS with all loads in flight, then 16 lanes per token run the
+// vec_dot_f32 chains from LDS.  Blocks also split the Q8_0 quantization of x.
+// The last block to finish (device-scope counter) ranks, normalises and
+// dispatches: with n*k <= 2*32 pairs the counting sort is a short serial loop.
+constexpr int RS_THREADS = 256;
+constexpr int RS_LDS_BYTES = 48 * 1024;
+
+bool route_small_fits(int n, int d, int E) {
+    return n >= 1 && n <= ROUTE_SMALL_MAX_N && E <= MAX_E && (size_t)(1 + n) * d * sizeof(float) <= RS_LDS_BYTES &&
+           d % 4 == 0;
+}
+
+__device__ __forceinline__ float coherent_load(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ void __launch_bounds__(RS_THREADS)
+k_route_small(RouteArgs a, int* done, int* counts, int* offs, int* act, int* n_act, int* pair_f, int* pos_of,
+              int4* tiles, int* n_tiles) {
+    extern __shared__ float lds[];  // [0, d): router row; then n token rows
+    __shared__ int s_last;
+    __shared__ int rank_sel[ROUTE_SMALL_MAX_N][MAX_K];
+    const int r = blockIdx.x, tid = threadIdx.x;
+    const int d = a.d, n = a.n, E = a.E;
+    float* ws = lds;
+    float* xs = lds + d;
+    const float* w = r < E ? a.router + (size_t)r * d : a.shgate;
+    for (int i = tid * 4; i < d; i += RS_THREADS * 4)
+        *reinterpret_cast<float4*>(ws + i) = *reinterpret_cast<const float4*>(w + i);
+    for (int t = 0; t < n; ++t)
+        for (int i = tid * 4; i < d; i += RS_THREADS * 4)
+            *reinterpret_cast<float4*>(xs + (size_t)t * d + i) = *reinterpret_cast<const float4*>(a.x + (size_t)t * d + i);
+    __syncthreads();
+
+    // this block's share of the Q8_0 blocks of x (32 lanes per block)
+    {
+        const int nb = d / 32, tot = n * nb;
+        const int per = (tot + gridDim.x - 1) / gridDim.x;
+        const int b0 = r * per, b1 = min(tot, b0 + per);
+        const int lane = tid & 63, wave = tid >> 6, half = lane >> 5, l32 = lane & 31;
+        for (int bb = b0 + wave * 2; bb < b1; bb += (RS_THREADS / 64) * 2) {
+            const int b = bb + half;
+            const bool ok = b < b1;
+            const float v = ok ? xs[(size_t)b * 32 + l32] : 0.0f;
+            const float amax = wave_max32(__builtin_fabsf(v));
+            const float dd = amax / 127.0f;
+            const float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
+            float rr = round_away(v * id);
+            rr = fminf(fmaxf(rr, -127.0f), 127.0f);
+            const int q = (int)rr;
+            const int sq = wave_sum32i(q);
+            if (ok) {
+                a.xq.q[(size_t)b * 32 + l32] = (int8_t)q;  // token-major: b = t*nb + block
+                if (l32 == 0) a.xq.s[b] = make_float2(f16_to_f32(f32_to_f16_trunc(dd)), (float)sq);
+            }
+        }
+    }
+
+    // router row r for every token: vec_dot_f32 order (see k_route)
+    if (tid < 16 * ROUTE_SMALL_MAX_N) {
+        const int t = tid >> 4, j = tid & 15;
+        const bool ok = t < n;
+        const float* xt = xs + (size_t)(ok ? t : 0) * d;
+        const int d16 = (d / 16) * 16;
+        const bool has8 = (d - d16) >= 8;
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int i = 0; i < d16; i += 16) acc = __builtin_fmaf(ws[i + j], xt[i + j], acc);
+        const float hi = __shfl_down(acc, 8, 16);
+        float v = acc + hi;
+        if (has8 && j < 8) v = __builtin_fmaf(ws[d16 + j], xt[d16 + j], v);
+        float s = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) s += __shfl(v, q, 16);
+        for (int i = d16 + (has8 ? 8 : 0); i < d; ++i) s = __builtin_fmaf(ws[i], xt[i], s);
+        if (ok && j == 0) {
+            if (r < E) a.logits[(size_t)t * E + r] = a.bias ? s + a.bias[r] : s;
+            else a.shscale[t] = s;  // raw shared-gate logit; the last block applies the sigmoid
+        }
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) s_last = atomicAdd(done, 1) == (int)gridDim.x - 1;
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+
+    // ---- last block: top-k + softmax for every token
+    const int k = a.k;
+    float* lgs = lds;  // reuse LDS: [n][E] logits
+    for (int i = tid; i < n * E; i += RS_THREADS) lgs[i] = coherent_load(a.logits + i);
+    if (tid < n * MAX_K) rank_sel[tid / MAX_K][tid % MAX_K] = tid % MAX_K;  // valid default slots
+    __syncthreads();
+    for (int i = tid; i < n * E; i += RS_THREADS) {
+        const int t = i / E, e = i % E;
+        const float* lt = lgs + (size_t)t * E;
+        const float le = lt[e];
+        int rank = 0;
+        for (int f = 0; f < E; ++f) rank += (lt[f] > le) || (lt[f] == le && f < e);
+        if (rank < k) rank_sel[t][rank] = e;
+    }
+    __syncthreads();
+    if (tid < n) {
+        const int t = tid;
+        const float* lt = lgs + (size_t)t * E;
+        float p[MAX_K];
+        float mx = lt[rank_sel[t][0]];
+        for (int i = 1; i < k; ++i) mx = fmaxf(mx, lt[rank_sel[t][i]]);
+        float sum = 0.0f;
+        for (int i = 0; i < k; ++i) {
+            p[i] = expf(lt[rank_sel[t][i]] - mx);
+            sum += p[i];
+        }
+        const float inv = (sum > 0.0f) ? 1.0f / sum : 1.0f / (float)k;
+        for (int i = 0; i < k; ++i) {
+            a.ids[(size_t)t * k + i] = rank_sel[t][i];
+            a.probs[(size_t)t * k + i] = p[i] * inv;
+        }
+        if (a.shscale) a.shscale[t] = a.shgate ? 1.0f / (1.0f + expf(-coherent_load(a.shscale + t))) : 1.0f;
+    }
+    __syncthreads();
+    // ---- dispatch (stable counting sort over the n*k pairs)
+    for (int e = tid; e < E; e += RS_THREADS) counts[e] = 0;
+    __syncthreads();
+    if (tid == 0) {
+        const int nk = n * k;
+        int* hist = reinterpret_cast<int*>(lgs);  // E ints
+        for (int e = 0; e < E; ++e) hist[e] = 0;
+        for (int f = 0; f < nk; ++f) hist[rank_sel[f / k][f % k]]++;
+        int off = 0, na = 0, nt = 0;
+        for (int e = 0; e < E; ++e) {
+            const int c = hist[e];
+            counts[e] = c;
+            offs[e] = off;
+            if (c > 0) {
+                act[na++] = e;
+                for (int i = 0; i * MFMA_BN < c; ++i) tiles[nt++] = make_int4(e, off + i * MFMA_BN, min(MFMA_BN, c - i * MFMA_BN), 0);
+            }
+            hist[e] = off;  // running write position
+            off += c;
+        }
+        offs[E] = off;
+        *n_act = na;
+        *n_tiles = nt;
+        for (int f = 0; f < nk; ++f) {
+            const int e = rank_sel[f / k][f % k];
+            const int pos = hist[e]++;
+            pair_f[pos] = f;
+            pos_of[f] = pos;
+        }
+        *done = 0;
+    }
+}
+
+void launch_route_small(const RouteArgs& a, int* done, int* counts, int* offs, int* act, int* n_act, int* pair_f,
+                        int* pos_of, int4* tiles, int* n_tiles, hipStream_t st) {
+    const int rows = a.E + (a.shgate ? 1 : 0);
+    const size_t lds = std::max((size_t)(1 + a.n) * a.d, (size_t)a.n * a.E + 1) * sizeof(float);
+    hipLaunchKernelGGL(k_route_small, dim3(rows), dim3(RS_THREADS), lds, st, a, done, counts, offs, act, n_act, pair_f,
+                       pos_of, tiles, n_tiles);
+}
+
 // One block per expert.  Every block builds the full per-expert histogram in
 // LDS (no global atomics, nothing to clear between calls), derives its pair
 // offset, MFMA tile offset and active-list slot, then writes the positions of
@@ -216,35 +384,27 @@ void launch_dispatch(const int* ids, int nk, int E, int top_k, int* counts, int*
 
 // MoE combine (transformer.cpp:2728-2730 and 2752-2754): starting from 0, for
 // each selected expert in descending-logit order acc = fma(p, y, acc), then
-// acc = fma(shared_scale, y_shared, acc).  Split-K slices of y are summed
-// first, in slice order.
+// acc = fma(shared_scale, y_shared, acc).
 __global__ void __launch_bounds__(256)
-k_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, int ysl, size_t y_slice,
-          const float* ysh, int shsl, size_t ysh_slice, const float* shscale, float* out) {
+k_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
+          const float* shscale, float* out) {
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= (size_t)n * d) return;
     const int t = (int)(idx / d), i = (int)(idx % d);
     float acc = 0.0f;
     for (int s = 0; s < k; ++s) {
         const size_t p = (size_t)pos_of[(size_t)t * k + s];
-        float v = y[p * d + i];
-        for (int sl = 1; sl < ysl; ++sl) v = v + y[sl * y_slice + p * d + i];
-        acc = __builtin_fmaf(probs[(size_t)t * k + s], v, acc);
+        acc = __builtin_fmaf(probs[(size_t)t * k + s], y[p * d + i], acc);
     }
-    if (ysh) {
-        float v = ysh[(size_t)t * d + i];
-        for (int sl = 1; sl < shsl; ++sl) v = v + ysh[sl * ysh_slice + (size_t)t * d + i];
-        acc = __builtin_fmaf(shscale[t], v, acc);
-    }
+    if (ysh) acc = __builtin_fmaf(shscale[t], ysh[(size_t)t * d + i], acc);
     out[idx] = acc;
 }
 
-void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, int ysl,
-                    size_t y_slice, const float* ysh, int shsl, size_t ysh_slice, const float* shscale,
-                    float* out, hipStream_t st) {
+void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
+                    const float* shscale, float* out, hipStream_t st) {
     const size_t tot = (size_t)n * d;
     hipLaunchKernelGGL(k_combine, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, n, d, k, probs, pos_of, y,
-                       ysl, y_slice, ysh, shsl, ysh_slice, shscale, out);
+                       ysh, shscale, out);
 }
 
 // Q8_0 of `rows` rows of K fp32 values (quantize_row_q8_0, src/quant.cpp:1029-1045),

@@ -6,6 +6,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <string>
@@ -138,8 +139,24 @@ struct jx_moe_layer {
     int4* tiles = nullptr;
     jx::ActQ8 xq, hq, hqs;
     float *hf = nullptr, *hfs = nullptr, *y = nullptr, *ysh = nullptr;
+    int* done = nullptr;  // zeroed counter for the last-block pattern of the small-n router
     int last_n = 0;
     Prof prof;
+    hipStream_t own = nullptr;  // used when the caller passes the null stream
+    struct GraphKey {
+        int n;
+        const float* x;
+        float* out;
+        uint32_t flags;
+        bool operator<(const GraphKey& o) const {
+            if (n != o.n) return n < o.n;
+            if (x != o.x) return x < o.x;
+            if (out != o.out) return out < o.out;
+            return flags < o.flags;
+        }
+    };
+    std::map<GraphKey, hipGraphExec_t> graphs;
+    bool use_graphs = true;
 };
 
 struct jx_qmatrix {
@@ -152,6 +169,9 @@ namespace {
 
 int ensure_workspace(jx_moe_layer* L, int n) {
     if (n <= L->cap) return JX_OK;
+    // captured graphs hold the old buffer addresses
+    for (auto& kv : L->graphs) (void)hipGraphExecDestroy(kv.second);
+    L->graphs.clear();
     const int cap = std::max(n, L->cap * 2);
     const size_t nk = (size_t)cap * L->k;
     int r;
@@ -211,6 +231,9 @@ void free_layer(jx_moe_layer* L) {
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     for (auto ev : L->prof.pool) (void)hipEventDestroy(ev);
+    for (auto& kv : L->graphs) (void)hipGraphExecDestroy(kv.second);
+    if (L->done) (void)hipFree(L->done);
+    if (L->own) (void)hipStreamDestroy(L->own);
     delete L;
 }
 
@@ -261,11 +284,15 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     const int E = L->E, k = L->k, d = L->d;
     const int nk = n * k;
     jx::RouteArgs ra{xdev, n, d, E, k, L->router, L->bias, L->shgate, L->xq, L->ids, L->probs, L->shscale, L->logits};
-    {
-        Launch l(L, "route", st);
-        jx::launch_route(ra, st);
-    }
-    {
+    if (jx::route_small_fits(n, d, E)) {
+        Launch l(L, "route_dispatch", st);
+        jx::launch_route_small(ra, L->done, L->counts, L->offs, L->act, L->n_act, L->pair_f, L->pos_of, L->tiles,
+                               L->n_tiles, st);
+    } else {
+        {
+            Launch l(L, "route", st);
+            jx::launch_route(ra, st);
+        }
         Launch l(L, "dispatch", st);
         jx::launch_dispatch(L->ids, nk, E, k, L->counts, L->offs, L->act, L->n_act, L->pair_f, L->pos_of, L->tiles,
                             L->n_tiles, st);
@@ -294,7 +321,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         }
         Launch l(L, L->down_f32 ? "down_gemv_f32" : "down_mfma", st);
         if (L->down_f32)
-            jx::launch_gemv_down(L->down.m, L->hq, L->hf, (int)fpad, grp, slots, 4, 1, L->y, 0, st);
+            jx::launch_gemv_down(L->down.m, L->hq, L->hf, (int)fpad, grp, slots, 4, L->y, st);
         else
             jx::launch_mfma_down(L->down.m, L->hq, grp, tiles_ub, L->y, st);
     } else {
@@ -303,8 +330,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
             jx::launch_gemv_gateup(L->gate.m, L->up.m, L->xq, grp, slots, tb, L->hq, L->down_f32 ? L->hf : nullptr, st);
         }
         Launch l(L, L->down_f32 ? "down_gemv_f32" : "down_gemv", st);
-        jx::launch_gemv_down(L->down.m, L->hq, L->down_f32 ? L->hf : nullptr, (int)fpad, grp, slots, tb, 1, L->y, 0,
-                             st);
+        jx::launch_gemv_down(L->down.m, L->hq, L->down_f32 ? L->hf : nullptr, (int)fpad, grp, slots, tb, L->y, st);
     }
     if (L->shared) {
         jx::Groups sg;
@@ -321,7 +347,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
             }
             Launch l(L, "shared_down", st);
             if (L->sdown_f32)
-                jx::launch_gemv_down(L->sdown.m, L->hqs, L->hfs, (int)fspad, sg, 1, 4, 1, L->ysh, 0, st);
+                jx::launch_gemv_down(L->sdown.m, L->hqs, L->hfs, (int)fspad, sg, 1, 4, L->ysh, st);
             else
                 jx::launch_mfma_down(L->sdown.m, L->hqs, sg, (n + jx::MFMA_BN - 1) / jx::MFMA_BN, L->ysh, st);
         } else {
@@ -331,14 +357,13 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
                                        st);
             }
             Launch l(L, "shared_down", st);
-            jx::launch_gemv_down(L->sdown.m, L->hqs, L->sdown_f32 ? L->hfs : nullptr, (int)fspad, sg, 1, tb, 1, L->ysh,
-                                 0, st);
+            jx::launch_gemv_down(L->sdown.m, L->hqs, L->sdown_f32 ? L->hfs : nullptr, (int)fspad, sg, 1, tb, L->ysh,
+                                 st);
         }
     }
     {
         Launch l(L, "combine", st);
-        jx::launch_combine(n, d, k, L->probs, L->pos_of, L->y, 1, 0, L->shared ? L->ysh : nullptr, 1, 0, L->shscale,
-                           outdev, st);
+        jx::launch_combine(n, d, k, L->probs, L->pos_of, L->y, L->shared ? L->ysh : nullptr, L->shscale, outdev, st);
     }
     HIPCHK(hipGetLastError());
     return JX_OK;
@@ -447,6 +472,10 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
         }
     }
     if ((r = ensure_workspace(L, 1)) != JX_OK) return bail(r);
+    if ((r = dalloc(L->done, 1)) != JX_OK) return bail(r);
+    if (hipMemset(L->done, 0, sizeof(int)) != hipSuccess) return bail(fail(JX_ERR_HIP, "counter init"));
+    if (hipStreamCreate(&L->own) != hipSuccess) return bail(fail(JX_ERR_HIP, "stream create"));
+    if (const char* g = std::getenv("JX_NO_GRAPH")) L->use_graphs = std::strcmp(g, "0") == 0;
     *out = L;
     return JX_OK;
 }
@@ -466,7 +495,7 @@ int jx_moe_forward(jx_moe_layer* L, const float* x, int32_t n_tok, float* out, i
     HIPCHK(hipSetDevice(L->device));
     int r = ensure_workspace(L, n_tok);
     if (r != JX_OK) return r;
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipStream_t st = stream ? reinterpret_cast<hipStream_t>(stream) : L->own;
     const bool dev = flags & JX_FWD_DEVICE_PTRS;
     const size_t xd = (size_t)n_tok * L->d;
     const float* xin = x;
@@ -476,7 +505,36 @@ int jx_moe_forward(jx_moe_layer* L, const float* x, int32_t n_tok, float* out, i
         xin = L->x;
         outp = L->out;
     }
-    if ((r = run_forward(L, xin, n_tok, outp, st, flags)) != JX_OK) return r;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    HIPCHK(hipStreamIsCapturing(st, &cap));
+    if (L->use_graphs && !L->prof.on && cap == hipStreamCaptureStatusNone) {
+        // the launch sequence depends only on (n, buffers, regime flags): replay a captured graph
+        const jx_moe_layer::GraphKey key{n_tok, xin, outp, flags & (JX_FWD_FORCE_GEMV | JX_FWD_FORCE_MFMA)};
+        auto it = L->graphs.find(key);
+        if (it == L->graphs.end()) {
+            HIPCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+            r = run_forward(L, xin, n_tok, outp, st, flags);
+            hipGraph_t g = nullptr;
+            const hipError_t e = hipStreamEndCapture(st, &g);
+            if (r != JX_OK) {
+                if (g) (void)hipGraphDestroy(g);
+                return r;
+            }
+            if (e != hipSuccess) return fail(JX_ERR_HIP, std::string("graph capture: ") + hipGetErrorString(e));
+            hipGraphExec_t ex = nullptr;
+            const hipError_t ei = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            if (ei != hipSuccess) return fail(JX_ERR_HIP, std::string("graph instantiate: ") + hipGetErrorString(ei));
+            if (L->graphs.size() >= 32) {
+                for (auto& kv : L->graphs) (void)hipGraphExecDestroy(kv.second);
+                L->graphs.clear();
+            }
+            it = L->graphs.emplace(key, ex).first;
+        }
+        HIPCHK(hipGraphLaunch(it->second, st));
+    } else if ((r = run_forward(L, xin, n_tok, outp, st, flags)) != JX_OK) {
+        return r;
+    }
     L->last_n = n_tok;
     const size_t nk = (size_t)n_tok * L->k;
     const hipMemcpyKind k2 = dev ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost;
@@ -584,10 +642,10 @@ int jx_matmul_quant_f32(jx_qmatrix* W, const float* x, float* out) {
         a.K = cols;
         if (!a.q || !a.s) return fail(JX_ERR_NOMEM, "scratch allocation");
         jx::launch_quantize_q8(xd, 1, cols, a, nullptr);
-        jx::launch_gemv_down(W->w.m, a, nullptr, 0, g, 1, 1, 1, yd, 0, nullptr);
+        jx::launch_gemv_down(W->w.m, a, nullptr, 0, g, 1, 1, yd, nullptr);
     } else {
         a.K = (int)kpad;
-        jx::launch_gemv_down(W->w.m, a, xd, (int)kpad, g, 1, 1, 1, yd, 0, nullptr);
+        jx::launch_gemv_down(W->w.m, a, xd, (int)kpad, g, 1, 1, yd, nullptr);
     }
     HIPCHK(hipGetLastError());
     HIPCHK(hipMemcpy(out, yd, (size_t)rows * 4, hipMemcpyDeviceToHost));

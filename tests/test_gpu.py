@@ -174,3 +174,21 @@ def test_edge_cases(moe, port):
         assert np.array_equal(c, [70, 70])
         assert rel_err(o, want2) <= REL_TOL
     L2.close()
+
+
+def test_graph_replays_match_eager(moe, monkeypatch):
+    """Captured-graph replays, interleaved with eager launches and syncs, equal the eager result bit for bit."""
+    cfg, lw = layer("dsv2lite")
+    monkeypatch.setenv("JX_NO_GRAPH", "1")
+    eager = moe.MoELayer.from_weights(lw)
+    monkeypatch.delenv("JX_NO_GRAPH")
+    graphed = moe.MoELayer.from_weights(lw)
+    for n in (1, 32, 1):
+        x = synth.make_tokens(cfg, n, seed=n + 11)
+        want = eager.forward(x)
+        for rep in range(3):
+            got = graphed.forward(x)
+            assert all(np.array_equal(a, b) for a, b in zip(got, want)), f"replay {rep} differs (n={n})"
+            eager.forward(synth.make_tokens(cfg, 3, seed=rep))  # eager work between replays
+    eager.close()
+    graphed.close()
