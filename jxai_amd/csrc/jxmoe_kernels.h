@@ -14,9 +14,7 @@ namespace jx {
 //   Q8_0  qs  [e][rt][b][2 halves][32 rows][16 B]  sc  [e][rt][b][32] fp16 d
 //   Q4_K  qs  [e][rt][sb][4 pairs][2 halves][32 rows][16 B]
 //         sc  [e][rt][sb][32 rows][16 B]  = (d, dmin, scales[12]) headers
-//         kt  [e][rt][sb][8 sub-blocks][32 rows] float2 (d*sc, dmin*m)
-// Byte totals of qs+sc equal the GGUF tensor (18/34/144 B per block); kt is a
-// decoded copy of the Q4_K scales used only by the MFMA prefill kernels.
+// Byte totals of qs+sc equal the GGUF tensor (18/34/144 B per block).
 struct QMat {
     int type = 0;
     int rows = 0;       // per expert, multiple of 32
@@ -25,8 +23,7 @@ struct QMat {
     int nkb = 0;        // K-units: 32-blocks (Q4_0/Q8_0) or 256-super-blocks (Q4_K)
     const uint8_t* qs = nullptr;
     const uint8_t* sc = nullptr;
-    const float2* kt = nullptr;
-    size_t qs_es = 0, sc_es = 0, kt_es = 0;  // per-expert strides (bytes, bytes, float2s)
+    size_t qs_es = 0, sc_es = 0;  // per-expert strides (bytes)
     int n_mats = 0;     // experts held
 };
 
@@ -36,6 +33,19 @@ struct ActQ8 {
     int8_t* q = nullptr;
     float2* s = nullptr;
     int K = 0;
+};
+
+// Q8_0 activations in the form the matrix-core GEMMs consume, rows padded to
+// whole 256-element units (KU = ceil(K/256)):
+//   q16 [rows][KU*256]  fp16 bit patterns of the integer quants
+//   dx  [rows][KU*8]    block scales (fp16-truncated, widened to fp32)
+//   xm  [rows][KU][16]  per unit: fp16 hi x8, then lo x8, of dx * sum(q) per block
+struct ActH {
+    uint16_t* q16 = nullptr;
+    float* dx = nullptr;
+    uint16_t* xm = nullptr;
+    int K = 0;
+    int KU = 0;
 };
 
 // Token -> expert grouping produced by the dispatch kernel.
@@ -52,7 +62,8 @@ struct Groups {
     int n_tok = 0;
 };
 
-constexpr int MFMA_BN = 32;  // pairs per MFMA tile
+constexpr int MFMA_BN = 128;  // pairs per matrix-core GEMM tile
+constexpr int MFMA_MIN_SHARED_TOKENS = 32;  // shared expert on the matrix cores from this many tokens
 
 struct RouteArgs {
     const float* x;        // [n][d]
@@ -60,7 +71,8 @@ struct RouteArgs {
     const float* router;   // [E][d]
     const float* bias;     // [E] or null
     const float* shgate;   // [d] or null
-    ActQ8 xq;              // out: Q8_0 of x
+    ActQ8 xq;              // out: Q8_0 of x (int8 + (scale, sum))
+    ActH xh;               // out: Q8_0 of x for the matrix-core GEMMs (q16 == null: not written)
     int* ids;              // [n][k]
     float* probs;          // [n][k]
     float* shscale;        // [n]
@@ -78,11 +90,11 @@ void launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Gro
 // Decode regime: down projection over Q8_0 (hq) or fp32 (hf) activations into y[pair][d].
 void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp,
                       int slots, int tb, float* y, hipStream_t st);
-// Prefill regime: int8 MFMA grouped GEMMs over the dispatch tile table.
-void launch_mfma_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int tiles_ub,
-                        ActQ8 hq, float* hf, hipStream_t st);
-void launch_mfma_down(const QMat& dn, const ActQ8& hq, const Groups& grp, int tiles_ub, float* y,
-                      hipStream_t st);
+// Prefill regime: matrix-core grouped GEMMs over the dispatch tile table.
+// gate/up writes SwiGLU(h) as ActH (hq.q16 != null) and/or fp32 (hf != null).
+void launch_mfma_gateup(const QMat& g, const QMat& u, const ActH& xin, const Groups& grp, int tiles_ub,
+                        const ActH& hq, float* hf, hipStream_t st);
+void launch_mfma_down(const QMat& dn, const ActH& hin, const Groups& grp, int tiles_ub, float* y, hipStream_t st);
 
 // out[t] = sum_s p[t][s] * y[pos(t,s)] (+ shscale[t] * ysh[t]), fma in selection order.
 void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
@@ -102,6 +114,6 @@ void launch_quantize_q8(const float* x, int rows, int K, ActQ8 out, hipStream_t 
 
 // Repack a GGUF block matrix set [n_mats][rows][cols] (already on the device
 // as raw bytes) into the QMat layout.
-void launch_repack(const uint8_t* raw, QMat m, uint8_t* qs, uint8_t* sc, float2* kt, hipStream_t st);
+void launch_repack(const uint8_t* raw, QMat m, uint8_t* qs, uint8_t* sc, hipStream_t st);
 
 }  // namespace jx

@@ -12,6 +12,46 @@ constexpr int ROUTE_THREADS = 512;
 constexpr int MAX_E = 512;
 constexpr int MAX_K = 32;
 
+// Q8_0 of one 32-block held one value per lane of a half-wave
+// (quantize_row_q8_0, src/quant.cpp:1029-1045): amax, d = amax/127 (IEEE
+// division), id = 1/d, q = clamp(round-half-away(x*id)), stored scale =
+// truncated fp16 of d.  Writes the int8 form (+ the block sum of q, which
+// feeds the Q4_0 -8 offset and the Q4_K min term) and, when requested, the
+// matrix-core form (fp16 quants, scale, exact bf16 3-piece split of
+// scale * sum(q)).
+__device__ __forceinline__ void quant_block(float v, int l32, bool ok, const ActQ8& o8, const ActH& oh, size_t row,
+                                            int b) {
+    const float amax = wave_max32(__builtin_fabsf(v));
+    const float dd = amax / 127.0f;
+    const float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
+    float r = round_away(v * id);
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    const int q = (int)r;
+    const int s = wave_sum32i(q);
+    if (!ok) return;
+    const float dw = f16_to_f32(f32_to_f16_trunc(dd));
+    if (o8.q) {
+        o8.q[row * o8.K + b * 32 + l32] = (int8_t)q;
+        if (l32 == 0) o8.s[row * (o8.K / 32) + b] = make_float2(dw, (float)s);
+    }
+    if (oh.q16) {
+        const _Float16 qh = (_Float16)r;
+        oh.q16[row * (size_t)oh.KU * 256 + b * 32 + l32] = __builtin_bit_cast(uint16_t, qh);
+        if (l32 == 0) {
+            oh.dx[row * (size_t)oh.KU * 8 + b] = dw;
+            const float X = dw * (float)s;  // exact: 11-bit scale x |sum| < 2^12
+            const uint32_t bh = __float_as_uint(X) & 0xFFFF0000u;
+            const float r1 = X - __uint_as_float(bh);
+            const uint32_t bm = __float_as_uint(r1) & 0xFFFF0000u;
+            const float r2 = r1 - __uint_as_float(bm);
+            uint16_t* xm = oh.xm + row * (size_t)oh.KU * 32 + (b / 8) * 32 + (b % 8);
+            xm[0] = (uint16_t)(bh >> 16);
+            xm[8] = (uint16_t)(bm >> 16);
+            xm[16] = (uint16_t)(__float_as_uint(r2) >> 16);
+        }
+    }
+}
+
 // One block per token.
 //  1. x -> LDS.
 //  2. Q8_0 of x, 32 lanes per block (quantize_row_q8_0, src/quant.cpp:1029-1045):
@@ -47,18 +87,7 @@ __global__ void __launch_bounds__(ROUTE_THREADS) k_route(RouteArgs a) {
         for (int bb = wave * 2; bb < nb; bb += (ROUTE_THREADS / 64) * 2) {
             const int b = bb + half;
             const bool ok = b < nb;
-            const float v = ok ? xs[b * 32 + l32] : 0.0f;
-            const float amax = wave_max32(__builtin_fabsf(v));
-            const float dd = amax / 127.0f;
-            const float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
-            float r = round_away(v * id);
-            r = fminf(fmaxf(r, -127.0f), 127.0f);
-            const int q = (int)r;
-            const int s = wave_sum32i(q);
-            if (ok) {
-                a.xq.q[(size_t)t * d + b * 32 + l32] = (int8_t)q;
-                if (l32 == 0) a.xq.s[(size_t)t * nb + b] = make_float2(f16_to_f32(f32_to_f16_trunc(dd)), (float)s);
-            }
+            quant_block(ok ? xs[b * 32 + l32] : 0.0f, l32, ok, a.xq, a.xh, (size_t)t, b);
         }
     }
 
@@ -186,20 +215,9 @@ k_route_small(RouteArgs a, int* done, int* counts, int* offs, int* act, int* n_a
         const int b0 = r * per, b1 = min(tot, b0 + per);
         const int lane = tid & 63, wave = tid >> 6, half = lane >> 5, l32 = lane & 31;
         for (int bb = b0 + wave * 2; bb < b1; bb += (RS_THREADS / 64) * 2) {
-            const int b = bb + half;
+            const int b = bb + half;  // token-major: b = t*nb + block
             const bool ok = b < b1;
-            const float v = ok ? xs[(size_t)b * 32 + l32] : 0.0f;
-            const float amax = wave_max32(__builtin_fabsf(v));
-            const float dd = amax / 127.0f;
-            const float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
-            float rr = round_away(v * id);
-            rr = fminf(fmaxf(rr, -127.0f), 127.0f);
-            const int q = (int)rr;
-            const int sq = wave_sum32i(q);
-            if (ok) {
-                a.xq.q[(size_t)b * 32 + l32] = (int8_t)q;  // token-major: b = t*nb + block
-                if (l32 == 0) a.xq.s[b] = make_float2(f16_to_f32(f32_to_f16_trunc(dd)), (float)sq);
-            }
+            quant_block(ok ? xs[(size_t)b * 32 + l32] : 0.0f, l32, ok, a.xq, a.xh, (size_t)(b / nb), b % nb);
         }
     }
 
@@ -415,18 +433,7 @@ __global__ void __launch_bounds__(256) k_quant_q8(const float* x, int rows, int 
     const int half = (threadIdx.x >> 5) & 1, l32 = threadIdx.x & 31;
     const size_t blk = gid * 2 + half;
     const bool ok = blk < (size_t)rows * nb;
-    const float v = ok ? x[blk * 32 + l32] : 0.0f;
-    const float amax = wave_max32(__builtin_fabsf(v));
-    const float dd = amax / 127.0f;
-    const float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
-    float r = round_away(v * id);
-    r = fminf(fmaxf(r, -127.0f), 127.0f);
-    const int q = (int)r;
-    const int s = wave_sum32i(q);
-    if (ok) {
-        out.q[blk * 32 + l32] = (int8_t)q;
-        if (l32 == 0) out.s[blk] = make_float2(f16_to_f32(f32_to_f16_trunc(dd)), (float)s);
-    }
+    quant_block(ok ? x[blk * 32 + l32] : 0.0f, l32, ok, out, ActH{}, blk / nb, (int)(blk % nb));
 }
 
 void launch_quantize_q8(const float* x, int rows, int K, ActQ8 out, hipStream_t st) {
@@ -437,7 +444,7 @@ void launch_quantize_q8(const float* x, int rows, int K, ActQ8 out, hipStream_t 
 
 // One thread per (matrix, row, K-unit): scatter a GGUF block into the tile
 // layout described in jxmoe_kernels.h.
-__global__ void __launch_bounds__(256) k_repack(const uint8_t* raw, QMat m, uint8_t* qs, uint8_t* sc, float2* kt) {
+__global__ void __launch_bounds__(256) k_repack(const uint8_t* raw, QMat m, uint8_t* qs, uint8_t* sc) {
     const size_t units = (size_t)m.n_mats * m.rows * m.nkb;
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= units) return;
@@ -470,19 +477,12 @@ __global__ void __launch_bounds__(256) k_repack(const uint8_t* raw, QMat m, uint
                 uint8_t* dq = qs + (((tile * 4 + p) * 2 + h) * 32 + mm) * 16;
                 for (int i = 0; i < 16; ++i) dq[i] = src[16 + 32 * p + 16 * h + i];
             }
-        const float d = f16_to_f32((uint32_t)src[0] | ((uint32_t)src[1] << 8));
-        const float dmin = f16_to_f32((uint32_t)src[2] | ((uint32_t)src[3] << 8));
-        for (int j = 0; j < 8; ++j) {
-            int s, mn;
-            q4k_scale_min(j, src + 4, s, mn);
-            kt[(tile * 8 + j) * 32 + mm] = make_float2(d * (float)s, dmin * (float)mn);
-        }
     }
 }
 
-void launch_repack(const uint8_t* raw, QMat m, uint8_t* qs, uint8_t* sc, float2* kt, hipStream_t st) {
+void launch_repack(const uint8_t* raw, QMat m, uint8_t* qs, uint8_t* sc, hipStream_t st) {
     const size_t units = (size_t)m.n_mats * m.rows * m.nkb;
-    hipLaunchKernelGGL(k_repack, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, st, raw, m, qs, sc, kt);
+    hipLaunchKernelGGL(k_repack, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, st, raw, m, qs, sc);
 }
 
 }  // namespace jx

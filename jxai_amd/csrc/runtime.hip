@@ -56,13 +56,10 @@ struct DevMat {
     jx::QMat m;
     uint8_t* qs = nullptr;
     uint8_t* sc = nullptr;
-    float2* kt = nullptr;
     void release() {
         if (qs) (void)hipFree(qs);
         if (sc) (void)hipFree(sc);
-        if (kt) (void)hipFree(kt);
         qs = sc = nullptr;
-        kt = nullptr;
     }
 };
 
@@ -83,19 +80,16 @@ int upload_matrix(int type, int n_mats, int rows, int cols, const void* host, De
     const size_t sc_u = type == jx::T_Q4_K ? 16 : 2;
     m.qs_es = units * qs_u;
     m.sc_es = units * sc_u;
-    m.kt_es = type == jx::T_Q4_K ? units * 8 : 0;
     const size_t raw_bytes = (size_t)n_mats * rows * row_bytes(type, cols);
     uint8_t* raw = nullptr;
     HIPCHK(hipMalloc(&out.qs, m.qs_es * n_mats));
     HIPCHK(hipMalloc(&out.sc, m.sc_es * n_mats));
-    if (m.kt_es) HIPCHK(hipMalloc(&out.kt, m.kt_es * n_mats * sizeof(float2)));
     HIPCHK(hipMalloc(&raw, raw_bytes));
     hipError_t e = hipMemcpyAsync(raw, host, raw_bytes, hipMemcpyHostToDevice, st);
     if (e == hipSuccess) {
         m.qs = out.qs;
         m.sc = out.sc;
-        m.kt = out.kt;
-        jx::launch_repack(raw, m, out.qs, out.sc, out.kt, st);
+        jx::launch_repack(raw, m, out.qs, out.sc, st);
         e = hipGetLastError();
     }
     if (e == hipSuccess) e = hipStreamSynchronize(st);
@@ -112,6 +106,27 @@ int dalloc(T*& p, size_t n) {
     HIPCHK(hipMalloc(&p, n * sizeof(T)));
     return JX_OK;
 }
+
+// Matrix-core activation buffers for `rows` rows of K (rows padded to whole
+// 256-element units).
+struct DevActH {
+    jx::ActH a;
+    void release() {
+        if (a.q16) (void)hipFree(a.q16);
+        if (a.dx) (void)hipFree(a.dx);
+        if (a.xm) (void)hipFree(a.xm);
+        a = jx::ActH{};
+    }
+    int alloc(size_t rows, int K) {
+        release();
+        a.K = K;
+        a.KU = (K + 255) / 256;
+        HIPCHK(hipMalloc(&a.q16, rows * a.KU * 256 * sizeof(uint16_t)));
+        HIPCHK(hipMalloc(&a.dx, rows * a.KU * 8 * sizeof(float)));
+        HIPCHK(hipMalloc(&a.xm, rows * a.KU * 32 * sizeof(uint16_t)));
+        return JX_OK;
+    }
+};
 
 struct Prof {
     bool on = false;
@@ -138,6 +153,7 @@ struct jx_moe_layer {
         *pos_of = nullptr, *n_tiles = nullptr;
     int4* tiles = nullptr;
     jx::ActQ8 xq, hq, hqs;
+    DevActH xh, hh, hhs;  // matrix-core forms of x, h, shared h
     float *hf = nullptr, *hfs = nullptr, *y = nullptr, *ysh = nullptr;
     int* done = nullptr;  // zeroed counter for the last-block pattern of the small-n router
     int last_n = 0;
@@ -194,6 +210,14 @@ int ensure_workspace(jx_moe_layer* L, int n) {
     WS(L->pos_of, nk);
     WS(L->n_tiles, 1);
     WS(L->tiles, nk / jx::MFMA_BN + std::min<size_t>(L->E, nk) + 1);
+    if ((r = L->xh.alloc((size_t)cap, L->d)) != JX_OK || (r = L->hh.alloc(nk, L->F)) != JX_OK) {
+        L->cap = 0;
+        return r;
+    }
+    if (L->shared && (r = L->hhs.alloc((size_t)cap, L->Fs)) != JX_OK) {
+        L->cap = 0;
+        return r;
+    }
     WS(L->xq.q, (size_t)cap * L->d);
     WS(L->xq.s, (size_t)cap * L->d / 32);
     L->xq.K = L->d;
@@ -230,6 +254,9 @@ void free_layer(jx_moe_layer* L) {
                     L->xq.q, L->xq.s, L->hq.q, L->hq.s, L->hqs.q, L->hqs.s, L->hf, L->hfs, L->y, L->ysh};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
+    L->xh.release();
+    L->hh.release();
+    L->hhs.release();
     for (auto ev : L->prof.pool) (void)hipEventDestroy(ev);
     for (auto& kv : L->graphs) (void)hipGraphExecDestroy(kv.second);
     if (L->done) (void)hipFree(L->done);
@@ -283,7 +310,12 @@ constexpr int MFMA_MIN_PAIRS_PER_EXPERT = 16;
 int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStream_t st, uint32_t flags) {
     const int E = L->E, k = L->k, d = L->d;
     const int nk = n * k;
-    jx::RouteArgs ra{xdev, n, d, E, k, L->router, L->bias, L->shgate, L->xq, L->ids, L->probs, L->shscale, L->logits};
+    bool mfma = (size_t)nk >= (size_t)MFMA_MIN_PAIRS_PER_EXPERT * E;
+    if (flags & JX_FWD_FORCE_GEMV) mfma = false;
+    if (flags & JX_FWD_FORCE_MFMA) mfma = true;
+    const bool smfma = L->shared && n >= jx::MFMA_MIN_SHARED_TOKENS && !(flags & JX_FWD_FORCE_GEMV);
+    jx::RouteArgs ra{xdev, n, d, E, k, L->router, L->bias, L->shgate, L->xq, (mfma || smfma) ? L->xh.a : jx::ActH{},
+                     L->ids, L->probs, L->shscale, L->logits};
     if (jx::route_small_fits(n, d, E)) {
         Launch l(L, "route_dispatch", st);
         jx::launch_route_small(ra, L->done, L->counts, L->offs, L->act, L->n_act, L->pair_f, L->pos_of, L->tiles,
@@ -307,9 +339,6 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     grp.n_tiles = L->n_tiles;
     grp.top_k = k;
     grp.n_tok = n;
-    bool mfma = (size_t)nk >= (size_t)MFMA_MIN_PAIRS_PER_EXPERT * E;
-    if (flags & JX_FWD_FORCE_GEMV) mfma = false;
-    if (flags & JX_FWD_FORCE_MFMA) mfma = true;
     const int slots = std::min(E, nk);
     const int tb = n == 1 ? 1 : 4;
     const int tiles_ub = nk / jx::MFMA_BN + slots;
@@ -317,13 +346,14 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     if (mfma) {
         {
             Launch l(L, "gateup_mfma", st);
-            jx::launch_mfma_gateup(L->gate.m, L->up.m, L->xq, grp, tiles_ub, L->hq, L->down_f32 ? L->hf : nullptr, st);
+            jx::launch_mfma_gateup(L->gate.m, L->up.m, L->xh.a, grp, tiles_ub, L->down_f32 ? jx::ActH{} : L->hh.a,
+                                   L->down_f32 ? L->hf : nullptr, st);
         }
         Launch l(L, L->down_f32 ? "down_gemv_f32" : "down_mfma", st);
         if (L->down_f32)
             jx::launch_gemv_down(L->down.m, L->hq, L->hf, (int)fpad, grp, slots, 4, L->y, st);
         else
-            jx::launch_mfma_down(L->down.m, L->hq, grp, tiles_ub, L->y, st);
+            jx::launch_mfma_down(L->down.m, L->hh.a, grp, tiles_ub, L->y, st);
     } else {
         {
             Launch l(L, "gateup_gemv", st);
@@ -338,18 +368,18 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         sg.n_tok = n;
         sg.top_k = 1;
         const size_t fspad = ((size_t)L->Fs + 255) / 256 * 256;
-        const bool smfma = n >= jx::MFMA_BN && !(flags & JX_FWD_FORCE_GEMV);
         if (smfma) {
+            const int st_ub = (n + jx::MFMA_BN - 1) / jx::MFMA_BN;
             {
                 Launch l(L, "shared_gateup_mfma", st);
-                jx::launch_mfma_gateup(L->sgate.m, L->sup.m, L->xq, sg, (n + jx::MFMA_BN - 1) / jx::MFMA_BN, L->hqs,
+                jx::launch_mfma_gateup(L->sgate.m, L->sup.m, L->xh.a, sg, st_ub, L->sdown_f32 ? jx::ActH{} : L->hhs.a,
                                        L->sdown_f32 ? L->hfs : nullptr, st);
             }
             Launch l(L, "shared_down", st);
             if (L->sdown_f32)
                 jx::launch_gemv_down(L->sdown.m, L->hqs, L->hfs, (int)fspad, sg, 1, 4, L->ysh, st);
             else
-                jx::launch_mfma_down(L->sdown.m, L->hqs, sg, (n + jx::MFMA_BN - 1) / jx::MFMA_BN, L->ysh, st);
+                jx::launch_mfma_down(L->sdown.m, L->hhs.a, sg, st_ub, L->ysh, st);
         } else {
             {
                 Launch l(L, "shared_gateup_gemv", st);
