@@ -261,7 +261,7 @@ __device__ __forceinline__ void group_of(const Groups& g, int slot, int& e, int&
 }
 
 __device__ __forceinline__ int token_of(const Groups& g, int p) {
-    return g.identity ? p : g.pair_f[p] / g.top_k;
+    return g.identity ? p : g.pair_tok[p];
 }
 
 // Q8_0 of one 32-row block of h held by lanes 0..31 (quantize_row_q8_0).

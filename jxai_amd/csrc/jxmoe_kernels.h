@@ -35,17 +35,21 @@ struct ActQ8 {
     int K = 0;
 };
 
-// Q8_0 activations in the form the matrix-core GEMMs consume, rows padded to
-// whole 256-element units (KU = ceil(K/256)):
-//   q16 [rows][KU*256]  fp16 bit patterns of the integer quants
-//   dx  [rows][KU*8]    block scales (fp16-truncated, widened to fp32)
-//   xm  [rows][KU][16]  per unit: fp16 hi x8, then lo x8, of dx * sum(q) per block
+// Q8_0 activations in the form the matrix-core GEMMs consume (K % 128 == 0):
+//   hl [rows][KH][256]   per 128-element half-unit: fp16 hi x128, then lo x128,
+//                        of dx * q * 2^-E (an exact split of the dequantized
+//                        value scaled into fp16 range)
+//   pe [rows][KH]        2^E of each half-unit (E = exponent of its largest
+//                        block scale - 7, so |dx * q| * 2^-E < 2^15)
+//   xm [rows][KU][3][8]  per 256-element unit: bf16 pieces (hi, mid, lo) of
+//                        dx * sum(q) for its 8 blocks (Q4_K min term, unscaled)
 struct ActH {
-    uint16_t* q16 = nullptr;
-    float* dx = nullptr;
+    uint16_t* hl = nullptr;
+    float* pe = nullptr;
     uint16_t* xm = nullptr;
     int K = 0;
-    int KU = 0;
+    int KH = 0;  // K / 128
+    int KU = 0;  // ceil(K / 256)
 };
 
 // Token -> expert grouping produced by the dispatch kernel.
@@ -54,7 +58,7 @@ struct Groups {
     const int* offs = nullptr;    // [E+1]
     const int* act = nullptr;     // [E] active experts, increasing id
     const int* n_act = nullptr;   // [1]
-    const int* pair_f = nullptr;  // [P] sorted pair -> flat index t*k + s
+    const int* pair_tok = nullptr;  // [P] sorted pair -> token
     const int4* tiles = nullptr;  // [T] (expert, first pair, pair count, 0) MFMA tiles
     const int* n_tiles = nullptr; // [1]
     int top_k = 1;
@@ -72,7 +76,7 @@ struct RouteArgs {
     const float* bias;     // [E] or null
     const float* shgate;   // [d] or null
     ActQ8 xq;              // out: Q8_0 of x (int8 + (scale, sum))
-    ActH xh;               // out: Q8_0 of x for the matrix-core GEMMs (q16 == null: not written)
+    ActH xh;               // out: Q8_0 of x for the matrix-core GEMMs (hl == null: not written)
     int* ids;              // [n][k]
     float* probs;          // [n][k]
     float* shscale;        // [n]
@@ -81,7 +85,7 @@ struct RouteArgs {
 
 void launch_route(const RouteArgs& a, hipStream_t st);
 void launch_dispatch(const int* ids, int nk, int E, int top_k, int* counts, int* offs, int* act, int* n_act,
-                     int* pair_f, int* pos_of, int4* tiles, int* n_tiles, hipStream_t st);
+                     int* pair_tok, int* pos_of, int4* tiles, int* n_tiles, hipStream_t st);
 
 // Decode regime: gate+up dequant-GEMV with SwiGLU and Q8_0 re-quantization.
 // Output rows are sorted pairs (routed) or tokens (shared).
@@ -91,7 +95,7 @@ void launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Gro
 void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp,
                       int slots, int tb, float* y, hipStream_t st);
 // Prefill regime: matrix-core grouped GEMMs over the dispatch tile table.
-// gate/up writes SwiGLU(h) as ActH (hq.q16 != null) and/or fp32 (hf != null).
+// gate/up writes SwiGLU(h) as ActH (hq.hl != null) and/or fp32 (hf != null).
 void launch_mfma_gateup(const QMat& g, const QMat& u, const ActH& xin, const Groups& grp, int tiles_ub,
                         const ActH& hq, float* hf, hipStream_t st);
 void launch_mfma_down(const QMat& dn, const ActH& hin, const Groups& grp, int tiles_ub, float* y, hipStream_t st);
@@ -106,11 +110,14 @@ void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, 
 // kernel leaves at zero.
 constexpr int ROUTE_SMALL_MAX_N = 2;
 bool route_small_fits(int n, int d, int E);
-void launch_route_small(const RouteArgs& a, int* done, int* counts, int* offs, int* act, int* n_act, int* pair_f,
+void launch_route_small(const RouteArgs& a, int* done, int* counts, int* offs, int* act, int* n_act, int* pair_tok,
                         int* pos_of, int4* tiles, int* n_tiles, hipStream_t st);
 
 // Q8_0 of rows x K fp32 (row-major, K % 32 == 0).
 void launch_quantize_q8(const float* x, int rows, int K, ActQ8 out, hipStream_t st);
+
+// Matrix-core form of existing Q8_0 activations (int8 quants + (scale, sum)).
+void launch_q8_to_acth(const ActQ8& in, int rows, ActH out, hipStream_t st);
 
 // Repack a GGUF block matrix set [n_mats][rows][cols] (already on the device
 // as raw bytes) into the QMat layout.

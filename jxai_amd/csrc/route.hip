@@ -15,12 +15,10 @@ constexpr int MAX_K = 32;
 // Q8_0 of one 32-block held one value per lane of a half-wave
 // (quantize_row_q8_0, src/quant.cpp:1029-1045): amax, d = amax/127 (IEEE
 // division), id = 1/d, q = clamp(round-half-away(x*id)), stored scale =
-// truncated fp16 of d.  Writes the int8 form (+ the block sum of q, which
-// feeds the Q4_0 -8 offset and the Q4_K min term) and, when requested, the
-// matrix-core form (fp16 quants, scale, exact bf16 3-piece split of
-// scale * sum(q)).
-__device__ __forceinline__ void quant_block(float v, int l32, bool ok, const ActQ8& o8, const ActH& oh, size_t row,
-                                            int b) {
+// truncated fp16 of d.  Writes the int8 quants and (scale, block sum of q);
+// the sum feeds the Q4_0 -8 offset and the Q4_K min term.  Returns q.
+__device__ __forceinline__ int quant_block(float v, int l32, bool ok, const ActQ8& o8, size_t row, int b,
+                                           float2* scale_out = nullptr) {
     const float amax = wave_max32(__builtin_fabsf(v));
     const float dd = amax / 127.0f;
     const float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
@@ -28,23 +26,43 @@ __device__ __forceinline__ void quant_block(float v, int l32, bool ok, const Act
     r = fminf(fmaxf(r, -127.0f), 127.0f);
     const int q = (int)r;
     const int s = wave_sum32i(q);
-    if (!ok) return;
-    const float dw = f16_to_f32(f32_to_f16_trunc(dd));
-    if (o8.q) {
+    if (ok) {
+        const float2 sv = make_float2(f16_to_f32(f32_to_f16_trunc(dd)), (float)s);
         o8.q[row * o8.K + b * 32 + l32] = (int8_t)q;
-        if (l32 == 0) o8.s[row * (o8.K / 32) + b] = make_float2(dw, (float)s);
-    }
-    if (oh.q16) {
-        const _Float16 qh = (_Float16)r;
-        oh.q16[row * (size_t)oh.KU * 256 + b * 32 + l32] = __builtin_bit_cast(uint16_t, qh);
         if (l32 == 0) {
-            oh.dx[row * (size_t)oh.KU * 8 + b] = dw;
-            const float X = dw * (float)s;  // exact: 11-bit scale x |sum| < 2^12
+            o8.s[row * (o8.K / 32) + b] = sv;
+            if (scale_out) *scale_out = sv;
+        }
+    }
+    return q;
+}
+
+// Matrix-core form (ActH) of one activation row from its Q8_0 quants q[K] and
+// (scale, sum) per 32-block, written by the NTH threads of one block.  Per
+// 128-element half-unit E = exponent(max block scale) - 7, so every
+// dx * q * 2^-E (exact in fp32: an 11-bit scale times |q| <= 127) is below
+// 2^15 and splits exactly into fp16 hi + lo.
+template <int NTH>
+__device__ void write_acth_row(const int8_t* q, const float2* sc, int K, const ActH& o, size_t row, int tid) {
+    const int KH = K / 128;
+    for (int i = tid; i < K; i += NTH) {
+        const int b = i >> 5, hh = i >> 7;
+        const float M = fmaxf(fmaxf(sc[4 * hh].x, sc[4 * hh + 1].x), fmaxf(sc[4 * hh + 2].x, sc[4 * hh + 3].x));
+        const int E = (M > 0.0f) ? (int)((__float_as_uint(M) >> 23) & 0xFF) - 127 - 7 : 0;
+        const float v = sc[b].x * (float)q[i] * __uint_as_float((uint32_t)(127 - E) << 23);
+        const _Float16 hi = (_Float16)v;
+        const _Float16 lo = (_Float16)(v - (float)hi);
+        uint16_t* hl = o.hl + row * (size_t)KH * 256 + hh * 256 + (i & 127);
+        hl[0] = __builtin_bit_cast(uint16_t, hi);
+        hl[128] = __builtin_bit_cast(uint16_t, lo);
+        if ((i & 127) == 0) o.pe[row * (size_t)KH + hh] = __uint_as_float((uint32_t)(127 + E) << 23);
+        if ((i & 31) == 0) {
+            const float X = sc[b].x * sc[b].y;  // exact: 11-bit scale x |sum| < 2^12
             const uint32_t bh = __float_as_uint(X) & 0xFFFF0000u;
             const float r1 = X - __uint_as_float(bh);
             const uint32_t bm = __float_as_uint(r1) & 0xFFFF0000u;
             const float r2 = r1 - __uint_as_float(bm);
-            uint16_t* xm = oh.xm + row * (size_t)oh.KU * 32 + (b / 8) * 32 + (b % 8);
+            uint16_t* xm = o.xm + row * (size_t)o.KU * 24 + (b / 8) * 24 + (b % 8);
             xm[0] = (uint16_t)(bh >> 16);
             xm[8] = (uint16_t)(bm >> 16);
             xm[16] = (uint16_t)(__float_as_uint(r2) >> 16);
@@ -67,7 +85,7 @@ __device__ __forceinline__ void quant_block(float v, int l32, bool ok, const Act
 //  4. Top-k by rank counting (descending logit, ties by index) and softmax over
 //     the k selected logits (select_experts_cache_aware, src/tier.cpp:144-188).
 __global__ void __launch_bounds__(ROUTE_THREADS) k_route(RouteArgs a) {
-    extern __shared__ float xs[];  // d floats
+    extern __shared__ float xs[];  // d floats, then (matrix-core output) d int8 quants and d/32 (scale, sum)
     __shared__ float lg[MAX_E];
     __shared__ int sel[MAX_K];
     __shared__ float shl;
@@ -84,10 +102,17 @@ __global__ void __launch_bounds__(ROUTE_THREADS) k_route(RouteArgs a) {
     {
         const int lane = tid & 63, wave = tid >> 6, half = lane >> 5, l32 = lane & 31;
         const int nb = d / 32;
+        int8_t* qs = reinterpret_cast<int8_t*>(xs + d);
+        float2* ss = reinterpret_cast<float2*>(qs + d);
         for (int bb = wave * 2; bb < nb; bb += (ROUTE_THREADS / 64) * 2) {
             const int b = bb + half;
             const bool ok = b < nb;
-            quant_block(ok ? xs[b * 32 + l32] : 0.0f, l32, ok, a.xq, a.xh, (size_t)t, b);
+            const int q = quant_block(ok ? xs[b * 32 + l32] : 0.0f, l32, ok, a.xq, (size_t)t, b, ok ? ss + b : nullptr);
+            if (ok && a.xh.hl) qs[b * 32 + l32] = (int8_t)q;
+        }
+        if (a.xh.hl) {
+            __syncthreads();
+            write_acth_row<ROUTE_THREADS>(qs, ss, d, a.xh, (size_t)t, tid);
         }
     }
 
@@ -167,7 +192,18 @@ __global__ void __launch_bounds__(ROUTE_THREADS) k_route(RouteArgs a) {
 }
 
 void launch_route(const RouteArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL(k_route, dim3(a.n), dim3(ROUTE_THREADS), (size_t)a.d * sizeof(float), st, a);
+    const size_t lds = (size_t)a.d * sizeof(float) + (a.xh.hl ? (size_t)a.d + (size_t)a.d / 32 * sizeof(float2) : 0);
+    hipLaunchKernelGGL(k_route, dim3(a.n), dim3(ROUTE_THREADS), lds, st, a);
+}
+
+// Matrix-core form of Q8_0 activations already in global memory, one block per row.
+__global__ void __launch_bounds__(256) k_q8_to_acth(ActQ8 in, ActH out) {
+    const size_t row = blockIdx.x;
+    write_acth_row<256>(in.q + row * in.K, in.s + row * (in.K / 32), in.K, out, row, threadIdx.x);
+}
+
+void launch_q8_to_acth(const ActQ8& in, int rows, ActH out, hipStream_t st) {
+    hipLaunchKernelGGL(k_q8_to_acth, dim3(rows), dim3(256), 0, st, in, out);
 }
 
 // ---------------------------------------------------------------- few tokens
@@ -191,7 +227,7 @@ __device__ __forceinline__ float coherent_load(const float* p) {
 }
 
 __global__ void __launch_bounds__(RS_THREADS)
-k_route_small(RouteArgs a, int* done, int* counts, int* offs, int* act, int* n_act, int* pair_f, int* pos_of,
+k_route_small(RouteArgs a, int* done, int* counts, int* offs, int* act, int* n_act, int* pair_tok, int* pos_of,
               int4* tiles, int* n_tiles) {
     extern __shared__ float lds[];  // [0, d): router row; then n token rows
     __shared__ int s_last;
@@ -217,7 +253,7 @@ k_route_small(RouteArgs a, int* done, int* counts, int* offs, int* act, int* n_a
         for (int bb = b0 + wave * 2; bb < b1; bb += (RS_THREADS / 64) * 2) {
             const int b = bb + half;  // token-major: b = t*nb + block
             const bool ok = b < b1;
-            quant_block(ok ? xs[(size_t)b * 32 + l32] : 0.0f, l32, ok, a.xq, a.xh, (size_t)(b / nb), b % nb);
+            quant_block(ok ? xs[(size_t)b * 32 + l32] : 0.0f, l32, ok, a.xq, (size_t)(b / nb), b % nb);
         }
     }
 
@@ -310,18 +346,18 @@ k_route_small(RouteArgs a, int* done, int* counts, int* offs, int* act, int* n_a
         for (int f = 0; f < nk; ++f) {
             const int e = rank_sel[f / k][f % k];
             const int pos = hist[e]++;
-            pair_f[pos] = f;
+            pair_tok[pos] = f / k;
             pos_of[f] = pos;
         }
         *done = 0;
     }
 }
 
-void launch_route_small(const RouteArgs& a, int* done, int* counts, int* offs, int* act, int* n_act, int* pair_f,
+void launch_route_small(const RouteArgs& a, int* done, int* counts, int* offs, int* act, int* n_act, int* pair_tok,
                         int* pos_of, int4* tiles, int* n_tiles, hipStream_t st) {
     const int rows = a.E + (a.shgate ? 1 : 0);
     const size_t lds = std::max((size_t)(1 + a.n) * a.d, (size_t)a.n * a.E + 1) * sizeof(float);
-    hipLaunchKernelGGL(k_route_small, dim3(rows), dim3(RS_THREADS), lds, st, a, done, counts, offs, act, n_act, pair_f,
+    hipLaunchKernelGGL(k_route_small, dim3(rows), dim3(RS_THREADS), lds, st, a, done, counts, offs, act, n_act, pair_tok,
                        pos_of, tiles, n_tiles);
 }
 
@@ -333,7 +369,7 @@ void launch_route_small(const RouteArgs& a, int* done, int* counts, int* offs, i
 constexpr int DISPATCH_THREADS = 256;
 
 __global__ void __launch_bounds__(DISPATCH_THREADS)
-k_dispatch(const int* ids, int nk, int E, int* counts, int* offs, int* act, int* n_act, int* pair_f, int* pos_of,
+k_dispatch(const int* ids, int nk, int E, int top_k, int* counts, int* offs, int* act, int* n_act, int* pair_tok, int* pos_of,
            int4* tiles, int* n_tiles) {
     extern __shared__ int hist[];
     __shared__ int wtot[DISPATCH_THREADS / 64];
@@ -385,7 +421,7 @@ k_dispatch(const int* ids, int nk, int E, int* counts, int* offs, int* act, int*
         }
         if (pred) {
             const int p = off + run + woff + lp;
-            pair_f[p] = f;
+            pair_tok[p] = f / top_k;
             pos_of[f] = p;
         }
         run += tot;
@@ -394,10 +430,9 @@ k_dispatch(const int* ids, int nk, int E, int* counts, int* offs, int* act, int*
 }
 
 void launch_dispatch(const int* ids, int nk, int E, int top_k, int* counts, int* offs, int* act, int* n_act,
-                     int* pair_f, int* pos_of, int4* tiles, int* n_tiles, hipStream_t st) {
-    (void)top_k;
-    hipLaunchKernelGGL(k_dispatch, dim3(E), dim3(DISPATCH_THREADS), (size_t)E * sizeof(int), st, ids, nk, E,
-                       counts, offs, act, n_act, pair_f, pos_of, tiles, n_tiles);
+                     int* pair_tok, int* pos_of, int4* tiles, int* n_tiles, hipStream_t st) {
+    hipLaunchKernelGGL(k_dispatch, dim3(E), dim3(DISPATCH_THREADS), (size_t)E * sizeof(int), st, ids, nk, E, top_k,
+                       counts, offs, act, n_act, pair_tok, pos_of, tiles, n_tiles);
 }
 
 // MoE combine (transformer.cpp:2728-2730 and 2752-2754): starting from 0, for
@@ -433,7 +468,7 @@ __global__ void __launch_bounds__(256) k_quant_q8(const float* x, int rows, int 
     const int half = (threadIdx.x >> 5) & 1, l32 = threadIdx.x & 31;
     const size_t blk = gid * 2 + half;
     const bool ok = blk < (size_t)rows * nb;
-    quant_block(ok ? x[blk * 32 + l32] : 0.0f, l32, ok, out, ActH{}, blk / nb, (int)(blk % nb));
+    quant_block(ok ? x[blk * 32 + l32] : 0.0f, l32, ok, out, blk / nb, (int)(blk % nb));
 }
 
 void launch_quantize_q8(const float* x, int rows, int K, ActQ8 out, hipStream_t st) {

@@ -107,23 +107,24 @@ int dalloc(T*& p, size_t n) {
     return JX_OK;
 }
 
-// Matrix-core activation buffers for `rows` rows of K (rows padded to whole
-// 256-element units).
+// Matrix-core activation buffers for `rows` rows of K.
 struct DevActH {
     jx::ActH a;
     void release() {
-        if (a.q16) (void)hipFree(a.q16);
-        if (a.dx) (void)hipFree(a.dx);
+        if (a.hl) (void)hipFree(a.hl);
+        if (a.pe) (void)hipFree(a.pe);
         if (a.xm) (void)hipFree(a.xm);
         a = jx::ActH{};
     }
     int alloc(size_t rows, int K) {
         release();
         a.K = K;
+        a.KH = K / 128;
         a.KU = (K + 255) / 256;
-        HIPCHK(hipMalloc(&a.q16, rows * a.KU * 256 * sizeof(uint16_t)));
-        HIPCHK(hipMalloc(&a.dx, rows * a.KU * 8 * sizeof(float)));
-        HIPCHK(hipMalloc(&a.xm, rows * a.KU * 32 * sizeof(uint16_t)));
+        if (K % 128 != 0) return JX_OK;  // the matrix-core path is not used for this shape
+        HIPCHK(hipMalloc(&a.hl, rows * a.KH * 256 * sizeof(uint16_t)));
+        HIPCHK(hipMalloc(&a.pe, rows * a.KH * sizeof(float)));
+        HIPCHK(hipMalloc(&a.xm, rows * a.KU * 24 * sizeof(uint16_t)));
         return JX_OK;
     }
 };
@@ -149,7 +150,7 @@ struct jx_moe_layer {
     // workspace
     int cap = 0;
     float *x = nullptr, *out = nullptr, *probs = nullptr, *shscale = nullptr, *logits = nullptr;
-    int *ids = nullptr, *counts = nullptr, *offs = nullptr, *act = nullptr, *n_act = nullptr, *pair_f = nullptr,
+    int *ids = nullptr, *counts = nullptr, *offs = nullptr, *act = nullptr, *n_act = nullptr, *pair_tok = nullptr,
         *pos_of = nullptr, *n_tiles = nullptr;
     int4* tiles = nullptr;
     jx::ActQ8 xq, hq, hqs;
@@ -206,7 +207,7 @@ int ensure_workspace(jx_moe_layer* L, int n) {
     WS(L->offs, L->E + 1);
     WS(L->act, L->E);
     WS(L->n_act, 1);
-    WS(L->pair_f, nk);
+    WS(L->pair_tok, nk);
     WS(L->pos_of, nk);
     WS(L->n_tiles, 1);
     WS(L->tiles, nk / jx::MFMA_BN + std::min<size_t>(L->E, nk) + 1);
@@ -250,7 +251,7 @@ void free_layer(jx_moe_layer* L) {
     (void)hipSetDevice(L->device);
     for (auto* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown}) m->release();
     void* ptrs[] = {L->router, L->bias, L->shgate, L->x, L->out, L->probs, L->shscale, L->logits, L->ids,
-                    L->counts, L->offs, L->act, L->n_act, L->pair_f, L->pos_of, L->n_tiles, L->tiles,
+                    L->counts, L->offs, L->act, L->n_act, L->pair_tok, L->pos_of, L->n_tiles, L->tiles,
                     L->xq.q, L->xq.s, L->hq.q, L->hq.s, L->hqs.q, L->hqs.s, L->hf, L->hfs, L->y, L->ysh};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
@@ -313,20 +314,30 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     bool mfma = (size_t)nk >= (size_t)MFMA_MIN_PAIRS_PER_EXPERT * E;
     if (flags & JX_FWD_FORCE_GEMV) mfma = false;
     if (flags & JX_FWD_FORCE_MFMA) mfma = true;
-    const bool smfma = L->shared && n >= jx::MFMA_MIN_SHARED_TOKENS && !(flags & JX_FWD_FORCE_GEMV);
+    // the matrix-core GEMMs stage K in 128-element half-units
+    const bool mfma_shape = d % 128 == 0 && (L->down_f32 || L->F % 128 == 0);
+    mfma = mfma && mfma_shape;
+    const bool smfma = L->shared && n >= jx::MFMA_MIN_SHARED_TOKENS && !(flags & JX_FWD_FORCE_GEMV) && d % 128 == 0 &&
+                       (L->sdown_f32 || L->Fs % 128 == 0);
     jx::RouteArgs ra{xdev, n, d, E, k, L->router, L->bias, L->shgate, L->xq, (mfma || smfma) ? L->xh.a : jx::ActH{},
                      L->ids, L->probs, L->shscale, L->logits};
     if (jx::route_small_fits(n, d, E)) {
-        Launch l(L, "route_dispatch", st);
-        jx::launch_route_small(ra, L->done, L->counts, L->offs, L->act, L->n_act, L->pair_f, L->pos_of, L->tiles,
-                               L->n_tiles, st);
+        {
+            Launch l(L, "route_dispatch", st);
+            jx::launch_route_small(ra, L->done, L->counts, L->offs, L->act, L->n_act, L->pair_tok, L->pos_of, L->tiles,
+                                   L->n_tiles, st);
+        }
+        if (mfma || smfma) {
+            Launch l(L, "to_matrix_form", st);
+            jx::launch_q8_to_acth(L->xq, n, L->xh.a, st);
+        }
     } else {
         {
             Launch l(L, "route", st);
             jx::launch_route(ra, st);
         }
         Launch l(L, "dispatch", st);
-        jx::launch_dispatch(L->ids, nk, E, k, L->counts, L->offs, L->act, L->n_act, L->pair_f, L->pos_of, L->tiles,
+        jx::launch_dispatch(L->ids, nk, E, k, L->counts, L->offs, L->act, L->n_act, L->pair_tok, L->pos_of, L->tiles,
                             L->n_tiles, st);
     }
     jx::Groups grp;
@@ -334,7 +345,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     grp.offs = L->offs;
     grp.act = L->act;
     grp.n_act = L->n_act;
-    grp.pair_f = L->pair_f;
+    grp.pair_tok = L->pair_tok;
     grp.tiles = L->tiles;
     grp.n_tiles = L->n_tiles;
     grp.top_k = k;
