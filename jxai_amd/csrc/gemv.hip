@@ -1,26 +1,35 @@
 // Decode regime (few tokens per expert): bandwidth-bound dequant-GEMV.
 //
 // A block owns one 32-row tile of one active expert's matrix (or two: gate
-// and up) and every token routed to that expert; its waves split K.  Lane
-// (m = lane % 32, h = lane / 32) streams 16-byte chunks of row m -- the 32
-// lanes of a half-wave read one contiguous 512-byte run of the tile layout --
-// and multiplies them against the tokens' Q8_0 activations with
-// v_dot4_i32_i8.  The next K-unit's chunks are loaded before the current one
-// is consumed.  Integer block sums are exact; each is scaled once in fp32
-// (weight scale x activation scale) as in the reference's vec_dot_*_q8_0
-// kernels (src/quant.cpp:3307-3573); only the fp32 summation order differs.
+// and up) and every token routed to that expert; its waves split K.  The
+// block first stages its tokens' activations (Q8_0 quants and block scales,
+// or fp32 rows) in LDS, so the only global loads in the K loop are weight
+// streams: the activation loads are issued before the first weight loads, and
+// inside the loop activations come over the LDS path with its own counter, so
+// a wave never waits on an HBM prefetch it does not need yet.  Weights run
+// through a three-deep register rotation (units u+1 and u+2 in flight while u
+// is consumed).  Lane (m = lane % 32, h = lane / 32) reads 16-byte chunks of
+// row m; the 32 lanes of a half-wave read one contiguous 512-byte run of the
+// tile layout, a wave load is 1 KB contiguous.  Products use v_dot4_i32_i8;
+// integer block sums are exact and each is scaled once in fp32 (weight scale
+// x activation scale) as in the reference's vec_dot_*_q8_0 kernels
+// (src/quant.cpp:3307-3573); only the fp32 summation order differs.
+//
+// K-units (four 1 KB wave loads each):
+//   Q4_K  one 256-element super-block: 4 pair chunks + the 16-byte header
+//   Q4_0  eight 32-blocks: lanes of half h take the four blocks of parity h
+//   Q8_0  four 32-blocks: lanes of half h take half h of each
+#include <algorithm>
+
 #include "jxmoe_device.h"
 #include "jxmoe_kernels.h"
 
 namespace jx {
 
 // ------------------------------------------------------------ weight chunks
-// Q4_0 / Q8_0: unit = one 32-block.  Q4_0 lanes of half h take the blocks of
-// parity h; Q8_0 lanes take half h of every block.  Q4_K: unit = one
-// 256-element super-block, lanes take half h of each of its 4 sub-block pairs.
-struct Raw32 {
-    uint4 q;
-    uint32_t d;  // fp16 bits of the block scale
+struct RawB {
+    uint4 q[4];
+    uint32_t d[4];  // fp16 bits of the block scales
 };
 struct RawQ4K {
     uint4 q[4];
@@ -30,47 +39,65 @@ struct RawQ4K {
 template <int TYPE>
 struct Fmt;
 
+// load(c, W, e, rt, u, m, h, ok): every lane issues the same loads whatever
+// `ok` and the unit's extent; a unit that is not wanted (ok false) or a block
+// past the matrix's K reads the zeroed pad instead (its bytes are never used).
 template <>
 struct Fmt<T_Q4_0> {
-    using Raw = Raw32;
-    static constexpr bool PARITY = true;
-    __device__ static Raw load(const QMat& W, int e, int rt, int u, int m, int h) {
-        (void)h;
-        const size_t t = ((size_t)rt * W.nkb + u) * 32 + m;
-        Raw c;
-        c.q = ld_stream16(W.qs + e * W.qs_es + t * 16);
-        c.d = reinterpret_cast<const uint16_t*>(W.sc + e * W.sc_es)[t];
-        return c;
+    using Raw = RawB;
+    static constexpr int BPU = 8;  // 32-blocks per unit
+    __device__ static void load(Raw& c, const QMat& W, int e, int rt, int u, int m, int h, bool ok) {
+        const size_t b0 = (size_t)rt * W.nkb + (size_t)u * BPU + h;
+        const uint8_t* qb = W.qs + e * W.qs_es;
+        const uint8_t* sb = W.sc + e * W.sc_es;
+        const int left = W.nkb - u * BPU - h;  // blocks 2i with 2i < left exist
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const bool v = ok && 2 * i < left;
+            const size_t qo = ((b0 + 2 * i) * 32 + m) * 16, so = ((b0 + 2 * i) * 32 + m) * 2;
+            c.q[i] = ld_stream16(v ? qb + qo : W.pad_qs + m * 16);
+            c.d[i] = *reinterpret_cast<const uint16_t*>(v ? sb + so : W.pad_sc + m * 2);
+        }
     }
 };
 
 template <>
 struct Fmt<T_Q8_0> {
-    using Raw = Raw32;
-    static constexpr bool PARITY = false;
-    __device__ static Raw load(const QMat& W, int e, int rt, int u, int m, int h) {
-        const size_t t = (size_t)rt * W.nkb + u;
-        Raw c;
-        c.q = ld_stream16(W.qs + e * W.qs_es + ((t * 2 + h) * 32 + m) * 16);
-        c.d = reinterpret_cast<const uint16_t*>(W.sc + e * W.sc_es)[t * 32 + m];
-        return c;
+    using Raw = RawB;
+    static constexpr int BPU = 4;
+    __device__ static void load(Raw& c, const QMat& W, int e, int rt, int u, int m, int h, bool ok) {
+        const size_t b0 = (size_t)rt * W.nkb + (size_t)u * BPU;
+        const uint8_t* qb = W.qs + e * W.qs_es;
+        const uint8_t* sb = W.sc + e * W.sc_es;
+        const int left = W.nkb - u * BPU;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const bool v = ok && i < left;
+            const size_t qo = (((b0 + i) * 2 + h) * 32 + m) * 16, so = ((b0 + i) * 32 + m) * 2;
+            c.q[i] = ld_stream16(v ? qb + qo : W.pad_qs + m * 16);
+            c.d[i] = *reinterpret_cast<const uint16_t*>(v ? sb + so : W.pad_sc + m * 2);
+        }
     }
 };
 
 template <>
 struct Fmt<T_Q4_K> {
     using Raw = RawQ4K;
-    static constexpr bool PARITY = false;
-    __device__ static Raw load(const QMat& W, int e, int rt, int u, int m, int h) {
+    static constexpr int BPU = 1;
+    __device__ static void load(Raw& c, const QMat& W, int e, int rt, int u, int m, int h, bool ok) {
         const size_t t = (size_t)rt * W.nkb + u;
-        const uint8_t* qb = W.qs + e * W.qs_es;
-        Raw c;
+        const uint8_t* qb = ok ? W.qs + e * W.qs_es + (t * 8 + h) * 512 : W.pad_qs;
+        const uint8_t* hb = ok ? W.sc + e * W.sc_es + t * 512 : W.pad_sc;
 #pragma unroll
-        for (int p = 0; p < 4; ++p) c.q[p] = ld_stream16(qb + (((t * 4 + p) * 2 + h) * 32 + m) * 16);
-        c.hd = ld_stream16(W.sc + e * W.sc_es + (t * 32 + m) * 16);
-        return c;
+        for (int p = 0; p < 4; ++p) c.q[p] = ld_stream16(qb + p * 1024 + m * 16);
+        c.hd = ld_stream16(hb + m * 16);
     }
 };
+
+template <int TYPE>
+__host__ __device__ constexpr int n_units(int nkb) {
+    return (nkb + Fmt<TYPE>::BPU - 1) / Fmt<TYPE>::BPU;
+}
 
 __device__ __forceinline__ uint32_t byte_of(const uint4& v, int i) {
     const uint32_t w = i < 4 ? v.y : (i < 8 ? v.z : v.w);
@@ -89,50 +116,73 @@ __device__ __forceinline__ void hd_scale_min(const uint4& hd, int j, int& sc, in
     }
 }
 
-// Accumulate one K-unit of one weight row against up to TB activation rows
-// (Q8_0 activations).
+// Activations of one token group in LDS: Q8_0 quants [TB][K] and (scale,
+// sum) [TB][K/32], or fp32 rows [TB][K].
+struct ActLds {
+    const int8_t* q;
+    const float2* s;
+    const float* f;
+    int K;
+};
+
+__device__ __forceinline__ uint4 lds16(const int8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// Accumulate one K-unit of one weight row against up to TB token rows.
 template <int TYPE, int TB>
-__device__ __forceinline__ void unit_accum(const typename Fmt<TYPE>::Raw& c, const int8_t* const* arow,
-                                           const float2* const* as, int u, int h, int nt, float* acc) {
+__device__ __forceinline__ void unit_accum(const typename Fmt<TYPE>::Raw& c, const ActLds& A, int u, int h, int nt,
+                                           int nkb, float* acc) {
+    const int KB = A.K / 32;
     if constexpr (TYPE == T_Q4_0) {
-        const float dw = f16_to_f32(c.d);
-        const uint32_t q[4] = {c.q.x, c.q.y, c.q.z, c.q.w};
-        int ql[4], qh[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            ql[i] = (int)(q[i] & 0x0F0F0F0Fu);
-            qh[i] = (int)((q[i] >> 4) & 0x0F0F0F0Fu);
-        }
+            const int b = u * 8 + 2 * i + h;
+            if (b < nkb) {
+                const float dw = f16_to_f32(c.d[i] & 0xFFFFu);
+                const uint32_t q[4] = {c.q[i].x, c.q[i].y, c.q[i].z, c.q[i].w};
+                int ql[4], qh[4];
 #pragma unroll
-        for (int j = 0; j < TB; ++j) {
-            if (j < nt) {
-                const uint4 a0 = ld16(arow[j] + u * 32);
-                const uint4 a1 = ld16(arow[j] + u * 32 + 16);
-                const float2 s = as[j][u];
-                int isum = sdot4(ql[0], (int)a0.x, 0);
-                isum = sdot4(ql[1], (int)a0.y, isum);
-                isum = sdot4(ql[2], (int)a0.z, isum);
-                isum = sdot4(ql[3], (int)a0.w, isum);
-                isum = sdot4(qh[0], (int)a1.x, isum);
-                isum = sdot4(qh[1], (int)a1.y, isum);
-                isum = sdot4(qh[2], (int)a1.z, isum);
-                isum = sdot4(qh[3], (int)a1.w, isum);
-                isum -= 8 * (int)s.y;  // weights are nibble - 8
-                acc[j] = __builtin_fmaf(dw * s.x, (float)isum, acc[j]);
+                for (int z = 0; z < 4; ++z) {
+                    ql[z] = (int)(q[z] & 0x0F0F0F0Fu);
+                    qh[z] = (int)((q[z] >> 4) & 0x0F0F0F0Fu);
+                }
+#pragma unroll
+                for (int j = 0; j < TB; ++j) {
+                    if (j < nt) {
+                        const uint4 a0 = lds16(A.q + j * A.K + b * 32);
+                        const uint4 a1 = lds16(A.q + j * A.K + b * 32 + 16);
+                        const float2 s = A.s[j * KB + b];
+                        int isum = sdot4(ql[0], (int)a0.x, 0);
+                        isum = sdot4(ql[1], (int)a0.y, isum);
+                        isum = sdot4(ql[2], (int)a0.z, isum);
+                        isum = sdot4(ql[3], (int)a0.w, isum);
+                        isum = sdot4(qh[0], (int)a1.x, isum);
+                        isum = sdot4(qh[1], (int)a1.y, isum);
+                        isum = sdot4(qh[2], (int)a1.z, isum);
+                        isum = sdot4(qh[3], (int)a1.w, isum);
+                        isum -= 8 * (int)s.y;  // weights are nibble - 8
+                        acc[j] = __builtin_fmaf(dw * s.x, (float)isum, acc[j]);
+                    }
+                }
             }
         }
     } else if constexpr (TYPE == T_Q8_0) {
-        const float dw = f16_to_f32(c.d);
 #pragma unroll
-        for (int j = 0; j < TB; ++j) {
-            if (j < nt) {
-                const uint4 a = ld16(arow[j] + u * 32 + 16 * h);
-                const float2 s = as[j][u];
-                int isum = sdot4((int)c.q.x, (int)a.x, 0);
-                isum = sdot4((int)c.q.y, (int)a.y, isum);
-                isum = sdot4((int)c.q.z, (int)a.z, isum);
-                isum = sdot4((int)c.q.w, (int)a.w, isum);
-                acc[j] = __builtin_fmaf(dw * s.x, (float)isum, acc[j]);
+        for (int i = 0; i < 4; ++i) {
+            const int b = u * 4 + i;
+            if (b < nkb) {
+                const float dw = f16_to_f32(c.d[i] & 0xFFFFu);
+#pragma unroll
+                for (int j = 0; j < TB; ++j) {
+                    if (j < nt) {
+                        const uint4 a = lds16(A.q + j * A.K + b * 32 + 16 * h);
+                        const float2 s = A.s[j * KB + b];
+                        int isum = sdot4((int)c.q[i].x, (int)a.x, 0);
+                        isum = sdot4((int)c.q[i].y, (int)a.y, isum);
+                        isum = sdot4((int)c.q[i].z, (int)a.z, isum);
+                        isum = sdot4((int)c.q[i].w, (int)a.w, isum);
+                        acc[j] = __builtin_fmaf(dw * s.x, (float)isum, acc[j]);
+                    }
+                }
             }
         }
     } else {
@@ -155,9 +205,9 @@ __device__ __forceinline__ void unit_accum(const typename Fmt<TYPE>::Raw& c, con
 #pragma unroll
             for (int j = 0; j < TB; ++j) {
                 if (j < nt) {
-                    const uint4 a = ld16(arow[j] + b0 * 32 + 16 * h);
-                    const uint4 b = ld16(arow[j] + (b0 + 1) * 32 + 16 * h);
-                    const float2 sa = as[j][b0], sb = as[j][b0 + 1];
+                    const uint4 a = lds16(A.q + j * A.K + b0 * 32 + 16 * h);
+                    const uint4 b = lds16(A.q + j * A.K + (b0 + 1) * 32 + 16 * h);
+                    const float2 sa = A.s[j * KB + b0], sb = A.s[j * KB + b0 + 1];
                     int ia = sdot4(ql[0], (int)a.x, 0);
                     ia = sdot4(ql[1], (int)a.y, ia);
                     ia = sdot4(ql[2], (int)a.z, ia);
@@ -184,8 +234,7 @@ __device__ __forceinline__ void unit_accum(const typename Fmt<TYPE>::Raw& c, con
 // src/quant.cpp:2910-3013, used when K % 256 != 0): rows of y are zero-padded
 // to whole super-blocks, so the partial last super-block needs no masking.
 template <int TB>
-__device__ __forceinline__ void unit_accum_f32(const RawQ4K& c, const float* const* yrow, int u, int h, int nt,
-                                               float* acc) {
+__device__ __forceinline__ void unit_accum_f32(const RawQ4K& c, const ActLds& A, int u, int h, int nt, float* acc) {
     const float d = f16_to_f32(c.hd.x & 0xFFFFu), dmin = f16_to_f32(c.hd.x >> 16);
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
@@ -198,7 +247,7 @@ __device__ __forceinline__ void unit_accum_f32(const RawQ4K& c, const float* con
 #pragma unroll
         for (int j = 0; j < TB; ++j) {
             if (j < nt) {
-                const float* ya = yrow[j] + u * 256 + 64 * p + 16 * h;
+                const float* ya = A.f + j * A.K + u * 256 + 64 * p + 16 * h;
                 const float* yb = ya + 32;
                 float sa = 0.0f, sb = 0.0f, ta = 0.0f, tb = 0.0f;
 #pragma unroll
@@ -223,24 +272,9 @@ __device__ __forceinline__ void unit_accum_f32(const RawQ4K& c, const float* con
                 v = __builtin_fmaf(-fm1, tb, v);
                 acc[j] = v;
             }
+            // one token's 32 activations at a time in registers
+            if constexpr (TB > 1) __builtin_amdgcn_sched_barrier(0);
         }
-    }
-}
-
-// K-units handled by lane (wave, h) of a WAVES-wave block: [lo, hi) by `step`.
-template <int TYPE, int WAVES>
-__device__ __forceinline__ void unit_range(int nkb, int wave, int h, int& lo, int& hi, int& step) {
-    if (Fmt<TYPE>::PARITY) {
-        const int npair = (nkb + 1) / 2;
-        const int per = (npair + WAVES - 1) / WAVES;
-        lo = 2 * (wave * per) + h;
-        hi = min(nkb, 2 * ((wave + 1) * per));
-        step = 2;
-    } else {
-        const int per = (nkb + WAVES - 1) / WAVES;
-        lo = wave * per;
-        hi = min(nkb, (wave + 1) * per);
-        step = 1;
     }
 }
 
@@ -264,6 +298,79 @@ __device__ __forceinline__ int token_of(const Groups& g, int p) {
     return g.identity ? p : g.pair_tok[p];
 }
 
+// LDS bytes of one token group's staged activations.
+__host__ __device__ inline size_t act_lds_bytes(int TB, int K, bool f32) {
+    return f32 ? (size_t)TB * K * sizeof(float) : (size_t)TB * K + (size_t)TB * (K / 32) * sizeof(float2);
+}
+
+// Activation staging into LDS, split so the global loads can be issued
+// before a wave's first weight loads and written to LDS after them: issue()
+// loads MQ 16-byte quant chunks and MS 8-byte (scale, sum) chunks per thread
+// into registers, write() stores them.  Indices past the group's last chunk
+// are clamped to it (the duplicate store writes the same bytes), so neither
+// half branches and the LDS stores wait only for the staging loads, not for
+// the weight loads issued after them.  Launchers guarantee
+// nt * K <= 16 * MQ * NTH and nt * K <= 32 * MS * NTH.
+template <int NTH, int MQ, int MS>
+struct StageQ8 {
+    uint4 vq[MQ];
+    float2 vs[MS];
+    template <typename RowFn>
+    __device__ __forceinline__ void issue(const ActQ8& g, int nt, RowFn src_row, int tid) {
+        const int K = g.K, KB = K / 32, cq = K / 16;
+#pragma unroll
+        for (int r = 0; r < MQ; ++r) {
+            const int i = min(tid + r * NTH, nt * cq - 1);
+            const int j = i / cq, c = i - j * cq;
+            vq[r] = ld16(g.q + src_row(j) * K + c * 16);
+        }
+#pragma unroll
+        for (int r = 0; r < MS; ++r) {
+            const int i = min(tid + r * NTH, nt * KB - 1);
+            const int j = i / KB, c = i - j * KB;
+            vs[r] = g.s[src_row(j) * KB + c];
+        }
+    }
+    // LDS layout: quants [TB][K], then (scale, sum) [TB][K/32]
+    __device__ __forceinline__ void write(int K, int TB, int nt, int8_t* lds, int tid) {
+        const int KB = K / 32, cq = K / 16;
+        float2* ls = reinterpret_cast<float2*>(lds + TB * K);
+#pragma unroll
+        for (int r = 0; r < MQ; ++r) {
+            const int i = min(tid + r * NTH, nt * cq - 1);
+            *reinterpret_cast<uint4*>(lds + i * 16) = vq[r];  // row j = i / cq at j * K + 16 (i % cq)
+        }
+#pragma unroll
+        for (int r = 0; r < MS; ++r) {
+            const int i = min(tid + r * NTH, nt * KB - 1);
+            ls[i] = vs[r];
+        }
+    }
+};
+
+template <int NTH, int MF>
+struct StageF32 {
+    float4 v[MF];
+    template <typename RowFn>
+    __device__ __forceinline__ void issue(const float* src, int ld, int K, int nt, RowFn src_row, int tid) {
+        const int cq = K / 4;
+#pragma unroll
+        for (int r = 0; r < MF; ++r) {
+            const int i = min(tid + r * NTH, nt * cq - 1);
+            const int j = i / cq, c = i - j * cq;
+            v[r] = *reinterpret_cast<const float4*>(src + src_row(j) * (size_t)ld + c * 4);
+        }
+    }
+    __device__ __forceinline__ void write(float* lds, int nt, int K, int tid) {
+        const int cq = K / 4;
+#pragma unroll
+        for (int r = 0; r < MF; ++r) {
+            const int i = min(tid + r * NTH, nt * cq - 1);
+            *reinterpret_cast<float4*>(lds + i * 4) = v[r];
+        }
+    }
+};
+
 // Q8_0 of one 32-row block of h held by lanes 0..31 (quantize_row_q8_0).
 __device__ __forceinline__ void store_q8_block(float hv, int m, bool writer, ActQ8& hq, size_t row, int blk) {
     const float amax = wave_max32(__builtin_fabsf(hv));
@@ -279,65 +386,92 @@ __device__ __forceinline__ void store_q8_block(float hv, int m, bool writer, Act
     }
 }
 
+// The K loop of one wave over units lo, lo + stride, ... < nu of one or two
+// weight matrices: two register sets alternate, so unit u+stride is in flight
+// while u is consumed (and u+2*stride is issued right after).  pre() runs
+// after the first two units' loads are issued (it finishes the activation
+// staging and synchronizes the block, so every wave calls it).
+template <int TYPE, int NMAT, typename Pre, typename Acc>
+__device__ __forceinline__ void kloop(const QMat& W0, const QMat& W1, int e, int rt, int lo, int nu, int stride, int m,
+                                      int h, Pre&& pre, Acc&& accum) {
+    using F = Fmt<TYPE>;
+    typename F::Raw a0, a1, b0, b1;
+    // loads are issued unconditionally (units past the end read the pad), so
+    // every path through the loop has the same loads in flight and each wait
+    // covers only the unit about to be consumed
+    auto ld = [&](typename F::Raw& r0, typename F::Raw& r1, int u) {
+        F::load(r0, W0, e, rt, u, m, h, u < nu);
+        if constexpr (NMAT == 2) F::load(r1, W1, e, rt, u, m, h, u < nu);
+    };
+    int u = lo;
+    ld(a0, a1, u);
+    ld(b0, b1, u + stride);
+    pre();
+    for (; u < nu; u += 2 * stride) {
+        accum(a0, a1, u);
+        ld(a0, a1, u + 2 * stride);
+        if (u + stride >= nu) break;
+        accum(b0, b1, u + stride);
+        ld(b0, b1, u + 3 * stride);
+    }
+}
+
+// Resident waves per SIMD the GEMVs are compiled for (single-token groups:
+// <= 128 VGPRs, every block of a decode step resident at once with enough
+// 1 KB weight loads in flight per CU to cover HBM latency).
+#define GEMV_WAVES_PER_SIMD(TB) ((TB) == 1 ? 4 : 2)
+
 // Gate + up + SwiGLU (matmul_swiglu_quant_f32, src/quant.cpp:3970-4009) and
 // the Q8_0 quantization of the result for the down projection
-// (matmul_quant_f32's quantize_row_q8_0, 3908-3914).
+// (matmul_quant_f32's quantize_row_q8_0, 3908-3914).  The first half of the
+// waves streams the gate tile, the second half the up tile.
 template <int TYPE, int TB, int WAVES>
-__global__ void __launch_bounds__(WAVES * 64)
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(GEMV_WAVES_PER_SIMD(TB))))
 k_gemv_gateup(QMat G, QMat U, ActQ8 xq, Groups grp, ActQ8 hq, float* hf, int hf_ld) {
-    using F = Fmt<TYPE>;
-    __shared__ float red[WAVES][TB][2][32];
+    constexpr int HW = WAVES / 2;  // waves per matrix
+    extern __shared__ __align__(16) int8_t smem[];
+    __shared__ float red[WAVES][TB][32];
     const int rt = blockIdx.x;
     int e, p0, cnt;
     group_of(grp, blockIdx.y, e, p0, cnt);
     if (cnt == 0) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 31, h = lane >> 5;
-    const int K = xq.K, KB = K / 32;
-    int lo, hi, step;
-    unit_range<TYPE, WAVES>(G.nkb, wave, h, lo, hi, step);
+    const int mat = wave / HW, kw = wave % HW;
+    const QMat& W = mat ? U : G;
+    const int K = xq.K;
+    const int nu = n_units<TYPE>(G.nkb);
+    const ActLds A{smem, reinterpret_cast<const float2*>(smem + TB * K), nullptr, K};
     for (int tb0 = 0; tb0 < cnt; tb0 += TB) {
         const int nt = min(TB, cnt - tb0);
-        const int8_t* arow[TB];
-        const float2* as[TB];
+        if (tb0) __syncthreads();  // previous group's LDS reads are done
+        auto src = [&](int j) { return (size_t)token_of(grp, p0 + tb0 + j); };
+        StageQ8<WAVES * 64, TB == 1 ? 4 : 8, TB == 1 ? 2 : 4> sg;
+        sg.issue(xq, nt, src, tid);
+        float acc[TB];
+#pragma unroll
+        for (int j = 0; j < TB; ++j) acc[j] = 0.0f;
+        kloop<TYPE, 1>(
+            W, W, e, rt, kw, nu, HW, m, h,
+            [&] {
+                sg.write(K, TB, nt, smem, tid);
+                __syncthreads();
+            },
+            [&](const typename Fmt<TYPE>::Raw& c, const typename Fmt<TYPE>::Raw&, int u) {
+                unit_accum<TYPE, TB>(c, A, u, h, nt, G.nkb, acc);
+            });
 #pragma unroll
         for (int j = 0; j < TB; ++j) {
-            const int tok = token_of(grp, p0 + tb0 + min(j, nt - 1));
-            arow[j] = xq.q + (size_t)tok * K;
-            as[j] = xq.s + (size_t)tok * KB;
-        }
-        float ag[TB], au[TB];
-#pragma unroll
-        for (int j = 0; j < TB; ++j) ag[j] = au[j] = 0.0f;
-        if (lo < hi) {
-            auto cg = F::load(G, e, rt, lo, m, h);
-            auto cu = F::load(U, e, rt, lo, m, h);
-            for (int u = lo; u < hi; u += step) {
-                const int un = min(u + step, hi - 1);
-                const auto ng = F::load(G, e, rt, un, m, h);
-                const auto nu = F::load(U, e, rt, un, m, h);
-                unit_accum<TYPE, TB>(cg, arow, as, u, h, nt, ag);
-                unit_accum<TYPE, TB>(cu, arow, as, u, h, nt, au);
-                cg = ng;
-                cu = nu;
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < TB; ++j) {
-            ag[j] += __shfl_xor(ag[j], 32, 64);
-            au[j] += __shfl_xor(au[j], 32, 64);
-            if (h == 0) {
-                red[wave][j][0][m] = ag[j];
-                red[wave][j][1][m] = au[j];
-            }
+            acc[j] += __shfl_xor(acc[j], 32, 64);
+            if (h == 0) red[wave][j][m] = acc[j];
         }
         __syncthreads();
         if (wave == 0) {
             for (int j = 0; j < nt; ++j) {
                 float g = 0.0f, u = 0.0f;
 #pragma unroll
-                for (int w = 0; w < WAVES; ++w) {
-                    g += red[w][j][0][m];
-                    u += red[w][j][1][m];
+                for (int w = 0; w < HW; ++w) {
+                    g += red[w][j][m];
+                    u += red[HW + w][j][m];
                 }
                 const float hv = (g / (1.0f + expf(-g))) * u;
                 const size_t row = (size_t)(p0 + tb0 + j);
@@ -345,50 +479,51 @@ k_gemv_gateup(QMat G, QMat U, ActQ8 xq, Groups grp, ActQ8 hq, float* hf, int hf_
                 if (hf && h == 0) hf[row * (size_t)hf_ld + rt * 32 + m] = hv;
             }
         }
-        __syncthreads();
     }
 }
 
 // Down projection into y[pair][rows].
 template <int TYPE, int TB, int WAVES, bool F32ACT>
-__global__ void __launch_bounds__(WAVES * 64)
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(GEMV_WAVES_PER_SIMD(TB))))
 k_gemv_down(QMat D, ActQ8 hq, const float* hf, int hf_ld, Groups grp, float* y) {
-    using F = Fmt<TYPE>;
+    extern __shared__ __align__(16) int8_t smem[];
     __shared__ float red[WAVES][TB][32];
     const int rt = blockIdx.x;
     int e, p0, cnt;
     group_of(grp, blockIdx.y, e, p0, cnt);
     if (cnt == 0) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 31, h = lane >> 5;
-    int lo, hi, step;
-    unit_range<TYPE, WAVES>(D.nkb, wave, h, lo, hi, step);
-    const int K = hq.K, KB = K / 32;
+    const int K = F32ACT ? hf_ld : hq.K;
+    const int nu = n_units<TYPE>(D.nkb);
+    const ActLds A{smem, reinterpret_cast<const float2*>(smem + TB * K), reinterpret_cast<const float*>(smem), K};
     for (int tb0 = 0; tb0 < cnt; tb0 += TB) {
         const int nt = min(TB, cnt - tb0);
-        const int8_t* arow[TB];
-        const float2* as[TB];
-        const float* yrow[TB];
-#pragma unroll
-        for (int j = 0; j < TB; ++j) {
-            const size_t row = (size_t)(p0 + tb0 + min(j, nt - 1));
-            arow[j] = F32ACT ? nullptr : hq.q + row * K;
-            as[j] = F32ACT ? nullptr : hq.s + row * KB;
-            yrow[j] = F32ACT ? hf + row * (size_t)hf_ld : nullptr;
-        }
+        if (tb0) __syncthreads();
+        auto src = [&](int j) { return (size_t)(p0 + tb0 + j); };
+        StageQ8<WAVES * 64, TB == 1 ? 4 : 8, TB == 1 ? 2 : 4> sq;
+        StageF32<WAVES * 64, TB == 1 ? 2 : 4> sf;
+        if constexpr (F32ACT)
+            sf.issue(hf, hf_ld, K, nt, src, tid);
+        else
+            sq.issue(hq, nt, src, tid);
         float acc[TB];
 #pragma unroll
         for (int j = 0; j < TB; ++j) acc[j] = 0.0f;
-        if (lo < hi) {
-            auto c = F::load(D, e, rt, lo, m, h);
-            for (int u = lo; u < hi; u += step) {
-                const auto nc = F::load(D, e, rt, min(u + step, hi - 1), m, h);
+        kloop<TYPE, 1>(
+            D, D, e, rt, wave, nu, WAVES, m, h,
+            [&] {
                 if constexpr (F32ACT)
-                    unit_accum_f32<TB>(c, yrow, u, h, nt, acc);
+                    sf.write(reinterpret_cast<float*>(smem), nt, K, tid);
                 else
-                    unit_accum<TYPE, TB>(c, arow, as, u, h, nt, acc);
-                c = nc;
-            }
-        }
+                    sq.write(K, TB, nt, smem, tid);
+                __syncthreads();
+            },
+            [&](const typename Fmt<TYPE>::Raw& c, const typename Fmt<TYPE>::Raw&, int u) {
+                           if constexpr (F32ACT)
+                               unit_accum_f32<TB>(c, A, u, h, nt, acc);
+                           else
+                               unit_accum<TYPE, TB>(c, A, u, h, nt, D.nkb, acc);
+                       });
 #pragma unroll
         for (int j = 0; j < TB; ++j) {
             acc[j] += __shfl_xor(acc[j], 32, 64);
@@ -403,24 +538,45 @@ k_gemv_down(QMat D, ActQ8 hq, const float* hf, int hf_ld, Groups grp, float* y) 
                 y[(size_t)(p0 + tb0 + j) * D.rows + rt * 32 + m] = s;
             }
         }
-        __syncthreads();
     }
 }
 
 constexpr int GATEUP_WAVES = 4;
 constexpr int DOWN_WAVES = 8;
 
+// Largest K one token group of TB rows stages (the StageQ8 / StageF32
+// register slots: 16 * MQ * NTH quant bytes, 32 * MS * NTH block scales,
+// 4 * MF * NTH floats).
+int gemv_max_k(bool gateup, int tb, bool f32) {
+    const int nth = 64 * (gateup ? GATEUP_WAVES : DOWN_WAVES);
+    if (f32) return (tb <= 1 ? 2 : 4) * 4 * nth / (tb <= 1 ? 1 : 4);
+    const int mq = tb <= 1 ? 4 : 8, ms = tb <= 1 ? 2 : 4, rows = tb <= 1 ? 1 : 4;
+    return std::min(16 * mq * nth, 32 * ms * nth) / rows;
+}
+
+// Dynamic LDS above the default 64 KB needs the kernel's opt-in.
+template <typename Kern>
+static void lds_optin(Kern k, size_t bytes) {
+    if (bytes > 65536) (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
 template <int TYPE>
 static void gateup_t(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots, int tb,
                      ActQ8 hq, float* hf, hipStream_t st) {
     dim3 grid(g.nrt, slots);
     const int hf_ld = ((g.rows + 255) / 256) * 256;
-    if (tb <= 1)
-        hipLaunchKernelGGL((k_gemv_gateup<TYPE, 1, GATEUP_WAVES>), grid, dim3(GATEUP_WAVES * 64), 0, st, g, u, xq,
+    if (tb <= 1) {
+        const size_t lds = act_lds_bytes(1, xq.K, false);
+        lds_optin(k_gemv_gateup<TYPE, 1, GATEUP_WAVES>, lds);
+        hipLaunchKernelGGL((k_gemv_gateup<TYPE, 1, GATEUP_WAVES>), grid, dim3(GATEUP_WAVES * 64), lds, st, g, u, xq,
                            grp, hq, hf, hf_ld);
-    else
-        hipLaunchKernelGGL((k_gemv_gateup<TYPE, 4, GATEUP_WAVES>), grid, dim3(GATEUP_WAVES * 64), 0, st, g, u, xq,
+    } else {
+        const size_t lds = act_lds_bytes(4, xq.K, false);
+        lds_optin(k_gemv_gateup<TYPE, 4, GATEUP_WAVES>, lds);
+        hipLaunchKernelGGL((k_gemv_gateup<TYPE, 4, GATEUP_WAVES>), grid, dim3(GATEUP_WAVES * 64), lds, st, g, u, xq,
                            grp, hq, hf, hf_ld);
+    }
 }
 
 void launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots, int tb,
@@ -437,12 +593,18 @@ template <int TYPE, bool F32ACT>
 static void down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp, int slots,
                    int tb, float* y, hipStream_t st) {
     dim3 grid(dn.nrt, slots);
-    if (tb <= 1)
-        hipLaunchKernelGGL((k_gemv_down<TYPE, 1, DOWN_WAVES, F32ACT>), grid, dim3(DOWN_WAVES * 64), 0, st, dn, hq,
+    const int K = F32ACT ? hf_ld : hq.K;
+    if (tb <= 1) {
+        const size_t lds = act_lds_bytes(1, K, F32ACT);
+        lds_optin(k_gemv_down<TYPE, 1, DOWN_WAVES, F32ACT>, lds);
+        hipLaunchKernelGGL((k_gemv_down<TYPE, 1, DOWN_WAVES, F32ACT>), grid, dim3(DOWN_WAVES * 64), lds, st, dn, hq,
                            hf, hf_ld, grp, y);
-    else
-        hipLaunchKernelGGL((k_gemv_down<TYPE, 4, DOWN_WAVES, F32ACT>), grid, dim3(DOWN_WAVES * 64), 0, st, dn, hq,
+    } else {
+        const size_t lds = act_lds_bytes(4, K, F32ACT);
+        lds_optin(k_gemv_down<TYPE, 4, DOWN_WAVES, F32ACT>, lds);
+        hipLaunchKernelGGL((k_gemv_down<TYPE, 4, DOWN_WAVES, F32ACT>), grid, dim3(DOWN_WAVES * 64), lds, st, dn, hq,
                            hf, hf_ld, grp, y);
+    }
 }
 
 void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp, int slots,

@@ -25,7 +25,12 @@ struct QMat {
     const uint8_t* sc = nullptr;
     size_t qs_es = 0, sc_es = 0;  // per-expert strides (bytes)
     int n_mats = 0;     // experts held
+    // Zeroed QMAT_PAD-byte tails of the qs / sc allocations: loads a kernel
+    // issues for units it will not use read here (uniform instruction streams).
+    const uint8_t* pad_qs = nullptr;
+    const uint8_t* pad_sc = nullptr;
 };
+constexpr size_t QMAT_PAD = 8192;
 
 // Q8_0 activations on the device: q [rows][K] int8, s [rows][K/32] = (fp16-truncated
 // scale as fp32, sum of the 32 quants as fp32).
@@ -91,6 +96,9 @@ void launch_dispatch(const int* ids, int nk, int E, int top_k, int* counts, int*
 // Output rows are sorted pairs (routed) or tokens (shared).
 void launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots,
                         int tb, ActQ8 hq, float* hf, hipStream_t st);
+// Largest K the GEMVs accept for token groups of `tb` rows (gate/up or down,
+// Q8_0 or fp32 activations).
+int gemv_max_k(bool gateup, int tb, bool f32);
 // Decode regime: down projection over Q8_0 (hq) or fp32 (hf) activations into y[pair][d].
 void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp,
                       int slots, int tb, float* y, hipStream_t st);

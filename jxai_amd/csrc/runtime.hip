@@ -82,8 +82,12 @@ int upload_matrix(int type, int n_mats, int rows, int cols, const void* host, De
     m.sc_es = units * sc_u;
     const size_t raw_bytes = (size_t)n_mats * rows * row_bytes(type, cols);
     uint8_t* raw = nullptr;
-    HIPCHK(hipMalloc(&out.qs, m.qs_es * n_mats));
-    HIPCHK(hipMalloc(&out.sc, m.sc_es * n_mats));
+    HIPCHK(hipMalloc(&out.qs, m.qs_es * n_mats + jx::QMAT_PAD));
+    HIPCHK(hipMalloc(&out.sc, m.sc_es * n_mats + jx::QMAT_PAD));
+    HIPCHK(hipMemsetAsync(out.qs + m.qs_es * n_mats, 0, jx::QMAT_PAD, st));
+    HIPCHK(hipMemsetAsync(out.sc + m.sc_es * n_mats, 0, jx::QMAT_PAD, st));
+    m.pad_qs = out.qs + m.qs_es * n_mats;
+    m.pad_sc = out.sc + m.sc_es * n_mats;
     HIPCHK(hipMalloc(&raw, raw_bytes));
     hipError_t e = hipMemcpyAsync(raw, host, raw_bytes, hipMemcpyHostToDevice, st);
     if (e == hipSuccess) {
@@ -471,6 +475,14 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
         if (!q8_activation(D->sh_down_type, D->d_ff_shared) && D->sh_down_type != jx::T_Q4_K)
             return fail(JX_ERR_UNSUPPORTED, "shared down projection shape not covered");
     }
+    {  // the GEMVs stage up to 4 token rows of activations in LDS
+        auto down_k = [](int t, int f) { return q8_activation(t, f) ? f : (f + 255) / 256 * 256; };
+        if (D->d_model > jx::gemv_max_k(true, 4, false) ||
+            down_k(D->down_type, D->d_ff) > jx::gemv_max_k(false, 4, !q8_activation(D->down_type, D->d_ff)) ||
+            (D->d_ff_shared > 0 && down_k(D->sh_down_type, D->d_ff_shared) >
+                                       jx::gemv_max_k(false, 4, !q8_activation(D->sh_down_type, D->d_ff_shared))))
+            return fail(JX_ERR_UNSUPPORTED, "d_model / d_ff exceed the GEMVs' staged activation capacity");
+    }
     auto* L = new jx_moe_layer();
     L->device = g_device;
     L->E = D->n_experts;
@@ -666,6 +678,8 @@ int jx_matmul_quant_f32(jx_qmatrix* W, const float* x, float* out) {
     const bool q8 = rows >= 8 && q8_activation(W->type, cols);
     if (!q8 && W->type != jx::T_Q4_K)
         return fail(JX_ERR_UNSUPPORTED, "fp32-activation dot only implemented for Q4_K");
+    if (((size_t)cols + 255) / 256 * 256 > (size_t)jx::gemv_max_k(false, 1, !q8))
+        return fail(JX_ERR_UNSUPPORTED, "cols exceeds the GEMV's staged activation capacity");
     Scratch s;
     const size_t kpad = ((size_t)cols + 255) / 256 * 256;
     float* xd = s.get<float>(kpad);
@@ -701,6 +715,8 @@ int jx_matmul_swiglu_quant_f32(jx_qmatrix* Wg, jx_qmatrix* Wu, const float* x, f
     const int rows = Wg->rows, cols = Wg->cols;
     if (!(rows >= 8 && cols % 32 == 0 && q8_activation(Wg->type, cols)))
         return fail(JX_ERR_UNSUPPORTED, "fp32-activation gate/up not implemented");
+    if (cols > jx::gemv_max_k(true, 1, false))
+        return fail(JX_ERR_UNSUPPORTED, "cols exceeds the GEMV's staged activation capacity");
     Scratch s;
     float* xd = s.get<float>(cols);
     const size_t fpad = ((size_t)rows + 255) / 256 * 256;
