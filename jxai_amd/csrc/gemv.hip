@@ -278,24 +278,18 @@ __device__ __forceinline__ void unit_accum_f32(const RawQ4K& c, const ActLds& A,
     }
 }
 
-__device__ __forceinline__ void group_of(const Groups& g, int slot, int& e, int& p0, int& cnt) {
-    if (g.identity) {
-        e = 0;
-        p0 = 0;
-        cnt = slot == 0 ? g.n_tok : 0;
-    } else if (slot < *g.n_act) {
-        e = g.act[slot];
-        p0 = g.offs[e];
-        cnt = g.counts[e];
-    } else {
-        e = 0;
-        p0 = 0;
-        cnt = 0;
-    }
+// (expert, first pair, pair count, first token) of a slot: one 16-byte load
+// of the dispatch record, so the weight streams start one L2 round trip after
+// the kernel does.
+__device__ __forceinline__ int4 group_of(const Groups& g, int slot) {
+    if (g.identity) return make_int4(0, 0, slot == 0 ? g.n_tok : 0, 0);
+    return g.slots[slot];
 }
 
-__device__ __forceinline__ int token_of(const Groups& g, int p) {
-    return g.identity ? p : g.pair_tok[p];
+// Token of sorted pair p0 + i of a group (the first one is in its record).
+__device__ __forceinline__ int token_of(const Groups& g, const int4& rec, int i) {
+    if (g.identity) return rec.y + i;
+    return i == 0 ? rec.w : g.pair_tok[rec.y + i];
 }
 
 // LDS bytes of one token group's staged activations.
@@ -386,6 +380,10 @@ __device__ __forceinline__ void store_q8_block(float hv, int m, bool writer, Act
     }
 }
 
+#ifndef JX_GEMV_DEPTH
+#define JX_GEMV_DEPTH 2
+#endif
+
 // The K loop of one wave over units lo, lo + stride, ... < nu of one or two
 // weight matrices: two register sets alternate, so unit u+stride is in flight
 // while u is consumed (and u+2*stride is issued right after).  pre() runs
@@ -404,6 +402,16 @@ __device__ __forceinline__ void kloop(const QMat& W0, const QMat& W1, int e, int
         if constexpr (NMAT == 2) F::load(r1, W1, e, rt, u, m, h, u < nu);
     };
     int u = lo;
+#if JX_GEMV_DEPTH == 1
+    ld(a0, a1, u);
+    pre();
+    for (; u < nu; u += stride) {
+        accum(a0, a1, u);
+        ld(a0, a1, u + stride);
+    }
+    (void)b0;
+    (void)b1;
+#else
     ld(a0, a1, u);
     ld(b0, b1, u + stride);
     pre();
@@ -414,6 +422,7 @@ __device__ __forceinline__ void kloop(const QMat& W0, const QMat& W1, int e, int
         accum(b0, b1, u + stride);
         ld(b0, b1, u + 3 * stride);
     }
+#endif
 }
 
 // Resident waves per SIMD the GEMVs are compiled for (single-token groups:
@@ -432,8 +441,8 @@ k_gemv_gateup(QMat G, QMat U, ActQ8 xq, Groups grp, ActQ8 hq, float* hf, int hf_
     extern __shared__ __align__(16) int8_t smem[];
     __shared__ float red[WAVES][TB][32];
     const int rt = blockIdx.x;
-    int e, p0, cnt;
-    group_of(grp, blockIdx.y, e, p0, cnt);
+    const int4 rec = group_of(grp, blockIdx.y);
+    const int e = rec.x, p0 = rec.y, cnt = rec.z;
     if (cnt == 0) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 31, h = lane >> 5;
     const int mat = wave / HW, kw = wave % HW;
@@ -444,7 +453,7 @@ k_gemv_gateup(QMat G, QMat U, ActQ8 xq, Groups grp, ActQ8 hq, float* hf, int hf_
     for (int tb0 = 0; tb0 < cnt; tb0 += TB) {
         const int nt = min(TB, cnt - tb0);
         if (tb0) __syncthreads();  // previous group's LDS reads are done
-        auto src = [&](int j) { return (size_t)token_of(grp, p0 + tb0 + j); };
+        auto src = [&](int j) { return (size_t)token_of(grp, rec, tb0 + j); };
         StageQ8<WAVES * 64, TB == 1 ? 4 : 8, TB == 1 ? 2 : 4> sg;
         sg.issue(xq, nt, src, tid);
         float acc[TB];
@@ -489,8 +498,8 @@ k_gemv_down(QMat D, ActQ8 hq, const float* hf, int hf_ld, Groups grp, float* y) 
     extern __shared__ __align__(16) int8_t smem[];
     __shared__ float red[WAVES][TB][32];
     const int rt = blockIdx.x;
-    int e, p0, cnt;
-    group_of(grp, blockIdx.y, e, p0, cnt);
+    const int4 rec = group_of(grp, blockIdx.y);
+    const int e = rec.x, p0 = rec.y, cnt = rec.z;
     if (cnt == 0) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 31, h = lane >> 5;
     const int K = F32ACT ? hf_ld : hq.K;
@@ -541,8 +550,14 @@ k_gemv_down(QMat D, ActQ8 hq, const float* hf, int hf_ld, Groups grp, float* y) 
     }
 }
 
-constexpr int GATEUP_WAVES = 4;
-constexpr int DOWN_WAVES = 8;
+#ifndef JX_GEMV_GATEUP_WAVES
+#define JX_GEMV_GATEUP_WAVES 4
+#endif
+#ifndef JX_GEMV_DOWN_WAVES
+#define JX_GEMV_DOWN_WAVES 8
+#endif
+constexpr int GATEUP_WAVES = JX_GEMV_GATEUP_WAVES;
+constexpr int DOWN_WAVES = JX_GEMV_DOWN_WAVES;
 
 // Largest K one token group of TB rows stages (the StageQ8 / StageF32
 // register slots: 16 * MQ * NTH quant bytes, 32 * MS * NTH block scales,
@@ -554,11 +569,13 @@ int gemv_max_k(bool gateup, int tb, bool f32) {
     return std::min(16 * mq * nth, 32 * ms * nth) / rows;
 }
 
-// Dynamic LDS above the default 64 KB needs the kernel's opt-in.
+// Dynamic LDS above the default 64 KB needs the kernel's opt-in (a refusal
+// surfaces as the launch's error).
 template <typename Kern>
 static void lds_optin(Kern k, size_t bytes) {
-    if (bytes > 65536) (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (bytes > 65536)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)bytes);
 }
 
 template <int TYPE>

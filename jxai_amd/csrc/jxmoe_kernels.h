@@ -63,6 +63,8 @@ struct Groups {
     const int* offs = nullptr;    // [E+1]
     const int* act = nullptr;     // [E] active experts, increasing id
     const int* n_act = nullptr;   // [1]
+    const int4* slots = nullptr;  // [E] per active-expert slot: (expert, first pair, pair count, first
+                                  // pair's token); slots >= n_act hold a zero count
     const int* pair_tok = nullptr;  // [P] sorted pair -> token
     const int4* tiles = nullptr;  // [T] (expert, first pair, pair count, 0) MFMA tiles
     const int* n_tiles = nullptr; // [1]
@@ -88,9 +90,21 @@ struct RouteArgs {
     float* logits;         // [n][E] or null
 };
 
+// Outputs of the token -> expert dispatch (the device side of Groups).
+struct DispatchOut {
+    int* counts;    // [E]
+    int* offs;      // [E+1]
+    int* act;       // [E]
+    int* n_act;     // [1]
+    int* pair_tok;  // [n*k]
+    int* pos_of;    // [n*k] flat (token, slot) -> sorted pair
+    int4* tiles;    // MFMA tiles
+    int* n_tiles;   // [1]
+    int4* slots;    // [E] see Groups::slots
+};
+
 void launch_route(const RouteArgs& a, hipStream_t st);
-void launch_dispatch(const int* ids, int nk, int E, int top_k, int* counts, int* offs, int* act, int* n_act,
-                     int* pair_tok, int* pos_of, int4* tiles, int* n_tiles, hipStream_t st);
+void launch_dispatch(const int* ids, int nk, int E, int top_k, const DispatchOut& o, hipStream_t st);
 
 // Decode regime: gate+up dequant-GEMV with SwiGLU and Q8_0 re-quantization.
 // Output rows are sorted pairs (routed) or tokens (shared).
@@ -112,14 +126,15 @@ void launch_mfma_down(const QMat& dn, const ActH& hin, const Groups& grp, int ti
 void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
                     const float* shscale, float* out, hipStream_t st);
 
-// Routing for a few tokens (n <= ROUTE_SMALL_MAX_N): one block per router row
-// with the row staged in LDS; the last block to finish does top-k, softmax and
-// the dispatch (replacing launch_dispatch).  `done` is a zeroed counter the
-// kernel leaves at zero.
+// Routing for a few tokens (n <= ROUTE_SMALL_MAX_N), two launches: one block
+// per router row (the row and the tokens staged in LDS) writes the logits and
+// its share of the Q8_0 activations; then one block ranks, normalises and
+// dispatches (replacing launch_dispatch).  The kernel boundary orders the two
+// (no device-scope fences, which on a multi-XCD part write back and
+// invalidate L2).
 constexpr int ROUTE_SMALL_MAX_N = 2;
 bool route_small_fits(int n, int d, int E);
-void launch_route_small(const RouteArgs& a, int* done, int* counts, int* offs, int* act, int* n_act, int* pair_tok,
-                        int* pos_of, int4* tiles, int* n_tiles, hipStream_t st);
+void launch_route_small(const RouteArgs& a, const DispatchOut& o, hipStream_t st);
 
 // Q8_0 of rows x K fp32 (row-major, K % 32 == 0).
 void launch_quantize_q8(const float* x, int rows, int K, ActQ8 out, hipStream_t st);

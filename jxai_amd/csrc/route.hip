@@ -212,8 +212,8 @@ void launch_q8_to_acth(const ActQ8& in, int rows, ActH out, hipStream_t st) {
 // or the shared-expert gate vector as row E): it stages that row and the n
 // tokens in LDS with all loads in flight, then 16 lanes per token run the
 // vec_dot_f32 chains from LDS.  Blocks also split the Q8_0 quantization of x.
-// The last block to finish (device-scope counter) ranks, normalises and
-// dispatches: with n*k <= 2*32 pairs the counting sort is a short serial loop.
+// A second one-block launch ranks, normalises and dispatches: with
+// n*k <= 2*32 pairs the counting sort is a short serial loop.
 constexpr int RS_THREADS = 256;
 constexpr int RS_LDS_BYTES = 48 * 1024;
 
@@ -222,26 +222,30 @@ bool route_small_fits(int n, int d, int E) {
            d % 4 == 0;
 }
 
-__device__ __forceinline__ float coherent_load(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 __global__ void __launch_bounds__(RS_THREADS)
-k_route_small(RouteArgs a, int* done, int* counts, int* offs, int* act, int* n_act, int* pair_tok, int* pos_of,
-              int4* tiles, int* n_tiles) {
+k_route_small(RouteArgs a) {
     extern __shared__ float lds[];  // [0, d): router row; then n token rows
-    __shared__ int s_last;
-    __shared__ int rank_sel[ROUTE_SMALL_MAX_N][MAX_K];
     const int r = blockIdx.x, tid = threadIdx.x;
     const int d = a.d, n = a.n, E = a.E;
     float* ws = lds;
-    float* xs = lds + d;
     const float* w = r < E ? a.router + (size_t)r * d : a.shgate;
-    for (int i = tid * 4; i < d; i += RS_THREADS * 4)
-        *reinterpret_cast<float4*>(ws + i) = *reinterpret_cast<const float4*>(w + i);
-    for (int t = 0; t < n; ++t)
-        for (int i = tid * 4; i < d; i += RS_THREADS * 4)
-            *reinterpret_cast<float4*>(xs + (size_t)t * d + i) = *reinterpret_cast<const float4*>(a.x + (size_t)t * d + i);
+    {  // router row + token rows -> LDS: every load in flight before the first store
+        constexpr int PER = RS_LDS_BYTES / 16 / RS_THREADS;
+        const int c4 = d / 4, tot = (1 + n) * c4;  // route_small_fits: tot * 16 <= RS_LDS_BYTES
+        float4 v[PER];
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int i = min(tid + q * RS_THREADS, tot - 1);
+            const float* src = i < c4 ? w + 4 * i : a.x + 4 * (i - c4);
+            v[q] = *reinterpret_cast<const float4*>(src);
+        }
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int i = min(tid + q * RS_THREADS, tot - 1);
+            *reinterpret_cast<float4*>(lds + 4 * i) = v[q];
+        }
+    }
+    float* xs = lds + d;
     __syncthreads();
 
     // this block's share of the Q8_0 blocks of x (32 lanes per block)
@@ -276,23 +280,22 @@ k_route_small(RouteArgs a, int* done, int* counts, int* offs, int* act, int* n_a
         for (int i = d16 + (has8 ? 8 : 0); i < d; ++i) s = __builtin_fmaf(ws[i], xt[i], s);
         if (ok && j == 0) {
             if (r < E) a.logits[(size_t)t * E + r] = a.bias ? s + a.bias[r] : s;
-            else a.shscale[t] = s;  // raw shared-gate logit; the last block applies the sigmoid
+            else a.shscale[t] = s;  // raw shared-gate logit; k_topk_small applies the sigmoid
         }
     }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_last = atomicAdd(done, 1) == (int)gridDim.x - 1;
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+}
 
-    // ---- last block: top-k + softmax for every token
-    const int k = a.k;
-    float* lgs = lds;  // reuse LDS: [n][E] logits
-    for (int i = tid; i < n * E; i += RS_THREADS) lgs[i] = coherent_load(a.logits + i);
+// Top-k + softmax (select_experts_cache_aware, src/tier.cpp:144-188) and the
+// dispatch for n <= ROUTE_SMALL_MAX_N tokens, by one block of NTH threads:
+// lgs holds the [n][E] logits in LDS (reused for the histogram), shl the raw
+// shared-gate logit of each token (null: no shared gate).
+template <int NTH>
+__device__ void topk_dispatch_small(const RouteArgs& a, const DispatchOut& o, float* lgs, const float* shl,
+                                    int (*rank_sel)[MAX_K], int tid) {
+    const int n = a.n, E = a.E, k = a.k;
     if (tid < n * MAX_K) rank_sel[tid / MAX_K][tid % MAX_K] = tid % MAX_K;  // valid default slots
     __syncthreads();
-    for (int i = tid; i < n * E; i += RS_THREADS) {
+    for (int i = tid; i < n * E; i += NTH) {
         const int t = i / E, e = i % E;
         const float* lt = lgs + (size_t)t * E;
         const float le = lt[e];
@@ -317,48 +320,160 @@ k_route_small(RouteArgs a, int* done, int* counts, int* offs, int* act, int* n_a
             a.ids[(size_t)t * k + i] = rank_sel[t][i];
             a.probs[(size_t)t * k + i] = p[i] * inv;
         }
-        if (a.shscale) a.shscale[t] = a.shgate ? 1.0f / (1.0f + expf(-coherent_load(a.shscale + t))) : 1.0f;
+        if (a.shscale) a.shscale[t] = shl ? 1.0f / (1.0f + expf(-shl[t])) : 1.0f;
     }
     __syncthreads();
-    // ---- dispatch (stable counting sort over the n*k pairs)
-    for (int e = tid; e < E; e += RS_THREADS) counts[e] = 0;
+    // ---- dispatch (stable counting sort over the n*k pairs); the serial part
+    // keeps every value it re-reads in LDS (a global read-back would cost an
+    // L2 round trip per expert)
+    int* hist = reinterpret_cast<int*>(lgs);  // [E] counts, then [E] running offsets
+    int* pos = hist + E;
+    for (int e = tid; e < E; e += NTH) hist[e] = 0;
     __syncthreads();
     if (tid == 0) {
         const int nk = n * k;
-        int* hist = reinterpret_cast<int*>(lgs);  // E ints
-        for (int e = 0; e < E; ++e) hist[e] = 0;
         for (int f = 0; f < nk; ++f) hist[rank_sel[f / k][f % k]]++;
         int off = 0, na = 0, nt = 0;
         for (int e = 0; e < E; ++e) {
             const int c = hist[e];
-            counts[e] = c;
-            offs[e] = off;
+            pos[e] = off;
             if (c > 0) {
-                act[na++] = e;
-                for (int i = 0; i * MFMA_BN < c; ++i) tiles[nt++] = make_int4(e, off + i * MFMA_BN, min(MFMA_BN, c - i * MFMA_BN), 0);
+                o.act[na] = e;
+                // first pair of an active expert is its smallest flat index
+                int f0 = 0;
+                while (rank_sel[f0 / k][f0 % k] != e) ++f0;
+                o.slots[na] = make_int4(e, off, c, f0 / k);
+                ++na;
+                for (int i = 0; i * MFMA_BN < c; ++i)
+                    o.tiles[nt++] = make_int4(e, off + i * MFMA_BN, min(MFMA_BN, c - i * MFMA_BN), 0);
             }
-            hist[e] = off;  // running write position
             off += c;
         }
-        offs[E] = off;
-        *n_act = na;
-        *n_tiles = nt;
+        o.offs[E] = off;
+        *o.n_act = na;
+        *o.n_tiles = nt;
+        for (int s2 = na; s2 < E; ++s2) o.slots[s2] = make_int4(0, 0, 0, 0);
         for (int f = 0; f < nk; ++f) {
             const int e = rank_sel[f / k][f % k];
-            const int pos = hist[e]++;
-            pair_tok[pos] = f / k;
-            pos_of[f] = pos;
+            const int p = pos[e]++;
+            o.pair_tok[p] = f / k;
+            o.pos_of[f] = p;
         }
-        *done = 0;
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += NTH) {  // counts and offsets, written in parallel
+        o.counts[e] = hist[e];
+        o.offs[e] = pos[e] - hist[e];
     }
 }
 
-void launch_route_small(const RouteArgs& a, int* done, int* counts, int* offs, int* act, int* n_act, int* pair_tok,
-                        int* pos_of, int4* tiles, int* n_tiles, hipStream_t st) {
+// Second launch of the few-token router: logits from k_route_small.
+__global__ void __launch_bounds__(RS_THREADS) k_topk_small(RouteArgs a, DispatchOut o) {
+    extern __shared__ float lds[];
+    __shared__ int rank_sel[ROUTE_SMALL_MAX_N][MAX_K];
+    __shared__ float shl[ROUTE_SMALL_MAX_N];
+    const int tid = threadIdx.x;
+    for (int i = tid; i < a.n * a.E; i += RS_THREADS) lds[i] = a.logits[i];
+    if (tid < a.n) shl[tid] = a.shgate ? a.shscale[tid] : 0.0f;
+    __syncthreads();
+    topk_dispatch_small<RS_THREADS>(a, o, lds, a.shgate ? shl : nullptr, rank_sel, tid);
+}
+
+// The whole few-token routing in one block when the router fits in LDS
+// (Mixtral-sized routers: 8 x 4096 fp32 = 128 KB): stage router + tokens with
+// every load in flight, Q8_0 of x, the vec_dot_f32 chains (16 lanes each, as
+// in k_route), then top-k, softmax and dispatch.  One launch instead of two,
+// one HBM round trip.
+constexpr int R1_THREADS = 1024;
+constexpr int R1_PER = 10;  // float4 staging slots per thread
+constexpr size_t R1_LDS_BYTES = (size_t)R1_THREADS * R1_PER * 16;
+
+static size_t route_one_lds(int n, int d, int E, bool shgate) {
+    return ((size_t)(E + (shgate ? 1 : 0) + n) * d + (size_t)std::max(n, 2) * E) * sizeof(float);
+}
+
+bool route_one_fits(int n, int d, int E, bool shgate) {
+    return n >= 1 && n <= ROUTE_SMALL_MAX_N && E <= 64 && d % 16 == 0 &&
+           (size_t)(E + (shgate ? 1 : 0) + n) * d * sizeof(float) <= R1_LDS_BYTES &&
+           route_one_lds(n, d, E, shgate) <= 160 * 1024;
+}
+
+__global__ void __launch_bounds__(R1_THREADS) k_route_one(RouteArgs a, DispatchOut o) {
+    extern __shared__ float lds[];  // [rows][d] router (+ shared gate), [n][d] tokens, [n][E] logits
+    __shared__ int rank_sel[ROUTE_SMALL_MAX_N][MAX_K];
+    __shared__ float shl[ROUTE_SMALL_MAX_N];
+    const int tid = threadIdx.x;
+    const int d = a.d, n = a.n, E = a.E, rows = E + (a.shgate ? 1 : 0);
+    float* xs = lds + (size_t)rows * d;
+    float* lgs = xs + (size_t)n * d;
+    {
+        const int c4 = d / 4, tot = (rows + n) * c4;  // route_one_fits: tot <= R1_THREADS * R1_PER
+        float4 v[R1_PER];
+#pragma unroll
+        for (int q = 0; q < R1_PER; ++q) {
+            const int i = min(tid + q * R1_THREADS, tot - 1);
+            const int row = i / c4, c = i - row * c4;
+            const float* src = row < E ? a.router + (size_t)row * d : (row < rows ? a.shgate : a.x + (size_t)(row - rows) * d);
+            v[q] = *reinterpret_cast<const float4*>(src + 4 * c);
+        }
+#pragma unroll
+        for (int q = 0; q < R1_PER; ++q) {
+            const int i = min(tid + q * R1_THREADS, tot - 1);
+            *reinterpret_cast<float4*>(lds + 4 * i) = v[q];
+        }
+    }
+    __syncthreads();
+    // the first CW waves run the (token, router row) chains, the others quantize x
+    const int chains = n * rows, CW = min(R1_THREADS / 64 - 1, (chains + 3) / 4);
+    if ((tid >> 6) >= CW) {  // Q8_0 of x, one 32-block per half-wave
+        const int nb = d / 32, lane = tid & 63, half = lane >> 5, l32 = lane & 31;
+        for (int b = ((tid >> 6) - CW) * 2 + half; b < n * nb; b += (R1_THREADS / 64 - CW) * 2)
+            quant_block(xs[(size_t)b * 32 + l32], l32, true, a.xq, (size_t)(b / nb), b % nb);
+    }
+    // chains, 16 lanes each, vec_dot_f32 order (d % 16 == 0: no tails)
+    for (int c = tid >> 4; c < chains && (tid >> 6) < CW; c += CW * 4) {
+        const int t = c / rows, r = c % rows, j = tid & 15;
+        const float* w = lds + (size_t)r * d;
+        const float* xt = xs + (size_t)t * d;
+        float acc = 0.0f;
+#pragma unroll 32
+        for (int i = 0; i < d; i += 16) acc = __builtin_fmaf(w[i + j], xt[i + j], acc);
+        const float hi = __shfl_down(acc, 8, 16);
+        const float v = acc + hi;
+        float s = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) s += __shfl(v, q, 16);
+        if (j == 0) {
+            if (r < E) {
+                const float l = a.bias ? s + a.bias[r] : s;
+                lgs[t * E + r] = l;
+                a.logits[(size_t)t * E + r] = l;
+            } else {
+                shl[t] = s;
+            }
+        }
+    }
+    __syncthreads();
+    topk_dispatch_small<R1_THREADS>(a, o, lgs, a.shgate ? shl : nullptr, rank_sel, tid);
+}
+
+void launch_route_small(const RouteArgs& a, const DispatchOut& o, hipStream_t st) {
     const int rows = a.E + (a.shgate ? 1 : 0);
-    const size_t lds = std::max((size_t)(1 + a.n) * a.d, (size_t)a.n * a.E + 1) * sizeof(float);
-    hipLaunchKernelGGL(k_route_small, dim3(rows), dim3(RS_THREADS), lds, st, a, done, counts, offs, act, n_act, pair_tok,
-                       pos_of, tiles, n_tiles);
+    if (route_one_fits(a.n, a.d, a.E, a.shgate != nullptr)) {
+        const size_t lds = route_one_lds(a.n, a.d, a.E, a.shgate != nullptr);
+        // dynamic LDS above 64 KB needs the kernel's opt-in; without it, the two-launch path
+        const bool ok = lds <= 65536 || hipFuncSetAttribute(reinterpret_cast<const void*>(k_route_one),
+                                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                            (int)lds) == hipSuccess;
+        if (ok) {
+            hipLaunchKernelGGL(k_route_one, dim3(1), dim3(R1_THREADS), lds, st, a, o);
+            return;
+        }
+        (void)hipGetLastError();  // clear the refused opt-in
+    }
+    hipLaunchKernelGGL(k_route_small, dim3(rows), dim3(RS_THREADS), (size_t)(1 + a.n) * a.d * sizeof(float), st, a);
+    hipLaunchKernelGGL(k_topk_small, dim3(1), dim3(RS_THREADS), (size_t)std::max(a.n, 2) * a.E * sizeof(float), st, a,
+                       o);
 }
 
 // One block per expert.  Every block builds the full per-expert histogram in
@@ -369,11 +484,10 @@ void launch_route_small(const RouteArgs& a, int* done, int* counts, int* offs, i
 constexpr int DISPATCH_THREADS = 256;
 
 __global__ void __launch_bounds__(DISPATCH_THREADS)
-k_dispatch(const int* ids, int nk, int E, int top_k, int* counts, int* offs, int* act, int* n_act, int* pair_tok, int* pos_of,
-           int4* tiles, int* n_tiles) {
+k_dispatch(const int* ids, int nk, int E, int top_k, DispatchOut o) {
     extern __shared__ int hist[];
     __shared__ int wtot[DISPATCH_THREADS / 64];
-    __shared__ int s_off, s_toff;
+    __shared__ int s_off, s_toff, s_na;
     const int e = blockIdx.x;
     const int tid = threadIdx.x;
     for (int i = tid; i < E; i += DISPATCH_THREADS) hist[i] = 0;
@@ -389,21 +503,23 @@ k_dispatch(const int* ids, int nk, int E, int top_k, int* counts, int* offs, int
         }
         s_off = off;
         s_toff = toff;
+        s_na = na;
         const int c = hist[e];
-        counts[e] = c;
-        offs[e] = off;
-        if (c > 0) act[na] = e;
+        o.counts[e] = c;
+        o.offs[e] = off;
+        if (c > 0) o.act[na] = e;
+        else o.slots[E - 1 - (e - na)] = make_int4(0, 0, 0, 0);  // inactive experts fill slots n_act..E-1
         if (e == E - 1) {
-            offs[E] = off + c;
-            *n_act = na + (c > 0);
-            *n_tiles = toff + (c + MFMA_BN - 1) / MFMA_BN;
+            o.offs[E] = off + c;
+            *o.n_act = na + (c > 0);
+            *o.n_tiles = toff + (c + MFMA_BN - 1) / MFMA_BN;
         }
     }
     __syncthreads();
     const int cnt = hist[e];
     const int off = s_off;
     for (int i = tid; i * MFMA_BN < cnt; i += DISPATCH_THREADS)
-        tiles[s_toff + i] = make_int4(e, off + i * MFMA_BN, min(MFMA_BN, cnt - i * MFMA_BN), 0);
+        o.tiles[s_toff + i] = make_int4(e, off + i * MFMA_BN, min(MFMA_BN, cnt - i * MFMA_BN), 0);
     if (cnt == 0) return;
     const int lane = tid & 63, wave = tid >> 6;
     int run = 0;
@@ -421,18 +537,17 @@ k_dispatch(const int* ids, int nk, int E, int top_k, int* counts, int* offs, int
         }
         if (pred) {
             const int p = off + run + woff + lp;
-            pair_tok[p] = f / top_k;
-            pos_of[f] = p;
+            o.pair_tok[p] = f / top_k;
+            o.pos_of[f] = p;
+            if (p == off) o.slots[s_na] = make_int4(e, off, cnt, f / top_k);
         }
         run += tot;
         __syncthreads();
     }
 }
 
-void launch_dispatch(const int* ids, int nk, int E, int top_k, int* counts, int* offs, int* act, int* n_act,
-                     int* pair_tok, int* pos_of, int4* tiles, int* n_tiles, hipStream_t st) {
-    hipLaunchKernelGGL(k_dispatch, dim3(E), dim3(DISPATCH_THREADS), (size_t)E * sizeof(int), st, ids, nk, E, top_k,
-                       counts, offs, act, n_act, pair_tok, pos_of, tiles, n_tiles);
+void launch_dispatch(const int* ids, int nk, int E, int top_k, const DispatchOut& o, hipStream_t st) {
+    hipLaunchKernelGGL(k_dispatch, dim3(E), dim3(DISPATCH_THREADS), (size_t)E * sizeof(int), st, ids, nk, E, top_k, o);
 }
 
 // MoE combine (transformer.cpp:2728-2730 and 2752-2754): starting from 0, for

@@ -157,10 +157,10 @@ struct jx_moe_layer {
     int *ids = nullptr, *counts = nullptr, *offs = nullptr, *act = nullptr, *n_act = nullptr, *pair_tok = nullptr,
         *pos_of = nullptr, *n_tiles = nullptr;
     int4* tiles = nullptr;
+    int4* slots = nullptr;
     jx::ActQ8 xq, hq, hqs;
     DevActH xh, hh, hhs;  // matrix-core forms of x, h, shared h
     float *hf = nullptr, *hfs = nullptr, *y = nullptr, *ysh = nullptr;
-    int* done = nullptr;  // zeroed counter for the last-block pattern of the small-n router
     int last_n = 0;
     Prof prof;
     hipStream_t own = nullptr;  // used when the caller passes the null stream
@@ -215,6 +215,7 @@ int ensure_workspace(jx_moe_layer* L, int n) {
     WS(L->pos_of, nk);
     WS(L->n_tiles, 1);
     WS(L->tiles, nk / jx::MFMA_BN + std::min<size_t>(L->E, nk) + 1);
+    WS(L->slots, L->E);
     if ((r = L->xh.alloc((size_t)cap, L->d)) != JX_OK || (r = L->hh.alloc(nk, L->F)) != JX_OK) {
         L->cap = 0;
         return r;
@@ -256,7 +257,7 @@ void free_layer(jx_moe_layer* L) {
     for (auto* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown}) m->release();
     void* ptrs[] = {L->router, L->bias, L->shgate, L->x, L->out, L->probs, L->shscale, L->logits, L->ids,
                     L->counts, L->offs, L->act, L->n_act, L->pair_tok, L->pos_of, L->n_tiles, L->tiles,
-                    L->xq.q, L->xq.s, L->hq.q, L->hq.s, L->hqs.q, L->hqs.s, L->hf, L->hfs, L->y, L->ysh};
+                    L->slots, L->xq.q, L->xq.s, L->hq.q, L->hq.s, L->hqs.q, L->hqs.s, L->hf, L->hfs, L->y, L->ysh};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     L->xh.release();
@@ -264,7 +265,6 @@ void free_layer(jx_moe_layer* L) {
     L->hhs.release();
     for (auto ev : L->prof.pool) (void)hipEventDestroy(ev);
     for (auto& kv : L->graphs) (void)hipGraphExecDestroy(kv.second);
-    if (L->done) (void)hipFree(L->done);
     if (L->own) (void)hipStreamDestroy(L->own);
     delete L;
 }
@@ -325,11 +325,12 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
                        (L->sdown_f32 || L->Fs % 128 == 0);
     jx::RouteArgs ra{xdev, n, d, E, k, L->router, L->bias, L->shgate, L->xq, (mfma || smfma) ? L->xh.a : jx::ActH{},
                      L->ids, L->probs, L->shscale, L->logits};
+    const jx::DispatchOut dout{L->counts, L->offs,   L->act,   L->n_act, L->pair_tok,
+                               L->pos_of,  L->tiles, L->n_tiles, L->slots};
     if (jx::route_small_fits(n, d, E)) {
         {
             Launch l(L, "route_dispatch", st);
-            jx::launch_route_small(ra, L->done, L->counts, L->offs, L->act, L->n_act, L->pair_tok, L->pos_of, L->tiles,
-                                   L->n_tiles, st);
+            jx::launch_route_small(ra, dout, st);
         }
         if (mfma || smfma) {
             Launch l(L, "to_matrix_form", st);
@@ -341,14 +342,14 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
             jx::launch_route(ra, st);
         }
         Launch l(L, "dispatch", st);
-        jx::launch_dispatch(L->ids, nk, E, k, L->counts, L->offs, L->act, L->n_act, L->pair_tok, L->pos_of, L->tiles,
-                            L->n_tiles, st);
+        jx::launch_dispatch(L->ids, nk, E, k, dout, st);
     }
     jx::Groups grp;
     grp.counts = L->counts;
     grp.offs = L->offs;
     grp.act = L->act;
     grp.n_act = L->n_act;
+    grp.slots = L->slots;
     grp.pair_tok = L->pair_tok;
     grp.tiles = L->tiles;
     grp.n_tiles = L->n_tiles;
@@ -359,23 +360,12 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     const int tiles_ub = nk / jx::MFMA_BN + slots;
     const size_t fpad = ((size_t)L->F + 255) / 256 * 256;
     if (mfma) {
-        {
-            Launch l(L, "gateup_mfma", st);
-            jx::launch_mfma_gateup(L->gate.m, L->up.m, L->xh.a, grp, tiles_ub, L->down_f32 ? jx::ActH{} : L->hh.a,
-                                   L->down_f32 ? L->hf : nullptr, st);
-        }
-        Launch l(L, L->down_f32 ? "down_gemv_f32" : "down_mfma", st);
-        if (L->down_f32)
-            jx::launch_gemv_down(L->down.m, L->hq, L->hf, (int)fpad, grp, slots, 4, L->y, st);
-        else
-            jx::launch_mfma_down(L->down.m, L->hh.a, grp, tiles_ub, L->y, st);
+        Launch l(L, "gateup_mfma", st);
+        jx::launch_mfma_gateup(L->gate.m, L->up.m, L->xh.a, grp, tiles_ub, L->down_f32 ? jx::ActH{} : L->hh.a,
+                               L->down_f32 ? L->hf : nullptr, st);
     } else {
-        {
-            Launch l(L, "gateup_gemv", st);
-            jx::launch_gemv_gateup(L->gate.m, L->up.m, L->xq, grp, slots, tb, L->hq, L->down_f32 ? L->hf : nullptr, st);
-        }
-        Launch l(L, L->down_f32 ? "down_gemv_f32" : "down_gemv", st);
-        jx::launch_gemv_down(L->down.m, L->hq, L->down_f32 ? L->hf : nullptr, (int)fpad, grp, slots, tb, L->y, st);
+        Launch l(L, "gateup_gemv", st);
+        jx::launch_gemv_gateup(L->gate.m, L->up.m, L->xq, grp, slots, tb, L->hq, L->down_f32 ? L->hf : nullptr, st);
     }
     if (L->shared) {
         jx::Groups sg;
@@ -405,6 +395,15 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
             jx::launch_gemv_down(L->sdown.m, L->hqs, L->sdown_f32 ? L->hfs : nullptr, (int)fspad, sg, 1, tb, L->ysh,
                                  st);
         }
+    }
+    {
+        Launch l(L, mfma ? (L->down_f32 ? "down_gemv_f32" : "down_mfma") : (L->down_f32 ? "down_gemv_f32" : "down_gemv"),
+                 st);
+        if (mfma && !L->down_f32)
+            jx::launch_mfma_down(L->down.m, L->hh.a, grp, tiles_ub, L->y, st);
+        else
+            jx::launch_gemv_down(L->down.m, L->hq, L->down_f32 ? L->hf : nullptr, (int)fpad, grp, slots, mfma ? 4 : tb,
+                                 L->y, st);
     }
     {
         Launch l(L, "combine", st);
@@ -525,8 +524,6 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
         }
     }
     if ((r = ensure_workspace(L, 1)) != JX_OK) return bail(r);
-    if ((r = dalloc(L->done, 1)) != JX_OK) return bail(r);
-    if (hipMemset(L->done, 0, sizeof(int)) != hipSuccess) return bail(fail(JX_ERR_HIP, "counter init"));
     if (hipStreamCreate(&L->own) != hipSuccess) return bail(fail(JX_ERR_HIP, "stream create"));
     if (const char* g = std::getenv("JX_NO_GRAPH")) L->use_graphs = std::strcmp(g, "0") == 0;
     *out = L;
