@@ -31,6 +31,35 @@ from jxai_amd import synth  # noqa: E402
 METRIC = "MoE-layer tok/s (1 GPU); decode HBM GB/s % peak; prefill int8 MFMA % peak"
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "mixtral_layer_traffic.json")
+
+
+def measured_traffic(kernel, tokens):
+    """HBM bytes per launch of `kernel` at `tokens` tokens from the rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by what the counter reads for
+    a plain device copy of known size), or None when no summary covers this kernel."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    k = t.get("kernels", {}).get(f"{kernel}@{tokens}")
+    if not k:
+        return None
+    return 1024.0 * (k["fetch_kib"] * t["fetch_scale"] + k["write_kib"] * t["write_scale"])
+
+
+def copy_calibration():
+    """A plain device copy of 256 MiB, three times: the reference reading for the TCC byte counters."""
+    import torch
+    nbytes = 256 << 20
+    a = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(f"[bench] copied {nbytes} bytes x3", file=sys.stderr, flush=True)
 
 
 def algorithmic(cfg, n, counts):
@@ -103,7 +132,12 @@ def main():
     ap.add_argument("--prefill-tokens", type=int, default=2048)
     ap.add_argument("--decode-tokens", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 256 MiB device copy (scale for the rocprofv3 byte counters)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (experts would shard by "
               "expert parallelism, see DESIGN.md); run with --gpus 1", file=sys.stderr)
@@ -122,9 +156,10 @@ def main():
     a_pre = algorithmic(cfg, n, counts_pre)
     gu_ms, gu_n = prof_pre.get("gateup_mfma", (0.0, 1))
     gu_avg = gu_ms / max(gu_n, 1) / 1e3
-    pre_roof = {"bound": "mfma", "kernel": "k_mfma_gateup (gate+up, int8 MFMA)",
+    pre_roof = {"bound": "mfma", "kernel": "k_wgemm<Q4_K, gate+up> (matrix-core grouped GEMM + SwiGLU)",
                 "achieved": a_pre["gateup_ops"] / gu_avg / 1e12, "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
-                "frac": a_pre["gateup_ops"] / gu_avg / 1e12 / INT8_PEAK_TOPS, "traffic": None,
+                "frac": a_pre["gateup_ops"] / gu_avg / 1e12 / INT8_PEAK_TOPS,
+                "traffic": measured_traffic("k_wgemm<12, true>", n),
                 "avg_launch_us": gu_avg * 1e6,
                 "layer_int8_frac": a_pre["ops"] / s_pre / 1e12 / INT8_PEAK_TOPS}
 
@@ -134,9 +169,10 @@ def main():
     a_dec = algorithmic(cfg, nd, counts_dec)
     dg_ms, dg_n = prof_dec.get("gateup_gemv", (0.0, 1))
     dg_avg = dg_ms / max(dg_n, 1) / 1e3
-    dec_roof = {"bound": "hbm", "kernel": "k_gemv_gateup (gate+up dequant-GEMV)",
+    dec_roof = {"bound": "hbm", "kernel": "k_gemv_gateup<Q4_K> (gate+up dequant-GEMV + SwiGLU)",
                 "achieved": a_dec["gateup_bytes"] / dg_avg / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": a_dec["gateup_bytes"] / dg_avg / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                "frac": a_dec["gateup_bytes"] / dg_avg / 1e9 / HBM_PEAK_GBS,
+                "traffic": measured_traffic("k_gemv_gateup<12, 1, 4>", nd),
                 "avg_launch_us": dg_avg * 1e6,
                 "layer_hbm_frac": a_dec["bytes"] / s_dec / 1e9 / HBM_PEAK_GBS}
 
