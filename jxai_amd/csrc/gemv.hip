@@ -22,6 +22,7 @@
 #include <algorithm>
 
 #include "jxmoe_device.h"
+#include "jxmoe_dispatch.h"
 #include "jxmoe_kernels.h"
 
 namespace jx {
@@ -281,15 +282,33 @@ __device__ __forceinline__ void unit_accum_f32(const RawQ4K& c, const ActLds& A,
 // (expert, first pair, pair count, first token) of a slot: one 16-byte load
 // of the dispatch record, so the weight streams start one L2 round trip after
 // the kernel does.
+// With router logits instead of tables (few-token decode), every wave derives
+// the record itself.
 __device__ __forceinline__ int4 group_of(const Groups& g, int slot) {
     if (g.identity) return make_int4(0, 0, slot == 0 ? g.n_tok : 0, 0);
+    if (g.logits) return small_group(g, slot);
     return g.slots[slot];
 }
 
 // Token of sorted pair p0 + i of a group (the first one is in its record).
 __device__ __forceinline__ int token_of(const Groups& g, const int4& rec, int i) {
     if (g.identity) return rec.y + i;
+    if (g.logits) return rec.w + i;  // n <= 2: a group of two holds tokens 0 and 1
     return i == 0 ? rec.w : g.pair_tok[rec.y + i];
+}
+
+// On the few-token path one extra block of the routed gate/up GEMV writes the
+// dispatch tables (ids, probs, shared-gate scale, counts, offsets, slots, pair
+// lists) while the others stream weights; the kernels after it read them.
+template <int NTH>
+__device__ void small_tail(const SmallTail& t, int tid) {
+    __shared__ float lgs[ROUTE_SMALL_MAX_N * SMALL_GROUP_MAX_E];  // [n][E] logits, then the histogram
+    __shared__ int rank_sel[ROUTE_SMALL_MAX_N][MAX_K];
+    __shared__ float shl[ROUTE_SMALL_MAX_N];
+    for (int i = tid; i < t.a.n * t.a.E; i += NTH) lgs[i] = t.a.logits[i];
+    if (tid < t.a.n) shl[tid] = t.a.shgate ? t.a.shscale[tid] : 0.0f;
+    __syncthreads();
+    topk_dispatch_small<NTH>(t.a, t.o, lgs, t.a.shgate ? shl : nullptr, rank_sel, tid);
 }
 
 // LDS bytes of one token group's staged activations.
@@ -436,10 +455,14 @@ __device__ __forceinline__ void kloop(const QMat& W0, const QMat& W1, int e, int
 // waves streams the gate tile, the second half the up tile.
 template <int TYPE, int TB, int WAVES>
 __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(GEMV_WAVES_PER_SIMD(TB))))
-k_gemv_gateup(QMat G, QMat U, ActQ8 xq, Groups grp, ActQ8 hq, float* hf, int hf_ld) {
+k_gemv_gateup(QMat G, QMat U, ActQ8 xq, Groups grp, ActQ8 hq, float* hf, int hf_ld, SmallTail tail) {
     constexpr int HW = WAVES / 2;  // waves per matrix
     extern __shared__ __align__(16) int8_t smem[];
     __shared__ float red[WAVES][TB][32];
+    if (tail.on && blockIdx.y == gridDim.y - 1) {  // the extra grid row: dispatch tables only
+        if (blockIdx.x == 0) small_tail<WAVES * 64>(tail, threadIdx.x);
+        return;
+    }
     const int rt = blockIdx.x;
     const int4 rec = group_of(grp, blockIdx.y);
     const int e = rec.x, p0 = rec.y, cnt = rec.z;
@@ -580,28 +603,29 @@ static void lds_optin(Kern k, size_t bytes) {
 
 template <int TYPE>
 static void gateup_t(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots, int tb,
-                     ActQ8 hq, float* hf, hipStream_t st) {
-    dim3 grid(g.nrt, slots);
+                     ActQ8 hq, float* hf, hipStream_t st, const SmallTail& tail) {
+    dim3 grid(g.nrt, slots + (tail.on ? 1 : 0));
     const int hf_ld = ((g.rows + 255) / 256) * 256;
     if (tb <= 1) {
         const size_t lds = act_lds_bytes(1, xq.K, false);
         lds_optin(k_gemv_gateup<TYPE, 1, GATEUP_WAVES>, lds);
         hipLaunchKernelGGL((k_gemv_gateup<TYPE, 1, GATEUP_WAVES>), grid, dim3(GATEUP_WAVES * 64), lds, st, g, u, xq,
-                           grp, hq, hf, hf_ld);
+                           grp, hq, hf, hf_ld, tail);
     } else {
         const size_t lds = act_lds_bytes(4, xq.K, false);
         lds_optin(k_gemv_gateup<TYPE, 4, GATEUP_WAVES>, lds);
         hipLaunchKernelGGL((k_gemv_gateup<TYPE, 4, GATEUP_WAVES>), grid, dim3(GATEUP_WAVES * 64), lds, st, g, u, xq,
-                           grp, hq, hf, hf_ld);
+                           grp, hq, hf, hf_ld, tail);
     }
 }
 
 void launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots, int tb,
-                        ActQ8 hq, float* hf, hipStream_t st) {
+                        ActQ8 hq, float* hf, hipStream_t st, const SmallTail* tail) {
+    const SmallTail t = tail ? *tail : SmallTail{};
     switch (g.type) {
-        case T_Q4_0: gateup_t<T_Q4_0>(g, u, xq, grp, slots, tb, hq, hf, st); break;
-        case T_Q8_0: gateup_t<T_Q8_0>(g, u, xq, grp, slots, tb, hq, hf, st); break;
-        case T_Q4_K: gateup_t<T_Q4_K>(g, u, xq, grp, slots, tb, hq, hf, st); break;
+        case T_Q4_0: gateup_t<T_Q4_0>(g, u, xq, grp, slots, tb, hq, hf, st, t); break;
+        case T_Q8_0: gateup_t<T_Q8_0>(g, u, xq, grp, slots, tb, hq, hf, st, t); break;
+        case T_Q4_K: gateup_t<T_Q4_K>(g, u, xq, grp, slots, tb, hq, hf, st, t); break;
         default: break;
     }
 }

@@ -71,7 +71,13 @@ struct Groups {
     int top_k = 1;
     int identity = 0;             // shared expert: pair p is token p, one group of n_tok
     int n_tok = 0;
+    // Few-token decode (n_tok <= ROUTE_SMALL_MAX_N, n_experts <= SMALL_GROUP_MAX_E): when set,
+    // each block derives its slot's group from the router logits [n_tok][n_experts] itself
+    // instead of reading dispatch tables (small_group in jxmoe_dispatch.h).
+    const float* logits = nullptr;
+    int n_experts = 0;
 };
+constexpr int SMALL_GROUP_MAX_E = 64;
 
 constexpr int MFMA_BN = 128;  // pairs per matrix-core GEMM tile
 constexpr int MFMA_MIN_SHARED_TOKENS = 32;  // shared expert on the matrix cores from this many tokens
@@ -103,13 +109,22 @@ struct DispatchOut {
     int4* slots;    // [E] see Groups::slots
 };
 
+// Dispatch tables written by block (0, 0) of the routed gate/up GEMV when its
+// groups come from the logits (the few-token decode path), for the kernels
+// after it and the caller's outputs.
+struct SmallTail {
+    RouteArgs a;      // n, E, k, logits, ids, probs, shscale (raw shared-gate logits on entry), shgate
+    DispatchOut o;
+    int on = 0;
+};
+
 void launch_route(const RouteArgs& a, hipStream_t st);
 void launch_dispatch(const int* ids, int nk, int E, int top_k, const DispatchOut& o, hipStream_t st);
 
 // Decode regime: gate+up dequant-GEMV with SwiGLU and Q8_0 re-quantization.
 // Output rows are sorted pairs (routed) or tokens (shared).
 void launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots,
-                        int tb, ActQ8 hq, float* hf, hipStream_t st);
+                        int tb, ActQ8 hq, float* hf, hipStream_t st, const SmallTail* tail = nullptr);
 // Largest K the GEMVs accept for token groups of `tb` rows (gate/up or down,
 // Q8_0 or fp32 activations).
 int gemv_max_k(bool gateup, int tb, bool f32);
@@ -125,6 +140,12 @@ void launch_mfma_down(const QMat& dn, const ActH& hin, const Groups& grp, int ti
 // out[t] = sum_s p[t][s] * y[pos(t,s)] (+ shscale[t] * ysh[t]), fma in selection order.
 void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
                     const float* shscale, float* out, hipStream_t st);
+
+// Decode routing for n <= ROUTE_SMALL_MAX_N tokens and E <= SMALL_GROUP_MAX_E
+// experts without a dispatch launch: router logits and Q8_0 of x (one block
+// per router row); the routed gate/up GEMV then groups from the logits and
+// writes the tables (SmallTail).
+void launch_route_logits(const RouteArgs& a, hipStream_t st);
 
 // Routing for a few tokens (n <= ROUTE_SMALL_MAX_N), two launches: one block
 // per router row (the row and the tokens staged in LDS) writes the logits and

@@ -4,13 +4,12 @@
 #include <algorithm>
 
 #include "jxmoe_device.h"
+#include "jxmoe_dispatch.h"
 #include "jxmoe_kernels.h"
 
 namespace jx {
 
 constexpr int ROUTE_THREADS = 512;
-constexpr int MAX_E = 512;
-constexpr int MAX_K = 32;
 
 // Q8_0 of one 32-block held one value per lane of a half-wave
 // (quantize_row_q8_0, src/quant.cpp:1029-1045): amax, d = amax/127 (IEEE
@@ -162,14 +161,11 @@ __global__ void __launch_bounds__(ROUTE_THREADS) k_route(RouteArgs a) {
 
     // -- top-k by rank
     for (int e = tid; e < a.E; e += ROUTE_THREADS) {
-        const float le = lg[e];
+        const float le = rank_key(lg[e]);
         int rank = 0;
-        for (int f = 0; f < a.E; ++f) {
-            const float lf = lg[f];
-            rank += (lf > le) || (lf == le && f < e);
-        }
+        for (int f = 0; f < a.E; ++f) rank += ranks_above(rank_key(lg[f]), f, le, e);
         if (rank < a.k) sel[rank] = e;
-        if (a.logits) a.logits[(size_t)t * a.E + e] = le;
+        if (a.logits) a.logits[(size_t)t * a.E + e] = lg[e];
     }
     __syncthreads();
     if (tid == 0) {
@@ -215,155 +211,95 @@ void launch_q8_to_acth(const ActQ8& in, int rows, ActH out, hipStream_t st) {
 // A second one-block launch ranks, normalises and dispatches: with
 // n*k <= 2*32 pairs the counting sort is a short serial loop.
 constexpr int RS_THREADS = 256;
-constexpr int RS_LDS_BYTES = 48 * 1024;
+constexpr int RS_LDS_BYTES = 64 * 1024;
+
+// Rows staged chain-major: element 16 i + j of a row at j * rs_stride(d) + i,
+// so lane j of a vec_dot_f32 chain reads its operands four at a time
+// (stride padded to a multiple of 4 floats, plus 4 against bank conflicts).
+__host__ __device__ inline int rs_stride(int d) { return ((d / 16 + 3) & ~3) + 4; }
+static size_t rs_lds(int n, int d) { return (size_t)(1 + n) * 16 * rs_stride(d) * sizeof(float); }
 
 bool route_small_fits(int n, int d, int E) {
-    return n >= 1 && n <= ROUTE_SMALL_MAX_N && E <= MAX_E && (size_t)(1 + n) * d * sizeof(float) <= RS_LDS_BYTES &&
-           d % 4 == 0;
+    return n >= 1 && n <= ROUTE_SMALL_MAX_N && E <= MAX_E && d % 32 == 0 && rs_lds(n, d) <= RS_LDS_BYTES;
 }
 
 __global__ void __launch_bounds__(RS_THREADS)
 k_route_small(RouteArgs a) {
-    extern __shared__ float lds[];  // [0, d): router row; then n token rows
+    extern __shared__ float lds[];  // (1 + n) chain-major rows: router row r, then the n tokens
     const int r = blockIdx.x, tid = threadIdx.x;
-    const int d = a.d, n = a.n, E = a.E;
-    float* ws = lds;
+    const int d = a.d, n = a.n, E = a.E, S = rs_stride(d), RS = 16 * S;
     const float* w = r < E ? a.router + (size_t)r * d : a.shgate;
     {  // router row + token rows -> LDS: every load in flight before the first store
-        constexpr int PER = RS_LDS_BYTES / 16 / RS_THREADS;
-        const int c4 = d / 4, tot = (1 + n) * c4;  // route_small_fits: tot * 16 <= RS_LDS_BYTES
+        constexpr int PER = (ROUTE_SMALL_MAX_N + 1) * 8192 / 4 / RS_THREADS;  // float4 slots: d <= 8192
+        const int c4 = d / 4, tot = (1 + n) * c4;
         float4 v[PER];
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
-            const int i = min(tid + q * RS_THREADS, tot - 1);
-            const float* src = i < c4 ? w + 4 * i : a.x + 4 * (i - c4);
+            const int i = tid + q * RS_THREADS;
+            if (i >= tot) break;
+            const int row = i / c4, c = i - row * c4;
+            const float* src = row == 0 ? w + 4 * c : a.x + (size_t)(row - 1) * d + 4 * c;
             v[q] = *reinterpret_cast<const float4*>(src);
         }
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
-            const int i = min(tid + q * RS_THREADS, tot - 1);
-            *reinterpret_cast<float4*>(lds + 4 * i) = v[q];
+            const int i = tid + q * RS_THREADS;
+            if (i >= tot) break;
+            const int row = i / c4, c = i - row * c4;
+            float* dst = lds + row * RS + 4 * (c & 3) * S + (c >> 2);  // elements 4c..4c+3: j = 4(c%4)+q, i = c/4
+            dst[0] = v[q].x;
+            dst[S] = v[q].y;
+            dst[2 * S] = v[q].z;
+            dst[3 * S] = v[q].w;
         }
     }
-    float* xs = lds + d;
     __syncthreads();
-
-    // this block's share of the Q8_0 blocks of x (32 lanes per block)
-    {
+    const int wave = tid >> 6, lane = tid & 63;
+    if (wave == 0) {
+        // router row r for every token: vec_dot_f32 order (src/quant.cpp:2756-2778): lane j of
+        // token group t runs the FMA chain over elements 16 i + j (lanes 0-7 the reference's acc0,
+        // 8-15 its acc1), then acc0 + acc1 and the sequential sum of the 8 lanes (d % 16 == 0: no
+        // tails)
+        const int t = lane >> 4, j = lane & 15;
+        if (t < n) {
+            const float* wr = lds + j * S;
+            const float* xr = lds + (1 + t) * RS + j * S;
+            const int m = d / 16, m4 = m & ~3;
+            float acc = 0.0f;
+#pragma unroll 8
+            for (int i = 0; i < m4; i += 4) {
+                const float4 p = *reinterpret_cast<const float4*>(wr + i);
+                const float4 q = *reinterpret_cast<const float4*>(xr + i);
+                acc = __builtin_fmaf(p.x, q.x, acc);
+                acc = __builtin_fmaf(p.y, q.y, acc);
+                acc = __builtin_fmaf(p.z, q.z, acc);
+                acc = __builtin_fmaf(p.w, q.w, acc);
+            }
+            for (int i = m4; i < m; ++i) acc = __builtin_fmaf(wr[i], xr[i], acc);
+            const float hi = __shfl_down(acc, 8, 16);
+            const float v = acc + hi;
+            float s = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) s += __shfl(v, q, 16);
+            if (j == 0) {
+                if (r < E) a.logits[(size_t)t * E + r] = a.bias ? s + a.bias[r] : s;
+                else a.shscale[t] = s;  // raw shared-gate logit; the top-k step applies the sigmoid
+            }
+        }
+    } else {
+        // this block's share of the Q8_0 blocks of x, one per half-wave of waves 1..
         const int nb = d / 32, tot = n * nb;
         const int per = (tot + gridDim.x - 1) / gridDim.x;
         const int b0 = r * per, b1 = min(tot, b0 + per);
-        const int lane = tid & 63, wave = tid >> 6, half = lane >> 5, l32 = lane & 31;
-        for (int bb = b0 + wave * 2; bb < b1; bb += (RS_THREADS / 64) * 2) {
+        const int half = lane >> 5, l32 = lane & 31;
+        constexpr int QW = RS_THREADS / 64 - 1;
+        for (int bb = b0 + (wave - 1) * 2; bb < b1; bb += QW * 2) {
             const int b = bb + half;  // token-major: b = t*nb + block
             const bool ok = b < b1;
-            quant_block(ok ? xs[(size_t)b * 32 + l32] : 0.0f, l32, ok, a.xq, (size_t)(b / nb), b % nb);
+            const int t = ok ? b / nb : 0, q = ok ? (b % nb) * 32 + l32 : 0;
+            const float xv = lds[(1 + t) * RS + (q & 15) * S + (q >> 4)];
+            quant_block(xv, l32, ok, a.xq, (size_t)t, ok ? b % nb : 0);
         }
-    }
-
-    // router row r for every token: vec_dot_f32 order (see k_route)
-    if (tid < 16 * ROUTE_SMALL_MAX_N) {
-        const int t = tid >> 4, j = tid & 15;
-        const bool ok = t < n;
-        const float* xt = xs + (size_t)(ok ? t : 0) * d;
-        const int d16 = (d / 16) * 16;
-        const bool has8 = (d - d16) >= 8;
-        float acc = 0.0f;
-#pragma unroll 8
-        for (int i = 0; i < d16; i += 16) acc = __builtin_fmaf(ws[i + j], xt[i + j], acc);
-        const float hi = __shfl_down(acc, 8, 16);
-        float v = acc + hi;
-        if (has8 && j < 8) v = __builtin_fmaf(ws[d16 + j], xt[d16 + j], v);
-        float s = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) s += __shfl(v, q, 16);
-        for (int i = d16 + (has8 ? 8 : 0); i < d; ++i) s = __builtin_fmaf(ws[i], xt[i], s);
-        if (ok && j == 0) {
-            if (r < E) a.logits[(size_t)t * E + r] = a.bias ? s + a.bias[r] : s;
-            else a.shscale[t] = s;  // raw shared-gate logit; k_topk_small applies the sigmoid
-        }
-    }
-}
-
-// Top-k + softmax (select_experts_cache_aware, src/tier.cpp:144-188) and the
-// dispatch for n <= ROUTE_SMALL_MAX_N tokens, by one block of NTH threads:
-// lgs holds the [n][E] logits in LDS (reused for the histogram), shl the raw
-// shared-gate logit of each token (null: no shared gate).
-template <int NTH>
-__device__ void topk_dispatch_small(const RouteArgs& a, const DispatchOut& o, float* lgs, const float* shl,
-                                    int (*rank_sel)[MAX_K], int tid) {
-    const int n = a.n, E = a.E, k = a.k;
-    if (tid < n * MAX_K) rank_sel[tid / MAX_K][tid % MAX_K] = tid % MAX_K;  // valid default slots
-    __syncthreads();
-    for (int i = tid; i < n * E; i += NTH) {
-        const int t = i / E, e = i % E;
-        const float* lt = lgs + (size_t)t * E;
-        const float le = lt[e];
-        int rank = 0;
-        for (int f = 0; f < E; ++f) rank += (lt[f] > le) || (lt[f] == le && f < e);
-        if (rank < k) rank_sel[t][rank] = e;
-    }
-    __syncthreads();
-    if (tid < n) {
-        const int t = tid;
-        const float* lt = lgs + (size_t)t * E;
-        float p[MAX_K];
-        float mx = lt[rank_sel[t][0]];
-        for (int i = 1; i < k; ++i) mx = fmaxf(mx, lt[rank_sel[t][i]]);
-        float sum = 0.0f;
-        for (int i = 0; i < k; ++i) {
-            p[i] = expf(lt[rank_sel[t][i]] - mx);
-            sum += p[i];
-        }
-        const float inv = (sum > 0.0f) ? 1.0f / sum : 1.0f / (float)k;
-        for (int i = 0; i < k; ++i) {
-            a.ids[(size_t)t * k + i] = rank_sel[t][i];
-            a.probs[(size_t)t * k + i] = p[i] * inv;
-        }
-        if (a.shscale) a.shscale[t] = shl ? 1.0f / (1.0f + expf(-shl[t])) : 1.0f;
-    }
-    __syncthreads();
-    // ---- dispatch (stable counting sort over the n*k pairs); the serial part
-    // keeps every value it re-reads in LDS (a global read-back would cost an
-    // L2 round trip per expert)
-    int* hist = reinterpret_cast<int*>(lgs);  // [E] counts, then [E] running offsets
-    int* pos = hist + E;
-    for (int e = tid; e < E; e += NTH) hist[e] = 0;
-    __syncthreads();
-    if (tid == 0) {
-        const int nk = n * k;
-        for (int f = 0; f < nk; ++f) hist[rank_sel[f / k][f % k]]++;
-        int off = 0, na = 0, nt = 0;
-        for (int e = 0; e < E; ++e) {
-            const int c = hist[e];
-            pos[e] = off;
-            if (c > 0) {
-                o.act[na] = e;
-                // first pair of an active expert is its smallest flat index
-                int f0 = 0;
-                while (rank_sel[f0 / k][f0 % k] != e) ++f0;
-                o.slots[na] = make_int4(e, off, c, f0 / k);
-                ++na;
-                for (int i = 0; i * MFMA_BN < c; ++i)
-                    o.tiles[nt++] = make_int4(e, off + i * MFMA_BN, min(MFMA_BN, c - i * MFMA_BN), 0);
-            }
-            off += c;
-        }
-        o.offs[E] = off;
-        *o.n_act = na;
-        *o.n_tiles = nt;
-        for (int s2 = na; s2 < E; ++s2) o.slots[s2] = make_int4(0, 0, 0, 0);
-        for (int f = 0; f < nk; ++f) {
-            const int e = rank_sel[f / k][f % k];
-            const int p = pos[e]++;
-            o.pair_tok[p] = f / k;
-            o.pos_of[f] = p;
-        }
-    }
-    __syncthreads();
-    for (int e = tid; e < E; e += NTH) {  // counts and offsets, written in parallel
-        o.counts[e] = hist[e];
-        o.offs[e] = pos[e] - hist[e];
     }
 }
 
@@ -457,6 +393,11 @@ __global__ void __launch_bounds__(R1_THREADS) k_route_one(RouteArgs a, DispatchO
     topk_dispatch_small<R1_THREADS>(a, o, lgs, a.shgate ? shl : nullptr, rank_sel, tid);
 }
 
+void launch_route_logits(const RouteArgs& a, hipStream_t st) {
+    const int rows = a.E + (a.shgate ? 1 : 0);
+    hipLaunchKernelGGL(k_route_small, dim3(rows), dim3(RS_THREADS), rs_lds(a.n, a.d), st, a);
+}
+
 void launch_route_small(const RouteArgs& a, const DispatchOut& o, hipStream_t st) {
     const int rows = a.E + (a.shgate ? 1 : 0);
     if (route_one_fits(a.n, a.d, a.E, a.shgate != nullptr)) {
@@ -471,7 +412,7 @@ void launch_route_small(const RouteArgs& a, const DispatchOut& o, hipStream_t st
         }
         (void)hipGetLastError();  // clear the refused opt-in
     }
-    hipLaunchKernelGGL(k_route_small, dim3(rows), dim3(RS_THREADS), (size_t)(1 + a.n) * a.d * sizeof(float), st, a);
+    hipLaunchKernelGGL(k_route_small, dim3(rows), dim3(RS_THREADS), rs_lds(a.n, a.d), st, a);
     hipLaunchKernelGGL(k_topk_small, dim3(1), dim3(RS_THREADS), (size_t)std::max(a.n, 2) * a.E * sizeof(float), st, a,
                        o);
 }

@@ -327,7 +327,13 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
                      L->ids, L->probs, L->shscale, L->logits};
     const jx::DispatchOut dout{L->counts, L->offs,   L->act,   L->n_act, L->pair_tok,
                                L->pos_of,  L->tiles, L->n_tiles, L->slots};
-    if (jx::route_small_fits(n, d, E)) {
+    // few-token decode: logits on one block per router row, grouping in the GEMVs
+    const bool small_logits = !mfma && !smfma && n <= jx::ROUTE_SMALL_MAX_N && E <= jx::SMALL_GROUP_MAX_E &&
+                              jx::route_small_fits(n, d, E);
+    if (small_logits) {
+        Launch l(L, "route", st);
+        jx::launch_route_logits(ra, st);
+    } else if (jx::route_small_fits(n, d, E)) {
         {
             Launch l(L, "route_dispatch", st);
             jx::launch_route_small(ra, dout, st);
@@ -363,6 +369,17 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         Launch l(L, "gateup_mfma", st);
         jx::launch_mfma_gateup(L->gate.m, L->up.m, L->xh.a, grp, tiles_ub, L->down_f32 ? jx::ActH{} : L->hh.a,
                                L->down_f32 ? L->hf : nullptr, st);
+    } else if (small_logits) {
+        jx::Groups lg = grp;
+        lg.logits = L->logits;
+        lg.n_experts = E;
+        jx::SmallTail tail;
+        tail.a = ra;
+        tail.o = dout;
+        tail.on = 1;
+        Launch l(L, "gateup_gemv", st);
+        jx::launch_gemv_gateup(L->gate.m, L->up.m, L->xq, lg, slots, tb, L->hq, L->down_f32 ? L->hf : nullptr, st,
+                               &tail);
     } else {
         Launch l(L, "gateup_gemv", st);
         jx::launch_gemv_gateup(L->gate.m, L->up.m, L->xq, grp, slots, tb, L->hq, L->down_f32 ? L->hf : nullptr, st);

@@ -110,7 +110,9 @@ def test_layer_vs_golden(moe, case):
 @pytest.mark.parametrize("name,n,regime", [("toy", 1, "mfma"), ("toy", 40, "gemv"), ("toy", 300, "mfma"),
                                            ("qwen15moe", 64, "mfma"), ("qwen15moe", 100, "gemv"),
                                            ("dsv2lite", 32, "mfma"), ("dsv2lite", 7, "gemv"),
-                                           ("qwen3moe", 200, "gemv"), ("qwen3moe", 96, "mfma")])
+                                           ("qwen3moe", 200, "gemv"), ("qwen3moe", 96, "mfma"),
+                                           ("toy", 2, "gemv"), ("qwen15moe", 2, "gemv"), ("mixtral", 2, "gemv"),
+                                           ("dsv2lite", 2, "gemv"), ("qwen15moe", 1, "gemv")])
 def test_layer_regimes_vs_oracle(moe, port, name, n, regime):
     say(f"{name} n={n} regime={regime}")
     cfg, lw = layer(name)
@@ -174,6 +176,24 @@ def test_edge_cases(moe, port):
         assert np.array_equal(c, [70, 70])
         assert rel_err(o, want2) <= REL_TOL
     L2.close()
+
+
+@pytest.mark.parametrize("name", ["toy", "qwen15moe", "mixtral"])
+def test_decode_two_tokens_same_experts(moe, port, name):
+    """Two identical tokens: every active expert holds a group of two pairs on the few-token path."""
+    say(f"{name} n=2 identical tokens")
+    cfg, lw = layer(name)
+    x1 = synth.make_tokens(cfg, 1, seed=13)
+    x = np.repeat(x1, 2, axis=0)
+    L = moe.MoELayer.from_weights(lw)
+    out, ids, w, counts = L.forward(x, regime="gemv")
+    lg_o, ids_o, w_o = port.route(lw, x)
+    assert np.array_equal(ids, ids_o)
+    assert np.array_equal(counts[counts > 0], np.full(cfg.top_k, 2))
+    want = port.moe_forward(lw, x)[0]
+    assert rel_err(out, want) <= REL_TOL
+    assert np.array_equal(out[0], out[1])
+    L.close()
 
 
 def test_graph_replays_match_eager(moe, monkeypatch):
