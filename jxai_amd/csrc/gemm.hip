@@ -2,36 +2,37 @@
 //
 // The reference's dots (vec_dot_{q4_0,q8_0,q4_K}_q8_0, src/quant.cpp:3307-3573)
 // sum each 32-element block exactly and scale it by (weight scale x
-// activation scale).  On int8 MFMA that costs a convert, a multiply and an
-// fma per output per 32-K block on the VALU, which on gfx950 barely overlaps
-// the matrix core.  This kernel moves the scaling into the fp16 matrix core
-// with operands that fp16 holds exactly:
+// activation scale).  Scaling every 32-K block on the VALU would cost more
+// than the matrix core's own work, so the scales ride in fp16 MFMA operands
+// that fp16 holds exactly:
 //   A (weights)      Q4_K: sc_j * q  (0..945)   Q4_0: q - 8   Q8_0: q
 //   B (activations)  dx * q * 2^-E of the Q8_0 activations as an exact fp16
 //                    hi/lo pair (an 11-bit scale times |q| <= 127 has <= 18
-//                    significant bits; hi + lo carry 22), with one power of
-//                    two 2^E per 128-element half-unit keeping it in range
-// Every product is exact in fp32, so each block's sum equals the
-// reference's integer block sum times (sc_j and) dx up to fp32 rounding of
-// the accumulation.  What is left on the VALU:
-//   Q4_K      acc += (d 2^E) * D  once per half-unit (D accumulates its 4
-//             sub-blocks inside the MFMA), and the min term
-//             -dmin * sum_j m_j * (dx_j * sum q_j) as three bf16 MFMAs on
-//             exact 3-piece splits (bf16 keeps fp32's range) accumulating
-//             straight into acc once per super-block;
-//   Q4_0/Q8_0 acc += (d_b 2^E) * D_b  per 32-block.
-// Only the fp32 summation order differs from the reference.
+//                    significant bits; hi + lo carry 22): two MFMAs per product
+// Every product is exact in fp32, so each block's sum equals the reference's
+// integer block sum times (sc_j and) dx up to fp32 rounding of the
+// accumulation.  (The exactness matters: h = SiLU(g) * u is re-quantized to
+// Q8_0 before the down projection, and a relative error of 2^-11 in g and u
+// moves ~1.4% of h's quants by one step, ~2.6e-3 relative in the layer output.)
+// What is left on the VALU:
+//   Q4_K, gate/up (one E per token)  acc += d * S once per 256-K super-block
+//   Q4_K, down    (one E per 128 K)  acc += (d 2^E) * S once per half-unit
+//   Q4_0/Q8_0                         acc += (d_b [2^E]) * D_b per 32-block
+// (S, D: MFMA sums started from zero at each scale period), plus the Q4_K min
+// term -dmin * sum_j m_j * (dx_j * sum q_j) as three bf16 MFMAs on exact
+// 3-piece splits once per super-block, straight into acc.  Only the fp32
+// summation order differs from the reference.
 //
-// Work split: a workgroup (8 waves) owns one tile of MFMA_BN = 128 (token,
-// expert) pairs of one expert and a group of weight rows; each wave owns 32
-// rows (one MFMA M-edge) x 128 pairs (4 MFMA N-edges).  Gate/up: waves 0-3
-// take 128 gate rows, waves 4-7 the same 128 up rows; SwiGLU and the Q8_0
-// quantization of h for the down projection run in the epilogue.  Down: 8
-// waves x 32 rows.  Activations are staged per 128-K half-unit into LDS with
-// direct global->LDS loads (double-buffered; 16-byte chunks XOR-swizzled by
-// row so the B-operand reads are bank-conflict free, and every lane's read
-// offsets are precomputed).  Each wave streams its own weight rows from HBM
-// into registers one half-unit ahead and converts them in registers.
+// Work split: a workgroup owns one tile of MFMA_BN = 128 (token, expert) pairs
+// of one expert and a group of weight rows -- gate/up: 128 gate rows and the
+// same 128 up rows (one half-unit of the down projection's K, so h's exponent
+// and Q8_0 blocks are settled inside the workgroup); down: 256 rows.  A wave
+// owns TM row tiles x TN pair tiles of 32 (MFMA 32x32 edges): every B operand
+// read from LDS feeds TM MFMAs and every A operand converted in registers
+// feeds TN.  Activations are staged per 128-K half-unit into LDS with direct
+// global->LDS loads (double-buffered; 16-byte chunks XOR-swizzled by pair so
+// the B reads are bank-conflict free).  Each wave streams its own weight rows
+// from HBM into registers one half-unit ahead and converts them there.
 // Workgroups are numbered XCD-major so the ~32 resident on one XCD share a
 // pair tile, whose activations then stay in that XCD's L2.
 //
@@ -51,31 +52,19 @@ typedef __bf16 b8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int GW = 8;                 // waves per workgroup (two per SIMD)
-constexpr int GT = GW * 64;
-constexpr int NT = MFMA_BN / 32;      // MFMA N-edges per wave
 constexpr int HB = 4;                 // 32-blocks per staged half-unit
-constexpr int HROW = 2 * HB * 32 * 2; // staged bytes per activation row per half-unit (hi + lo)
-constexpr int TILE_B = 32 * HROW;     // LDS bytes of one 32-pair MFMA N-edge
+constexpr int HROW = 2 * HB * 32 * 2; // staged bytes per pair per half-unit (hi + lo)
 
-template <bool MIN>
 struct Stage {
-    uint8_t q[MFMA_BN * HROW];                // row r, 16-byte chunk c at chunk (c ^ (r & 31))
-    float pe[MFMA_BN];                        // 2^E of each row's half-unit
-    uint16_t xm[MIN ? 3 * MFMA_BN * 8 : 8];   // [piece][row][8 blocks] bf16 of dx * sum(q)
+    uint8_t q[MFMA_BN * HROW];            // pair r, 16-byte chunk c at chunk (c ^ (r & 31))
+    float pe[MFMA_BN];                    // 2^E of each pair's half-unit
+    uint16_t xm[3 * MFMA_BN * 8];         // Q4_K: [piece][pair][8 sub-blocks] bf16 of dx * sum(q)
 };
 
-template <int TYPE>
 struct GemmSmem {
-    static constexpr bool MIN = TYPE == T_Q4_K;
-    Stage<MIN> st[2];
-    int src[MFMA_BN];                 // activation row (token or pair) of each staged row
-    float wsc[GW][MIN ? 32 : HB * 32];  // per-wave weight scales: Q4_K d per row, else [block][row]
+    Stage st[2];
+    int src[MFMA_BN];  // activation row (token or pair) of each staged pair
 };
-
-static_assert(sizeof(GemmSmem<T_Q4_K>) <= 160 * 1024 && sizeof(GemmSmem<T_Q4_0>) <= 160 * 1024, "LDS budget");
-// the gate/up epilogue reuses the stage buffers for the up accumulators and the block scales of h
-static_assert(sizeof(Stage<false>) * 2 >= (4 * NT * 16 * 64 + 4 * MFMA_BN) * sizeof(float), "exchange buffer");
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
@@ -139,46 +128,6 @@ __device__ __forceinline__ void split2h(float v, uint16_t& h, uint16_t& l) {
     l = __builtin_bit_cast(uint16_t, b);
 }
 
-// ---------------------------------------------------------------- weights
-// Raw weight bytes of one half-unit for lane (n, g) of row tile rt.
-template <int TYPE>
-struct WRaw;
-
-template <>
-struct WRaw<T_Q4_K> {
-    uint4 q[2];   // pairs 2s, 2s+1 of super-block h/2 (s = h&1), half g: elements 16g..16g+15
-                  // of sub-blocks 2p (low nibbles) and 2p+1 (high nibbles)
-    uint4 hd;     // header of row n (d | dmin << 16, scales[12]); loaded with the even half
-    __device__ void load(const QMat& W, int e, int rt, int h, int n, int g, int lane, int nb) {
-        (void)lane;
-        (void)nb;
-        const size_t t = (size_t)rt * W.nkb + (h >> 1);
-        const uint8_t* qb = W.qs + e * W.qs_es;
-        const int p0 = 2 * (h & 1);
-#pragma unroll
-        for (int p = 0; p < 2; ++p) q[p] = ld16(qb + (((t * 4 + p0 + p) * 2 + g) * 32 + n) * 16);
-        if (!(h & 1)) hd = ld16(W.sc + e * W.sc_es + (t * 32 + n) * 16);
-    }
-};
-
-template <int TYPE>
-struct WRaw {  // Q4_0 / Q8_0: 16 bytes per 32-block, block scales of the half-unit
-    uint4 q[HB];
-    uint32_t sc;  // fp16 scales of block (lane/16), rows 2*(lane%16) and +1
-    __device__ void load(const QMat& W, int e, int rt, int h, int n, int g, int lane, int nb) {
-        const uint8_t* qb = W.qs + e * W.qs_es;
-#pragma unroll
-        for (int j = 0; j < HB; ++j) {
-            if (j < nb) {
-                const size_t b = (size_t)rt * W.nkb + h * HB + j;
-                q[j] = TYPE == T_Q4_0 ? ld16(qb + (b * 32 + n) * 16) : ld16(qb + ((b * 2 + g) * 32 + n) * 16);
-            }
-        }
-        if ((lane >> 4) < nb)
-            sc = *reinterpret_cast<const uint32_t*>(W.sc + e * W.sc_es + (((size_t)rt * W.nkb + h * HB) * 32 + 2 * lane) * 2);
-    }
-};
-
 // (scale, min) j of a Q4_K header in registers (get_scale_min_k4,
 // src/quant.cpp:1107-1115).
 __device__ __forceinline__ void hdr_scale_min(const uint4& hd, int j, int& sc, int& mn) {
@@ -220,71 +169,94 @@ __device__ __forceinline__ void work_item(int L, int n_items, int R, int& ti, in
     rg = i - ti * R;
 }
 
-// Q8_0 of one 32-row block of h per pair, held as 16 registers in each lane
-// half (quantize_row_q8_0, src/quant.cpp:1029-1045).  Returns the stored
-// (fp16-truncated, widened) scale; q[] gets the quants.
-__device__ __forceinline__ float q8_block16(const float h[16], int q[16], int& qsum) {
-    float amax = 0.0f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) amax = fmaxf(amax, __builtin_fabsf(h[r]));
-    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-    const float dd = amax / 127.0f;
-    const float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
-    int s = 0;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        float v = round_away(h[r] * id);
-        v = fminf(fmaxf(v, -127.0f), 127.0f);
-        q[r] = (int)v;
-        s += q[r];
-    }
-    qsum = s + __shfl_xor(s, 32, 64);
-    return f16_to_f32(f32_to_f16_trunc(dd));
-}
 
 // Exponent of a half-unit from its largest block scale M: |dx * q| * 2^-E < 2^15.
 __device__ __forceinline__ int half_exp(float M) {
     return (M > 0.0f) ? (int)((__float_as_uint(M) >> 23) & 0xFF) - 127 - 7 : 0;
 }
 
-// Writes one pair's Q8_0 block of h (32 rows = K-block `blk` of the down
-// projection) in the matrix-core activation format with half-unit exponent E;
-// lane half g holds rows 8*(r/4) + 4g + r%4.
-__device__ __forceinline__ void store_hq(const ActH& o, size_t p, int blk, int g, const int q[16], float dd, int qsum,
-                                         int E) {
-    uint16_t* row = o.hl + p * (size_t)o.KH * 256 + (blk / HB) * 256 + (blk % HB) * 32 + 4 * g;
-    const float sc = dd * __uint_as_float((uint32_t)(127 - E) << 23);  // exact: power-of-two scaling
-#pragma unroll
-    for (int ii = 0; ii < 4; ++ii) {
-        uint16_t h[4], l[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) split2h(sc * (float)q[4 * ii + c], h[c], l[c]);
-        *reinterpret_cast<uint2*>(row + 8 * ii) =
-            make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
-        *reinterpret_cast<uint2*>(row + 128 + 8 * ii) =
-            make_uint2((uint32_t)l[0] | ((uint32_t)l[1] << 16), (uint32_t)l[2] | ((uint32_t)l[3] << 16));
+// ---------------------------------------------------------------- weights
+// Raw weight bytes of one half-unit for lane (n, g) of one row tile: the lane
+// reads row n.  off() is the lane's byte offset of its row in the tile layout
+// (jxmoe_kernels.h), at() the half-unit's offset, the same for every lane.
+template <int TYPE>
+struct WRaw;
+
+template <>
+struct WRaw<T_Q4_K> {
+    uint4 q[2];   // sub-block pairs 2s, 2s+1 of super-block h/2 (s = h&1), half g: elements
+                  // 16g..16g+15 of sub-blocks 2p (low nibbles) and 2p+1 (high nibbles)
+    uint4 hd;     // header of row n (d | dmin << 16, scales[12]); loaded with the even half
+    __device__ static uint32_t qoff(const QMat& W, int rt, int n, int g) {
+        return (uint32_t)((((size_t)rt * W.nkb * 8 + g) * 32 + n) * 16);
     }
-    if (g == 0) {
-        uint16_t h, m, l;
-        split3(dd * (float)qsum, h, m, l);  // exact product: 11-bit scale x |sum| < 2^12
-        uint16_t* xm = o.xm + p * (size_t)o.KU * 24 + (blk / 8) * 24 + (blk % 8);
-        xm[0] = h;
-        xm[8] = m;
-        xm[16] = l;
-        if (blk % HB == 0) o.pe[p * (size_t)o.KH + blk / HB] = __uint_as_float((uint32_t)(127 + E) << 23);
+    __device__ static uint32_t soff(const QMat& W, int rt, int n) {
+        return (uint32_t)(((size_t)rt * W.nkb * 32 + n) * 16);
     }
-}
+    __device__ void load(const uint8_t* qb, const uint8_t* sb, uint32_t qo, uint32_t so, int h, int nb) {
+        (void)nb;
+        const uint8_t* qh = qb + (size_t)(h >> 1) * 4096 + (h & 1) * 2048;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) q[p] = ld16(qh + p * 1024 + qo);
+        if (!(h & 1)) hd = ld16(sb + (size_t)(h >> 1) * 512 + so);
+    }
+};
+
+template <int TYPE>
+struct WRaw {  // Q4_0 / Q8_0: 16 bytes per 32-block, and row n's fp16 block scales
+    uint4 q[HB];
+    uint32_t d[HB];
+    __device__ static uint32_t qoff(const QMat& W, int rt, int n, int g) {
+        return TYPE == T_Q4_0 ? (uint32_t)(((size_t)rt * W.nkb * 32 + n) * 16)
+                              : (uint32_t)((((size_t)rt * W.nkb * 2 + g) * 32 + n) * 16);
+    }
+    __device__ static uint32_t soff(const QMat& W, int rt, int n) {
+        return (uint32_t)(((size_t)rt * W.nkb * 32 + n) * 2);
+    }
+    __device__ void load(const uint8_t* qb, const uint8_t* sb, uint32_t qo, uint32_t so, int h, int nb) {
+        constexpr int QB = TYPE == T_Q4_0 ? 512 : 1024;  // bytes per 32-block of a row tile
+#pragma unroll
+        for (int j = 0; j < HB; ++j) {
+            if (j < nb) {
+                q[j] = ld16(qb + (size_t)(h * HB + j) * QB + qo);
+                d[j] = *reinterpret_cast<const uint16_t*>(sb + (size_t)(h * HB + j) * 64 + so);
+            }
+        }
+    }
+};
 
 template <bool V>
 struct Parity {
     static constexpr bool value = V;
 };
 
-template <int TYPE, bool GATEUP>
-__global__ void __launch_bounds__(GT)
-k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActH hq, float* hf, int hf_ld, float* y) {
-    constexpr bool MIN = TYPE == T_Q4_K;
-    __shared__ GemmSmem<TYPE> sm;
+constexpr int TNW = MFMA_BN / 32;  // pair tiles per wave: every wave covers the workgroup's 128 pairs
+
+// Row tiles per workgroup and matrix.  Gate/up: wave w takes row tile w of
+// the gate matrix and the same tile of the up matrix (TM = 2: tile 0 gate,
+// tile 1 up), so SwiGLU needs no exchange; GW tiles = HPW h half-units, so h's
+// exponent and Q8_0 blocks are settled inside the workgroup.  Down: GW * TM.
+template <bool GATEUP, int GW, int TM>
+struct Arr {
+    static constexpr int WROWS = GATEUP ? GW : GW * TM;
+    static constexpr int HPW = GATEUP ? WROWS / HB : 0;
+    static_assert(!GATEUP || (TM == 2 && HPW * HB == WROWS), "gate/up: gate + up tile per wave, whole h half-units");
+};
+
+// The MFMAs take the activations as operand A and the weights as operand B,
+// so in each 32x32 result lane (n, g) holds weight row n (its scales are the
+// lane's own) and registers r span pairs 8*(r/4) + 4g + r%4.
+template <int TYPE, bool GATEUP, int GW, int TM>
+__global__ void __launch_bounds__(GW * 64) __attribute__((amdgpu_waves_per_eu(GW / 4, GW / 4)))
+k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, float* hf, int hf_ld, float* y) {
+    constexpr int NTH = GW * 64;
+    constexpr bool Q4K = TYPE == T_Q4_K;
+    // Q4_K: no per-period sums; acc is kept in units of the current
+    // super-block's d (per weight row) and rescaled by d_prev / d_cur at each
+    // super-block (fp32 rounding ~2^-24 per step)
+    constexpr bool RESCALE = Q4K;
+    constexpr int PER = 64 / GW;    // 1 KB staging loads per wave and half-unit
+    __shared__ GemmSmem sm;
     int ti, rg;
     work_item(blockIdx.x, n_items, R, ti, rg);
     int e, p0, cnt;
@@ -292,291 +264,393 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActH hq, floa
 
     const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, g = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int mat = GATEUP ? (wave >> 2) : 0;
-    const int rt = GATEUP ? rg * 4 + (wave & 3) : rg * GW + wave;
-    const QMat& W = (GATEUP && mat) ? W1 : W0;
-    const bool active = rt < W.nrt;  // wave-uniform; inactive waves still stage and sync
+    // the wave's row tiles: gate/up tile rt0 of both matrices, or down tiles rt0 .. rt0 + TM - 1
+    const int rt0 = GATEUP ? rg * GW + wave : rg * GW * TM + wave * TM;
+    const bool active = rt0 < W0.nrt;  // wave-uniform; inactive waves still stage and sync
 
-    if (tid < MFMA_BN) {  // activation row of each staged row: token (gate/up) or pair (down)
+    if (tid < MFMA_BN) {  // activation row of each staged pair: token (gate/up) or pair (down)
         const int p = p0 + min(tid, cnt - 1);
         sm.src[tid] = (GATEUP && !grp.identity) ? grp.pair_tok[p] : p;
     }
     __syncthreads();
-    const int xrow = sm.src[64 * (wave & 1) + lane];
-
-    // LDS byte offsets of this lane's B-operand chunks: (hi/lo, block j, K-half m)
-    int boff[2 * HB * 2];
-#pragma unroll
-    for (int hl = 0; hl < 2; ++hl)
-#pragma unroll
-        for (int j = 0; j < HB; ++j)
-#pragma unroll
-            for (int m = 0; m < 2; ++m)
-                boff[(hl * HB + j) * 2 + m] = n * HROW + (((16 * hl + 4 * j + 2 * g + m) ^ n) << 4);
 
     const int H = in.KH;
-    const size_t ldq = (size_t)H * 256;
     const int KB = in.K / 32;
-
-    auto stage = [&](int h) {
-        Stage<MIN>& S = sm.st[h & 1];
+    // Staging: a DMA instruction moves 2 pairs x 512 bytes; lane l takes chunk l % 32 of pair
+    // 2 * slot + l / 32, stored at chunk (c ^ (pair % 32)), so the B reads of 16 lanes hit 16
+    // distinct 16-byte bank groups.  The half-unit adds h * 512, a uniform term.
+    uint32_t soff[PER];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int r = 2 * (wave * 8 + k) + g;
-            const int c = n ^ (r & 31);
-            dma16(in.hl + (size_t)sm.src[r] * ldq + h * 256 + c * 8, S.q + (wave * 8 + k) * 1024);
+    for (int k = 0; k < PER; ++k) {
+        const int r = 2 * (wave * PER + k) + g;
+        soff[k] = (uint32_t)sm.src[r] * (uint32_t)(H * 512) + (uint32_t)((n ^ (r & 31)) << 4);
+    }
+    const int sj = wave & 1;  // pe / xm: lane l of waves 0, 1 takes pair 64 * sj + l
+    const int srow = sm.src[64 * sj + lane];
+    const uint32_t peoff = (uint32_t)srow * (uint32_t)(H * 4);
+    const uint32_t xoff = Q4K ? (uint32_t)srow * (uint32_t)(in.KU * 48) : 0u;
+    auto stage = [&](int h) {
+        Stage& S = sm.st[h & 1];
+        const uint8_t* base = reinterpret_cast<const uint8_t*>(in.hl) + (size_t)h * 512;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) dma16(base + soff[k], S.q + (wave * PER + k) * 1024);
+        if constexpr (Q4K) {
+            if (h & 1) {  // min-term values of the super-block: piece pc of the lane's pair
+                const uint8_t* xb = reinterpret_cast<const uint8_t*>(in.xm) + (size_t)(h >> 1) * 48;
+                if (wave < 2)
+                    for (int pc = 0; pc < 3; ++pc) dma16(xb + xoff + pc * 16, S.xm + pc * (MFMA_BN * 8) + 64 * sj * 8);
+            }
         }
-        if constexpr (MIN) {
-            if ((h & 1) && wave < 6)
-                dma16(in.xm + (size_t)xrow * in.KU * 24 + (h >> 1) * 24 + (wave >> 1) * 8,
-                      S.xm + (wave >> 1) * (MFMA_BN * 8) + 64 * (wave & 1) * 8);
-        }
-        if (wave >= 6) dma4(in.pe + (size_t)xrow * H + h, S.pe + 64 * (wave & 1));
+        if (wave < 2) dma4(reinterpret_cast<const uint8_t*>(in.pe) + (size_t)h * 4 + peoff, S.pe + 64 * sj);
     };
 
-    v16f acc[NT];
+    // weights: uniform bases, per-lane offsets of the wave's row tiles (tiles past the matrix load
+    // a valid one; their results are dropped)
+    const uint8_t* qbase[TM];
+    const uint8_t* sbase[TM];
+    uint32_t qo[TM], so[TM];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = v16f{};
+    for (int i = 0; i < TM; ++i) {
+        const QMat& W = (GATEUP && i == 1) ? W1 : W0;
+        qbase[i] = W.qs + (size_t)e * W.qs_es;
+        sbase[i] = W.sc + (size_t)e * W.sc_es;
+        const int rt = min(GATEUP ? rt0 : rt0 + i, W.nrt - 1);
+        qo[i] = WRaw<TYPE>::qoff(W, rt, n, g);
+        so[i] = WRaw<TYPE>::soff(W, rt, n);
+    }
 
-    WRaw<TYPE> cur, nxt;
-    uint4 hdr = make_uint4(0, 0, 0, 0);  // Q4_K header of the current super-block
-    if (active) cur.load(W, e, rt, 0, n, g, lane, min(HB, KB));
+    v16f acc[TM][TNW];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int t = 0; t < TNW; ++t) acc[i][t] = v16f{};
+    v16f sb[TM][TNW];  // MFMA sums of the current scale period
+
+    WRaw<TYPE> wa[TM], wb[TM];
+    uint4 hdr[TM];  // Q4_K headers of the current super-block
+    float dl[TM];   // Q4_K d of the lane's row (RESCALE: the unit acc is kept in)
+    float iu[TM];   // RESCALE: 1 / unit
+    bool dz[TM];    // RESCALE: this super-block's d is zero (its sc * q terms vanish)
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        hdr[i] = make_uint4(0, 0, 0, 0);
+        dl[i] = RESCALE ? 1.0f : 0.0f;
+        iu[i] = 1.0f;
+        dz[i] = false;
+    }
+    if (active)
+#pragma unroll
+        for (int i = 0; i < TM; ++i) wa[i].load(qbase[i], sbase[i], qo[i], so[i], 0, min(HB, KB));
     stage(0);
 
-    auto half = [&](int h, auto parity) {
+    // LDS byte offset of this lane's A chunk (hi/lo hl, sub-block j of the half-unit, K-half m) in pair tile 0
+    auto boff = [&](int hl, int j, int m) { return n * HROW + (((16 * hl + 4 * j + 2 * g + m) ^ n) << 4); };
+
+    auto half = [&](int h, auto parity, WRaw<TYPE>(&cur)[TM], WRaw<TYPE>(&nxt)[TM]) {
         constexpr bool ODD = decltype(parity)::value;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (h + 1 < H) {
             stage(h + 1);
-            if (active) nxt.load(W, e, rt, h + 1, n, g, lane, min(HB, KB - (h + 1) * HB));
-        }
-        if (active) {
-            const uint8_t* sq = sm.st[ODD].q;
-            const float* pe = sm.st[ODD].pe;
-            float* wsc = sm.wsc[wave];
-            // B operands, one (block j, K-half m, hi/lo) group of 4 N-edges ahead of its MFMAs
-            h8 bq[2][NT];
-            auto loadB = [&](int G, int buf) {
-                const int j = G >> 2, m = (G >> 1) & 1, hl = G & 1;
+            if (active)
 #pragma unroll
-                for (int t = 0; t < NT; ++t)
-                    bq[buf][t] = *reinterpret_cast<const h8*>(sq + boff[(hl * HB + j) * 2 + m] + t * TILE_B);
-            };
-            if constexpr (TYPE == T_Q4_K) {
-                if (!ODD) {
-                    hdr = cur.hd;
-                    if (g == 0) wsc[n] = f16_to_f32(hdr.x & 0xFFFFu);
-                } else {
-                    // min term, once per super-block: acc += sum_j (-dmin m_j) (dx_j sum q_j) on
-                    // bf16 3-piece splits; six of the nine piece products (all above 2^-24
-                    // relative) in three MFMAs, (MFMA, lane half) -> (A piece, B piece):
-                    // (0,0) h.h (0,1) h.m (1,0) m.h (1,1) h.l (2,0) l.h (2,1) m.m
-                    const float dmin = f16_to_f32(hdr.x >> 16);
-                    b8 am[3];
+                for (int i = 0; i < TM; ++i)
+                    nxt[i].load(qbase[i], sbase[i], qo[i], so[i], h + 1, min(HB, KB - (h + 1) * HB));
+        }
+        if (!active) return;
+        const uint8_t* sa = sm.st[ODD].q;
+        if constexpr (Q4K) {
+            if (!ODD) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    hdr[i] = cur[i].hd;
+                    const float d = f16_to_f32(hdr[i].x & 0xFFFFu);
+                    if constexpr (RESCALE) {
+                        dz[i] = d == 0.0f;
+                        const float u = dz[i] ? dl[i] : d;
+                        const float r = __builtin_amdgcn_rcpf(u);  // ~1 ulp; the units only need to be consistent
+                        const float ratio = dl[i] * r;
+                        dl[i] = u;
+                        iu[i] = r;
+#pragma unroll
+                        for (int t = 0; t < TNW; ++t)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) acc[i][t][r] *= ratio;
+                    } else {
+                        (void)d;
+                    }
+                }
+            } else {
+                // min term, once per super-block: acc += sum_j (dx_j sum q_j) (-dmin m_j) on bf16
+                // 3-piece splits; six of the nine piece products (all above 2^-24 relative) in
+                // three MFMAs, (MFMA, lane half) -> (activation piece, weight piece):
+                // (0,0) h.h (0,1) m.h (1,0) h.m (1,1) l.h (2,0) h.l (2,1) m.m
+                const uint16_t* xm = sm.st[1].xm;
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    // RESCALE: in units of dl (rounded to fp32 once, then split exactly)
+                    const float dmin = f16_to_f32(hdr[i].x >> 16) * (RESCALE ? iu[i] : 1.0f);
+                    b8 wm[3];
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
                         int sc, mn;
-                        hdr_scale_min(hdr, j, sc, mn);
+                        hdr_scale_min(hdr[i], j, sc, mn);
                         uint16_t vh, vm, vl;
-                        split3(-dmin * (float)mn, vh, vm, vl);  // exact: 11-bit x 6-bit
-                        am[0][j] = __builtin_bit_cast(__bf16, vh);
-                        am[1][j] = __builtin_bit_cast(__bf16, g ? vh : vm);
-                        am[2][j] = __builtin_bit_cast(__bf16, g ? vm : vl);
-                    }
-                    const uint16_t* xm = sm.st[1].xm;
-#pragma unroll
-                    for (int t = 0; t < NT; ++t) {
-                        const int row = 32 * t + n;
-                        const b8 b0 = *reinterpret_cast<const b8*>(xm + (g ? 1 : 0) * MFMA_BN * 8 + row * 8);
-                        const b8 b1 = *reinterpret_cast<const b8*>(xm + (g ? 2 : 0) * MFMA_BN * 8 + row * 8);
-                        acc[t] = mfma16b(am[0], b0, acc[t]);
-                        acc[t] = mfma16b(am[1], b1, acc[t]);
-                        acc[t] = mfma16b(am[2], b0, acc[t]);
-                    }
-                }
-                v16f sb[NT];  // this half-unit's 4 sub-blocks, accumulated by the MFMAs
-                h8 A[2];
-                loadB(0, 0);
-#pragma unroll
-                for (int G = 0; G < 4 * HB; ++G) {
-                    const int j = G >> 2, m = (G >> 1) & 1, hl = G & 1;
-                    if (G + 1 < 4 * HB) loadB(G + 1, (G + 1) & 1);
-                    if ((G & 3) == 0) {
-                        int sc, mn;
-                        hdr_scale_min(hdr, 4 * ODD + j, sc, mn);
-                        const uint4 raw = cur.q[j >> 1];
-                        const bool hi = j & 1;
-                        const h2v c1 = splat(hi ? (float)sc * 0.0625f : (float)sc);
-                        const h2v c0 = splat(hi ? -64.0f * (float)sc : -1024.0f * (float)sc);
-                        const uint32_t mask = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
-                        A[0] = cvt8(raw.x, raw.y, mask, 0u, c1, c0);
-                        A[1] = cvt8(raw.z, raw.w, mask, 0u, c1, c0);
+                        split3(-dmin * (float)mn, vh, vm, vl);  // exact: 11-bit x 6-bit (RESCALE: 24-bit)
+                        wm[0][j] = __builtin_bit_cast(__bf16, vh);
+                        wm[1][j] = __builtin_bit_cast(__bf16, g ? vh : vm);
+                        wm[2][j] = __builtin_bit_cast(__bf16, g ? vm : vl);
                     }
 #pragma unroll
-                    for (int t = 0; t < NT; ++t) sb[t] = mfma16(A[m], bq[G & 1][t], G == 0 ? v16f{} : sb[t]);
-                }
-                float dr[16];
-#pragma unroll
-                for (int ii = 0; ii < 4; ++ii) {
-                    const float4 v = *reinterpret_cast<const float4*>(wsc + 8 * ii + 4 * g);
-                    dr[4 * ii] = v.x;
-                    dr[4 * ii + 1] = v.y;
-                    dr[4 * ii + 2] = v.z;
-                    dr[4 * ii + 3] = v.w;
-                }
-#pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    const float p2 = pe[32 * t + n];
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[t][r] = __builtin_fmaf(dr[r] * p2, sb[t][r], acc[t][r]);
-                }
-            } else {
-                const int nb = min(HB, KB - h * HB);
-                if ((lane >> 4) < nb)
-                    *reinterpret_cast<float2*>(wsc + 2 * lane) =
-                        make_float2(f16_to_f32(cur.sc & 0xFFFFu), f16_to_f32(cur.sc >> 16));
-                uint32_t mask, flip;
-                h2v c1, c0;
-                if (TYPE == T_Q8_0) {
-                    mask = 0xFFFFFFFFu;
-                    flip = 0x80808080u;
-                    c1 = splat(1.0f);
-                    c0 = splat(-1152.0f);
-                } else {
-                    mask = g ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
-                    flip = 0u;
-                    c1 = splat(g ? 0.0625f : 1.0f);
-                    c0 = splat(g ? -72.0f : -1032.0f);
-                }
-                h8 A[2];
-                v16f D[NT];
-                loadB(0, 0);
-#pragma unroll
-                for (int G = 0; G < 4 * HB; ++G) {
-                    const int j = G >> 2, m = (G >> 1) & 1;
-                    if (j >= nb) break;
-                    if (G + 1 < 4 * nb) loadB(G + 1, (G + 1) & 1);
-                    if ((G & 3) == 0) {
-                        const uint4 raw = cur.q[j];
-                        A[0] = cvt8(raw.x, raw.y, mask, flip, c1, c0);
-                        A[1] = cvt8(raw.z, raw.w, mask, flip, c1, c0);
-                    }
-#pragma unroll
-                    for (int t = 0; t < NT; ++t) D[t] = mfma16(A[m], bq[G & 1][t], (G & 3) == 0 ? v16f{} : D[t]);
-                    if ((G & 3) == 3) {
-                        float dr[16];
-#pragma unroll
-                        for (int ii = 0; ii < 4; ++ii) {
-                            const float4 v = *reinterpret_cast<const float4*>(wsc + j * 32 + 8 * ii + 4 * g);
-                            dr[4 * ii] = v.x;
-                            dr[4 * ii + 1] = v.y;
-                            dr[4 * ii + 2] = v.z;
-                            dr[4 * ii + 3] = v.w;
-                        }
-#pragma unroll
-                        for (int t = 0; t < NT; ++t) {
-                            const float p2 = pe[32 * t + n];
-#pragma unroll
-                            for (int r = 0; r < 16; ++r) acc[t][r] = __builtin_fmaf(dr[r] * p2, D[t][r], acc[t][r]);
-                        }
+                    for (int t = 0; t < TNW; ++t) {
+                        const int pr = 32 * t + n;
+                        const b8 x0 = *reinterpret_cast<const b8*>(xm + (g ? 1 : 0) * MFMA_BN * 8 + pr * 8);
+                        const b8 x1 = *reinterpret_cast<const b8*>(xm + (g ? 2 : 0) * MFMA_BN * 8 + pr * 8);
+                        acc[i][t] = mfma16b(x0, wm[0], acc[i][t]);
+                        acc[i][t] = mfma16b(x1, wm[1], acc[i][t]);
+                        acc[i][t] = mfma16b(x0, wm[2], acc[i][t]);
                     }
                 }
             }
+            // 8 K-steps of 16 per half-unit (sub-block jj = st / 2, K-half m = st % 2), software
+            // pipelined: while step st's 2 * TNW * TM MFMAs run, the activation operands of step st + 1
+            // are read from LDS and its weights converted (the schedule is pinned below)
+            h8 av[2][TNW][2];
+            h8 wv[2][TM];
+            h2v c1[TM], c0[TM];
+            auto read_av = [&](int st, h8(&dst)[TNW][2]) {
+#pragma unroll
+                for (int t = 0; t < TNW; ++t)
+#pragma unroll
+                    for (int hl = 0; hl < 2; ++hl)
+                        dst[t][hl] = *reinterpret_cast<const h8*>(sa + t * 16384 + boff(hl, st >> 1, st & 1));
+            };
+            auto convert = [&](int st, h8(&dst)[TM]) {
+                const int jj = st >> 1, m = st & 1;
+                if (m == 0) {
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) {
+                        int sc, mn;
+                        hdr_scale_min(hdr[i], 4 * ODD + jj, sc, mn);
+                        const _Float16 sv = (_Float16)(RESCALE && dz[i] ? 0.0f : (float)sc);  // exact
+                        const _Float16 s1 = (jj & 1) ? sv * (_Float16)0.0625f : sv;
+                        const _Float16 s0 = (jj & 1) ? sv * (_Float16)-64.0f : sv * (_Float16)-1024.0f;
+                        c1[i] = h2v{s1, s1};
+                        c0[i] = h2v{s0, s0};
+                    }
+                }
+                const uint32_t mask = (jj & 1) ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    const uint4 raw = cur[i].q[jj >> 1];
+                    dst[i] = m ? cvt8(raw.z, raw.w, mask, 0u, c1[i], c0[i]) : cvt8(raw.x, raw.y, mask, 0u, c1[i], c0[i]);
+                }
+            };
+            read_av(0, av[0]);
+            convert(0, wv[0]);
+#pragma unroll
+            for (int st = 0; st < 2 * HB; ++st) {
+                const int b = st & 1;
+
+                // the next step's LDS reads go out before this step's MFMAs (nothing crosses the
+                // scheduling barriers), so their latency hides behind 2 * TNW * TM MFMAs
+                if (st + 1 < 2 * HB) read_av(st + 1, av[b ^ 1]);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+                    for (int t = 0; t < TNW; ++t)
+#pragma unroll
+                        for (int i = 0; i < TM; ++i) acc[i][t] = mfma16(av[b][t][hl], wv[b][i], acc[i][t]);
+                if (st + 1 < 2 * HB) {
+                    convert(st + 1, wv[b ^ 1]);  // VALU work spread between the MFMAs
+#pragma unroll
+                    for (int k = 0; k < 2 * TNW * TM; ++k) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+            const int nb = min(HB, KB - h * HB);
+            uint32_t mask, flip;
+            h2v c1, c0;
+            if (TYPE == T_Q8_0) {
+                mask = 0xFFFFFFFFu;
+                flip = 0x80808080u;
+                c1 = splat(1.0f);
+                c0 = splat(-1152.0f);
+            } else {
+                mask = g ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+                flip = 0u;
+                c1 = splat(g ? 0.0625f : 1.0f);
+                c0 = splat(g ? -72.0f : -1032.0f);
+            }
+#pragma unroll
+            for (int j = 0; j < HB; ++j) {
+                if (j >= nb) break;
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    h8 wv[TM], av[TNW][2];
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) {
+                        const uint4 raw = cur[i].q[j];
+                        wv[i] = m ? cvt8(raw.z, raw.w, mask, flip, c1, c0) : cvt8(raw.x, raw.y, mask, flip, c1, c0);
+                    }
+#pragma unroll
+                    for (int t = 0; t < TNW; ++t)
+#pragma unroll
+                        for (int hl = 0; hl < 2; ++hl)
+                            av[t][hl] = *reinterpret_cast<const h8*>(sa + t * 16384 + boff(hl, j, m));
+#pragma unroll
+                    for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+                        for (int t = 0; t < TNW; ++t)
+#pragma unroll
+                            for (int i = 0; i < TM; ++i)
+                                sb[i][t] = mfma16(av[t][hl], wv[i], (m == 0 && hl == 0) ? v16f{} : sb[i][t]);
+                }
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {  // fold: acc += d_b * D_b
+                    const float db = f16_to_f32(cur[i].d[j]);
+#pragma unroll
+                    for (int t = 0; t < TNW; ++t)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[i][t][r] = __builtin_fmaf(db, sb[i][t][r], acc[i][t][r]);
+                }
+            }
         }
-        cur = nxt;
     };
 
     for (int h = 0; h < H; h += 2) {
-        half(h, Parity<false>{});
-        if (h + 1 < H) half(h + 1, Parity<true>{});
+        half(h, Parity<false>{}, wa, wb);
+        if (h + 1 < H) half(h + 1, Parity<true>{}, wb, wa);
     }
 
     // ------------------------------------------------------------ epilogue
+    if (active) {  // back to natural units: the row's unit (RESCALE) and the token's exponent
+        const float* pe = sm.st[(H - 1) & 1].pe;
+#pragma unroll
+        for (int t = 0; t < TNW; ++t)
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+                const float4 v = *reinterpret_cast<const float4*>(pe + 32 * t + 8 * ii + 4 * g);
+                const float pv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) acc[i][t][4 * ii + c] *= RESCALE ? pv[c] * dl[i] : pv[c];
+            }
+    }
     if constexpr (GATEUP) {
+        // h = SiLU(g) * u in registers, written transposed to LDS: [pair][row of the workgroup]
+        constexpr int HLD = GW * 32 + 4;                  // h row stride (floats)
+        float* hs = reinterpret_cast<float*>(&sm.st[0]);  // [128 pairs][HLD], over both stage buffers
+        static_assert((size_t)MFMA_BN * HLD * 4 <= 2 * sizeof(Stage), "epilogue buffer");
         __syncthreads();  // every wave is done with the stage buffers
-        float* ex = reinterpret_cast<float*>(&sm.st[0]);
-        float* dsh = ex + 4 * NT * 16 * 64;  // [4 row tiles][128 pairs] block scales of h
-        if (mat == 1) {
+        if (active) {
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) ex[((((wave & 3) * NT + t) * 16) + r) * 64 + lane] = acc[t][r];
-        }
-        __syncthreads();
-        const bool work = mat == 0 && active;
-        if (work) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
+            for (int t = 0; t < TNW; ++t)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const float gv = acc[t][r];
-                    const float uv = ex[((((wave & 3) * NT + t) * 16) + r) * 64 + lane];
-                    acc[t][r] = (gv / (1.0f + expf(-gv))) * uv;  // SwiGLU, h in place
+                    const float gv = acc[0][t][r], uv = acc[1][t][r];
+                    const int pr = 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
+                    hs[pr * HLD + wave * 32 + n] = (gv / (1.0f + expf(-gv))) * uv;  // SwiGLU
                 }
-                const int pr = 32 * t + n;
-                const size_t p = (size_t)(p0 + pr);
-                if (hf && pr < cnt) {
-                    float* fd = hf + p * (size_t)hf_ld + rt * 32 + 4 * g;
-#pragma unroll
-                    for (int ii = 0; ii < 4; ++ii)
-                        *reinterpret_cast<float4*>(fd + 8 * ii) =
-                            make_float4(acc[t][4 * ii], acc[t][4 * ii + 1], acc[t][4 * ii + 2], acc[t][4 * ii + 3]);
-                }
-                if (hq.hl) {
-                    int q[16], qsum;
-                    float hv[16];
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) hv[r] = acc[t][r];
-                    const float dd = q8_block16(hv, q, qsum);
-                    if (g == 0) dsh[(wave & 3) * MFMA_BN + pr] = dd;
-                }
-            }
         }
-        if (!hq.hl) return;
-        __syncthreads();  // block scales of the 4 row tiles (one half-unit of the down K) are in dsh
-        if (!work) return;
+        __syncthreads();
+        // Q8_0 of h (quantize_row_q8_0 over the down projection's K = these rows), one thread per
+        // (pair, 32-row block = gate/up row tile)
+        for (int it = tid; it < GW * MFMA_BN; it += NTH) {
+            const int pr = it % MFMA_BN, b = it / MFMA_BN;
+            const int blk = rg * GW + b;
+            if (pr >= cnt || blk >= W0.nrt) continue;
+            const size_t p = (size_t)(p0 + pr);
+            const float* hv = hs + pr * HLD + b * 32;
+            float v[32];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const int pr = 32 * t + n;
-            float M = 0.0f;
+            for (int c = 0; c < 8; ++c) {
+                const float4 f = *reinterpret_cast<const float4*>(hv + 4 * c);
+                v[4 * c] = f.x;
+                v[4 * c + 1] = f.y;
+                v[4 * c + 2] = f.z;
+                v[4 * c + 3] = f.w;
+            }
+            if (hf) {
+                float* fd = hf + p * (size_t)hf_ld + blk * 32;
 #pragma unroll
-            for (int w = 0; w < 4; ++w)
-                if (rg * 4 + w < W0.nrt) M = fmaxf(M, dsh[w * MFMA_BN + pr]);
-            int q[16], qsum;
-            float hv[16];
+                for (int c = 0; c < 8; ++c)
+                    *reinterpret_cast<float4*>(fd + 4 * c) = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
+            }
+            if (!hq.q) continue;
+            float amax = 0.0f;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) hv[r] = acc[t][r];
-            const float dd = q8_block16(hv, q, qsum);
-            if (pr < cnt) store_hq(hq, (size_t)(p0 + pr), rt, g, q, dd, qsum, half_exp(M));
+            for (int c = 0; c < 32; ++c) amax = fmaxf(amax, __builtin_fabsf(v[c]));
+            const float d = amax / 127.0f;
+            const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+            int s = 0;
+            uint32_t w[8];
+#pragma unroll
+            for (int c = 0; c < 32; ++c) {
+                float r = round_away(v[c] * id);
+                r = fminf(fmaxf(r, -127.0f), 127.0f);
+                const int q = (int)r;
+                s += q;
+                if ((c & 3) == 0) w[c >> 2] = 0;
+                w[c >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (c & 3));
+            }
+            uint4* qd = reinterpret_cast<uint4*>(hq.q + p * (size_t)hq.K + blk * 32);
+            qd[0] = make_uint4(w[0], w[1], w[2], w[3]);
+            qd[1] = make_uint4(w[4], w[5], w[6], w[7]);
+            hq.s[p * (size_t)(hq.K / 32) + blk] = make_float2(f16_to_f32(f32_to_f16_trunc(d)), (float)s);
         }
     } else {
         if (!active) return;
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const int pr = 32 * t + n;
-            if (pr >= cnt) continue;
-            float* dst = y + (size_t)(p0 + pr) * W0.rows + rt * 32 + 4 * g;
+        for (int i = 0; i < TM; ++i) {
+            const int rt = rt0 + i;
+            if (rt >= W0.nrt) continue;
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii)
-                *reinterpret_cast<float4*>(dst + 8 * ii) =
-                    make_float4(acc[t][4 * ii], acc[t][4 * ii + 1], acc[t][4 * ii + 2], acc[t][4 * ii + 3]);
+            for (int t = 0; t < TNW; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int pr = 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (pr < cnt) y[(size_t)(p0 + pr) * W0.rows + rt * 32 + n] = acc[i][t][r];
+                }
         }
     }
 }
 
+// Workgroup shape (every wave covers 128 pairs): one wave per SIMD, whose
+// 512 registers hold the accumulators, double-buffered operands and the next
+// half-unit's weights.
 template <int TYPE, bool GATEUP>
-static void launch_t(const QMat& w0, const QMat& w1, const ActH& in, const Groups& grp, int tiles_ub, const ActH& hq,
+struct Shape {
+#ifndef JX_DOWN_GW
+#define JX_DOWN_GW 4
+#endif
+#ifndef JX_DOWN_TM
+#define JX_DOWN_TM 2
+#endif
+    static constexpr int GW = GATEUP ? 4 : JX_DOWN_GW;
+    static constexpr int TM = GATEUP ? 2 : JX_DOWN_TM;
+};
+
+template <int TYPE, bool GATEUP>
+static void launch_t(const QMat& w0, const QMat& w1, const ActH& in, const Groups& grp, int tiles_ub, const ActQ8& hq,
                      float* hf, int hf_ld, float* y, hipStream_t st) {
-    const int R = GATEUP ? (w0.nrt + 3) / 4 : (w0.nrt + GW - 1) / GW;
+    constexpr int GW = Shape<TYPE, GATEUP>::GW, TM = Shape<TYPE, GATEUP>::TM;
+    constexpr int rows_per_wg = Arr<GATEUP, GW, TM>::WROWS;  // row tiles of each matrix per workgroup
+    const int R = (w0.nrt + rows_per_wg - 1) / rows_per_wg;
     const int n_items = R * tiles_ub;
     if (n_items <= 0) return;
-    hipLaunchKernelGGL((k_wgemm<TYPE, GATEUP>), dim3(n_items), dim3(GT), 0, st, w0, w1, in, grp, R, n_items, hq, hf,
-                       hf_ld, y);
+    hipLaunchKernelGGL((k_wgemm<TYPE, GATEUP, GW, TM>), dim3(n_items), dim3(GW * 64), 0, st, w0, w1, in, grp, R,
+                       n_items, hq, hf, hf_ld, y);
 }
 
 void launch_mfma_gateup(const QMat& g, const QMat& u, const ActH& xin, const Groups& grp, int tiles_ub,
-                        const ActH& hq, float* hf, hipStream_t st) {
+                        const ActQ8& hq, float* hf, hipStream_t st) {
     const int hf_ld = ((g.rows + 255) / 256) * 256;
     switch (g.type) {
         case T_Q4_0: launch_t<T_Q4_0, true>(g, u, xin, grp, tiles_ub, hq, hf, hf_ld, nullptr, st); break;
@@ -587,7 +661,7 @@ void launch_mfma_gateup(const QMat& g, const QMat& u, const ActH& xin, const Gro
 }
 
 void launch_mfma_down(const QMat& dn, const ActH& hin, const Groups& grp, int tiles_ub, float* y, hipStream_t st) {
-    const ActH none{};
+    const ActQ8 none{};
     switch (dn.type) {
         case T_Q4_0: launch_t<T_Q4_0, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st); break;
         case T_Q8_0: launch_t<T_Q8_0, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st); break;

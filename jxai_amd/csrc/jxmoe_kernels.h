@@ -44,10 +44,15 @@ struct ActQ8 {
 //   hl [rows][KH][256]   per 128-element half-unit: fp16 hi x128, then lo x128,
 //                        of dx * q * 2^-E (an exact split of the dequantized
 //                        value scaled into fp16 range)
-//   pe [rows][KH]        2^E of each half-unit (E = exponent of its largest
-//                        block scale - 7, so |dx * q| * 2^-E < 2^15)
+//   pe [rows][KH]        2^E of each half-unit.  Gate/up inputs (written by the
+//                        router kernels) use one E per row, the exponent of the
+//                        row's largest block scale - 7; the down input (h, written
+//                        by the gate/up GEMM's epilogue) one E per half-unit, the
+//                        exponent of the half-unit's largest block scale - 7.
+//                        Either way |dx * q| * 2^-E < 2^15.
 //   xm [rows][KU][3][8]  per 256-element unit: bf16 pieces (hi, mid, lo) of
-//                        dx * sum(q) for its 8 blocks (Q4_K min term, unscaled)
+//                        dx * sum(q) for its 8 blocks (Q4_K min term): times 2^-E
+//                        for per-row E, unscaled for per-half-unit E
 struct ActH {
     uint16_t* hl = nullptr;
     float* pe = nullptr;
@@ -132,9 +137,10 @@ int gemv_max_k(bool gateup, int tb, bool f32);
 void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp,
                       int slots, int tb, float* y, hipStream_t st);
 // Prefill regime: matrix-core grouped GEMMs over the dispatch tile table.
-// gate/up writes SwiGLU(h) as ActH (hq.hl != null) and/or fp32 (hf != null).
+// gate/up writes SwiGLU(h) as Q8_0 (hq.q != null; the down GEMM takes it after
+// launch_q8_to_acth) and/or fp32 (hf != null).
 void launch_mfma_gateup(const QMat& g, const QMat& u, const ActH& xin, const Groups& grp, int tiles_ub,
-                        const ActH& hq, float* hf, hipStream_t st);
+                        const ActQ8& hq, float* hf, hipStream_t st);
 void launch_mfma_down(const QMat& dn, const ActH& hin, const Groups& grp, int tiles_ub, float* y, hipStream_t st);
 
 // out[t] = sum_s p[t][s] * y[pos(t,s)] (+ shscale[t] * ysh[t]), fma in selection order.

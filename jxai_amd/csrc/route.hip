@@ -37,26 +37,51 @@ __device__ __forceinline__ int quant_block(float v, int l32, bool ok, const ActQ
 }
 
 // Matrix-core form (ActH) of one activation row from its Q8_0 quants q[K] and
-// (scale, sum) per 32-block, written by the NTH threads of one block.  Per
-// 128-element half-unit E = exponent(max block scale) - 7, so every
+// (scale, sum) per 32-block, written by the NTH threads of one block.  One
+// exponent per row: E = exponent(max block scale of the row) - 7, so every
 // dx * q * 2^-E (exact in fp32: an 11-bit scale times |q| <= 127) is below
-// 2^15 and splits exactly into fp16 hi + lo.
+// 2^15 and splits into fp16 hi + lo exactly (a block whose scale is 2^21
+// times smaller than the row's largest loses bits of lo in fp16's subnormal
+// range: at most 2^-25 absolute, 2^-40 of the row's largest value).  The Q4_K
+// min-term values dx * sum(q) are stored times 2^-E as well; pe holds 2^E
+// for every half-unit of the row.
 template <int NTH>
 __device__ void write_acth_row(const int8_t* q, const float2* sc, int K, const ActH& o, size_t row, int tid) {
-    const int KH = K / 128;
-    for (int i = tid; i < K; i += NTH) {
-        const int b = i >> 5, hh = i >> 7;
-        const float M = fmaxf(fmaxf(sc[4 * hh].x, sc[4 * hh + 1].x), fmaxf(sc[4 * hh + 2].x, sc[4 * hh + 3].x));
-        const int E = (M > 0.0f) ? (int)((__float_as_uint(M) >> 23) & 0xFF) - 127 - 7 : 0;
-        const float v = sc[b].x * (float)q[i] * __uint_as_float((uint32_t)(127 - E) << 23);
-        const _Float16 hi = (_Float16)v;
-        const _Float16 lo = (_Float16)(v - (float)hi);
+    __shared__ float wmax[NTH / 64];
+    const int KH = K / 128, KB = K / 32;
+    float M = 0.0f;
+    for (int b = tid; b < KB; b += NTH) M = fmaxf(M, sc[b].x);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    if ((tid & 63) == 0) wmax[tid >> 6] = M;
+    __syncthreads();
+    M = wmax[0];
+#pragma unroll
+    for (int w = 1; w < NTH / 64; ++w) M = fmaxf(M, wmax[w]);
+    const int E = (M > 0.0f) ? (int)((__float_as_uint(M) >> 23) & 0xFF) - 127 - 7 : 0;
+    const float dn = __uint_as_float((uint32_t)(127 - E) << 23), up = __uint_as_float((uint32_t)(127 + E) << 23);
+    // eight consecutive elements per thread: one 16-byte store each of hi and lo
+    for (int c = tid; c < K / 8; c += NTH) {
+        const int i = 8 * c, b = i >> 5, hh = i >> 7;
+        const uint2 qq = *reinterpret_cast<const uint2*>(q + i);
+        const float s = sc[b].x * dn;  // exact: power-of-two scaling
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t word = u < 2 ? qq.x : qq.y;
+            const int q0 = (int)(int8_t)(word >> (16 * (u & 1))), q1 = (int)(int8_t)(word >> (16 * (u & 1) + 8));
+            const float v0 = s * (float)q0, v1 = s * (float)q1;  // exact: 11-bit scale x |q| <= 127
+            const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
+            const _Float16 l0 = (_Float16)(v0 - (float)h0), l1 = (_Float16)(v1 - (float)h1);
+            hw[u] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+            lw[u] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+        }
         uint16_t* hl = o.hl + row * (size_t)KH * 256 + hh * 256 + (i & 127);
-        hl[0] = __builtin_bit_cast(uint16_t, hi);
-        hl[128] = __builtin_bit_cast(uint16_t, lo);
-        if ((i & 127) == 0) o.pe[row * (size_t)KH + hh] = __uint_as_float((uint32_t)(127 + E) << 23);
+        *reinterpret_cast<uint4*>(hl) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        *reinterpret_cast<uint4*>(hl + 128) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        if ((i & 127) == 0) o.pe[row * (size_t)KH + hh] = up;
         if ((i & 31) == 0) {
-            const float X = sc[b].x * sc[b].y;  // exact: 11-bit scale x |sum| < 2^12
+            const float X = sc[b].x * sc[b].y * dn;  // exact: 11-bit scale x |sum| < 2^12, times 2^-E
             const uint32_t bh = __float_as_uint(X) & 0xFFFF0000u;
             const float r1 = X - __uint_as_float(bh);
             const uint32_t bm = __float_as_uint(r1) & 0xFFFF0000u;

@@ -367,7 +367,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     const size_t fpad = ((size_t)L->F + 255) / 256 * 256;
     if (mfma) {
         Launch l(L, "gateup_mfma", st);
-        jx::launch_mfma_gateup(L->gate.m, L->up.m, L->xh.a, grp, tiles_ub, L->down_f32 ? jx::ActH{} : L->hh.a,
+        jx::launch_mfma_gateup(L->gate.m, L->up.m, L->xh.a, grp, tiles_ub, L->down_f32 ? jx::ActQ8{} : L->hq,
                                L->down_f32 ? L->hf : nullptr, st);
     } else if (small_logits) {
         jx::Groups lg = grp;
@@ -394,14 +394,16 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
             const int st_ub = (n + jx::MFMA_BN - 1) / jx::MFMA_BN;
             {
                 Launch l(L, "shared_gateup_mfma", st);
-                jx::launch_mfma_gateup(L->sgate.m, L->sup.m, L->xh.a, sg, st_ub, L->sdown_f32 ? jx::ActH{} : L->hhs.a,
+                jx::launch_mfma_gateup(L->sgate.m, L->sup.m, L->xh.a, sg, st_ub, L->sdown_f32 ? jx::ActQ8{} : L->hqs,
                                        L->sdown_f32 ? L->hfs : nullptr, st);
             }
             Launch l(L, "shared_down", st);
             if (L->sdown_f32)
                 jx::launch_gemv_down(L->sdown.m, L->hqs, L->hfs, (int)fspad, sg, 1, 4, L->ysh, st);
-            else
+            else {
+                jx::launch_q8_to_acth(L->hqs, n, L->hhs.a, st);
                 jx::launch_mfma_down(L->sdown.m, L->hhs.a, sg, st_ub, L->ysh, st);
+            }
         } else {
             {
                 Launch l(L, "shared_gateup_gemv", st);
@@ -416,8 +418,10 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     {
         Launch l(L, mfma ? (L->down_f32 ? "down_gemv_f32" : "down_mfma") : (L->down_f32 ? "down_gemv_f32" : "down_gemv"),
                  st);
-        if (mfma && !L->down_f32)
+        if (mfma && !L->down_f32) {
+            jx::launch_q8_to_acth(L->hq, nk, L->hh.a, st);
             jx::launch_mfma_down(L->down.m, L->hh.a, grp, tiles_ub, L->y, st);
+        }
         else
             jx::launch_gemv_down(L->down.m, L->hq, L->down_f32 ? L->hf : nullptr, (int)fpad, grp, slots, mfma ? 4 : tb,
                                  L->y, st);
