@@ -52,17 +52,22 @@ typedef __bf16 b8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int HB = 4;                 // 32-blocks per staged half-unit
-constexpr int HROW = 2 * HB * 32 * 2; // staged bytes per pair per half-unit (hi + lo)
+constexpr int HB = 4;  // 32-blocks per staged half-unit
 
+// One staged half-unit of MFMA_BN activation rows: HL = 2 stages fp16 hi and
+// lo (256 bytes each per row), HL = 1 hi only.
+template <int HL>
 struct Stage {
-    uint8_t q[MFMA_BN * HROW];            // pair r, 16-byte chunk c at chunk (c ^ (r & 31))
-    float pe[MFMA_BN];                    // 2^E of each pair's half-unit
-    uint16_t xm[3 * MFMA_BN * 8];         // Q4_K: [piece][pair][8 sub-blocks] bf16 of dx * sum(q)
+    static constexpr int PB = 256 * HL;   // bytes per row
+    static constexpr int CPP = PB / 16;   // 16-byte chunks per row
+    uint8_t q[MFMA_BN * PB];              // row r, chunk c at chunk (c ^ (r % CPP))
+    float pe[MFMA_BN];                    // 2^E of each row
+    uint16_t xm[3 * MFMA_BN * 8];         // Q4_K: [piece][row][8 sub-blocks] bf16 of dx * sum(q)
 };
 
+template <int HL>
 struct GemmSmem {
-    Stage st[2];
+    Stage<HL> st[2];
     int src[MFMA_BN];  // activation row (token or pair) of each staged pair
 };
 
@@ -230,24 +235,25 @@ struct Parity {
     static constexpr bool value = V;
 };
 
-constexpr int TNW = MFMA_BN / 32;  // pair tiles per wave: every wave covers the workgroup's 128 pairs
 
-// Row tiles per workgroup and matrix.  Gate/up: wave w takes row tile w of
-// the gate matrix and the same tile of the up matrix (TM = 2: tile 0 gate,
-// tile 1 up), so SwiGLU needs no exchange; GW tiles = HPW h half-units, so h's
-// exponent and Q8_0 blocks are settled inside the workgroup.  Down: GW * TM.
-template <bool GATEUP, int GW, int TM>
+// Wave arrangement: NPG pair groups of TN pair tiles (32 pairs each) side by
+// side, RW row slots.  Gate/up: row slot s takes row tile s of the gate
+// matrix and the same tile of the up matrix (TM = 2: tile 0 gate, tile 1
+// up), so SwiGLU needs no exchange.  Down: row slot s takes TM row tiles.
+template <bool GATEUP, int GW, int TM, int TN>
 struct Arr {
-    static constexpr int WROWS = GATEUP ? GW : GW * TM;
-    static constexpr int HPW = GATEUP ? WROWS / HB : 0;
-    static_assert(!GATEUP || (TM == 2 && HPW * HB == WROWS), "gate/up: gate + up tile per wave, whole h half-units");
+    static constexpr int NPG = MFMA_BN / (32 * TN);
+    static constexpr int RW = GW / NPG;
+    static constexpr int WROWS = GATEUP ? RW : RW * TM;  // row tiles of each matrix per workgroup
+    static_assert(NPG * TN * 32 == MFMA_BN && NPG * RW == GW, "wave arrangement");
+    static_assert(!GATEUP || TM == 2, "gate/up: a gate and an up tile per wave");
 };
 
 // The MFMAs take the activations as operand A and the weights as operand B,
 // so in each 32x32 result lane (n, g) holds weight row n (its scales are the
 // lane's own) and registers r span pairs 8*(r/4) + 4g + r%4.
-template <int TYPE, bool GATEUP, int GW, int TM>
-__global__ void __launch_bounds__(GW * 64) __attribute__((amdgpu_waves_per_eu(GW / 4, GW / 4)))
+template <int TYPE, bool GATEUP, int GW, int TM, int TN, int WPE>
+__global__ void __launch_bounds__(GW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, float* hf, int hf_ld, float* y) {
     constexpr int NTH = GW * 64;
     constexpr bool Q4K = TYPE == T_Q4_K;
@@ -255,8 +261,13 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
     // super-block's d (per weight row) and rescaled by d_prev / d_cur at each
     // super-block (fp32 rounding ~2^-24 per step)
     constexpr bool RESCALE = Q4K;
-    constexpr int PER = 64 / GW;    // 1 KB staging loads per wave and half-unit
-    __shared__ GemmSmem sm;
+    // gate/up: exact hi + lo activation operands (h is re-quantized after SwiGLU); down: the hi
+    // half only (relative error <= 2^-12 per activation, no re-quantization downstream)
+    constexpr int HL = GATEUP ? 2 : 1;
+    using St = Stage<HL>;
+    constexpr int PB = St::PB, CPP = St::CPP, PPI = 64 / CPP;  // row bytes, chunks, rows per DMA
+    constexpr int PER = MFMA_BN / PPI / GW;  // 1 KB staging loads per wave and half-unit
+    __shared__ GemmSmem<HL> sm;
     int ti, rg;
     work_item(blockIdx.x, n_items, R, ti, rg);
     int e, p0, cnt;
@@ -264,8 +275,11 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
 
     const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, g = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    using A_ = Arr<GATEUP, GW, TM, TN>;
+    const int pg = wave % A_::NPG, rw = wave / A_::NPG;  // pair group, row slot
+    const int pbase = pg * TN * 32;                       // first pair of the wave within the tile
     // the wave's row tiles: gate/up tile rt0 of both matrices, or down tiles rt0 .. rt0 + TM - 1
-    const int rt0 = GATEUP ? rg * GW + wave : rg * GW * TM + wave * TM;
+    const int rt0 = GATEUP ? rg * A_::RW + rw : (rg * A_::RW + rw) * TM;
     const bool active = rt0 < W0.nrt;  // wave-uniform; inactive waves still stage and sync
 
     if (tid < MFMA_BN) {  // activation row of each staged pair: token (gate/up) or pair (down)
@@ -276,21 +290,21 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
 
     const int H = in.KH;
     const int KB = in.K / 32;
-    // Staging: a DMA instruction moves 2 pairs x 512 bytes; lane l takes chunk l % 32 of pair
-    // 2 * slot + l / 32, stored at chunk (c ^ (pair % 32)), so the B reads of 16 lanes hit 16
-    // distinct 16-byte bank groups.  The half-unit adds h * 512, a uniform term.
+    // Staging: a DMA instruction moves PPI rows x PB bytes; lane l takes chunk l % CPP of row
+    // PPI * slot + l / CPP, stored at chunk ((l % CPP) ^ (row % CPP)), so the operand reads of 16
+    // lanes hit 16 distinct 16-byte bank groups.  The half-unit adds h * 512, a uniform term.
     uint32_t soff[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-        const int r = 2 * (wave * PER + k) + g;
-        soff[k] = (uint32_t)sm.src[r] * (uint32_t)(H * 512) + (uint32_t)((n ^ (r & 31)) << 4);
+        const int r = PPI * (wave * PER + k) + lane / CPP;
+        soff[k] = (uint32_t)sm.src[r] * (uint32_t)(H * 512) + (uint32_t)(((lane % CPP) ^ (r % CPP)) << 4);
     }
     const int sj = wave & 1;  // pe / xm: lane l of waves 0, 1 takes pair 64 * sj + l
     const int srow = sm.src[64 * sj + lane];
     const uint32_t peoff = (uint32_t)srow * (uint32_t)(H * 4);
     const uint32_t xoff = Q4K ? (uint32_t)srow * (uint32_t)(in.KU * 48) : 0u;
     auto stage = [&](int h) {
-        Stage& S = sm.st[h & 1];
+        St& S = sm.st[h & 1];
         const uint8_t* base = reinterpret_cast<const uint8_t*>(in.hl) + (size_t)h * 512;
 #pragma unroll
         for (int k = 0; k < PER; ++k) dma16(base + soff[k], S.q + (wave * PER + k) * 1024);
@@ -319,12 +333,12 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
         so[i] = WRaw<TYPE>::soff(W, rt, n);
     }
 
-    v16f acc[TM][TNW];
+    v16f acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int t = 0; t < TNW; ++t) acc[i][t] = v16f{};
-    v16f sb[TM][TNW];  // MFMA sums of the current scale period
+        for (int t = 0; t < TN; ++t) acc[i][t] = v16f{};
+    v16f sb[TM][TN];  // MFMA sums of the current scale period
 
     WRaw<TYPE> wa[TM], wb[TM];
     uint4 hdr[TM];  // Q4_K headers of the current super-block
@@ -344,7 +358,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
     stage(0);
 
     // LDS byte offset of this lane's A chunk (hi/lo hl, sub-block j of the half-unit, K-half m) in pair tile 0
-    auto boff = [&](int hl, int j, int m) { return n * HROW + (((16 * hl + 4 * j + 2 * g + m) ^ n) << 4); };
+    auto boff = [&](int hl, int j, int m) { return n * PB + (((16 * hl + 4 * j + 2 * g + m) ^ (n % CPP)) << 4); };
 
     auto half = [&](int h, auto parity, WRaw<TYPE>(&cur)[TM], WRaw<TYPE>(&nxt)[TM]) {
         constexpr bool ODD = decltype(parity)::value;
@@ -358,7 +372,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
                     nxt[i].load(qbase[i], sbase[i], qo[i], so[i], h + 1, min(HB, KB - (h + 1) * HB));
         }
         if (!active) return;
-        const uint8_t* sa = sm.st[ODD].q;
+        const uint8_t* sa = sm.st[ODD].q + pg * TN * 32 * PB;
         if constexpr (Q4K) {
             if (!ODD) {
 #pragma unroll
@@ -373,7 +387,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
                         dl[i] = u;
                         iu[i] = r;
 #pragma unroll
-                        for (int t = 0; t < TNW; ++t)
+                        for (int t = 0; t < TN; ++t)
 #pragma unroll
                             for (int r = 0; r < 16; ++r) acc[i][t][r] *= ratio;
                     } else {
@@ -385,7 +399,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
                 // 3-piece splits; six of the nine piece products (all above 2^-24 relative) in
                 // three MFMAs, (MFMA, lane half) -> (activation piece, weight piece):
                 // (0,0) h.h (0,1) m.h (1,0) h.m (1,1) l.h (2,0) h.l (2,1) m.m
-                const uint16_t* xm = sm.st[1].xm;
+                const uint16_t* xm = sm.st[1].xm + pbase * 8;
 #pragma unroll
                 for (int i = 0; i < TM; ++i) {
                     // RESCALE: in units of dl (rounded to fp32 once, then split exactly)
@@ -402,7 +416,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
                         wm[2][j] = __builtin_bit_cast(__bf16, g ? vm : vl);
                     }
 #pragma unroll
-                    for (int t = 0; t < TNW; ++t) {
+                    for (int t = 0; t < TN; ++t) {
                         const int pr = 32 * t + n;
                         const b8 x0 = *reinterpret_cast<const b8*>(xm + (g ? 1 : 0) * MFMA_BN * 8 + pr * 8);
                         const b8 x1 = *reinterpret_cast<const b8*>(xm + (g ? 2 : 0) * MFMA_BN * 8 + pr * 8);
@@ -413,17 +427,17 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
                 }
             }
             // 8 K-steps of 16 per half-unit (sub-block jj = st / 2, K-half m = st % 2), software
-            // pipelined: while step st's 2 * TNW * TM MFMAs run, the activation operands of step st + 1
+            // pipelined: while step st's 2 * TN * TM MFMAs run, the activation operands of step st + 1
             // are read from LDS and its weights converted (the schedule is pinned below)
-            h8 av[2][TNW][2];
+            h8 av[2][TN][HL];
             h8 wv[2][TM];
             h2v c1[TM], c0[TM];
-            auto read_av = [&](int st, h8(&dst)[TNW][2]) {
+            auto read_av = [&](int st, h8(&dst)[TN][HL]) {
 #pragma unroll
-                for (int t = 0; t < TNW; ++t)
+                for (int t = 0; t < TN; ++t)
 #pragma unroll
-                    for (int hl = 0; hl < 2; ++hl)
-                        dst[t][hl] = *reinterpret_cast<const h8*>(sa + t * 16384 + boff(hl, st >> 1, st & 1));
+                    for (int hl = 0; hl < HL; ++hl)
+                        dst[t][hl] = *reinterpret_cast<const h8*>(sa + t * 32 * PB + boff(hl, st >> 1, st & 1));
             };
             auto convert = [&](int st, h8(&dst)[TM]) {
                 const int jj = st >> 1, m = st & 1;
@@ -453,19 +467,19 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
                 const int b = st & 1;
 
                 // the next step's LDS reads go out before this step's MFMAs (nothing crosses the
-                // scheduling barriers), so their latency hides behind 2 * TNW * TM MFMAs
+                // scheduling barriers), so their latency hides behind 2 * TN * TM MFMAs
                 if (st + 1 < 2 * HB) read_av(st + 1, av[b ^ 1]);
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int hl = 0; hl < 2; ++hl)
+                for (int hl = 0; hl < HL; ++hl)
 #pragma unroll
-                    for (int t = 0; t < TNW; ++t)
+                    for (int t = 0; t < TN; ++t)
 #pragma unroll
                         for (int i = 0; i < TM; ++i) acc[i][t] = mfma16(av[b][t][hl], wv[b][i], acc[i][t]);
                 if (st + 1 < 2 * HB) {
                     convert(st + 1, wv[b ^ 1]);  // VALU work spread between the MFMAs
 #pragma unroll
-                    for (int k = 0; k < 2 * TNW * TM; ++k) {
+                    for (int k = 0; k < HL * TN * TM; ++k) {
                         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
                         __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
                     }
@@ -492,21 +506,21 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
                 if (j >= nb) break;
 #pragma unroll
                 for (int m = 0; m < 2; ++m) {
-                    h8 wv[TM], av[TNW][2];
+                    h8 wv[TM], av[TN][HL];
 #pragma unroll
                     for (int i = 0; i < TM; ++i) {
                         const uint4 raw = cur[i].q[j];
                         wv[i] = m ? cvt8(raw.z, raw.w, mask, flip, c1, c0) : cvt8(raw.x, raw.y, mask, flip, c1, c0);
                     }
 #pragma unroll
-                    for (int t = 0; t < TNW; ++t)
+                    for (int t = 0; t < TN; ++t)
 #pragma unroll
-                        for (int hl = 0; hl < 2; ++hl)
-                            av[t][hl] = *reinterpret_cast<const h8*>(sa + t * 16384 + boff(hl, j, m));
+                        for (int hl = 0; hl < HL; ++hl)
+                            av[t][hl] = *reinterpret_cast<const h8*>(sa + t * 32 * PB + boff(hl, j, m));
 #pragma unroll
-                    for (int hl = 0; hl < 2; ++hl)
+                    for (int hl = 0; hl < HL; ++hl)
 #pragma unroll
-                        for (int t = 0; t < TNW; ++t)
+                        for (int t = 0; t < TN; ++t)
 #pragma unroll
                             for (int i = 0; i < TM; ++i)
                                 sb[i][t] = mfma16(av[t][hl], wv[i], (m == 0 && hl == 0) ? v16f{} : sb[i][t]);
@@ -515,7 +529,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
                 for (int i = 0; i < TM; ++i) {  // fold: acc += d_b * D_b
                     const float db = f16_to_f32(cur[i].d[j]);
 #pragma unroll
-                    for (int t = 0; t < TNW; ++t)
+                    for (int t = 0; t < TN; ++t)
 #pragma unroll
                         for (int r = 0; r < 16; ++r) acc[i][t][r] = __builtin_fmaf(db, sb[i][t][r], acc[i][t][r]);
                 }
@@ -530,9 +544,9 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
 
     // ------------------------------------------------------------ epilogue
     if (active) {  // back to natural units: the row's unit (RESCALE) and the token's exponent
-        const float* pe = sm.st[(H - 1) & 1].pe;
+        const float* pe = sm.st[(H - 1) & 1].pe + pbase;
 #pragma unroll
-        for (int t = 0; t < TNW; ++t)
+        for (int t = 0; t < TN; ++t)
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) {
                 const float4 v = *reinterpret_cast<const float4*>(pe + 32 * t + 8 * ii + 4 * g);
@@ -545,26 +559,26 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
     }
     if constexpr (GATEUP) {
         // h = SiLU(g) * u in registers, written transposed to LDS: [pair][row of the workgroup]
-        constexpr int HLD = GW * 32 + 4;                  // h row stride (floats)
+        constexpr int HLD = A_::RW * 32 + 4;              // h row stride (floats)
         float* hs = reinterpret_cast<float*>(&sm.st[0]);  // [128 pairs][HLD], over both stage buffers
-        static_assert((size_t)MFMA_BN * HLD * 4 <= 2 * sizeof(Stage), "epilogue buffer");
+        static_assert((size_t)MFMA_BN * HLD * 4 <= 2 * sizeof(St), "epilogue buffer");
         __syncthreads();  // every wave is done with the stage buffers
         if (active) {
 #pragma unroll
-            for (int t = 0; t < TNW; ++t)
+            for (int t = 0; t < TN; ++t)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const float gv = acc[0][t][r], uv = acc[1][t][r];
-                    const int pr = 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
-                    hs[pr * HLD + wave * 32 + n] = (gv / (1.0f + expf(-gv))) * uv;  // SwiGLU
+                    const int pr = pbase + 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
+                    hs[pr * HLD + rw * 32 + n] = (gv / (1.0f + expf(-gv))) * uv;  // SwiGLU
                 }
         }
         __syncthreads();
         // Q8_0 of h (quantize_row_q8_0 over the down projection's K = these rows), one thread per
         // (pair, 32-row block = gate/up row tile)
-        for (int it = tid; it < GW * MFMA_BN; it += NTH) {
+        for (int it = tid; it < A_::RW * MFMA_BN; it += NTH) {
             const int pr = it % MFMA_BN, b = it / MFMA_BN;
-            const int blk = rg * GW + b;
+            const int blk = rg * A_::RW + b;
             if (pr >= cnt || blk >= W0.nrt) continue;
             const size_t p = (size_t)(p0 + pr);
             const float* hv = hs + pr * HLD + b * 32;
@@ -612,41 +626,55 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
             const int rt = rt0 + i;
             if (rt >= W0.nrt) continue;
 #pragma unroll
-            for (int t = 0; t < TNW; ++t)
+            for (int t = 0; t < TN; ++t)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int pr = 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
+                    const int pr = pbase + 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
                     if (pr < cnt) y[(size_t)(p0 + pr) * W0.rows + rt * 32 + n] = acc[i][t][r];
                 }
         }
     }
 }
 
-// Workgroup shape (every wave covers 128 pairs): one wave per SIMD, whose
-// 512 registers hold the accumulators, double-buffered operands and the next
-// half-unit's weights.
-template <int TYPE, bool GATEUP>
-struct Shape {
+// Workgroup shape: waves, row tiles and pair tiles per wave.
+#ifndef JX_GEMM_GU_GW
+#define JX_GEMM_GU_GW 4
+#endif
+#ifndef JX_GEMM_GU_TN
+#define JX_GEMM_GU_TN 4
+#endif
 #ifndef JX_DOWN_GW
 #define JX_DOWN_GW 4
 #endif
 #ifndef JX_DOWN_TM
-#define JX_DOWN_TM 2
+#define JX_DOWN_TM 1
 #endif
-    static constexpr int GW = GATEUP ? 4 : JX_DOWN_GW;
+#ifndef JX_DOWN_TN
+#define JX_DOWN_TN 4
+#endif
+#ifndef JX_DOWN_WGS
+#define JX_DOWN_WGS 2
+#endif
+// WPE: waves per SIMD the registers are budgeted for.  The hi-only down GEMM
+// stages half the bytes, so two workgroups share a CU.
+template <int TYPE, bool GATEUP>
+struct Shape {
+    static constexpr int GW = GATEUP ? JX_GEMM_GU_GW : JX_DOWN_GW;
     static constexpr int TM = GATEUP ? 2 : JX_DOWN_TM;
+    static constexpr int TN = GATEUP ? JX_GEMM_GU_TN : JX_DOWN_TN;
+    static constexpr int WPE = GATEUP ? GW / 4 : JX_DOWN_WGS * GW / 4;
 };
 
 template <int TYPE, bool GATEUP>
 static void launch_t(const QMat& w0, const QMat& w1, const ActH& in, const Groups& grp, int tiles_ub, const ActQ8& hq,
                      float* hf, int hf_ld, float* y, hipStream_t st) {
-    constexpr int GW = Shape<TYPE, GATEUP>::GW, TM = Shape<TYPE, GATEUP>::TM;
-    constexpr int rows_per_wg = Arr<GATEUP, GW, TM>::WROWS;  // row tiles of each matrix per workgroup
+    using S = Shape<TYPE, GATEUP>;
+    constexpr int rows_per_wg = Arr<GATEUP, S::GW, S::TM, S::TN>::WROWS;  // row tiles of each matrix per workgroup
     const int R = (w0.nrt + rows_per_wg - 1) / rows_per_wg;
     const int n_items = R * tiles_ub;
     if (n_items <= 0) return;
-    hipLaunchKernelGGL((k_wgemm<TYPE, GATEUP, GW, TM>), dim3(n_items), dim3(GW * 64), 0, st, w0, w1, in, grp, R,
-                       n_items, hq, hf, hf_ld, y);
+    hipLaunchKernelGGL((k_wgemm<TYPE, GATEUP, S::GW, S::TM, S::TN, S::WPE>), dim3(n_items), dim3(S::GW * 64), 0, st, w0, w1, in,
+                       grp, R, n_items, hq, hf, hf_ld, y);
 }
 
 void launch_mfma_gateup(const QMat& g, const QMat& u, const ActH& xin, const Groups& grp, int tiles_ub,

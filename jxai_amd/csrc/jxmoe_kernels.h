@@ -167,7 +167,8 @@ void launch_route_small(const RouteArgs& a, const DispatchOut& o, hipStream_t st
 void launch_quantize_q8(const float* x, int rows, int K, ActQ8 out, hipStream_t st);
 
 // Matrix-core form of existing Q8_0 activations (int8 quants + (scale, sum)).
-void launch_q8_to_acth(const ActQ8& in, int rows, ActH out, hipStream_t st);
+// lo = false writes only the fp16 hi halves (the down GEMM's operand).
+void launch_q8_to_acth(const ActQ8& in, int rows, ActH out, hipStream_t st, bool lo = true);
 
 // Repack a GGUF block matrix set [n_mats][rows][cols] (already on the device
 // as raw bytes) into the QMat layout.

@@ -46,7 +46,8 @@ __device__ __forceinline__ int quant_block(float v, int l32, bool ok, const ActQ
 // min-term values dx * sum(q) are stored times 2^-E as well; pe holds 2^E
 // for every half-unit of the row.
 template <int NTH>
-__device__ void write_acth_row(const int8_t* q, const float2* sc, int K, const ActH& o, size_t row, int tid) {
+__device__ void write_acth_row(const int8_t* q, const float2* sc, int K, const ActH& o, size_t row, int tid,
+                               bool lo = true) {
     __shared__ float wmax[NTH / 64];
     const int KH = K / 128, KB = K / 32;
     float M = 0.0f;
@@ -78,7 +79,7 @@ __device__ void write_acth_row(const int8_t* q, const float2* sc, int K, const A
         }
         uint16_t* hl = o.hl + row * (size_t)KH * 256 + hh * 256 + (i & 127);
         *reinterpret_cast<uint4*>(hl) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-        *reinterpret_cast<uint4*>(hl + 128) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        if (lo) *reinterpret_cast<uint4*>(hl + 128) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
         if ((i & 127) == 0) o.pe[row * (size_t)KH + hh] = up;
         if ((i & 31) == 0) {
             const float X = sc[b].x * sc[b].y * dn;  // exact: 11-bit scale x |sum| < 2^12, times 2^-E
@@ -218,13 +219,13 @@ void launch_route(const RouteArgs& a, hipStream_t st) {
 }
 
 // Matrix-core form of Q8_0 activations already in global memory, one block per row.
-__global__ void __launch_bounds__(256) k_q8_to_acth(ActQ8 in, ActH out) {
+__global__ void __launch_bounds__(256) k_q8_to_acth(ActQ8 in, ActH out, int lo) {
     const size_t row = blockIdx.x;
-    write_acth_row<256>(in.q + row * in.K, in.s + row * (in.K / 32), in.K, out, row, threadIdx.x);
+    write_acth_row<256>(in.q + row * in.K, in.s + row * (in.K / 32), in.K, out, row, threadIdx.x, lo != 0);
 }
 
-void launch_q8_to_acth(const ActQ8& in, int rows, ActH out, hipStream_t st) {
-    hipLaunchKernelGGL(k_q8_to_acth, dim3(rows), dim3(256), 0, st, in, out);
+void launch_q8_to_acth(const ActQ8& in, int rows, ActH out, hipStream_t st, bool lo) {
+    hipLaunchKernelGGL(k_q8_to_acth, dim3(rows), dim3(256), 0, st, in, out, lo ? 1 : 0);
 }
 
 // ---------------------------------------------------------------- few tokens

@@ -401,7 +401,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
             if (L->sdown_f32)
                 jx::launch_gemv_down(L->sdown.m, L->hqs, L->hfs, (int)fspad, sg, 1, 4, L->ysh, st);
             else {
-                jx::launch_q8_to_acth(L->hqs, n, L->hhs.a, st);
+                jx::launch_q8_to_acth(L->hqs, n, L->hhs.a, st, false);
                 jx::launch_mfma_down(L->sdown.m, L->hhs.a, sg, st_ub, L->ysh, st);
             }
         } else {
@@ -419,7 +419,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         Launch l(L, mfma ? (L->down_f32 ? "down_gemv_f32" : "down_mfma") : (L->down_f32 ? "down_gemv_f32" : "down_gemv"),
                  st);
         if (mfma && !L->down_f32) {
-            jx::launch_q8_to_acth(L->hq, nk, L->hh.a, st);
+            jx::launch_q8_to_acth(L->hq, nk, L->hh.a, st, false);
             jx::launch_mfma_down(L->down.m, L->hh.a, grp, tiles_ub, L->y, st);
         }
         else

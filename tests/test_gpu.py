@@ -100,7 +100,9 @@ def test_layer_vs_golden(moe, case):
     assert np.array_equal(ids, z["topk_ids"]), "routing differs"
     assert np.array_equal(counts, z["counts"])
     np.testing.assert_allclose(w, z["topk_w"], rtol=2e-6, atol=0)
-    assert rel_err(out[z["rows"]], z["out"]) <= REL_TOL
+    err = rel_err(out[z["rows"]], z["out"])
+    say(f"layer {case}: max rel err {err:.2e}")
+    assert err <= REL_TOL
     lg = L.last_logits(n)
     assert np.array_equal(lg[z["rows"]].view(np.uint32), z["logits_rows"].view(np.uint32)), "router logits not bit-exact"
     L.close()
@@ -125,7 +127,9 @@ def test_layer_regimes_vs_oracle(moe, port, name, n, regime):
     np.testing.assert_allclose(w, w_o, rtol=2e-6, atol=0)
     sel = np.unique(np.linspace(0, n - 1, min(n, 6)).astype(np.int32))
     want = port.moe_forward(lw, x, sel)[0]
-    assert rel_err(out[sel], want) <= REL_TOL
+    err = rel_err(out[sel], want)
+    say(f"{name} n={n} regime={regime}: max rel err {err:.2e}")
+    assert err <= REL_TOL
     L.close()
 
 
