@@ -23,10 +23,11 @@
 // 3-piece splits once per super-block, straight into acc.  Only the fp32
 // summation order differs from the reference.
 //
-// Work split: a workgroup owns one tile of MFMA_BN = 128 (token, expert) pairs
-// of one expert and a group of weight rows -- gate/up: 128 gate rows and the
-// same 128 up rows (one half-unit of the down projection's K, so h's exponent
-// and Q8_0 blocks are settled inside the workgroup); down: 256 rows.  A wave
+// Work split: the dispatch tables cut each expert's pairs into tiles of
+// MFMA_BN = 128 (token, expert) pairs; a workgroup owns a tile (down) or half
+// of one (gate/up: 64 pairs) and a group of weight rows -- gate/up: 128 gate
+// rows and the same 128 up rows (one half-unit of the down projection's K, so
+// h's Q8_0 blocks are settled inside the workgroup); down: 128 rows.  A wave
 // owns TM row tiles x TN pair tiles of 32 (MFMA 32x32 edges): every B operand
 // read from LDS feeds TM MFMAs and every A operand converted in registers
 // feeds TN.  Activations are staged per 128-K half-unit into LDS with direct
@@ -54,21 +55,21 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int HB = 4;  // 32-blocks per staged half-unit
 
-// One staged half-unit of MFMA_BN activation rows: HL = 2 stages fp16 hi and
-// lo (256 bytes each per row), HL = 1 hi only.
-template <int HL>
+// One staged half-unit of BN activation rows: HL = 2 stages fp16 hi and lo
+// (256 bytes each per row), HL = 1 hi only.
+template <int HL, int BN>
 struct Stage {
     static constexpr int PB = 256 * HL;   // bytes per row
     static constexpr int CPP = PB / 16;   // 16-byte chunks per row
-    uint8_t q[MFMA_BN * PB];              // row r, chunk c at chunk (c ^ (r % CPP))
-    float pe[MFMA_BN];                    // 2^E of each row
-    uint16_t xm[3 * MFMA_BN * 8];         // Q4_K: [piece][row][8 sub-blocks] bf16 of dx * sum(q)
+    uint8_t q[BN * PB];                   // row r, chunk c at chunk (c ^ (r % CPP))
+    float pe[BN];                         // 2^E of each row
+    uint16_t xm[3 * BN * 8];              // Q4_K: [piece][row][8 sub-blocks] bf16 of dx * sum(q)
 };
 
-template <int HL>
+template <int HL, int BN>
 struct GemmSmem {
-    Stage<HL> st[2];
-    int src[MFMA_BN];  // activation row (token or pair) of each staged pair
+    Stage<HL, BN> st[2];
+    int src[BN];  // activation row (token or pair) of each staged pair
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
@@ -164,14 +165,16 @@ __device__ __forceinline__ bool pair_tile(const Groups& grp, int ti, int& e, int
     return true;
 }
 
-// Workgroup -> (pair tile, row group): XCD-major numbering (hardware deals
-// workgroups round-robin over the 8 XCDs), row group fastest.
-__device__ __forceinline__ void work_item(int L, int n_items, int R, int& ti, int& rg) {
+// Workgroup -> (pair tile, part of the tile, row group): XCD-major numbering
+// (hardware deals workgroups round-robin over the 8 XCDs), row group fastest.
+__device__ __forceinline__ void work_item(int L, int n_items, int R, int S, int& ti, int& sub, int& rg) {
     const int x = L & 7, s = L >> 3;
     const int q = n_items >> 3, rem = n_items & 7;
     const int i = x * q + min(x, rem) + s;
-    ti = i / R;
-    rg = i - ti * R;
+    const int ts = i / R;
+    rg = i - ts * R;
+    ti = ts / S;
+    sub = ts - ti * S;
 }
 
 
@@ -236,23 +239,24 @@ struct Parity {
 };
 
 
-// Wave arrangement: NPG pair groups of TN pair tiles (32 pairs each) side by
-// side, RW row slots.  Gate/up: row slot s takes row tile s of the gate
-// matrix and the same tile of the up matrix (TM = 2: tile 0 gate, tile 1
+// Wave arrangement of a workgroup owning BN pairs (a dispatch tile of
+// MFMA_BN, or a part of one): NPG pair groups of TN pair tiles (32 pairs each)
+// side by side, RW row slots.  Gate/up: row slot s takes row tile s of the
+// gate matrix and the same tile of the up matrix (TM = 2: tile 0 gate, tile 1
 // up), so SwiGLU needs no exchange.  Down: row slot s takes TM row tiles.
-template <bool GATEUP, int GW, int TM, int TN>
+template <bool GATEUP, int GW, int TM, int TN, int BN>
 struct Arr {
-    static constexpr int NPG = MFMA_BN / (32 * TN);
+    static constexpr int NPG = BN / (32 * TN);
     static constexpr int RW = GW / NPG;
     static constexpr int WROWS = GATEUP ? RW : RW * TM;  // row tiles of each matrix per workgroup
-    static_assert(NPG * TN * 32 == MFMA_BN && NPG * RW == GW, "wave arrangement");
+    static_assert(NPG * TN * 32 == BN && NPG * RW == GW && MFMA_BN % BN == 0, "wave arrangement");
     static_assert(!GATEUP || TM == 2, "gate/up: a gate and an up tile per wave");
 };
 
 // The MFMAs take the activations as operand A and the weights as operand B,
 // so in each 32x32 result lane (n, g) holds weight row n (its scales are the
 // lane's own) and registers r span pairs 8*(r/4) + 4g + r%4.
-template <int TYPE, bool GATEUP, int GW, int TM, int TN, int WPE>
+template <int TYPE, bool GATEUP, int GW, int TM, int TN, int WPE, int BN>
 __global__ void __launch_bounds__(GW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, float* hf, int hf_ld, float* y) {
     constexpr int NTH = GW * 64;
@@ -264,25 +268,30 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
     // gate/up: exact hi + lo activation operands (h is re-quantized after SwiGLU); down: the hi
     // half only (relative error <= 2^-12 per activation, no re-quantization downstream)
     constexpr int HL = GATEUP ? 2 : 1;
-    using St = Stage<HL>;
+    using St = Stage<HL, BN>;
     constexpr int PB = St::PB, CPP = St::CPP, PPI = 64 / CPP;  // row bytes, chunks, rows per DMA
-    constexpr int PER = MFMA_BN / PPI / GW;  // 1 KB staging loads per wave and half-unit
-    __shared__ GemmSmem<HL> sm;
-    int ti, rg;
-    work_item(blockIdx.x, n_items, R, ti, rg);
+    constexpr int PER = BN / PPI / GW;  // 1 KB staging loads per wave and half-unit
+    static_assert(PER * PPI * GW == BN, "staging split");
+    __shared__ GemmSmem<HL, BN> sm;
+    int ti, sub, rg;
+    work_item(blockIdx.x, n_items, R, MFMA_BN / BN, ti, sub, rg);
     int e, p0, cnt;
     if (!pair_tile(grp, ti, e, p0, cnt)) return;  // whole workgroup
+    p0 += sub * BN;  // this workgroup's part of the tile
+    cnt -= sub * BN;
+    if (cnt <= 0) return;
+    cnt = min(cnt, BN);
 
     const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, g = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    using A_ = Arr<GATEUP, GW, TM, TN>;
+    using A_ = Arr<GATEUP, GW, TM, TN, BN>;
     const int pg = wave % A_::NPG, rw = wave / A_::NPG;  // pair group, row slot
     const int pbase = pg * TN * 32;                       // first pair of the wave within the tile
     // the wave's row tiles: gate/up tile rt0 of both matrices, or down tiles rt0 .. rt0 + TM - 1
     const int rt0 = GATEUP ? rg * A_::RW + rw : (rg * A_::RW + rw) * TM;
     const bool active = rt0 < W0.nrt;  // wave-uniform; inactive waves still stage and sync
 
-    if (tid < MFMA_BN) {  // activation row of each staged pair: token (gate/up) or pair (down)
+    if (tid < BN) {  // activation row of each staged pair: token (gate/up) or pair (down)
         const int p = p0 + min(tid, cnt - 1);
         sm.src[tid] = (GATEUP && !grp.identity) ? grp.pair_tok[p] : p;
     }
@@ -299,8 +308,8 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
         const int r = PPI * (wave * PER + k) + lane / CPP;
         soff[k] = (uint32_t)sm.src[r] * (uint32_t)(H * 512) + (uint32_t)(((lane % CPP) ^ (r % CPP)) << 4);
     }
-    const int sj = wave & 1;  // pe / xm: lane l of waves 0, 1 takes pair 64 * sj + l
-    const int srow = sm.src[64 * sj + lane];
+    const int sj = wave;  // pe / xm: lane l of wave w < BN / 64 takes pair 64 * w + l
+    const int srow = sm.src[64 * min(sj, BN / 64 - 1) + lane];
     const uint32_t peoff = (uint32_t)srow * (uint32_t)(H * 4);
     const uint32_t xoff = Q4K ? (uint32_t)srow * (uint32_t)(in.KU * 48) : 0u;
     auto stage = [&](int h) {
@@ -311,11 +320,11 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
         if constexpr (Q4K) {
             if (h & 1) {  // min-term values of the super-block: piece pc of the lane's pair
                 const uint8_t* xb = reinterpret_cast<const uint8_t*>(in.xm) + (size_t)(h >> 1) * 48;
-                if (wave < 2)
-                    for (int pc = 0; pc < 3; ++pc) dma16(xb + xoff + pc * 16, S.xm + pc * (MFMA_BN * 8) + 64 * sj * 8);
+                if (wave < BN / 64)
+                    for (int pc = 0; pc < 3; ++pc) dma16(xb + xoff + pc * 16, S.xm + pc * (BN * 8) + 64 * sj * 8);
             }
         }
-        if (wave < 2) dma4(reinterpret_cast<const uint8_t*>(in.pe) + (size_t)h * 4 + peoff, S.pe + 64 * sj);
+        if (wave < BN / 64) dma4(reinterpret_cast<const uint8_t*>(in.pe) + (size_t)h * 4 + peoff, S.pe + 64 * sj);
     };
 
     // weights: uniform bases, per-lane offsets of the wave's row tiles (tiles past the matrix load
@@ -418,8 +427,8 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
 #pragma unroll
                     for (int t = 0; t < TN; ++t) {
                         const int pr = 32 * t + n;
-                        const b8 x0 = *reinterpret_cast<const b8*>(xm + (g ? 1 : 0) * MFMA_BN * 8 + pr * 8);
-                        const b8 x1 = *reinterpret_cast<const b8*>(xm + (g ? 2 : 0) * MFMA_BN * 8 + pr * 8);
+                        const b8 x0 = *reinterpret_cast<const b8*>(xm + (g ? 1 : 0) * BN * 8 + pr * 8);
+                        const b8 x1 = *reinterpret_cast<const b8*>(xm + (g ? 2 : 0) * BN * 8 + pr * 8);
                         acc[i][t] = mfma16b(x0, wm[0], acc[i][t]);
                         acc[i][t] = mfma16b(x1, wm[1], acc[i][t]);
                         acc[i][t] = mfma16b(x0, wm[2], acc[i][t]);
@@ -561,7 +570,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
         // h = SiLU(g) * u in registers, written transposed to LDS: [pair][row of the workgroup]
         constexpr int HLD = A_::RW * 32 + 4;              // h row stride (floats)
         float* hs = reinterpret_cast<float*>(&sm.st[0]);  // [128 pairs][HLD], over both stage buffers
-        static_assert((size_t)MFMA_BN * HLD * 4 <= 2 * sizeof(St), "epilogue buffer");
+        static_assert((size_t)BN * HLD * 4 <= 2 * sizeof(St), "epilogue buffer");
         __syncthreads();  // every wave is done with the stage buffers
         if (active) {
 #pragma unroll
@@ -576,8 +585,8 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
         __syncthreads();
         // Q8_0 of h (quantize_row_q8_0 over the down projection's K = these rows), one thread per
         // (pair, 32-row block = gate/up row tile)
-        for (int it = tid; it < A_::RW * MFMA_BN; it += NTH) {
-            const int pr = it % MFMA_BN, b = it / MFMA_BN;
+        for (int it = tid; it < A_::RW * BN; it += NTH) {
+            const int pr = it % BN, b = it / BN;
             const int blk = rg * A_::RW + b;
             if (pr >= cnt || blk >= W0.nrt) continue;
             const size_t p = (size_t)(p0 + pr);
@@ -636,12 +645,22 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
     }
 }
 
-// Workgroup shape: waves, row tiles and pair tiles per wave.
+// Workgroup shape: waves, row tiles and pair tiles per wave, pairs per
+// workgroup (BN) and workgroups per CU (WGS; the registers are budgeted for
+// WGS * GW / 4 waves per SIMD).  Gate/up stages 64 pairs (hi and lo, 72 KB of
+// LDS) and the hi-only down GEMM 128 pairs (78 KB), so two workgroups share a
+// CU and one's staging waits overlap the other's matrix-core work.
 #ifndef JX_GEMM_GU_GW
 #define JX_GEMM_GU_GW 4
 #endif
 #ifndef JX_GEMM_GU_TN
-#define JX_GEMM_GU_TN 4
+#define JX_GEMM_GU_TN 2
+#endif
+#ifndef JX_GEMM_GU_WGS
+#define JX_GEMM_GU_WGS 2
+#endif
+#ifndef JX_GEMM_GU_BN
+#define JX_GEMM_GU_BN 64
 #endif
 #ifndef JX_DOWN_GW
 #define JX_DOWN_GW 4
@@ -655,25 +674,24 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
 #ifndef JX_DOWN_WGS
 #define JX_DOWN_WGS 2
 #endif
-// WPE: waves per SIMD the registers are budgeted for.  The hi-only down GEMM
-// stages half the bytes, so two workgroups share a CU.
 template <int TYPE, bool GATEUP>
 struct Shape {
     static constexpr int GW = GATEUP ? JX_GEMM_GU_GW : JX_DOWN_GW;
     static constexpr int TM = GATEUP ? 2 : JX_DOWN_TM;
     static constexpr int TN = GATEUP ? JX_GEMM_GU_TN : JX_DOWN_TN;
-    static constexpr int WPE = GATEUP ? GW / 4 : JX_DOWN_WGS * GW / 4;
+    static constexpr int WPE = (GATEUP ? JX_GEMM_GU_WGS : JX_DOWN_WGS) * GW / 4;
+    static constexpr int BN = GATEUP ? JX_GEMM_GU_BN : MFMA_BN;
 };
 
 template <int TYPE, bool GATEUP>
 static void launch_t(const QMat& w0, const QMat& w1, const ActH& in, const Groups& grp, int tiles_ub, const ActQ8& hq,
                      float* hf, int hf_ld, float* y, hipStream_t st) {
     using S = Shape<TYPE, GATEUP>;
-    constexpr int rows_per_wg = Arr<GATEUP, S::GW, S::TM, S::TN>::WROWS;  // row tiles of each matrix per workgroup
+    constexpr int rows_per_wg = Arr<GATEUP, S::GW, S::TM, S::TN, S::BN>::WROWS;  // row tiles of each matrix per workgroup
     const int R = (w0.nrt + rows_per_wg - 1) / rows_per_wg;
-    const int n_items = R * tiles_ub;
+    const int n_items = R * tiles_ub * (MFMA_BN / S::BN);
     if (n_items <= 0) return;
-    hipLaunchKernelGGL((k_wgemm<TYPE, GATEUP, S::GW, S::TM, S::TN, S::WPE>), dim3(n_items), dim3(S::GW * 64), 0, st, w0, w1, in,
+    hipLaunchKernelGGL((k_wgemm<TYPE, GATEUP, S::GW, S::TM, S::TN, S::WPE, S::BN>), dim3(n_items), dim3(S::GW * 64), 0, st, w0, w1, in,
                        grp, R, n_items, hq, hf, hf_ld, y);
 }
 
