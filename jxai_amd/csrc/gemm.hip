@@ -43,6 +43,8 @@
 // column l % 32.  A 32-K block takes two K-halves m; in half m, lane g
 // carries block elements 16g + 8m + i of both operands (the sum is
 // order-free).
+#include <algorithm>
+
 #include "jxmoe_device.h"
 #include "jxmoe_kernels.h"
 
@@ -165,18 +167,26 @@ __device__ __forceinline__ bool pair_tile(const Groups& grp, int ti, int& e, int
     return true;
 }
 
-// Workgroup -> (pair tile, part of the tile, row group): XCD-major numbering
-// (hardware deals workgroups round-robin over the 8 XCDs), row group fastest.
-__device__ __forceinline__ void work_item(int L, int n_items, int R, int S, int& ti, int& sub, int& rg) {
+// Workgroup -> (pair tile, part of the tile, row group).  Numbering is
+// XCD-major (hardware deals workgroups round-robin over the 8 XCDs, so XCD x
+// runs a contiguous range of items), and within it bands of RC row groups
+// sweep every pair tile: the ~64 workgroups resident on one XCD then cover
+// about RC row groups x 64 / RC tile parts, and each weight row group and each
+// staged activation tile is fetched into that XCD's L2 once for several
+// workgroups.  RC = R: all row groups of a tile part before the next part.
+__device__ __forceinline__ void work_item(int L, int n_items, int R, int S, int RC, int& ti, int& sub, int& rg) {
     const int x = L & 7, s = L >> 3;
     const int q = n_items >> 3, rem = n_items & 7;
     const int i = x * q + min(x, rem) + s;
-    const int ts = i / R;
-    rg = i - ts * R;
+    const int TS = n_items / R;             // tile parts
+    const int band = i / (RC * TS);         // full bands hold RC * TS items; the last one fewer rows
+    const int rows = min(RC, R - band * RC);
+    const int j = i - band * RC * TS;
+    const int ts = j / rows;
+    rg = band * RC + (j - ts * rows);
     ti = ts / S;
     sub = ts - ti * S;
 }
-
 
 // Exponent of a half-unit from its largest block scale M: |dx * q| * 2^-E < 2^15.
 __device__ __forceinline__ int half_exp(float M) {
@@ -258,7 +268,8 @@ struct Arr {
 // lane's own) and registers r span pairs 8*(r/4) + 4g + r%4.
 template <int TYPE, bool GATEUP, int GW, int TM, int TN, int WPE, int BN>
 __global__ void __launch_bounds__(GW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
-k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, float* hf, int hf_ld, float* y) {
+k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8 hq, float* hf, int hf_ld,
+        float* y) {
     constexpr int NTH = GW * 64;
     constexpr bool Q4K = TYPE == T_Q4_K;
     // Q4_K: no per-period sums; acc is kept in units of the current
@@ -274,7 +285,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
     static_assert(PER * PPI * GW == BN, "staging split");
     __shared__ GemmSmem<HL, BN> sm;
     int ti, sub, rg;
-    work_item(blockIdx.x, n_items, R, MFMA_BN / BN, ti, sub, rg);
+    work_item(blockIdx.x, n_items, R, MFMA_BN / BN, RC, ti, sub, rg);
     int e, p0, cnt;
     if (!pair_tile(grp, ti, e, p0, cnt)) return;  // whole workgroup
     p0 += sub * BN;  // this workgroup's part of the tile
@@ -674,6 +685,14 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, ActQ8 hq, flo
 #ifndef JX_DOWN_WGS
 #define JX_DOWN_WGS 2
 #endif
+// Row groups per band of the workgroup order (0: all of them); 4 measured
+// best for both GEMMs on the 2048-token Mixtral layer (2, 8, 16 and all slower).
+#ifndef JX_GEMM_GU_RC
+#define JX_GEMM_GU_RC 4
+#endif
+#ifndef JX_DOWN_RC
+#define JX_DOWN_RC 4
+#endif
 template <int TYPE, bool GATEUP>
 struct Shape {
     static constexpr int GW = GATEUP ? JX_GEMM_GU_GW : JX_DOWN_GW;
@@ -681,6 +700,7 @@ struct Shape {
     static constexpr int TN = GATEUP ? JX_GEMM_GU_TN : JX_DOWN_TN;
     static constexpr int WPE = (GATEUP ? JX_GEMM_GU_WGS : JX_DOWN_WGS) * GW / 4;
     static constexpr int BN = GATEUP ? JX_GEMM_GU_BN : MFMA_BN;
+    static constexpr int RC = GATEUP ? JX_GEMM_GU_RC : JX_DOWN_RC;
 };
 
 template <int TYPE, bool GATEUP>
@@ -691,8 +711,9 @@ static void launch_t(const QMat& w0, const QMat& w1, const ActH& in, const Group
     const int R = (w0.nrt + rows_per_wg - 1) / rows_per_wg;
     const int n_items = R * tiles_ub * (MFMA_BN / S::BN);
     if (n_items <= 0) return;
-    hipLaunchKernelGGL((k_wgemm<TYPE, GATEUP, S::GW, S::TM, S::TN, S::WPE, S::BN>), dim3(n_items), dim3(S::GW * 64), 0, st, w0, w1, in,
-                       grp, R, n_items, hq, hf, hf_ld, y);
+    const int RC = S::RC > 0 ? std::min(S::RC, R) : R;
+    hipLaunchKernelGGL((k_wgemm<TYPE, GATEUP, S::GW, S::TM, S::TN, S::WPE, S::BN>), dim3(n_items), dim3(S::GW * 64), 0, st,
+                       w0, w1, in, grp, R, n_items, RC, hq, hf, hf_ld, y);
 }
 
 void launch_mfma_gateup(const QMat& g, const QMat& u, const ActH& xin, const Groups& grp, int tiles_ub,

@@ -99,6 +99,7 @@ struct RouteArgs {
     float* probs;          // [n][k]
     float* shscale;        // [n]
     float* logits;         // [n][E] or null
+    const float* router_cm;  // the router rows, then the shared gate, chain-major (chain_rows)
 };
 
 // Outputs of the token -> expert dispatch (the device side of Groups).
@@ -124,6 +125,10 @@ struct SmallTail {
 };
 
 void launch_route(const RouteArgs& a, hipStream_t st);
+// Host side: nrows rows of d floats in the chain-major order launch_route reads
+// (out holds nrows * 16 * chain_stride(d) floats).
+int chain_stride(int d);
+void chain_rows(const float* rows, int nrows, int d, float* out);
 void launch_dispatch(const int* ids, int nk, int E, int top_k, const DispatchOut& o, hipStream_t st);
 
 // Decode regime: gate+up dequant-GEMV with SwiGLU and Q8_0 re-quantization.

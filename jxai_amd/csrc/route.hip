@@ -9,8 +9,6 @@
 
 namespace jx {
 
-constexpr int ROUTE_THREADS = 512;
-
 // Q8_0 of one 32-block held one value per lane of a half-wave
 // (quantize_row_q8_0, src/quant.cpp:1029-1045): amax, d = amax/127 (IEEE
 // division), id = 1/d, q = clamp(round-half-away(x*id)), stored scale =
@@ -45,11 +43,54 @@ __device__ __forceinline__ int quant_block(float v, int l32, bool ok, const ActQ
 // range: at most 2^-25 absolute, 2^-40 of the row's largest value).  The Q4_K
 // min-term values dx * sum(q) are stored times 2^-E as well; pe holds 2^E
 // for every half-unit of the row.
+// Row exponent of the matrix-core form from the row's largest block scale M.
+__device__ __forceinline__ int acth_exponent(float M) {
+    return (M > 0.0f) ? (int)((__float_as_uint(M) >> 23) & 0xFF) - 127 - 7 : 0;
+}
+
+// Elements 8c .. 8c+7 of one row (all in one 32-block): one 16-byte store
+// each of hi and lo, plus the row's pe entry and the block's min-term pieces
+// when the chunk opens them.
+__device__ __forceinline__ void acth_chunk(const int8_t* q, const float2* sc, int K, const ActH& o, size_t row, int c,
+                                           int E, bool lo) {
+    const int KH = K / 128;
+    const float dn = __uint_as_float((uint32_t)(127 - E) << 23), up = __uint_as_float((uint32_t)(127 + E) << 23);
+    const int i = 8 * c, b = i >> 5, hh = i >> 7;
+    const uint2 qq = *reinterpret_cast<const uint2*>(q + i);
+    const float s = sc[b].x * dn;  // exact: power-of-two scaling
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const uint32_t word = u < 2 ? qq.x : qq.y;
+        const int q0 = (int)(int8_t)(word >> (16 * (u & 1))), q1 = (int)(int8_t)(word >> (16 * (u & 1) + 8));
+        const float v0 = s * (float)q0, v1 = s * (float)q1;  // exact: 11-bit scale x |q| <= 127
+        const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
+        const _Float16 l0 = (_Float16)(v0 - (float)h0), l1 = (_Float16)(v1 - (float)h1);
+        hw[u] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+        lw[u] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+    }
+    uint16_t* hl = o.hl + row * (size_t)KH * 256 + hh * 256 + (i & 127);
+    *reinterpret_cast<uint4*>(hl) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    if (lo) *reinterpret_cast<uint4*>(hl + 128) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    if ((i & 127) == 0) o.pe[row * (size_t)KH + hh] = up;
+    if ((i & 31) == 0) {
+        const float X = sc[b].x * sc[b].y * dn;  // exact: 11-bit scale x |sum| < 2^12, times 2^-E
+        const uint32_t bh = __float_as_uint(X) & 0xFFFF0000u;
+        const float r1 = X - __uint_as_float(bh);
+        const uint32_t bm = __float_as_uint(r1) & 0xFFFF0000u;
+        const float r2 = r1 - __uint_as_float(bm);
+        uint16_t* xm = o.xm + row * (size_t)o.KU * 24 + (b / 8) * 24 + (b % 8);
+        xm[0] = (uint16_t)(bh >> 16);
+        xm[8] = (uint16_t)(bm >> 16);
+        xm[16] = (uint16_t)(__float_as_uint(r2) >> 16);
+    }
+}
+
 template <int NTH>
 __device__ void write_acth_row(const int8_t* q, const float2* sc, int K, const ActH& o, size_t row, int tid,
                                bool lo = true) {
     __shared__ float wmax[NTH / 64];
-    const int KH = K / 128, KB = K / 32;
+    const int KB = K / 32;
     float M = 0.0f;
     for (int b = tid; b < KB; b += NTH) M = fmaxf(M, sc[b].x);
 #pragma unroll
@@ -59,163 +100,247 @@ __device__ void write_acth_row(const int8_t* q, const float2* sc, int K, const A
     M = wmax[0];
 #pragma unroll
     for (int w = 1; w < NTH / 64; ++w) M = fmaxf(M, wmax[w]);
-    const int E = (M > 0.0f) ? (int)((__float_as_uint(M) >> 23) & 0xFF) - 127 - 7 : 0;
-    const float dn = __uint_as_float((uint32_t)(127 - E) << 23), up = __uint_as_float((uint32_t)(127 + E) << 23);
-    // eight consecutive elements per thread: one 16-byte store each of hi and lo
-    for (int c = tid; c < K / 8; c += NTH) {
-        const int i = 8 * c, b = i >> 5, hh = i >> 7;
-        const uint2 qq = *reinterpret_cast<const uint2*>(q + i);
-        const float s = sc[b].x * dn;  // exact: power-of-two scaling
-        uint32_t hw[4], lw[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t word = u < 2 ? qq.x : qq.y;
-            const int q0 = (int)(int8_t)(word >> (16 * (u & 1))), q1 = (int)(int8_t)(word >> (16 * (u & 1) + 8));
-            const float v0 = s * (float)q0, v1 = s * (float)q1;  // exact: 11-bit scale x |q| <= 127
-            const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
-            const _Float16 l0 = (_Float16)(v0 - (float)h0), l1 = (_Float16)(v1 - (float)h1);
-            hw[u] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-            lw[u] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
-        }
-        uint16_t* hl = o.hl + row * (size_t)KH * 256 + hh * 256 + (i & 127);
-        *reinterpret_cast<uint4*>(hl) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-        if (lo) *reinterpret_cast<uint4*>(hl + 128) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-        if ((i & 127) == 0) o.pe[row * (size_t)KH + hh] = up;
-        if ((i & 31) == 0) {
-            const float X = sc[b].x * sc[b].y * dn;  // exact: 11-bit scale x |sum| < 2^12, times 2^-E
-            const uint32_t bh = __float_as_uint(X) & 0xFFFF0000u;
-            const float r1 = X - __uint_as_float(bh);
-            const uint32_t bm = __float_as_uint(r1) & 0xFFFF0000u;
-            const float r2 = r1 - __uint_as_float(bm);
-            uint16_t* xm = o.xm + row * (size_t)o.KU * 24 + (b / 8) * 24 + (b % 8);
-            xm[0] = (uint16_t)(bh >> 16);
-            xm[8] = (uint16_t)(bm >> 16);
-            xm[16] = (uint16_t)(__float_as_uint(r2) >> 16);
-        }
-    }
+    const int E = acth_exponent(M);
+    for (int c = tid; c < K / 8; c += NTH) acth_chunk(q, sc, K, o, row, c, E, lo);
 }
 
-// One block per token.
-//  1. x -> LDS.
-//  2. Q8_0 of x, 32 lanes per block (quantize_row_q8_0, src/quant.cpp:1029-1045):
-//     amax, d = amax/127 (IEEE division), id = 1/d, q = clamp(round-half-away(x*id)),
-//     stored scale = truncated fp16 of d; the block sum of q rides along for the
-//     Q4_0 (-8 offset) and Q4_K (min) terms.
+// Chain-major rows: element 16 i + j of a row at j * S + i, so lane j of a
+// vec_dot_f32 chain reads its operands four at a time.  In LDS the stride is
+// padded to a multiple of 4 floats plus 4 against bank conflicts; the router
+// copy in global memory (chain_rows) uses the bare multiple of 4, and each
+// lane's run of steps then sits in a few L1 lines it revisits (measured
+// faster than interleaving the 16 chains for contiguous group loads).
+__host__ __device__ inline int rs_stride(int d) { return ((d / 16 + 3) & ~3) + 4; }
+__host__ __device__ inline int chain_stride_of(int d) { return (d / 16 + 3) & ~3; }
+int chain_stride(int d) { return chain_stride_of(d); }
+
+void chain_rows(const float* rows, int nrows, int d, float* out) {
+    const int S = chain_stride_of(d);
+    std::fill(out, out + (size_t)nrows * 16 * S, 0.0f);
+    for (int r = 0; r < nrows; ++r)
+        for (int e = 0; e < d; ++e) out[(size_t)r * 16 * S + (e & 15) * S + (e >> 4)] = rows[(size_t)r * d + e];
+}
+
+// Routing for many tokens, RT_TMAX (or fewer, when d is large) per block of
+// RT_THREADS:
+//  1. the block's token rows -> LDS, chain-major.
+//  2. Q8_0 of x, one thread per 32-block (quantize_row_q8_0,
+//     src/quant.cpp:1029-1045): amax, d = amax/127 (IEEE division), id = 1/d,
+//     q = clamp(round-half-away(x*id)), stored scale = truncated fp16 of d; the
+//     block sum of q rides along for the Q4_0 (-8 offset) and Q4_K (min)
+//     terms.  With a matrix-core consumer the rows' ActH form follows.
 //  3. Router logits in vec_dot_f32's exact fp32 order (src/quant.cpp:2756-2778):
-//     16 lanes per expert, lane j runs the FMA chain over elements 16i+j (lanes
-//     0-7 are the reference's acc0, 8-15 its acc1), then acc0+acc1, the optional
-//     8-element pass, the sequential sum of 8 lanes and the scalar tail.  Four
-//     experts per 16-lane group run interleaved for ILP.  The shared-expert gate
-//     vector (transformer.cpp:2748-2751) is one more row of the same GEMV.
+//     16 lanes per router row, lane j runs the FMA chain over elements 16i+j
+//     (lanes 0-7 are the reference's acc0, 8-15 its acc1), then acc0+acc1 and
+//     the sequential sum of the 8 lanes (d % 32 == 0: no tails).  One router
+//     load (four chain steps, chain-major copy) feeds every token of the block,
+//     whose chains are independent.  The shared-expert gate vector
+//     (transformer.cpp:2748-2751) is one more row.
 //  4. Top-k by rank counting (descending logit, ties by index) and softmax over
 //     the k selected logits (select_experts_cache_aware, src/tier.cpp:144-188).
-__global__ void __launch_bounds__(ROUTE_THREADS) k_route(RouteArgs a) {
-    extern __shared__ float xs[];  // d floats, then (matrix-core output) d int8 quants and d/32 (scale, sum)
-    __shared__ float lg[MAX_E];
-    __shared__ int sel[MAX_K];
-    __shared__ float shl;
-    const int t = blockIdx.x;
-    const int tid = threadIdx.x;
-    const int d = a.d;
-    const float* x = a.x + (size_t)t * d;
-    for (int i = tid; i < d; i += ROUTE_THREADS) xs[i] = x[i];
+#ifndef JX_RT_TMAX
+#define JX_RT_TMAX 2
+#endif
+#ifndef JX_RT_LDS_KB
+#define JX_RT_LDS_KB 80
+#endif
+constexpr int RT_THREADS = 256;
+constexpr int RT_TMAX = JX_RT_TMAX;
+constexpr size_t RT_LDS_TARGET = JX_RT_LDS_KB * 1024;
+
+static size_t route_lds(int T, int d, int E) {
+    return (size_t)T * 16 * rs_stride(d) * sizeof(float) + (size_t)T * d + (size_t)T * (d / 32) * sizeof(float2) +
+           (size_t)T * E * sizeof(float);
+}
+
+static int route_tokens_per_block(int d, int E) {
+    for (int T = RT_TMAX; T > 1; --T)
+        if (route_lds(T, d, E) <= RT_LDS_TARGET) return T;
+    return 1;
+}
+
+__global__ void __launch_bounds__(RT_THREADS) k_route(RouteArgs a, int T) {
+    extern __shared__ __align__(16) float lds[];
+    __shared__ int sel[RT_TMAX][MAX_K];
+    __shared__ float shl[RT_TMAX];
+    __shared__ float rmax[RT_TMAX];
+    const int d = a.d, E = a.E, S = rs_stride(d), RS = 16 * S, KB = d / 32;
+    const int t0 = blockIdx.x * T, nt = min(T, a.n - t0);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float* xs = lds;                                       // [T][16][S] chain-major rows
+    int8_t* qs = reinterpret_cast<int8_t*>(xs + T * RS);   // [T][d] quants
+    float2* ss = reinterpret_cast<float2*>(qs + T * d);    // [T][KB] (scale, sum)
+    float* lg = reinterpret_cast<float*>(ss + T * KB);     // [T][E] logits
     // every selection slot holds a valid expert even if NaN logits break the ranking
-    if (tid < a.k) sel[tid] = tid;
+    if (tid < RT_TMAX * MAX_K) sel[tid / MAX_K][tid % MAX_K] = tid % MAX_K;
+
+    // -- 1. rows -> LDS, four loads in flight per thread before their stores
+    {
+        const int c4 = d / 4, tot = nt * c4;
+        for (int i0 = 0; i0 < tot; i0 += 4 * RT_THREADS) {
+            float4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = min(i0 + u * RT_THREADS + tid, tot - 1);
+                const int t = i / c4, c = i - t * c4;
+                v[u] = *reinterpret_cast<const float4*>(a.x + (size_t)(t0 + t) * d + 4 * c);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = min(i0 + u * RT_THREADS + tid, tot - 1);  // clamped duplicates store the same values
+                const int t = i / c4, c = i - t * c4;
+                float* dst = xs + t * RS + 4 * (c & 3) * S + (c >> 2);  // elements 4c..4c+3: j = 4(c%4)+q, i = c/4
+                dst[0] = v[u].x;
+                dst[S] = v[u].y;
+                dst[2 * S] = v[u].z;
+                dst[3 * S] = v[u].w;
+            }
+        }
+    }
     __syncthreads();
 
-    // -- Q8_0 of x
-    {
-        const int lane = tid & 63, wave = tid >> 6, half = lane >> 5, l32 = lane & 31;
-        const int nb = d / 32;
-        int8_t* qs = reinterpret_cast<int8_t*>(xs + d);
-        float2* ss = reinterpret_cast<float2*>(qs + d);
-        for (int bb = wave * 2; bb < nb; bb += (ROUTE_THREADS / 64) * 2) {
-            const int b = bb + half;
-            const bool ok = b < nb;
-            const int q = quant_block(ok ? xs[b * 32 + l32] : 0.0f, l32, ok, a.xq, (size_t)t, b, ok ? ss + b : nullptr);
-            if (ok && a.xh.hl) qs[b * 32 + l32] = (int8_t)q;
+    // -- 2. Q8_0 of x: one thread per 32-block (its max and integer sum are order-free)
+    for (int i = tid; i < nt * KB; i += RT_THREADS) {
+        const int t = i / KB, b = i - t * KB;
+        const float* xr = xs + t * RS + 2 * b;  // element 32b + u at (u % 16) * S + 2b + u / 16
+        float v[32];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const float2 p = *reinterpret_cast<const float2*>(xr + u * S);
+            v[u] = p.x;
+            v[16 + u] = p.y;
         }
-        if (a.xh.hl) {
-            __syncthreads();
-            write_acth_row<ROUTE_THREADS>(qs, ss, d, a.xh, (size_t)t, tid);
+        float amax = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 32; ++u) amax = fmaxf(amax, __builtin_fabsf(v[u]));
+        const float dd = amax / 127.0f;
+        const float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
+        int sum = 0;
+        uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int u = 0; u < 32; ++u) {
+            float r = round_away(v[u] * id);
+            r = fminf(fmaxf(r, -127.0f), 127.0f);
+            const int q = (int)r;
+            sum += q;
+            w[u >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (u & 3));
+        }
+        const float2 sv = make_float2(f16_to_f32(f32_to_f16_trunc(dd)), (float)sum);
+        const uint4 w0 = make_uint4(w[0], w[1], w[2], w[3]), w1 = make_uint4(w[4], w[5], w[6], w[7]);
+        uint4* gq = reinterpret_cast<uint4*>(a.xq.q + (size_t)(t0 + t) * a.xq.K + 32 * b);
+        gq[0] = w0;
+        gq[1] = w1;
+        a.xq.s[(size_t)(t0 + t) * KB + b] = sv;
+        uint4* lq = reinterpret_cast<uint4*>(qs + t * d + 32 * b);
+        lq[0] = w0;
+        lq[1] = w1;
+        ss[t * KB + b] = sv;
+    }
+    __syncthreads();
+    if (a.xh.hl) {  // matrix-core form: one exponent per row from its largest block scale
+        if (wave < nt) {
+            float M = 0.0f;
+            for (int b = lane; b < KB; b += 64) M = fmaxf(M, ss[wave * KB + b].x);
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+            if (lane == 0) rmax[wave] = M;
+        }
+        __syncthreads();
+        const int cpr = d / 8;
+        for (int c = tid; c < nt * cpr; c += RT_THREADS) {
+            const int t = c / cpr;
+            acth_chunk(qs + t * d, ss + t * KB, d, a.xh, (size_t)(t0 + t), c - t * cpr, acth_exponent(rmax[t]), true);
         }
     }
 
-    // -- router GEMV, exact vec_dot_f32 order
+    // -- 3. router chains, exact vec_dot_f32 order
     {
-        const int grp = tid >> 4, j = tid & 15, ngrp = ROUTE_THREADS / 16;
-        const int nrows = a.E + (a.shgate ? 1 : 0);
-        const int d16 = (d / 16) * 16;
-        const bool has8 = (d - d16) >= 8;
-        for (int base = 0; base < nrows; base += ngrp * 4) {
-            const float* w[4];
-            bool ok[4];
-            float acc[4];
+        const int grp = tid >> 4, j = tid & 15;
+        const int R = E + (a.shgate ? 1 : 0);
+        const int m = d / 16, m4 = m & ~3, Sg = chain_stride_of(d);
+        for (int r = grp; r < R; r += RT_THREADS / 16) {
+            const float* wr = a.router_cm + (size_t)r * 16 * Sg + j * Sg;
+            const float* xr = xs + j * S;
+            float acc[RT_TMAX];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int e = base + c * ngrp + grp;
-                ok[c] = e < nrows;
-                w[c] = ok[c] ? (e < a.E ? a.router + (size_t)e * d : a.shgate) : a.router;
-                acc[c] = 0.0f;
+            for (int t = 0; t < RT_TMAX; ++t) acc[t] = 0.0f;
+#pragma unroll 8
+            for (int i = 0; i < m4; i += 4) {
+                const float4 w4 = *reinterpret_cast<const float4*>(wr + i);
+#pragma unroll
+                for (int t = 0; t < RT_TMAX; ++t) {
+                    if (t < nt) {
+                        const float4 x4 = *reinterpret_cast<const float4*>(xr + t * RS + i);
+                        acc[t] = __builtin_fmaf(w4.x, x4.x, acc[t]);
+                        acc[t] = __builtin_fmaf(w4.y, x4.y, acc[t]);
+                        acc[t] = __builtin_fmaf(w4.z, x4.z, acc[t]);
+                        acc[t] = __builtin_fmaf(w4.w, x4.w, acc[t]);
+                    }
+                }
             }
-#pragma unroll 4
-            for (int i = 0; i < d16; i += 16) {
-                const float xv = xs[i + j];
+            for (int i = m4; i < m; ++i) {
+                const float wv = wr[i];
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    if (ok[c]) acc[c] = __builtin_fmaf(w[c][i + j], xv, acc[c]);
+                for (int t = 0; t < RT_TMAX; ++t)
+                    if (t < nt) acc[t] = __builtin_fmaf(wv, xr[t * RS + i], acc[t]);
             }
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const float hi = __shfl_down(acc[c], 8, 16);
-                float v = acc[c] + hi;  // acc0[j] + acc1[j] for j < 8
-                if (has8 && ok[c] && j < 8) v = __builtin_fmaf(w[c][d16 + j], xs[d16 + j], v);
-                float s = 0.0f;
+            for (int t = 0; t < RT_TMAX; ++t) {
+                if (t < nt) {
+                    const float hi = __shfl_down(acc[t], 8, 16);
+                    const float v = acc[t] + hi;  // acc0[j] + acc1[j] for j < 8
+                    float s = 0.0f;
 #pragma unroll
-                for (int q = 0; q < 8; ++q) s += __shfl(v, q, 16);
-                for (int i = d16 + (has8 ? 8 : 0); i < d; ++i)
-                    if (ok[c]) s = __builtin_fmaf(w[c][i], xs[i], s);
-                const int e = base + c * ngrp + grp;
-                if (j == 0 && ok[c]) {
-                    if (e < a.E) lg[e] = a.bias ? s + a.bias[e] : s;
-                    else shl = s;
+                    for (int q = 0; q < 8; ++q) s += __shfl(v, q, 16);
+                    if (j == 0) {
+                        if (r < E) lg[t * E + r] = a.bias ? s + a.bias[r] : s;
+                        else shl[t] = s;
+                    }
                 }
             }
         }
     }
     __syncthreads();
 
-    // -- top-k by rank
-    for (int e = tid; e < a.E; e += ROUTE_THREADS) {
-        const float le = rank_key(lg[e]);
+    // -- 4. top-k by rank, softmax over the selected logits
+    for (int i = tid; i < nt * E; i += RT_THREADS) {
+        const int t = i / E, e = i - t * E;
+        const float* lt = lg + t * E;
+        const float le = rank_key(lt[e]);
         int rank = 0;
-        for (int f = 0; f < a.E; ++f) rank += ranks_above(rank_key(lg[f]), f, le, e);
-        if (rank < a.k) sel[rank] = e;
-        if (a.logits) a.logits[(size_t)t * a.E + e] = lg[e];
+        for (int f = 0; f < E; ++f) rank += ranks_above(rank_key(lt[f]), f, le, e);
+        if (rank < a.k) sel[t][rank] = e;
+        if (a.logits) a.logits[(size_t)(t0 + t) * E + e] = lt[e];
     }
     __syncthreads();
-    if (tid == 0) {
-        const int k = a.k;
+    if (tid < nt) {
+        const int t = tid, k = a.k;
+        const float* lt = lg + t * E;
         float p[MAX_K];
-        float mx = lg[sel[0]];
-        for (int i = 1; i < k; ++i) mx = fmaxf(mx, lg[sel[i]]);
+        float mx = lt[sel[t][0]];
+        for (int i = 1; i < k; ++i) mx = fmaxf(mx, lt[sel[t][i]]);
         float sum = 0.0f;
         for (int i = 0; i < k; ++i) {
-            p[i] = expf(lg[sel[i]] - mx);
+            p[i] = expf(lt[sel[t][i]] - mx);
             sum += p[i];
         }
         const float inv = (sum > 0.0f) ? 1.0f / sum : 1.0f / (float)k;
+        const size_t o = (size_t)(t0 + t) * k;
         for (int i = 0; i < k; ++i) {
-            a.ids[(size_t)t * k + i] = sel[i];
-            a.probs[(size_t)t * k + i] = p[i] * inv;
+            a.ids[o + i] = sel[t][i];
+            a.probs[o + i] = p[i] * inv;
         }
-        if (a.shscale) a.shscale[t] = a.shgate ? 1.0f / (1.0f + expf(-shl)) : 1.0f;
+        if (a.shscale) a.shscale[t0 + t] = a.shgate ? 1.0f / (1.0f + expf(-shl[t])) : 1.0f;
     }
 }
 
 void launch_route(const RouteArgs& a, hipStream_t st) {
-    const size_t lds = (size_t)a.d * sizeof(float) + (a.xh.hl ? (size_t)a.d + (size_t)a.d / 32 * sizeof(float2) : 0);
-    hipLaunchKernelGGL(k_route, dim3(a.n), dim3(ROUTE_THREADS), lds, st, a);
+    const int T = route_tokens_per_block(a.d, a.E);
+    const size_t lds = route_lds(T, a.d, a.E);
+    if (lds > 65536)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_route), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)lds);
+    hipLaunchKernelGGL(k_route, dim3((a.n + T - 1) / T), dim3(RT_THREADS), lds, st, a, T);
 }
 
 // Matrix-core form of Q8_0 activations already in global memory, one block per row.
@@ -239,10 +364,6 @@ void launch_q8_to_acth(const ActQ8& in, int rows, ActH out, hipStream_t st, bool
 constexpr int RS_THREADS = 256;
 constexpr int RS_LDS_BYTES = 64 * 1024;
 
-// Rows staged chain-major: element 16 i + j of a row at j * rs_stride(d) + i,
-// so lane j of a vec_dot_f32 chain reads its operands four at a time
-// (stride padded to a multiple of 4 floats, plus 4 against bank conflicts).
-__host__ __device__ inline int rs_stride(int d) { return ((d / 16 + 3) & ~3) + 4; }
 static size_t rs_lds(int n, int d) { return (size_t)(1 + n) * 16 * rs_stride(d) * sizeof(float); }
 
 bool route_small_fits(int n, int d, int E) {

@@ -148,6 +148,7 @@ struct jx_moe_layer {
     int E = 0, k = 0, d = 0, F = 0, Fs = 0;
     bool shared = false, down_f32 = false, sdown_f32 = false;
     float* router = nullptr;
+    float* router_cm = nullptr;  // router rows + shared gate, chain-major
     float* bias = nullptr;
     float* shgate = nullptr;
     DevMat gate, up, down, sgate, sup, sdown;
@@ -255,7 +256,7 @@ int ensure_workspace(jx_moe_layer* L, int n) {
 void free_layer(jx_moe_layer* L) {
     (void)hipSetDevice(L->device);
     for (auto* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown}) m->release();
-    void* ptrs[] = {L->router, L->bias, L->shgate, L->x, L->out, L->probs, L->shscale, L->logits, L->ids,
+    void* ptrs[] = {L->router, L->router_cm, L->bias, L->shgate, L->x, L->out, L->probs, L->shscale, L->logits, L->ids,
                     L->counts, L->offs, L->act, L->n_act, L->pair_tok, L->pos_of, L->n_tiles, L->tiles,
                     L->slots, L->xq.q, L->xq.s, L->hq.q, L->hq.s, L->hqs.q, L->hqs.s, L->hf, L->hfs, L->y, L->ysh};
     for (void* p : ptrs)
@@ -324,7 +325,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     const bool smfma = L->shared && n >= jx::MFMA_MIN_SHARED_TOKENS && !(flags & JX_FWD_FORCE_GEMV) && d % 128 == 0 &&
                        (L->sdown_f32 || L->Fs % 128 == 0);
     jx::RouteArgs ra{xdev, n, d, E, k, L->router, L->bias, L->shgate, L->xq, (mfma || smfma) ? L->xh.a : jx::ActH{},
-                     L->ids, L->probs, L->shscale, L->logits};
+                     L->ids, L->probs, L->shscale, L->logits, L->router_cm};
     const jx::DispatchOut dout{L->counts, L->offs,   L->act,   L->n_act, L->pair_tok,
                                L->pos_of,  L->tiles, L->n_tiles, L->slots};
     // few-token decode: logits on one block per router row, grouping in the GEMVs
@@ -415,16 +416,17 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
                                  st);
         }
     }
-    {
-        Launch l(L, mfma ? (L->down_f32 ? "down_gemv_f32" : "down_mfma") : (L->down_f32 ? "down_gemv_f32" : "down_gemv"),
-                 st);
-        if (mfma && !L->down_f32) {
+    if (mfma && !L->down_f32) {
+        {
+            Launch l(L, "h_to_matrix_form", st);
             jx::launch_q8_to_acth(L->hq, nk, L->hh.a, st, false);
-            jx::launch_mfma_down(L->down.m, L->hh.a, grp, tiles_ub, L->y, st);
         }
-        else
-            jx::launch_gemv_down(L->down.m, L->hq, L->down_f32 ? L->hf : nullptr, (int)fpad, grp, slots, mfma ? 4 : tb,
-                                 L->y, st);
+        Launch l(L, "down_mfma", st);
+        jx::launch_mfma_down(L->down.m, L->hh.a, grp, tiles_ub, L->y, st);
+    } else {
+        Launch l(L, L->down_f32 ? "down_gemv_f32" : "down_gemv", st);
+        jx::launch_gemv_down(L->down.m, L->hq, L->down_f32 ? L->hf : nullptr, (int)fpad, grp, slots, mfma ? 4 : tb,
+                             L->y, st);
     }
     {
         Launch l(L, "combine", st);
@@ -543,6 +545,16 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
             if (hipMemcpy(L->shgate, D->sh_gate_inp, d * 4, hipMemcpyHostToDevice) != hipSuccess)
                 return bail(fail(JX_ERR_HIP, "shared gate upload"));
         }
+    }
+    {  // chain-major router copy for the many-token router
+        const int R = L->E + (L->shgate ? 1 : 0);
+        std::vector<float> rows((size_t)R * d), cm((size_t)R * 16 * jx::chain_stride((int)d));
+        std::copy(D->router, D->router + E * d, rows.begin());
+        if (L->shgate) std::copy(D->sh_gate_inp, D->sh_gate_inp + d, rows.begin() + E * d);
+        jx::chain_rows(rows.data(), R, (int)d, cm.data());
+        if ((r = dalloc(L->router_cm, cm.size())) != JX_OK) return bail(r);
+        if (hipMemcpy(L->router_cm, cm.data(), cm.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+            return bail(fail(JX_ERR_HIP, "router upload"));
     }
     if ((r = ensure_workspace(L, 1)) != JX_OK) return bail(r);
     if (hipStreamCreate(&L->own) != hipSuccess) return bail(fail(JX_ERR_HIP, "stream create"));
