@@ -188,11 +188,6 @@ __device__ __forceinline__ void work_item(int L, int n_items, int R, int S, int 
     sub = ts - ti * S;
 }
 
-// Exponent of a half-unit from its largest block scale M: |dx * q| * 2^-E < 2^15.
-__device__ __forceinline__ int half_exp(float M) {
-    return (M > 0.0f) ? (int)((__float_as_uint(M) >> 23) & 0xFF) - 127 - 7 : 0;
-}
-
 // ---------------------------------------------------------------- weights
 // Raw weight bytes of one half-unit for lane (n, g) of one row tile: the lane
 // reads row n.  off() is the lane's byte offset of its row in the tile layout
