@@ -200,18 +200,29 @@ struct WRaw<T_Q4_K> {
     uint4 q[2];   // sub-block pairs 2s, 2s+1 of super-block h/2 (s = h&1), half g: elements
                   // 16g..16g+15 of sub-blocks 2p (low nibbles) and 2p+1 (high nibbles)
     uint4 hd;     // header of row n (d | dmin << 16, scales[12]); loaded with the even half
+    uint4 mn[3];  // min-term pieces of row n (hi, mid, lo; QMat::mn); loaded with the odd half
     __device__ static uint32_t qoff(const QMat& W, int rt, int n, int g) {
         return (uint32_t)((((size_t)rt * W.nkb * 8 + g) * 32 + n) * 16);
     }
     __device__ static uint32_t soff(const QMat& W, int rt, int n) {
         return (uint32_t)(((size_t)rt * W.nkb * 32 + n) * 16);
     }
-    __device__ void load(const uint8_t* qb, const uint8_t* sb, uint32_t qo, uint32_t so, int h, int nb) {
+    __device__ static uint32_t moff(const QMat& W, int rt, int n) {
+        return (uint32_t)(((size_t)rt * W.nkb * 96 + n) * 16);
+    }
+    __device__ void load(const uint8_t* qb, const uint8_t* sb, const uint8_t* mb, uint32_t qo, uint32_t so,
+                         uint32_t mo, int h, int nb) {
         (void)nb;
         const uint8_t* qh = qb + (size_t)(h >> 1) * 4096 + (h & 1) * 2048;
 #pragma unroll
         for (int p = 0; p < 2; ++p) q[p] = ld16(qh + p * 1024 + qo);
-        if (!(h & 1)) hd = ld16(sb + (size_t)(h >> 1) * 512 + so);
+        if (!(h & 1)) {
+            hd = ld16(sb + (size_t)(h >> 1) * 512 + so);
+        } else {
+            const uint8_t* mh = mb + (size_t)(h >> 1) * 1536 + mo;
+#pragma unroll
+            for (int c = 0; c < 3; ++c) mn[c] = ld16(mh + c * 512);
+        }
     }
 };
 
@@ -226,7 +237,9 @@ struct WRaw {  // Q4_0 / Q8_0: 16 bytes per 32-block, and row n's fp16 block sca
     __device__ static uint32_t soff(const QMat& W, int rt, int n) {
         return (uint32_t)(((size_t)rt * W.nkb * 32 + n) * 2);
     }
-    __device__ void load(const uint8_t* qb, const uint8_t* sb, uint32_t qo, uint32_t so, int h, int nb) {
+    __device__ static uint32_t moff(const QMat&, int, int) { return 0; }
+    __device__ void load(const uint8_t* qb, const uint8_t* sb, const uint8_t*, uint32_t qo, uint32_t so, uint32_t,
+                         int h, int nb) {
         constexpr int QB = TYPE == T_Q4_0 ? 512 : 1024;  // bytes per 32-block of a row tile
 #pragma unroll
         for (int j = 0; j < HB; ++j) {
@@ -337,15 +350,18 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
     // a valid one; their results are dropped)
     const uint8_t* qbase[TM];
     const uint8_t* sbase[TM];
-    uint32_t qo[TM], so[TM];
+    const uint8_t* mbase[TM];
+    uint32_t qo[TM], so[TM], mo[TM];
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         const QMat& W = (GATEUP && i == 1) ? W1 : W0;
         qbase[i] = W.qs + (size_t)e * W.qs_es;
         sbase[i] = W.sc + (size_t)e * W.sc_es;
+        mbase[i] = Q4K ? W.mn + (size_t)e * W.mn_es : nullptr;
         const int rt = min(GATEUP ? rt0 : rt0 + i, W.nrt - 1);
         qo[i] = WRaw<TYPE>::qoff(W, rt, n, g);
         so[i] = WRaw<TYPE>::soff(W, rt, n);
+        mo[i] = WRaw<TYPE>::moff(W, rt, n);
     }
 
     v16f acc[TM][TN];
@@ -358,18 +374,16 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
     WRaw<TYPE> wa[TM], wb[TM];
     uint4 hdr[TM];  // Q4_K headers of the current super-block
     float dl[TM];   // Q4_K d of the lane's row (RESCALE: the unit acc is kept in)
-    float iu[TM];   // RESCALE: 1 / unit
-    bool dz[TM];    // RESCALE: this super-block's d is zero (its sc * q terms vanish)
+    bool dz[TM];    // RESCALE: this super-block's d is zero (its sc * q terms vanish, unit 1)
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         hdr[i] = make_uint4(0, 0, 0, 0);
         dl[i] = RESCALE ? 1.0f : 0.0f;
-        iu[i] = 1.0f;
         dz[i] = false;
     }
     if (active)
 #pragma unroll
-        for (int i = 0; i < TM; ++i) wa[i].load(qbase[i], sbase[i], qo[i], so[i], 0, min(HB, KB));
+        for (int i = 0; i < TM; ++i) wa[i].load(qbase[i], sbase[i], mbase[i], qo[i], so[i], mo[i], 0, min(HB, KB));
     stage(0);
 
     // LDS byte offset of this lane's A chunk (hi/lo hl, sub-block j of the half-unit, K-half m) in pair tile 0
@@ -384,7 +398,8 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
             if (active)
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
-                    nxt[i].load(qbase[i], sbase[i], qo[i], so[i], h + 1, min(HB, KB - (h + 1) * HB));
+                    nxt[i].load(qbase[i], sbase[i], mbase[i], qo[i], so[i], mo[i], h + 1,
+                                min(HB, KB - (h + 1) * HB));
         }
         if (!active) return;
         const uint8_t* sa = sm.st[ODD].q + pg * TN * 32 * PB;
@@ -396,11 +411,9 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
                     const float d = f16_to_f32(hdr[i].x & 0xFFFFu);
                     if constexpr (RESCALE) {
                         dz[i] = d == 0.0f;
-                        const float u = dz[i] ? dl[i] : d;
-                        const float r = __builtin_amdgcn_rcpf(u);  // ~1 ulp; the units only need to be consistent
-                        const float ratio = dl[i] * r;
+                        const float u = dz[i] ? 1.0f : d;  // the unit the min table divides by
+                        const float ratio = dl[i] * __builtin_amdgcn_rcpf(u);  // ~1 ulp
                         dl[i] = u;
-                        iu[i] = r;
 #pragma unroll
                         for (int t = 0; t < TN; ++t)
 #pragma unroll
@@ -410,26 +423,16 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
                     }
                 }
             } else {
-                // min term, once per super-block: acc += sum_j (dx_j sum q_j) (-dmin m_j) on bf16
-                // 3-piece splits; six of the nine piece products (all above 2^-24 relative) in
-                // three MFMAs, (MFMA, lane half) -> (activation piece, weight piece):
-                // (0,0) h.h (0,1) m.h (1,0) h.m (1,1) l.h (2,0) h.l (2,1) m.m
+                // min term, once per super-block: acc += sum_j (dx_j sum q_j) (-dmin m_j / unit) on bf16
+                // 3-piece splits (the activation side in xm, the weight side from the min table); six of
+                // the nine piece products (all above 2^-24 relative) in three MFMAs, (MFMA, lane half) ->
+                // (activation piece, weight piece): (0,0) h.h (0,1) m.h (1,0) h.m (1,1) l.h (2,0) h.l (2,1) m.m
                 const uint16_t* xm = sm.st[1].xm + pbase * 8;
 #pragma unroll
                 for (int i = 0; i < TM; ++i) {
-                    // RESCALE: in units of dl (rounded to fp32 once, then split exactly)
-                    const float dmin = f16_to_f32(hdr[i].x >> 16) * (RESCALE ? iu[i] : 1.0f);
-                    b8 wm[3];
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        int sc, mn;
-                        hdr_scale_min(hdr[i], j, sc, mn);
-                        uint16_t vh, vm, vl;
-                        split3(-dmin * (float)mn, vh, vm, vl);  // exact: 11-bit x 6-bit (RESCALE: 24-bit)
-                        wm[0][j] = __builtin_bit_cast(__bf16, vh);
-                        wm[1][j] = __builtin_bit_cast(__bf16, g ? vh : vm);
-                        wm[2][j] = __builtin_bit_cast(__bf16, g ? vm : vl);
-                    }
+                    const uint4 w1 = g ? cur[i].mn[0] : cur[i].mn[1], w2 = g ? cur[i].mn[1] : cur[i].mn[2];
+                    const b8 wm[3] = {__builtin_bit_cast(b8, cur[i].mn[0]), __builtin_bit_cast(b8, w1),
+                                      __builtin_bit_cast(b8, w2)};
 #pragma unroll
                     for (int t = 0; t < TN; ++t) {
                         const int pr = 32 * t + n;
@@ -649,6 +652,42 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
                 }
         }
     }
+}
+
+// Min-term table of a repacked Q4_K matrix, one thread per (expert, row tile,
+// super-block, row): the bf16 pieces of -dmin * m_j / u (u = d, 1 where d is
+// zero) for the 8 sub-blocks, in the unit the GEMM's accumulator uses for that
+// super-block.  -dmin * m_j is exact in fp32 (11-bit x 6-bit); the division
+// rounds once; the split is exact.
+__global__ void __launch_bounds__(256) k_min_table(QMat m, uint8_t* mn) {
+    const size_t n = (size_t)m.n_mats * m.nrt * m.nkb * 32;
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= n) return;
+    const size_t t = idx / 32, row = idx % 32;  // t = (e * nrt + rt) * nkb + super-block
+    const uint4 hd = ld16(m.sc + (t * 32 + row) * 16);
+    const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
+    const float u = d == 0.0f ? 1.0f : d;
+    uint32_t pw[3][4];
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+        uint16_t p[3][2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            int sc, mv;
+            hdr_scale_min(hd, j + k, sc, mv);
+            split3((-dmin * (float)mv) / u, p[0][k], p[1][k], p[2][k]);
+        }
+#pragma unroll
+        for (int c = 0; c < 3; ++c) pw[c][j / 2] = (uint32_t)p[c][0] | ((uint32_t)p[c][1] << 16);
+    }
+#pragma unroll
+    for (int c = 0; c < 3; ++c)
+        *reinterpret_cast<uint4*>(mn + ((t * 3 + c) * 32 + row) * 16) = make_uint4(pw[c][0], pw[c][1], pw[c][2], pw[c][3]);
+}
+
+void launch_min_table(const QMat& m, uint8_t* mn, hipStream_t st) {
+    const size_t n = (size_t)m.n_mats * m.nrt * m.nkb * 32;
+    hipLaunchKernelGGL(k_min_table, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, m, mn);
 }
 
 // Workgroup shape: waves, row tiles and pair tiles per wave, pairs per

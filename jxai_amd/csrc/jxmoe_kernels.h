@@ -29,6 +29,12 @@ struct QMat {
     // issues for units it will not use read here (uniform instruction streams).
     const uint8_t* pad_qs = nullptr;
     const uint8_t* pad_sc = nullptr;
+    // Q4_K min-term table for the matrix-core GEMMs (launch_min_table; null for
+    // other types and for matrices only the GEMVs read): per (expert, row tile,
+    // super-block) 3 x [32 rows][16 B] = the bf16 pieces (hi, mid, lo) of
+    // -dmin * m_j / u for the 8 sub-blocks j, u = d (1 where d is zero).
+    const uint8_t* mn = nullptr;
+    size_t mn_es = 0;  // per-expert stride (bytes)
 };
 constexpr size_t QMAT_PAD = 8192;
 
@@ -147,6 +153,8 @@ void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_l
 void launch_mfma_gateup(const QMat& g, const QMat& u, const ActH& xin, const Groups& grp, int tiles_ub,
                         const ActQ8& hq, float* hf, hipStream_t st);
 void launch_mfma_down(const QMat& dn, const ActH& hin, const Groups& grp, int tiles_ub, float* y, hipStream_t st);
+// Fill m.mn (m.n_mats * m.nrt * m.nkb * 1536 bytes) from a repacked Q4_K matrix.
+void launch_min_table(const QMat& m, uint8_t* mn, hipStream_t st);
 
 // out[t] = sum_s p[t][s] * y[pos(t,s)] (+ shscale[t] * ysh[t]), fma in selection order.
 void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,

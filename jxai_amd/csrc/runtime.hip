@@ -56,15 +56,20 @@ struct DevMat {
     jx::QMat m;
     uint8_t* qs = nullptr;
     uint8_t* sc = nullptr;
+    uint8_t* mn = nullptr;  // Q4_K min-term table (matrix-core GEMMs)
     void release() {
         if (qs) (void)hipFree(qs);
         if (sc) (void)hipFree(sc);
-        qs = sc = nullptr;
+        if (mn) (void)hipFree(mn);
+        qs = sc = mn = nullptr;
     }
 };
 
-// Upload n_mats [rows][cols] block matrices and repack them on the device.
-int upload_matrix(int type, int n_mats, int rows, int cols, const void* host, DevMat& out, hipStream_t st) {
+// Upload n_mats [rows][cols] block matrices and repack them on the device;
+// with `gemm`, Q4_K matrices of whole super-blocks also get the matrix-core
+// GEMMs' min-term table.
+int upload_matrix(int type, int n_mats, int rows, int cols, const void* host, DevMat& out, hipStream_t st,
+                  bool gemm = false) {
     if (!expert_type_ok(type)) return fail(JX_ERR_UNSUPPORTED, "expert weight type must be Q4_0, Q8_0 or Q4_K");
     if (rows % jx::ROWS_PER_TILE != 0) return fail(JX_ERR_UNSUPPORTED, "matrix rows must be a multiple of 32");
     if (cols % 32 != 0) return fail(JX_ERR_UNSUPPORTED, "matrix cols must be a multiple of 32");
@@ -95,6 +100,15 @@ int upload_matrix(int type, int n_mats, int rows, int cols, const void* host, De
         m.sc = out.sc;
         jx::launch_repack(raw, m, out.qs, out.sc, st);
         e = hipGetLastError();
+    }
+    if (e == hipSuccess && gemm && type == jx::T_Q4_K && cols % 256 == 0) {
+        m.mn_es = (size_t)m.nrt * m.nkb * 1536;
+        e = hipMalloc(&out.mn, m.mn_es * n_mats);
+        if (e == hipSuccess) {
+            m.mn = out.mn;
+            jx::launch_min_table(m, out.mn, st);
+            e = hipGetLastError();
+        }
     }
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     (void)hipFree(raw);
@@ -319,11 +333,14 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     bool mfma = (size_t)nk >= (size_t)MFMA_MIN_PAIRS_PER_EXPERT * E;
     if (flags & JX_FWD_FORCE_GEMV) mfma = false;
     if (flags & JX_FWD_FORCE_MFMA) mfma = true;
-    // the matrix-core GEMMs stage K in 128-element half-units
-    const bool mfma_shape = d % 128 == 0 && (L->down_f32 || L->F % 128 == 0);
+    // the matrix-core GEMMs stage K in 128-element half-units; their Q4_K matrices carry the min table
+    auto ready = [](const DevMat& M) { return M.m.type != jx::T_Q4_K || M.m.mn != nullptr; };
+    const bool mfma_shape = d % 128 == 0 && (L->down_f32 || L->F % 128 == 0) && ready(L->gate) && ready(L->up) &&
+                            (L->down_f32 || ready(L->down));
     mfma = mfma && mfma_shape;
     const bool smfma = L->shared && n >= jx::MFMA_MIN_SHARED_TOKENS && !(flags & JX_FWD_FORCE_GEMV) && d % 128 == 0 &&
-                       (L->sdown_f32 || L->Fs % 128 == 0);
+                       (L->sdown_f32 || L->Fs % 128 == 0) && ready(L->sgate) && ready(L->sup) &&
+                       (L->sdown_f32 || ready(L->sdown));
     jx::RouteArgs ra{xdev, n, d, E, k, L->router, L->bias, L->shgate, L->xq, (mfma || smfma) ? L->xh.a : jx::ActH{},
                      L->ids, L->probs, L->shscale, L->logits, L->router_cm};
     const jx::DispatchOut dout{L->counts, L->offs,   L->act,   L->n_act, L->pair_tok,
@@ -533,13 +550,13 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
         if (hipMemcpy(L->bias, D->router_bias, E * 4, hipMemcpyHostToDevice) != hipSuccess)
             return bail(fail(JX_ERR_HIP, "router bias upload"));
     }
-    if ((r = upload_matrix(D->gate_type, L->E, L->F, L->d, D->gate_exps, L->gate, st)) != JX_OK) return bail(r);
-    if ((r = upload_matrix(D->up_type, L->E, L->F, L->d, D->up_exps, L->up, st)) != JX_OK) return bail(r);
-    if ((r = upload_matrix(D->down_type, L->E, L->d, L->F, D->down_exps, L->down, st)) != JX_OK) return bail(r);
+    if ((r = upload_matrix(D->gate_type, L->E, L->F, L->d, D->gate_exps, L->gate, st, true)) != JX_OK) return bail(r);
+    if ((r = upload_matrix(D->up_type, L->E, L->F, L->d, D->up_exps, L->up, st, true)) != JX_OK) return bail(r);
+    if ((r = upload_matrix(D->down_type, L->E, L->d, L->F, D->down_exps, L->down, st, true)) != JX_OK) return bail(r);
     if (L->shared) {
-        if ((r = upload_matrix(D->sh_gate_type, 1, L->Fs, L->d, D->sh_gate, L->sgate, st)) != JX_OK) return bail(r);
-        if ((r = upload_matrix(D->sh_up_type, 1, L->Fs, L->d, D->sh_up, L->sup, st)) != JX_OK) return bail(r);
-        if ((r = upload_matrix(D->sh_down_type, 1, L->d, L->Fs, D->sh_down, L->sdown, st)) != JX_OK) return bail(r);
+        if ((r = upload_matrix(D->sh_gate_type, 1, L->Fs, L->d, D->sh_gate, L->sgate, st, true)) != JX_OK) return bail(r);
+        if ((r = upload_matrix(D->sh_up_type, 1, L->Fs, L->d, D->sh_up, L->sup, st, true)) != JX_OK) return bail(r);
+        if ((r = upload_matrix(D->sh_down_type, 1, L->d, L->Fs, D->sh_down, L->sdown, st, true)) != JX_OK) return bail(r);
         if (D->sh_gate_inp) {
             if ((r = dalloc(L->shgate, d)) != JX_OK) return bail(r);
             if (hipMemcpy(L->shgate, D->sh_gate_inp, d * 4, hipMemcpyHostToDevice) != hipSuccess)
