@@ -182,6 +182,8 @@ void launch_quantize_q8(const float* x, int rows, int K, ActQ8 out, hipStream_t 
 // Matrix-core form of existing Q8_0 activations (int8 quants + (scale, sum)).
 // lo = false writes only the fp16 hi halves (the down GEMM's operand).
 void launch_q8_to_acth(const ActQ8& in, int rows, ActH out, hipStream_t st, bool lo = true);
+// Matrix-core form (hi only) of fp32 activation rows [rows][ld], ld = out.K % 256 == 0, zero-padded.
+void launch_f32_to_acth(const float* h, int ld, int rows, ActH out, hipStream_t st);
 
 // Repack a GGUF block matrix set [n_mats][rows][cols] (already on the device
 // as raw bytes) into the QMat layout.

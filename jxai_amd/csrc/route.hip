@@ -353,6 +353,66 @@ void launch_q8_to_acth(const ActQ8& in, int rows, ActH out, hipStream_t st, bool
     hipLaunchKernelGGL(k_q8_to_acth, dim3(rows), dim3(256), 0, st, in, out, lo ? 1 : 0);
 }
 
+// Matrix-core form (fp16 hi only) of fp32 activation rows h [rows][ld], ld =
+// out.K a multiple of 256 with zero padding past the real columns (the
+// reference's fp32-activation products, vec_dot_q4_K_f32, src/quant.cpp:2910-3013,
+// for a down projection whose K is not a multiple of 256).  One block per
+// row: E = exponent(max |h|) - 14 so every h * 2^-E is below 2^15; hi =
+// fp16(h * 2^-E) (relative error <= 2^-12 per value, as the Q8_0 down operand);
+// the min-term value of each 32-block is its fp32 sum times 2^-E, split into
+// three exact bf16 pieces.
+__global__ void __launch_bounds__(256) k_f32_to_acth(const float* h, int ld, ActH o) {
+    __shared__ float wmax[4];
+    const size_t row = blockIdx.x;
+    const int tid = threadIdx.x, K = o.K, KH = K / 128;
+    const float* hr = h + row * (size_t)ld;
+    float M = 0.0f;
+    for (int i = tid; i < K / 4; i += 256) {
+        const float4 v = *reinterpret_cast<const float4*>(hr + 4 * i);
+        M = fmaxf(M, fmaxf(fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)), fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w))));
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    if ((tid & 63) == 0) wmax[tid >> 6] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const int E = (M > 0.0f) ? (int)((__float_as_uint(M) >> 23) & 0xFF) - 127 - 14 : 0;
+    const float dn = __uint_as_float((uint32_t)(127 - E) << 23), up = __uint_as_float((uint32_t)(127 + E) << 23);
+    // eight consecutive values per thread; the four threads of a 32-block are consecutive lanes
+    for (int c = tid; c < K / 8; c += 256) {
+        const int i = 8 * c, b = i >> 5, hh = i >> 7;
+        const float4 v0 = *reinterpret_cast<const float4*>(hr + i), v1 = *reinterpret_cast<const float4*>(hr + i + 4);
+        const float f[8] = {v0.x * dn, v0.y * dn, v0.z * dn, v0.w * dn, v1.x * dn, v1.y * dn, v1.z * dn, v1.w * dn};
+        uint32_t hw[4];
+        float sum = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const _Float16 h0 = (_Float16)f[2 * u], h1 = (_Float16)f[2 * u + 1];
+            hw[u] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+            sum += f[2 * u] + f[2 * u + 1];
+        }
+        uint16_t* hl = o.hl + row * (size_t)KH * 256 + hh * 256 + (i & 127);
+        *reinterpret_cast<uint4*>(hl) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        if ((i & 127) == 0) o.pe[row * (size_t)KH + hh] = up;
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        if ((i & 31) == 0) {
+            const uint32_t bh = __float_as_uint(sum) & 0xFFFF0000u;
+            const float r1 = sum - __uint_as_float(bh);
+            const uint32_t bm = __float_as_uint(r1) & 0xFFFF0000u;
+            const float r2 = r1 - __uint_as_float(bm);
+            uint16_t* xm = o.xm + row * (size_t)o.KU * 24 + (b / 8) * 24 + (b % 8);
+            xm[0] = (uint16_t)(bh >> 16);
+            xm[8] = (uint16_t)(bm >> 16);
+            xm[16] = (uint16_t)(__float_as_uint(r2) >> 16);
+        }
+    }
+}
+
+void launch_f32_to_acth(const float* h, int ld, int rows, ActH out, hipStream_t st) {
+    hipLaunchKernelGGL(k_f32_to_acth, dim3(rows), dim3(256), 0, st, h, ld, out);
+}
+
 // ---------------------------------------------------------------- few tokens
 // Decode routing: a one-block-per-token kernel would serialise every router
 // row behind one CU's load latency.  Here block r owns router row r (expert r,

@@ -66,8 +66,7 @@ struct DevMat {
 };
 
 // Upload n_mats [rows][cols] block matrices and repack them on the device;
-// with `gemm`, Q4_K matrices of whole super-blocks also get the matrix-core
-// GEMMs' min-term table.
+// with `gemm`, Q4_K matrices also get the matrix-core GEMMs' min-term table.
 int upload_matrix(int type, int n_mats, int rows, int cols, const void* host, DevMat& out, hipStream_t st,
                   bool gemm = false) {
     if (!expert_type_ok(type)) return fail(JX_ERR_UNSUPPORTED, "expert weight type must be Q4_0, Q8_0 or Q4_K");
@@ -101,7 +100,7 @@ int upload_matrix(int type, int n_mats, int rows, int cols, const void* host, De
         jx::launch_repack(raw, m, out.qs, out.sc, st);
         e = hipGetLastError();
     }
-    if (e == hipSuccess && gemm && type == jx::T_Q4_K && cols % 256 == 0) {
+    if (e == hipSuccess && gemm && type == jx::T_Q4_K) {
         m.mn_es = (size_t)m.nrt * m.nkb * 1536;
         e = hipMalloc(&out.mn, m.mn_es * n_mats);
         if (e == hipSuccess) {
@@ -231,11 +230,14 @@ int ensure_workspace(jx_moe_layer* L, int n) {
     WS(L->n_tiles, 1);
     WS(L->tiles, nk / jx::MFMA_BN + std::min<size_t>(L->E, nk) + 1);
     WS(L->slots, L->E);
-    if ((r = L->xh.alloc((size_t)cap, L->d)) != JX_OK || (r = L->hh.alloc(nk, L->F)) != JX_OK) {
+    // h's matrix-core form: K = d_ff, or d_ff padded to whole super-blocks for fp32 h
+    const int hK = L->down_f32 ? (L->F + 255) / 256 * 256 : L->F;
+    const int hKs = L->sdown_f32 ? (L->Fs + 255) / 256 * 256 : L->Fs;
+    if ((r = L->xh.alloc((size_t)cap, L->d)) != JX_OK || (r = L->hh.alloc(nk, hK)) != JX_OK) {
         L->cap = 0;
         return r;
     }
-    if (L->shared && (r = L->hhs.alloc((size_t)cap, L->Fs)) != JX_OK) {
+    if (L->shared && (r = L->hhs.alloc((size_t)cap, hKs)) != JX_OK) {
         L->cap = 0;
         return r;
     }
@@ -336,11 +338,10 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     // the matrix-core GEMMs stage K in 128-element half-units; their Q4_K matrices carry the min table
     auto ready = [](const DevMat& M) { return M.m.type != jx::T_Q4_K || M.m.mn != nullptr; };
     const bool mfma_shape = d % 128 == 0 && (L->down_f32 || L->F % 128 == 0) && ready(L->gate) && ready(L->up) &&
-                            (L->down_f32 || ready(L->down));
+                            ready(L->down);
     mfma = mfma && mfma_shape;
     const bool smfma = L->shared && n >= jx::MFMA_MIN_SHARED_TOKENS && !(flags & JX_FWD_FORCE_GEMV) && d % 128 == 0 &&
-                       (L->sdown_f32 || L->Fs % 128 == 0) && ready(L->sgate) && ready(L->sup) &&
-                       (L->sdown_f32 || ready(L->sdown));
+                       (L->sdown_f32 || L->Fs % 128 == 0) && ready(L->sgate) && ready(L->sup) && ready(L->sdown);
     jx::RouteArgs ra{xdev, n, d, E, k, L->router, L->bias, L->shgate, L->xq, (mfma || smfma) ? L->xh.a : jx::ActH{},
                      L->ids, L->probs, L->shscale, L->logits, L->router_cm};
     const jx::DispatchOut dout{L->counts, L->offs,   L->act,   L->n_act, L->pair_tok,
@@ -417,11 +418,10 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
             }
             Launch l(L, "shared_down", st);
             if (L->sdown_f32)
-                jx::launch_gemv_down(L->sdown.m, L->hqs, L->hfs, (int)fspad, sg, 1, 4, L->ysh, st);
-            else {
+                jx::launch_f32_to_acth(L->hfs, (int)fspad, n, L->hhs.a, st);
+            else
                 jx::launch_q8_to_acth(L->hqs, n, L->hhs.a, st, false);
-                jx::launch_mfma_down(L->sdown.m, L->hhs.a, sg, st_ub, L->ysh, st);
-            }
+            jx::launch_mfma_down(L->sdown.m, L->hhs.a, sg, st_ub, L->ysh, st);
         } else {
             {
                 Launch l(L, "shared_gateup_gemv", st);
@@ -433,10 +433,17 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
                                  st);
         }
     }
-    if (mfma && !L->down_f32) {
+    // fp32 h (Q4_K down with d_ff % 256 != 0) takes the matrix-core down GEMM whenever the dispatch
+    // tables hold MFMA tiles (every path but the few-token one): the GEMV re-streams the weights per
+    // group of 4 tokens and works in fp32
+    const bool mfma_down = mfma || (L->down_f32 && !small_logits && mfma_shape);
+    if (mfma_down) {
         {
             Launch l(L, "h_to_matrix_form", st);
-            jx::launch_q8_to_acth(L->hq, nk, L->hh.a, st, false);
+            if (L->down_f32)
+                jx::launch_f32_to_acth(L->hf, (int)fpad, nk, L->hh.a, st);
+            else
+                jx::launch_q8_to_acth(L->hq, nk, L->hh.a, st, false);
         }
         Launch l(L, "down_mfma", st);
         jx::launch_mfma_down(L->down.m, L->hh.a, grp, tiles_ub, L->y, st);
