@@ -121,10 +121,11 @@ void chain_rows(const float* rows, int nrows, int d, float* out) {
         for (int e = 0; e < d; ++e) out[(size_t)r * 16 * S + (e & 15) * S + (e >> 4)] = rows[(size_t)r * d + e];
 }
 
-// Routing for many tokens, RT_TMAX (or fewer, when d is large) per block of
-// RT_THREADS:
+// Routing for many tokens.  A block takes T tokens (T <= RT_TMAX, fewer when
+// d is large or n small) and a split of the router rows (RPB rows; a single
+// split when the rows fit one block's 16 lane groups):
 //  1. the block's token rows -> LDS, chain-major.
-//  2. Q8_0 of x, one thread per 32-block (quantize_row_q8_0,
+//  2. (row split 0) Q8_0 of x, one thread per 32-block (quantize_row_q8_0,
 //     src/quant.cpp:1029-1045): amax, d = amax/127 (IEEE division), id = 1/d,
 //     q = clamp(round-half-away(x*id)), stored scale = truncated fp16 of d; the
 //     block sum of q rides along for the Q4_0 (-8 offset) and Q4_K (min)
@@ -137,42 +138,65 @@ void chain_rows(const float* rows, int nrows, int d, float* out) {
 //     whose chains are independent.  The shared-expert gate vector
 //     (transformer.cpp:2748-2751) is one more row.
 //  4. Top-k by rank counting (descending logit, ties by index) and softmax over
-//     the k selected logits (select_experts_cache_aware, src/tier.cpp:144-188).
+//     the k selected logits (select_experts_cache_aware, src/tier.cpp:144-188):
+//     in the block with a single row split, else in k_route_topk once every
+//     split has written its logits.
 #ifndef JX_RT_TMAX
-#define JX_RT_TMAX 2
+#define JX_RT_TMAX 4
 #endif
 #ifndef JX_RT_LDS_KB
 #define JX_RT_LDS_KB 80
 #endif
+#ifndef JX_RT_UNROLL
+#define JX_RT_UNROLL 4
+#endif
 constexpr int RT_THREADS = 256;
+constexpr int RT_GROUPS = RT_THREADS / 16;  // router rows in flight per block
+constexpr int RT_UNROLL = JX_RT_UNROLL;     // router loads in flight per lane (four chain steps each)
 constexpr int RT_TMAX = JX_RT_TMAX;
-constexpr size_t RT_LDS_TARGET = JX_RT_LDS_KB * 1024;
+constexpr size_t RT_LDS_TARGET = JX_RT_LDS_KB * 1024;  // two blocks per CU
 
 static size_t route_lds(int T, int d, int E) {
     return (size_t)T * 16 * rs_stride(d) * sizeof(float) + (size_t)T * d + (size_t)T * (d / 32) * sizeof(float2) +
            (size_t)T * E * sizeof(float);
 }
 
-static int route_tokens_per_block(int d, int E) {
-    for (int T = RT_TMAX; T > 1; --T)
-        if (route_lds(T, d, E) <= RT_LDS_TARGET) return T;
-    return 1;
+struct RouteShape {
+    int T, RS, RPB;
+};
+
+// Rows R = E (+1 shared gate): up to 16 rows one split (fused top-k), more in
+// splits of 16.  Tokens per block: a fused Mixtral-sized router measured best
+// at 2, split routers (61 and 128 rows, d 2048) at 4 (1, 2 and 6-8 slower);
+// small batches take one token per block for parallelism.
+static RouteShape route_shape(const RouteArgs& a) {
+    const int R = a.E + (a.shgate ? 1 : 0);
+    RouteShape r;
+    r.RS = R <= RT_GROUPS ? 1 : (R + RT_GROUPS - 1) / RT_GROUPS;
+    r.RPB = r.RS == 1 ? R : RT_GROUPS;
+    int T = r.RS == 1 ? 2 : RT_TMAX;
+    if (a.n < 64 * T) T = std::max(1, a.n / 64);
+    while (T > 1 && route_lds(T, a.d, a.E) > RT_LDS_TARGET) --T;
+    r.T = T;
+    return r;
 }
 
-__global__ void __launch_bounds__(RT_THREADS) k_route(RouteArgs a, int T) {
+template <int T>
+__global__ void __launch_bounds__(RT_THREADS) k_route(RouteArgs a, int nsplit, int rpb) {
     extern __shared__ __align__(16) float lds[];
-    __shared__ int sel[RT_TMAX][MAX_K];
-    __shared__ float shl[RT_TMAX];
-    __shared__ float rmax[RT_TMAX];
+    __shared__ int sel[T][MAX_K];
+    __shared__ float shl[T];
+    __shared__ float rmax[T];
     const int d = a.d, E = a.E, S = rs_stride(d), RS = 16 * S, KB = d / 32;
-    const int t0 = blockIdx.x * T, nt = min(T, a.n - t0);
+    const int split = blockIdx.x % nsplit;
+    const int t0 = (blockIdx.x / nsplit) * T, nt = min(T, a.n - t0);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float* xs = lds;                                       // [T][16][S] chain-major rows
     int8_t* qs = reinterpret_cast<int8_t*>(xs + T * RS);   // [T][d] quants
     float2* ss = reinterpret_cast<float2*>(qs + T * d);    // [T][KB] (scale, sum)
     float* lg = reinterpret_cast<float*>(ss + T * KB);     // [T][E] logits
     // every selection slot holds a valid expert even if NaN logits break the ranking
-    if (tid < RT_TMAX * MAX_K) sel[tid / MAX_K][tid % MAX_K] = tid % MAX_K;
+    for (int i = tid; i < T * MAX_K; i += RT_THREADS) sel[i / MAX_K][i % MAX_K] = i % MAX_K;
 
     // -- 1. rows -> LDS, four loads in flight per thread before their stores
     {
@@ -199,93 +223,97 @@ __global__ void __launch_bounds__(RT_THREADS) k_route(RouteArgs a, int T) {
     }
     __syncthreads();
 
-    // -- 2. Q8_0 of x: one thread per 32-block (its max and integer sum are order-free)
-    for (int i = tid; i < nt * KB; i += RT_THREADS) {
-        const int t = i / KB, b = i - t * KB;
-        const float* xr = xs + t * RS + 2 * b;  // element 32b + u at (u % 16) * S + 2b + u / 16
-        float v[32];
+    if (split == 0) {  // block-uniform
+        // -- 2. Q8_0 of x: one thread per 32-block (its max and integer sum are order-free)
+        for (int i = tid; i < nt * KB; i += RT_THREADS) {
+            const int t = i / KB, b = i - t * KB;
+            const float* xr = xs + t * RS + 2 * b;  // element 32b + u at (u % 16) * S + 2b + u / 16
+            float v[32];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const float2 p = *reinterpret_cast<const float2*>(xr + u * S);
-            v[u] = p.x;
-            v[16 + u] = p.y;
-        }
-        float amax = 0.0f;
+            for (int u = 0; u < 16; ++u) {
+                const float2 p = *reinterpret_cast<const float2*>(xr + u * S);
+                v[u] = p.x;
+                v[16 + u] = p.y;
+            }
+            float amax = 0.0f;
 #pragma unroll
-        for (int u = 0; u < 32; ++u) amax = fmaxf(amax, __builtin_fabsf(v[u]));
-        const float dd = amax / 127.0f;
-        const float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
-        int sum = 0;
-        uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int u = 0; u < 32; ++u) amax = fmaxf(amax, __builtin_fabsf(v[u]));
+            const float dd = amax / 127.0f;
+            const float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
+            int sum = 0;
+            uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-        for (int u = 0; u < 32; ++u) {
-            float r = round_away(v[u] * id);
-            r = fminf(fmaxf(r, -127.0f), 127.0f);
-            const int q = (int)r;
-            sum += q;
-            w[u >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (u & 3));
-        }
-        const float2 sv = make_float2(f16_to_f32(f32_to_f16_trunc(dd)), (float)sum);
-        const uint4 w0 = make_uint4(w[0], w[1], w[2], w[3]), w1 = make_uint4(w[4], w[5], w[6], w[7]);
-        uint4* gq = reinterpret_cast<uint4*>(a.xq.q + (size_t)(t0 + t) * a.xq.K + 32 * b);
-        gq[0] = w0;
-        gq[1] = w1;
-        a.xq.s[(size_t)(t0 + t) * KB + b] = sv;
-        uint4* lq = reinterpret_cast<uint4*>(qs + t * d + 32 * b);
-        lq[0] = w0;
-        lq[1] = w1;
-        ss[t * KB + b] = sv;
-    }
-    __syncthreads();
-    if (a.xh.hl) {  // matrix-core form: one exponent per row from its largest block scale
-        if (wave < nt) {
-            float M = 0.0f;
-            for (int b = lane; b < KB; b += 64) M = fmaxf(M, ss[wave * KB + b].x);
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-            if (lane == 0) rmax[wave] = M;
+            for (int u = 0; u < 32; ++u) {
+                float r = round_away(v[u] * id);
+                r = fminf(fmaxf(r, -127.0f), 127.0f);
+                const int q = (int)r;
+                sum += q;
+                w[u >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (u & 3));
+            }
+            const float2 sv = make_float2(f16_to_f32(f32_to_f16_trunc(dd)), (float)sum);
+            const uint4 w0 = make_uint4(w[0], w[1], w[2], w[3]), w1 = make_uint4(w[4], w[5], w[6], w[7]);
+            uint4* gq = reinterpret_cast<uint4*>(a.xq.q + (size_t)(t0 + t) * a.xq.K + 32 * b);
+            gq[0] = w0;
+            gq[1] = w1;
+            a.xq.s[(size_t)(t0 + t) * KB + b] = sv;
+            uint4* lq = reinterpret_cast<uint4*>(qs + t * d + 32 * b);
+            lq[0] = w0;
+            lq[1] = w1;
+            ss[t * KB + b] = sv;
         }
         __syncthreads();
-        const int cpr = d / 8;
-        for (int c = tid; c < nt * cpr; c += RT_THREADS) {
-            const int t = c / cpr;
-            acth_chunk(qs + t * d, ss + t * KB, d, a.xh, (size_t)(t0 + t), c - t * cpr, acth_exponent(rmax[t]), true);
+        if (a.xh.hl) {  // matrix-core form: one exponent per row from its largest block scale
+            for (int t = wave; t < nt; t += RT_THREADS / 64) {
+                float M = 0.0f;
+                for (int b = lane; b < KB; b += 64) M = fmaxf(M, ss[t * KB + b].x);
+#pragma unroll
+                for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+                if (lane == 0) rmax[t] = M;
+            }
+            __syncthreads();
+            const int cpr = d / 8;
+            for (int c = tid; c < nt * cpr; c += RT_THREADS) {
+                const int t = c / cpr;
+                acth_chunk(qs + t * d, ss + t * KB, d, a.xh, (size_t)(t0 + t), c - t * cpr, acth_exponent(rmax[t]), true);
+            }
         }
     }
 
-    // -- 3. router chains, exact vec_dot_f32 order
+    // -- 3. router chains of this split's rows, exact vec_dot_f32 order
     {
         const int grp = tid >> 4, j = tid & 15;
         const int R = E + (a.shgate ? 1 : 0);
+        const int r1 = min(R, (split + 1) * rpb);
         const int m = d / 16, m4 = m & ~3, Sg = chain_stride_of(d);
-        for (int r = grp; r < R; r += RT_THREADS / 16) {
+        for (int r = split * rpb + grp; r < r1; r += RT_GROUPS) {
             const float* wr = a.router_cm + (size_t)r * 16 * Sg + j * Sg;
-            const float* xr = xs + j * S;
-            float acc[RT_TMAX];
+            // token rows of the chains: tokens past nt (last block) repeat the last one, results dropped,
+            // so the loop has no branches and the router loads can run ahead
+            const float* xr[T];
 #pragma unroll
-            for (int t = 0; t < RT_TMAX; ++t) acc[t] = 0.0f;
-#pragma unroll 8
+            for (int t = 0; t < T; ++t) xr[t] = xs + min(t, nt - 1) * RS + j * S;
+            float acc[T];
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[t] = 0.0f;
+#pragma unroll RT_UNROLL
             for (int i = 0; i < m4; i += 4) {
                 const float4 w4 = *reinterpret_cast<const float4*>(wr + i);
 #pragma unroll
-                for (int t = 0; t < RT_TMAX; ++t) {
-                    if (t < nt) {
-                        const float4 x4 = *reinterpret_cast<const float4*>(xr + t * RS + i);
-                        acc[t] = __builtin_fmaf(w4.x, x4.x, acc[t]);
-                        acc[t] = __builtin_fmaf(w4.y, x4.y, acc[t]);
-                        acc[t] = __builtin_fmaf(w4.z, x4.z, acc[t]);
-                        acc[t] = __builtin_fmaf(w4.w, x4.w, acc[t]);
-                    }
+                for (int t = 0; t < T; ++t) {
+                    const float4 x4 = *reinterpret_cast<const float4*>(xr[t] + i);
+                    acc[t] = __builtin_fmaf(w4.x, x4.x, acc[t]);
+                    acc[t] = __builtin_fmaf(w4.y, x4.y, acc[t]);
+                    acc[t] = __builtin_fmaf(w4.z, x4.z, acc[t]);
+                    acc[t] = __builtin_fmaf(w4.w, x4.w, acc[t]);
                 }
             }
             for (int i = m4; i < m; ++i) {
                 const float wv = wr[i];
 #pragma unroll
-                for (int t = 0; t < RT_TMAX; ++t)
-                    if (t < nt) acc[t] = __builtin_fmaf(wv, xr[t * RS + i], acc[t]);
+                for (int t = 0; t < T; ++t) acc[t] = __builtin_fmaf(wv, xr[t][i], acc[t]);
             }
 #pragma unroll
-            for (int t = 0; t < RT_TMAX; ++t) {
+            for (int t = 0; t < T; ++t) {
                 if (t < nt) {
                     const float hi = __shfl_down(acc[t], 8, 16);
                     const float v = acc[t] + hi;  // acc0[j] + acc1[j] for j < 8
@@ -293,13 +321,22 @@ __global__ void __launch_bounds__(RT_THREADS) k_route(RouteArgs a, int T) {
 #pragma unroll
                     for (int q = 0; q < 8; ++q) s += __shfl(v, q, 16);
                     if (j == 0) {
-                        if (r < E) lg[t * E + r] = a.bias ? s + a.bias[r] : s;
-                        else shl[t] = s;
+                        const size_t tok = (size_t)(t0 + t);
+                        if (r < E) {
+                            const float l = a.bias ? s + a.bias[r] : s;
+                            if (nsplit == 1) lg[t * E + r] = l;
+                            else a.logits[tok * E + r] = l;
+                        } else if (nsplit == 1) {
+                            shl[t] = s;
+                        } else {
+                            a.shscale[tok] = s;  // raw shared-gate logit; k_route_topk applies the sigmoid
+                        }
                     }
                 }
             }
         }
     }
+    if (nsplit > 1) return;  // block-uniform
     __syncthreads();
 
     // -- 4. top-k by rank, softmax over the selected logits
@@ -334,13 +371,58 @@ __global__ void __launch_bounds__(RT_THREADS) k_route(RouteArgs a, int T) {
     }
 }
 
+// Step 4 for split routers: one block of RT_THREADS per token, logits from
+// global memory (the same rank counting and softmax as in k_route).
+__global__ void __launch_bounds__(RT_THREADS) k_route_topk(RouteArgs a) {
+    __shared__ float lg[MAX_E];
+    __shared__ int sel[MAX_K];
+    const size_t t = blockIdx.x;
+    const int tid = threadIdx.x, E = a.E, k = a.k;
+    for (int e = tid; e < E; e += RT_THREADS) lg[e] = a.logits[t * E + e];
+    if (tid < MAX_K) sel[tid] = tid;
+    __syncthreads();
+    for (int e = tid; e < E; e += RT_THREADS) {
+        const float le = rank_key(lg[e]);
+        int rank = 0;
+        for (int f = 0; f < E; ++f) rank += ranks_above(rank_key(lg[f]), f, le, e);
+        if (rank < k) sel[rank] = e;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float p[MAX_K];
+        float mx = lg[sel[0]];
+        for (int i = 1; i < k; ++i) mx = fmaxf(mx, lg[sel[i]]);
+        float sum = 0.0f;
+        for (int i = 0; i < k; ++i) {
+            p[i] = expf(lg[sel[i]] - mx);
+            sum += p[i];
+        }
+        const float inv = (sum > 0.0f) ? 1.0f / sum : 1.0f / (float)k;
+        for (int i = 0; i < k; ++i) {
+            a.ids[t * k + i] = sel[i];
+            a.probs[t * k + i] = p[i] * inv;
+        }
+        if (a.shscale) a.shscale[t] = a.shgate ? 1.0f / (1.0f + expf(-a.shscale[t])) : 1.0f;
+    }
+}
+
 void launch_route(const RouteArgs& a, hipStream_t st) {
-    const int T = route_tokens_per_block(a.d, a.E);
-    const size_t lds = route_lds(T, a.d, a.E);
-    if (lds > 65536)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_route), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)lds);
-    hipLaunchKernelGGL(k_route, dim3((a.n + T - 1) / T), dim3(RT_THREADS), lds, st, a, T);
+    RouteShape r = route_shape(a);
+    r.T = r.T >= 4 ? 4 : r.T >= 2 ? 2 : 1;  // instantiated token counts
+    const size_t lds = route_lds(r.T, a.d, a.E);
+    const int tb = (a.n + r.T - 1) / r.T;
+    auto go = [&](auto kern) {
+        if (lds > 65536)
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)lds);
+        hipLaunchKernelGGL(kern, dim3(tb * r.RS), dim3(RT_THREADS), lds, st, a, r.RS, r.RPB);
+    };
+    switch (r.T) {
+        case 4: go(k_route<4>); break;
+        case 2: go(k_route<2>); break;
+        default: go(k_route<1>); break;
+    }
+    if (r.RS > 1) hipLaunchKernelGGL(k_route_topk, dim3(a.n), dim3(RT_THREADS), 0, st, a);
 }
 
 // Matrix-core form of Q8_0 activations already in global memory, one block per row.
