@@ -175,9 +175,14 @@ struct jx_moe_layer {
     jx::ActQ8 xq, hq, hqs;
     DevActH xh, hh, hhs;  // matrix-core forms of x, h, shared h
     float *hf = nullptr, *hfs = nullptr, *y = nullptr, *ysh = nullptr;
+    unsigned* tile_cnt = nullptr;  // per down row tile: blocks done (the GEMV's folded combine), zero between launches
     int last_n = 0;
     Prof prof;
     hipStream_t own = nullptr;  // used when the caller passes the null stream
+    // the shared expert runs on a second stream between a fork after routing and a join before the
+    // routed down projection (it needs only the quantized x)
+    hipStream_t side = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     struct GraphKey {
         int n;
         const float* x;
@@ -248,6 +253,8 @@ int ensure_workspace(jx_moe_layer* L, int n) {
     WS(L->hq.s, nk * L->F / 32);
     L->hq.K = L->F;
     WS(L->y, nk * L->d);
+    WS(L->tile_cnt, (size_t)L->d / 32);
+    HIPCHK(hipMemset(L->tile_cnt, 0, (size_t)L->d / 32 * sizeof(unsigned)));
     const size_t fpad = ((size_t)L->F + 255) / 256 * 256;
     if (L->down_f32) {
         WS(L->hf, nk * fpad);
@@ -274,7 +281,7 @@ void free_layer(jx_moe_layer* L) {
     for (auto* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown}) m->release();
     void* ptrs[] = {L->router, L->router_cm, L->bias, L->shgate, L->x, L->out, L->probs, L->shscale, L->logits, L->ids,
                     L->counts, L->offs, L->act, L->n_act, L->pair_tok, L->pos_of, L->n_tiles, L->tiles,
-                    L->slots, L->xq.q, L->xq.s, L->hq.q, L->hq.s, L->hqs.q, L->hqs.s, L->hf, L->hfs, L->y, L->ysh};
+                    L->slots, L->xq.q, L->xq.s, L->hq.q, L->hq.s, L->hqs.q, L->hqs.s, L->hf, L->hfs, L->y, L->ysh, L->tile_cnt};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     L->xh.release();
@@ -283,6 +290,9 @@ void free_layer(jx_moe_layer* L) {
     for (auto ev : L->prof.pool) (void)hipEventDestroy(ev);
     for (auto& kv : L->graphs) (void)hipGraphExecDestroy(kv.second);
     if (L->own) (void)hipStreamDestroy(L->own);
+    if (L->side) (void)hipStreamDestroy(L->side);
+    if (L->ev_fork) (void)hipEventDestroy(L->ev_fork);
+    if (L->ev_join) (void)hipEventDestroy(L->ev_join);
     delete L;
 }
 
@@ -384,6 +394,41 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     const int tb = n == 1 ? 1 : 4;
     const int tiles_ub = nk / jx::MFMA_BN + slots;
     const size_t fpad = ((size_t)L->F + 255) / 256 * 256;
+    // shared expert on the side stream, concurrent with the routed gate/up
+    if (L->shared) {
+        HIPCHK(hipEventRecord(L->ev_fork, st));
+        HIPCHK(hipStreamWaitEvent(L->side, L->ev_fork, 0));
+        hipStream_t ss = L->side;
+        jx::Groups sg;
+        sg.identity = 1;
+        sg.n_tok = n;
+        sg.top_k = 1;
+        const size_t fspad = ((size_t)L->Fs + 255) / 256 * 256;
+        if (smfma) {
+            const int st_ub = (n + jx::MFMA_BN - 1) / jx::MFMA_BN;
+            {
+                Launch l(L, "shared_gateup_mfma", ss);
+                jx::launch_mfma_gateup(L->sgate.m, L->sup.m, L->xh.a, sg, st_ub, L->sdown_f32 ? jx::ActQ8{} : L->hqs,
+                                       L->sdown_f32 ? L->hfs : nullptr, ss);
+            }
+            Launch l(L, "shared_down", ss);
+            if (L->sdown_f32)
+                jx::launch_f32_to_acth(L->hfs, (int)fspad, n, L->hhs.a, ss);
+            else
+                jx::launch_q8_to_acth(L->hqs, n, L->hhs.a, ss, false);
+            jx::launch_mfma_down(L->sdown.m, L->hhs.a, sg, st_ub, L->ysh, ss);
+        } else {
+            {
+                Launch l(L, "shared_gateup_gemv", ss);
+                jx::launch_gemv_gateup(L->sgate.m, L->sup.m, L->xq, sg, 1, tb, L->hqs, L->sdown_f32 ? L->hfs : nullptr,
+                                       ss);
+            }
+            Launch l(L, "shared_down", ss);
+            jx::launch_gemv_down(L->sdown.m, L->hqs, L->sdown_f32 ? L->hfs : nullptr, (int)fspad, sg, 1, tb, L->ysh,
+                                 ss);
+        }
+        HIPCHK(hipEventRecord(L->ev_join, ss));
+    }
     if (mfma) {
         Launch l(L, "gateup_mfma", st);
         jx::launch_mfma_gateup(L->gate.m, L->up.m, L->xh.a, grp, tiles_ub, L->down_f32 ? jx::ActQ8{} : L->hq,
@@ -403,40 +448,12 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         Launch l(L, "gateup_gemv", st);
         jx::launch_gemv_gateup(L->gate.m, L->up.m, L->xq, grp, slots, tb, L->hq, L->down_f32 ? L->hf : nullptr, st);
     }
-    if (L->shared) {
-        jx::Groups sg;
-        sg.identity = 1;
-        sg.n_tok = n;
-        sg.top_k = 1;
-        const size_t fspad = ((size_t)L->Fs + 255) / 256 * 256;
-        if (smfma) {
-            const int st_ub = (n + jx::MFMA_BN - 1) / jx::MFMA_BN;
-            {
-                Launch l(L, "shared_gateup_mfma", st);
-                jx::launch_mfma_gateup(L->sgate.m, L->sup.m, L->xh.a, sg, st_ub, L->sdown_f32 ? jx::ActQ8{} : L->hqs,
-                                       L->sdown_f32 ? L->hfs : nullptr, st);
-            }
-            Launch l(L, "shared_down", st);
-            if (L->sdown_f32)
-                jx::launch_f32_to_acth(L->hfs, (int)fspad, n, L->hhs.a, st);
-            else
-                jx::launch_q8_to_acth(L->hqs, n, L->hhs.a, st, false);
-            jx::launch_mfma_down(L->sdown.m, L->hhs.a, sg, st_ub, L->ysh, st);
-        } else {
-            {
-                Launch l(L, "shared_gateup_gemv", st);
-                jx::launch_gemv_gateup(L->sgate.m, L->sup.m, L->xq, sg, 1, tb, L->hqs, L->sdown_f32 ? L->hfs : nullptr,
-                                       st);
-            }
-            Launch l(L, "shared_down", st);
-            jx::launch_gemv_down(L->sdown.m, L->hqs, L->sdown_f32 ? L->hfs : nullptr, (int)fspad, sg, 1, tb, L->ysh,
-                                 st);
-        }
-    }
-    // fp32 h (Q4_K down with d_ff % 256 != 0) takes the matrix-core down GEMM whenever the dispatch
-    // tables hold MFMA tiles (every path but the few-token one): the GEMV re-streams the weights per
-    // group of 4 tokens and works in fp32
-    const bool mfma_down = mfma || (L->down_f32 && !small_logits && mfma_shape);
+    if (L->shared) HIPCHK(hipStreamWaitEvent(st, L->ev_join, 0));  // the combine reads ysh
+    // fp32 h (Q4_K down with d_ff % 256 != 0) takes the matrix-core down GEMM from 2 tokens on (every
+    // dispatch path writes the MFMA tiles, the few-token one from the gate/up GEMV's tail block): the
+    // fp32 GEMV's multi-token form re-streams the weights per group of 4 tokens in fp32
+    const bool mfma_down = mfma || (L->down_f32 && n >= 2 && mfma_shape);
+    bool combined = false;
     if (mfma_down) {
         {
             Launch l(L, "h_to_matrix_form", st);
@@ -448,11 +465,24 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         Launch l(L, "down_mfma", st);
         jx::launch_mfma_down(L->down.m, L->hh.a, grp, tiles_ub, L->y, st);
     } else {
+        // few tokens: the last block of each row tile also does the weighted combine
+        jx::CombineTail ct;
+        ct.on = n <= jx::COMBINE_TAIL_MAX_N;
+        ct.n = n;
+        ct.k = k;
+        ct.probs = L->probs;
+        ct.pos_of = L->pos_of;
+        ct.ysh = L->shared ? L->ysh : nullptr;
+        ct.shscale = L->shscale;
+        ct.n_act = L->n_act;
+        ct.counter = L->tile_cnt;
+        ct.out = outdev;
         Launch l(L, L->down_f32 ? "down_gemv_f32" : "down_gemv", st);
         jx::launch_gemv_down(L->down.m, L->hq, L->down_f32 ? L->hf : nullptr, (int)fpad, grp, slots, mfma ? 4 : tb,
-                             L->y, st);
+                             L->y, st, &ct);
+        combined = ct.on;
     }
-    {
+    if (!combined) {
         Launch l(L, "combine", st);
         jx::launch_combine(n, d, k, L->probs, L->pos_of, L->y, L->shared ? L->ysh : nullptr, L->shscale, outdev, st);
     }
@@ -582,6 +612,10 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
     }
     if ((r = ensure_workspace(L, 1)) != JX_OK) return bail(r);
     if (hipStreamCreate(&L->own) != hipSuccess) return bail(fail(JX_ERR_HIP, "stream create"));
+    if (L->shared && (hipStreamCreate(&L->side) != hipSuccess ||
+                      hipEventCreateWithFlags(&L->ev_fork, hipEventDisableTiming) != hipSuccess ||
+                      hipEventCreateWithFlags(&L->ev_join, hipEventDisableTiming) != hipSuccess))
+        return bail(fail(JX_ERR_HIP, "shared-expert stream create"));
     if (const char* g = std::getenv("JX_NO_GRAPH")) L->use_graphs = std::strcmp(g, "0") == 0;
     *out = L;
     return JX_OK;
