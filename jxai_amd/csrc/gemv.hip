@@ -517,7 +517,7 @@ k_gemv_gateup(QMat G, QMat U, ActQ8 xq, Groups grp, ActQ8 hq, float* hf, int hf_
 // Down projection into y[pair][rows].
 template <int TYPE, int TB, int WAVES, bool F32ACT>
 __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(GEMV_WAVES_PER_SIMD(TB))))
-k_gemv_down(QMat D, ActQ8 hq, const float* hf, int hf_ld, Groups grp, float* y, CombineTail ct) {
+k_gemv_down(QMat D, ActQ8 hq, const float* hf, int hf_ld, Groups grp, float* y) {
     extern __shared__ __align__(16) int8_t smem[];
     __shared__ float red[WAVES][TB][32];
     const int rt = blockIdx.x;
@@ -569,31 +569,6 @@ k_gemv_down(QMat D, ActQ8 hq, const float* hf, int hf_ld, Groups grp, float* y, 
                 for (int w = 0; w < WAVES; ++w) s += red[w][j][m];
                 y[(size_t)(p0 + tb0 + j) * D.rows + rt * 32 + m] = s;
             }
-        }
-    }
-    if (ct.on && wave == 0) {
-        // release this block's y rows at agent scope, count it in; the last block of the row tile
-        // (acquire) combines: out[t] = sum_s p[t][s] * y[pos(t,s)] (+ shscale[t] * ysh[t]), fma in
-        // selection order (k_combine's order), for the tile's 32 features
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        unsigned old = 0;
-        if (lane == 0) old = __hip_atomic_fetch_add(ct.counter + rt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        old = __shfl(old, 0, 64);
-        if (old + 1 == (unsigned)*ct.n_act) {
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            if (h == 0) {
-                const int d = D.rows, f = rt * 32 + m;
-                for (int t = 0; t < ct.n; ++t) {
-                    float acc = 0.0f;
-                    for (int s = 0; s < ct.k; ++s) {
-                        const size_t p = (size_t)ct.pos_of[(size_t)t * ct.k + s];
-                        acc = __builtin_fmaf(ct.probs[(size_t)t * ct.k + s], y[p * d + f], acc);
-                    }
-                    if (ct.ysh) acc = __builtin_fmaf(ct.shscale[t], ct.ysh[(size_t)t * d + f], acc);
-                    ct.out[(size_t)t * d + f] = acc;
-                }
-            }
-            if (lane == 0) __hip_atomic_store(ct.counter + rt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -657,33 +632,32 @@ void launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Gro
 
 template <int TYPE, bool F32ACT>
 static void down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp, int slots,
-                   int tb, float* y, hipStream_t st, const CombineTail& ct) {
+                   int tb, float* y, hipStream_t st) {
     dim3 grid(dn.nrt, slots);
     const int K = F32ACT ? hf_ld : hq.K;
     if (tb <= 1) {
         const size_t lds = act_lds_bytes(1, K, F32ACT);
         lds_optin(k_gemv_down<TYPE, 1, DOWN_WAVES, F32ACT>, lds);
         hipLaunchKernelGGL((k_gemv_down<TYPE, 1, DOWN_WAVES, F32ACT>), grid, dim3(DOWN_WAVES * 64), lds, st, dn, hq,
-                           hf, hf_ld, grp, y, ct);
+                           hf, hf_ld, grp, y);
     } else {
         const size_t lds = act_lds_bytes(4, K, F32ACT);
         lds_optin(k_gemv_down<TYPE, 4, DOWN_WAVES, F32ACT>, lds);
         hipLaunchKernelGGL((k_gemv_down<TYPE, 4, DOWN_WAVES, F32ACT>), grid, dim3(DOWN_WAVES * 64), lds, st, dn, hq,
-                           hf, hf_ld, grp, y, ct);
+                           hf, hf_ld, grp, y);
     }
 }
 
 void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp, int slots,
-                      int tb, float* y, hipStream_t st, const CombineTail* ctp) {
-    const CombineTail ct = ctp ? *ctp : CombineTail{};
+                      int tb, float* y, hipStream_t st) {
     if (hf) {
-        down_t<T_Q4_K, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, ct);
+        down_t<T_Q4_K, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st);
         return;
     }
     switch (dn.type) {
-        case T_Q4_0: down_t<T_Q4_0, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, ct); break;
-        case T_Q8_0: down_t<T_Q8_0, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, ct); break;
-        case T_Q4_K: down_t<T_Q4_K, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, ct); break;
+        case T_Q4_0: down_t<T_Q4_0, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st); break;
+        case T_Q8_0: down_t<T_Q8_0, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st); break;
+        case T_Q4_K: down_t<T_Q4_K, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st); break;
         default: break;
     }
 }

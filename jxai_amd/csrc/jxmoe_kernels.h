@@ -145,23 +145,8 @@ void launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Gro
 // Q8_0 or fp32 activations).
 int gemv_max_k(bool gateup, int tb, bool f32);
 // Decode regime: down projection over Q8_0 (hq) or fp32 (hf) activations into y[pair][d].
-// The weighted combine folded into the decode down GEMV: the last block to
-// finish a row tile (counted in counter[rt], which it resets) computes that
-// tile's outputs for every token, in the same order as launch_combine.
-constexpr int COMBINE_TAIL_MAX_N = 16;
-struct CombineTail {
-    int on = 0;
-    int n = 0, k = 0;
-    const float* probs = nullptr;   // [n][k]
-    const int* pos_of = nullptr;    // [n*k] -> row of y
-    const float* ysh = nullptr;     // [n][d] shared expert output or null
-    const float* shscale = nullptr; // [n]
-    const int* n_act = nullptr;     // blocks taking part per row tile
-    unsigned* counter = nullptr;    // [row tiles], zero between launches
-    float* out = nullptr;           // [n][d]
-};
 void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp,
-                      int slots, int tb, float* y, hipStream_t st, const CombineTail* ct = nullptr);
+                      int slots, int tb, float* y, hipStream_t st);
 // Prefill regime: matrix-core grouped GEMMs over the dispatch tile table.
 // gate/up writes SwiGLU(h) as Q8_0 (hq.q != null; the down GEMM takes it after
 // launch_q8_to_acth) and/or fp32 (hf != null).

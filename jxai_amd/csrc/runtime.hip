@@ -175,7 +175,6 @@ struct jx_moe_layer {
     jx::ActQ8 xq, hq, hqs;
     DevActH xh, hh, hhs;  // matrix-core forms of x, h, shared h
     float *hf = nullptr, *hfs = nullptr, *y = nullptr, *ysh = nullptr;
-    unsigned* tile_cnt = nullptr;  // per down row tile: blocks done (the GEMV's folded combine), zero between launches
     int last_n = 0;
     Prof prof;
     hipStream_t own = nullptr;  // used when the caller passes the null stream
@@ -253,8 +252,6 @@ int ensure_workspace(jx_moe_layer* L, int n) {
     WS(L->hq.s, nk * L->F / 32);
     L->hq.K = L->F;
     WS(L->y, nk * L->d);
-    WS(L->tile_cnt, (size_t)L->d / 32);
-    HIPCHK(hipMemset(L->tile_cnt, 0, (size_t)L->d / 32 * sizeof(unsigned)));
     const size_t fpad = ((size_t)L->F + 255) / 256 * 256;
     if (L->down_f32) {
         WS(L->hf, nk * fpad);
@@ -281,7 +278,7 @@ void free_layer(jx_moe_layer* L) {
     for (auto* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown}) m->release();
     void* ptrs[] = {L->router, L->router_cm, L->bias, L->shgate, L->x, L->out, L->probs, L->shscale, L->logits, L->ids,
                     L->counts, L->offs, L->act, L->n_act, L->pair_tok, L->pos_of, L->n_tiles, L->tiles,
-                    L->slots, L->xq.q, L->xq.s, L->hq.q, L->hq.s, L->hqs.q, L->hqs.s, L->hf, L->hfs, L->y, L->ysh, L->tile_cnt};
+                    L->slots, L->xq.q, L->xq.s, L->hq.q, L->hq.s, L->hqs.q, L->hqs.s, L->hf, L->hfs, L->y, L->ysh};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     L->xh.release();
@@ -448,12 +445,11 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         Launch l(L, "gateup_gemv", st);
         jx::launch_gemv_gateup(L->gate.m, L->up.m, L->xq, grp, slots, tb, L->hq, L->down_f32 ? L->hf : nullptr, st);
     }
-    if (L->shared) HIPCHK(hipStreamWaitEvent(st, L->ev_join, 0));  // the combine reads ysh
+    if (L->shared) HIPCHK(hipStreamWaitEvent(st, L->ev_join, 0));
     // fp32 h (Q4_K down with d_ff % 256 != 0) takes the matrix-core down GEMM from 2 tokens on (every
     // dispatch path writes the MFMA tiles, the few-token one from the gate/up GEMV's tail block): the
     // fp32 GEMV's multi-token form re-streams the weights per group of 4 tokens in fp32
     const bool mfma_down = mfma || (L->down_f32 && n >= 2 && mfma_shape);
-    bool combined = false;
     if (mfma_down) {
         {
             Launch l(L, "h_to_matrix_form", st);
@@ -465,24 +461,11 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         Launch l(L, "down_mfma", st);
         jx::launch_mfma_down(L->down.m, L->hh.a, grp, tiles_ub, L->y, st);
     } else {
-        // few tokens: the last block of each row tile also does the weighted combine
-        jx::CombineTail ct;
-        ct.on = n <= jx::COMBINE_TAIL_MAX_N;
-        ct.n = n;
-        ct.k = k;
-        ct.probs = L->probs;
-        ct.pos_of = L->pos_of;
-        ct.ysh = L->shared ? L->ysh : nullptr;
-        ct.shscale = L->shscale;
-        ct.n_act = L->n_act;
-        ct.counter = L->tile_cnt;
-        ct.out = outdev;
         Launch l(L, L->down_f32 ? "down_gemv_f32" : "down_gemv", st);
         jx::launch_gemv_down(L->down.m, L->hq, L->down_f32 ? L->hf : nullptr, (int)fpad, grp, slots, mfma ? 4 : tb,
-                             L->y, st, &ct);
-        combined = ct.on;
+                             L->y, st);
     }
-    if (!combined) {
+    {
         Launch l(L, "combine", st);
         jx::launch_combine(n, d, k, L->probs, L->pos_of, L->y, L->shared ? L->ysh : nullptr, L->shscale, outdev, st);
     }
