@@ -447,7 +447,10 @@ __device__ __forceinline__ void kloop(const QMat& W0, const QMat& W1, int e, int
 // Resident waves per SIMD the GEMVs are compiled for (single-token groups:
 // <= 128 VGPRs, every block of a decode step resident at once with enough
 // 1 KB weight loads in flight per CU to cover HBM latency).
-#define GEMV_WAVES_PER_SIMD(TB) ((TB) == 1 ? 4 : 2)
+#ifndef JX_GEMV_TB4_WPS
+#define JX_GEMV_TB4_WPS 2
+#endif
+#define GEMV_WAVES_PER_SIMD(TB) ((TB) == 1 ? 4 : JX_GEMV_TB4_WPS)
 
 // Gate + up + SwiGLU (matmul_swiglu_quant_f32, src/quant.cpp:3970-4009) and
 // the Q8_0 quantization of the result for the down projection

@@ -91,7 +91,9 @@ struct Groups {
 constexpr int SMALL_GROUP_MAX_E = 64;
 
 constexpr int MFMA_BN = 128;  // pairs per matrix-core GEMM tile
-constexpr int MFMA_MIN_SHARED_TOKENS = 32;  // shared expert on the matrix cores from this many tokens
+// shared expert on the matrix cores from this many tokens (one dense expert fills few GEMM
+// workgroups below that: measured 2x slower than its GEMV at 8 tokens, even at 32, Qwen1.5-shaped)
+constexpr int MFMA_MIN_SHARED_TOKENS = 32;
 
 struct RouteArgs {
     const float* x;        // [n][d]

@@ -333,13 +333,19 @@ int resolve_profile(jx_moe_layer* L) {
     return JX_OK;
 }
 
-// MFMA tiles when the average expert sees at least this many pairs.
-constexpr int MFMA_MIN_PAIRS_PER_EXPERT = 16;
+// Regime: the matrix-core GEMMs once the average expert sees this many (token, slot) pairs.  The
+// multi-token GEMV streams an expert's weights once per group of 4 tokens and the GEMM once per
+// 64-pair tile (computing the whole tile), so the crossover follows the weight bytes per element:
+// measured on MI355X at 4-8 pairs for the 4-bit layers (Mixtral-, Qwen1.5-, DeepSeek-V2-Lite-shaped)
+// and 2-4 for the Q8_0 one (Qwen3-shaped).
+constexpr int MFMA_MIN_PAIRS_PER_EXPERT_Q4 = 6;
+constexpr int MFMA_MIN_PAIRS_PER_EXPERT_Q8 = 3;
 
 int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStream_t st, uint32_t flags) {
     const int E = L->E, k = L->k, d = L->d;
     const int nk = n * k;
-    bool mfma = (size_t)nk >= (size_t)MFMA_MIN_PAIRS_PER_EXPERT * E;
+    const int min_ppe = L->gate.m.type == jx::T_Q8_0 ? MFMA_MIN_PAIRS_PER_EXPERT_Q8 : MFMA_MIN_PAIRS_PER_EXPERT_Q4;
+    bool mfma = (size_t)nk >= (size_t)min_ppe * E;
     if (flags & JX_FWD_FORCE_GEMV) mfma = false;
     if (flags & JX_FWD_FORCE_MFMA) mfma = true;
     // the matrix-core GEMMs stage K in 128-element half-units; their Q4_K matrices carry the min table
