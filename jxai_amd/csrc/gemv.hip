@@ -576,6 +576,220 @@ k_gemv_down(QMat D, ActQ8 hq, const float* hf, int hf_ld, Groups grp, float* y) 
     }
 }
 
+// ---------------------------------------------------------------- several tokens per expert
+// Multi-token GEMV on the matrix cores: one v_mfma_i32_32x32x32_i8 per 32-element block gives the
+// exact integer block sums of up to MX_NT tokens against the 32 rows of a tile.  Operand B is the
+// weight tile as the GEMV layout holds it (lane (m, h): 16 elements of row m, half h of the block;
+// Q4_0 lanes load their block whole and take their nibble half); operand A holds the tokens' Q8_0
+// quants (lane (t, g): token t, half g; tokens past the group give zeros).  Lane (m, g) receives
+// D[token 8(r/4) + 4g + r%4][row m] in register r, r < 8.  Each sum is scaled in fp32 by its row's
+// weight scale and its token's activation scale: the integer block sums and scale products of
+// vec_dot_*_q8_0 (src/quant.cpp:3307-3573); the Q4_0 -8 offset is applied to the integer sum; only
+// the fp32 summation order differs.  The weights are read once per MX_NT tokens instead of once per
+// 4, and the scaling is a few instructions per (row, token, block) instead of the GEMV's per-token
+// dot products.  The tokens' (scale, sum) pairs are staged in LDS per pass; quants and weights
+// stream one unit ahead.
+constexpr int MX_NT = 16;  // tokens per pass: D registers 0..7
+
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef int v16i_t __attribute__((ext_vector_type(16)));
+
+template <int TYPE>
+struct Mx;
+
+// Q4_K: one super-block per unit (the GEMV's unit); sub-block 2p = low nibbles of chunk p, 2p+1 = high.
+template <>
+struct Mx<T_Q4_K> {
+    static constexpr int BPU = 8;
+    using Raw = RawQ4K;
+    __device__ static int units(const QMat& W) { return W.nkb; }
+    __device__ static void load(Raw& c, const QMat& W, int e, int rt, int u, int m, int h, bool ok) {
+        Fmt<T_Q4_K>::load(c, W, e, rt, u, m, h, ok);
+    }
+    __device__ static uint4 bop(const Raw& c, int j, int) {
+        const uint4 v = c.q[j >> 1];
+        const int sh = (j & 1) * 4;
+        return make_uint4((v.x >> sh) & 0x0F0F0F0Fu, (v.y >> sh) & 0x0F0F0F0Fu, (v.z >> sh) & 0x0F0F0F0Fu,
+                          (v.w >> sh) & 0x0F0F0F0Fu);
+    }
+    // row scale and min scale of sub-block j (get_scale_min_k4, src/quant.cpp:1107-1115)
+    __device__ static void scales(const Raw& c, int j, float& rs, float& rmin) {
+        int sc, mn;
+        hd_scale_min(c.hd, j, sc, mn);
+        rs = f16_to_f32(c.hd.x) * (float)sc;
+        rmin = -f16_to_f32(c.hd.x >> 16) * (float)mn;
+    }
+};
+
+// Q8_0: four blocks per unit, the GEMV layout (lane half h holds half h of each block).
+template <>
+struct Mx<T_Q8_0> {
+    static constexpr int BPU = 4;
+    using Raw = RawB;
+    __device__ static int units(const QMat& W) { return (W.nkb + BPU - 1) / BPU; }
+    __device__ static void load(Raw& c, const QMat& W, int e, int rt, int u, int m, int h, bool ok) {
+        Fmt<T_Q8_0>::load(c, W, e, rt, u, m, h, ok);
+    }
+    __device__ static uint4 bop(const Raw& c, int j, int) { return c.q[j]; }
+    __device__ static void scales(const Raw& c, int j, float& rs, float& rmin) {
+        rs = f16_to_f32(c.d[j] & 0xFFFFu);
+        rmin = 0.0f;
+    }
+};
+
+// Q4_0: four blocks per unit; both lane halves load a row's whole block (16 bytes) and take the low
+// (elements 0..15) or high (16..31) nibbles.
+template <>
+struct Mx<T_Q4_0> {
+    static constexpr int BPU = 4;
+    using Raw = RawB;
+    __device__ static int units(const QMat& W) { return (W.nkb + BPU - 1) / BPU; }
+    __device__ static void load(Raw& c, const QMat& W, int e, int rt, int u, int m, int, bool ok) {
+        const uint8_t* qb = W.qs + e * W.qs_es;
+        const uint8_t* sb = W.sc + e * W.sc_es;
+        const size_t b0 = (size_t)rt * W.nkb + (size_t)u * BPU;
+        const int left = W.nkb - u * BPU;
+#pragma unroll
+        for (int i = 0; i < BPU; ++i) {
+            const bool v = ok && i < left;
+            c.q[i] = ld_stream16(v ? qb + ((b0 + i) * 32 + m) * 16 : W.pad_qs + m * 16);
+            c.d[i] = *reinterpret_cast<const uint16_t*>(v ? sb + ((b0 + i) * 32 + m) * 2 : W.pad_sc + m * 2);
+        }
+    }
+    __device__ static uint4 bop(const Raw& c, int j, int h) {
+        const uint4 v = c.q[j];
+        const int sh = h * 4;
+        return make_uint4((v.x >> sh) & 0x0F0F0F0Fu, (v.y >> sh) & 0x0F0F0F0Fu, (v.z >> sh) & 0x0F0F0F0Fu,
+                          (v.w >> sh) & 0x0F0F0F0Fu);
+    }
+    __device__ static void scales(const Raw& c, int j, float& rs, float& rmin) {
+        rs = f16_to_f32(c.d[j] & 0xFFFFu);
+        rmin = 0.0f;
+    }
+};
+
+// Gate + up (+ SwiGLU + Q8_0 of h) or down for up to MX_NT tokens per pass of one expert's row tile.
+// Gate/up: the first half of the waves streams the gate tile, the second half the up tile.
+template <int TYPE, bool GATEUP, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
+k_gemv_mx(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_ld, float* y, SmallTail tail) {
+    using X = Mx<TYPE>;
+    using Raw = typename X::Raw;
+    constexpr int BPU = X::BPU;
+    constexpr int HW = GATEUP ? WAVES / 2 : WAVES;  // waves per matrix
+    extern __shared__ __align__(16) float2 msc[];   // [block][MX_NT]: (scale, sum) of each token
+    __shared__ float red[WAVES][MX_NT / 2][64];
+    if (GATEUP && tail.on && blockIdx.y == gridDim.y - 1) {  // the extra grid row: dispatch tables only
+        if (blockIdx.x == 0) small_tail<WAVES * 64>(tail, threadIdx.x);
+        return;
+    }
+    const int rt = blockIdx.x;
+    const int4 rec = group_of(grp, blockIdx.y);
+    const int e = rec.x, p0 = rec.y, cnt = rec.z;
+    if (cnt == 0) return;
+    const int tid = threadIdx.x, lane = tid & 63, m = lane & 31, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar unit loop and branches
+    const int kw = wave % HW;
+    const QMat& W = (GATEUP && wave >= HW) ? W1 : W0;
+    const int K = act.K, KB = K / 32;
+    const int nu = X::units(W0);
+    for (int tb0 = 0; tb0 < cnt; tb0 += MX_NT) {
+        const int nt = min(MX_NT, cnt - tb0);
+        if (tb0) __syncthreads();  // the previous pass is done with msc and red
+        auto src = [&](int i) -> size_t {
+            return GATEUP ? (size_t)token_of(grp, rec, tb0 + i) : (size_t)(p0 + tb0 + i);
+        };
+        for (int i = tid; i < KB * MX_NT; i += WAVES * 64) {
+            const int b = i / MX_NT, t = i - b * MX_NT;
+            float2 v = make_float2(0.0f, 0.0f);
+            if (t < nt) {
+                const float2 sv = act.s[src(t) * KB + b];
+                v = make_float2(sv.x, TYPE == T_Q4_K ? sv.x * sv.y : sv.y);  // Q4_K: scale * sum; Q4_0: sum
+            }
+            msc[i] = v;
+        }
+        const bool hi8 = nt > 8;  // tokens 8.. present: D registers 4-7 carry results
+        // A row of this lane: token m; lanes past the pass's tokens read token 0 (their D rows are dropped)
+        const int8_t* arow = act.q + src(m < nt ? m : 0) * (size_t)K + 16 * h;
+        float acc[MX_NT / 2];
+#pragma unroll
+        for (int r = 0; r < MX_NT / 2; ++r) acc[r] = 0.0f;
+        Raw wa, wb;
+        uint4 aa[BPU], ab[BPU];
+        auto ld = [&](Raw& w, uint4(&a)[BPU], int u) {
+            X::load(w, W, e, rt, u, m, h, u < nu);
+#pragma unroll
+            for (int j = 0; j < BPU; ++j)  // in bounds past the end too (their results are never used)
+                a[j] = ld16(arow + (size_t)min(u * BPU + j, KB - 1) * 32);
+        };
+        auto accum = [&](const Raw& w, const uint4(&a)[BPU], int u) {
+#pragma unroll
+            for (int j = 0; j < BPU; ++j) {
+                const int b = u * BPU + j;
+                if (TYPE != T_Q4_K && b >= KB) break;  // wave-uniform; Q4_K units are whole super-blocks
+                const v16i_t D = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i_t, a[j]),
+                                                                       __builtin_bit_cast(v4i_t, X::bop(w, j, h)),
+                                                                       v16i_t{}, 0, 0, 0);
+                float rs, rmin;
+                X::scales(w, j, rs, rmin);
+                // tokens of registers 0-3: 4h..4h+3, of 4-7: 8+4h..11+4h (only when the pass has them)
+                const float4* sp = reinterpret_cast<const float4*>(msc + b * MX_NT + 4 * h);
+                const float4 s0 = sp[0], s1 = sp[1];
+                const float4 s2 = hi8 ? sp[4] : s0, s3 = hi8 ? sp[5] : s1;
+                const float sx[8] = {s0.x, s0.z, s1.x, s1.z, s2.x, s2.z, s3.x, s3.z};
+                const float sy[8] = {s0.y, s0.w, s1.y, s1.w, s2.y, s2.w, s3.y, s3.w};
+#pragma unroll
+                for (int r = 0; r < MX_NT / 2; ++r) {
+                    if (r >= 4 && !hi8) break;  // pass-uniform
+                    if constexpr (TYPE == T_Q4_K) {
+                        acc[r] = __builtin_fmaf(rs * sx[r], (float)D[r], acc[r]);
+                        acc[r] = __builtin_fmaf(rmin, sy[r], acc[r]);
+                    } else if constexpr (TYPE == T_Q4_0) {
+                        const int isum = D[r] - 8 * (int)sy[r];  // weights are nibble - 8; sy exact (|sum| < 2^12)
+                        acc[r] = __builtin_fmaf(rs * sx[r], (float)isum, acc[r]);
+                    } else {
+                        acc[r] = __builtin_fmaf(rs * sx[r], (float)D[r], acc[r]);
+                    }
+                }
+            }
+        };
+        // two units in flight per wave, as the GEMV's K loop
+        int u = kw;
+        ld(wa, aa, u);
+        ld(wb, ab, u + HW);
+        __syncthreads();  // msc staged
+        for (; u < nu; u += 2 * HW) {
+            accum(wa, aa, u);
+            ld(wa, aa, u + 2 * HW);
+            if (u + HW >= nu) break;
+            accum(wb, ab, u + HW);
+            ld(wb, ab, u + 3 * HW);
+        }
+#pragma unroll
+        for (int r = 0; r < MX_NT / 2; ++r) red[wave][r][lane] = acc[r];
+        __syncthreads();
+        if (wave == 0) {
+#pragma unroll
+            for (int r = 0; r < MX_NT / 2; ++r) {
+                const int t = (r < 4 ? 4 * h + r : 8 + 4 * h + (r - 4));
+                float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+                for (int w = 0; w < HW; ++w) v0 += red[w][r][lane];
+                const size_t row = (size_t)(p0 + tb0 + t);
+                if constexpr (GATEUP) {
+#pragma unroll
+                    for (int w = 0; w < HW; ++w) v1 += red[HW + w][r][lane];
+                    const float hv = (v0 / (1.0f + expf(-v0))) * v1;
+                    store_q8_block(hv, m, t < nt && hq.q != nullptr, hq, row, rt);
+                    if (hf && t < nt) hf[row * (size_t)hf_ld + rt * 32 + m] = hv;
+                } else {
+                    if (t < nt) y[row * W0.rows + rt * 32 + m] = v0;
+                }
+            }
+        }
+    }
+}
+
 #ifndef JX_GEMV_GATEUP_WAVES
 #define JX_GEMV_GATEUP_WAVES 4
 #endif
@@ -614,11 +828,16 @@ static void gateup_t(const QMat& g, const QMat& u, const ActQ8& xq, const Groups
         lds_optin(k_gemv_gateup<TYPE, 1, GATEUP_WAVES>, lds);
         hipLaunchKernelGGL((k_gemv_gateup<TYPE, 1, GATEUP_WAVES>), grid, dim3(GATEUP_WAVES * 64), lds, st, g, u, xq,
                            grp, hq, hf, hf_ld, tail);
-    } else {
+    } else if (tb <= 4) {
         const size_t lds = act_lds_bytes(4, xq.K, false);
         lds_optin(k_gemv_gateup<TYPE, 4, GATEUP_WAVES>, lds);
         hipLaunchKernelGGL((k_gemv_gateup<TYPE, 4, GATEUP_WAVES>), grid, dim3(GATEUP_WAVES * 64), lds, st, g, u, xq,
                            grp, hq, hf, hf_ld, tail);
+    } else {  // several tokens per expert: the matrix-core form
+        const size_t lds = (size_t)(xq.K / 32) * MX_NT * sizeof(float2);
+        lds_optin(k_gemv_mx<TYPE, true, GATEUP_WAVES>, lds);
+        hipLaunchKernelGGL((k_gemv_mx<TYPE, true, GATEUP_WAVES>), grid, dim3(GATEUP_WAVES * 64), lds, st, g, u, xq,
+                           grp, hq, hf, hf_ld, nullptr, tail);
     }
 }
 
@@ -643,6 +862,11 @@ static void down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, 
         lds_optin(k_gemv_down<TYPE, 1, DOWN_WAVES, F32ACT>, lds);
         hipLaunchKernelGGL((k_gemv_down<TYPE, 1, DOWN_WAVES, F32ACT>), grid, dim3(DOWN_WAVES * 64), lds, st, dn, hq,
                            hf, hf_ld, grp, y);
+    } else if (tb > 4 && !F32ACT) {  // several tokens per expert: the matrix-core form
+        const size_t lds = (size_t)(K / 32) * MX_NT * sizeof(float2);
+        lds_optin(k_gemv_mx<TYPE, false, DOWN_WAVES>, lds);
+        hipLaunchKernelGGL((k_gemv_mx<TYPE, false, DOWN_WAVES>), grid, dim3(DOWN_WAVES * 64), lds, st, dn, dn, hq,
+                           grp, ActQ8{}, nullptr, 0, y, SmallTail{});
     } else {
         const size_t lds = act_lds_bytes(4, K, F32ACT);
         lds_optin(k_gemv_down<TYPE, 4, DOWN_WAVES, F32ACT>, lds);

@@ -34,18 +34,11 @@ __device__ __forceinline__ uint32_t f32_to_f16_trunc(float f) {
     return sign | ((uint32_t)e << 10) | (m >> 13);
 }
 
-// Exact fp16 -> fp32 with integer ops only (independent of the fp16
-// denormal mode).
+// fp16 -> fp32 (the low 16 bits of h): one v_cvt_f32_f16, exact for every
+// finite input including subnormals (kernels run with fp16 denormals
+// preserved: the default .amdhsa_float_denorm_mode_16_64 = 3).
 __device__ __forceinline__ float f16_to_f32(uint32_t h) {
-    const uint32_t sign = (h & 0x8000u) << 16;
-    const uint32_t e = (h >> 10) & 0x1Fu;
-    const uint32_t m = h & 0x3FFu;
-    if (e == 0) {
-        const float v = (float)m * 0x1p-24f;
-        return sign ? -v : v;
-    }
-    if (e == 31) return __uint_as_float(sign | 0x7F800000u | (m << 13));
-    return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
 // Round half away from zero (C roundf), exact for every finite input.

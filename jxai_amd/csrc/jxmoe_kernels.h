@@ -92,8 +92,9 @@ constexpr int SMALL_GROUP_MAX_E = 64;
 
 constexpr int MFMA_BN = 128;  // pairs per matrix-core GEMM tile
 // shared expert on the matrix cores from this many tokens (one dense expert fills few GEMM
-// workgroups below that: measured 2x slower than its GEMV at 8 tokens, even at 32, Qwen1.5-shaped)
-constexpr int MFMA_MIN_SHARED_TOKENS = 32;
+// workgroups below that; against the 16-token matrix-core GEMV the crossover measured 32-128 tokens
+// on the Qwen1.5- and DeepSeek-V2-Lite-shaped layers)
+constexpr int MFMA_MIN_SHARED_TOKENS = 64;
 
 struct RouteArgs {
     const float* x;        // [n][d]

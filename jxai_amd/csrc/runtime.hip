@@ -334,12 +334,12 @@ int resolve_profile(jx_moe_layer* L) {
 }
 
 // Regime: the matrix-core GEMMs once the average expert sees this many (token, slot) pairs.  The
-// multi-token GEMV streams an expert's weights once per group of 4 tokens and the GEMM once per
-// 64-pair tile (computing the whole tile), so the crossover follows the weight bytes per element:
-// measured on MI355X at 4-8 pairs for the 4-bit layers (Mixtral-, Qwen1.5-, DeepSeek-V2-Lite-shaped)
-// and 2-4 for the Q8_0 one (Qwen3-shaped).
-constexpr int MFMA_MIN_PAIRS_PER_EXPERT_Q4 = 6;
-constexpr int MFMA_MIN_PAIRS_PER_EXPERT_Q8 = 3;
+// multi-token GEMV (int8 matrix cores, 16 tokens per weight pass) streams an expert's weights once
+// per 16 tokens, the GEMM once per 64-pair tile computing the whole tile; measured on MI355X the
+// crossover lies at 8-16 pairs for the 4-bit layers (Mixtral-, Qwen1.5-, DeepSeek-V2-Lite-shaped)
+// and above 8 for the Q8_0 one (Qwen3-shaped).
+constexpr int MFMA_MIN_PAIRS_PER_EXPERT_Q4 = 12;
+constexpr int MFMA_MIN_PAIRS_PER_EXPERT_Q8 = 16;
 
 int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStream_t st, uint32_t flags) {
     const int E = L->E, k = L->k, d = L->d;
@@ -394,7 +394,15 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     grp.top_k = k;
     grp.n_tok = n;
     const int slots = std::min(E, nk);
-    const int tb = n == 1 ? 1 : 4;
+    // GEMV form: one token; groups of 4 on the VALU (few tokens per expert); or 16 per weight pass on
+    // the int8 matrix cores, which streams faster once experts see ~2.5 tokens on average (Q8_0, whose
+    // VALU form is slower, from 0.5): measured on every configured shape
+    const bool q8w = L->gate.m.type == jx::T_Q8_0;
+    auto gemv_tb = [&](int tokens_per_expert_x2) {  // twice the average tokens per expert
+        return n == 1 ? 1 : (tokens_per_expert_x2 >= (q8w ? 1 : 5) ? 16 : 4);
+    };
+    const int tb = gemv_tb(2 * nk / E);
+    const int tbs = n == 1 ? 1 : (n >= 3 ? 16 : 4);  // the shared expert sees every token
     const int tiles_ub = nk / jx::MFMA_BN + slots;
     const size_t fpad = ((size_t)L->F + 255) / 256 * 256;
     // shared expert on the side stream, concurrent with the routed gate/up
@@ -423,11 +431,11 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         } else {
             {
                 Launch l(L, "shared_gateup_gemv", ss);
-                jx::launch_gemv_gateup(L->sgate.m, L->sup.m, L->xq, sg, 1, tb, L->hqs, L->sdown_f32 ? L->hfs : nullptr,
+                jx::launch_gemv_gateup(L->sgate.m, L->sup.m, L->xq, sg, 1, tbs, L->hqs, L->sdown_f32 ? L->hfs : nullptr,
                                        ss);
             }
             Launch l(L, "shared_down", ss);
-            jx::launch_gemv_down(L->sdown.m, L->hqs, L->sdown_f32 ? L->hfs : nullptr, (int)fspad, sg, 1, tb, L->ysh,
+            jx::launch_gemv_down(L->sdown.m, L->hqs, L->sdown_f32 ? L->hfs : nullptr, (int)fspad, sg, 1, tbs, L->ysh,
                                  ss);
         }
         HIPCHK(hipEventRecord(L->ev_join, ss));

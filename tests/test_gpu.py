@@ -115,11 +115,12 @@ def test_layer_vs_golden(moe, case):
                                            ("qwen3moe", 200, "gemv"), ("qwen3moe", 96, "mfma"),
                                            ("toy", 2, "gemv"), ("qwen15moe", 2, "gemv"), ("mixtral", 2, "gemv"),
                                            ("dsv2lite", 2, "gemv"), ("qwen15moe", 1, "gemv"),
-                                           # the library's own choice around the regime thresholds: routed
-                                           # experts on the matrix cores from 6 (4-bit) or 3 (Q8_0) pairs per
-                                           # expert, the shared expert from 32 tokens
+                                           # the library's own choice around its thresholds: the 4-token and
+                                           # 16-token GEMV forms, routed experts on the GEMM from 12 (4-bit) or
+                                           # 16 (Q8_0) pairs per expert, the shared expert from 64 tokens
                                            ("qwen15moe", 40, None), ("dsv2lite", 64, None), ("mixtral", 32, None),
-                                           ("qwen3moe", 48, None), ("toy", 24, None)])
+                                           ("qwen3moe", 48, None), ("toy", 24, None), ("mixtral", 8, None),
+                                           ("qwen15moe", 70, None), ("dsv2lite", 20, None)])
 def test_layer_regimes_vs_oracle(moe, port, name, n, regime):
     say(f"{name} n={n} regime={regime}")
     cfg, lw = layer(name)
