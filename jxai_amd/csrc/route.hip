@@ -783,24 +783,39 @@ void launch_dispatch(const int* ids, int nk, int E, int top_k, const DispatchOut
 // MoE combine (transformer.cpp:2728-2730 and 2752-2754): starting from 0, for
 // each selected expert in descending-logit order acc = fma(p, y, acc), then
 // acc = fma(shared_scale, y_shared, acc).
+// Four consecutive features of one token per thread (d % 32 == 0), 16-byte loads and stores; the
+// per-feature order is k_combine's contract (fma in selection order, then the shared expert).
 __global__ void __launch_bounds__(256)
 k_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
           const float* shscale, float* out) {
-    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (size_t)n * d) return;
-    const int t = (int)(idx / d), i = (int)(idx % d);
-    float acc = 0.0f;
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;  // float4 index
+    const int d4 = d / 4;
+    if (idx >= (size_t)n * d4) return;
+    const int t = (int)(idx / d4), i = 4 * (int)(idx % d4);
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int s = 0; s < k; ++s) {
         const size_t p = (size_t)pos_of[(size_t)t * k + s];
-        acc = __builtin_fmaf(probs[(size_t)t * k + s], y[p * d + i], acc);
+        const float w = probs[(size_t)t * k + s];
+        const float4 v = *reinterpret_cast<const float4*>(y + p * d + i);
+        acc.x = __builtin_fmaf(w, v.x, acc.x);
+        acc.y = __builtin_fmaf(w, v.y, acc.y);
+        acc.z = __builtin_fmaf(w, v.z, acc.z);
+        acc.w = __builtin_fmaf(w, v.w, acc.w);
     }
-    if (ysh) acc = __builtin_fmaf(shscale[t], ysh[(size_t)t * d + i], acc);
-    out[idx] = acc;
+    if (ysh) {
+        const float w = shscale[t];
+        const float4 v = *reinterpret_cast<const float4*>(ysh + (size_t)t * d + i);
+        acc.x = __builtin_fmaf(w, v.x, acc.x);
+        acc.y = __builtin_fmaf(w, v.y, acc.y);
+        acc.z = __builtin_fmaf(w, v.z, acc.z);
+        acc.w = __builtin_fmaf(w, v.w, acc.w);
+    }
+    *reinterpret_cast<float4*>(out + (size_t)t * d + i) = acc;
 }
 
 void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
                     const float* shscale, float* out, hipStream_t st) {
-    const size_t tot = (size_t)n * d;
+    const size_t tot = (size_t)n * (d / 4);
     hipLaunchKernelGGL(k_combine, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, n, d, k, probs, pos_of, y,
                        ysh, shscale, out);
 }
