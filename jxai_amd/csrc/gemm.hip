@@ -14,14 +14,14 @@
 // accumulation.  (The exactness matters: h = SiLU(g) * u is re-quantized to
 // Q8_0 before the down projection, and a relative error of 2^-11 in g and u
 // moves ~1.4% of h's quants by one step, ~2.6e-3 relative in the layer output.)
-// What is left on the VALU:
-//   Q4_K, gate/up (one E per token)  acc += d * S once per 256-K super-block
-//   Q4_K, down    (one E per 128 K)  acc += (d 2^E) * S once per half-unit
-//   Q4_0/Q8_0                         acc += (d_b [2^E]) * D_b per 32-block
-// (S, D: MFMA sums started from zero at each scale period), plus the Q4_K min
-// term -dmin * sum_j m_j * (dx_j * sum q_j) as three bf16 MFMAs on exact
-// 3-piece splits once per super-block, straight into acc.  Only the fp32
-// summation order differs from the reference.
+// What is left on the VALU: the accumulator is kept in units of the current
+// weight scale d of its row (Q4_K: per 256-K super-block; Q4_0 / Q8_0: per
+// 32-block; 1 where d is zero, the weight operand then zeroed) and rescaled
+// by d_prev / d_cur when the period changes; the token's exponent 2^E (one
+// per row) and the last unit are applied once at the end.  The Q4_K min term
+// -dmin * sum_j m_j * (dx_j * sum q_j) is three bf16 MFMAs on exact 3-piece
+// splits once per super-block, straight into acc.  Only the fp32 rounding of
+// the accumulation differs from the reference.
 //
 // Work split: the dispatch tables cut each expert's pairs into tiles of
 // MFMA_BN = 128 (token, expert) pairs; a workgroup owns a tile (down) or half
@@ -283,7 +283,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
     // Q4_K: no per-period sums; acc is kept in units of the current
     // super-block's d (per weight row) and rescaled by d_prev / d_cur at each
     // super-block (fp32 rounding ~2^-24 per step)
-    constexpr bool RESCALE = Q4K;
+    constexpr bool RESCALE = true;
     // gate/up: exact hi + lo activation operands (h is re-quantized after SwiGLU); down: the hi
     // half only (relative error <= 2^-12 per activation, no re-quantization downstream)
     constexpr int HL = GATEUP ? 2 : 1;
@@ -369,12 +369,12 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int t = 0; t < TN; ++t) acc[i][t] = v16f{};
-    v16f sb[TM][TN];  // MFMA sums of the current scale period
 
     WRaw<TYPE> wa[TM], wb[TM];
     uint4 hdr[TM];  // Q4_K headers of the current super-block
-    float dl[TM];   // Q4_K d of the lane's row (RESCALE: the unit acc is kept in)
-    bool dz[TM];    // RESCALE: this super-block's d is zero (its sc * q terms vanish, unit 1)
+    float dl[TM];   // the unit acc is kept in for the lane's row: the current super-block's (Q4_K) or
+                    // block's (Q4_0 / Q8_0) weight scale d, 1 where d is zero
+    bool dz[TM];    // Q4_K: this super-block's d is zero (its sc * q terms vanish)
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         hdr[i] = make_uint4(0, 0, 0, 0);
@@ -505,30 +505,39 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
                 __builtin_amdgcn_sched_barrier(0);
             }
         } else {
+            // per 32-block: acc rescaled into the block's weight scale d (unit 1 and a zeroed weight
+            // operand where d is zero), then the block's MFMAs straight into acc
             const int nb = min(HB, KB - h * HB);
-            uint32_t mask, flip;
-            h2v c1, c0;
-            if (TYPE == T_Q8_0) {
-                mask = 0xFFFFFFFFu;
-                flip = 0x80808080u;
-                c1 = splat(1.0f);
-                c0 = splat(-1152.0f);
-            } else {
-                mask = g ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
-                flip = 0u;
-                c1 = splat(g ? 0.0625f : 1.0f);
-                c0 = splat(g ? -72.0f : -1032.0f);
-            }
+            const uint32_t mask = TYPE == T_Q8_0 ? 0xFFFFFFFFu : (g ? 0xF0F0F0F0u : 0x0F0F0F0Fu);
+            const uint32_t flip = TYPE == T_Q8_0 ? 0x80808080u : 0u;
+            const float k1 = TYPE == T_Q8_0 ? 1.0f : (g ? 0.0625f : 1.0f);
+            const float k0 = TYPE == T_Q8_0 ? -1152.0f : (g ? -72.0f : -1032.0f);
 #pragma unroll
             for (int j = 0; j < HB; ++j) {
                 if (j >= nb) break;
+                h2v c1[TM], c0[TM];
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    const float d = f16_to_f32(cur[i].d[j]);
+                    const bool z = d == 0.0f;
+                    const float u = z ? 1.0f : d;
+                    const float ratio = dl[i] * __builtin_amdgcn_rcpf(u);  // ~1 ulp; units only need consistency
+                    dl[i] = u;
+#pragma unroll
+                    for (int t = 0; t < TN; ++t)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[i][t][r] *= ratio;
+                    c1[i] = splat(z ? 0.0f : k1);
+                    c0[i] = splat(z ? 0.0f : k0);
+                }
 #pragma unroll
                 for (int m = 0; m < 2; ++m) {
                     h8 wv[TM], av[TN][HL];
 #pragma unroll
                     for (int i = 0; i < TM; ++i) {
                         const uint4 raw = cur[i].q[j];
-                        wv[i] = m ? cvt8(raw.z, raw.w, mask, flip, c1, c0) : cvt8(raw.x, raw.y, mask, flip, c1, c0);
+                        wv[i] = m ? cvt8(raw.z, raw.w, mask, flip, c1[i], c0[i])
+                                  : cvt8(raw.x, raw.y, mask, flip, c1[i], c0[i]);
                     }
 #pragma unroll
                     for (int t = 0; t < TN; ++t)
@@ -540,16 +549,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
 #pragma unroll
                         for (int t = 0; t < TN; ++t)
 #pragma unroll
-                            for (int i = 0; i < TM; ++i)
-                                sb[i][t] = mfma16(av[t][hl], wv[i], (m == 0 && hl == 0) ? v16f{} : sb[i][t]);
-                }
-#pragma unroll
-                for (int i = 0; i < TM; ++i) {  // fold: acc += d_b * D_b
-                    const float db = f16_to_f32(cur[i].d[j]);
-#pragma unroll
-                    for (int t = 0; t < TN; ++t)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) acc[i][t][r] = __builtin_fmaf(db, sb[i][t][r], acc[i][t][r]);
+                            for (int i = 0; i < TM; ++i) acc[i][t] = mfma16(av[t][hl], wv[i], acc[i][t]);
                 }
             }
         }
