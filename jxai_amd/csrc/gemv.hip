@@ -300,15 +300,9 @@ __device__ __forceinline__ int token_of(const Groups& g, const int4& rec, int i)
 // On the few-token path one extra block of the routed gate/up GEMV writes the
 // dispatch tables (ids, probs, shared-gate scale, counts, offsets, slots, pair
 // lists) while the others stream weights; the kernels after it read them.
-template <int NTH>
 __device__ void small_tail(const SmallTail& t, int tid) {
-    __shared__ float lgs[ROUTE_SMALL_MAX_N * SMALL_GROUP_MAX_E];  // [n][E] logits, then the histogram
-    __shared__ int rank_sel[ROUTE_SMALL_MAX_N][MAX_K];
-    __shared__ float shl[ROUTE_SMALL_MAX_N];
-    for (int i = tid; i < t.a.n * t.a.E; i += NTH) lgs[i] = t.a.logits[i];
-    if (tid < t.a.n) shl[tid] = t.a.shgate ? t.a.shscale[tid] : 0.0f;
-    __syncthreads();
-    topk_dispatch_small<NTH>(t.a, t.o, lgs, t.a.shgate ? shl : nullptr, rank_sel, tid);
+    static_assert(SMALL_GROUP_MAX_E <= 128, "two expert chunks");
+    if (tid < 64) topk_dispatch_wave<2>(t.a, t.o, t.a.logits, t.a.shgate ? t.a.shscale : nullptr);
 }
 
 // LDS bytes of one token group's staged activations.
@@ -463,7 +457,7 @@ k_gemv_gateup(QMat G, QMat U, ActQ8 xq, Groups grp, ActQ8 hq, float* hf, int hf_
     extern __shared__ __align__(16) int8_t smem[];
     __shared__ float red[WAVES][TB][32];
     if (tail.on && blockIdx.y == gridDim.y - 1) {  // the extra grid row: dispatch tables only
-        if (blockIdx.x == 0) small_tail<WAVES * 64>(tail, threadIdx.x);
+        if (blockIdx.x == 0) small_tail(tail, threadIdx.x);
         return;
     }
     const int rt = blockIdx.x;
@@ -680,7 +674,7 @@ k_gemv_mx(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_l
     extern __shared__ __align__(16) float2 msc[];   // [block][MX_NT]: (scale, sum) of each token
     __shared__ float red[WAVES][MX_NT / 2][64];
     if (GATEUP && tail.on && blockIdx.y == gridDim.y - 1) {  // the extra grid row: dispatch tables only
-        if (blockIdx.x == 0) small_tail<WAVES * 64>(tail, threadIdx.x);
+        if (blockIdx.x == 0) small_tail(tail, threadIdx.x);
         return;
     }
     const int rt = blockIdx.x;

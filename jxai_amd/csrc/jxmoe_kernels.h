@@ -88,7 +88,7 @@ struct Groups {
     const float* logits = nullptr;
     int n_experts = 0;
 };
-constexpr int SMALL_GROUP_MAX_E = 64;
+constexpr int SMALL_GROUP_MAX_E = 128;
 
 constexpr int MFMA_BN = 128;  // pairs per matrix-core GEMM tile
 // shared expert on the matrix cores from this many tokens (one dense expert fills few GEMM

@@ -110,8 +110,8 @@ __device__ void write_acth_row(const int8_t* q, const float2* sc, int K, const A
 // copy in global memory (chain_rows) uses the bare multiple of 4, and each
 // lane's run of steps then sits in a few L1 lines it revisits (measured
 // faster than interleaving the 16 chains for contiguous group loads).
-__host__ __device__ inline int rs_stride(int d) { return ((d / 16 + 3) & ~3) + 4; }
-__host__ __device__ inline int chain_stride_of(int d) { return (d / 16 + 3) & ~3; }
+__host__ __device__ constexpr int rs_stride(int d) { return ((d / 16 + 3) & ~3) + 4; }
+__host__ __device__ constexpr int chain_stride_of(int d) { return (d / 16 + 3) & ~3; }
 int chain_stride(int d) { return chain_stride_of(d); }
 
 void chain_rows(const float* rows, int nrows, int d, float* out) {
@@ -181,6 +181,7 @@ static RouteShape route_shape(const RouteArgs& a) {
     return r;
 }
 
+// rpb = 0: only steps 1-2 (the quantized and matrix-core forms of x), for k_route_rows.
 template <int T>
 __global__ void __launch_bounds__(RT_THREADS) k_route(RouteArgs a, int nsplit, int rpb) {
     extern __shared__ __align__(16) float lds[];
@@ -279,6 +280,7 @@ __global__ void __launch_bounds__(RT_THREADS) k_route(RouteArgs a, int nsplit, i
         }
     }
 
+    if (rpb == 0) return;  // block-uniform
     // -- 3. router chains of this split's rows, exact vec_dot_f32 order
     {
         const int grp = tid >> 4, j = tid & 15;
@@ -343,31 +345,125 @@ __global__ void __launch_bounds__(RT_THREADS) k_route(RouteArgs a, int nsplit, i
     for (int i = tid; i < nt * E; i += RT_THREADS) {
         const int t = i / E, e = i - t * E;
         const float* lt = lg + t * E;
-        const float le = rank_key(lt[e]);
-        int rank = 0;
-        for (int f = 0; f < E; ++f) rank += ranks_above(rank_key(lt[f]), f, le, e);
+        const int rank = rank_of(lt, E, e);
         if (rank < a.k) sel[t][rank] = e;
         if (a.logits) a.logits[(size_t)(t0 + t) * E + e] = lt[e];
     }
     __syncthreads();
-    if (tid < nt) {
-        const int t = tid, k = a.k;
-        const float* lt = lg + t * E;
-        float p[MAX_K];
-        float mx = lt[sel[t][0]];
-        for (int i = 1; i < k; ++i) mx = fmaxf(mx, lt[sel[t][i]]);
-        float sum = 0.0f;
-        for (int i = 0; i < k; ++i) {
-            p[i] = expf(lt[sel[t][i]] - mx);
-            sum += p[i];
-        }
-        const float inv = (sum > 0.0f) ? 1.0f / sum : 1.0f / (float)k;
+    static_assert(32 * T <= RT_THREADS, "one half-wave per token");
+    if (tid < 32 * nt) {
+        const int t = tid >> 5, i = tid & 31, k = a.k;
         const size_t o = (size_t)(t0 + t) * k;
-        for (int i = 0; i < k; ++i) {
-            a.ids[o + i] = sel[t][i];
-            a.probs[o + i] = p[i] * inv;
+        softmax_selected(lg + t * E, sel[t], k, i, a.ids + o, a.probs + o);
+        if (i == 0 && a.shscale) a.shscale[t0 + t] = a.shgate ? 1.0f / (1.0f + expf(-shl[t])) : 1.0f;
+    }
+}
+
+// Router logits for many tokens against a router of more than 16 rows with
+// d <= 16 * 4 * RR_M4MAX (2048): a block owns 16 rows and RR_TPB tokens.  Lane j
+// of a row's 16-lane group keeps its whole vec_dot_f32 chain of router values
+// in registers (read once), and the tokens stream through LDS four at a time,
+// chain-major, the next chunk's loads in flight while the current one is
+// consumed.  Router traffic is one read per block instead of one per 4 tokens.
+// Same chain order and reduction as k_route (src/quant.cpp:2756-2778).
+#ifndef JX_RR_TPB
+#define JX_RR_TPB 32
+#endif
+#ifndef JX_RR_TC
+#define JX_RR_TC 4
+#endif
+constexpr int RR_TPB = JX_RR_TPB;  // tokens per block
+constexpr int RR_TC = JX_RR_TC;    // tokens per LDS chunk
+constexpr int RR_M4MAX = 32;
+
+template <int M4>  // d / 64 float4 chain steps per lane
+__global__ void __launch_bounds__(RT_THREADS) k_route_rows(RouteArgs a, int nsplit) {
+    extern __shared__ __align__(16) float xs[];  // [2][RR_TC][16][S]
+    constexpr int d = 64 * M4, C4 = d / 4, S = rs_stride(d), RS = 16 * S, Sg = chain_stride_of(d);
+    constexpr int PER = (RR_TC * C4 + RT_THREADS - 1) / RT_THREADS;  // float4 per thread per chunk
+    const int split = blockIdx.x % nsplit, t0 = (blockIdx.x / nsplit) * RR_TPB;
+    const int tend = min(a.n, t0 + RR_TPB);
+    const int tid = threadIdx.x, grp = tid >> 4, j = tid & 15;
+    const int E = a.E, R = E + (a.shgate ? 1 : 0);
+    const int r = split * RT_GROUPS + grp;
+    const bool live = r < R;
+    float4 w[M4];
+    {
+        const float* wr = a.router_cm + (size_t)min(r, R - 1) * 16 * Sg + j * Sg;
+#pragma unroll
+        for (int i = 0; i < M4; ++i) w[i] = *reinterpret_cast<const float4*>(wr + 4 * i);
+    }
+    // chunk staging: RR_TC tokens x d floats; float4 c of token t holds chains 4(c%4)..4(c%4)+3 at step c/4
+    float4 v[PER];
+    auto issue = [&](int c0) {
+        const int last = min(RR_TC, tend - c0) * C4 - 1;
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i = min(u * RT_THREADS + tid, last);
+            v[u] = *reinterpret_cast<const float4*>(a.x + (size_t)c0 * d + 4 * i);
         }
-        if (a.shscale) a.shscale[t0 + t] = a.shgate ? 1.0f / (1.0f + expf(-shl[t])) : 1.0f;
+    };
+    auto store = [&](int c0, float* buf) {
+        const int last = min(RR_TC, tend - c0) * C4 - 1;
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i = min(u * RT_THREADS + tid, last);  // clamped duplicates store the same values
+            const int t = i / C4, c = i % C4;
+            float* dst = buf + t * RS + 4 * (c & 3) * S + (c >> 2);
+            dst[0] = v[u].x;
+            dst[S] = v[u].y;
+            dst[2 * S] = v[u].z;
+            dst[3 * S] = v[u].w;
+        }
+    };
+    issue(t0);
+    store(t0, xs);
+    int buf = 0;
+    for (int c0 = t0; c0 < tend; c0 += RR_TC) {
+        const int nt = min(RR_TC, tend - c0);
+        if (c0 + RR_TC < tend) issue(c0 + RR_TC);  // block-uniform
+        __syncthreads();  // chunk c0 staged; the other buffer's readers are done
+        const float* xb = xs + buf * RR_TC * RS;
+        if (live) {
+            const float* xr[RR_TC];
+#pragma unroll
+            for (int t = 0; t < RR_TC; ++t) xr[t] = xb + min(t, nt - 1) * RS + j * S;
+            float acc[RR_TC];
+#pragma unroll
+            for (int t = 0; t < RR_TC; ++t) acc[t] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < M4; ++i) {
+#pragma unroll
+                for (int t = 0; t < RR_TC; ++t) {
+                    const float4 x4 = *reinterpret_cast<const float4*>(xr[t] + 4 * i);
+                    acc[t] = __builtin_fmaf(w[i].x, x4.x, acc[t]);
+                    acc[t] = __builtin_fmaf(w[i].y, x4.y, acc[t]);
+                    acc[t] = __builtin_fmaf(w[i].z, x4.z, acc[t]);
+                    acc[t] = __builtin_fmaf(w[i].w, x4.w, acc[t]);
+                }
+            }
+            float sums[RR_TC];
+#pragma unroll
+            for (int t = 0; t < RR_TC; ++t) {
+                const float hi = __shfl_down(acc[t], 8, 16);
+                const float vv = acc[t] + hi;  // acc0[j] + acc1[j] for j < 8
+                float sum = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) sum += __shfl(vv, q, 16);
+                sums[t] = sum;
+            }
+#pragma unroll
+            for (int t = 0; t < RR_TC; ++t) {
+                const float sum = sums[t];
+                if (j == 0 && t < nt) {
+                    const size_t tok = (size_t)(c0 + t);
+                    if (r < E) a.logits[tok * E + r] = a.bias ? sum + a.bias[r] : sum;
+                    else a.shscale[tok] = sum;  // raw shared-gate logit; k_route_topk applies the sigmoid
+                }
+            }
+        }
+        if (c0 + RR_TC < tend) store(c0 + RR_TC, xs + (buf ^ 1) * RR_TC * RS);
+        buf ^= 1;
     }
 }
 
@@ -382,31 +478,50 @@ __global__ void __launch_bounds__(RT_THREADS) k_route_topk(RouteArgs a) {
     if (tid < MAX_K) sel[tid] = tid;
     __syncthreads();
     for (int e = tid; e < E; e += RT_THREADS) {
-        const float le = rank_key(lg[e]);
-        int rank = 0;
-        for (int f = 0; f < E; ++f) rank += ranks_above(rank_key(lg[f]), f, le, e);
+        const int rank = rank_of(lg, E, e);
         if (rank < k) sel[rank] = e;
     }
     __syncthreads();
-    if (tid == 0) {
-        float p[MAX_K];
-        float mx = lg[sel[0]];
-        for (int i = 1; i < k; ++i) mx = fmaxf(mx, lg[sel[i]]);
-        float sum = 0.0f;
-        for (int i = 0; i < k; ++i) {
-            p[i] = expf(lg[sel[i]] - mx);
-            sum += p[i];
-        }
-        const float inv = (sum > 0.0f) ? 1.0f / sum : 1.0f / (float)k;
-        for (int i = 0; i < k; ++i) {
-            a.ids[t * k + i] = sel[i];
-            a.probs[t * k + i] = p[i] * inv;
-        }
-        if (a.shscale) a.shscale[t] = a.shgate ? 1.0f / (1.0f + expf(-a.shscale[t])) : 1.0f;
+    if (tid < 32) {
+        softmax_selected(lg, sel, k, tid, a.ids + t * k, a.probs + t * k);
+        if (tid == 0 && a.shscale) a.shscale[t] = a.shgate ? 1.0f / (1.0f + expf(-a.shscale[t])) : 1.0f;
     }
 }
 
+static bool route_rows_fits(const RouteArgs& a) {
+    const int R = a.E + (a.shgate ? 1 : 0);
+    const int m4 = a.d / 64;
+    return R > RT_GROUPS && a.d % 64 == 0 && (m4 == 8 || m4 == 16 || m4 == 24 || m4 == 32) && a.n >= 2 * RR_TPB;
+}
+
 void launch_route(const RouteArgs& a, hipStream_t st) {
+    if (route_rows_fits(a)) {
+        // quantized / matrix-core forms of x, then the logits with register-resident router rows, then top-k
+        const int T = a.n >= 256 ? 4 : 1;
+        const size_t lq = route_lds(T, a.d, a.E);
+        auto q = T == 4 ? k_route<4> : k_route<1>;
+        if (lq > 65536)
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(q), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)lq);
+        hipLaunchKernelGGL(q, dim3((a.n + T - 1) / T), dim3(RT_THREADS), lq, st, a, 1, 0);
+        const int R = a.E + (a.shgate ? 1 : 0), RS = (R + RT_GROUPS - 1) / RT_GROUPS;
+        const size_t lr = (size_t)2 * RR_TC * 16 * rs_stride(a.d) * sizeof(float);
+        const dim3 grid(RS * ((a.n + RR_TPB - 1) / RR_TPB));
+        auto go = [&](auto kern) {
+            if (lr > 65536)
+                (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lr);
+            hipLaunchKernelGGL(kern, grid, dim3(RT_THREADS), lr, st, a, RS);
+        };
+        switch (a.d / 64) {
+            case 8: go(k_route_rows<8>); break;
+            case 16: go(k_route_rows<16>); break;
+            case 24: go(k_route_rows<24>); break;
+            default: go(k_route_rows<32>); break;
+        }
+        hipLaunchKernelGGL(k_route_topk, dim3(a.n), dim3(RT_THREADS), 0, st, a);
+        return;
+    }
     RouteShape r = route_shape(a);
     r.T = r.T >= 4 ? 4 : r.T >= 2 ? 2 : 1;  // instantiated token counts
     const size_t lds = route_lds(r.T, a.d, a.E);
@@ -592,16 +707,11 @@ k_route_small(RouteArgs a) {
     }
 }
 
-// Second launch of the few-token router: logits from k_route_small.
-__global__ void __launch_bounds__(RS_THREADS) k_topk_small(RouteArgs a, DispatchOut o) {
-    extern __shared__ float lds[];
-    __shared__ int rank_sel[ROUTE_SMALL_MAX_N][MAX_K];
-    __shared__ float shl[ROUTE_SMALL_MAX_N];
-    const int tid = threadIdx.x;
-    for (int i = tid; i < a.n * a.E; i += RS_THREADS) lds[i] = a.logits[i];
-    if (tid < a.n) shl[tid] = a.shgate ? a.shscale[tid] : 0.0f;
-    __syncthreads();
-    topk_dispatch_small<RS_THREADS>(a, o, lds, a.shgate ? shl : nullptr, rank_sel, tid);
+// Second launch of the few-token router: top-k and dispatch tables from the
+// logits of k_route_small (raw shared-gate logits in shscale), one wave.
+template <int NC>
+__global__ void __launch_bounds__(64) k_topk_small(RouteArgs a, DispatchOut o) {
+    topk_dispatch_wave<NC>(a, o, a.logits, a.shgate ? a.shscale : nullptr);
 }
 
 // The whole few-token routing in one block when the router fits in LDS
@@ -625,7 +735,6 @@ bool route_one_fits(int n, int d, int E, bool shgate) {
 
 __global__ void __launch_bounds__(R1_THREADS) k_route_one(RouteArgs a, DispatchOut o) {
     extern __shared__ float lds[];  // [rows][d] router (+ shared gate), [n][d] tokens, [n][E] logits
-    __shared__ int rank_sel[ROUTE_SMALL_MAX_N][MAX_K];
     __shared__ float shl[ROUTE_SMALL_MAX_N];
     const int tid = threadIdx.x;
     const int d = a.d, n = a.n, E = a.E, rows = E + (a.shgate ? 1 : 0);
@@ -679,7 +788,7 @@ __global__ void __launch_bounds__(R1_THREADS) k_route_one(RouteArgs a, DispatchO
         }
     }
     __syncthreads();
-    topk_dispatch_small<R1_THREADS>(a, o, lgs, a.shgate ? shl : nullptr, rank_sel, tid);
+    if (tid < 64) topk_dispatch_wave<1>(a, o, lgs, a.shgate ? shl : nullptr);
 }
 
 void launch_route_logits(const RouteArgs& a, hipStream_t st) {
@@ -702,8 +811,11 @@ void launch_route_small(const RouteArgs& a, const DispatchOut& o, hipStream_t st
         (void)hipGetLastError();  // clear the refused opt-in
     }
     hipLaunchKernelGGL(k_route_small, dim3(rows), dim3(RS_THREADS), rs_lds(a.n, a.d), st, a);
-    hipLaunchKernelGGL(k_topk_small, dim3(1), dim3(RS_THREADS), (size_t)std::max(a.n, 2) * a.E * sizeof(float), st, a,
-                       o);
+    const int nc = (a.E + 63) / 64;
+    if (nc <= 1) hipLaunchKernelGGL(k_topk_small<1>, dim3(1), dim3(64), 0, st, a, o);
+    else if (nc <= 2) hipLaunchKernelGGL(k_topk_small<2>, dim3(1), dim3(64), 0, st, a, o);
+    else if (nc <= 4) hipLaunchKernelGGL(k_topk_small<4>, dim3(1), dim3(64), 0, st, a, o);
+    else hipLaunchKernelGGL(k_topk_small<MAX_E / 64>, dim3(1), dim3(64), 0, st, a, o);
 }
 
 // One block per expert.  Every block builds the full per-expert histogram in
@@ -711,68 +823,155 @@ void launch_route_small(const RouteArgs& a, const DispatchOut& o, hipStream_t st
 // offset, MFMA tile offset and active-list slot, then writes the positions of
 // its (token, slot) pairs in flat order -- a stable counting sort, so tokens
 // keep their order inside each expert.
+//  - histogram: four ids per thread per 16-byte load; up to 16 experts by
+//    wave ballots (LDS atomics on so few bins would serialize), else LDS atomics;
+//  - positions: rounds of DP_ROUND ids, each wave a contiguous quarter: one
+//    pass records the matches as a 64-bit mask per lane (4 ids x DP_U loads),
+//    one barrier exchanges the wave totals, and the writes follow the masks
+//    in flat order (lane prefixes from three ballots of the per-lane count).
 constexpr int DISPATCH_THREADS = 256;
+constexpr int DP_U = 16;                                 // 16-byte id loads per lane per round
+constexpr int DP_WAVE = 64 * 4 * DP_U;                   // ids per wave per round
+constexpr int DP_ROUND = DISPATCH_THREADS / 64 * DP_WAVE;  // 16384
+
+__device__ __forceinline__ int4 load_ids4(const int* ids, int f, int nk) {
+    if (f + 3 < nk) return *reinterpret_cast<const int4*>(ids + f);  // ids 16-byte aligned, f % 4 == 0
+    return make_int4(f < nk ? ids[f] : -1, f + 1 < nk ? ids[f + 1] : -1, f + 2 < nk ? ids[f + 2] : -1, -1);
+}
 
 __global__ void __launch_bounds__(DISPATCH_THREADS)
 k_dispatch(const int* ids, int nk, int E, int top_k, DispatchOut o) {
     extern __shared__ int hist[];
-    __shared__ int wtot[DISPATCH_THREADS / 64];
-    __shared__ int s_off, s_toff, s_na;
+    __shared__ int red[3][DISPATCH_THREADS / 64];
+    __shared__ int wtot[2][DISPATCH_THREADS / 64];
     const int e = blockIdx.x;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int NW = DISPATCH_THREADS / 64;
     for (int i = tid; i < E; i += DISPATCH_THREADS) hist[i] = 0;
     __syncthreads();
-    for (int f = tid; f < nk; f += DISPATCH_THREADS) atomicAdd(&hist[ids[f]], 1);
-    __syncthreads();
-    if (tid == 0) {
-        int off = 0, toff = 0, na = 0;
-        for (int i = 0; i < e; ++i) {
-            off += hist[i];
-            toff += (hist[i] + MFMA_BN - 1) / MFMA_BN;
-            na += hist[i] > 0;
+    if (E <= 16) {
+        // per-thread 8-bit counters (experts 0-7 in lo, 8-15 in hi), flushed before any can reach 256
+        uint64_t lo = 0, hi = 0;
+        int since = 0;
+        auto flush = [&]() {
+            for (int x = 0; x < E; ++x) {  // wave-uniform
+                int c = (int)(((x < 8 ? lo : hi) >> (8 * (x & 7))) & 255u);
+#pragma unroll
+                for (int m = 32; m >= 1; m >>= 1) c += __shfl_xor(c, m, 64);
+                if (lane == 0) atomicAdd(&hist[x], c);
+            }
+            lo = hi = 0;
+        };
+        auto count = [&](int id) {
+            const uint64_t one = 1ull << (8 * (id & 7));
+            lo += id >= 0 && id < 8 ? one : 0ull;
+            hi += id >= 8 ? one : 0ull;
+        };
+        for (int base = wave * 256; base < nk; base += DISPATCH_THREADS * 4) {  // wave-uniform
+            const int4 v = load_ids4(ids, base + 4 * lane, nk);
+            count(v.x);
+            count(v.y);
+            count(v.z);
+            count(v.w);
+            if (++since == 63) {  // 63 * 4 = 252 per counter at most
+                flush();
+                since = 0;
+            }
         }
-        s_off = off;
-        s_toff = toff;
-        s_na = na;
-        const int c = hist[e];
-        o.counts[e] = c;
-        o.offs[e] = off;
-        if (c > 0) o.act[na] = e;
-        else o.slots[E - 1 - (e - na)] = make_int4(0, 0, 0, 0);  // inactive experts fill slots n_act..E-1
-        if (e == E - 1) {
-            o.offs[E] = off + c;
-            *o.n_act = na + (c > 0);
-            *o.n_tiles = toff + (c + MFMA_BN - 1) / MFMA_BN;
+        flush();
+    } else {
+        for (int f = 4 * tid; f < nk; f += 4 * DISPATCH_THREADS) {
+            const int4 v = load_ids4(ids, f, nk);
+            atomicAdd(&hist[v.x], 1);
+            if (v.y >= 0) atomicAdd(&hist[v.y], 1);
+            if (v.z >= 0) atomicAdd(&hist[v.z], 1);
+            if (v.w >= 0) atomicAdd(&hist[v.w], 1);
         }
     }
     __syncthreads();
+    // pair offset, tile offset and active index of expert e: sums over the experts before it
+    int off = 0, toff = 0, na = 0;
+    for (int i = tid; i < e; i += DISPATCH_THREADS) {
+        const int c = hist[i];
+        off += c;
+        toff += (c + MFMA_BN - 1) / MFMA_BN;
+        na += c > 0;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        off += __shfl_xor(off, m, 64);
+        toff += __shfl_xor(toff, m, 64);
+        na += __shfl_xor(na, m, 64);
+    }
+    if (lane == 0) {
+        red[0][wave] = off;
+        red[1][wave] = toff;
+        red[2][wave] = na;
+    }
+    __syncthreads();
+    off = toff = na = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        off += red[0][w];
+        toff += red[1][w];
+        na += red[2][w];
+    }
     const int cnt = hist[e];
-    const int off = s_off;
+    if (tid == 0) {
+        o.counts[e] = cnt;
+        o.offs[e] = off;
+        if (cnt > 0) o.act[na] = e;
+        else o.slots[E - 1 - (e - na)] = make_int4(0, 0, 0, 0);  // inactive experts fill slots n_act..E-1
+        if (e == E - 1) {
+            o.offs[E] = off + cnt;
+            *o.n_act = na + (cnt > 0);
+            *o.n_tiles = toff + (cnt + MFMA_BN - 1) / MFMA_BN;
+        }
+    }
     for (int i = tid; i * MFMA_BN < cnt; i += DISPATCH_THREADS)
-        o.tiles[s_toff + i] = make_int4(e, off + i * MFMA_BN, min(MFMA_BN, cnt - i * MFMA_BN), 0);
-    if (cnt == 0) return;
-    const int lane = tid & 63, wave = tid >> 6;
-    int run = 0;
-    for (int base = 0; base < nk; base += DISPATCH_THREADS) {
-        const int f = base + tid;
-        const bool pred = f < nk && ids[f] == e;
-        const unsigned long long m = __ballot(pred);
-        const int lp = __popcll(m & ((1ull << lane) - 1ull));
-        if (lane == 0) wtot[wave] = __popcll(m);
-        __syncthreads();
-        int woff = 0, tot = 0;
-        for (int w = 0; w < DISPATCH_THREADS / 64; ++w) {
-            woff += (w < wave) ? wtot[w] : 0;
-            tot += wtot[w];
+        o.tiles[toff + i] = make_int4(e, off + i * MFMA_BN, min(MFMA_BN, cnt - i * MFMA_BN), 0);
+    if (cnt == 0) return;  // block-uniform
+    const uint64_t lt_mask = (1ull << lane) - 1ull;
+    int run = off;
+    for (int r0 = 0, par = 0; r0 < nk; r0 += DP_ROUND, par ^= 1) {
+        const int wbase = r0 + wave * DP_WAVE;
+        uint64_t bits = 0;  // bit 4u + c: id wbase + 256u + 4 lane + c is expert e
+#pragma unroll
+        for (int u = 0; u < DP_U; ++u) {
+            const int4 v = load_ids4(ids, wbase + 256 * u + 4 * lane, nk);
+            const uint32_t m = (v.x == e) | (v.y == e) << 1 | (v.z == e) << 2 | (v.w == e) << 3;
+            bits |= (uint64_t)m << (4 * u);
         }
-        if (pred) {
-            const int p = off + run + woff + lp;
-            o.pair_tok[p] = f / top_k;
-            o.pos_of[f] = p;
-            if (p == off) o.slots[s_na] = make_int4(e, off, cnt, f / top_k);
+        int wt = __popcll(bits);
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) wt += __shfl_xor(wt, m, 64);
+        if (lane == 0) wtot[par][wave] = wt;
+        __syncthreads();  // wtot[par] complete; the previous round's readers of wtot[par ^ 1] are done
+        int p = run, total = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            p += w < wave ? wtot[par][w] : 0;
+            total += wtot[par][w];
         }
-        run += tot;
-        __syncthreads();
+        for (int u = 0; u < DP_U; ++u) {
+            const uint32_t m = (uint32_t)(bits >> (4 * u)) & 15u;
+            if (__ballot(m != 0) == 0) continue;  // wave-uniform
+            const int c = __popc(m);
+            const uint64_t b0 = __ballot(c & 1), b1 = __ballot(c & 2), b2 = __ballot(c & 4);
+            int q = p + __popcll(b0 & lt_mask) + 2 * __popcll(b1 & lt_mask) + 4 * __popcll(b2 & lt_mask);
+            const int f0 = wbase + 256 * u + 4 * lane;
+            for (int x = 0; x < 4; ++x) {
+                if ((m >> x) & 1u) {
+                    const int f = f0 + x;
+                    o.pair_tok[q] = f / top_k;
+                    o.pos_of[f] = q;
+                    if (q == off) o.slots[na] = make_int4(e, off, cnt, f / top_k);
+                    ++q;
+                }
+            }
+            p += __popcll(b0) + 2 * __popcll(b1) + 4 * __popcll(b2);
+        }
+        run += total;
     }
 }
 

@@ -120,7 +120,11 @@ def test_layer_vs_golden(moe, case):
                                            # 16 (Q8_0) pairs per expert, the shared expert from 64 tokens
                                            ("qwen15moe", 40, None), ("dsv2lite", 64, None), ("mixtral", 32, None),
                                            ("qwen3moe", 48, None), ("toy", 24, None), ("mixtral", 8, None),
-                                           ("qwen15moe", 70, None), ("dsv2lite", 20, None)])
+                                           ("qwen15moe", 70, None), ("dsv2lite", 20, None),
+                                           # 128 experts at one and two tokens: groups from the logits
+                                           ("qwen3moe", 1, None), ("qwen3moe", 2, None),
+                                           # few tokens on the matrix-core path: top-k in its own launch
+                                           ("qwen3moe", 1, "mfma"), ("qwen15moe", 2, "mfma")])
 def test_layer_regimes_vs_oracle(moe, port, name, n, regime):
     say(f"{name} n={n} regime={regime}")
     cfg, lw = layer(name)
@@ -186,6 +190,46 @@ def test_edge_cases(moe, port):
         assert np.array_equal(c, [70, 70])
         assert rel_err(o, want2) <= REL_TOL
     L2.close()
+
+
+@pytest.mark.parametrize("E", [100, 128, 200])
+def test_decode_ties_many_experts(moe, port, E):
+    """More than 64 experts at one and two tokens (groups derived from the logits in the GEMV up to
+    128 experts, a separate top-k launch above): all-equal logits select the lowest indices in index
+    order; random tokens match the oracle."""
+    cfg = synth.LayerConfig(f"ties{E}", 256, E, 6, 256, F.Q4_0)
+    lw = synth.make_layer(cfg, seed=E)
+    L = moe.MoELayer.from_weights(lw)
+    for n in (1, 2):
+        say(f"ties E={E} n={n}")
+        x = np.zeros((n, 256), np.float32)
+        out, ids, w, counts = L.forward(x)
+        assert np.array_equal(ids, np.tile(np.arange(6, dtype=np.int32), (n, 1)))
+        x = synth.make_tokens(cfg, n, seed=n)
+        out, ids, w, counts = L.forward(x)
+        lg_o, ids_o, w_o = port.route(lw, x)
+        assert np.array_equal(ids, ids_o)
+        assert rel_err(out, port.moe_forward(lw, x)[0]) <= REL_TOL
+    L.close()
+
+
+@pytest.mark.parametrize("E,k,n", [(8, 2, 33000), (32, 4, 5000), (40, 6, 2900)])
+def test_dispatch_many_pairs(moe, port, E, k, n):
+    """More (token, expert) pairs than one pass of the dispatch holds (16384), and for few experts more
+    than its per-thread 8-bit counters hold before a flush (64512): counts, ids and sampled outputs."""
+    say(f"dispatch E={E} k={k} n={n}")
+    cfg = synth.LayerConfig(f"wide{E}", 256, E, k, 256, F.Q4_0)
+    lw = synth.make_layer(cfg, seed=E)
+    L = moe.MoELayer.from_weights(lw)
+    x = synth.make_tokens(cfg, n, seed=E + 1)
+    out, ids, w, counts = L.forward(x)
+    lg_o, ids_o, w_o = port.route(lw, x)
+    assert np.array_equal(ids, ids_o)
+    assert np.array_equal(counts, np.bincount(ids_o.reshape(-1), minlength=E))
+    sel = np.unique(np.linspace(0, n - 1, 8).astype(np.int32))
+    want = port.moe_forward(lw, x, sel)[0]
+    assert rel_err(out[sel], want) <= REL_TOL
+    L.close()
 
 
 @pytest.mark.parametrize("name", ["toy", "qwen15moe", "mixtral"])
