@@ -426,7 +426,9 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
                 // min term, once per super-block: acc += sum_j (dx_j sum q_j) (-dmin m_j / unit) on bf16
                 // 3-piece splits (the activation side in xm, the weight side from the min table); six of
                 // the nine piece products (all above 2^-24 relative) in three MFMAs, (MFMA, lane half) ->
-                // (activation piece, weight piece): (0,0) h.h (0,1) m.h (1,0) h.m (1,1) l.h (2,0) h.l (2,1) m.m
+                // (activation piece, weight piece): (0,0) h.h (0,1) m.h (1,0) h.m (1,1) l.h (2,0) h.l (2,1) m.m.
+                // The down projection drops the third (h.l and m.m, ~2^-16 relative each): its hi-only
+                // activations already carry 2^-12, and nothing downstream re-quantizes.
                 const uint16_t* xm = sm.st[1].xm + pbase * 8;
 #pragma unroll
                 for (int i = 0; i < TM; ++i) {
@@ -440,7 +442,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
                         const b8 x1 = *reinterpret_cast<const b8*>(xm + (g ? 2 : 0) * BN * 8 + pr * 8);
                         acc[i][t] = mfma16b(x0, wm[0], acc[i][t]);
                         acc[i][t] = mfma16b(x1, wm[1], acc[i][t]);
-                        acc[i][t] = mfma16b(x0, wm[2], acc[i][t]);
+                        if constexpr (GATEUP) acc[i][t] = mfma16b(x0, wm[2], acc[i][t]);
                     }
                 }
             }

@@ -92,68 +92,82 @@ __device__ __forceinline__ uint64_t wave_max_key(uint64_t x) {
     return ((uint64_t)hi << 32) | lo;
 }
 
-// Top-k + softmax (select_experts_cache_aware, src/tier.cpp:144-188) and the
-// dispatch tables for n <= ROUTE_SMALL_MAX_N tokens, by ONE wave (all 64
-// lanes; no barriers, no LDS), NC = ceil(E / 64) <= MAX_E / 64 expert chunks.
-// lg: the [n][E] logits (global or LDS), shl: raw shared-gate logit per token
-// (null: no shared gate).  Per token: k rounds of the wave argmax (order:
-// logit descending, index ascending, NaN as -inf) give the selection in rank
-// order; the softmax folds the max and the sum in that order as the reference
-// does.  The tables follow from the selection masks: an expert's pair offset
-// and active index are popcounts of the masks below it, pairs ordered by
-// (expert, token).
+// Top-k + softmax of one token (select_experts_cache_aware,
+// src/tier.cpp:144-188) by ONE wave (all 64 lanes), NC = ceil(E / 64) <=
+// MAX_E / 64 expert chunks; lt: the token's E logits (global or LDS), shl:
+// its raw shared-gate logit (null: no shared gate).  k rounds of the wave
+// argmax (order: logit descending, index ascending, NaN as -inf) give the
+// selection in rank order; the softmax folds the max and the sum in that
+// order as the reference does.  Writes ids, probs and the shared-gate scale
+// of token t; returns the selection mask and, on lane r < k, the expert of
+// rank r.
+template <int NC>
+__device__ __forceinline__ int topk_token_wave(const RouteArgs& a, const float* lt, size_t t, const float* shl,
+                                               uint64_t (&msk)[NC]) {
+    static_assert(NC * 64 <= MAX_E, "expert chunks");
+    constexpr float NEG = -__builtin_inff();
+    const int lane = threadIdx.x & 63, E = a.E, k = a.k;
+    float raw[NC], key[NC];
+    uint32_t cand = 0;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int e = 64 * c + lane;
+        raw[c] = e < E ? lt[e] : 0.0f;
+        key[c] = e < E ? rank_key(raw[c]) : NEG;
+        cand |= e < E ? 1u << c : 0u;
+        msk[c] = 0;
+    }
+    float myl = 0.0f, mx = 0.0f;
+    int myid = 0;
+    for (int r = 0; r < k; ++r) {
+        uint64_t best = 0;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {  // the lane's best remaining candidate
+            const uint64_t kc = ((cand >> c) & 1u) ? sel_key(key[c], 64 * c + lane) : 0ull;
+            best = kc > best ? kc : best;
+        }
+        const int bi = sel_expert(wave_max_key(best));
+        const int bc = bi >> 6, bl = bi & 63;
+        float rv = raw[0];
+#pragma unroll
+        for (int c = 1; c < NC; ++c) rv = c == bc ? raw[c] : rv;
+        const float l = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rv), bl));
+        mx = r == 0 ? l : fmaxf(mx, l);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) msk[c] |= c == bc ? 1ull << bl : 0ull;
+        cand &= lane == bl ? ~(1u << bc) : ~0u;
+        myl = lane == r ? l : myl;
+        myid = lane == r ? bi : myid;
+    }
+    const float p = expf(myl - mx);
+    float sum = 0.0f;
+    for (int r = 0; r < k; ++r) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), r));
+    const float inv = (sum > 0.0f) ? 1.0f / sum : 1.0f / (float)k;
+    if (lane < k) {
+        a.ids[t * k + lane] = myid;
+        a.probs[t * k + lane] = p * inv;
+    }
+    if (lane == 0 && a.shscale) a.shscale[t] = shl ? 1.0f / (1.0f + expf(-shl[t])) : 1.0f;
+    return myid;
+}
+
+// Top-k + softmax and the dispatch tables for n <= ROUTE_SMALL_MAX_N tokens,
+// by ONE wave (all 64 lanes; no barriers, no LDS).  lg: the [n][E] logits,
+// shl: raw shared-gate logit per token (null: no shared gate).  The tables
+// follow from the selection masks: an expert's pair offset and active index
+// are popcounts of the masks below it, pairs ordered by (expert, token).
 template <int NC>
 __device__ void topk_dispatch_wave(const RouteArgs& a, const DispatchOut& o, const float* lg, const float* shl) {
     static_assert(ROUTE_SMALL_MAX_N <= 2 && NC * 64 <= MAX_E, "few-token tables");
-    constexpr float NEG = -__builtin_inff();
     const int lane = threadIdx.x & 63, n = a.n, E = a.E, k = a.k;
     uint64_t msk[ROUTE_SMALL_MAX_N][NC];
+    int sid[ROUTE_SMALL_MAX_N];  // lane r < k: the expert of rank r of each token
 #pragma unroll
     for (int t = 0; t < ROUTE_SMALL_MAX_N; ++t) {
+        sid[t] = 0;
 #pragma unroll
         for (int c = 0; c < NC; ++c) msk[t][c] = 0;
-        if (t >= n) continue;  // uniform
-        const float* lt = lg + (size_t)t * E;
-        float raw[NC], key[NC];
-        uint32_t cand = 0;
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const int e = 64 * c + lane;
-            raw[c] = e < E ? lt[e] : 0.0f;
-            key[c] = e < E ? rank_key(raw[c]) : NEG;
-            cand |= e < E ? 1u << c : 0u;
-        }
-        float myl = 0.0f, mx = 0.0f;
-        int myid = 0;
-        for (int r = 0; r < k; ++r) {
-            uint64_t best = 0;
-#pragma unroll
-            for (int c = 0; c < NC; ++c) {  // the lane's best remaining candidate
-                const uint64_t kc = ((cand >> c) & 1u) ? sel_key(key[c], 64 * c + lane) : 0ull;
-                best = kc > best ? kc : best;
-            }
-            const int bi = sel_expert(wave_max_key(best));
-            const int bc = bi >> 6, bl = bi & 63;
-            float rv = raw[0];
-#pragma unroll
-            for (int c = 1; c < NC; ++c) rv = c == bc ? raw[c] : rv;
-            const float l = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rv), bl));
-            mx = r == 0 ? l : fmaxf(mx, l);
-#pragma unroll
-            for (int c = 0; c < NC; ++c) msk[t][c] |= c == bc ? 1ull << bl : 0ull;
-            cand &= lane == bl ? ~(1u << bc) : ~0u;
-            myl = lane == r ? l : myl;
-            myid = lane == r ? bi : myid;
-        }
-        const float p = expf(myl - mx);
-        float sum = 0.0f;
-        for (int r = 0; r < k; ++r) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), r));
-        const float inv = (sum > 0.0f) ? 1.0f / sum : 1.0f / (float)k;
-        if (lane < k) {
-            a.ids[(size_t)t * k + lane] = myid;
-            a.probs[(size_t)t * k + lane] = p * inv;
-        }
-        if (lane == 0 && a.shscale) a.shscale[t] = shl ? 1.0f / (1.0f + expf(-shl[t])) : 1.0f;
+        if (t < n) sid[t] = topk_token_wave<NC>(a, lg + (size_t)t * E, (size_t)t, shl, msk[t]);  // uniform
     }
     // ---- dispatch from the masks
     const uint64_t below = (1ull << lane) - 1ull;
@@ -203,7 +217,7 @@ __device__ void topk_dispatch_wave(const RouteArgs& a, const DispatchOut& o, con
 #pragma unroll
     for (int t = 0; t < ROUTE_SMALL_MAX_N; ++t) {
         if (t >= n || lane >= k) continue;
-        const int e = a.ids[(size_t)t * k + lane];  // written above by this lane
+        const int e = sid[t];
         const int ec = e >> 6;
         const uint64_t eb = (1ull << (e & 63)) - 1ull;
         int p = 0, first_token_has = 0;

@@ -360,7 +360,7 @@ __global__ void __launch_bounds__(RT_THREADS) k_route(RouteArgs a, int nsplit, i
 }
 
 // Router logits for many tokens against a router of more than 16 rows with
-// d <= 16 * 4 * RR_M4MAX (2048): a block owns 16 rows and RR_TPB tokens.  Lane j
+// d <= 2048 (d / 64 in 8, 16, 24, 32): a block owns 16 rows and RR_TPB tokens.  Lane j
 // of a row's 16-lane group keeps its whole vec_dot_f32 chain of router values
 // in registers (read once), and the tokens stream through LDS four at a time,
 // chain-major, the next chunk's loads in flight while the current one is
@@ -374,7 +374,6 @@ __global__ void __launch_bounds__(RT_THREADS) k_route(RouteArgs a, int nsplit, i
 #endif
 constexpr int RR_TPB = JX_RR_TPB;  // tokens per block
 constexpr int RR_TC = JX_RR_TC;    // tokens per LDS chunk
-constexpr int RR_M4MAX = 32;
 
 template <int M4>  // d / 64 float4 chain steps per lane
 __global__ void __launch_bounds__(RT_THREADS) k_route_rows(RouteArgs a, int nsplit) {
@@ -467,25 +466,23 @@ __global__ void __launch_bounds__(RT_THREADS) k_route_rows(RouteArgs a, int nspl
     }
 }
 
-// Step 4 for split routers: one block of RT_THREADS per token, logits from
-// global memory (the same rank counting and softmax as in k_route).
-__global__ void __launch_bounds__(RT_THREADS) k_route_topk(RouteArgs a) {
-    __shared__ float lg[MAX_E];
-    __shared__ int sel[MAX_K];
-    const size_t t = blockIdx.x;
-    const int tid = threadIdx.x, E = a.E, k = a.k;
-    for (int e = tid; e < E; e += RT_THREADS) lg[e] = a.logits[t * E + e];
-    if (tid < MAX_K) sel[tid] = tid;
-    __syncthreads();
-    for (int e = tid; e < E; e += RT_THREADS) {
-        const int rank = rank_of(lg, E, e);
-        if (rank < k) sel[rank] = e;
-    }
-    __syncthreads();
-    if (tid < 32) {
-        softmax_selected(lg, sel, k, tid, a.ids + t * k, a.probs + t * k);
-        if (tid == 0 && a.shscale) a.shscale[t] = a.shgate ? 1.0f / (1.0f + expf(-a.shscale[t])) : 1.0f;
-    }
+// Top-k and softmax once every split has written its logits (raw shared-gate
+// logits in shscale): one wave per token, four tokens per block.
+template <int NC>
+__global__ void __launch_bounds__(256) k_route_topk(RouteArgs a) {
+    const size_t t = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= (size_t)a.n) return;  // wave-uniform
+    uint64_t msk[NC];
+    (void)topk_token_wave<NC>(a, a.logits + t * a.E, t, a.shgate ? a.shscale : nullptr, msk);
+}
+
+static void launch_route_topk(const RouteArgs& a, hipStream_t st) {
+    const dim3 grid((a.n + 3) / 4);
+    const int nc = (a.E + 63) / 64;
+    if (nc <= 1) hipLaunchKernelGGL(k_route_topk<1>, grid, dim3(256), 0, st, a);
+    else if (nc <= 2) hipLaunchKernelGGL(k_route_topk<2>, grid, dim3(256), 0, st, a);
+    else if (nc <= 4) hipLaunchKernelGGL(k_route_topk<4>, grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(k_route_topk<MAX_E / 64>, grid, dim3(256), 0, st, a);
 }
 
 static bool route_rows_fits(const RouteArgs& a) {
@@ -519,7 +516,7 @@ void launch_route(const RouteArgs& a, hipStream_t st) {
             case 24: go(k_route_rows<24>); break;
             default: go(k_route_rows<32>); break;
         }
-        hipLaunchKernelGGL(k_route_topk, dim3(a.n), dim3(RT_THREADS), 0, st, a);
+        launch_route_topk(a, st);
         return;
     }
     RouteShape r = route_shape(a);
@@ -537,7 +534,7 @@ void launch_route(const RouteArgs& a, hipStream_t st) {
         case 2: go(k_route<2>); break;
         default: go(k_route<1>); break;
     }
-    if (r.RS > 1) hipLaunchKernelGGL(k_route_topk, dim3(a.n), dim3(RT_THREADS), 0, st, a);
+    if (r.RS > 1) launch_route_topk(a, st);
 }
 
 // Matrix-core form of Q8_0 activations already in global memory, one block per row.
@@ -825,14 +822,12 @@ void launch_route_small(const RouteArgs& a, const DispatchOut& o, hipStream_t st
 // keep their order inside each expert.
 //  - histogram: four ids per thread per 16-byte load; up to 16 experts by
 //    wave ballots (LDS atomics on so few bins would serialize), else LDS atomics;
-//  - positions: rounds of DP_ROUND ids, each wave a contiguous quarter: one
-//    pass records the matches as a 64-bit mask per lane (4 ids x DP_U loads),
+//  - positions: rounds of up to 4 x DP_U x 256 ids, each wave a contiguous quarter:
+//    one pass records the matches as a 64-bit mask per lane (4 ids x DP_U loads),
 //    one barrier exchanges the wave totals, and the writes follow the masks
 //    in flat order (lane prefixes from three ballots of the per-lane count).
 constexpr int DISPATCH_THREADS = 256;
-constexpr int DP_U = 16;                                 // 16-byte id loads per lane per round
-constexpr int DP_WAVE = 64 * 4 * DP_U;                   // ids per wave per round
-constexpr int DP_ROUND = DISPATCH_THREADS / 64 * DP_WAVE;  // 16384
+constexpr int DP_U = 16;  // 16-byte id loads per lane per round, at most
 
 __device__ __forceinline__ int4 load_ids4(const int* ids, int f, int nk) {
     if (f + 3 < nk) return *reinterpret_cast<const int4*>(ids + f);  // ids 16-byte aligned, f % 4 == 0
@@ -932,15 +927,19 @@ k_dispatch(const int* ids, int nk, int E, int top_k, DispatchOut o) {
         o.tiles[toff + i] = make_int4(e, off + i * MFMA_BN, min(MFMA_BN, cnt - i * MFMA_BN), 0);
     if (cnt == 0) return;  // block-uniform
     const uint64_t lt_mask = (1ull << lane) - 1ull;
+    // loads per lane and round: up to DP_U, fewer when the pairs fit, so every wave takes a share
+    const int U = min(DP_U, (nk + NW * 256 - 1) / (NW * 256));
     int run = off;
-    for (int r0 = 0, par = 0; r0 < nk; r0 += DP_ROUND, par ^= 1) {
-        const int wbase = r0 + wave * DP_WAVE;
+    for (int r0 = 0, par = 0; r0 < nk; r0 += NW * 256 * U, par ^= 1) {
+        const int wbase = r0 + wave * 256 * U;
         uint64_t bits = 0;  // bit 4u + c: id wbase + 256u + 4 lane + c is expert e
 #pragma unroll
         for (int u = 0; u < DP_U; ++u) {
-            const int4 v = load_ids4(ids, wbase + 256 * u + 4 * lane, nk);
-            const uint32_t m = (v.x == e) | (v.y == e) << 1 | (v.z == e) << 2 | (v.w == e) << 3;
-            bits |= (uint64_t)m << (4 * u);
+            if (u < U) {  // uniform
+                const int4 v = load_ids4(ids, wbase + 256 * u + 4 * lane, nk);
+                const uint32_t m = (v.x == e) | (v.y == e) << 1 | (v.z == e) << 2 | (v.w == e) << 3;
+                bits |= (uint64_t)m << (4 * u);
+            }
         }
         int wt = __popcll(bits);
 #pragma unroll
@@ -953,7 +952,7 @@ k_dispatch(const int* ids, int nk, int E, int top_k, DispatchOut o) {
             p += w < wave ? wtot[par][w] : 0;
             total += wtot[par][w];
         }
-        for (int u = 0; u < DP_U; ++u) {
+        for (int u = 0; u < U; ++u) {
             const uint32_t m = (uint32_t)(bits >> (4 * u)) & 15u;
             if (__ballot(m != 0) == 0) continue;  // wave-uniform
             const int c = __popc(m);
