@@ -293,7 +293,13 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
     static_assert(PER * PPI * GW == BN, "staging split");
     __shared__ GemmSmem<HL, BN> sm;
     int ti, sub, rg;
-    work_item(blockIdx.x, n_items, R, MFMA_BN / BN, RC, ti, sub, rg);
+    // the grid covers the tile upper bound; the items of the tiles that exist are spread over the XCDs
+    // as if the grid were exact, and the rest exit (otherwise the XCDs whose ranges hold the missing
+    // tiles would idle)
+    int n_eff = n_items;
+    if (!grp.identity) n_eff = min(n_items, R * *grp.n_tiles * (MFMA_BN / BN));
+    if ((int)(blockIdx.x >> 3) >= (n_eff >> 3) + ((int)(blockIdx.x & 7) < (n_eff & 7) ? 1 : 0)) return;
+    work_item(blockIdx.x, n_eff, R, MFMA_BN / BN, RC, ti, sub, rg);
     int e, p0, cnt;
     if (!pair_tile(grp, ti, e, p0, cnt)) return;  // whole workgroup
     p0 += sub * BN;  // this workgroup's part of the tile
@@ -364,16 +370,25 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
         mo[i] = WRaw<TYPE>::moff(W, rt, n);
     }
 
-    v16f acc[TM][TN];
+    // Q4_0 / Q8_0 down: two accumulator sets, acc for even 32-blocks and acc2 for odd ones, each in its own
+    // unit (down only: with gate/up's two weight tiles per wave the second set spills, 394 -> 702 us)
+    constexpr bool DUAL = !Q4K && !GATEUP;
+    constexpr int TM2 = DUAL ? TM : 1, TN2 = DUAL ? TN : 1;
+    v16f acc[TM][TN], acc2[TM2][TN2];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int t = 0; t < TN; ++t) acc[i][t] = v16f{};
+#pragma unroll
+    for (int i = 0; i < TM2; ++i)
+#pragma unroll
+        for (int t = 0; t < TN2; ++t) acc2[i][t] = v16f{};
 
     WRaw<TYPE> wa[TM], wb[TM];
     uint4 hdr[TM];  // Q4_K headers of the current super-block
     float dl[TM];   // the unit acc is kept in for the lane's row: the current super-block's (Q4_K) or
                     // block's (Q4_0 / Q8_0) weight scale d, 1 where d is zero
+    float dl2[TM2]; // the unit of acc2
     bool dz[TM];    // Q4_K: this super-block's d is zero (its sc * q terms vanish)
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -381,6 +396,8 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
         dl[i] = RESCALE ? 1.0f : 0.0f;
         dz[i] = false;
     }
+#pragma unroll
+    for (int i = 0; i < TM2; ++i) dl2[i] = 1.0f;
     if (active)
 #pragma unroll
         for (int i = 0; i < TM; ++i) wa[i].load(qbase[i], sbase[i], mbase[i], qo[i], so[i], mo[i], 0, min(HB, KB));
@@ -507,28 +524,27 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
                 __builtin_amdgcn_sched_barrier(0);
             }
         } else {
-            // per 32-block: acc rescaled into the block's weight scale d (unit 1 and a zeroed weight
-            // operand where d is zero), then the block's MFMAs straight into acc
-            const int nb = min(HB, KB - h * HB);
+            // per 32-block: the block's accumulator set (acc for even blocks, acc2 for odd) rescaled into
+            // the block's weight scale d (unit 1 and a zeroed weight operand where d is zero), then the
+            // block's MFMAs straight into it. With two sets, one set's rescale does not wait for MFMAs
+            // still writing the other, and the MFMAs of one block overlap the rescale of the next.
             const uint32_t mask = TYPE == T_Q8_0 ? 0xFFFFFFFFu : (g ? 0xF0F0F0F0u : 0x0F0F0F0Fu);
             const uint32_t flip = TYPE == T_Q8_0 ? 0x80808080u : 0u;
             const float k1 = TYPE == T_Q8_0 ? 1.0f : (g ? 0.0625f : 1.0f);
             const float k0 = TYPE == T_Q8_0 ? -1152.0f : (g ? -72.0f : -1032.0f);
-#pragma unroll
-            for (int j = 0; j < HB; ++j) {
-                if (j >= nb) break;
+            auto block = [&](int j, auto& A, auto& D) {  // A: an accumulator set, D: its units
                 h2v c1[TM], c0[TM];
 #pragma unroll
                 for (int i = 0; i < TM; ++i) {
                     const float d = f16_to_f32(cur[i].d[j]);
                     const bool z = d == 0.0f;
                     const float u = z ? 1.0f : d;
-                    const float ratio = dl[i] * __builtin_amdgcn_rcpf(u);  // ~1 ulp; units only need consistency
-                    dl[i] = u;
+                    const float ratio = D[i] * __builtin_amdgcn_rcpf(u);  // ~1 ulp; units only need consistency
+                    D[i] = u;
 #pragma unroll
                     for (int t = 0; t < TN; ++t)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) acc[i][t][r] *= ratio;
+                        for (int r = 0; r < 16; ++r) A[i][t][r] *= ratio;
                     c1[i] = splat(z ? 0.0f : k1);
                     c0[i] = splat(z ? 0.0f : k0);
                 }
@@ -551,8 +567,19 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
 #pragma unroll
                         for (int t = 0; t < TN; ++t)
 #pragma unroll
-                            for (int i = 0; i < TM; ++i) acc[i][t] = mfma16(av[t][hl], wv[i], acc[i][t]);
+                            for (int i = 0; i < TM; ++i) A[i][t] = mfma16(av[t][hl], wv[i], A[i][t]);
                 }
+            };
+            static_assert(HB % 2 == 0, "block pairs");
+            if constexpr (DUAL) {  // K % 128 == 0: every half-unit holds HB full blocks
+#pragma unroll
+                for (int j = 0; j < HB; j += 2) {
+                    block(j, acc, dl);
+                    block(j + 1, acc2, dl2);
+                }
+            } else if constexpr (!Q4K) {
+#pragma unroll
+                for (int j = 0; j < HB; ++j) block(j, acc, dl);
             }
         }
     };
@@ -574,7 +601,12 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
 #pragma unroll
-                    for (int i = 0; i < TM; ++i) acc[i][t][4 * ii + c] *= RESCALE ? pv[c] * dl[i] : pv[c];
+                    for (int i = 0; i < TM; ++i) {
+                        if constexpr (!DUAL)
+                            acc[i][t][4 * ii + c] *= pv[c] * dl[i];
+                        else  // both sets, back to natural units
+                            acc[i][t][4 * ii + c] = (acc[i][t][4 * ii + c] * dl[i] + acc2[i][t][4 * ii + c] * dl2[i]) * pv[c];
+                    }
             }
     }
     if constexpr (GATEUP) {
