@@ -51,13 +51,13 @@ __device__ __forceinline__ int acth_exponent(float M) {
 // Elements 8c .. 8c+7 of one row (all in one 32-block): one 16-byte store
 // each of hi and lo, plus the row's pe entry and the block's min-term pieces
 // when the chunk opens them.
-__device__ __forceinline__ void acth_chunk(const int8_t* q, const float2* sc, int K, const ActH& o, size_t row, int c,
-                                           int E, bool lo) {
+// qq: the chunk's 8 quants, sb: its block's (scale, sum).
+__device__ __forceinline__ void acth_chunk_v(uint2 qq, float2 sb, int K, const ActH& o, size_t row, int c, int E,
+                                             bool lo) {
     const int KH = K / 128;
     const float dn = __uint_as_float((uint32_t)(127 - E) << 23), up = __uint_as_float((uint32_t)(127 + E) << 23);
     const int i = 8 * c, b = i >> 5, hh = i >> 7;
-    const uint2 qq = *reinterpret_cast<const uint2*>(q + i);
-    const float s = sc[b].x * dn;  // exact: power-of-two scaling
+    const float s = sb.x * dn;  // exact: power-of-two scaling
     uint32_t hw[4], lw[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -74,7 +74,7 @@ __device__ __forceinline__ void acth_chunk(const int8_t* q, const float2* sc, in
     if (lo) *reinterpret_cast<uint4*>(hl + 128) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
     if ((i & 127) == 0) o.pe[row * (size_t)KH + hh] = up;
     if ((i & 31) == 0) {
-        const float X = sc[b].x * sc[b].y * dn;  // exact: 11-bit scale x |sum| < 2^12, times 2^-E
+        const float X = sb.x * sb.y * dn;  // exact: 11-bit scale x |sum| < 2^12, times 2^-E
         const uint32_t bh = __float_as_uint(X) & 0xFFFF0000u;
         const float r1 = X - __uint_as_float(bh);
         const uint32_t bm = __float_as_uint(r1) & 0xFFFF0000u;
@@ -86,22 +86,37 @@ __device__ __forceinline__ void acth_chunk(const int8_t* q, const float2* sc, in
     }
 }
 
-template <int NTH>
-__device__ void write_acth_row(const int8_t* q, const float2* sc, int K, const ActH& o, size_t row, int tid,
+__device__ __forceinline__ void acth_chunk(const int8_t* q, const float2* sc, int K, const ActH& o, size_t row, int c,
+                                           int E, bool lo) {
+    acth_chunk_v(*reinterpret_cast<const uint2*>(q + 8 * c), sc[c >> 2], K, o, row, c, E, lo);
+}
+
+// One row by one wave (all 64 lanes): the row exponent from a wave maximum of
+// the block scales, then four chunks per lane per pass with every load issued
+// before the first store.
+__device__ void write_acth_row(const int8_t* q, const float2* sc, int K, const ActH& o, size_t row, int lane,
                                bool lo = true) {
-    __shared__ float wmax[NTH / 64];
     const int KB = K / 32;
     float M = 0.0f;
-    for (int b = tid; b < KB; b += NTH) M = fmaxf(M, sc[b].x);
+    for (int b = lane; b < KB; b += 64) M = fmaxf(M, sc[b].x);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-    if ((tid & 63) == 0) wmax[tid >> 6] = M;
-    __syncthreads();
-    M = wmax[0];
-#pragma unroll
-    for (int w = 1; w < NTH / 64; ++w) M = fmaxf(M, wmax[w]);
     const int E = acth_exponent(M);
-    for (int c = tid; c < K / 8; c += NTH) acth_chunk(q, sc, K, o, row, c, E, lo);
+    constexpr int U = 4;
+    const int nc = K / 8;
+    for (int c0 = lane; c0 < nc; c0 += U * 64) {
+        uint2 qq[U];
+        float2 sb[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = min(c0 + u * 64, nc - 1);
+            qq[u] = *reinterpret_cast<const uint2*>(q + 8 * c);
+            sb[u] = sc[c >> 2];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (c0 + u * 64 < nc) acth_chunk_v(qq[u], sb[u], K, o, row, c0 + u * 64, E, lo);
+    }
 }
 
 // Chain-major rows: element 16 i + j of a row at j * S + i, so lane j of a
@@ -537,14 +552,15 @@ void launch_route(const RouteArgs& a, hipStream_t st) {
     if (r.RS > 1) launch_route_topk(a, st);
 }
 
-// Matrix-core form of Q8_0 activations already in global memory, one block per row.
-__global__ void __launch_bounds__(256) k_q8_to_acth(ActQ8 in, ActH out, int lo) {
-    const size_t row = blockIdx.x;
-    write_acth_row<256>(in.q + row * in.K, in.s + row * (in.K / 32), in.K, out, row, threadIdx.x, lo != 0);
+// Matrix-core form of Q8_0 activations already in global memory, one wave per row.
+__global__ void __launch_bounds__(256) k_q8_to_acth(ActQ8 in, int rows, ActH out, int lo) {
+    const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= (size_t)rows) return;  // wave-uniform
+    write_acth_row(in.q + row * in.K, in.s + row * (in.K / 32), in.K, out, row, threadIdx.x & 63, lo != 0);
 }
 
 void launch_q8_to_acth(const ActQ8& in, int rows, ActH out, hipStream_t st, bool lo) {
-    hipLaunchKernelGGL(k_q8_to_acth, dim3(rows), dim3(256), 0, st, in, out, lo ? 1 : 0);
+    hipLaunchKernelGGL(k_q8_to_acth, dim3((rows + 3) / 4), dim3(256), 0, st, in, rows, out, lo ? 1 : 0);
 }
 
 // Matrix-core form (fp16 hi only) of fp32 activation rows h [rows][ld], ld =
@@ -983,6 +999,7 @@ void launch_dispatch(const int* ids, int nk, int E, int top_k, const DispatchOut
 // acc = fma(shared_scale, y_shared, acc).
 // Four consecutive features of one token per thread (d % 32 == 0), 16-byte loads and stores; the
 // per-feature order is k_combine's contract (fma in selection order, then the shared expert).
+template <int KU>  // slots whose loads go out together (the fma order stays the selection order)
 __global__ void __launch_bounds__(256)
 k_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
           const float* shscale, float* out) {
@@ -991,14 +1008,27 @@ k_combine(int n, int d, int k, const float* probs, const int* pos_of, const floa
     if (idx >= (size_t)n * d4) return;
     const int t = (int)(idx / d4), i = 4 * (int)(idx % d4);
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int s = 0; s < k; ++s) {
-        const size_t p = (size_t)pos_of[(size_t)t * k + s];
-        const float w = probs[(size_t)t * k + s];
-        const float4 v = *reinterpret_cast<const float4*>(y + p * d + i);
-        acc.x = __builtin_fmaf(w, v.x, acc.x);
-        acc.y = __builtin_fmaf(w, v.y, acc.y);
-        acc.z = __builtin_fmaf(w, v.z, acc.z);
-        acc.w = __builtin_fmaf(w, v.w, acc.w);
+    for (int s0 = 0; s0 < k; s0 += KU) {
+        int p[KU];
+        float w[KU];
+        float4 v[KU];
+#pragma unroll
+        for (int u = 0; u < KU; ++u) {
+            const int s = min(s0 + u, k - 1);
+            p[u] = pos_of[(size_t)t * k + s];
+            w[u] = probs[(size_t)t * k + s];
+        }
+#pragma unroll
+        for (int u = 0; u < KU; ++u) v[u] = *reinterpret_cast<const float4*>(y + (size_t)p[u] * d + i);
+#pragma unroll
+        for (int u = 0; u < KU; ++u) {
+            if (s0 + u < k) {
+                acc.x = __builtin_fmaf(w[u], v[u].x, acc.x);
+                acc.y = __builtin_fmaf(w[u], v[u].y, acc.y);
+                acc.z = __builtin_fmaf(w[u], v[u].z, acc.z);
+                acc.w = __builtin_fmaf(w[u], v[u].w, acc.w);
+            }
+        }
     }
     if (ysh) {
         const float w = shscale[t];
@@ -1014,8 +1044,10 @@ k_combine(int n, int d, int k, const float* probs, const int* pos_of, const floa
 void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
                     const float* shscale, float* out, hipStream_t st) {
     const size_t tot = (size_t)n * (d / 4);
-    hipLaunchKernelGGL(k_combine, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, n, d, k, probs, pos_of, y,
-                       ysh, shscale, out);
+    const dim3 grid((unsigned)((tot + 255) / 256));
+    if (k <= 2) hipLaunchKernelGGL(k_combine<2>, grid, dim3(256), 0, st, n, d, k, probs, pos_of, y, ysh, shscale, out);
+    else if (k <= 4) hipLaunchKernelGGL(k_combine<4>, grid, dim3(256), 0, st, n, d, k, probs, pos_of, y, ysh, shscale, out);
+    else hipLaunchKernelGGL(k_combine<8>, grid, dim3(256), 0, st, n, d, k, probs, pos_of, y, ysh, shscale, out);
 }
 
 // Q8_0 of `rows` rows of K fp32 values (quantize_row_q8_0, src/quant.cpp:1029-1045),
