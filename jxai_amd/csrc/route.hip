@@ -375,7 +375,7 @@ __global__ void __launch_bounds__(RT_THREADS) k_route(RouteArgs a, int nsplit, i
 }
 
 // Router logits for many tokens against a router of more than 16 rows with
-// d <= 2048 (d / 64 in 8, 16, 24, 32): a block owns 16 rows and RR_TPB tokens.  Lane j
+// d <= 2048 (d / 64 in 8, 16, 24, 32): a block owns 16 rows and tpb tokens.  Lane j
 // of a row's 16-lane group keeps its whole vec_dot_f32 chain of router values
 // in registers (read once), and the tokens stream through LDS four at a time,
 // chain-major, the next chunk's loads in flight while the current one is
@@ -387,16 +387,16 @@ __global__ void __launch_bounds__(RT_THREADS) k_route(RouteArgs a, int nsplit, i
 #ifndef JX_RR_TC
 #define JX_RR_TC 4
 #endif
-constexpr int RR_TPB = JX_RR_TPB;  // tokens per block
+constexpr int RR_TPB = JX_RR_TPB;  // tokens per block, at most (fewer keep small batches spread)
 constexpr int RR_TC = JX_RR_TC;    // tokens per LDS chunk
 
 template <int M4>  // d / 64 float4 chain steps per lane
-__global__ void __launch_bounds__(RT_THREADS) k_route_rows(RouteArgs a, int nsplit) {
+__global__ void __launch_bounds__(RT_THREADS) k_route_rows(RouteArgs a, int nsplit, int tpb) {
     extern __shared__ __align__(16) float xs[];  // [2][RR_TC][16][S]
     constexpr int d = 64 * M4, C4 = d / 4, S = rs_stride(d), RS = 16 * S, Sg = chain_stride_of(d);
     constexpr int PER = (RR_TC * C4 + RT_THREADS - 1) / RT_THREADS;  // float4 per thread per chunk
-    const int split = blockIdx.x % nsplit, t0 = (blockIdx.x / nsplit) * RR_TPB;
-    const int tend = min(a.n, t0 + RR_TPB);
+    const int split = blockIdx.x % nsplit, t0 = (blockIdx.x / nsplit) * tpb;
+    const int tend = min(a.n, t0 + tpb);
     const int tid = threadIdx.x, grp = tid >> 4, j = tid & 15;
     const int E = a.E, R = E + (a.shgate ? 1 : 0);
     const int r = split * RT_GROUPS + grp;
@@ -503,7 +503,11 @@ static void launch_route_topk(const RouteArgs& a, hipStream_t st) {
 static bool route_rows_fits(const RouteArgs& a) {
     const int R = a.E + (a.shgate ? 1 : 0);
     const int m4 = a.d / 64;
-    return R > RT_GROUPS && a.d % 64 == 0 && (m4 == 8 || m4 == 16 || m4 == 24 || m4 == 32) && a.n >= 2 * RR_TPB;
+// below ~512 tokens the split k_route (one token per block, router from L2) measured faster
+#ifndef JX_RR_MIN_N
+#define JX_RR_MIN_N 512
+#endif
+    return R > RT_GROUPS && a.d % 64 == 0 && (m4 == 8 || m4 == 16 || m4 == 24 || m4 == 32) && a.n >= JX_RR_MIN_N;
 }
 
 void launch_route(const RouteArgs& a, hipStream_t st) {
@@ -518,12 +522,14 @@ void launch_route(const RouteArgs& a, hipStream_t st) {
         hipLaunchKernelGGL(q, dim3((a.n + T - 1) / T), dim3(RT_THREADS), lq, st, a, 1, 0);
         const int R = a.E + (a.shgate ? 1 : 0), RS = (R + RT_GROUPS - 1) / RT_GROUPS;
         const size_t lr = (size_t)2 * RR_TC * 16 * rs_stride(a.d) * sizeof(float);
-        const dim3 grid(RS * ((a.n + RR_TPB - 1) / RR_TPB));
+        // tokens per block: about 512 blocks in all, in whole LDS chunks, at most RR_TPB
+        const int tpb = std::min(RR_TPB, std::max(RR_TC, ((a.n * RS + 511) / 512 + RR_TC - 1) / RR_TC * RR_TC));
+        const dim3 grid(RS * ((a.n + tpb - 1) / tpb));
         auto go = [&](auto kern) {
             if (lr > 65536)
                 (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lr);
-            hipLaunchKernelGGL(kern, grid, dim3(RT_THREADS), lr, st, a, RS);
+            hipLaunchKernelGGL(kern, grid, dim3(RT_THREADS), lr, st, a, RS, tpb);
         };
         switch (a.d / 64) {
             case 8: go(k_route_rows<8>); break;

@@ -124,7 +124,9 @@ def test_layer_vs_golden(moe, case):
                                            # 128 experts at one and two tokens: groups from the logits
                                            ("qwen3moe", 1, None), ("qwen3moe", 2, None),
                                            # few tokens on the matrix-core path: top-k in its own launch
-                                           ("qwen3moe", 1, "mfma"), ("qwen15moe", 2, "mfma")])
+                                           ("qwen3moe", 1, "mfma"), ("qwen15moe", 2, "mfma"),
+                                           # register-resident router rows with fewer tokens per block
+                                           ("qwen3moe", 600, None), ("qwen15moe", 700, None)])
 def test_layer_regimes_vs_oracle(moe, port, name, n, regime):
     say(f"{name} n={n} regime={regime}")
     cfg, lw = layer(name)
