@@ -335,16 +335,21 @@ int resolve_profile(jx_moe_layer* L) {
 
 // Regime: the matrix-core GEMMs once the average expert sees this many (token, slot) pairs.  The
 // multi-token GEMV (int8 matrix cores, 16 tokens per weight pass) streams an expert's weights once
-// per 16 tokens, the GEMM once per 64-pair tile computing the whole tile; measured on MI355X the
-// crossover lies at 8-16 pairs for the 4-bit layers (Mixtral-, Qwen1.5-, DeepSeek-V2-Lite-shaped)
-// and above 8 for the Q8_0 one (Qwen3-shaped).
+// per 16 tokens, the GEMM once per 64-pair tile computing the whole tile.  Forced-GEMV vs forced-GEMM
+// sweeps on MI355X put the crossover at 3-4 pairs for the Q8_0 layer (Qwen3-shaped), ~11 for the
+// small 4-bit experts (DeepSeek-V2-Lite-, Qwen1.5-shaped) and ~15 for large ones (Mixtral-shaped,
+// 14336 x 4096 per matrix, whose GEMV streams near its best rate).
 constexpr int MFMA_MIN_PAIRS_PER_EXPERT_Q4 = 12;
-constexpr int MFMA_MIN_PAIRS_PER_EXPERT_Q8 = 16;
+constexpr int MFMA_MIN_PAIRS_PER_EXPERT_Q4_LARGE = 16;
+constexpr int MFMA_MIN_PAIRS_PER_EXPERT_Q8 = 4;
+constexpr size_t LARGE_EXPERT_ELEMS = (size_t)1 << 25;  // d * d_ff per matrix
 
 int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStream_t st, uint32_t flags) {
     const int E = L->E, k = L->k, d = L->d;
     const int nk = n * k;
-    const int min_ppe = L->gate.m.type == jx::T_Q8_0 ? MFMA_MIN_PAIRS_PER_EXPERT_Q8 : MFMA_MIN_PAIRS_PER_EXPERT_Q4;
+    const int min_ppe = L->gate.m.type == jx::T_Q8_0                 ? MFMA_MIN_PAIRS_PER_EXPERT_Q8
+                        : (size_t)d * L->F >= LARGE_EXPERT_ELEMS ? MFMA_MIN_PAIRS_PER_EXPERT_Q4_LARGE
+                                                                 : MFMA_MIN_PAIRS_PER_EXPERT_Q4;
     bool mfma = (size_t)nk >= (size_t)min_ppe * E;
     if (flags & JX_FWD_FORCE_GEMV) mfma = false;
     if (flags & JX_FWD_FORCE_MFMA) mfma = true;

@@ -116,10 +116,12 @@ def test_layer_vs_golden(moe, case):
                                            ("toy", 2, "gemv"), ("qwen15moe", 2, "gemv"), ("mixtral", 2, "gemv"),
                                            ("dsv2lite", 2, "gemv"), ("qwen15moe", 1, "gemv"),
                                            # the library's own choice around its thresholds: the 4-token and
-                                           # 16-token GEMV forms, routed experts on the GEMM from 12 (4-bit) or
-                                           # 16 (Q8_0) pairs per expert, the shared expert from 64 tokens
+                                           # 16-token GEMV forms, routed experts on the GEMM from 4 (Q8_0), 12
+                                           # (small 4-bit) or 16 (Mixtral-sized 4-bit) pairs per expert, the
+                                           # shared expert from 64 tokens
                                            ("qwen15moe", 40, None), ("dsv2lite", 64, None), ("mixtral", 32, None),
-                                           ("qwen3moe", 48, None), ("toy", 24, None), ("mixtral", 8, None),
+                                           ("qwen3moe", 48, None), ("qwen3moe", 64, None), ("mixtral", 56, None),
+                                           ("mixtral", 64, None), ("toy", 24, None), ("mixtral", 8, None),
                                            ("qwen15moe", 70, None), ("dsv2lite", 20, None),
                                            # 128 experts at one and two tokens: groups from the logits
                                            ("qwen3moe", 1, None), ("qwen3moe", 2, None),
