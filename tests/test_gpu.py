@@ -147,6 +147,24 @@ def test_layer_regimes_vs_oracle(moe, port, name, n, regime):
     L.close()
 
 
+@pytest.mark.parametrize("name", ["mixtral", "qwen3moe", "qwen15moe", "dsv2lite"])
+def test_odd_token_counts(moe, port, name):
+    """The library's own regime choice at token counts that fill no tile, group or block evenly."""
+    cfg, lw = layer(name)
+    L = moe.MoELayer.from_weights(lw)
+    for n in (3, 13, 89, 377):
+        say(f"{name} n={n} (library's choice)")
+        x = synth.make_tokens(cfg, n, seed=n)
+        out, ids, w, counts = L.forward(x)
+        lg_o, ids_o, w_o = port.route(lw, x)
+        assert np.array_equal(ids, ids_o)
+        assert np.array_equal(counts, np.bincount(ids_o.reshape(-1), minlength=cfg.n_experts))
+        np.testing.assert_allclose(w, w_o, rtol=2e-6, atol=0)
+        sel = np.unique(np.linspace(0, n - 1, min(n, 4)).astype(np.int32))
+        assert rel_err(out[sel], port.moe_forward(lw, x, sel)[0]) <= REL_TOL
+    L.close()
+
+
 # ------------------------------------------------------------------ properties at full size
 def test_mixtral_prefill_properties(moe):
     """2048-token Mixtral layer: routing invariants, regime agreement, determinism."""
