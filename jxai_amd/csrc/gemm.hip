@@ -753,10 +753,11 @@ void launch_min_table(const QMat& m, uint8_t* mn, hipStream_t st) {
 #ifndef JX_DOWN_WGS
 #define JX_DOWN_WGS 2
 #endif
-// Row groups per band of the workgroup order (0: all of them); 4 measured
-// best for both GEMMs on the 2048-token Mixtral layer (2, 8, 16 and all slower).
+// Row groups per band of the workgroup order (0: all of them).  Gate/up: 8
+// (with the XCD-balanced item mapping, Qwen3-shaped 2048 tokens 384 -> 354 us,
+// the other shapes unchanged; 2 and 16 slower); down: 4 (2 and 8 slower).
 #ifndef JX_GEMM_GU_RC
-#define JX_GEMM_GU_RC 4
+#define JX_GEMM_GU_RC 8
 #endif
 #ifndef JX_DOWN_RC
 #define JX_DOWN_RC 4
