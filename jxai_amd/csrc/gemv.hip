@@ -456,12 +456,13 @@ k_gemv_gateup(QMat G, QMat U, ActQ8 xq, Groups grp, ActQ8 hq, float* hf, int hf_
     constexpr int HW = WAVES / 2;  // waves per matrix
     extern __shared__ __align__(16) int8_t smem[];
     __shared__ float red[WAVES][TB][32];
-    if (tail.on && blockIdx.y == gridDim.y - 1) {  // the extra grid row: dispatch tables only
-        if (blockIdx.x == 0) small_tail(tail, threadIdx.x);
+    // grid: row tile fastest over the slots, then the one tail block
+    if (tail.on && blockIdx.x == gridDim.x - 1) {  // the extra block: dispatch tables only
+        small_tail(tail, threadIdx.x);
         return;
     }
-    const int rt = blockIdx.x;
-    const int4 rec = group_of(grp, blockIdx.y);
+    const int rt = blockIdx.x % G.nrt;
+    const int4 rec = group_of(grp, blockIdx.x / G.nrt);
     const int e = rec.x, p0 = rec.y, cnt = rec.z;
     if (cnt == 0) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 31, h = lane >> 5;
@@ -517,8 +518,8 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
 k_gemv_down(QMat D, ActQ8 hq, const float* hf, int hf_ld, Groups grp, float* y) {
     extern __shared__ __align__(16) int8_t smem[];
     __shared__ float red[WAVES][TB][32];
-    const int rt = blockIdx.x;
-    const int4 rec = group_of(grp, blockIdx.y);
+    const int rt = blockIdx.x % D.nrt;  // grid: row tile fastest over the slots
+    const int4 rec = group_of(grp, blockIdx.x / D.nrt);
     const int e = rec.x, p0 = rec.y, cnt = rec.z;
     if (cnt == 0) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 31, h = lane >> 5;
@@ -673,12 +674,13 @@ k_gemv_mx(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_l
     constexpr int HW = GATEUP ? WAVES / 2 : WAVES;  // waves per matrix
     extern __shared__ __align__(16) float2 msc[];   // [block][MX_NT]: (scale, sum) of each token
     __shared__ float red[WAVES][MX_NT / 2][64];
-    if (GATEUP && tail.on && blockIdx.y == gridDim.y - 1) {  // the extra grid row: dispatch tables only
-        if (blockIdx.x == 0) small_tail(tail, threadIdx.x);
+    // grid: row tile fastest over the slots, then (gate/up) the one tail block
+    if (GATEUP && tail.on && blockIdx.x == gridDim.x - 1) {  // the extra block: dispatch tables only
+        small_tail(tail, threadIdx.x);
         return;
     }
-    const int rt = blockIdx.x;
-    const int4 rec = group_of(grp, blockIdx.y);
+    const int rt = blockIdx.x % W0.nrt;
+    const int4 rec = group_of(grp, blockIdx.x / W0.nrt);
     const int e = rec.x, p0 = rec.y, cnt = rec.z;
     if (cnt == 0) return;
     const int tid = threadIdx.x, lane = tid & 63, m = lane & 31, h = lane >> 5;
@@ -815,7 +817,7 @@ static void lds_optin(Kern k, size_t bytes) {
 template <int TYPE>
 static void gateup_t(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots, int tb,
                      ActQ8 hq, float* hf, hipStream_t st, const SmallTail& tail) {
-    dim3 grid(g.nrt, slots + (tail.on ? 1 : 0));
+    dim3 grid(g.nrt * slots + (tail.on ? 1 : 0));
     const int hf_ld = ((g.rows + 255) / 256) * 256;
     if (tb <= 1) {
         const size_t lds = act_lds_bytes(1, xq.K, false);
@@ -849,7 +851,7 @@ void launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Gro
 template <int TYPE, bool F32ACT>
 static void down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp, int slots,
                    int tb, float* y, hipStream_t st) {
-    dim3 grid(dn.nrt, slots);
+    dim3 grid(dn.nrt * slots);
     const int K = F32ACT ? hf_ld : hq.K;
     if (tb <= 1) {
         const size_t lds = act_lds_bytes(1, K, F32ACT);
