@@ -578,8 +578,84 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
                     block(j + 1, acc2, dl2);
                 }
             } else if constexpr (!Q4K) {
+                // software pipelined as the Q4_K path: step st = (block st / 2, K-half st % 2); the next
+                // step's LDS reads and weight conversion go out around this step's MFMAs. At a block's
+                // first step each tile is rescaled into the block's unit right before its own hi MFMA,
+                // so the MFMAs of the tiles before it run while the multiplies issue.
+                h8 av[2][TN][HL];
+                h8 wv[2][TM];
+                h2v c1[TM], c0[TM];
+                float ratio[TM];
+                auto scales = [&](int j) {
 #pragma unroll
-                for (int j = 0; j < HB; ++j) block(j, acc, dl);
+                    for (int i = 0; i < TM; ++i) {
+                        const float d = f16_to_f32(cur[i].d[j]);
+                        const bool z = d == 0.0f;
+                        const float u = z ? 1.0f : d;
+                        ratio[i] = dl[i] * __builtin_amdgcn_rcpf(u);  // ~1 ulp; units only need consistency
+                        dl[i] = u;
+                        c1[i] = splat(z ? 0.0f : k1);
+                        c0[i] = splat(z ? 0.0f : k0);
+                    }
+                };
+                auto read_av = [&](int st, h8(&dst)[TN][HL]) {
+#pragma unroll
+                    for (int t = 0; t < TN; ++t)
+#pragma unroll
+                        for (int hl = 0; hl < HL; ++hl)
+                            dst[t][hl] = *reinterpret_cast<const h8*>(sa + t * 32 * PB + boff(hl, st >> 1, st & 1));
+                };
+                auto convert = [&](int st, h8(&dst)[TM]) {
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) {
+                        const uint4 raw = cur[i].q[st >> 1];
+                        dst[i] = (st & 1) ? cvt8(raw.z, raw.w, mask, flip, c1[i], c0[i])
+                                          : cvt8(raw.x, raw.y, mask, flip, c1[i], c0[i]);
+                    }
+                };
+                scales(0);
+                read_av(0, av[0]);
+                convert(0, wv[0]);
+#pragma unroll
+                for (int st = 0; st < 2 * HB; ++st) {
+                    const int b = st & 1;
+                    if (st + 1 < 2 * HB) read_av(st + 1, av[b ^ 1]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if ((st & 1) == 0) {
+#pragma unroll
+                        for (int t = 0; t < TN; ++t)
+#pragma unroll
+                            for (int i = 0; i < TM; ++i) {
+#pragma unroll
+                                for (int r = 0; r < 16; ++r) acc[i][t][r] *= ratio[i];
+                                acc[i][t] = mfma16(av[b][t][0], wv[b][i], acc[i][t]);
+                            }
+#pragma unroll
+                        for (int hl = 1; hl < HL; ++hl)
+#pragma unroll
+                            for (int t = 0; t < TN; ++t)
+#pragma unroll
+                                for (int i = 0; i < TM; ++i) acc[i][t] = mfma16(av[b][t][hl], wv[b][i], acc[i][t]);
+#pragma unroll
+                        for (int k = 0; k < TN * TM; ++k) {
+                            __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // VALU: one tile's rescale
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA: its hi product
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    } else {
+#pragma unroll
+                        for (int hl = 0; hl < HL; ++hl)
+#pragma unroll
+                            for (int t = 0; t < TN; ++t)
+#pragma unroll
+                                for (int i = 0; i < TM; ++i) acc[i][t] = mfma16(av[b][t][hl], wv[b][i], acc[i][t]);
+                    }
+                    if (st + 1 < 2 * HB) {
+                        if (!((st + 1) & 1)) scales((st + 1) >> 1);  // the next block's unit and operand constants
+                        convert(st + 1, wv[b ^ 1]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
         }
     };
