@@ -440,7 +440,9 @@ __device__ __forceinline__ void kloop(const QMat& W0, const QMat& W1, int e, int
 
 // Resident waves per SIMD the GEMVs are compiled for (single-token groups:
 // <= 128 VGPRs, every block of a decode step resident at once with enough
-// 1 KB weight loads in flight per CU to cover HBM latency).
+// 1 KB weight loads in flight per CU to cover HBM latency).  The single-token
+// gate/up GEMV also comes compiled for 3 waves per SIMD (<= 168 VGPRs, no
+// spills), taken when the whole grid is resident at that occupancy.
 #ifndef JX_GEMV_TB4_WPS
 #define JX_GEMV_TB4_WPS 2
 #endif
@@ -450,8 +452,8 @@ __device__ __forceinline__ void kloop(const QMat& W0, const QMat& W1, int e, int
 // the Q8_0 quantization of the result for the down projection
 // (matmul_quant_f32's quantize_row_q8_0, 3908-3914).  The first half of the
 // waves streams the gate tile, the second half the up tile.
-template <int TYPE, int TB, int WAVES>
-__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(GEMV_WAVES_PER_SIMD(TB))))
+template <int TYPE, int TB, int WAVES, int WPS = GEMV_WAVES_PER_SIMD(TB)>
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WPS)))
 k_gemv_gateup(QMat G, QMat U, ActQ8 xq, Groups grp, ActQ8 hq, float* hf, int hf_ld, SmallTail tail) {
     constexpr int HW = WAVES / 2;  // waves per matrix
     extern __shared__ __align__(16) int8_t smem[];
@@ -814,6 +816,20 @@ static void lds_optin(Kern k, size_t bytes) {
                                   (int)bytes);
 }
 
+// Compute units of the current device (cached per device).
+static int num_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
 template <int TYPE>
 static void gateup_t(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots, int tb,
                      ActQ8 hq, float* hf, hipStream_t st, const SmallTail& tail) {
@@ -821,9 +837,15 @@ static void gateup_t(const QMat& g, const QMat& u, const ActQ8& xq, const Groups
     const int hf_ld = ((g.rows + 255) / 256) * 256;
     if (tb <= 1) {
         const size_t lds = act_lds_bytes(1, xq.K, false);
-        lds_optin(k_gemv_gateup<TYPE, 1, GATEUP_WAVES>, lds);
-        hipLaunchKernelGGL((k_gemv_gateup<TYPE, 1, GATEUP_WAVES>), grid, dim3(GATEUP_WAVES * 64), lds, st, g, u, xq,
-                           grp, hq, hf, hf_ld, tail);
+        // every block resident at 3 waves per SIMD: the spill-free build (measured: Qwen3-shaped 32.6 -> 31.0 us,
+        // Qwen1.5-shaped 43.6 -> 40 us per token; Mixtral-shaped, 896 blocks, keeps 4 waves per SIMD)
+        const bool w3 = (size_t)grid.x * GATEUP_WAVES <= (size_t)3 * 4 * num_cus();
+        auto go = [&](auto kern) {
+            lds_optin(kern, lds);
+            hipLaunchKernelGGL(kern, grid, dim3(GATEUP_WAVES * 64), lds, st, g, u, xq, grp, hq, hf, hf_ld, tail);
+        };
+        if (w3) go(k_gemv_gateup<TYPE, 1, GATEUP_WAVES, 3>);
+        else go(k_gemv_gateup<TYPE, 1, GATEUP_WAVES, 4>);
     } else if (tb <= 4) {
         const size_t lds = act_lds_bytes(4, xq.K, false);
         lds_optin(k_gemv_gateup<TYPE, 4, GATEUP_WAVES>, lds);
