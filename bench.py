@@ -10,9 +10,11 @@ batch of seeded synthetic activations already resident in HBM:
 Both lines report the roofline of their dominant kernel from HIP events
 recorded around every launch (a second pass of the same steps).  The prefill
 GEMMs run v_mfma_f32_32x32x16_f16 on exact integer-valued operands (Q4_K
-sc*q in A, the Q8_0 activations dx*q split into exact fp16 hi + lo in B), so
-their roofline peak is the fp16 one; the fraction of the int8 peak the north
-star names is reported beside it.  The reference's CPU
+gate/up: sc*q in A, the Q8_0 quants q in B, the accumulator rescaled per
+32-block into the activation scale's units; Q4_0/Q8_0 gate/up: dx*q split into
+exact fp16 hi + lo in B), so their roofline peak is the fp16 one; the fraction
+of the int8 peak the north star names, and of the fp16 peak counting the
+MFMAs actually issued, are reported beside it.  The reference's CPU
 path (its own quant.cpp/tier.cpp built in oracle/_ref, AVX2 dot order) is
 timed on a bounded sample of the same workload on the host cores.
 """
@@ -66,6 +68,12 @@ def copy_calibration():
         b.copy_(a)
     torch.cuda.synchronize()
     print(f"[bench] copied {nbytes} bytes x3", file=sys.stderr, flush=True)
+
+
+def issued_per_algorithmic(cfg):
+    """Matrix-core flops the gate/up GEMM issues per algorithmic flop: Q4_K one fp16 MFMA per
+    16 of K plus the min term's three per 256 of K (19 / 16); Q4_0 / Q8_0 hi and lo (2)."""
+    return 19 / 16 if cfg.wtype == F.Q4_K else 2.0
 
 
 def algorithmic(cfg, n, counts):
@@ -169,7 +177,7 @@ def main():
                 "traffic": measured_traffic("gateup_mfma", n),
                 "avg_launch_us": gu_avg * 1e6,
                 "int8_peak_frac": gu_rate / INT8_PEAK_TOPS,
-                "issued_fp16_frac": 2 * gu_rate / FP16_PEAK_TFLOPS,
+                "issued_fp16_frac": issued_per_algorithmic(cfg) * gu_rate / FP16_PEAK_TFLOPS,
                 "layer_int8_frac": a_pre["ops"] / s_pre / 1e12 / INT8_PEAK_TOPS}
 
     nd = args.decode_tokens

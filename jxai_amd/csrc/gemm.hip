@@ -58,18 +58,29 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int HB = 4;  // 32-blocks per staged half-unit
 
 // One staged half-unit of BN activation rows: HL = 2 stages fp16 hi and lo
-// (256 bytes each per row), HL = 1 hi only.
+// (256 bytes each per row), HL = 1 hi only (or the block-unit form's fp16
+// quants).
 template <int HL, int BN>
 struct Stage {
     static constexpr int PB = 256 * HL;   // bytes per row
     static constexpr int CPP = PB / 16;   // 16-byte chunks per row
     uint8_t q[BN * PB];                   // row r, chunk c at chunk (c ^ (r % CPP))
-    float pe[BN];                         // 2^E of each row
+    float pe[BN];                         // 2^E (block-unit form: the unit) of each row
     uint16_t xm[3 * BN * 8];              // Q4_K: [piece][row][8 sub-blocks] bf16 of dx * sum(q)
 };
 
-template <int HL, int BN>
-struct GemmSmem {
+// Block-unit form: the unit ratios of each stage's blocks, [stage][block][row]
+// (an empty base otherwise: every byte of LDS counts where two workgroups
+// share a CU).
+template <int BN, bool RX>
+struct RxStage {
+    float rx[2][HB * BN];
+};
+template <int BN>
+struct RxStage<BN, false> {};
+
+template <int HL, int BN, bool RX>
+struct GemmSmem : RxStage<BN, RX> {
     Stage<HL, BN> st[2];
     int src[BN];  // activation row (token or pair) of each staged pair
 };
@@ -210,13 +221,17 @@ struct WRaw<T_Q4_K> {
     __device__ static uint32_t moff(const QMat& W, int rt, int n) {
         return (uint32_t)(((size_t)rt * W.nkb * 96 + n) * 16);
     }
+    // PAR: the parity of h (even half-units carry the header, odd ones the min pieces), so each of the
+    // two alternating register sets holds only the fields its parity uses
+    template <int PAR>
     __device__ void load(const uint8_t* qb, const uint8_t* sb, const uint8_t* mb, uint32_t qo, uint32_t so,
                          uint32_t mo, int h, int nb) {
         (void)nb;
-        const uint8_t* qh = qb + (size_t)(h >> 1) * 4096 + (h & 1) * 2048;
+        static_assert(PAR == 0 || PAR == 1, "parity");
+        const uint8_t* qh = qb + (size_t)(h >> 1) * 4096 + PAR * 2048;
 #pragma unroll
         for (int p = 0; p < 2; ++p) q[p] = ld16(qh + p * 1024 + qo);
-        if (!(h & 1)) {
+        if (PAR == 0) {
             hd = ld16(sb + (size_t)(h >> 1) * 512 + so);
         } else {
             const uint8_t* mh = mb + (size_t)(h >> 1) * 1536 + mo;
@@ -238,6 +253,7 @@ struct WRaw {  // Q4_0 / Q8_0: 16 bytes per 32-block, and row n's fp16 block sca
         return (uint32_t)(((size_t)rt * W.nkb * 32 + n) * 2);
     }
     __device__ static uint32_t moff(const QMat&, int, int) { return 0; }
+    template <int PAR>
     __device__ void load(const uint8_t* qb, const uint8_t* sb, const uint8_t*, uint32_t qo, uint32_t so, uint32_t,
                          int h, int nb) {
         constexpr int QB = TYPE == T_Q4_0 ? 512 : 1024;  // bytes per 32-block of a row tile
@@ -284,14 +300,20 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
     // super-block's d (per weight row) and rescaled by d_prev / d_cur at each
     // super-block (fp32 rounding ~2^-24 per step)
     constexpr bool RESCALE = true;
-    // gate/up: exact hi + lo activation operands (h is re-quantized after SwiGLU); down: the hi
-    // half only (relative error <= 2^-12 per activation, no re-quantization downstream)
-    constexpr int HL = GATEUP ? 2 : 1;
+    // Q4_K gate/up: block-unit activations -- the exact quants q as the operand and acc kept in units of
+    // the current block's dx per pair, rescaled by u(b-1) / u(b) (one multiply per accumulator element
+    // and 32-block) before the block's MFMAs; the weight scale d stays per super-block.  Q4_0 / Q8_0
+    // gate/up (d per block as well): exact hi + lo activation operands.  (h is re-quantized after
+    // SwiGLU, so gate/up products stay exact.)  Down: the hi half only (relative error <= 2^-12 per
+    // activation, no re-quantization downstream).
+    constexpr bool UNIT = Q4K && GATEUP;
+    constexpr int HL = GATEUP && !UNIT ? 2 : 1;
+    constexpr int GB = UNIT ? 256 : 512;  // global bytes per row and half-unit
     using St = Stage<HL, BN>;
     constexpr int PB = St::PB, CPP = St::CPP, PPI = 64 / CPP;  // row bytes, chunks, rows per DMA
     constexpr int PER = BN / PPI / GW;  // 1 KB staging loads per wave and half-unit
     static_assert(PER * PPI * GW == BN, "staging split");
-    __shared__ GemmSmem<HL, BN> sm;
+    __shared__ GemmSmem<HL, BN, UNIT> sm;
     int ti, sub, rg;
     // the grid covers the tile upper bound; the items of the tiles that exist are spread over the XCDs
     // as if the grid were exact, and the rest exit (otherwise the XCDs whose ranges hold the missing
@@ -331,25 +353,36 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
         const int r = PPI * (wave * PER + k) + lane / CPP;
-        soff[k] = (uint32_t)sm.src[r] * (uint32_t)(H * 512) + (uint32_t)(((lane % CPP) ^ (r % CPP)) << 4);
+        soff[k] = (uint32_t)sm.src[r] * (uint32_t)(H * GB) + (uint32_t)(((lane % CPP) ^ (r % CPP)) << 4);
     }
-    const int sj = wave;  // pe / xm: lane l of wave w < BN / 64 takes pair 64 * w + l
+    const int sj = wave;  // pe / xm / rx: lane l of wave w < BN / 64 takes pair 64 * w + l
     const int srow = sm.src[64 * min(sj, BN / 64 - 1) + lane];
     const uint32_t peoff = (uint32_t)srow * (uint32_t)(H * 4);
     const uint32_t xoff = Q4K ? (uint32_t)srow * (uint32_t)(in.KU * 48) : 0u;
+    const uint32_t rxoff = UNIT ? (uint32_t)srow * (uint32_t)(H * HB * 4) : 0u;
+    const uint8_t* qsrc = reinterpret_cast<const uint8_t*>(UNIT ? in.q16 : in.hl);
+    const uint8_t* pesrc = reinterpret_cast<const uint8_t*>(UNIT ? in.pu : in.pe);
+    const uint8_t* xmsrc = reinterpret_cast<const uint8_t*>(UNIT ? in.xu : in.xm);
     auto stage = [&](int h) {
         St& S = sm.st[h & 1];
-        const uint8_t* base = reinterpret_cast<const uint8_t*>(in.hl) + (size_t)h * 512;
+        const uint8_t* base = qsrc + (size_t)h * GB;
 #pragma unroll
         for (int k = 0; k < PER; ++k) dma16(base + soff[k], S.q + (wave * PER + k) * 1024);
         if constexpr (Q4K) {
             if (h & 1) {  // min-term values of the super-block: piece pc of the lane's pair
-                const uint8_t* xb = reinterpret_cast<const uint8_t*>(in.xm) + (size_t)(h >> 1) * 48;
+                const uint8_t* xb = xmsrc + (size_t)(h >> 1) * 48;
                 if (wave < BN / 64)
                     for (int pc = 0; pc < 3; ++pc) dma16(xb + xoff + pc * 16, S.xm + pc * (BN * 8) + 64 * sj * 8);
             }
         }
-        if (wave < BN / 64) dma4(reinterpret_cast<const uint8_t*>(in.pe) + (size_t)h * 4 + peoff, S.pe + 64 * sj);
+        if constexpr (UNIT) {  // unit ratios of the half-unit's blocks, [block][pair]
+            if (wave < BN / 64) {
+                const uint8_t* rb = reinterpret_cast<const uint8_t*>(in.rx) + (size_t)h * (HB * 4) + rxoff;
+#pragma unroll
+                for (int j = 0; j < HB; ++j) dma4(rb + 4 * j, sm.rx[h & 1] + j * BN + 64 * sj);
+            }
+        }
+        if (wave < BN / 64) dma4(pesrc + (size_t)h * 4 + peoff, S.pe + 64 * sj);
     };
 
     // weights: uniform bases, per-lane offsets of the wave's row tiles (tiles past the matrix load
@@ -400,7 +433,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
     for (int i = 0; i < TM2; ++i) dl2[i] = 1.0f;
     if (active)
 #pragma unroll
-        for (int i = 0; i < TM; ++i) wa[i].load(qbase[i], sbase[i], mbase[i], qo[i], so[i], mo[i], 0, min(HB, KB));
+        for (int i = 0; i < TM; ++i) wa[i].template load<0>(qbase[i], sbase[i], mbase[i], qo[i], so[i], mo[i], 0, min(HB, KB));
     stage(0);
 
     // LDS byte offset of this lane's A chunk (hi/lo hl, sub-block j of the half-unit, K-half m) in pair tile 0
@@ -415,8 +448,8 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
             if (active)
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
-                    nxt[i].load(qbase[i], sbase[i], mbase[i], qo[i], so[i], mo[i], h + 1,
-                                min(HB, KB - (h + 1) * HB));
+                    nxt[i].template load<ODD ? 0 : 1>(qbase[i], sbase[i], mbase[i], qo[i], so[i], mo[i], h + 1,
+                                                      min(HB, KB - (h + 1) * HB));
         }
         if (!active) return;
         const uint8_t* sa = sm.st[ODD].q + pg * TN * 32 * PB;
@@ -497,8 +530,22 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
                     dst[i] = m ? cvt8(raw.z, raw.w, mask, 0u, c1[i], c0[i]) : cvt8(raw.x, raw.y, mask, 0u, c1[i], c0[i]);
                 }
             };
+            // block-unit form: each pair tile's 16 unit ratios of a block (register r <-> pair
+            // 8 (r / 4) + 4 g + r % 4), read from LDS one step ahead (measured faster than reading
+            // the second pair tile's at the block's first step, which saves registers)
+            float4 rxv[UNIT ? TN : 1][4];
+            const float* rxs = nullptr;
+            if constexpr (UNIT) rxs = sm.rx[ODD] + pbase + 4 * g;
+            auto read_rx = [&](int jj) {
+#pragma unroll
+                for (int t = 0; t < TN; ++t)
+#pragma unroll
+                    for (int ii = 0; ii < 4; ++ii)
+                        rxv[t][ii] = *reinterpret_cast<const float4*>(rxs + jj * BN + 32 * t + 8 * ii);
+            };
             read_av(0, av[0]);
             convert(0, wv[0]);
+            if constexpr (UNIT) read_rx(0);
 #pragma unroll
             for (int st = 0; st < 2 * HB; ++st) {
                 const int b = st & 1;
@@ -507,19 +554,45 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
                 // scheduling barriers), so their latency hides behind 2 * TN * TM MFMAs
                 if (st + 1 < 2 * HB) read_av(st + 1, av[b ^ 1]);
                 __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int hl = 0; hl < HL; ++hl)
+                if (UNIT && b == 0) {
+                    // a block's first step: each tile moves into the block's units right before its
+                    // MFMA, so the MFMAs of the tiles before it run while the multiplies issue
 #pragma unroll
                     for (int t = 0; t < TN; ++t)
 #pragma unroll
-                        for (int i = 0; i < TM; ++i) acc[i][t] = mfma16(av[b][t][hl], wv[b][i], acc[i][t]);
+                        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+                            for (int ii = 0; ii < 4; ++ii) {
+                                acc[i][t][4 * ii] *= rxv[t][ii].x;
+                                acc[i][t][4 * ii + 1] *= rxv[t][ii].y;
+                                acc[i][t][4 * ii + 2] *= rxv[t][ii].z;
+                                acc[i][t][4 * ii + 3] *= rxv[t][ii].w;
+                            }
+                            acc[i][t] = mfma16(av[b][t][0], wv[b][i], acc[i][t]);
+                        }
+#pragma unroll
+                    for (int k = 0; k < TN * TM; ++k) {
+                        __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // VALU: one tile's rescale
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA: its product
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                } else {
+#pragma unroll
+                    for (int hl = 0; hl < HL; ++hl)
+#pragma unroll
+                        for (int t = 0; t < TN; ++t)
+#pragma unroll
+                            for (int i = 0; i < TM; ++i) acc[i][t] = mfma16(av[b][t][hl], wv[b][i], acc[i][t]);
+                }
+                if (UNIT && b == 1 && st + 1 < 2 * HB) read_rx((st + 1) >> 1);
                 if (st + 1 < 2 * HB) {
                     convert(st + 1, wv[b ^ 1]);  // VALU work spread between the MFMAs
+                    if (!UNIT || b == 1)
 #pragma unroll
-                    for (int k = 0; k < HL * TN * TM; ++k) {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
-                    }
+                        for (int k = 0; k < HL * TN * TM; ++k) {
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+                        }
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -864,6 +937,9 @@ static void launch_t(const QMat& w0, const QMat& w1, const ActH& in, const Group
 void launch_mfma_gateup(const QMat& g, const QMat& u, const ActH& xin, const Groups& grp, int tiles_ub,
                         const ActQ8& hq, float* hf, hipStream_t st) {
     const int hf_ld = ((g.rows + 255) / 256) * 256;
+    // Q4_K reads the block-unit form, the others the hi/lo form (the caller allocates the forms its
+    // matrices need; a missing one is a caller bug, and nothing is launched on null pointers)
+    if (g.type == T_Q4_K ? !(xin.q16 && xin.rx && xin.pu && xin.xu) : !(xin.hl && xin.pe)) return;
     switch (g.type) {
         case T_Q4_0: launch_t<T_Q4_0, true>(g, u, xin, grp, tiles_ub, hq, hf, hf_ld, nullptr, st); break;
         case T_Q8_0: launch_t<T_Q8_0, true>(g, u, xin, grp, tiles_ub, hq, hf, hf_ld, nullptr, st); break;

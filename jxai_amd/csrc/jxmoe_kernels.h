@@ -59,10 +59,22 @@ struct ActQ8 {
 //   xm [rows][KU][3][8]  per 256-element unit: bf16 pieces (hi, mid, lo) of
 //                        dx * sum(q) for its 8 blocks (Q4_K min term): times 2^-E
 //                        for per-row E, unscaled for per-half-unit E
+// and, for the Q4_K gate/up GEMM, the block-unit form (each form is written
+// where its pointers are set):
+//   q16 [rows][K]        the quants q as fp16 (exact)
+//   rx [rows][K/32]      u(b-1) / u(b) per 32-block b, where the unit u(b) is the
+//                        block's scale dx, the previous unit where dx is zero, and
+//                        1 before the first nonzero scale (rx = 1 for block 0)
+//   pu [rows][KH]        u of the last block of each half-unit
+//   xu [rows][KU][3][8]  as xm, of dx * sum(q) / u(8s + 3) for super-block s
 struct ActH {
     uint16_t* hl = nullptr;
     float* pe = nullptr;
     uint16_t* xm = nullptr;
+    uint16_t* q16 = nullptr;
+    float* rx = nullptr;
+    float* pu = nullptr;
+    uint16_t* xu = nullptr;
     int K = 0;
     int KH = 0;  // K / 128
     int KU = 0;  // ceil(K / 256)
@@ -103,7 +115,7 @@ struct RouteArgs {
     const float* bias;     // [E] or null
     const float* shgate;   // [d] or null
     ActQ8 xq;              // out: Q8_0 of x (int8 + (scale, sum))
-    ActH xh;               // out: Q8_0 of x for the matrix-core GEMMs (hl == null: not written)
+    ActH xh;               // out: Q8_0 of x for the matrix-core GEMMs (forms with null pointers: not written)
     int* ids;              // [n][k]
     float* probs;          // [n][k]
     float* shscale;        // [n]

@@ -48,15 +48,62 @@ __device__ __forceinline__ int acth_exponent(float M) {
     return (M > 0.0f) ? (int)((__float_as_uint(M) >> 23) & 0xFF) - 127 - 7 : 0;
 }
 
-// Elements 8c .. 8c+7 of one row (all in one 32-block): one 16-byte store
-// each of hi and lo, plus the row's pe entry and the block's min-term pieces
-// when the chunk opens them.
-// qq: the chunk's 8 quants, sb: its block's (scale, sum).
-__device__ __forceinline__ void acth_chunk_v(uint2 qq, float2 sb, int K, const ActH& o, size_t row, int c, int E,
-                                             bool lo) {
+// Exact bf16 (hi, mid, lo) pieces of an fp32 value (truncation keeps each
+// remainder exact) at xm[0], xm[8], xm[16].
+__device__ __forceinline__ void store_pieces3(uint16_t* xm, float X) {
+    const uint32_t bh = __float_as_uint(X) & 0xFFFF0000u;
+    const float r1 = X - __uint_as_float(bh);
+    const uint32_t bm = __float_as_uint(r1) & 0xFFFF0000u;
+    const float r2 = r1 - __uint_as_float(bm);
+    xm[0] = (uint16_t)(bh >> 16);
+    xm[8] = (uint16_t)(bm >> 16);
+    xm[16] = (uint16_t)(__float_as_uint(r2) >> 16);
+}
+
+// Unit of the block-unit form after block b of a row with block scales
+// sc[0..]: the last nonzero scale at or before b, 1 if there is none.
+__device__ __forceinline__ float block_unit(const float2* sc, int b) {
+    for (; b >= 0; --b) {
+        const float d = sc[b].x;
+        if (d != 0.0f) return d;
+    }
+    return 1.0f;
+}
+
+// Elements 8c .. 8c+7 of one row (all in one 32-block): for the hi/lo form
+// one 16-byte store each of hi and lo, plus the row's pe entry and the
+// block's min-term pieces when the chunk opens them; for the block-unit form
+// the chunk's 8 quants as fp16, plus the block's unit ratio and min-term
+// pieces and the half-unit's unit when the chunk opens them.
+// qq: the chunk's 8 quants, sb: its block's (scale, sum), sr: the row's
+// (scale, sum) of every block.
+__device__ __forceinline__ void acth_chunk_v(uint2 qq, float2 sb, const float2* sr, int K, const ActH& o, size_t row,
+                                             int c, int E, bool lo) {
     const int KH = K / 128;
-    const float dn = __uint_as_float((uint32_t)(127 - E) << 23), up = __uint_as_float((uint32_t)(127 + E) << 23);
     const int i = 8 * c, b = i >> 5, hh = i >> 7;
+    if (o.q16) {
+        // a block whose fp16 scale is zero (an underflow leaves nonzero quants) contributes nothing:
+        // its quants are written as zeros, since the block keeps the previous block's unit
+        if (sb.x == 0.0f) qq = make_uint2(0u, 0u);
+        uint32_t w[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t word = u < 2 ? qq.x : qq.y;
+            const _Float16 h0 = (_Float16)(float)(int8_t)(word >> (16 * (u & 1)));
+            const _Float16 h1 = (_Float16)(float)(int8_t)(word >> (16 * (u & 1) + 8));
+            w[u] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+        }
+        *reinterpret_cast<uint4*>(o.q16 + row * (size_t)K + i) = make_uint4(w[0], w[1], w[2], w[3]);
+        if ((i & 31) == 0) {
+            const int KB = K / 32;
+            o.rx[row * (size_t)KB + b] = (b > 0 && sb.x != 0.0f) ? block_unit(sr, b - 1) / sb.x : 1.0f;
+            const float uref = block_unit(sr, min((b & ~7) + 3, KB - 1));
+            store_pieces3(o.xu + row * (size_t)o.KU * 24 + (b / 8) * 24 + (b % 8), sb.x * sb.y / uref);
+        }
+        if ((i & 127) == 0) o.pu[row * (size_t)KH + hh] = block_unit(sr, 4 * hh + 3);
+    }
+    if (!o.hl) return;
+    const float dn = __uint_as_float((uint32_t)(127 - E) << 23), up = __uint_as_float((uint32_t)(127 + E) << 23);
     const float s = sb.x * dn;  // exact: power-of-two scaling
     uint32_t hw[4], lw[4];
 #pragma unroll
@@ -73,22 +120,13 @@ __device__ __forceinline__ void acth_chunk_v(uint2 qq, float2 sb, int K, const A
     *reinterpret_cast<uint4*>(hl) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
     if (lo) *reinterpret_cast<uint4*>(hl + 128) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
     if ((i & 127) == 0) o.pe[row * (size_t)KH + hh] = up;
-    if ((i & 31) == 0) {
-        const float X = sb.x * sb.y * dn;  // exact: 11-bit scale x |sum| < 2^12, times 2^-E
-        const uint32_t bh = __float_as_uint(X) & 0xFFFF0000u;
-        const float r1 = X - __uint_as_float(bh);
-        const uint32_t bm = __float_as_uint(r1) & 0xFFFF0000u;
-        const float r2 = r1 - __uint_as_float(bm);
-        uint16_t* xm = o.xm + row * (size_t)o.KU * 24 + (b / 8) * 24 + (b % 8);
-        xm[0] = (uint16_t)(bh >> 16);
-        xm[8] = (uint16_t)(bm >> 16);
-        xm[16] = (uint16_t)(__float_as_uint(r2) >> 16);
-    }
+    if ((i & 31) == 0)  // exact: 11-bit scale x |sum| < 2^12, times 2^-E
+        store_pieces3(o.xm + row * (size_t)o.KU * 24 + (b / 8) * 24 + (b % 8), sb.x * sb.y * dn);
 }
 
 __device__ __forceinline__ void acth_chunk(const int8_t* q, const float2* sc, int K, const ActH& o, size_t row, int c,
                                            int E, bool lo) {
-    acth_chunk_v(*reinterpret_cast<const uint2*>(q + 8 * c), sc[c >> 2], K, o, row, c, E, lo);
+    acth_chunk_v(*reinterpret_cast<const uint2*>(q + 8 * c), sc[c >> 2], sc, K, o, row, c, E, lo);
 }
 
 // One row by one wave (all 64 lanes): the row exponent from a wave maximum of
@@ -115,7 +153,7 @@ __device__ void write_acth_row(const int8_t* q, const float2* sc, int K, const A
         }
 #pragma unroll
         for (int u = 0; u < U; ++u)
-            if (c0 + u * 64 < nc) acth_chunk_v(qq[u], sb[u], K, o, row, c0 + u * 64, E, lo);
+            if (c0 + u * 64 < nc) acth_chunk_v(qq[u], sb[u], sc, K, o, row, c0 + u * 64, E, lo);
     }
 }
 
@@ -278,7 +316,7 @@ __global__ void __launch_bounds__(RT_THREADS) k_route(RouteArgs a, int nsplit, i
             ss[t * KB + b] = sv;
         }
         __syncthreads();
-        if (a.xh.hl) {  // matrix-core form: one exponent per row from its largest block scale
+        if (a.xh.hl || a.xh.q16) {  // matrix-core forms (hi/lo: one exponent per row from its largest block scale)
             for (int t = wave; t < nt; t += RT_THREADS / 64) {
                 float M = 0.0f;
                 for (int b = lane; b < KB; b += 64) M = fmaxf(M, ss[t * KB + b].x);

@@ -124,24 +124,32 @@ int dalloc(T*& p, size_t n) {
     return JX_OK;
 }
 
-// Matrix-core activation buffers for `rows` rows of K.
+// Matrix-core activation buffers for `rows` rows of K: the hi/lo form, the
+// block-unit form (the Q4_K gate/up input), or both.
 struct DevActH {
     jx::ActH a;
     void release() {
-        if (a.hl) (void)hipFree(a.hl);
-        if (a.pe) (void)hipFree(a.pe);
-        if (a.xm) (void)hipFree(a.xm);
+        for (void* p : {(void*)a.hl, (void*)a.pe, (void*)a.xm, (void*)a.q16, (void*)a.rx, (void*)a.pu, (void*)a.xu})
+            if (p) (void)hipFree(p);
         a = jx::ActH{};
     }
-    int alloc(size_t rows, int K) {
+    int alloc(size_t rows, int K, bool hilo = true, bool unit = false) {
         release();
         a.K = K;
         a.KH = K / 128;
         a.KU = (K + 255) / 256;
         if (K % 128 != 0) return JX_OK;  // the matrix-core path is not used for this shape
-        HIPCHK(hipMalloc(&a.hl, rows * a.KH * 256 * sizeof(uint16_t)));
-        HIPCHK(hipMalloc(&a.pe, rows * a.KH * sizeof(float)));
-        HIPCHK(hipMalloc(&a.xm, rows * a.KU * 24 * sizeof(uint16_t)));
+        if (hilo) {
+            HIPCHK(hipMalloc(&a.hl, rows * a.KH * 256 * sizeof(uint16_t)));
+            HIPCHK(hipMalloc(&a.pe, rows * a.KH * sizeof(float)));
+            HIPCHK(hipMalloc(&a.xm, rows * a.KU * 24 * sizeof(uint16_t)));
+        }
+        if (unit) {
+            HIPCHK(hipMalloc(&a.q16, rows * (size_t)K * sizeof(uint16_t)));
+            HIPCHK(hipMalloc(&a.rx, rows * (size_t)(K / 32) * sizeof(float)));
+            HIPCHK(hipMalloc(&a.pu, rows * a.KH * sizeof(float)));
+            HIPCHK(hipMalloc(&a.xu, rows * a.KU * 24 * sizeof(uint16_t)));
+        }
         return JX_OK;
     }
 };
@@ -237,7 +245,10 @@ int ensure_workspace(jx_moe_layer* L, int n) {
     // h's matrix-core form: K = d_ff, or d_ff padded to whole super-blocks for fp32 h
     const int hK = L->down_f32 ? (L->F + 255) / 256 * 256 : L->F;
     const int hKs = L->sdown_f32 ? (L->Fs + 255) / 256 * 256 : L->Fs;
-    if ((r = L->xh.alloc((size_t)cap, L->d)) != JX_OK || (r = L->hh.alloc(nk, hK)) != JX_OK) {
+    // x's forms: block-unit for Q4_K gate/up matrices, hi/lo for the others (routed and shared)
+    const bool xunit = L->gate.m.type == jx::T_Q4_K || (L->shared && L->sgate.m.type == jx::T_Q4_K);
+    const bool xhilo = L->gate.m.type != jx::T_Q4_K || (L->shared && L->sgate.m.type != jx::T_Q4_K);
+    if ((r = L->xh.alloc((size_t)cap, L->d, xhilo, xunit)) != JX_OK || (r = L->hh.alloc(nk, hK)) != JX_OK) {
         L->cap = 0;
         return r;
     }

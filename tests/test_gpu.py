@@ -254,6 +254,41 @@ def test_dispatch_many_pairs(moe, port, E, k, n):
     L.close()
 
 
+@pytest.mark.parametrize("name", ["dsv2lite", "mixtral"])
+def test_q4k_gateup_block_scales(moe, port, name):
+    """The Q4_K gate/up GEMM keeps its accumulator in units of each 32-block's activation scale:
+    tokens with leading and inner zero blocks, a zero 256-block, one nonzero block, block scales
+    2^4 above (with these weights the reference's own output overflows fp32 from 2^8) and 2^-12
+    below the rest (unit ratios of 2^+-12 at every block), blocks whose fp16 scale underflows to
+    zero while their quants do not, and an all-zero token, on the matrix cores against the oracle."""
+    cfg, lw = layer(name)
+    n = 64
+    x = synth.make_tokens(cfg, n, seed=21).copy()
+    d = x.shape[1]
+    blocks = x.reshape(n, d // 32, 32)
+    x[0, :96] = 0.0
+    x[1, 256:512] = 0.0
+    x[2, :] = 0.0
+    x[2, 1000:1010] = 3.0
+    blocks[3, 1] *= 2.0 ** 4
+    blocks[4, ::2] *= 2.0 ** -12
+    blocks[5, 1::3] *= 2.0 ** -30  # fp16 scale 0, quants nonzero
+    x[6, :] = 0.0
+    x[7, : d // 2] = 0.0
+    say(f"{name} n={n} extreme block scales")
+    L = moe.MoELayer.from_weights(lw)
+    out, ids, w, counts = L.forward(x, regime="mfma")
+    lg_o, ids_o, w_o = port.route(lw, x)
+    assert np.array_equal(ids, ids_o)
+    sel = np.array([0, 1, 2, 3, 4, 5, 7, 40], np.int32)
+    want = port.moe_forward(lw, x, sel)[0]
+    err = rel_err(out[sel], want)
+    say(f"{name}: max rel err {err:.2e}")
+    assert err <= REL_TOL
+    assert not np.any(out[6]), "an all-zero token gives a zero output"
+    L.close()
+
+
 @pytest.mark.parametrize("name", ["toy", "qwen15moe", "mixtral"])
 def test_decode_two_tokens_same_experts(moe, port, name):
     """Two identical tokens: every active expert holds a group of two pairs on the few-token path."""
