@@ -50,15 +50,14 @@ struct ActQ8 {
 //   hl [rows][KH][256]   per 128-element half-unit: fp16 hi x128, then lo x128,
 //                        of dx * q * 2^-E (an exact split of the dequantized
 //                        value scaled into fp16 range)
-//   pe [rows][KH]        2^E of each half-unit.  Gate/up inputs (written by the
-//                        router kernels) use one E per row, the exponent of the
-//                        row's largest block scale - 7; the down input (h, written
-//                        by the gate/up GEMM's epilogue) one E per half-unit, the
-//                        exponent of the half-unit's largest block scale - 7.
-//                        Either way |dx * q| * 2^-E < 2^15.
+//   pe [rows][KH]        2^E of each half-unit, one E per row (the GEMMs apply
+//                        the last half-unit's): the exponent of the row's largest
+//                        block scale - 7 for Q8_0 rows (x from the router kernels,
+//                        h from k_q8_to_acth), so |dx * q| * 2^-E < 2^15; the
+//                        exponent of max |h| - 14 for fp32 rows (k_f32_to_acth)
 //   xm [rows][KU][3][8]  per 256-element unit: bf16 pieces (hi, mid, lo) of
-//                        dx * sum(q) for its 8 blocks (Q4_K min term): times 2^-E
-//                        for per-row E, unscaled for per-half-unit E
+//                        dx * sum(q) (fp32 rows: the block sum) times 2^-E for its
+//                        8 blocks (Q4_K min term)
 // and, for the Q4_K gate/up GEMM, the block-unit form (each form is written
 // where its pointers are set):
 //   q16 [rows][K]        the quants q as fp16 (exact)
