@@ -543,6 +543,20 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
                     for (int ii = 0; ii < 4; ++ii)
                         rxv[t][ii] = *reinterpret_cast<const float4*>(rxs + jj * BN + 32 * t + 8 * ii);
             };
+            auto read_rx1 = [&](int jj, int t) {
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii)
+                    rxv[t][ii] = *reinterpret_cast<const float4*>(rxs + jj * BN + 32 * t + 8 * ii);
+            };
+            auto rescale = [&](int i, int t) {
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) {
+                    acc[i][t][4 * ii] *= rxv[t][ii].x;
+                    acc[i][t][4 * ii + 1] *= rxv[t][ii].y;
+                    acc[i][t][4 * ii + 2] *= rxv[t][ii].z;
+                    acc[i][t][4 * ii + 3] *= rxv[t][ii].w;
+                }
+            };
             read_av(0, av[0]);
             convert(0, wv[0]);
             if constexpr (UNIT) read_rx(0);
@@ -554,7 +568,61 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
                 // scheduling barriers), so their latency hides behind 2 * TN * TM MFMAs
                 if (st + 1 < 2 * HB) read_av(st + 1, av[b ^ 1]);
                 __builtin_amdgcn_sched_barrier(0);
-                if (UNIT && b == 0) {
+                if constexpr (UNIT && TN == 2 && TM == 2) {
+                    // tiles k = (t, i) in order (0,0) (0,1) (1,0) (1,1); tile k's rescale into block jj's
+                    // units must fall between its last MFMA of block jj - 1 and its first of block jj:
+                    // pair tile 0's two go in block jj - 1's second step, after their own MFMAs there,
+                    // and pair tile 1's two in block jj's first step, before theirs, so every step
+                    // carries two rescales beside its four MFMAs (a half-unit's first block has its
+                    // ratios staged only at its own first step and takes all four there)
+                    const int jj = st >> 1;
+                    if (b == 0) {
+                        if (jj == 0) {
+                            rescale(0, 0);
+                            acc[0][0] = mfma16(av[b][0][0], wv[b][0], acc[0][0]);
+                            rescale(1, 0);
+                            acc[1][0] = mfma16(av[b][0][0], wv[b][1], acc[1][0]);
+                        } else {
+                            acc[0][0] = mfma16(av[b][0][0], wv[b][0], acc[0][0]);
+                            acc[1][0] = mfma16(av[b][0][0], wv[b][1], acc[1][0]);
+                        }
+                        rescale(0, 1);
+                        acc[0][1] = mfma16(av[b][1][0], wv[b][0], acc[0][1]);
+                        rescale(1, 1);
+                        acc[1][1] = mfma16(av[b][1][0], wv[b][1], acc[1][1]);
+                        if (jj + 1 < HB) read_rx1(jj + 1, 0);
+                        if (jj == 0) {
+#pragma unroll
+                            for (int k = 0; k < 4; ++k) {
+                                __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                            }
+                        } else {
+                            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    } else {
+                        acc[0][0] = mfma16(av[b][0][0], wv[b][0], acc[0][0]);
+                        acc[1][0] = mfma16(av[b][0][0], wv[b][1], acc[1][0]);
+                        acc[0][1] = mfma16(av[b][1][0], wv[b][0], acc[0][1]);
+                        acc[1][1] = mfma16(av[b][1][0], wv[b][1], acc[1][1]);
+                        if (jj + 1 < HB) {
+                            rescale(0, 0);
+                            rescale(1, 0);
+                            read_rx1(jj + 1, 1);
+                            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                } else if (UNIT && b == 0) {
                     // a block's first step: each tile moves into the block's units right before its
                     // MFMA, so the MFMAs of the tiles before it run while the multiplies issue
 #pragma unroll
@@ -584,10 +652,10 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
 #pragma unroll
                             for (int i = 0; i < TM; ++i) acc[i][t] = mfma16(av[b][t][hl], wv[b][i], acc[i][t]);
                 }
-                if (UNIT && b == 1 && st + 1 < 2 * HB) read_rx((st + 1) >> 1);
+                if (UNIT && !(TN == 2 && TM == 2) && b == 1 && st + 1 < 2 * HB) read_rx((st + 1) >> 1);
                 if (st + 1 < 2 * HB) {
                     convert(st + 1, wv[b ^ 1]);  // VALU work spread between the MFMAs
-                    if (!UNIT || b == 1)
+                    if (!UNIT || (b == 1 && !(TN == 2 && TM == 2)))
 #pragma unroll
                         for (int k = 0; k < HL * TN * TM; ++k) {
                             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
