@@ -6,12 +6,16 @@
 // than the matrix core's own work, so the scales ride in fp16 MFMA operands
 // that fp16 holds exactly:
 //   A (weights)      Q4_K: sc_j * q  (0..945)   Q4_0: q - 8   Q8_0: q
-//   B (activations)  dx * q * 2^-E of the Q8_0 activations as an exact fp16
-//                    hi/lo pair (an 11-bit scale times |q| <= 127 has <= 18
-//                    significant bits; hi + lo carry 22): two MFMAs per product
+//   B (activations)  Q4_K gate/up: the Q8_0 quants q (block-unit form); acc is
+//                    kept in units of the current block's dx per pair and
+//                    multiplied by u(b-1) / u(b) once per 32-block, so a block's
+//                    exact integer MFMA sum lands in the block's own units.
+//                    Otherwise: dx * q * 2^-E as an exact fp16 hi/lo pair (an
+//                    11-bit scale times |q| <= 127 has <= 18 significant bits;
+//                    hi + lo carry 22), two MFMAs per product (down: hi only)
 // Every product is exact in fp32, so each block's sum equals the reference's
 // integer block sum times (sc_j and) dx up to fp32 rounding of the
-// accumulation.  (The exactness matters: h = SiLU(g) * u is re-quantized to
+// accumulation (and of the block-unit ratios).  (The exactness matters: h = SiLU(g) * u is re-quantized to
 // Q8_0 before the down projection, and a relative error of 2^-11 in g and u
 // moves ~1.4% of h's quants by one step, ~2.6e-3 relative in the layer output.)
 // What is left on the VALU: the accumulator is kept in units of the current
