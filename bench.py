@@ -1,26 +1,31 @@
 """MoE-layer benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME] [--no-configs] [--no-cpu]
 
-Default workload: the Mixtral-8x7B-shaped Q4_K MoE layer (d_model 4096,
-8 experts, top-2, d_ff 14336).  A step is one pass of the MoE block over one
-batch of seeded synthetic activations already resident in HBM:
+A step is one pass of the MoE block over one batch of seeded synthetic
+activations already resident in HBM (weights uploaded beforehand, outside the
+timed region).  Headline workload: the Mixtral-8x7B-shaped Q4_K MoE layer
+(d_model 4096, 8 experts, top-2, d_ff 14336):
   * prefill: 2048 tokens (matrix-core regime)     -> `value` (tokens/s)
   * decode : 1 token (dequant-GEMV regime)         -> the `decode` object
-Both lines report the roofline of their dominant kernel from HIP events
-recorded around every launch (a second pass of the same steps).  The prefill
-GEMMs run v_mfma_f32_32x32x16_f16 on exact integer-valued operands (Q4_K
-gate/up: sc*q in A, the Q8_0 quants q in B, the accumulator rescaled per
-32-block into the activation scale's units; Q4_0/Q8_0 gate/up: dx*q split into
-exact fp16 hi + lo in B), so their roofline peak is the fp16 one; the fraction
-of the int8 peak the north star names, and of the fp16 peak counting the
-MFMAs actually issued, are reported beside it.  The reference's CPU
-path (its own quant.cpp/tier.cpp built in oracle/_ref, AVX2 dot order) is
-timed on a bounded sample of the same workload on the host cores.
+and `configs`, every configured layer shape at its token counts, each with the
+algorithmic bytes and int8 ops of the pass and their roofline fractions.
+
+Timing: K steps between two device synchronizations give `value` and
+`ms_per_step`; HIP events recorded on the forward's stream around each step in
+the same timed region give the per-step median and p10/p90.  Before timing,
+the device-pointer asynchronous path (the one timed) is checked bit for bit
+against the host-pointer path.  Kernel durations for the rooflines come from a
+second pass with HIP events around every launch.  The prefill GEMMs run
+v_mfma_f32_32x32x16_f16 on exact integer-valued operands, so their roofline
+peak is the fp16 one; the fraction of the int8 peak is reported beside it.
+The reference's CPU path (its own quant.cpp/tier.cpp built in oracle/_ref,
+AVX2 dot order) is timed on a bounded token sample on the host cores.
 """
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import os
 import sys
@@ -39,6 +44,54 @@ HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 FP16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "mixtral_layer_traffic.json")
+
+# every configured point: (config, tokens)
+POINTS = [("toy", 1), ("qwen15moe", 1), ("qwen15moe", 64), ("mixtral", 1), ("mixtral", 512), ("mixtral", 2048),
+          ("qwen3moe", 2048), ("dsv2lite", 32)]
+
+
+class Hip:
+    """Streams and timing events of the HIP runtime the library itself loaded (ctypes)."""
+
+    def __init__(self):
+        self.lib = C.CDLL("libamdhip64.so")
+        for fn in ("hipStreamCreate", "hipEventCreate"):
+            getattr(self.lib, fn).argtypes = [C.POINTER(C.c_void_p)]
+        self.lib.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        self.lib.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.lib.hipStreamSynchronize.argtypes = [C.c_void_p]
+        self.lib.hipEventDestroy.argtypes = [C.c_void_p]
+        s = C.c_void_p()
+        self._ok(self.lib.hipStreamCreate(C.byref(s)), "hipStreamCreate")
+        self.stream = s.value
+
+    @staticmethod
+    def _ok(rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed: {rc}")
+
+    def events(self, n):
+        evs = []
+        for _ in range(n):
+            e = C.c_void_p()
+            self._ok(self.lib.hipEventCreate(C.byref(e)), "hipEventCreate")
+            evs.append(e.value)
+        return evs
+
+    def record(self, ev):
+        self._ok(self.lib.hipEventRecord(ev, self.stream), "hipEventRecord")
+
+    def sync(self):
+        self._ok(self.lib.hipStreamSynchronize(self.stream), "hipStreamSynchronize")
+
+    def elapsed_ms(self, a, b):
+        ms = C.c_float()
+        self._ok(self.lib.hipEventElapsedTime(C.byref(ms), a, b), "hipEventElapsedTime")
+        return ms.value
+
+    def free(self, evs):
+        for e in evs:
+            self.lib.hipEventDestroy(e)
 
 
 def measured_traffic(role, tokens):
@@ -90,51 +143,98 @@ def algorithmic(cfg, n, counts):
                 gateup_ops=2 * n * cfg.top_k * 2 * d * Fd, down_bytes=distinct * dn_bytes)
 
 
-def run_gpu(L, cfg, n, steps, warmup, regime):
+def pct(a, q):
+    return float(np.percentile(np.asarray(a), q))
+
+
+def run_gpu(hip, L, cfg, n, steps, warmup, regime=None):
+    """Warm-up, a bit-exact check of the timed path, K timed steps, then a profiled pass."""
     from jxai_amd import moe
     x = synth.make_tokens(cfg, n)
     xb = moe.DeviceBuffer(x.nbytes).upload(x)
     ob = moe.DeviceBuffer(x.nbytes)
-    _, ids, w, counts = L.forward(x, regime=regime)  # routing of this batch (host copy)
+    want, ids, w, counts = L.forward(x, regime=regime)  # host-pointer path; routing of this batch
     for _ in range(warmup):
-        L.forward_device(xb, n, ob, sync=False, regime=regime)
+        L.forward_device(xb, n, ob, sync=False, regime=regime, stream=hip.stream)
+    hip.sync()
+    got = ob.download(np.empty_like(x))
+    if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
+        raise SystemExit(f"bench: the timed device path differs from the host path ({cfg.name}, n={n})")
+    evs = hip.events(2 * steps)
     moe.lib().jx_device_synchronize()
-    # timed region: the production path (captured graph replays), no per-launch events
+    # timed region: the production path (graph replays for small batches), events between steps only
     t0 = time.perf_counter()
-    for _ in range(steps):
-        L.forward_device(xb, n, ob, sync=False, regime=regime)
+    for i in range(steps):
+        hip.record(evs[2 * i])
+        L.forward_device(xb, n, ob, sync=False, regime=regime, stream=hip.stream)
+        hip.record(evs[2 * i + 1])
+    hip.sync()
     moe.lib().jx_device_synchronize()
     t1 = time.perf_counter()
+    step_ms = [hip.elapsed_ms(evs[2 * i], evs[2 * i + 1]) for i in range(steps)]
+    hip.free(evs)
     # kernel durations: the same steps again with HIP events around every launch
     L.profile(True)
     for _ in range(steps):
-        L.forward_device(xb, n, ob, sync=False, regime=regime)
-    moe.lib().jx_device_synchronize()
+        L.forward_device(xb, n, ob, sync=False, regime=regime, stream=hip.stream)
+    hip.sync()
     prof = L.profile_read()
     L.profile(False)
     xb.free()
     ob.free()
-    return (t1 - t0) / steps, prof, counts
+    return dict(wall_s=(t1 - t0) / steps, step_ms=step_ms, prof=prof, counts=counts)
 
 
-def cpu_baseline(lw, cfg, n, budget_s=12.0, max_tokens=None):
-    """Reference CPU path (oracle/_ref) or the C restatement on a bounded token sample."""
+def step_stats(r):
+    s = r["step_ms"]
+    return {"median": float(np.median(s)), "p10": pct(s, 10), "p90": pct(s, 90), "mean_wall": r["wall_s"] * 1e3}
+
+
+def point_line(cfg, n, r):
+    """tok/s, algorithmic work and roofline fractions of one configured point."""
+    a = algorithmic(cfg, n, r["counts"])
+    t = float(np.median(r["step_ms"])) / 1e3
+    return {"tokens": n, "tok_s": n / t, "step_ms": step_stats(r), "bytes": a["bytes"], "int8_ops": a["ops"],
+            "distinct_experts": a["distinct"], "hbm_frac": a["bytes"] / t / 1e9 / HBM_PEAK_GBS,
+            "int8_frac": a["ops"] / t / 1e12 / INT8_PEAK_TOPS,
+            "roofline_frac": max(a["bytes"] / (HBM_PEAK_GBS * 1e9), a["ops"] / (INT8_PEAK_TOPS * 1e12)) / t,
+            "kernels_us": {k: v[0] * 1e3 / max(v[1], 1) for k, v in r["prof"].items()}}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(lw, cfg, n, sample=512, runs=3):
+    """Reference CPU path (oracle/_ref) or the C restatement: one warm-up, then the median of `runs`
+    timings of the same contiguous token sample (the reference has no batched MoE: per token)."""
     from oracle import oracle as O
     kind = "reference" if O.available("reference") else "port"
     o = O.Oracle(kind, avx512=False)
     x = synth.make_tokens(cfg, n)
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    affinity = len(os.sched_getaffinity(0))
+    threads = int(os.environ.get("OMP_NUM_THREADS", affinity))
+    cores = min(threads, affinity)
+    m = min(sample, n)
+    sel = np.arange(m, dtype=np.int32)
     o.moe_forward(lw, x, np.array([0], np.int32))  # warm-up (page-in, thread pool)
-    done, t0 = 0, time.perf_counter()
-    limit = max_tokens or n
-    while done < limit and time.perf_counter() - t0 < budget_s:
-        m = min(8, limit - done)
-        o.moe_forward(lw, x, np.arange(done, done + m, dtype=np.int32))
-        done += m
-    dt = time.perf_counter() - t0
-    return {"value": done / dt, "unit": "tok/s", "cores": cores, "kind": kind,
-            "sample": f"first {done} of the {n} tokens through the MoE block, per-token path "
-                      f"(the reference has no batched MoE), {dt:.1f} s, OMP threads {cores}, AVX2 dot order"}
+    rates = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        o.moe_forward(lw, x, sel)
+        rates.append(m / (time.perf_counter() - t0))
+    scaled = "" if m == n else f", scaled: the first {m} of the {n} tokens"
+    return {"value": float(np.median(rates)), "unit": "tok/s", "cores": cores, "kind": kind,
+            "cpu_model": cpu_model(), "affinity_cpus": affinity, "runs_tok_s": rates,
+            "sample": f"median of {runs} runs over tokens 0..{m - 1} of the {n}-token batch through the MoE "
+                      f"block, per-token path{scaled}; AVX2 dot order, OpenMP threads {cores}"}
 
 
 def main():
@@ -146,6 +246,7 @@ def main():
     ap.add_argument("--prefill-tokens", type=int, default=2048)
     ap.add_argument("--decode-tokens", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-config object")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy (scale for the rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -156,19 +257,22 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path (experts would shard by "
               "expert parallelism, see DESIGN.md); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    steps = max(args.steps, 1)
 
     from jxai_amd import moe
     cfg = synth.CONFIGS[args.config]
     print(f"[bench] generating {cfg.describe}", file=sys.stderr, flush=True)
     lw = synth.make_layer(cfg)
     moe.init(0)
+    hip = Hip()
     L = moe.MoELayer.from_weights(lw)
 
     n = args.prefill_tokens
     print(f"[bench] prefill {n} tokens", file=sys.stderr, flush=True)
-    s_pre, prof_pre, counts_pre = run_gpu(L, cfg, n, args.steps, args.warmup, "mfma")
-    a_pre = algorithmic(cfg, n, counts_pre)
-    gu_ms, gu_n = prof_pre.get("gateup_mfma", (0.0, 1))
+    r_pre = run_gpu(hip, L, cfg, n, steps, args.warmup, "mfma")
+    s_pre = r_pre["wall_s"]
+    a_pre = algorithmic(cfg, n, r_pre["counts"])
+    gu_ms, gu_n = r_pre["prof"].get("gateup_mfma", (0.0, 1))
     gu_avg = gu_ms / max(gu_n, 1) / 1e3
     gu_rate = a_pre["gateup_ops"] / gu_avg / 1e12
     pre_roof = {"bound": "mfma", "kernel": "k_wgemm<Q4_K, gate+up> (fp16 matrix-core grouped GEMM + SwiGLU)",
@@ -182,28 +286,52 @@ def main():
 
     nd = args.decode_tokens
     print(f"[bench] decode {nd} token(s)", file=sys.stderr, flush=True)
-    s_dec, prof_dec, counts_dec = run_gpu(L, cfg, nd, max(args.steps * 10, 50), args.warmup * 4, "gemv")
-    a_dec = algorithmic(cfg, nd, counts_dec)
-    dg_ms, dg_n = prof_dec.get("gateup_gemv", (0.0, 1))
+    dsteps = max(steps * 10, 50)
+    r_dec = run_gpu(hip, L, cfg, nd, dsteps, args.warmup * 4, "gemv")
+    s_dec = r_dec["wall_s"]
+    a_dec = algorithmic(cfg, nd, r_dec["counts"])
+    dg_ms, dg_n = r_dec["prof"].get("gateup_gemv", (0.0, 1))
     dg_avg = dg_ms / max(dg_n, 1) / 1e3
+    dec_med = float(np.median(r_dec["step_ms"])) / 1e3
     dec_roof = {"bound": "hbm", "kernel": "k_gemv_gateup<Q4_K> (gate+up dequant-GEMV + SwiGLU)",
                 "achieved": a_dec["gateup_bytes"] / dg_avg / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": a_dec["gateup_bytes"] / dg_avg / 1e9 / HBM_PEAK_GBS,
                 "traffic": measured_traffic("gateup_gemv", nd),
                 "avg_launch_us": dg_avg * 1e6,
-                "layer_hbm_frac": a_dec["bytes"] / s_dec / 1e9 / HBM_PEAK_GBS}
+                "layer_hbm_frac": a_dec["bytes"] / s_dec / 1e9 / HBM_PEAK_GBS,
+                "layer_hbm_frac_median_step": a_dec["bytes"] / dec_med / 1e9 / HBM_PEAK_GBS}
 
     cpu = None
     if not args.no_cpu:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         cpu = cpu_baseline(lw, cfg, n)
+    L.close()
+    del lw
+
+    configs = None
+    if not args.no_configs:
+        configs = {}
+        layers = {}
+        for name, tok in POINTS:
+            if name not in layers:
+                layers.clear()
+                c = synth.CONFIGS[name]
+                print(f"[bench] configs: {c.describe}", file=sys.stderr, flush=True)
+                layers[name] = (c, moe.MoELayer.from_weights(synth.make_layer(c)))
+            c, Lc = layers[name]
+            print(f"[bench] configs: {name} @ {tok}", file=sys.stderr, flush=True)
+            reps = steps if tok >= 512 else max(steps * 5, 50)
+            r = run_gpu(hip, Lc, c, tok, reps, args.warmup)
+            configs[f"{name}@{tok}"] = point_line(c, tok, r)
+        for _, Lc in layers.values():
+            Lc.close()
 
     line = {
         "metric": METRIC,
         "value": n / s_pre,
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": s_pre * 1e3,
         "higher_is_better": True,
@@ -214,15 +342,17 @@ def main():
         "config": {"workload": f"{cfg.describe}, prefill {n} tokens", "d_model": cfg.d_model,
                    "n_experts": cfg.n_experts, "top_k": cfg.top_k, "d_ff": cfg.d_ff,
                    "weights": F.NAMES[cfg.wtype], "tokens": n},
+        "step_ms": step_stats(r_pre),
+        "timed_path_check": "device-pointer async path == host path, bit for bit (every measured point)",
         "roofline": pre_roof,
         "cpu_baseline": cpu,
-        "kernels_ms_per_step": {k: v[0] / args.steps for k, v in prof_pre.items()},
+        "kernels_ms_per_step": {k: v[0] / steps for k, v in r_pre["prof"].items()},
         "decode": {"value": nd / s_dec, "unit": "tok/s", "tokens": nd, "ms_per_step": s_dec * 1e3,
-                   "roofline": dec_roof,
-                   "kernels_us_per_step": {k: v[0] * 1e3 / max(args.steps * 10, 50) for k, v in prof_dec.items()}},
+                   "step_ms": step_stats(r_dec), "roofline": dec_roof,
+                   "kernels_us_per_step": {k: v[0] * 1e3 / dsteps for k, v in r_dec["prof"].items()}},
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
-    L.close()
 
 
 if __name__ == "__main__":

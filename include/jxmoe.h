@@ -35,12 +35,16 @@ enum {
 /* GGML tensor type codes, as GGMLType in include/common.h:45-77. */
 enum { JX_TYPE_F32 = 0, JX_TYPE_Q4_0 = 2, JX_TYPE_Q8_0 = 8, JX_TYPE_Q4_K = 12 };
 
+/* Gated activation of the expert FFN (hp_.use_gelu, src/transformer.cpp:1995,
+ * passed to matmul_swiglu_quant_f32 at 2724; src/quant.cpp:3999-4007). */
+enum { JX_ACT_SILU = 0, JX_ACT_GELU_TANH = 1 };
+
 /* jx_moe_forward flags */
 enum {
     JX_FWD_DEVICE_PTRS = 1u << 0, /* x, out, ids, weights, counts on the device  */
     JX_FWD_ASYNC = 1u << 1,       /* return after enqueueing (device ptrs only)   */
     JX_FWD_FORCE_GEMV = 1u << 2,  /* force the decode (dequant-GEMV) regime       */
-    JX_FWD_FORCE_MFMA = 1u << 3   /* force the prefill (int8 MFMA GEMM) regime    */
+    JX_FWD_FORCE_MFMA = 1u << 3   /* force the prefill (matrix-core GEMM) regime  */
 };
 
 /* One MoE layer, as bound by bind_tensors (src/transformer.cpp:2142-2186).
@@ -64,6 +68,12 @@ typedef struct jx_moe_layer_desc {
     const void* sh_up;
     const void* sh_down;
     const float* sh_gate_inp; /* [d] fp32 ffn_gate_inp_shexp, or NULL (scale 1) */
+    int32_t activation;    /* JX_ACT_SILU or JX_ACT_GELU_TANH (hp_.use_gelu)     */
+    int32_t router_type;   /* type of `router`: JX_TYPE_F32 (0).  The reference
+                              also accepts F16/BF16 routers through
+                              matmul_quant_f32 (transformer.cpp:2591), whose
+                              8-lane dot order (quant.cpp:3015-3055) this
+                              library does not reproduce: JX_ERR_UNSUPPORTED */
 } jx_moe_layer_desc;
 
 typedef struct jx_moe_layer jx_moe_layer;
@@ -99,6 +109,12 @@ int jx_moe_forward(jx_moe_layer* layer, const float* x, int32_t n_tok, float* ou
  * (the reference's router_logits vector, src/transformer.cpp:2589-2594). */
 int jx_moe_last_logits(jx_moe_layer* layer, float* logits_host, int32_t n_tok);
 
+/* Q8_0 blocks of the last forward's activations as the router kernels wrote
+ * them, [n_tok][d_model / 32] blocks of 34 bytes (fp16 d, 32 int8) in host
+ * memory: the x_q8 vector matmul_swiglu_quant_f32 builds with
+ * quantize_row_q8_0 (src/quant.cpp:3984-3992, 1029-1045). */
+int jx_moe_last_xq8(jx_moe_layer* layer, void* blocks_host, int32_t n_tok);
+
 /* Per-kernel-class device time of the forwards run since profiling was
  * enabled, measured with HIP events on the forward's stream.  names is a
  * ';'-separated list written into names_buf. */
@@ -119,9 +135,10 @@ void jx_qmatrix_destroy(jx_qmatrix* m);
  * (rows >= 8 and supports_q8_activation), fp32 otherwise.  Host pointers. */
 int jx_matmul_quant_f32(jx_qmatrix* W, const float* x, float* out);
 
-/* out[r] = SiLU(Wg[r] . x) * (Wu[r] . x)  (matmul_swiglu_quant_f32,
- * include/quant.h:354-362; src/quant.cpp:3970-4009).  Host pointers. */
-int jx_matmul_swiglu_quant_f32(jx_qmatrix* Wg, jx_qmatrix* Wu, const float* x, float* out);
+/* out[r] = act(Wg[r] . x) * (Wu[r] . x), act = SiLU or (use_gelu) GELU-tanh
+ * (matmul_swiglu_quant_f32, include/quant.h:354-362; src/quant.cpp:3970-4009).
+ * Host pointers. */
+int jx_matmul_swiglu_quant_f32(jx_qmatrix* Wg, jx_qmatrix* Wu, const float* x, float* out, int32_t use_gelu);
 
 /* quantize_row_q8_0 (include/quant.h:112; src/quant.cpp:1029-1045) on the
  * device: x [k] fp32 -> k/32 blocks of 34 bytes (fp16 d + 32 int8).  Host pointers. */

@@ -18,9 +18,13 @@ JX_FWD_ASYNC = 1 << 1
 JX_FWD_FORCE_GEMV = 1 << 2
 JX_FWD_FORCE_MFMA = 1 << 3
 
+JX_ACT_SILU = 0
+JX_ACT_GELU_TANH = 1
+
 # Every symbol include/jxmoe.h declares.
 EXPORTS = [
     "jx_moe_init", "jx_moe_layer_create", "jx_moe_layer_destroy", "jx_moe_forward", "jx_moe_last_logits",
+    "jx_moe_last_xq8",
     "jx_moe_profile", "jx_moe_profile_read", "jx_qmatrix_create", "jx_qmatrix_destroy", "jx_matmul_quant_f32",
     "jx_matmul_swiglu_quant_f32", "jx_quantize_row_q8_0", "jx_dev_alloc", "jx_dev_free", "jx_memcpy_htod",
     "jx_memcpy_dtoh", "jx_device_synchronize", "jx_moe_last_error",
@@ -41,6 +45,7 @@ class LayerDesc(C.Structure):
         ("sh_gate_type", C.c_int32), ("sh_up_type", C.c_int32), ("sh_down_type", C.c_int32),
         ("sh_gate", _vp), ("sh_up", _vp), ("sh_down", _vp),
         ("sh_gate_inp", _vp),
+        ("activation", C.c_int32), ("router_type", C.c_int32),
     ]
 
 
@@ -67,6 +72,7 @@ def lib() -> C.CDLL:
     L.jx_moe_layer_destroy.restype = None
     L.jx_moe_forward.argtypes = [_vp, _vp, C.c_int32, _vp, _vp, _vp, _vp, _vp, C.c_uint32]
     L.jx_moe_last_logits.argtypes = [_vp, _vp, C.c_int32]
+    L.jx_moe_last_xq8.argtypes = [_vp, _vp, C.c_int32]
     L.jx_moe_profile.argtypes = [_vp, C.c_int32]
     L.jx_moe_profile_read.argtypes = [_vp, C.c_char_p, C.c_size_t, C.POINTER(C.c_double), C.POINTER(C.c_int64),
                                       C.c_int32, C.POINTER(C.c_int32)]
@@ -74,7 +80,7 @@ def lib() -> C.CDLL:
     L.jx_qmatrix_destroy.argtypes = [_vp]
     L.jx_qmatrix_destroy.restype = None
     L.jx_matmul_quant_f32.argtypes = [_vp, _vp, _vp]
-    L.jx_matmul_swiglu_quant_f32.argtypes = [_vp, _vp, _vp, _vp]
+    L.jx_matmul_swiglu_quant_f32.argtypes = [_vp, _vp, _vp, _vp, C.c_int32]
     L.jx_quantize_row_q8_0.argtypes = [_vp, _vp, C.c_int64]
     L.jx_dev_alloc.argtypes = [C.c_size_t, C.POINTER(_vp)]
     L.jx_dev_free.argtypes = [_vp]

@@ -350,6 +350,11 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
 
     const int H = in.KH;
     const int KB = in.K / 32;
+    // Source rows ascend within a tile (an expert's pairs are in token order; down rows are
+    // consecutive pairs), so the workgroup's buffers are based at its first source row in 64 bits
+    // and every per-lane offset is relative to it: below 2^32 whenever n_tok rows of the activation
+    // forms are (jx_moe_forward refuses larger batches).
+    const size_t src0 = (size_t)sm.src[0];
     // Staging: a DMA instruction moves PPI rows x PB bytes; lane l takes chunk l % CPP of row
     // PPI * slot + l / CPP, stored at chunk ((l % CPP) ^ (row % CPP)), so the operand reads of 16
     // lanes hit 16 distinct 16-byte bank groups.  The half-unit adds h * 512, a uniform term.
@@ -357,16 +362,17 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
         const int r = PPI * (wave * PER + k) + lane / CPP;
-        soff[k] = (uint32_t)sm.src[r] * (uint32_t)(H * GB) + (uint32_t)(((lane % CPP) ^ (r % CPP)) << 4);
+        soff[k] = (uint32_t)(sm.src[r] - (int)src0) * (uint32_t)(H * GB) + (uint32_t)(((lane % CPP) ^ (r % CPP)) << 4);
     }
     const int sj = wave;  // pe / xm / rx: lane l of wave w < BN / 64 takes pair 64 * w + l
-    const int srow = sm.src[64 * min(sj, BN / 64 - 1) + lane];
-    const uint32_t peoff = (uint32_t)srow * (uint32_t)(H * 4);
-    const uint32_t xoff = Q4K ? (uint32_t)srow * (uint32_t)(in.KU * 48) : 0u;
-    const uint32_t rxoff = UNIT ? (uint32_t)srow * (uint32_t)(H * HB * 4) : 0u;
-    const uint8_t* qsrc = reinterpret_cast<const uint8_t*>(UNIT ? in.q16 : in.hl);
-    const uint8_t* pesrc = reinterpret_cast<const uint8_t*>(UNIT ? in.pu : in.pe);
-    const uint8_t* xmsrc = reinterpret_cast<const uint8_t*>(UNIT ? in.xu : in.xm);
+    const uint32_t srow = (uint32_t)(sm.src[64 * min(sj, BN / 64 - 1) + lane] - (int)src0);
+    const uint32_t peoff = srow * (uint32_t)(H * 4);
+    const uint32_t xoff = Q4K ? srow * (uint32_t)(in.KU * 48) : 0u;
+    const uint32_t rxoff = UNIT ? srow * (uint32_t)(H * HB * 4) : 0u;
+    const uint8_t* qsrc = reinterpret_cast<const uint8_t*>(UNIT ? in.q16 : in.hl) + src0 * (size_t)(H * GB);
+    const uint8_t* pesrc = reinterpret_cast<const uint8_t*>(UNIT ? in.pu : in.pe) + src0 * (size_t)(H * 4);
+    const uint8_t* xmsrc = reinterpret_cast<const uint8_t*>(UNIT ? in.xu : in.xm) + src0 * (size_t)(in.KU * 48);
+    const uint8_t* rxsrc = UNIT ? reinterpret_cast<const uint8_t*>(in.rx) + src0 * (size_t)(H * HB * 4) : nullptr;
     auto stage = [&](int h) {
         St& S = sm.st[h & 1];
         const uint8_t* base = qsrc + (size_t)h * GB;
@@ -381,7 +387,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
         }
         if constexpr (UNIT) {  // unit ratios of the half-unit's blocks, [block][pair]
             if (wave < BN / 64) {
-                const uint8_t* rb = reinterpret_cast<const uint8_t*>(in.rx) + (size_t)h * (HB * 4) + rxoff;
+                const uint8_t* rb = rxsrc + (size_t)h * (HB * 4) + rxoff;
 #pragma unroll
                 for (int j = 0; j < HB; ++j) dma4(rb + 4 * j, sm.rx[h & 1] + j * BN + 64 * sj);
             }
@@ -843,7 +849,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
                 for (int r = 0; r < 16; ++r) {
                     const float gv = acc[0][t][r], uv = acc[1][t][r];
                     const int pr = pbase + 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
-                    hs[pr * HLD + rw * 32 + n] = (gv / (1.0f + expf(-gv))) * uv;  // SwiGLU
+                    hs[pr * HLD + rw * 32 + n] = gated(gv, uv, W0.act);  // SwiGLU / GELU
                 }
         }
         __syncthreads();

@@ -505,7 +505,7 @@ k_gemv_gateup(QMat G, QMat U, ActQ8 xq, Groups grp, ActQ8 hq, float* hf, int hf_
                     g += red[w][j][m];
                     u += red[HW + w][j][m];
                 }
-                const float hv = (g / (1.0f + expf(-g))) * u;
+                const float hv = gated(g, u, G.act);
                 const size_t row = (size_t)(p0 + tb0 + j);
                 store_q8_block(hv, m, h == 0 && hq.q != nullptr, hq, row, rt);
                 if (hf && h == 0) hf[row * (size_t)hf_ld + rt * 32 + m] = hv;
@@ -777,7 +777,7 @@ k_gemv_mx(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_l
                 if constexpr (GATEUP) {
 #pragma unroll
                     for (int w = 0; w < HW; ++w) v1 += red[HW + w][r][lane];
-                    const float hv = (v0 / (1.0f + expf(-v0))) * v1;
+                    const float hv = gated(v0, v1, W0.act);
                     store_q8_block(hv, m, t < nt && hq.q != nullptr, hq, row, rt);
                     if (hf && t < nt) hf[row * (size_t)hf_ld + rt * 32 + m] = hv;
                 } else {

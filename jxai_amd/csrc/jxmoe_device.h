@@ -48,6 +48,19 @@ __device__ __forceinline__ float round_away(float v) {
     return (__builtin_fabsf(fr) >= 0.5f) ? t + __builtin_copysignf(1.0f, v) : t;
 }
 
+enum : int { ACT_SILU = 0, ACT_GELU_TANH = 1 };
+
+// The gated activation of matmul_swiglu_quant_f32 (src/quant.cpp:3999-4007):
+// SiLU(g) * u, or with use_gelu (the gemma family, transformer.cpp:1995) the
+// tanh form of GELU, 0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3))) * u.
+__device__ __forceinline__ float gated(float g, float u, int act) {
+    if (act == ACT_GELU_TANH) {
+        const float inner = 0.7978845608028654f * __builtin_fmaf(0.044715f * g * g, g, g);
+        return 0.5f * g * (1.0f + tanhf(inner)) * u;
+    }
+    return (g / (1.0f + expf(-g))) * u;
+}
+
 __device__ __forceinline__ int sdot4(int a, int b, int c) {
     return __builtin_amdgcn_sdot4(a, b, c, false);
 }

@@ -35,6 +35,9 @@ struct QMat {
     // -dmin * m_j / u for the 8 sub-blocks j, u = d (1 where d is zero).
     const uint8_t* mn = nullptr;
     size_t mn_es = 0;  // per-expert stride (bytes)
+    // Gated activation applied to this matrix's outputs when it is the gate of
+    // a gate/up pair (ACT_SILU or ACT_GELU_TANH); unused otherwise.
+    int act = 0;
 };
 constexpr size_t QMAT_PAD = 8192;
 

@@ -1,10 +1,12 @@
 // C-ABI runtime of the MoE expert path: device init, one-time upload and
 // repack of a layer, workspace management, the forward pipeline
-//   route -> dispatch -> {dequant-GEMV | int8-MFMA GEMM} x (gate/up, down) -> combine
+//   route -> dispatch -> {dequant-GEMV | matrix-core GEMM} x (gate/up, down) -> combine
 // and the function-level drop-ins of the reference's math API.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
+#include <climits>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -19,7 +21,9 @@
 namespace {
 
 thread_local std::string g_err;
-int g_device = -1;
+// The device jx_moe_init selected, for the whole process (layers and matrices
+// keep their own device; entry points make it current on the calling thread).
+std::atomic<int> g_device{-1};
 
 int fail(int code, const std::string& msg) {
     g_err = msg;
@@ -84,6 +88,9 @@ int upload_matrix(int type, int n_mats, int rows, int cols, const void* host, De
     const size_t sc_u = type == jx::T_Q4_K ? 16 : 2;
     m.qs_es = units * qs_u;
     m.sc_es = units * sc_u;
+    // the GEMMs address one expert's matrix with 32-bit offsets (min table: 12x the headers)
+    if (m.qs_es >= ((size_t)1 << 32) || m.sc_es * 12 >= ((size_t)1 << 32))
+        return fail(JX_ERR_UNSUPPORTED, "one expert matrix exceeds 4 GiB");
     const size_t raw_bytes = (size_t)n_mats * rows * row_bytes(type, cols);
     uint8_t* raw = nullptr;
     HIPCHK(hipMalloc(&out.qs, m.qs_es * n_mats + jx::QMAT_PAD));
@@ -202,7 +209,14 @@ struct jx_moe_layer {
             return flags < o.flags;
         }
     };
-    std::map<GraphKey, hipGraphExec_t> graphs;
+    struct Graph {
+        hipGraphExec_t exec;
+        uint64_t last;  // graph_clock at the last replay
+    };
+    static constexpr int GRAPH_MAX_N = 64;      // token counts replayed from graphs
+    static constexpr size_t GRAPH_CACHE = 64;   // graphs kept (least recently used evicted)
+    std::map<GraphKey, Graph> graphs;
+    uint64_t graph_clock = 0;
     bool use_graphs = true;
 };
 
@@ -217,7 +231,7 @@ namespace {
 int ensure_workspace(jx_moe_layer* L, int n) {
     if (n <= L->cap) return JX_OK;
     // captured graphs hold the old buffer addresses
-    for (auto& kv : L->graphs) (void)hipGraphExecDestroy(kv.second);
+    for (auto& kv : L->graphs) (void)hipGraphExecDestroy(kv.second.exec);
     L->graphs.clear();
     const int cap = std::max(n, L->cap * 2);
     const size_t nk = (size_t)cap * L->k;
@@ -296,7 +310,7 @@ void free_layer(jx_moe_layer* L) {
     L->hh.release();
     L->hhs.release();
     for (auto ev : L->prof.pool) (void)hipEventDestroy(ev);
-    for (auto& kv : L->graphs) (void)hipGraphExecDestroy(kv.second);
+    for (auto& kv : L->graphs) (void)hipGraphExecDestroy(kv.second.exec);
     if (L->own) (void)hipStreamDestroy(L->own);
     if (L->side) (void)hipStreamDestroy(L->side);
     if (L->ev_fork) (void)hipEventDestroy(L->ev_fork);
@@ -503,6 +517,33 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     return JX_OK;
 }
 
+// The fp16 bits of a value that is an fp16 widened to fp32 (exact narrowing).
+uint16_t narrow_f16(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    const uint32_t sign = (u >> 16) & 0x8000u;
+    const int e = (int)((u >> 23) & 0xFF) - 112;
+    const uint32_t m = u & 0x7FFFFFu;
+    if (e <= 0) return (e < -10) ? (uint16_t)sign : (uint16_t)(sign | ((m | 0x800000u) >> (uint32_t)(14 - e)));
+    if (e >= 31) return (uint16_t)(sign | 0x7C00u);
+    return (uint16_t)(sign | ((uint32_t)e << 10) | (m >> 13));
+}
+
+// Q8_0 blocks (fp16 d, 32 int8) from a device ActQ8 of `rows` rows.
+int download_q8_blocks(const jx::ActQ8& a, int rows, uint8_t* out) {
+    const size_t k = (size_t)a.K, nb = (size_t)rows * (k / 32);
+    std::vector<int8_t> q((size_t)rows * k);
+    std::vector<float2> sc(nb);
+    HIPCHK(hipMemcpy(q.data(), a.q, q.size(), hipMemcpyDeviceToHost));
+    HIPCHK(hipMemcpy(sc.data(), a.s, nb * sizeof(float2), hipMemcpyDeviceToHost));
+    for (size_t b = 0; b < nb; ++b) {
+        const uint16_t h = narrow_f16(sc[b].x);
+        std::memcpy(out + b * 34, &h, 2);
+        std::memcpy(out + b * 34 + 2, q.data() + b * 32, 32);
+    }
+    return JX_OK;
+}
+
 // Scratch for the drop-ins (allocated per call; these are function-level
 // entry points for parity checks and single-matrix callers, not the layer path).
 struct Scratch {
@@ -548,6 +589,10 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
         return fail(JX_ERR_UNSUPPORTED, "d_model must be a multiple of 32, at most 8192");
     if (D->d_ff < 32 || D->d_ff % 32 != 0) return fail(JX_ERR_UNSUPPORTED, "d_ff must be a multiple of 32");
     if (!D->router || !D->gate_exps || !D->up_exps || !D->down_exps) return fail(JX_ERR_INVALID, "missing tensor");
+    if (D->router_type != JX_TYPE_F32)
+        return fail(JX_ERR_UNSUPPORTED, "router must be F32 (the F16/BF16 dot order of matmul_quant_f32 is not reproduced)");
+    if (D->activation != JX_ACT_SILU && D->activation != JX_ACT_GELU_TANH)
+        return fail(JX_ERR_INVALID, "activation must be JX_ACT_SILU or JX_ACT_GELU_TANH");
     if (D->gate_type != D->up_type) return fail(JX_ERR_UNSUPPORTED, "gate and up must share a type");
     // gate/up consume Q8_0 activations (cols = d_model); the fp32-activation
     // fallback of the reference is only implemented for Q4_K down projections.
@@ -601,10 +646,12 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
             return bail(fail(JX_ERR_HIP, "router bias upload"));
     }
     if ((r = upload_matrix(D->gate_type, L->E, L->F, L->d, D->gate_exps, L->gate, st, true)) != JX_OK) return bail(r);
+    L->gate.m.act = D->activation;
     if ((r = upload_matrix(D->up_type, L->E, L->F, L->d, D->up_exps, L->up, st, true)) != JX_OK) return bail(r);
     if ((r = upload_matrix(D->down_type, L->E, L->d, L->F, D->down_exps, L->down, st, true)) != JX_OK) return bail(r);
     if (L->shared) {
         if ((r = upload_matrix(D->sh_gate_type, 1, L->Fs, L->d, D->sh_gate, L->sgate, st, true)) != JX_OK) return bail(r);
+        L->sgate.m.act = D->activation;
         if ((r = upload_matrix(D->sh_up_type, 1, L->Fs, L->d, D->sh_up, L->sup, st, true)) != JX_OK) return bail(r);
         if ((r = upload_matrix(D->sh_down_type, 1, L->d, L->Fs, D->sh_down, L->sdown, st, true)) != JX_OK) return bail(r);
         if (D->sh_gate_inp) {
@@ -646,6 +693,10 @@ int jx_moe_forward(jx_moe_layer* L, const float* x, int32_t n_tok, float* out, i
         return fail(JX_ERR_INVALID, "JX_FWD_ASYNC needs JX_FWD_DEVICE_PTRS");
     if ((flags & JX_FWD_FORCE_GEMV) && (flags & JX_FWD_FORCE_MFMA))
         return fail(JX_ERR_INVALID, "conflicting regime flags");
+    // (token, slot) pairs are int32 indices, and the matrix-core GEMMs address a tile's activation rows
+    // with 32-bit offsets from its first row (n_tok rows of x's hi/lo form: 4 bytes per element)
+    if ((int64_t)n_tok * L->k > INT_MAX / 2 || (int64_t)n_tok * L->d * 4 >= ((int64_t)1 << 32))
+        return fail(JX_ERR_UNSUPPORTED, "n_tok too large for one call (split the batch)");
     HIPCHK(hipSetDevice(L->device));
     int r = ensure_workspace(L, n_tok);
     if (r != JX_OK) return r;
@@ -661,7 +712,10 @@ int jx_moe_forward(jx_moe_layer* L, const float* x, int32_t n_tok, float* out, i
     }
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     HIPCHK(hipStreamIsCapturing(st, &cap));
-    if (L->use_graphs && !L->prof.on && cap == hipStreamCaptureStatusNone) {
+    // Graphs pay off where launch overhead is a large share of the step: batches up to GRAPH_MAX_N
+    // tokens (decode and batched decode).  Larger batches (prefill: milliseconds of GEMM, and a new
+    // length per prompt) launch directly instead of capturing a graph for every length.
+    if (L->use_graphs && !L->prof.on && cap == hipStreamCaptureStatusNone && n_tok <= jx_moe_layer::GRAPH_MAX_N) {
         // the launch sequence depends only on (n, buffers, regime flags): replay a captured graph
         const jx_moe_layer::GraphKey key{n_tok, xin, outp, flags & (JX_FWD_FORCE_GEMV | JX_FWD_FORCE_MFMA)};
         auto it = L->graphs.find(key);
@@ -679,13 +733,17 @@ int jx_moe_forward(jx_moe_layer* L, const float* x, int32_t n_tok, float* out, i
             const hipError_t ei = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
             (void)hipGraphDestroy(g);
             if (ei != hipSuccess) return fail(JX_ERR_HIP, std::string("graph instantiate: ") + hipGetErrorString(ei));
-            if (L->graphs.size() >= 32) {
-                for (auto& kv : L->graphs) (void)hipGraphExecDestroy(kv.second);
-                L->graphs.clear();
+            if (L->graphs.size() >= jx_moe_layer::GRAPH_CACHE) {  // evict the least recently used
+                auto lru = L->graphs.begin();
+                for (auto g2 = L->graphs.begin(); g2 != L->graphs.end(); ++g2)
+                    if (g2->second.last < lru->second.last) lru = g2;
+                (void)hipGraphExecDestroy(lru->second.exec);
+                L->graphs.erase(lru);
             }
-            it = L->graphs.emplace(key, ex).first;
+            it = L->graphs.emplace(key, jx_moe_layer::Graph{ex, 0}).first;
         }
-        HIPCHK(hipGraphLaunch(it->second, st));
+        it->second.last = ++L->graph_clock;
+        HIPCHK(hipGraphLaunch(it->second.exec, st));
     } else if ((r = run_forward(L, xin, n_tok, outp, st, flags)) != JX_OK) {
         return r;
     }
@@ -710,6 +768,14 @@ int jx_moe_last_logits(jx_moe_layer* L, float* logits_host, int32_t n_tok) {
     HIPCHK(hipDeviceSynchronize());
     HIPCHK(hipMemcpy(logits_host, L->logits, (size_t)n_tok * L->E * 4, hipMemcpyDeviceToHost));
     return JX_OK;
+}
+
+int jx_moe_last_xq8(jx_moe_layer* L, void* blocks_host, int32_t n_tok) {
+    if (!L || !blocks_host) return fail(JX_ERR_INVALID, "null argument");
+    if (n_tok < 1 || n_tok > L->last_n) return fail(JX_ERR_INVALID, "n_tok exceeds the last forward");
+    HIPCHK(hipSetDevice(L->device));
+    HIPCHK(hipDeviceSynchronize());
+    return download_q8_blocks(L->xq, n_tok, static_cast<uint8_t*>(blocks_host));
 }
 
 int jx_moe_profile(jx_moe_layer* L, int32_t enable) {
@@ -808,7 +874,7 @@ int jx_matmul_quant_f32(jx_qmatrix* W, const float* x, float* out) {
     return JX_OK;
 }
 
-int jx_matmul_swiglu_quant_f32(jx_qmatrix* Wg, jx_qmatrix* Wu, const float* x, float* out) {
+int jx_matmul_swiglu_quant_f32(jx_qmatrix* Wg, jx_qmatrix* Wu, const float* x, float* out, int32_t use_gelu) {
     if (!Wg || !Wu || !x || !out) return fail(JX_ERR_INVALID, "null argument");
     if (Wg->rows != Wu->rows || Wg->cols != Wu->cols || Wg->type != Wu->type)
         return fail(JX_ERR_UNSUPPORTED, "gate and up must share shape and type");
@@ -833,7 +899,9 @@ int jx_matmul_swiglu_quant_f32(jx_qmatrix* Wg, jx_qmatrix* Wu, const float* x, f
     g.identity = 1;
     g.n_tok = 1;
     hq.K = rows;  // q == nullptr: no Q8_0 output wanted
-    jx::launch_gemv_gateup(Wg->w.m, Wu->w.m, a, g, 1, 1, hq, hf, nullptr);
+    jx::QMat gm = Wg->w.m;
+    gm.act = use_gelu ? jx::ACT_GELU_TANH : jx::ACT_SILU;
+    jx::launch_gemv_gateup(gm, Wu->w.m, a, g, 1, 1, hq, hf, nullptr);
     HIPCHK(hipGetLastError());
     HIPCHK(hipMemcpy(out, hf, (size_t)rows * 4, hipMemcpyDeviceToHost));
     return JX_OK;
@@ -854,31 +922,7 @@ int jx_quantize_row_q8_0(const float* x, void* blocks, int64_t k) {
     HIPCHK(hipMemcpy(xd, x, (size_t)k * 4, hipMemcpyHostToDevice));
     jx::launch_quantize_q8(xd, 1, (int)k, a, nullptr);
     HIPCHK(hipGetLastError());
-    std::vector<int8_t> q((size_t)k);
-    std::vector<float2> sc((size_t)k / 32);
-    HIPCHK(hipMemcpy(q.data(), a.q, (size_t)k, hipMemcpyDeviceToHost));
-    HIPCHK(hipMemcpy(sc.data(), a.s, (size_t)k / 32 * sizeof(float2), hipMemcpyDeviceToHost));
-    auto* out = static_cast<uint8_t*>(blocks);
-    for (size_t b = 0; b < (size_t)k / 32; ++b) {
-        // the scale is an fp16 value widened exactly; narrow it back bit for bit
-        const float f = sc[b].x;
-        uint32_t u;
-        std::memcpy(&u, &f, 4);
-        const uint32_t sign = (u >> 16) & 0x8000u;
-        const int e = (int)((u >> 23) & 0xFF) - 112;
-        uint32_t m = u & 0x7FFFFFu;
-        uint16_t h;
-        if (e <= 0) {
-            h = (e < -10) ? (uint16_t)sign : (uint16_t)(sign | ((m | 0x800000u) >> (uint32_t)(14 - e)));
-        } else if (e >= 31) {
-            h = (uint16_t)(sign | 0x7C00u);
-        } else {
-            h = (uint16_t)(sign | ((uint32_t)e << 10) | (m >> 13));
-        }
-        std::memcpy(out + b * 34, &h, 2);
-        std::memcpy(out + b * 34 + 2, q.data() + b * 32, 32);
-    }
-    return JX_OK;
+    return download_q8_blocks(a, 1, static_cast<uint8_t*>(blocks));
 }
 
 int jx_dev_alloc(size_t bytes, void** ptr) {

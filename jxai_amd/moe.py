@@ -70,12 +70,13 @@ class MoELayer:
     def __init__(self, *, n_experts, top_k, d_model, d_ff, gate_type, up_type, down_type, router,
                  gate_exps, up_exps, down_exps, router_bias=None, d_ff_shared=0, sh_gate_type=None,
                  sh_up_type=None, sh_down_type=None, sh_gate=None, sh_up=None, sh_down=None,
-                 sh_gate_inp=None, device: int = 0):
+                 sh_gate_inp=None, activation: int = 0, router_type: int = F.F32, device: int = 0):
         init(device)
         keep = [np.ascontiguousarray(a) if a is not None else None
                 for a in (router, router_bias, gate_exps, up_exps, down_exps, sh_gate, sh_up, sh_down, sh_gate_inp)]
         router, router_bias, gate_exps, up_exps, down_exps, sh_gate, sh_up, sh_down, sh_gate_inp = keep
-        assert router.dtype == np.float32 and router.size == n_experts * d_model
+        if router_type == F.F32:
+            assert router.dtype == np.float32 and router.size == n_experts * d_model
         for name, a, t, rows, cols in (("gate", gate_exps, gate_type, d_ff, d_model),
                                        ("up", up_exps, up_type, d_ff, d_model),
                                        ("down", down_exps, down_type, d_model, d_ff)):
@@ -85,7 +86,7 @@ class MoELayer:
         D = LayerDesc(n_experts, top_k, d_model, d_ff, gate_type, up_type, down_type,
                       _p(router), _p(router_bias), _p(gate_exps), _p(up_exps), _p(down_exps),
                       d_ff_shared, sh_gate_type or 0, sh_up_type or 0, sh_down_type or 0,
-                      _p(sh_gate), _p(sh_up), _p(sh_down), _p(sh_gate_inp))
+                      _p(sh_gate), _p(sh_up), _p(sh_down), _p(sh_gate_inp), activation, router_type)
         self.handle = C.c_void_p()
         check(lib().jx_moe_layer_create(C.byref(D), C.byref(self.handle)), "jx_moe_layer_create")
         self.E, self.k, self.d, self.F = n_experts, top_k, d_model, d_ff
@@ -101,7 +102,7 @@ class MoELayer:
                       sh_gate=lw.sh_gate, sh_up=lw.sh_up, sh_down=lw.sh_down, sh_gate_inp=lw.sh_gate_inp)
         return cls(n_experts=cfg.n_experts, top_k=cfg.top_k, d_model=cfg.d_model, d_ff=cfg.d_ff,
                    gate_type=gt, up_type=ut, down_type=dt, router=lw.router, router_bias=lw.router_bias,
-                   gate_exps=lw.gate, up_exps=lw.up, down_exps=lw.down, device=device, **kw)
+                   gate_exps=lw.gate, up_exps=lw.up, down_exps=lw.down, activation=cfg.act, device=device, **kw)
 
     def forward(self, x: np.ndarray, regime: str | None = None):
         """MoE block over host activations [n][d] -> (out [n][d], topk_ids, topk_w, counts)."""
@@ -116,16 +117,25 @@ class MoELayer:
               "jx_moe_forward")
         return out, ids, w, counts
 
-    def forward_device(self, x: DeviceBuffer, n: int, out: DeviceBuffer, sync: bool = True, regime=None) -> None:
-        """MoE block over device-resident activations (no host copies)."""
+    def forward_device(self, x: DeviceBuffer, n: int, out: DeviceBuffer, sync: bool = True, regime=None,
+                       stream=None) -> None:
+        """MoE block over device-resident activations (no host copies), enqueued on `stream`
+        (a hipStream_t as an integer; None: the layer's own stream)."""
         flags = JX_FWD_DEVICE_PTRS | (0 if sync else JX_FWD_ASYNC)
         flags |= {None: 0, "gemv": JX_FWD_FORCE_GEMV, "mfma": JX_FWD_FORCE_MFMA}[regime]
-        check(lib().jx_moe_forward(self.handle, x.ptr, n, out.ptr, None, None, None, None, flags), "jx_moe_forward")
+        st = None if stream is None else C.c_void_p(stream)
+        check(lib().jx_moe_forward(self.handle, x.ptr, n, out.ptr, None, None, None, st, flags), "jx_moe_forward")
 
     def last_logits(self, n: int) -> np.ndarray:
         out = np.empty((n, self.E), np.float32)
         check(lib().jx_moe_last_logits(self.handle, _p(out), n), "jx_moe_last_logits")
         return out
+
+    def last_xq8(self, n: int) -> np.ndarray:
+        """Q8_0 blocks of the last forward's activations as the router kernels wrote them."""
+        out = np.empty(n * (self.d // 32) * 34, np.uint8)
+        check(lib().jx_moe_last_xq8(self.handle, _p(out), n), "jx_moe_last_xq8")
+        return out.reshape(n, -1)
 
     def profile(self, enable: bool = True) -> None:
         check(lib().jx_moe_profile(self.handle, 1 if enable else 0), "jx_moe_profile")
@@ -184,13 +194,15 @@ def matmul_quant_f32(qtype: int, W, x, rows: int, cols: int) -> np.ndarray:
     return out
 
 
-def matmul_swiglu_quant_f32(gate_type: int, W_gate, up_type: int, W_up, x, exp_dim: int, cols: int) -> np.ndarray:
-    """SiLU(W_gate x) * (W_up x) on the GPU (reference: matmul_swiglu_quant_f32)."""
+def matmul_swiglu_quant_f32(gate_type: int, W_gate, up_type: int, W_up, x, exp_dim: int, cols: int,
+                            use_gelu: bool = False) -> np.ndarray:
+    """act(W_gate x) * (W_up x), act = SiLU or GELU-tanh, on the GPU (reference: matmul_swiglu_quant_f32)."""
     g = W_gate if isinstance(W_gate, QMatrix) else QMatrix(gate_type, W_gate, exp_dim, cols)
     u = W_up if isinstance(W_up, QMatrix) else QMatrix(up_type, W_up, exp_dim, cols)
     x = np.ascontiguousarray(x, dtype=np.float32)
     out = np.empty(exp_dim, np.float32)
-    check(lib().jx_matmul_swiglu_quant_f32(g.handle, u.handle, _p(x), _p(out)), "jx_matmul_swiglu_quant_f32")
+    check(lib().jx_matmul_swiglu_quant_f32(g.handle, u.handle, _p(x), _p(out), 1 if use_gelu else 0),
+          "jx_matmul_swiglu_quant_f32")
     return out
 
 

@@ -145,6 +145,7 @@ class LayerConfig:
     d_ff_shared: int = 0
     shared_gate: bool = False
     zipf_gamma: float = 0.0
+    act: int = 0  # gated activation: 0 SiLU, 1 GELU-tanh (the reference's use_gelu)
     decode_tokens: tuple = field(default_factory=tuple)
     describe: str = ""
 
@@ -156,6 +157,9 @@ class LayerConfig:
 CONFIGS = {
     "toy": LayerConfig("toy", 512, 8, 2, 1024, F.Q4_0, decode_tokens=(1,),
                        describe="Toy MoE FFN d512 E8 top-2 F1024 Q4_0"),
+    # the toy layer with the gemma family's GELU-tanh gate (the reference's use_gelu)
+    "toy_gelu": LayerConfig("toy_gelu", 512, 8, 2, 1024, F.Q4_0, act=1, decode_tokens=(1, 64),
+                            describe="Toy MoE FFN d512 E8 top-2 F1024 Q4_0, GELU-tanh gate"),
     "qwen15moe": LayerConfig("qwen15moe", 2048, 60, 4, 1408, F.Q4_0, d_ff_shared=5632,
                              shared_gate=True, decode_tokens=(1, 64),
                              describe="Qwen1.5-MoE-A2.7B-shaped d2048 E60 top-4 F1408 Q4_0 + shared 5632 (sigmoid gate)"),

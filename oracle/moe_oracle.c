@@ -453,9 +453,13 @@ void jxo_matmul_quant_f32(int32_t type, const uint8_t* W, const float* x, float*
 }
 
 /* matmul_swiglu_quant_f32 (src/quant.cpp:3970-4009): Q8_0 activations iff
- * exp_dim >= 8 and cols % 32 == 0; out = (g / (1 + exp(-g))) * u. */
+ * exp_dim >= 8 and cols % 32 == 0; out = (g / (1 + exp(-g))) * u, or with
+ * use_gelu (3999-4003) GELU-tanh(g) * u: inner = sqrt(2/pi) * (g + 0.044715 g^3),
+ * whose inner sum the reference build contracts to one fma (GCC's default
+ * -ffp-contract=fast with -mfma), then 0.5 g (1 + tanh(inner)) * u. */
 void jxo_matmul_swiglu_quant_f32(int32_t gate_type, const uint8_t* Wg, int32_t up_type, const uint8_t* Wu,
-                                 const float* x, float* out, int64_t exp_dim, int64_t cols, int32_t order) {
+                                 const float* x, float* out, int64_t exp_dim, int64_t cols, int32_t use_gelu,
+                                 int32_t order) {
     const int64_t gb = jxo_row_bytes(gate_type, cols), ub = jxo_row_bytes(up_type, cols);
     uint8_t* xq = NULL;
     if (exp_dim >= 8 && cols % 32 == 0) {
@@ -467,7 +471,12 @@ void jxo_matmul_swiglu_quant_f32(int32_t gate_type, const uint8_t* Wg, int32_t u
     for (int64_t r = 0; r < exp_dim; ++r) {
         const float g = row_dot(gate_type, Wg + r * gb, x, xq, cols, order);
         const float u = row_dot(up_type, Wu + r * ub, x, xq, cols, order);
-        out[r] = (g / (1.0f + expf(-g))) * u;
+        if (use_gelu) {
+            const float inner = 0.7978845608028654f * fmaf(0.044715f * g * g, g, g);
+            out[r] = 0.5f * g * (1.0f + tanhf(inner)) * u;
+        } else {
+            out[r] = (g / (1.0f + expf(-g))) * u;
+        }
     }
     free(xq);
 }
@@ -543,13 +552,14 @@ static void moe_token(const jxo_moe_desc* L, const float* x, float* out, int32_t
     for (int32_t s = 0; s < k; ++s) {
         const int64_t e = ids[s];
         jxo_matmul_swiglu_quant_f32(L->gate_type, L->gate + e * gsl, L->up_type, L->up + e * usl,
-                                    x, h, Fd, d, order);
+                                    x, h, Fd, d, L->activation, order);
         jxo_matmul_quant_f32(L->down_type, L->down + e * dsl, h, y, d, Fd, order);
         for (int32_t i = 0; i < d; ++i) out[i] = fmaf(probs[s], y[i], out[i]);
     }
     if (L->d_ff_shared > 0 && L->sh_gate && L->sh_up && L->sh_down) {
         const int32_t Fs = L->d_ff_shared;
-        jxo_matmul_swiglu_quant_f32(L->sh_gate_type, L->sh_gate, L->sh_up_type, L->sh_up, x, h, Fs, d, order);
+        jxo_matmul_swiglu_quant_f32(L->sh_gate_type, L->sh_gate, L->sh_up_type, L->sh_up, x, h, Fs, d,
+                                    L->activation, order);
         jxo_matmul_quant_f32(L->sh_down_type, L->sh_down, h, y, d, Fs, order);
         float sh = 1.0f;
         if (L->sh_gate_inp) {

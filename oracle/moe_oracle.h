@@ -38,6 +38,7 @@ typedef struct {
     const uint8_t* sh_up;
     const uint8_t* sh_down;
     const float* sh_gate_inp;  /* [d] fp32 sigmoid gate, or NULL             */
+    int32_t activation;        /* 0 SiLU, 1 GELU-tanh (the reference's use_gelu) */
 } jxo_moe_desc;
 
 uint16_t jxo_fp32_to_fp16(float f);
@@ -51,7 +52,8 @@ float jxo_vec_dot_q4_K_f32(const uint8_t* w, const float* y, int64_t k);
 void jxo_matmul_quant_f32(int32_t type, const uint8_t* W, const float* x, float* out,
                           int64_t rows, int64_t cols, int32_t order);
 void jxo_matmul_swiglu_quant_f32(int32_t gate_type, const uint8_t* Wg, int32_t up_type, const uint8_t* Wu,
-                                 const float* x, float* out, int64_t exp_dim, int64_t cols, int32_t order);
+                                 const float* x, float* out, int64_t exp_dim, int64_t cols, int32_t use_gelu,
+                                 int32_t order);
 int32_t jxo_select_experts(const float* logits, int32_t n_experts, int32_t top_k,
                            int32_t* ids, float* probs);
 /* One MoE block over the tokens listed in token_idx (all n_tok when NULL). */

@@ -33,6 +33,7 @@ class MoeDesc(C.Structure):
         ("sh_gate_type", C.c_int32), ("sh_up_type", C.c_int32), ("sh_down_type", C.c_int32),
         ("sh_gate", _u8), ("sh_up", _u8), ("sh_down", _u8),
         ("sh_gate_inp", _fp),
+        ("activation", C.c_int32),
     ]
 
 
@@ -83,7 +84,7 @@ class Oracle:
             L.jxo_vec_dot_q8.argtypes = [C.c_int32, _u8, _u8, C.c_int64, C.c_int32]
             L.jxo_matmul_quant_f32.argtypes = [C.c_int32, _u8, _fp, _fp, C.c_int64, C.c_int64, C.c_int32]
             L.jxo_matmul_swiglu_quant_f32.argtypes = [C.c_int32, _u8, C.c_int32, _u8, _fp, _fp,
-                                                     C.c_int64, C.c_int64, C.c_int32]
+                                                     C.c_int64, C.c_int64, C.c_int32, C.c_int32]
             L.jxo_moe_forward.argtypes = [C.POINTER(MoeDesc), _fp, C.c_int32, _i32, C.c_int32,
                                           _fp, _i32, _fp, _fp, C.c_int32]
             L.jxo_route.argtypes = [C.POINTER(MoeDesc), _fp, C.c_int32, _fp, _i32, _fp]
@@ -92,7 +93,7 @@ class Oracle:
             L.jxr_vec_dot_q8.argtypes = [C.c_int32, _u8, _u8, C.c_int64]
             L.jxr_matmul_quant_f32.argtypes = [C.c_int32, _u8, _fp, _fp, C.c_int64, C.c_int64]
             L.jxr_matmul_swiglu_quant_f32.argtypes = [C.c_int32, _u8, C.c_int32, _u8, _fp, _fp,
-                                                     C.c_int64, C.c_int64]
+                                                     C.c_int64, C.c_int64, C.c_int32]
             L.jxr_moe_forward.argtypes = [C.POINTER(MoeDesc), _fp, C.c_int32, _i32, C.c_int32,
                                           _fp, _i32, _fp, _fp]
 
@@ -142,17 +143,18 @@ class Oracle:
             self.lib.jxr_matmul_quant_f32(qtype, _ptr(W, _u8), _ptr(x, _fp), _ptr(out, _fp), rows, cols)
         return out
 
-    def matmul_swiglu_quant_f32(self, gt: int, Wg, ut: int, Wu, x, exp_dim: int, cols: int) -> np.ndarray:
+    def matmul_swiglu_quant_f32(self, gt: int, Wg, ut: int, Wu, x, exp_dim: int, cols: int,
+                                use_gelu: bool = False) -> np.ndarray:
         Wg = np.ascontiguousarray(Wg, dtype=np.uint8)
         Wu = np.ascontiguousarray(Wu, dtype=np.uint8)
         x = np.ascontiguousarray(x, dtype=np.float32)
         out = np.zeros(exp_dim, dtype=np.float32)
         if self.kind == "port":
             self.lib.jxo_matmul_swiglu_quant_f32(gt, _ptr(Wg, _u8), ut, _ptr(Wu, _u8), _ptr(x, _fp),
-                                                 _ptr(out, _fp), exp_dim, cols, self.order)
+                                                 _ptr(out, _fp), exp_dim, cols, int(use_gelu), self.order)
         else:
             self.lib.jxr_matmul_swiglu_quant_f32(gt, _ptr(Wg, _u8), ut, _ptr(Wu, _u8), _ptr(x, _fp),
-                                                 _ptr(out, _fp), exp_dim, cols)
+                                                 _ptr(out, _fp), exp_dim, cols, int(use_gelu))
         return out
 
     def select_experts(self, logits, k: int):
@@ -183,7 +185,7 @@ class Oracle:
                     P(lw.gate, _u8), P(lw.up, _u8), P(lw.down, _u8),
                     cfg.d_ff_shared, gt, ut, dt,
                     P(lw.sh_gate, _u8), P(lw.sh_up, _u8), P(lw.sh_down, _u8),
-                    P(lw.sh_gate_inp, _fp))
+                    P(lw.sh_gate_inp, _fp), cfg.act)
         return D, keep
 
     def moe_forward(self, lw, x: np.ndarray, token_idx=None, threads: int = 0):

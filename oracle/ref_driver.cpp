@@ -55,9 +55,9 @@ void jxr_matmul_quant_f32(int32_t type, const uint8_t* W, const float* x, float*
 }
 
 void jxr_matmul_swiglu_quant_f32(int32_t gt, const uint8_t* Wg, int32_t ut, const uint8_t* Wu,
-                                 const float* x, float* out, int64_t exp_dim, int64_t cols) {
+                                 const float* x, float* out, int64_t exp_dim, int64_t cols, int32_t use_gelu) {
     moe::matmul_swiglu_quant_f32(static_cast<GGMLType>(gt), Wg, static_cast<GGMLType>(ut), Wu,
-                                 x, out, exp_dim, cols, false);
+                                 x, out, exp_dim, cols, use_gelu != 0);
 }
 
 // select_experts_cache_aware with CACHE_ROUTE off (eps = 0, nothing resident).
@@ -111,7 +111,7 @@ int32_t jxr_moe_forward(const jxo_moe_desc* L, const float* x, int32_t n_tok,
             const auto& sel = selected[s];
             const size_t e = sel.expert_idx;
             moe::matmul_swiglu_quant_f32(gt, L->gate + e * gsl, ut, L->up + e * usl,
-                                         xn, gate_buf.data(), Fd, d, false);
+                                         xn, gate_buf.data(), Fd, d, L->activation != 0);
             moe::matmul_quant_f32(dt, L->down + e * dsl, gate_buf.data(), down_buf.data(), d, Fd);
             for (uint32_t j = 0; j < d; ++j) moe_accum[j] += sel.prob * down_buf[j];
             topk_ids[static_cast<size_t>(i) * k + s] = static_cast<int32_t>(sel.expert_idx);
@@ -122,7 +122,7 @@ int32_t jxr_moe_forward(const jxo_moe_desc* L, const float* x, int32_t n_tok,
             std::vector<float> sh_buf(sh_dim, 0.0f);
             moe::matmul_swiglu_quant_f32(static_cast<GGMLType>(L->sh_gate_type), L->sh_gate,
                                          static_cast<GGMLType>(L->sh_up_type), L->sh_up,
-                                         xn, sh_buf.data(), sh_dim, d, false);
+                                         xn, sh_buf.data(), sh_dim, d, L->activation != 0);
             moe::matmul_quant_f32(static_cast<GGMLType>(L->sh_down_type), L->sh_down,
                                   sh_buf.data(), down_buf.data(), d, sh_dim);
             float sh_scale = 1.0f;

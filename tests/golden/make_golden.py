@@ -30,17 +30,48 @@ from oracle.oracle import Oracle, build  # noqa: E402
 
 OUT = os.path.dirname(os.path.abspath(__file__))
 
-# (config, n tokens, tokens whose full output row is stored)
+# (config, n tokens, tokens whose full output row is stored, or the tile granularity the rows must cover:
+# ("tiles", routed pairs per tile, shared-expert tokens per tile) -- 32 where the library takes the
+# matrix-core GEMMs (their 32-pair MFMA tiles), 16 where it takes the 16-token matrix-core GEMV)
 CASES = [
     ("toy", 1, [0]),
     ("qwen15moe", 1, [0]),
-    ("qwen15moe", 64, [0, 17, 63]),
+    ("qwen15moe", 64, ("tiles", 16, 32)),
     ("mixtral", 1, [0]),
-    ("mixtral", 512, [0, 255, 511]),
-    ("mixtral", 2048, [0, 1000, 2047]),
-    ("qwen3moe", 2048, [0, 5, 1024, 2047]),
-    ("dsv2lite", 32, [0, 7, 19, 31]),
+    ("mixtral", 512, ("tiles", 32, 0)),
+    ("mixtral", 2048, ("tiles", 32, 0)),
+    ("qwen3moe", 2048, ("tiles", 32, 0)),
+    ("dsv2lite", 32, ("tiles", 16, 16)),
+    ("toy_gelu", 1, [0]),
+    ("toy_gelu", 64, ("tiles", 32, 0)),
 ]
+
+
+def covering_rows(ids: np.ndarray, n_experts: int, g_routed: int, g_shared: int) -> list[int]:
+    """Tokens whose output rows together touch every tile of the grouped kernels.
+
+    The dispatch is a stable counting sort, so expert e's pairs are its tokens in token order and the
+    j-th of them sits in tile j // g_routed of that expert; the shared expert's tile of token t is
+    t // g_shared.  Greedy set cover over those (expert, tile) units, seeded with the first and last
+    token: every tile, each expert's last partial one included, holds at least one checked row."""
+    n, k = ids.shape
+    seen = np.zeros(n_experts, np.int64)
+    units = [set() for _ in range(n)]
+    for t in range(n):
+        for s in range(k):
+            e = int(ids[t, s])
+            units[t].add((e, int(seen[e]) // g_routed))
+            seen[e] += 1
+        if g_shared:
+            units[t].add((-1, t // g_shared))
+    want = set().union(*units)
+    rows = sorted({0, n - 1})
+    covered = set().union(*(units[t] for t in rows))
+    while covered != want:
+        best = max(range(n), key=lambda t: (len(units[t] - covered), -t))
+        rows.append(best)
+        covered |= units[best]
+    return sorted(rows)
 
 
 def digest(*arrays) -> str:
@@ -56,12 +87,10 @@ def layer_digest(lw) -> str:
                   lw.sh_gate, lw.sh_up, lw.sh_down, lw.sh_gate_inp)
 
 
-def make_case(ref: Oracle, name: str, n: int, rows: list[int], tag: str = "") -> str:
+def make_case(ref: Oracle, name: str, n: int, rows, tag: str = "") -> str:
     cfg = synth.CONFIGS[name]
     lw = synth.make_layer(cfg)
     x = synth.make_tokens(cfg, n)
-    # full MoE-block outputs for `rows`, routing for every token (the router is cheap)
-    out, ids_r, w_r, lg_r = ref.moe_forward(lw, x, np.asarray(rows, dtype=np.int32))
     ids_all = np.zeros((n, cfg.top_k), np.int32)
     w_all = np.zeros((n, cfg.top_k), np.float32)
     lg_all = np.zeros((n, cfg.n_experts), np.float32)
@@ -72,6 +101,10 @@ def make_case(ref: Oracle, name: str, n: int, rows: list[int], tag: str = "") ->
             logits = (logits + lw.router_bias).astype(np.float32)
         i, p, _ = ref.select_experts(logits, cfg.top_k)
         ids_all[t], w_all[t], lg_all[t] = i, p, logits
+    if isinstance(rows, tuple):  # ("tiles", routed, shared): rows covering every tile of the dispatch
+        rows = covering_rows(ids_all, cfg.n_experts, rows[1], rows[2])
+    # full MoE-block outputs for `rows`
+    out, ids_r, w_r, lg_r = ref.moe_forward(lw, x, np.asarray(rows, dtype=np.int32))
     assert np.array_equal(ids_all[rows], ids_r) and np.array_equal(w_all[rows].view(np.uint32), w_r.view(np.uint32))
     counts = np.bincount(ids_all.reshape(-1), minlength=cfg.n_experts).astype(np.int32)
     path = os.path.join(OUT, f"{name}_n{n}{tag}.npz")

@@ -3,6 +3,7 @@ include/jxmoe.h; host-side argument checks work without a GPU."""
 import ctypes as C
 import os
 import re
+import subprocess
 
 import numpy as np
 import pytest
@@ -61,3 +62,23 @@ def test_python_mirror_fails_loudly_without_library(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(_lib.JxError, match="no CPU fallback"):
         _lib.lib()
+
+
+def build_caller(out_dir) -> str:
+    """g++ build of tests/abi_caller.cpp against include/jxmoe.h and libjxmoe.so."""
+    from jxai_amd import _lib
+    exe = os.path.join(str(out_dir), "abi_caller")
+    subprocess.run(["g++", "-std=c++17", "-O1", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
+                    os.path.join(ROOT, "tests", "abi_caller.cpp"), "-o", exe, _lib.LIB_PATH,
+                    "-Wl,-rpath," + os.path.dirname(_lib.LIB_PATH)], check=True)
+    return exe
+
+
+def test_compiled_caller_without_device(jxlib, tmp_path):
+    """A C++ program that sees only include/jxmoe.h compiles, links and gets JX_ERR_NODEVICE here."""
+    if os.path.exists("/dev/kfd"):
+        pytest.skip("a GPU is present; the no-device path is not reachable")
+    exe = build_caller(tmp_path)
+    r = subprocess.run([exe, "nodevice"], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "-> 5" in r.stdout

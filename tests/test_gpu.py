@@ -35,10 +35,20 @@ def moe():
 
 _LAYERS = {}
 
+# small layers for cases the configured shapes do not reach
+EXTRA = {
+    # a Q4_K layer with the GELU-tanh gate, shared expert with a sigmoid gate
+    "gelu_q4k": synth.LayerConfig("gelu_q4k", 512, 8, 2, 768, F.Q4_K, d_ff_shared=512, shared_gate=True, act=1),
+    # every token on both experts: pair j of each expert is token j, so a token's position picks its
+    # MFMA pair tile (j % 64 // 32) and its part of the 128-pair dispatch tile (j % 128 // 64)
+    "e2_mixtral": synth.LayerConfig("e2_mixtral", 4096, 2, 2, 2048, F.Q4_K),
+    "e2_dsv2lite": synth.LayerConfig("e2_dsv2lite", 2048, 2, 2, 1408, F.Q4_K),
+}
+
 
 def layer(name):
     if name not in _LAYERS:
-        cfg = synth.CONFIGS[name]
+        cfg = synth.CONFIGS[name] if name in synth.CONFIGS else EXTRA[name]
         _LAYERS.clear()
         _LAYERS[name] = (cfg, synth.make_layer(cfg))
     return _LAYERS[name]
@@ -71,20 +81,21 @@ def test_matmul_quant_f32(moe, port, qt, rows, cols):
     assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
 
 
+@pytest.mark.parametrize("use_gelu", [False, True])
 @pytest.mark.parametrize("qt,rows,cols", [(F.Q4_0, 1408, 2048), (F.Q4_K, 1024, 4096), (F.Q8_0, 768, 2048)])
-def test_matmul_swiglu_quant_f32(moe, port, qt, rows, cols):
-    say(f"matmul_swiglu_quant_f32 type={qt} {rows}x{cols}")
+def test_matmul_swiglu_quant_f32(moe, port, qt, rows, cols, use_gelu):
+    say(f"matmul_swiglu_quant_f32 type={qt} {rows}x{cols} gelu={use_gelu}")
     Wg = synth.quant_matrix(synth.sub_seed("gpu", f"g{qt}"), qt, rows, cols)
     Wu = synth.quant_matrix(synth.sub_seed("gpu", f"u{qt}"), qt, rows, cols)
     x = synth.normal_f32(synth.sub_seed("gpu", f"sx{cols}"), cols, 1.0)
-    got = moe.matmul_swiglu_quant_f32(qt, Wg, qt, Wu, x, rows, cols)
-    want = port.matmul_swiglu_quant_f32(qt, Wg, qt, Wu, x, rows, cols)
+    got = moe.matmul_swiglu_quant_f32(qt, Wg, qt, Wu, x, rows, cols, use_gelu=use_gelu)
+    want = port.matmul_swiglu_quant_f32(qt, Wg, qt, Wu, x, rows, cols, use_gelu=use_gelu)
     assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max()
 
 
 # ------------------------------------------------------------------ layer vs the golden vectors
 GOLDEN_CASES = ["toy_n1", "qwen15moe_n1", "qwen15moe_n64", "mixtral_n1", "mixtral_n512", "mixtral_n2048",
-                "qwen3moe_n2048", "dsv2lite_n32"]
+                "qwen3moe_n2048", "dsv2lite_n32", "toy_gelu_n1", "toy_gelu_n64"]
 
 
 @pytest.mark.parametrize("case", GOLDEN_CASES)
@@ -101,7 +112,7 @@ def test_layer_vs_golden(moe, case):
     assert np.array_equal(counts, z["counts"])
     np.testing.assert_allclose(w, z["topk_w"], rtol=2e-6, atol=0)
     err = rel_err(out[z["rows"]], z["out"])
-    say(f"layer {case}: max rel err {err:.2e}")
+    say(f"layer {case}: max rel err {err:.2e} over {len(z['rows'])} rows")
     assert err <= REL_TOL
     lg = L.last_logits(n)
     assert np.array_equal(lg[z["rows"]].view(np.uint32), z["logits_rows"].view(np.uint32)), "router logits not bit-exact"
@@ -128,7 +139,11 @@ def test_layer_vs_golden(moe, case):
                                            # few tokens on the matrix-core path: top-k in its own launch
                                            ("qwen3moe", 1, "mfma"), ("qwen15moe", 2, "mfma"),
                                            # register-resident router rows with fewer tokens per block
-                                           ("qwen3moe", 600, None), ("qwen15moe", 700, None)])
+                                           ("qwen3moe", 600, None), ("qwen15moe", 700, None),
+                                           # GELU-tanh gate in every gate/up epilogue
+                                           ("toy_gelu", 1, None), ("toy_gelu", 40, "gemv"), ("toy_gelu", 300, "mfma"),
+                                           ("toy_gelu", 24, None), ("gelu_q4k", 1, None), ("gelu_q4k", 2, "gemv"),
+                                           ("gelu_q4k", 20, "gemv"), ("gelu_q4k", 200, "mfma")])
 def test_layer_regimes_vs_oracle(moe, port, name, n, regime):
     say(f"{name} n={n} regime={regime}")
     cfg, lw = layer(name)
@@ -323,3 +338,171 @@ def test_graph_replays_match_eager(moe, monkeypatch):
             eager.forward(synth.make_tokens(cfg, 3, seed=rep))  # eager work between replays
     eager.close()
     graphed.close()
+
+
+@pytest.mark.parametrize("name", ["e2_mixtral", "e2_dsv2lite"])
+def test_q4k_gateup_block_scales_every_tile_position(moe, port, name):
+    """The extreme 32-block scales of the test above placed in every pair-tile position of the Q4_K
+    gate/up GEMM: with two experts and top-2, token j is pair j of both experts, so tokens 0-7 sit
+    in pair tile 0 of the first 64-pair part, 40-47 in pair tile 1 (its rescales follow a different
+    schedule), 70-77 and 100-107 in pair tiles 0 and 1 of the second part, 130-137 and 230-237 in
+    the next 128-pair dispatch tile."""
+    cfg, lw = layer(name)
+    n = 256
+    x = synth.make_tokens(cfg, n, seed=23).copy()
+    d = x.shape[1]
+    blocks = x.reshape(n, d // 32, 32)
+    starts = [0, 40, 70, 100, 130, 230]
+    for t0 in starts:
+        x[t0 + 0, :96] = 0.0
+        x[t0 + 1, 256:512] = 0.0
+        x[t0 + 2, :] = 0.0
+        x[t0 + 2, 1000:1010] = 3.0
+        blocks[t0 + 3, 1] *= 2.0 ** 4
+        blocks[t0 + 4, ::2] *= 2.0 ** -12
+        blocks[t0 + 5, 1::3] *= 2.0 ** -30  # fp16 scale 0, quants nonzero
+        x[t0 + 6, :] = 0.0
+        x[t0 + 7, : d // 2] = 0.0
+    say(f"{name} n={n} extreme block scales at {starts}")
+    L = moe.MoELayer.from_weights(lw)
+    out, ids, w, counts = L.forward(x, regime="mfma")
+    assert np.array_equal(counts, [n, n])
+    sel = np.array([t0 + i for t0 in starts for i in (0, 1, 2, 3, 4, 5, 7)] + [20, 60, 90, 120, 200, 255], np.int32)
+    want = port.moe_forward(lw, x, sel)[0]
+    err = rel_err(out[sel], want)
+    say(f"{name}: max rel err {err:.2e}")
+    assert err <= REL_TOL
+    for t0 in starts:
+        assert not np.any(out[t0 + 6]), "an all-zero token gives a zero output"
+    L.close()
+
+
+# (config, tokens, regime) -> the router kernel that writes x's Q8_0 blocks
+ROUTER_VARIANTS = [
+    ("mixtral", 1, None),        # decode: logits one block per router row, quantization in waves 1..
+    ("mixtral", 1, "mfma"),      # one-block router + top-k + dispatch (k_route_one)
+    ("qwen3moe", 2, "mfma"),     # split few-token router + one-wave top-k (k_route_small, k_topk_small)
+    ("mixtral", 100, None),      # many tokens, <= 16 router rows: one token per block (k_route<1>)
+    ("mixtral", 300, None),      # two tokens per block (k_route<2>)
+    ("qwen15moe", 40, None),     # router rows split over blocks, one token per block
+    ("qwen3moe", 300, None),     # split rows, four tokens per block (k_route<4>)
+    ("qwen3moe", 600, None),     # quantization ahead of the register-resident router rows
+    ("toy", 70, None),
+]
+
+
+@pytest.mark.parametrize("name,n,regime", ROUTER_VARIANTS)
+def test_router_q8_bitexact(moe, port, name, n, regime):
+    """The Q8_0 of x that each router kernel writes on its way (the activation the expert dots
+    consume) equals quantize_row_q8_0 (src/quant.cpp:1029-1045) bit for bit, token by token."""
+    cfg, lw = layer(name)
+    x = synth.make_tokens(cfg, n, seed=31).copy()
+    x[0, :64] = 0.0                                   # zero blocks: d = 0, id = 0
+    if n > 1:
+        x[1, :32] = np.arange(32, dtype=np.float32) - 15.5  # exact .5 ties
+        x[-1] *= np.float32(1e-6)                     # small scales (fp16 subnormal range)
+    say(f"router q8 {name} n={n} regime={regime}")
+    L = moe.MoELayer.from_weights(lw)
+    L.forward(x, regime=regime)
+    got = L.last_xq8(n)
+    for t in range(n):
+        assert np.array_equal(got[t], port.quantize_row_q8_0(x[t])), f"token {t}"
+    L.close()
+
+
+@pytest.mark.parametrize("name,ns", [("mixtral", (1, 2048)), ("dsv2lite", (1, 32, 300)), ("qwen3moe", (2, 2048)),
+                                     ("qwen15moe", (1, 64))])
+def test_device_async_path_matches_host(moe, name, ns):
+    """The path the benchmark times (device pointers, asynchronous, replayed graphs for small batches)
+    gives the host-pointer path's outputs bit for bit, over several replays."""
+    cfg, lw = layer(name)
+    L = moe.MoELayer.from_weights(lw)
+    for n in ns:
+        say(f"{name} n={n}: device async vs host")
+        x = synth.make_tokens(cfg, n)
+        want = L.forward(x)[0]
+        xb = moe.DeviceBuffer(x.nbytes).upload(x)
+        ob = moe.DeviceBuffer(x.nbytes)
+        for rep in range(3):
+            L.forward_device(xb, n, ob, sync=False)
+            moe.lib().jx_device_synchronize()
+            got = ob.download(np.empty_like(x))
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"replay {rep}"
+        xb.free()
+        ob.free()
+    L.close()
+
+
+def test_pair_offsets_beyond_4gib(moe, port):
+    """80000 (token, expert) pairs of 14336-element hidden rows: the down GEMM's activation rows span
+    4.6 GB, past 32-bit byte offsets; the last tokens' outputs match the oracle."""
+    cfg = synth.LayerConfig("wide_f", 256, 2, 2, 14336, F.Q4_0)
+    lw = synth.make_layer(cfg, seed=5)
+    n = 40000
+    x = synth.make_tokens(cfg, n, seed=5)
+    say(f"wide_f n={n} (4.6 GB of down activations)")
+    L = moe.MoELayer.from_weights(lw)
+    out, ids, w, counts = L.forward(x, regime="mfma")
+    assert np.array_equal(counts, [n, n])
+    sel = np.array([0, 1, 20000, 37500, 37501, 39990, 39998, 39999], np.int32)
+    want = port.moe_forward(lw, x, sel)[0]
+    err = rel_err(out[sel], want)
+    say(f"wide_f: max rel err {err:.2e}")
+    assert err <= REL_TOL
+    L.close()
+
+
+def test_batch_limit_refused(moe):
+    """A batch whose activation rows would pass 32-bit offsets is refused before any work."""
+    cfg, lw = layer("toy")
+    L = moe.MoELayer.from_weights(lw)
+    x = np.zeros((1, cfg.d_model), np.float32)
+    out = np.zeros_like(x)
+    n = (1 << 32) // (cfg.d_model * 4)
+    rc = moe.lib().jx_moe_forward(L.handle, x.ctypes.data, n, out.ctypes.data, None, None, None, None, 0)
+    assert rc == 2 and b"split the batch" in moe.lib().jx_moe_last_error()
+    L.close()
+
+
+def test_layer_desc_refusals(moe):
+    """Router types other than F32 and unknown activations are refused with a message."""
+    cfg, lw = layer("toy")
+    from jxai_amd._lib import JxError
+    with pytest.raises(JxError, match="router must be F32"):
+        moe.MoELayer(n_experts=8, top_k=2, d_model=512, d_ff=1024, gate_type=F.Q4_0, up_type=F.Q4_0,
+                     down_type=F.Q4_0, router=lw.router.astype(np.float16), gate_exps=lw.gate, up_exps=lw.up,
+                     down_exps=lw.down, router_type=F.F16)
+    with pytest.raises(JxError, match="activation"):
+        moe.MoELayer(n_experts=8, top_k=2, d_model=512, d_ff=1024, gate_type=F.Q4_0, up_type=F.Q4_0,
+                     down_type=F.Q4_0, router=lw.router, gate_exps=lw.gate, up_exps=lw.up, down_exps=lw.down,
+                     activation=7)
+
+
+def test_compiled_caller(moe, port, tmp_path):
+    """The C++ caller of include/jxmoe.h (tests/abi_caller.cpp) runs one token and a 64-token batch;
+    the Python binding on the same bytes gives the same results bit for bit, and the oracle the same
+    routing and outputs within the bar."""
+    from tests.test_abi import build_caller
+    import subprocess
+    exe = build_caller(tmp_path)
+    say("compiled caller: run")
+    r = subprocess.run([exe, "run", str(tmp_path)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    ld = lambda name, dt: np.fromfile(os.path.join(str(tmp_path), name), dtype=dt)  # noqa: E731
+    cfg = synth.LayerConfig("caller", 512, 8, 2, 1024, F.Q4_0)
+    lw = synth.LayerWeights(cfg, ld("router.bin", np.float32).reshape(8, 512), None, ld("gate.bin", np.uint8),
+                            ld("up.bin", np.uint8), ld("down.bin", np.uint8))
+    x = ld("x.bin", np.float32).reshape(64, 512)
+    L = moe.MoELayer.from_weights(lw)
+    o1, i1, _, _ = L.forward(x[:1])
+    assert np.array_equal(o1[0].view(np.uint32), ld("out1.bin", np.float32).view(np.uint32))
+    assert np.array_equal(i1[0], ld("ids1.bin", np.int32))
+    assert np.array_equal((x[0] + o1[0]).view(np.uint32), ld("resid1.bin", np.float32).view(np.uint32))
+    o, ids, _, counts = L.forward(x)
+    assert np.array_equal(o.view(np.uint32), ld("out.bin", np.float32).view(np.uint32).reshape(64, 512))
+    assert np.array_equal(ids, ld("ids.bin", np.int32).reshape(64, 2))
+    assert np.array_equal(counts, ld("counts.bin", np.int32))
+    want, ids_o, _, _ = port.moe_forward(lw, x)
+    assert np.array_equal(ids, ids_o)
+    assert rel_err(o, want) <= REL_TOL
+    L.close()

@@ -169,6 +169,53 @@ def test_swiglu_golden(port):
     np.testing.assert_allclose(got, g / (1 + np.exp(-g)) * u, rtol=1e-5, atol=1e-6)
 
 
+def _gelu64(g):
+    return 0.5 * g * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (g + 0.044715 * g ** 3)))
+
+
+@pytest.mark.parametrize("qt,rows,cols", [(F.Q4_0, 256, 512), (F.Q4_K, 128, 1024), (F.Q8_0, 128, 2048)])
+def test_gelu_gate_float64(port, qt, rows, cols):
+    """use_gelu (src/quant.cpp:3999-4003): GELU-tanh of the gate times up, against a float64 closed form."""
+    Wg = synth.quant_matrix(synth.sub_seed("gelu", f"g{qt}"), qt, rows, cols)
+    Wu = synth.quant_matrix(synth.sub_seed("gelu", f"u{qt}"), qt, rows, cols)
+    x = synth.normal_f32(synth.sub_seed("gelu", f"x{qt}"), cols, 3.0)
+    got = port.matmul_swiglu_quant_f32(qt, Wg, qt, Wu, x, rows, cols, use_gelu=True)
+    xa = deq_q8_blocks(port.quantize_row_q8_0(x))
+    g, u = deq_matrix(qt, Wg, rows, cols) @ xa, deq_matrix(qt, Wu, rows, cols) @ xa
+    want = _gelu64(g) * u
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+    assert not np.array_equal(got, port.matmul_swiglu_quant_f32(qt, Wg, qt, Wu, x, rows, cols))
+
+
+@pytest.mark.parametrize("qt,rows,cols", [(F.Q4_0, 256, 512), (F.Q4_K, 128, 1024), (F.Q8_0, 128, 2048)])
+def test_gelu_gate_live_vs_reference(port, ref, qt, rows, cols):
+    """Bit-exact against the reference build, gates spread over |g| up to ~100 (the fma the build
+    contracts the cubic's sum into changes the bits of ~16% of such sums)."""
+    Wg = synth.quant_matrix(synth.sub_seed("gelu", f"g{qt}"), qt, rows, cols)
+    Wu = synth.quant_matrix(synth.sub_seed("gelu", f"u{qt}"), qt, rows, cols)
+    for scale in (0.3, 3.0, 30.0):
+        x = synth.normal_f32(synth.sub_seed("gelu", f"x{qt}_{scale}"), cols, scale)
+        a = port.matmul_swiglu_quant_f32(qt, Wg, qt, Wu, x, rows, cols, use_gelu=True)
+        b = ref.matmul_swiglu_quant_f32(qt, Wg, qt, Wu, x, rows, cols, use_gelu=True)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("qt,cols", [(F.Q4_0, 512), (F.Q8_0, 512), (F.Q4_K, 1024)])
+def test_dequantize_row(port, qt, cols):
+    """dequantize_row_q4_0 / _q8_0 / _q4_K (src/quant.cpp:1014-1057, 1209-1249) against the formats'
+    closed form, and against the reference build when it is present."""
+    w = synth.quant_matrix(synth.sub_seed("deq", f"{qt}"), qt, 1, cols)
+    got = port.dequantize_row(qt, w, cols)
+    exact = deq_matrix(qt, w, 1, cols)[0]
+    # Q4_0 / Q8_0 values are exact in fp32; Q4_K's d * sc * q - dmin * m rounds in fp32
+    tol = 0.0 if qt != F.Q4_K else 2.0 ** -22 * np.abs(exact).max()
+    assert np.abs(got.astype(np.float64) - exact).max() <= tol
+    from oracle import oracle as O
+    if O.available("reference"):
+        want = O.Oracle("reference").dequantize_row(qt, w, cols)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 # --------------------------------------------------------------- top-k + softmax
 @pytest.mark.parametrize("E,k", [(8, 2), (60, 4), (128, 8), (64, 6), (5, 5)])
 def test_select_experts_bruteforce(port, E, k):
@@ -195,7 +242,7 @@ def test_select_experts_live_vs_reference(port, ref):
 
 # --------------------------------------------------------------- whole MoE block vs the golden vectors
 GOLDEN_CASES = ["toy_n1", "qwen15moe_n1", "qwen15moe_n64", "mixtral_n1", "mixtral_n512",
-                "mixtral_n2048", "qwen3moe_n2048", "dsv2lite_n32"]
+                "mixtral_n2048", "qwen3moe_n2048", "dsv2lite_n32", "toy_gelu_n1", "toy_gelu_n64"]
 
 
 def _layer(name, n):
@@ -235,9 +282,12 @@ def test_moe_block_golden_avx512_order(case):
 
 def test_moe_block_live_vs_reference(port, ref):
     """Bit-exact against the reference build on fresh seeds (small shapes of every format)."""
-    for qt, E, k, d, Fd, Fs, gate in [(F.Q4_0, 8, 2, 512, 1024, 0, False), (F.Q8_0, 16, 4, 256, 320, 0, False),
-                                      (F.Q4_K, 8, 3, 512, 768, 512, True), (F.Q4_K, 6, 2, 256, 1408, 1408, False)]:
-        cfg = synth.LayerConfig(f"live{qt}_{Fd}", d, E, k, Fd, qt, d_ff_shared=Fs, shared_gate=gate)
+    for qt, E, k, d, Fd, Fs, gate, act in [(F.Q4_0, 8, 2, 512, 1024, 0, False, 0),
+                                           (F.Q8_0, 16, 4, 256, 320, 0, False, 0),
+                                           (F.Q4_K, 8, 3, 512, 768, 512, True, 0),
+                                           (F.Q4_K, 6, 2, 256, 1408, 1408, False, 0),
+                                           (F.Q4_K, 8, 2, 512, 768, 512, True, 1)]:
+        cfg = synth.LayerConfig(f"live{qt}_{Fd}_{act}", d, E, k, Fd, qt, d_ff_shared=Fs, shared_gate=gate, act=act)
         lw = synth.make_layer(cfg, seed=99)
         x = synth.make_tokens(cfg, 6, seed=99)
         a = port.moe_forward(lw, x)
@@ -260,14 +310,14 @@ def _block_float64(port, lw, x, ids, probs):
         for s in range(cfg.top_k):
             e = ids[i, s]
             g, u = G[e] @ xa, U[e] @ xa
-            h = (g / (1 + np.exp(-g)) * u).astype(np.float32)
+            h = ((_gelu64(g) if cfg.act else g / (1 + np.exp(-g))) * u).astype(np.float32)
             ha = deq_q8_blocks(port.quantize_row_q8_0(h)) if F.supports_q8_activation(t, Fd) else h.astype(np.float64)
             out[i] += probs[i, s] * (D[e] @ ha)
         if cfg.has_shared:
             Fs = cfg.d_ff_shared
             g = deq_matrix(t, lw.sh_gate, Fs, d) @ xa
             u = deq_matrix(t, lw.sh_up, Fs, d) @ xa
-            h = (g / (1 + np.exp(-g)) * u).astype(np.float32)
+            h = ((_gelu64(g) if cfg.act else g / (1 + np.exp(-g))) * u).astype(np.float32)
             ha = deq_q8_blocks(port.quantize_row_q8_0(h)) if F.supports_q8_activation(t, Fs) else h.astype(np.float64)
             sh = 1.0
             if lw.sh_gate_inp is not None:
@@ -276,7 +326,7 @@ def _block_float64(port, lw, x, ids, probs):
     return out
 
 
-@pytest.mark.parametrize("name,n", [("toy", 3), ("dsv2lite", 2), ("qwen15moe", 2)])
+@pytest.mark.parametrize("name,n", [("toy", 3), ("dsv2lite", 2), ("qwen15moe", 2), ("toy_gelu", 3)])
 def test_moe_block_float64_restatement(port, name, n):
     cfg, lw, x = _layer(name, 64 if name == "qwen15moe" else n)
     x = x[:n]
