@@ -135,6 +135,20 @@ void jx_qmatrix_destroy(jx_qmatrix* m);
  * (rows >= 8 and supports_q8_activation), fp32 otherwise.  Host pointers. */
 int jx_matmul_quant_f32(jx_qmatrix* W, const float* x, float* out);
 
+/* jx_matmul_quant_f32 on device pointers that allocates nothing.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  x_dev [cols] and out_dev [rows] are device fp32; the
+ * work is enqueued on `stream` (hipStream_t, NULL = default stream) and the
+ * call returns without synchronizing.  The activation scratch (Q8_0 form or
+ * zero-padded fp32 copy) is one static device buffer per GPU holding at most
+ * JX_NOALLOC_MAX_COLS columns (cols rounded up to 256); wider matrices are
+ * refused with JX_ERR_UNSUPPORTED.  Every call on a GPU shares that buffer:
+ * calls that overlap on one GPU (other streams, other threads) race on it.
+ * Needs jx_moe_init on the matrix's device. */
+#define JX_NOALLOC_MAX_COLS 65536
+int jx_matmul_quant_f32_noalloc(jx_qmatrix* W, const float* x_dev, float* out_dev, void* stream);
+
 /* out[r] = act(Wg[r] . x) * (Wu[r] . x), act = SiLU or (use_gelu) GELU-tanh
  * (matmul_swiglu_quant_f32, include/quant.h:354-362; src/quant.cpp:3970-4009).
  * Host pointers. */

@@ -26,7 +26,7 @@ EXPORTS = [
     "jx_moe_init", "jx_moe_layer_create", "jx_moe_layer_destroy", "jx_moe_forward", "jx_moe_last_logits",
     "jx_moe_last_xq8",
     "jx_moe_profile", "jx_moe_profile_read", "jx_qmatrix_create", "jx_qmatrix_destroy", "jx_matmul_quant_f32",
-    "jx_matmul_swiglu_quant_f32", "jx_quantize_row_q8_0", "jx_dev_alloc", "jx_dev_free", "jx_memcpy_htod",
+    "jx_matmul_swiglu_quant_f32", "jx_quantize_row_q8_0", "jx_matmul_quant_f32_noalloc", "jx_dev_alloc", "jx_dev_free", "jx_memcpy_htod",
     "jx_memcpy_dtoh", "jx_device_synchronize", "jx_moe_last_error",
 ]
 
@@ -80,6 +80,7 @@ def lib() -> C.CDLL:
     L.jx_qmatrix_destroy.argtypes = [_vp]
     L.jx_qmatrix_destroy.restype = None
     L.jx_matmul_quant_f32.argtypes = [_vp, _vp, _vp]
+    L.jx_matmul_quant_f32_noalloc.argtypes = [_vp, _vp, _vp, _vp]
     L.jx_matmul_swiglu_quant_f32.argtypes = [_vp, _vp, _vp, _vp, C.c_int32]
     L.jx_quantize_row_q8_0.argtypes = [_vp, _vp, C.c_int64]
     L.jx_dev_alloc.argtypes = [C.c_size_t, C.POINTER(_vp)]

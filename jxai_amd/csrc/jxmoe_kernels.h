@@ -195,6 +195,8 @@ void launch_route_small(const RouteArgs& a, const DispatchOut& o, hipStream_t st
 
 // Q8_0 of rows x K fp32 (row-major, K % 32 == 0).
 void launch_quantize_q8(const float* x, int rows, int K, ActQ8 out, hipStream_t st);
+// dst[0 .. kpad) = x[0 .. n) then zeros.
+void launch_copy_pad(const float* x, int n, int kpad, float* dst, hipStream_t st);
 
 // Matrix-core form of existing Q8_0 activations (int8 quants + (scale, sum)).
 // lo = false writes only the fp16 hi halves (the down GEMM's operand).

@@ -1105,6 +1105,17 @@ __global__ void __launch_bounds__(256) k_quant_q8(const float* x, int rows, int 
     quant_block(ok ? x[blk * 32 + l32] : 0.0f, l32, ok, out, blk / nb, (int)(blk % nb));
 }
 
+// dst[0 .. kpad) = x[0 .. n) followed by zeros: the zero-padded fp32 activation row the
+// fp32-activation GEMV reads (written by a kernel, so a captured graph holds no memset node).
+__global__ void __launch_bounds__(256) k_copy_pad(const float* x, int n, int kpad, float* dst) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < kpad) dst[i] = i < n ? x[i] : 0.0f;
+}
+
+void launch_copy_pad(const float* x, int n, int kpad, float* dst, hipStream_t st) {
+    hipLaunchKernelGGL(k_copy_pad, dim3((unsigned)((kpad + 255) / 256)), dim3(256), 0, st, x, n, kpad, dst);
+}
+
 void launch_quantize_q8(const float* x, int rows, int K, ActQ8 out, hipStream_t st) {
     const size_t blocks = (size_t)rows * (K / 32);
     const size_t waves = (blocks + 1) / 2;

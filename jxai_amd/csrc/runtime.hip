@@ -25,6 +25,18 @@ thread_local std::string g_err;
 // keep their own device; entry points make it current on the calling thread).
 std::atomic<int> g_device{-1};
 
+// Scratch of jx_matmul_quant_f32_noalloc: the Q8_0 activations (block scales
+// and sums, then the quants) or the zero-padded fp32 copy of one activation
+// row of at most NOALLOC_MAX_COLS columns.  Each GPU the library runs on holds
+// its own copy until the process ends.  In host code `scratch` names a
+// host-side stand-in: kernels and copies take the device address that
+// jx_moe_init resolves per device (g_scratch).
+constexpr size_t NOALLOC_MAX_COLS = JX_NOALLOC_MAX_COLS;
+constexpr size_t NOALLOC_SCRATCH_BYTES = NOALLOC_MAX_COLS * sizeof(float);  // >= the Q8_0 form's 1.25 B/col
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+constexpr int MAX_DEVICES = 64;
+std::atomic<void*> g_scratch[MAX_DEVICES];
+
 int fail(int code, const std::string& msg) {
     g_err = msg;
     return code;
@@ -575,6 +587,13 @@ int jx_moe_init(int32_t device) {
     if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0)
         return fail(JX_ERR_NODEVICE, std::string("device is ") + p.gcnArchName + ", this build targets gfx950");
     HIPCHK(hipSetDevice(device));
+    if (device >= MAX_DEVICES) return fail(JX_ERR_NODEVICE, "device index beyond the library's table");
+    if (!g_scratch[device].load()) {  // this device's copy of the static scratch, with the device current
+        void* p = nullptr;
+        HIPCHK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(JX_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+        g_scratch[device].store(p);
+    }
     g_device = device;
     return JX_OK;
 }
@@ -871,6 +890,43 @@ int jx_matmul_quant_f32(jx_qmatrix* W, const float* x, float* out) {
     }
     HIPCHK(hipGetLastError());
     HIPCHK(hipMemcpy(out, yd, (size_t)rows * 4, hipMemcpyDeviceToHost));
+    return JX_OK;
+}
+
+int jx_matmul_quant_f32_noalloc(jx_qmatrix* W, const float* x_dev, float* out_dev, void* stream) {
+    if (!W || !x_dev || !out_dev) return fail(JX_ERR_INVALID, "null argument");
+    const int rows = W->rows, cols = W->cols;
+    const bool q8 = rows >= 8 && q8_activation(W->type, cols);
+    if (!q8 && W->type != jx::T_Q4_K)
+        return fail(JX_ERR_UNSUPPORTED, "fp32-activation dot only implemented for Q4_K");
+    const size_t kpad = ((size_t)cols + 255) / 256 * 256;
+    if (kpad > NOALLOC_MAX_COLS)
+        return fail(JX_ERR_UNSUPPORTED, "cols exceed the no-allocation scratch (" + std::to_string(NOALLOC_MAX_COLS) +
+                                            " columns)");
+    if (kpad > (size_t)jx::gemv_max_k(false, 1, !q8))
+        return fail(JX_ERR_UNSUPPORTED, "cols exceeds the GEMV's staged activation capacity");
+    if (W->device < 0 || W->device >= MAX_DEVICES || !g_scratch[W->device].load())
+        return fail(JX_ERR_NODEVICE, "jx_moe_init has not been called for the matrix's device");
+    HIPCHK(hipSetDevice(W->device));
+    uint8_t* sp = static_cast<uint8_t*>(g_scratch[W->device].load());
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    jx::Groups g;
+    g.identity = 1;
+    g.n_tok = 1;
+    jx::ActQ8 a;
+    if (q8) {  // every scale, sum and quant of the row is written before the GEMV reads it
+        a.s = reinterpret_cast<float2*>(sp);
+        a.q = reinterpret_cast<int8_t*>(sp + (size_t)cols / 32 * sizeof(float2));
+        a.K = cols;
+        jx::launch_quantize_q8(x_dev, 1, cols, a, st);
+        jx::launch_gemv_down(W->w.m, a, nullptr, 0, g, 1, 1, out_dev, st);
+    } else {  // fp32 activations zero-padded to whole super-blocks (the padding is rewritten every call)
+        float* xf = reinterpret_cast<float*>(sp);
+        jx::launch_copy_pad(x_dev, cols, (int)kpad, xf, st);
+        a.K = (int)kpad;
+        jx::launch_gemv_down(W->w.m, a, xf, (int)kpad, g, 1, 1, out_dev, st);
+    }
+    HIPCHK(hipGetLastError());
     return JX_OK;
 }
 
