@@ -51,6 +51,22 @@ def _compile(src: str) -> str:
     return obj
 
 
+PROBES = [os.path.join(HERE, "probe", "mfma_rate.hip")]
+
+
+def build_probes() -> list[str]:
+    """Standalone measurement programs (jxai_amd/probe/*.hip -> executables beside them)."""
+    out = []
+    for src in PROBES:
+        exe = src[:-4]
+        cmd = [HIPCC, *[f for f in CFLAGS if f != "-fPIC"], src, "-o", exe]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}{r.stderr}")
+        out.append(exe)
+    return out
+
+
 def build(verbose: bool = True) -> str:
     if shutil.which(HIPCC) is None and not os.path.exists(HIPCC):
         raise RuntimeError("hipcc not found: the MoE path needs ROCm's hipcc to build")
@@ -61,8 +77,9 @@ def build(verbose: bool = True) -> str:
     tmp = LIB + ".tmp"
     subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-o", tmp, *objs], check=True)
     os.replace(tmp, LIB)
+    probes = build_probes()
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB}, " + ", ".join(os.path.relpath(p, HERE) for p in probes))
     return LIB
 
 

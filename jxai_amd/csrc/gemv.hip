@@ -517,7 +517,7 @@ k_gemv_gateup(QMat G, QMat U, ActQ8 xq, Groups grp, ActQ8 hq, float* hf, int hf_
 // Down projection into y[pair][rows].
 template <int TYPE, int TB, int WAVES, bool F32ACT>
 __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(GEMV_WAVES_PER_SIMD(TB))))
-k_gemv_down(QMat D, ActQ8 hq, const float* hf, int hf_ld, Groups grp, float* y) {
+k_gemv_down(QMat D, ActQ8 hq, const float* hf, int hf_ld, Groups grp, float* y, CombineOut comb) {
     extern __shared__ __align__(16) int8_t smem[];
     __shared__ float red[WAVES][TB][32];
     const int rt = blockIdx.x % D.nrt;  // grid: row tile fastest over the slots
@@ -567,7 +567,15 @@ k_gemv_down(QMat D, ActQ8 hq, const float* hf, int hf_ld, Groups grp, float* y) 
                 float s = 0.0f;
 #pragma unroll
                 for (int w = 0; w < WAVES; ++w) s += red[w][j][m];
-                y[(size_t)(p0 + tb0 + j) * D.rows + rt * 32 + m] = s;
+                if (comb.out) {  // folded combine: out[token] += p * y (CombineOut)
+                    const int t = token_of(grp, rec, tb0 + j);
+                    float p = 0.0f;
+                    for (int q = 0; q < comb.k; ++q)
+                        if (comb.ids[(size_t)t * comb.k + q] == e) p = comb.probs[(size_t)t * comb.k + q];
+                    atomicAdd(comb.out + (size_t)t * D.rows + rt * 32 + m, p * s);
+                } else {
+                    y[(size_t)(p0 + tb0 + j) * D.rows + rt * 32 + m] = s;
+                }
             }
         }
     }
@@ -872,14 +880,14 @@ void launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Gro
 
 template <int TYPE, bool F32ACT>
 static void down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp, int slots,
-                   int tb, float* y, hipStream_t st) {
+                   int tb, float* y, hipStream_t st, const CombineOut& comb) {
     dim3 grid(dn.nrt * slots);
     const int K = F32ACT ? hf_ld : hq.K;
     if (tb <= 1) {
         const size_t lds = act_lds_bytes(1, K, F32ACT);
         lds_optin(k_gemv_down<TYPE, 1, DOWN_WAVES, F32ACT>, lds);
         hipLaunchKernelGGL((k_gemv_down<TYPE, 1, DOWN_WAVES, F32ACT>), grid, dim3(DOWN_WAVES * 64), lds, st, dn, hq,
-                           hf, hf_ld, grp, y);
+                           hf, hf_ld, grp, y, comb);
     } else if (tb > 4 && !F32ACT) {  // several tokens per expert: the matrix-core form
         const size_t lds = (size_t)(K / 32) * MX_NT * sizeof(float2);
         lds_optin(k_gemv_mx<TYPE, false, DOWN_WAVES>, lds);
@@ -889,20 +897,22 @@ static void down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, 
         const size_t lds = act_lds_bytes(4, K, F32ACT);
         lds_optin(k_gemv_down<TYPE, 4, DOWN_WAVES, F32ACT>, lds);
         hipLaunchKernelGGL((k_gemv_down<TYPE, 4, DOWN_WAVES, F32ACT>), grid, dim3(DOWN_WAVES * 64), lds, st, dn, hq,
-                           hf, hf_ld, grp, y);
+                           hf, hf_ld, grp, y, comb);
     }
 }
 
 void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp, int slots,
-                      int tb, float* y, hipStream_t st) {
+                      int tb, float* y, hipStream_t st, const CombineOut& comb) {
+    // the folded combine is written for the single-token and four-token GEMVs (the few-token path)
+    const CombineOut c = tb <= 4 ? comb : CombineOut{};
     if (hf) {
-        down_t<T_Q4_K, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st);
+        down_t<T_Q4_K, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c);
         return;
     }
     switch (dn.type) {
-        case T_Q4_0: down_t<T_Q4_0, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st); break;
-        case T_Q8_0: down_t<T_Q8_0, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st); break;
-        case T_Q4_K: down_t<T_Q4_K, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st); break;
+        case T_Q4_0: down_t<T_Q4_0, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
+        case T_Q8_0: down_t<T_Q8_0, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
+        case T_Q4_K: down_t<T_Q4_K, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
         default: break;
     }
 }

@@ -110,6 +110,18 @@ constexpr int MFMA_BN = 128;  // pairs per matrix-core GEMM tile
 // on the Qwen1.5- and DeepSeek-V2-Lite-shaped layers)
 constexpr int MFMA_MIN_SHARED_TOKENS = 64;
 
+// The weighted combine folded into the down GEMV (few-token decode with at most two
+// contributions per output element: top_k <= 2 and no shared expert): out [n][d] is
+// zeroed by the first kernel of the forward and each down block adds p * y for its
+// rows atomically.  Two adds onto an exact zero commute, so the result does not
+// depend on their order.
+struct CombineOut {
+    float* out = nullptr;         // [n][d]; null: the down GEMV writes y[pair][d] instead
+    const float* probs = nullptr; // [n][k] softmax weights in selection order
+    const int* ids = nullptr;     // [n][k] selected experts
+    int k = 0;
+};
+
 struct RouteArgs {
     const float* x;        // [n][d]
     int n, d, E, k;
@@ -123,6 +135,8 @@ struct RouteArgs {
     float* shscale;        // [n]
     float* logits;         // [n][E] or null
     const float* router_cm;  // the router rows, then the shared gate, chain-major (chain_rows)
+    float* zero_out = nullptr;  // few-token routers: zero this many floats here first (the folded
+    int zero_count = 0;         // combine's output; CombineOut)
 };
 
 // Outputs of the token -> expert dispatch (the device side of Groups).
@@ -163,7 +177,7 @@ void launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Gro
 int gemv_max_k(bool gateup, int tb, bool f32);
 // Decode regime: down projection over Q8_0 (hq) or fp32 (hf) activations into y[pair][d].
 void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp,
-                      int slots, int tb, float* y, hipStream_t st);
+                      int slots, int tb, float* y, hipStream_t st, const CombineOut& comb = CombineOut{});
 // Prefill regime: matrix-core grouped GEMMs over the dispatch tile table.
 // gate/up writes SwiGLU(h) as Q8_0 (hq.q != null; the down GEMM takes it after
 // launch_q8_to_acth) and/or fp32 (hf != null).

@@ -688,6 +688,8 @@ __global__ void __launch_bounds__(RS_THREADS)
 k_route_small(RouteArgs a) {
     extern __shared__ float lds[];  // (1 + n) chain-major rows: router row r, then the n tokens
     const int r = blockIdx.x, tid = threadIdx.x;
+    if (r == 0)  // the folded combine's output starts at zero (CombineOut)
+        for (int i = tid; i < a.zero_count; i += RS_THREADS) a.zero_out[i] = 0.0f;
     const int d = a.d, n = a.n, E = a.E, S = rs_stride(d), RS = 16 * S;
     const float* w = r < E ? a.router + (size_t)r * d : a.shgate;
     {  // router row + token rows -> LDS: every load in flight before the first store
@@ -795,6 +797,7 @@ __global__ void __launch_bounds__(R1_THREADS) k_route_one(RouteArgs a, DispatchO
     __shared__ float shl[ROUTE_SMALL_MAX_N];
     const int tid = threadIdx.x;
     const int d = a.d, n = a.n, E = a.E, rows = E + (a.shgate ? 1 : 0);
+    for (int i = tid; i < a.zero_count; i += R1_THREADS) a.zero_out[i] = 0.0f;  // folded combine (CombineOut)
     float* xs = lds + (size_t)rows * d;
     float* lgs = xs + (size_t)n * d;
     {

@@ -230,6 +230,7 @@ struct jx_moe_layer {
     std::map<GraphKey, Graph> graphs;
     uint64_t graph_clock = 0;
     bool use_graphs = true;
+    bool fold_combine = true;  // JX_NO_FOLD=1 keeps the separate combine launch (A/B measurement)
 };
 
 struct jx_qmatrix {
@@ -404,6 +405,26 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     // few-token decode: logits on one block per router row, grouping in the GEMVs
     const bool small_logits = !mfma && !smfma && n <= jx::ROUTE_SMALL_MAX_N && E <= jx::SMALL_GROUP_MAX_E &&
                               jx::route_small_fits(n, d, E);
+    // GEMV form: one token; groups of 4 on the VALU (few tokens per expert); or 16 per weight pass on
+    // the int8 matrix cores, which streams faster once experts see ~2.5 tokens on average (Q8_0, whose
+    // VALU form is slower, from 0.5): measured on every configured shape
+    const bool q8w = L->gate.m.type == jx::T_Q8_0;
+    auto gemv_tb = [&](int tokens_per_expert_x2) {  // twice the average tokens per expert
+        return n == 1 ? 1 : (tokens_per_expert_x2 >= (q8w ? 1 : 5) ? 16 : 4);
+    };
+    const int tb = gemv_tb(2 * nk / E);
+    // fp32 h (Q4_K down with d_ff % 256 != 0) takes the matrix-core down GEMM from 2 tokens on (every
+    // dispatch path writes the MFMA tiles, the few-token one from the gate/up GEMV's tail block): the
+    // fp32 GEMV's multi-token form re-streams the weights per group of 4 tokens in fp32
+    const bool mfma_down = mfma || (L->down_f32 && n >= 2 && mfma_shape);
+    // The weighted combine folds into the down GEMV when the few-token routers run and every output
+    // element receives at most two contributions (top_k <= 2, no shared expert; CombineOut).
+    const bool fold = jx::route_small_fits(n, d, E) && k <= 2 && !L->shared && !mfma_down && tb <= 4 &&
+                      L->fold_combine;
+    if (fold) {
+        ra.zero_out = outdev;
+        ra.zero_count = n * d;
+    }
     if (small_logits) {
         Launch l(L, "route", st);
         jx::launch_route_logits(ra, st);
@@ -436,14 +457,6 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     grp.top_k = k;
     grp.n_tok = n;
     const int slots = std::min(E, nk);
-    // GEMV form: one token; groups of 4 on the VALU (few tokens per expert); or 16 per weight pass on
-    // the int8 matrix cores, which streams faster once experts see ~2.5 tokens on average (Q8_0, whose
-    // VALU form is slower, from 0.5): measured on every configured shape
-    const bool q8w = L->gate.m.type == jx::T_Q8_0;
-    auto gemv_tb = [&](int tokens_per_expert_x2) {  // twice the average tokens per expert
-        return n == 1 ? 1 : (tokens_per_expert_x2 >= (q8w ? 1 : 5) ? 16 : 4);
-    };
-    const int tb = gemv_tb(2 * nk / E);
     const int tbs = n == 1 ? 1 : (n >= 3 ? 16 : 4);  // the shared expert sees every token
     const int tiles_ub = nk / jx::MFMA_BN + slots;
     const size_t fpad = ((size_t)L->F + 255) / 256 * 256;
@@ -502,10 +515,6 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         jx::launch_gemv_gateup(L->gate.m, L->up.m, L->xq, grp, slots, tb, L->hq, L->down_f32 ? L->hf : nullptr, st);
     }
     if (L->shared) HIPCHK(hipStreamWaitEvent(st, L->ev_join, 0));
-    // fp32 h (Q4_K down with d_ff % 256 != 0) takes the matrix-core down GEMM from 2 tokens on (every
-    // dispatch path writes the MFMA tiles, the few-token one from the gate/up GEMV's tail block): the
-    // fp32 GEMV's multi-token form re-streams the weights per group of 4 tokens in fp32
-    const bool mfma_down = mfma || (L->down_f32 && n >= 2 && mfma_shape);
     if (mfma_down) {
         {
             Launch l(L, "h_to_matrix_form", st);
@@ -517,11 +526,18 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         Launch l(L, "down_mfma", st);
         jx::launch_mfma_down(L->down.m, L->hh.a, grp, tiles_ub, L->y, st);
     } else {
-        Launch l(L, L->down_f32 ? "down_gemv_f32" : "down_gemv", st);
+        jx::CombineOut comb;
+        if (fold) {
+            comb.out = outdev;
+            comb.probs = L->probs;
+            comb.ids = L->ids;
+            comb.k = k;
+        }
+        Launch l(L, fold ? "down_gemv_combine" : (L->down_f32 ? "down_gemv_f32" : "down_gemv"), st);
         jx::launch_gemv_down(L->down.m, L->hq, L->down_f32 ? L->hf : nullptr, (int)fpad, grp, slots, mfma ? 4 : tb,
-                             L->y, st);
+                             L->y, st, comb);
     }
-    {
+    if (!fold) {
         Launch l(L, "combine", st);
         jx::launch_combine(n, d, k, L->probs, L->pos_of, L->y, L->shared ? L->ysh : nullptr, L->shscale, outdev, st);
     }
@@ -696,6 +712,7 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
                       hipEventCreateWithFlags(&L->ev_join, hipEventDisableTiming) != hipSuccess))
         return bail(fail(JX_ERR_HIP, "shared-expert stream create"));
     if (const char* g = std::getenv("JX_NO_GRAPH")) L->use_graphs = std::strcmp(g, "0") == 0;
+    if (const char* f = std::getenv("JX_NO_FOLD")) L->fold_combine = std::strcmp(f, "0") == 0;
     *out = L;
     return JX_OK;
 }
