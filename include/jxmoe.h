@@ -158,6 +158,28 @@ int jx_matmul_swiglu_quant_f32(jx_qmatrix* Wg, jx_qmatrix* Wu, const float* x, f
  * device: x [k] fp32 -> k/32 blocks of 34 bytes (fp16 d + 32 int8).  Host pointers. */
 int jx_quantize_row_q8_0(const float* x, void* blocks, int64_t k);
 
+/* ---- host telemetry (no device work) ------------------------------------- */
+
+/* The counter side effects of select_experts_cache_aware (src/tier.cpp:186-194)
+ * replayed from a batch the GPU routed: tokens in order, token t at step
+ * first_step + t (step_tick runs once per token, src/transformer.cpp:2371),
+ * and for each selection s of token t, in rank order, with e = topk_ids[t][s]:
+ *   activation_counts[layer * n_experts + e] += 1
+ *   last_step        [layer * n_experts + e]  = first_step + t
+ *   last_prob        [layer * n_experts + e]  = topk_w[t][s]
+ * The tables are the caller's (LFRUTierManager's activation_counts_,
+ * last_step_, last_prob_), table_len entries each; entries past table_len are
+ * skipped as the reference skips them. */
+int jx_tier_record(uint32_t layer, uint32_t n_experts, const int32_t* topk_ids, const float* topk_w, int32_t n_tok,
+                   int32_t top_k, uint32_t first_step, uint32_t* activation_counts, uint32_t* last_step,
+                   float* last_prob, size_t table_len);
+
+/* LFRU score of one expert as snapshot_telemetry reports it (src/tier.cpp:233-263
+ * with compute_lfru_score, 32-34): activations * 256 + recency, recency =
+ * 255 - (current_step - last_step), 0 when that age reaches 255 or the expert
+ * never ran (last_step 0). */
+uint32_t jx_tier_lfru_score(uint32_t activations, uint32_t last_step, uint32_t current_step);
+
 /* ---- device buffers (plumbing for callers without their own allocator) -- */
 int jx_dev_alloc(size_t bytes, void** ptr);
 int jx_dev_free(void* ptr);

@@ -27,7 +27,7 @@ EXPORTS = [
     "jx_moe_last_xq8",
     "jx_moe_profile", "jx_moe_profile_read", "jx_qmatrix_create", "jx_qmatrix_destroy", "jx_matmul_quant_f32",
     "jx_matmul_swiglu_quant_f32", "jx_quantize_row_q8_0", "jx_matmul_quant_f32_noalloc", "jx_dev_alloc", "jx_dev_free", "jx_memcpy_htod",
-    "jx_memcpy_dtoh", "jx_device_synchronize", "jx_moe_last_error",
+    "jx_memcpy_dtoh", "jx_device_synchronize", "jx_moe_last_error", "jx_tier_record", "jx_tier_lfru_score",
 ]
 
 _fp = C.POINTER(C.c_float)
@@ -88,6 +88,10 @@ def lib() -> C.CDLL:
     L.jx_memcpy_htod.argtypes = [_vp, _vp, C.c_size_t]
     L.jx_memcpy_dtoh.argtypes = [_vp, _vp, C.c_size_t]
     L.jx_device_synchronize.argtypes = []
+    L.jx_tier_record.argtypes = [C.c_uint32, C.c_uint32, _vp, _vp, C.c_int32, C.c_int32, C.c_uint32, _vp, _vp, _vp,
+                                 C.c_size_t]
+    L.jx_tier_lfru_score.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32]
+    L.jx_tier_lfru_score.restype = C.c_uint32
     _lib = L
     return L
 

@@ -72,6 +72,31 @@ int32_t jxr_select_experts(const float* logits, int32_t E, int32_t k, int32_t* i
     return static_cast<int32_t>(sel.size());
 }
 
+// The counters select_experts_cache_aware leaves in LFRUTierManager
+// (tier.cpp:186-194) for n_tok tokens routed one forward_token at a time
+// (step_tick first, transformer.cpp:2371), after ticks_before earlier steps,
+// read back through snapshot_telemetry (tier.cpp:233-263): activations, LFRU
+// score and last probability per (layer, expert), flat [n_layers][E].
+int32_t jxr_tier_replay(const float* logits, int32_t n_tok, int32_t E, int32_t k, int32_t layer, int32_t n_layers,
+                        int32_t ticks_before, uint32_t* activations, uint32_t* lfru_score, float* last_prob) {
+    moe::LFRUTierManager tier;
+    tier.init(static_cast<uint32_t>(n_layers), static_cast<uint32_t>(E), 0, 0, 0.0f);
+    for (int32_t i = 0; i < ticks_before; ++i) tier.step_tick();
+    for (int32_t t = 0; t < n_tok; ++t) {
+        tier.step_tick();
+        (void)tier.select_experts_cache_aware(static_cast<uint32_t>(layer), logits + static_cast<size_t>(t) * E,
+                                              static_cast<uint32_t>(E), static_cast<uint32_t>(k));
+    }
+    const auto snap = tier.snapshot_telemetry();
+    for (const auto& e : snap) {
+        const size_t flat = static_cast<size_t>(e.layer) * static_cast<size_t>(E) + e.expert;
+        activations[flat] = e.activations;
+        lfru_score[flat] = e.lfru_score;
+        last_prob[flat] = e.last_prob;
+    }
+    return static_cast<int32_t>(snap.size());
+}
+
 // The MoE block of forward_token (transformer.cpp:2589-2757) for the listed
 // tokens: router GEMV, optional harness-side logit bias, top-k, routed experts
 // in selection order, shared expert with optional sigmoid gate.
