@@ -44,7 +44,9 @@ enum {
     JX_FWD_DEVICE_PTRS = 1u << 0, /* x, out, ids, weights, counts on the device  */
     JX_FWD_ASYNC = 1u << 1,       /* return after enqueueing (device ptrs only)   */
     JX_FWD_FORCE_GEMV = 1u << 2,  /* force the decode (dequant-GEMV) regime       */
-    JX_FWD_FORCE_MFMA = 1u << 3   /* force the prefill (matrix-core GEMM) regime  */
+    JX_FWD_FORCE_MFMA = 1u << 3,  /* force the prefill (matrix-core GEMM) regime  */
+    JX_FWD_RESIDUAL = 1u << 4     /* x is the residual stream before ffn_norm: the
+                                     whole FFN step of forward_token (see below)   */
 };
 
 /* One MoE layer, as bound by bind_tensors (src/transformer.cpp:2142-2186).
@@ -74,6 +76,11 @@ typedef struct jx_moe_layer_desc {
                               matmul_quant_f32 (transformer.cpp:2591), whose
                               8-lane dot order (quant.cpp:3015-3055) this
                               library does not reproduce: JX_ERR_UNSUPPORTED */
+    /* The steps either side of the block, used with JX_FWD_RESIDUAL
+     * (src/transformer.cpp:2585-2587, 2758-2764): */
+    const float* ffn_norm;      /* [d] fp32 blk.L.ffn_norm, or NULL (weight 1)       */
+    const float* post_ffw_norm; /* [d] fp32 blk.L.post_ffw_norm, or NULL (none)      */
+    float rms_norm_eps;         /* hp_.rms_norm_eps (<arch>.attention.layer_norm_rms_epsilon) */
 } jx_moe_layer_desc;
 
 typedef struct jx_moe_layer jx_moe_layer;
@@ -101,7 +108,13 @@ void jx_moe_layer_destroy(jx_moe_layer* layer);
  *   stream      hipStream_t (NULL = default stream)
  * With CACHE_ROUTE off, ids/order/counts are those of
  * select_experts_cache_aware (src/tier.cpp:124-198); exact logit ties are
- * ordered by expert index. */
+ * ordered by expert index.
+ * With JX_FWD_RESIDUAL, x is the residual stream and the call is the whole
+ * FFN step of forward_token (src/transformer.cpp:2585-2764):
+ *   x_norm = rms_norm(x, ffn_norm, eps)       (2585-2587; weight 1 when NULL)
+ *   acc    = the MoE block on x_norm          (2589-2757)
+ *   acc    = rms_norm(acc, post_ffw_norm, eps) if the layer has one (2758-2760)
+ *   out    = x + acc                          (2762-2764; out may alias x) */
 int jx_moe_forward(jx_moe_layer* layer, const float* x, int32_t n_tok, float* out, int32_t* topk_ids,
                    float* topk_w, int32_t* expert_counts, void* stream, uint32_t flags);
 
@@ -154,9 +167,54 @@ int jx_matmul_quant_f32_noalloc(jx_qmatrix* W, const float* x_dev, float* out_de
  * Host pointers. */
 int jx_matmul_swiglu_quant_f32(jx_qmatrix* Wg, jx_qmatrix* Wu, const float* x, float* out, int32_t use_gelu);
 
+/* Device-pointer forms of the dense projections, enqueued on `stream`
+ * (hipStream_t; returns without synchronizing), no per-call allocation: each
+ * matrix holds a workspace for one activation row, allocated by
+ * jx_qmatrix_create, so calls on one matrix (or one q/k/v set, whose first
+ * matrix's workspace is used) must not overlap.
+ *   jx_matmul_quant_f32_dev:     matmul_quant_f32 (src/quant.cpp:3895-3922)
+ *   jx_matmul_qkv_quant_f32_dev: matmul_qkv_quant_f32 (src/quant.cpp:3924-3968):
+ *     x quantized once when the given matrices hold >= 8 rows together; any of
+ *     Wq, Wk, Wv may be NULL; they share cols. */
+int jx_matmul_quant_f32_dev(jx_qmatrix* W, const float* x_dev, float* out_dev, void* stream);
+int jx_matmul_qkv_quant_f32_dev(jx_qmatrix* Wq, jx_qmatrix* Wk, jx_qmatrix* Wv, const float* x_dev, float* q_dev,
+                                float* k_dev, float* v_dev, void* stream);
+
 /* quantize_row_q8_0 (include/quant.h:112; src/quant.cpp:1029-1045) on the
  * device: x [k] fp32 -> k/32 blocks of 34 bytes (fp16 d + 32 int8).  Host pointers. */
 int jx_quantize_row_q8_0(const float* x, void* blocks, int64_t k);
+
+/* ---- GGUF model files (host only) ---------------------------------------- */
+
+/* A GGUF v2/v3 file mapped read-only and parsed: header, metadata, tensor table
+ * (ModelFile::open / parse_gguf, src/gguf.cpp:810-889), every read bounds-checked;
+ * each tensor must lie inside the file.  Errors: jx_gguf_last_error(). */
+typedef struct jx_gguf jx_gguf;
+int jx_gguf_open(const char* path, jx_gguf** out);
+void jx_gguf_close(jx_gguf* g);
+int64_t jx_gguf_tensor_count(const jx_gguf* g);
+/* index of a tensor by name (ModelFile::find_tensor, include/gguf.h:73), -1 if absent */
+int64_t jx_gguf_find_tensor(const jx_gguf* g, const char* name);
+/* name, GGML type, dims (4 entries, 1-padded), absolute file offset, whole-tensor
+ * bytes (tensor_byte_size, include/common.h:191-195) and mapped bytes of tensor i
+ * (TensorDescriptor, include/gguf.h:36-46); outputs may be NULL */
+int jx_gguf_tensor_info(const jx_gguf* g, int64_t i, const char** name, int32_t* type, int32_t* n_dims, uint64_t* dims,
+                        uint64_t* file_offset, uint64_t* nbytes, const void** data);
+/* metadata as ModelFile::get_u32 / get_f32 / get_str read it (src/gguf.cpp:1629-1642):
+ * `def` when the key is absent; get_str gives NULL for absent or non-string keys */
+int jx_gguf_get_u32(const jx_gguf* g, const char* key, uint32_t def, uint32_t* out);
+int jx_gguf_get_f32(const jx_gguf* g, const char* key, float def, float* out);
+int jx_gguf_get_str(const jx_gguf* g, const char* key, const char** out);
+/* The MoE tensors of layer `layer` bound as bind_tensors binds them
+ * (src/transformer.cpp:1954-1972, 2116-2199): router blk.L.ffn_gate_inp, the
+ * packed ffn_{gate,up,down}_exps (n_experts and d_ff from their dims, top_k from
+ * <arch>.expert_used_count), the shared expert ffn_*_shexp with
+ * ffn_gate_inp_shexp, GELU-tanh for the gemma family; a dense FFN
+ * (ffn_{gate,up,down}.weight) binds as one expert at top-1.  The pointers point
+ * into the mapping: valid until jx_gguf_close; pass the desc to
+ * jx_moe_layer_create, which copies the bytes to HBM. */
+int jx_gguf_moe_layer_desc(jx_gguf* g, int32_t layer, jx_moe_layer_desc* desc);
+const char* jx_gguf_last_error(void);
 
 /* ---- host telemetry (no device work) ------------------------------------- */
 

@@ -17,6 +17,7 @@ JX_FWD_DEVICE_PTRS = 1 << 0
 JX_FWD_ASYNC = 1 << 1
 JX_FWD_FORCE_GEMV = 1 << 2
 JX_FWD_FORCE_MFMA = 1 << 3
+JX_FWD_RESIDUAL = 1 << 4
 
 JX_ACT_SILU = 0
 JX_ACT_GELU_TANH = 1
@@ -28,6 +29,9 @@ EXPORTS = [
     "jx_moe_profile", "jx_moe_profile_read", "jx_qmatrix_create", "jx_qmatrix_destroy", "jx_matmul_quant_f32",
     "jx_matmul_swiglu_quant_f32", "jx_quantize_row_q8_0", "jx_matmul_quant_f32_noalloc", "jx_dev_alloc", "jx_dev_free", "jx_memcpy_htod",
     "jx_memcpy_dtoh", "jx_device_synchronize", "jx_moe_last_error", "jx_tier_record", "jx_tier_lfru_score",
+    "jx_gguf_open", "jx_gguf_close", "jx_gguf_tensor_count", "jx_gguf_find_tensor", "jx_gguf_tensor_info",
+    "jx_gguf_get_u32", "jx_gguf_get_f32", "jx_gguf_get_str", "jx_gguf_moe_layer_desc", "jx_gguf_last_error",
+    "jx_matmul_quant_f32_dev", "jx_matmul_qkv_quant_f32_dev",
 ]
 
 _fp = C.POINTER(C.c_float)
@@ -46,6 +50,7 @@ class LayerDesc(C.Structure):
         ("sh_gate", _vp), ("sh_up", _vp), ("sh_down", _vp),
         ("sh_gate_inp", _vp),
         ("activation", C.c_int32), ("router_type", C.c_int32),
+        ("ffn_norm", _vp), ("post_ffw_norm", _vp), ("rms_norm_eps", C.c_float),
     ]
 
 
@@ -81,6 +86,8 @@ def lib() -> C.CDLL:
     L.jx_qmatrix_destroy.restype = None
     L.jx_matmul_quant_f32.argtypes = [_vp, _vp, _vp]
     L.jx_matmul_quant_f32_noalloc.argtypes = [_vp, _vp, _vp, _vp]
+    L.jx_matmul_quant_f32_dev.argtypes = [_vp, _vp, _vp, _vp]
+    L.jx_matmul_qkv_quant_f32_dev.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
     L.jx_matmul_swiglu_quant_f32.argtypes = [_vp, _vp, _vp, _vp, C.c_int32]
     L.jx_quantize_row_q8_0.argtypes = [_vp, _vp, C.c_int64]
     L.jx_dev_alloc.argtypes = [C.c_size_t, C.POINTER(_vp)]
@@ -92,6 +99,21 @@ def lib() -> C.CDLL:
                                  C.c_size_t]
     L.jx_tier_lfru_score.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32]
     L.jx_tier_lfru_score.restype = C.c_uint32
+    L.jx_gguf_open.argtypes = [C.c_char_p, C.POINTER(_vp)]
+    L.jx_gguf_close.argtypes = [_vp]
+    L.jx_gguf_close.restype = None
+    L.jx_gguf_tensor_count.argtypes = [_vp]
+    L.jx_gguf_tensor_count.restype = C.c_int64
+    L.jx_gguf_find_tensor.argtypes = [_vp, C.c_char_p]
+    L.jx_gguf_find_tensor.restype = C.c_int64
+    L.jx_gguf_tensor_info.argtypes = [_vp, C.c_int64, C.POINTER(C.c_char_p), C.POINTER(C.c_int32),
+                                      C.POINTER(C.c_int32), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
+                                      C.POINTER(C.c_uint64), C.POINTER(_vp)]
+    L.jx_gguf_get_u32.argtypes = [_vp, C.c_char_p, C.c_uint32, C.POINTER(C.c_uint32)]
+    L.jx_gguf_get_f32.argtypes = [_vp, C.c_char_p, C.c_float, C.POINTER(C.c_float)]
+    L.jx_gguf_get_str.argtypes = [_vp, C.c_char_p, C.POINTER(C.c_char_p)]
+    L.jx_gguf_moe_layer_desc.argtypes = [_vp, C.c_int32, C.POINTER(LayerDesc)]
+    L.jx_gguf_last_error.restype = C.c_char_p
     _lib = L
     return L
 

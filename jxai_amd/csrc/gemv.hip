@@ -567,6 +567,7 @@ k_gemv_down(QMat D, ActQ8 hq, const float* hf, int hf_ld, Groups grp, float* y, 
                 float s = 0.0f;
 #pragma unroll
                 for (int w = 0; w < WAVES; ++w) s += red[w][j][m];
+                if (D.valid_rows && rt * 32 + m >= D.valid_rows) continue;  // padding rows of a single matrix
                 if (comb.out) {  // folded combine: out[token] += p * y (CombineOut)
                     const int t = token_of(grp, rec, tb0 + j);
                     float p = 0.0f;

@@ -38,6 +38,10 @@ struct QMat {
     // Gated activation applied to this matrix's outputs when it is the gate of
     // a gate/up pair (ACT_SILU or ACT_GELU_TANH); unused otherwise.
     int act = 0;
+    // Rows that exist when `rows` was padded to whole tiles with zero blocks (a
+    // single matrix of any row count, jx_qmatrix_create); the single-token down
+    // GEMV writes outputs for these only.  0: every row.
+    int valid_rows = 0;
 };
 constexpr size_t QMAT_PAD = 8192;
 
@@ -187,9 +191,14 @@ void launch_mfma_down(const QMat& dn, const ActH& hin, const Groups& grp, int ti
 // Fill m.mn (m.n_mats * m.nrt * m.nkb * 1536 bytes) from a repacked Q4_K matrix.
 void launch_min_table(const QMat& m, uint8_t* mn, hipStream_t st);
 
-// out[t] = sum_s p[t][s] * y[pos(t,s)] (+ shscale[t] * ysh[t]), fma in selection order.
+// acc[t] = sum_s p[t][s] * y[pos(t,s)] (+ shscale[t] * ysh[t]), fma in selection order;
+// out[t] = acc[t], or resid[t] + acc[t] (resid != null), or with post_w:
+// (resid[t] +) rms_norm(acc[t], post_w, eps) (post_ffw_norm, transformer.cpp:2758-2764).
 void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
-                    const float* shscale, float* out, hipStream_t st);
+                    const float* shscale, float* out, hipStream_t st, const float* resid = nullptr,
+                    const float* post_w = nullptr, float eps = 0.0f);
+// MoETransformerEngine::rms_norm (transformer.cpp:67-73) of rows x d floats: out = x * inv * w.
+void launch_rms_norm(const float* x, const float* w, int rows, int d, float eps, float* out, hipStream_t st);
 
 // Decode routing for n <= ROUTE_SMALL_MAX_N tokens and E <= SMALL_GROUP_MAX_E
 // experts without a dispatch launch: router logits and Q8_0 of x (one block

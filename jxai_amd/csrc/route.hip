@@ -1041,6 +1041,61 @@ void launch_dispatch(const int* ids, int nk, int E, int top_k, const DispatchOut
     hipLaunchKernelGGL(k_dispatch, dim3(E), dim3(DISPATCH_THREADS), (size_t)E * sizeof(int), st, ids, nk, E, top_k, o);
 }
 
+// sum_i x[i] * x[i] over one row in vec_dot_f32's order (src/quant.cpp:2756-2778;
+// d % 16 == 0): lane j < 16 of the calling wave runs the fma chain over the
+// elements 16 i + j of the chain-major row xs (element 16 i + j at j * S + i),
+// lanes 0-7 are the reference's acc0, 8-15 its acc1; then acc0 + acc1 and the
+// sequential sum of the 8 lanes.  Every lane of the wave calls it; the result
+// is valid in lanes 0-15.
+__device__ __forceinline__ float row_sumsq_chain(const float* xs, int S, int m, int lane) {
+    const int j = lane & 15;
+    float acc = 0.0f;
+    if (lane < 16)
+        for (int i = 0; i < m; ++i) {
+            const float v = xs[j * S + i];
+            acc = __builtin_fmaf(v, v, acc);
+        }
+    const float hi = __shfl_down(acc, 8, 16);
+    const float v = acc + hi;  // acc0[j] + acc1[j] for j < 8
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) s += __shfl(v, q, 16);
+    return s;
+}
+
+// MoETransformerEngine::rms_norm (src/transformer.cpp:67-73) of `rows` rows of
+// d floats, one block per row: ss = vec_dot_f32(x, x) in the reference's
+// order, inv = 1 / sqrt(ss / d + eps) (IEEE division and square root), then
+// out[i] = x[i] * inv * w[i] (w == null: weight 1).
+__global__ void __launch_bounds__(256) k_rms_norm(const float* x, const float* w, int d, float eps, float* out) {
+    extern __shared__ float xs[];  // chain-major row
+    __shared__ float inv_s;
+    const size_t row = blockIdx.x;
+    const int tid = threadIdx.x, S = d / 16 + 1;  // odd stride: the 16 chains hit distinct banks
+    const float* xr = x + row * (size_t)d;
+    for (int e = tid; e < d; e += 256) xs[(e & 15) * S + (e >> 4)] = xr[e];
+    __syncthreads();
+    if (tid < 64) {
+        const float ss = row_sumsq_chain(xs, S, d / 16, tid);
+        if (tid == 0) inv_s = 1.0f / sqrtf(ss / (float)d + eps);
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    float* orow = out + row * (size_t)d;
+    for (int e = tid; e < d; e += 256) {
+        const float v = xr[e] * inv;
+        orow[e] = w ? v * w[e] : v;
+    }
+}
+
+void launch_rms_norm(const float* x, const float* w, int rows, int d, float eps, float* out, hipStream_t st) {
+    const size_t lds = (size_t)16 * (d / 16 + 1) * sizeof(float);
+    if (lds > 65536)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_rms_norm), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)lds);
+    hipLaunchKernelGGL(k_rms_norm, dim3((unsigned)rows), dim3(256), lds, st, x, w, d, eps, out);
+}
+
 // MoE combine (transformer.cpp:2728-2730 and 2752-2754): starting from 0, for
 // each selected expert in descending-logit order acc = fma(p, y, acc), then
 // acc = fma(shared_scale, y_shared, acc).
@@ -1049,7 +1104,7 @@ void launch_dispatch(const int* ids, int nk, int E, int top_k, const DispatchOut
 template <int KU>  // slots whose loads go out together (the fma order stays the selection order)
 __global__ void __launch_bounds__(256)
 k_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
-          const float* shscale, float* out) {
+          const float* shscale, const float* resid, float* out) {
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;  // float4 index
     const int d4 = d / 4;
     if (idx >= (size_t)n * d4) return;
@@ -1085,16 +1140,65 @@ k_combine(int n, int d, int k, const float* probs, const int* pos_of, const floa
         acc.z = __builtin_fmaf(w, v.z, acc.z);
         acc.w = __builtin_fmaf(w, v.w, acc.w);
     }
+    if (resid) {  // the residual add after the block (transformer.cpp:2762-2764)
+        const float4 r = *reinterpret_cast<const float4*>(resid + (size_t)t * d + i);
+        acc = make_float4(r.x + acc.x, r.y + acc.y, r.z + acc.z, r.w + acc.w);
+    }
     *reinterpret_cast<float4*>(out + (size_t)t * d + i) = acc;
 }
 
+// The combine of one token per block followed by post_ffw_norm
+// (transformer.cpp:2758-2760: rms_norm of moe_accum in place) and the residual
+// add (2762-2764): out = resid + rms_norm(acc, post_w).  acc as k_combine
+// computes it, staged chain-major for the exact vec_dot_f32 order of the norm.
+__global__ void __launch_bounds__(256)
+k_combine_norm(int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
+               const float* shscale, const float* post_w, float eps, const float* resid, float* out) {
+    extern __shared__ float as[];  // chain-major acc row
+    __shared__ float inv_s;
+    const int t = blockIdx.x, tid = threadIdx.x, S = d / 16 + 1;
+    for (int i = tid; i < d; i += 256) {
+        float acc = 0.0f;
+        for (int s = 0; s < k; ++s) {
+            const float w = probs[(size_t)t * k + s];
+            acc = __builtin_fmaf(w, y[(size_t)pos_of[(size_t)t * k + s] * d + i], acc);
+        }
+        if (ysh) acc = __builtin_fmaf(shscale[t], ysh[(size_t)t * d + i], acc);
+        as[(i & 15) * S + (i >> 4)] = acc;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const float ss = row_sumsq_chain(as, S, d / 16, tid);
+        if (tid == 0) inv_s = 1.0f / sqrtf(ss / (float)d + eps);
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    for (int i = tid; i < d; i += 256) {
+        const float v = as[(i & 15) * S + (i >> 4)] * inv * post_w[i];
+        out[(size_t)t * d + i] = resid ? resid[(size_t)t * d + i] + v : v;
+    }
+}
+
 void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
-                    const float* shscale, float* out, hipStream_t st) {
+                    const float* shscale, float* out, hipStream_t st, const float* resid, const float* post_w,
+                    float eps) {
+    if (post_w) {
+        const size_t lds = (size_t)16 * (d / 16 + 1) * sizeof(float);
+        if (lds > 65536)
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_combine_norm),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        hipLaunchKernelGGL(k_combine_norm, dim3((unsigned)n), dim3(256), lds, st, d, k, probs, pos_of, y, ysh, shscale,
+                           post_w, eps, resid, out);
+        return;
+    }
     const size_t tot = (size_t)n * (d / 4);
     const dim3 grid((unsigned)((tot + 255) / 256));
-    if (k <= 2) hipLaunchKernelGGL(k_combine<2>, grid, dim3(256), 0, st, n, d, k, probs, pos_of, y, ysh, shscale, out);
-    else if (k <= 4) hipLaunchKernelGGL(k_combine<4>, grid, dim3(256), 0, st, n, d, k, probs, pos_of, y, ysh, shscale, out);
-    else hipLaunchKernelGGL(k_combine<8>, grid, dim3(256), 0, st, n, d, k, probs, pos_of, y, ysh, shscale, out);
+    if (k <= 2)
+        hipLaunchKernelGGL(k_combine<2>, grid, dim3(256), 0, st, n, d, k, probs, pos_of, y, ysh, shscale, resid, out);
+    else if (k <= 4)
+        hipLaunchKernelGGL(k_combine<4>, grid, dim3(256), 0, st, n, d, k, probs, pos_of, y, ysh, shscale, resid, out);
+    else
+        hipLaunchKernelGGL(k_combine<8>, grid, dim3(256), 0, st, n, d, k, probs, pos_of, y, ysh, shscale, resid, out);
 }
 
 // Q8_0 of `rows` rows of K fp32 values (quantize_row_q8_0, src/quant.cpp:1029-1045),

@@ -188,6 +188,10 @@ struct jx_moe_layer {
     int E = 0, k = 0, d = 0, F = 0, Fs = 0;
     bool shared = false, down_f32 = false, sdown_f32 = false;
     float* router = nullptr;
+    float* ffn_norm = nullptr;   // [d] or null (weight 1)
+    float* post_norm = nullptr;  // [d] or null (no post_ffw_norm)
+    float eps = 1e-5f;
+    float* xn = nullptr;         // workspace: rms_norm of the residual stream (JX_FWD_RESIDUAL)
     float* router_cm = nullptr;  // router rows + shared gate, chain-major
     float* bias = nullptr;
     float* shgate = nullptr;
@@ -237,6 +241,10 @@ struct jx_qmatrix {
     int device = 0;
     int type = 0, rows = 0, cols = 0;
     DevMat w;
+    // workspace of the device-pointer drop-ins, allocated with the matrix: the Q8_0 form of
+    // one activation row of `cols`, and its fp32 copy zero-padded to whole super-blocks
+    jx::ActQ8 xq;
+    float* xf = nullptr;
 };
 
 namespace {
@@ -255,6 +263,7 @@ int ensure_workspace(jx_moe_layer* L, int n) {
         return r;                                      \
     }
     WS(L->x, (size_t)cap * L->d);
+    WS(L->xn, (size_t)cap * L->d);
     WS(L->out, (size_t)cap * L->d);
     WS(L->probs, nk);
     WS(L->ids, nk);
@@ -314,7 +323,7 @@ int ensure_workspace(jx_moe_layer* L, int n) {
 void free_layer(jx_moe_layer* L) {
     (void)hipSetDevice(L->device);
     for (auto* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown}) m->release();
-    void* ptrs[] = {L->router, L->router_cm, L->bias, L->shgate, L->x, L->out, L->probs, L->shscale, L->logits, L->ids,
+    void* ptrs[] = {L->router, L->router_cm, L->bias, L->shgate, L->ffn_norm, L->post_norm, L->xn, L->x, L->out, L->probs, L->shscale, L->logits, L->ids,
                     L->counts, L->offs, L->act, L->n_act, L->pair_tok, L->pos_of, L->n_tiles, L->tiles,
                     L->slots, L->xq.q, L->xq.s, L->hq.q, L->hq.s, L->hqs.q, L->hqs.s, L->hf, L->hfs, L->y, L->ysh};
     for (void* p : ptrs)
@@ -384,6 +393,14 @@ constexpr size_t LARGE_EXPERT_ELEMS = (size_t)1 << 25;  // d * d_ff per matrix
 
 int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStream_t st, uint32_t flags) {
     const int E = L->E, k = L->k, d = L->d;
+    // the residual-stream form: x_norm = rms_norm(x, ffn_norm) feeds the router; x is added back in the combine
+    const bool resid = flags & JX_FWD_RESIDUAL;
+    const float* xres = xdev;
+    if (resid) {
+        Launch l(L, "rms_norm", st);
+        jx::launch_rms_norm(xdev, L->ffn_norm, n, d, L->eps, L->xn, st);
+        xdev = L->xn;
+    }
     const int nk = n * k;
     const int min_ppe = L->gate.m.type == jx::T_Q8_0                 ? MFMA_MIN_PAIRS_PER_EXPERT_Q8
                         : (size_t)d * L->F >= LARGE_EXPERT_ELEMS ? MFMA_MIN_PAIRS_PER_EXPERT_Q4_LARGE
@@ -420,7 +437,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     // The weighted combine folds into the down GEMV when the few-token routers run and every output
     // element receives at most two contributions (top_k <= 2, no shared expert; CombineOut).
     const bool fold = jx::route_small_fits(n, d, E) && k <= 2 && !L->shared && !mfma_down && tb <= 4 &&
-                      L->fold_combine;
+                      !resid && L->fold_combine;
     if (fold) {
         ra.zero_out = outdev;
         ra.zero_count = n * d;
@@ -539,7 +556,8 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     }
     if (!fold) {
         Launch l(L, "combine", st);
-        jx::launch_combine(n, d, k, L->probs, L->pos_of, L->y, L->shared ? L->ysh : nullptr, L->shscale, outdev, st);
+        jx::launch_combine(n, d, k, L->probs, L->pos_of, L->y, L->shared ? L->ysh : nullptr, L->shscale, outdev, st,
+                           resid ? xres : nullptr, resid ? L->post_norm : nullptr, L->eps);
     }
     HIPCHK(hipGetLastError());
     return JX_OK;
@@ -695,6 +713,17 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
                 return bail(fail(JX_ERR_HIP, "shared gate upload"));
         }
     }
+    L->eps = D->rms_norm_eps;
+    if (D->ffn_norm) {
+        if ((r = dalloc(L->ffn_norm, d)) != JX_OK) return bail(r);
+        if (hipMemcpy(L->ffn_norm, D->ffn_norm, d * 4, hipMemcpyHostToDevice) != hipSuccess)
+            return bail(fail(JX_ERR_HIP, "ffn_norm upload"));
+    }
+    if (D->post_ffw_norm) {
+        if ((r = dalloc(L->post_norm, d)) != JX_OK) return bail(r);
+        if (hipMemcpy(L->post_norm, D->post_ffw_norm, d * 4, hipMemcpyHostToDevice) != hipSuccess)
+            return bail(fail(JX_ERR_HIP, "post_ffw_norm upload"));
+    }
     {  // chain-major router copy for the many-token router
         const int R = L->E + (L->shgate ? 1 : 0);
         std::vector<float> rows((size_t)R * d), cm((size_t)R * 16 * jx::chain_stride((int)d));
@@ -753,7 +782,8 @@ int jx_moe_forward(jx_moe_layer* L, const float* x, int32_t n_tok, float* out, i
     // length per prompt) launch directly instead of capturing a graph for every length.
     if (L->use_graphs && !L->prof.on && cap == hipStreamCaptureStatusNone && n_tok <= jx_moe_layer::GRAPH_MAX_N) {
         // the launch sequence depends only on (n, buffers, regime flags): replay a captured graph
-        const jx_moe_layer::GraphKey key{n_tok, xin, outp, flags & (JX_FWD_FORCE_GEMV | JX_FWD_FORCE_MFMA)};
+        const jx_moe_layer::GraphKey key{n_tok, xin, outp,
+                                         flags & (JX_FWD_FORCE_GEMV | JX_FWD_FORCE_MFMA | JX_FWD_RESIDUAL)};
         auto it = L->graphs.find(key);
         if (it == L->graphs.end()) {
             HIPCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
@@ -857,12 +887,27 @@ int jx_qmatrix_create(int32_t type, int64_t rows, int64_t cols, const void* host
     m->type = type;
     m->rows = (int)rows;
     m->cols = (int)cols;
-    const int r = upload_matrix(type, 1, (int)rows, (int)cols, host, m->w, nullptr);
+    // rows padded to whole 32-row tiles with zero blocks (their dots are zero and never written out)
+    const int64_t rpad = (rows + jx::ROWS_PER_TILE - 1) / jx::ROWS_PER_TILE * jx::ROWS_PER_TILE;
+    const size_t rb = row_bytes(type, cols);
+    std::vector<uint8_t> padded;
+    const void* src = host;
+    if (rpad != rows && rb) {
+        padded.assign((size_t)rpad * rb, 0);
+        std::memcpy(padded.data(), host, (size_t)rows * rb);
+        src = padded.data();
+    }
+    int r = upload_matrix(type, 1, (int)rpad, (int)cols, src, m->w, nullptr);
+    m->w.m.valid_rows = (int)rows;
+    const size_t kpad = ((size_t)cols + 255) / 256 * 256;
+    if (r == JX_OK) r = dalloc(m->xq.q, kpad);
+    if (r == JX_OK) r = dalloc(m->xq.s, kpad / 32);
+    if (r == JX_OK) r = dalloc(m->xf, kpad);
     if (r != JX_OK) {
-        m->w.release();
-        delete m;
+        jx_qmatrix_destroy(m);
         return r;
     }
+    m->xq.K = (int)cols;
     *out = m;
     return JX_OK;
 }
@@ -871,7 +916,82 @@ void jx_qmatrix_destroy(jx_qmatrix* m) {
     if (!m) return;
     (void)hipSetDevice(m->device);
     m->w.release();
+    for (void* p : {(void*)m->xq.q, (void*)m->xq.s, (void*)m->xf})
+        if (p) (void)hipFree(p);
     delete m;
+}
+
+// One matrix of the device-pointer drop-ins: out[r] = W[r] . x over the Q8_0 form xq (q8) or the
+// zero-padded fp32 copy xf of the same activation row.
+static int dev_gemv(jx_qmatrix* W, bool q8, const jx::ActQ8& xq, float* xf, float* out, hipStream_t st) {
+    const size_t kpad = ((size_t)W->cols + 255) / 256 * 256;
+    if (!q8 && W->type != jx::T_Q4_K) return fail(JX_ERR_UNSUPPORTED, "fp32-activation dot only implemented for Q4_K");
+    if (kpad > (size_t)jx::gemv_max_k(false, 1, !q8))
+        return fail(JX_ERR_UNSUPPORTED, "cols exceeds the GEMV's staged activation capacity");
+    jx::Groups g;
+    g.identity = 1;
+    g.n_tok = 1;
+    if (q8) {
+        jx::launch_gemv_down(W->w.m, xq, nullptr, 0, g, 1, 1, out, st);
+    } else {
+        jx::ActQ8 a;
+        a.K = (int)kpad;
+        jx::launch_gemv_down(W->w.m, a, xf, (int)kpad, g, 1, 1, out, st);
+    }
+    return JX_OK;
+}
+
+int jx_matmul_quant_f32_dev(jx_qmatrix* W, const float* x_dev, float* out_dev, void* stream) {
+    if (!W || !x_dev || !out_dev) return fail(JX_ERR_INVALID, "null argument");
+    HIPCHK(hipSetDevice(W->device));
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const bool q8 = W->rows >= 8 && q8_activation(W->type, W->cols);  // matmul_quant_f32, quant.cpp:3908
+    const size_t kpad = ((size_t)W->cols + 255) / 256 * 256;
+    if (q8)
+        jx::launch_quantize_q8(x_dev, 1, W->cols, W->xq, st);
+    else
+        jx::launch_copy_pad(x_dev, W->cols, (int)kpad, W->xf, st);
+    int r = dev_gemv(W, q8, W->xq, W->xf, out_dev, st);
+    if (r != JX_OK) return r;
+    HIPCHK(hipGetLastError());
+    return JX_OK;
+}
+
+int jx_matmul_qkv_quant_f32_dev(jx_qmatrix* Wq, jx_qmatrix* Wk, jx_qmatrix* Wv, const float* x_dev, float* q_dev,
+                                float* k_dev, float* v_dev, void* stream) {
+    jx_qmatrix* Ws[3] = {Wq, Wk, Wv};
+    float* outs[3] = {q_dev, k_dev, v_dev};
+    jx_qmatrix* first = nullptr;
+    int64_t total_rows = 0;
+    for (int i = 0; i < 3; ++i) {
+        if (!Ws[i]) continue;
+        if (!outs[i]) return fail(JX_ERR_INVALID, "null output for a given matrix");
+        if (!first) first = Ws[i];
+        if (Ws[i]->cols != first->cols || Ws[i]->device != first->device)
+            return fail(JX_ERR_INVALID, "q, k and v matrices must share cols and device");
+        total_rows += Ws[i]->rows;
+    }
+    if (!first || !x_dev) return fail(JX_ERR_INVALID, "null argument");
+    HIPCHK(hipSetDevice(first->device));
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int cols = first->cols;
+    const size_t kpad = ((size_t)cols + 255) / 256 * 256;
+    // x quantized once when the three matrices hold 8 rows or more (matmul_qkv_quant_f32,
+    // quant.cpp:3940-3947); each row then takes the Q8_0 form where its type allows
+    // (vec_dot_row_with_q8, 3841-3879), fp32 otherwise
+    const bool quantized = total_rows >= 8 && cols % 32 == 0;
+    bool need_f32 = false;
+    for (int i = 0; i < 3; ++i)
+        if (Ws[i] && !(quantized && q8_activation(Ws[i]->type, cols))) need_f32 = true;
+    if (quantized) jx::launch_quantize_q8(x_dev, 1, cols, first->xq, st);
+    if (need_f32) jx::launch_copy_pad(x_dev, cols, (int)kpad, first->xf, st);
+    for (int i = 0; i < 3; ++i) {
+        if (!Ws[i]) continue;
+        const int r = dev_gemv(Ws[i], quantized && q8_activation(Ws[i]->type, cols), first->xq, first->xf, outs[i], st);
+        if (r != JX_OK) return r;
+    }
+    HIPCHK(hipGetLastError());
+    return JX_OK;
 }
 
 int jx_matmul_quant_f32(jx_qmatrix* W, const float* x, float* out) {

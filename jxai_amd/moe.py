@@ -17,8 +17,8 @@ import ctypes as C
 import numpy as np
 
 from . import formats as F
-from ._lib import (JX_FWD_DEVICE_PTRS, JX_FWD_ASYNC, JX_FWD_FORCE_GEMV, JX_FWD_FORCE_MFMA, JxError,  # noqa: F401
-                   LayerDesc, check, lib)
+from ._lib import (JX_FWD_DEVICE_PTRS, JX_FWD_ASYNC, JX_FWD_FORCE_GEMV, JX_FWD_FORCE_MFMA, JX_FWD_RESIDUAL,  # noqa: F401
+                   JxError, LayerDesc, check, lib)
 
 _inited = {}
 
@@ -70,11 +70,14 @@ class MoELayer:
     def __init__(self, *, n_experts, top_k, d_model, d_ff, gate_type, up_type, down_type, router,
                  gate_exps, up_exps, down_exps, router_bias=None, d_ff_shared=0, sh_gate_type=None,
                  sh_up_type=None, sh_down_type=None, sh_gate=None, sh_up=None, sh_down=None,
-                 sh_gate_inp=None, activation: int = 0, router_type: int = F.F32, device: int = 0):
+                 sh_gate_inp=None, activation: int = 0, router_type: int = F.F32, ffn_norm=None,
+                 post_ffw_norm=None, rms_norm_eps: float = 1e-5, device: int = 0):
         init(device)
         keep = [np.ascontiguousarray(a) if a is not None else None
-                for a in (router, router_bias, gate_exps, up_exps, down_exps, sh_gate, sh_up, sh_down, sh_gate_inp)]
-        router, router_bias, gate_exps, up_exps, down_exps, sh_gate, sh_up, sh_down, sh_gate_inp = keep
+                for a in (router, router_bias, gate_exps, up_exps, down_exps, sh_gate, sh_up, sh_down, sh_gate_inp,
+                          ffn_norm, post_ffw_norm)]
+        (router, router_bias, gate_exps, up_exps, down_exps, sh_gate, sh_up, sh_down, sh_gate_inp, ffn_norm,
+         post_ffw_norm) = keep
         if router_type == F.F32:
             assert router.dtype == np.float32 and router.size == n_experts * d_model
         for name, a, t, rows, cols in (("gate", gate_exps, gate_type, d_ff, d_model),
@@ -86,10 +89,21 @@ class MoELayer:
         D = LayerDesc(n_experts, top_k, d_model, d_ff, gate_type, up_type, down_type,
                       _p(router), _p(router_bias), _p(gate_exps), _p(up_exps), _p(down_exps),
                       d_ff_shared, sh_gate_type or 0, sh_up_type or 0, sh_down_type or 0,
-                      _p(sh_gate), _p(sh_up), _p(sh_down), _p(sh_gate_inp), activation, router_type)
+                      _p(sh_gate), _p(sh_up), _p(sh_down), _p(sh_gate_inp), activation, router_type,
+                      _p(ffn_norm), _p(post_ffw_norm), rms_norm_eps)
         self.handle = C.c_void_p()
         check(lib().jx_moe_layer_create(C.byref(D), C.byref(self.handle)), "jx_moe_layer_create")
         self.E, self.k, self.d, self.F = n_experts, top_k, d_model, d_ff
+
+    @classmethod
+    def from_desc(cls, desc: LayerDesc, device: int = 0) -> "MoELayer":
+        """From a filled jx_moe_layer_desc (e.g. jxai_amd.gguf's binding of a model file)."""
+        init(device)
+        self = cls.__new__(cls)
+        self.handle = C.c_void_p()
+        check(lib().jx_moe_layer_create(C.byref(desc), C.byref(self.handle)), "jx_moe_layer_create")
+        self.E, self.k, self.d, self.F = desc.n_experts, desc.top_k, desc.d_model, desc.d_ff
+        return self
 
     @classmethod
     def from_weights(cls, lw, device: int = 0) -> "MoELayer":
@@ -102,10 +116,13 @@ class MoELayer:
                       sh_gate=lw.sh_gate, sh_up=lw.sh_up, sh_down=lw.sh_down, sh_gate_inp=lw.sh_gate_inp)
         return cls(n_experts=cfg.n_experts, top_k=cfg.top_k, d_model=cfg.d_model, d_ff=cfg.d_ff,
                    gate_type=gt, up_type=ut, down_type=dt, router=lw.router, router_bias=lw.router_bias,
-                   gate_exps=lw.gate, up_exps=lw.up, down_exps=lw.down, activation=cfg.act, device=device, **kw)
+                   gate_exps=lw.gate, up_exps=lw.up, down_exps=lw.down, activation=cfg.act,
+                   ffn_norm=lw.ffn_norm, post_ffw_norm=lw.post_ffw_norm, rms_norm_eps=cfg.rms_eps,
+                   device=device, **kw)
 
-    def forward(self, x: np.ndarray, regime: str | None = None):
-        """MoE block over host activations [n][d] -> (out [n][d], topk_ids, topk_w, counts)."""
+    def forward(self, x: np.ndarray, regime: str | None = None, residual: bool = False):
+        """MoE block over host activations [n][d] -> (out [n][d], topk_ids, topk_w, counts).
+        residual: x is the residual stream and out = x + the block on rms_norm(x) (JX_FWD_RESIDUAL)."""
         x = np.ascontiguousarray(x, dtype=np.float32)
         n = x.shape[0]
         out = np.empty((n, self.d), np.float32)
@@ -113,6 +130,7 @@ class MoELayer:
         w = np.empty((n, self.k), np.float32)
         counts = np.empty(self.E, np.int32)
         flags = {None: 0, "gemv": JX_FWD_FORCE_GEMV, "mfma": JX_FWD_FORCE_MFMA}[regime]
+        flags |= JX_FWD_RESIDUAL if residual else 0
         check(lib().jx_moe_forward(self.handle, _p(x), n, _p(out), _p(ids), _p(w), _p(counts), None, flags),
               "jx_moe_forward")
         return out, ids, w, counts

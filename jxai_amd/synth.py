@@ -146,6 +146,8 @@ class LayerConfig:
     shared_gate: bool = False
     zipf_gamma: float = 0.0
     act: int = 0  # gated activation: 0 SiLU, 1 GELU-tanh (the reference's use_gelu)
+    norms: bool = False  # ffn_norm and post_ffw_norm weights for the residual-stream form
+    rms_eps: float = 1e-5
     decode_tokens: tuple = field(default_factory=tuple)
     describe: str = ""
 
@@ -160,6 +162,9 @@ CONFIGS = {
     # the toy layer with the gemma family's GELU-tanh gate (the reference's use_gelu)
     "toy_gelu": LayerConfig("toy_gelu", 512, 8, 2, 1024, F.Q4_0, act=1, decode_tokens=(1, 64),
                             describe="Toy MoE FFN d512 E8 top-2 F1024 Q4_0, GELU-tanh gate"),
+    # the toy layer in its residual-stream form: ffn_norm before, post_ffw_norm and the residual add after
+    "toy_norm": LayerConfig("toy_norm", 512, 8, 2, 1024, F.Q4_0, norms=True, decode_tokens=(1, 64),
+                            describe="Toy MoE FFN d512 E8 top-2 F1024 Q4_0 with ffn_norm / post_ffw_norm"),
     "qwen15moe": LayerConfig("qwen15moe", 2048, 60, 4, 1408, F.Q4_0, d_ff_shared=5632,
                              shared_gate=True, decode_tokens=(1, 64),
                              describe="Qwen1.5-MoE-A2.7B-shaped d2048 E60 top-4 F1408 Q4_0 + shared 5632 (sigmoid gate)"),
@@ -195,6 +200,8 @@ class LayerWeights:
     sh_up: np.ndarray | None = None
     sh_down: np.ndarray | None = None
     sh_gate_inp: np.ndarray | None = None  # fp32 [d]
+    ffn_norm: np.ndarray | None = None      # fp32 [d]
+    post_ffw_norm: np.ndarray | None = None  # fp32 [d]
 
     @property
     def types(self):
@@ -218,6 +225,9 @@ def make_layer(cfg: LayerConfig, seed: int = BASE_SEED) -> LayerWeights:
         lw.sh_down = quant_matrix(s("down_shexp"), cfg.wtype, d, Fs)
         if cfg.shared_gate:
             lw.sh_gate_inp = normal_f32(s("gate_inp_shexp"), d, 0.02)
+    if cfg.norms:  # RMSNorm weights around 1
+        lw.ffn_norm = (1.0 + normal_f32(s("ffn_norm"), d, 0.1)).astype(np.float32)
+        lw.post_ffw_norm = (1.0 + normal_f32(s("post_ffw_norm"), d, 0.1)).astype(np.float32)
     return lw
 
 

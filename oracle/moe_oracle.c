@@ -481,6 +481,32 @@ void jxo_matmul_swiglu_quant_f32(int32_t gate_type, const uint8_t* Wg, int32_t u
     free(xq);
 }
 
+/* matmul_qkv_quant_f32 (src/quant.cpp:3924-3968): x quantized once when the
+ * given matrices (NULL ones skipped) hold 8 rows or more together and
+ * cols % 32 == 0; each row then takes the Q8_0 dot where its type allows. */
+void jxo_matmul_qkv_quant_f32(int32_t wq_type, const uint8_t* Wq, int64_t q_rows, float* q_out,
+                              int32_t wk_type, const uint8_t* Wk, int64_t k_rows, float* k_out,
+                              int32_t wv_type, const uint8_t* Wv, int64_t v_rows, float* v_out,
+                              const float* x, int64_t cols, int32_t order) {
+    const int64_t total = (Wq ? q_rows : 0) + (Wk ? k_rows : 0) + (Wv ? v_rows : 0);
+    if (total <= 0) return;
+    uint8_t* xq = NULL;
+    if (total >= 8 && cols % 32 == 0) {
+        xq = (uint8_t*)malloc((size_t)(cols / 32) * 34);
+        jxo_quantize_row_q8_0(x, xq, cols);
+    }
+    const int32_t types[3] = {wq_type, wk_type, wv_type};
+    const uint8_t* W[3] = {Wq, Wk, Wv};
+    const int64_t rows[3] = {q_rows, k_rows, v_rows};
+    float* outs[3] = {q_out, k_out, v_out};
+    for (int m = 0; m < 3; ++m) {
+        if (!W[m]) continue;
+        const int64_t rb = jxo_row_bytes(types[m], cols);
+        for (int64_t r = 0; r < rows[m]; ++r) outs[m][r] = row_dot(types[m], W[m] + r * rb, x, xq, cols, order);
+    }
+    free(xq);
+}
+
 /* ----------------------------------------------------------- routing -- */
 
 /* select_experts_cache_aware (src/tier.cpp:124-198) with CACHE_ROUTE off:
@@ -531,6 +557,15 @@ void jxo_route(const jxo_moe_desc* L, const float* x, int32_t n_tok,
     }
 }
 
+/* MoETransformerEngine::rms_norm (src/transformer.cpp:67-73): ss in
+ * vec_dot_f32's order, inv = 1 / sqrt(ss / size + eps), out = x * inv * w
+ * (w NULL: weight 1); out may alias x. */
+void jxo_rms_norm(float* out, const float* x, const float* weight, int64_t size, float eps) {
+    const float ss = jxo_vec_dot_f32(x, x, size);
+    const float inv = 1.0f / sqrtf((ss / (float)size) + eps);
+    for (int64_t i = 0; i < size; ++i) out[i] = x[i] * inv * (weight ? weight[i] : 1.0f);
+}
+
 /* ------------------------------------------------------- MoE block -- */
 
 /* One token through the MoE block (src/transformer.cpp:2589-2757, residual
@@ -579,16 +614,25 @@ int32_t jxo_moe_forward(const jxo_moe_desc* L, const float* x, int32_t n_tok,
     float* h = (float*)malloc(sizeof(float) * (size_t)fmax);
     float* y = (float*)malloc(sizeof(float) * (size_t)d);
     float* lg = (float*)malloc(sizeof(float) * (size_t)E);
+    float* xn = (float*)malloc(sizeof(float) * (size_t)d);
     const int32_t cnt = token_idx ? n_sel : n_tok;
     for (int32_t i = 0; i < cnt; ++i) {
         const int32_t t = token_idx ? token_idx[i] : i;
-        if (t < 0 || t >= n_tok) { free(h); free(y); free(lg); return -2; }
-        moe_token(L, x + (int64_t)t * d, out + (int64_t)i * d, topk_ids + (int64_t)i * k,
-                  topk_w + (int64_t)i * k, lg, order, h, y);
+        if (t < 0 || t >= n_tok) { free(h); free(y); free(lg); free(xn); return -2; }
+        const float* xt = x + (int64_t)t * d;
+        float* o = out + (int64_t)i * d;
+        if (L->residual) /* the FFN step of forward_token (transformer.cpp:2585-2764) */
+            jxo_rms_norm(xn, xt, L->ffn_norm, d, L->rms_eps);
+        moe_token(L, L->residual ? xn : xt, o, topk_ids + (int64_t)i * k, topk_w + (int64_t)i * k, lg, order, h, y);
+        if (L->residual) {
+            if (L->post_ffw_norm) jxo_rms_norm(o, o, L->post_ffw_norm, d, L->rms_eps);
+            for (int32_t j = 0; j < d; ++j) o[j] = xt[j] + o[j];
+        }
         if (logits) memcpy(logits + (int64_t)i * E, lg, sizeof(float) * (size_t)E);
     }
     free(h);
     free(y);
     free(lg);
+    free(xn);
     return 0;
 }

@@ -39,6 +39,10 @@ typedef struct {
     const uint8_t* sh_down;
     const float* sh_gate_inp;  /* [d] fp32 sigmoid gate, or NULL             */
     int32_t activation;        /* 0 SiLU, 1 GELU-tanh (the reference's use_gelu) */
+    const float* ffn_norm;     /* [d] fp32 or NULL (weight 1)                */
+    const float* post_ffw_norm;/* [d] fp32 or NULL (none)                    */
+    float rms_eps;
+    int32_t residual;          /* x is the residual stream: out = x + post(block(rms_norm(x))) */
 } jxo_moe_desc;
 
 uint16_t jxo_fp32_to_fp16(float f);
@@ -47,6 +51,7 @@ int64_t jxo_row_bytes(int32_t type, int64_t cols);
 void jxo_quantize_row_q8_0(const float* x, uint8_t* blocks, int64_t k);
 void jxo_dequantize_row(int32_t type, const uint8_t* w, float* y, int64_t k);
 float jxo_vec_dot_f32(const float* a, const float* b, int64_t k);
+void jxo_rms_norm(float* out, const float* x, const float* weight, int64_t size, float eps);
 float jxo_vec_dot_q8(int32_t type, const uint8_t* w, const uint8_t* xq8, int64_t k, int32_t order);
 float jxo_vec_dot_q4_K_f32(const uint8_t* w, const float* y, int64_t k);
 void jxo_matmul_quant_f32(int32_t type, const uint8_t* W, const float* x, float* out,
@@ -54,6 +59,10 @@ void jxo_matmul_quant_f32(int32_t type, const uint8_t* W, const float* x, float*
 void jxo_matmul_swiglu_quant_f32(int32_t gate_type, const uint8_t* Wg, int32_t up_type, const uint8_t* Wu,
                                  const float* x, float* out, int64_t exp_dim, int64_t cols, int32_t use_gelu,
                                  int32_t order);
+void jxo_matmul_qkv_quant_f32(int32_t wq_type, const uint8_t* Wq, int64_t q_rows, float* q_out,
+                              int32_t wk_type, const uint8_t* Wk, int64_t k_rows, float* k_out,
+                              int32_t wv_type, const uint8_t* Wv, int64_t v_rows, float* v_out,
+                              const float* x, int64_t cols, int32_t order);
 int32_t jxo_select_experts(const float* logits, int32_t n_experts, int32_t top_k,
                            int32_t* ids, float* probs);
 /* One MoE block over the tokens listed in token_idx (all n_tok when NULL). */

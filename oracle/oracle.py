@@ -34,6 +34,7 @@ class MoeDesc(C.Structure):
         ("sh_gate", _u8), ("sh_up", _u8), ("sh_down", _u8),
         ("sh_gate_inp", _fp),
         ("activation", C.c_int32),
+        ("ffn_norm", _fp), ("post_ffw_norm", _fp), ("rms_eps", C.c_float), ("residual", C.c_int32),
     ]
 
 
@@ -157,6 +158,26 @@ class Oracle:
                                                  _ptr(out, _fp), exp_dim, cols, int(use_gelu))
         return out
 
+    def matmul_qkv_quant_f32(self, mats, x) -> list:
+        """mats: three (type, W bytes, rows) or None; returns the three outputs (None for absent)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        args, outs = [], []
+        for m in mats:
+            if m is None:
+                args += [0, None, 0, None]
+                outs.append(None)
+            else:
+                t, W, rows = m
+                W = np.ascontiguousarray(W, dtype=np.uint8)
+                o = np.zeros(rows, np.float32)
+                args += [t, _ptr(W, _u8), rows, _ptr(o, _fp)]
+                outs.append((o, W))
+        fn = getattr(self.lib, self.p + "matmul_qkv_quant_f32")
+        fn.argtypes = [C.c_int32, _u8, C.c_int64, _fp] * 3 + [_fp, C.c_int64] + ([C.c_int32] if self.kind == "port" else [])
+        extra = [self.order] if self.kind == "port" else []
+        fn(*args, _ptr(x, _fp), x.size, *extra)
+        return [None if o is None else o[0] for o in outs]
+
     def select_experts(self, logits, k: int):
         logits = np.ascontiguousarray(logits, dtype=np.float32)
         ids = np.zeros(k, dtype=np.int32)
@@ -185,10 +206,20 @@ class Oracle:
                     P(lw.gate, _u8), P(lw.up, _u8), P(lw.down, _u8),
                     cfg.d_ff_shared, gt, ut, dt,
                     P(lw.sh_gate, _u8), P(lw.sh_up, _u8), P(lw.sh_down, _u8),
-                    P(lw.sh_gate_inp, _fp), cfg.act)
+                    P(lw.sh_gate_inp, _fp), cfg.act, P(lw.ffn_norm, _fp), P(lw.post_ffw_norm, _fp),
+                    cfg.rms_eps, 0)
         return D, keep
 
-    def moe_forward(self, lw, x: np.ndarray, token_idx=None, threads: int = 0):
+    def rms_norm(self, x, w, eps: float) -> np.ndarray:
+        """MoETransformerEngine::rms_norm of one row (port only)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros_like(x)
+        wp = None if w is None else np.ascontiguousarray(w, dtype=np.float32)
+        self.lib.jxo_rms_norm.argtypes = [_fp, _fp, _fp, C.c_int64, C.c_float]
+        self.lib.jxo_rms_norm(_ptr(out, _fp), _ptr(x, _fp), _ptr(wp, _fp), x.size, eps)
+        return out
+
+    def moe_forward(self, lw, x: np.ndarray, token_idx=None, threads: int = 0, residual: bool = False):
         """Run the MoE block for ``token_idx`` (all tokens when None).
 
         Returns (out [m][d], topk_ids [m][k], topk_w [m][k], logits [m][E])."""
@@ -202,6 +233,7 @@ class Oracle:
         w = np.zeros((m, cfg.top_k), dtype=np.float32)
         lg = np.zeros((m, cfg.n_experts), dtype=np.float32)
         D, keep = self.desc(lw)
+        D.residual = 1 if residual else 0
         if self.kind == "port":
             if threads:
                 self.lib.jxo_set_threads(threads)

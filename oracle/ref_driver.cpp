@@ -9,11 +9,13 @@
 // CPU path on the GPU host.  No reference source is copied: the MoE-block
 // sequence below replays src/transformer.cpp:2589-2757 by calling the
 // reference's own functions.
+#include <cmath>
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
 #include <vector>
 
+#include "gguf.h"
 #include "quant.h"
 #include "tier.h"
 
@@ -60,6 +62,13 @@ void jxr_matmul_swiglu_quant_f32(int32_t gt, const uint8_t* Wg, int32_t ut, cons
                                  x, out, exp_dim, cols, use_gelu != 0);
 }
 
+void jxr_matmul_qkv_quant_f32(int32_t qt, const uint8_t* Wq, int64_t q_rows, float* q_out, int32_t kt,
+                              const uint8_t* Wk, int64_t k_rows, float* k_out, int32_t vt, const uint8_t* Wv,
+                              int64_t v_rows, float* v_out, const float* x, int64_t cols) {
+    moe::matmul_qkv_quant_f32(static_cast<GGMLType>(qt), Wq, q_rows, q_out, static_cast<GGMLType>(kt), Wk, k_rows,
+                              k_out, static_cast<GGMLType>(vt), Wv, v_rows, v_out, x, cols);
+}
+
 // select_experts_cache_aware with CACHE_ROUTE off (eps = 0, nothing resident).
 int32_t jxr_select_experts(const float* logits, int32_t E, int32_t k, int32_t* ids, float* probs) {
     moe::LFRUTierManager tier;
@@ -70,6 +79,41 @@ int32_t jxr_select_experts(const float* logits, int32_t E, int32_t k, int32_t* i
         probs[i] = sel[i].prob;
     }
     return static_cast<int32_t>(sel.size());
+}
+
+// ModelFile::open on a GGUF file (src/gguf.cpp), for checking the library's
+// parser: the tensor count, then per name its type, dims, absolute offset and
+// byte size, and metadata through get_u32 / get_f32.
+void* jxr_gguf_open(const char* path) {
+    auto* mf = new moe::ModelFile();
+    std::string err;
+    if (!mf->open(path, err)) {
+        delete mf;
+        return nullptr;
+    }
+    return mf;
+}
+void jxr_gguf_close(void* mf) { delete static_cast<moe::ModelFile*>(mf); }
+int64_t jxr_gguf_tensor_count(void* mf) { return (int64_t)static_cast<moe::ModelFile*>(mf)->tensor_names().size(); }
+const char* jxr_gguf_tensor_name(void* mf, int64_t i) {
+    return static_cast<moe::ModelFile*>(mf)->tensor_names()[(size_t)i].c_str();
+}
+int32_t jxr_gguf_tensor(void* mf, const char* name, int32_t* type, int32_t* n_dims, uint64_t* dims,
+                        uint64_t* abs_offset, uint64_t* byte_size) {
+    const auto* t = static_cast<moe::ModelFile*>(mf)->find_tensor(name);
+    if (!t) return -1;
+    *type = static_cast<int32_t>(t->type);
+    *n_dims = static_cast<int32_t>(t->n_dims);
+    for (int d = 0; d < 4; ++d) dims[d] = t->dims[d];
+    *abs_offset = t->abs_file_offset;
+    *byte_size = t->byte_size;
+    return 0;
+}
+uint32_t jxr_gguf_get_u32(void* mf, const char* key, uint32_t def) {
+    return static_cast<moe::ModelFile*>(mf)->get_u32(key, def);
+}
+float jxr_gguf_get_f32(void* mf, const char* key, float def) {
+    return static_cast<moe::ModelFile*>(mf)->get_f32(key, def);
 }
 
 // The counters select_experts_cache_aware leaves in LFRUTierManager
@@ -95,6 +139,15 @@ int32_t jxr_tier_replay(const float* logits, int32_t n_tok, int32_t E, int32_t k
         last_prob[flat] = e.last_prob;
     }
     return static_cast<int32_t>(snap.size());
+}
+
+// MoETransformerEngine::rms_norm (transformer.cpp:67-73) is a member of the
+// engine, whose translation unit needs the whole engine; its three steps around
+// the reference's own vec_dot_f32, for the residual-stream form below.
+static void ref_rms_norm(float* out, const float* x, const float* w, int64_t size, float eps) {
+    const float ss = moe::vec_dot_f32(x, x, size);
+    const float inv_rms = 1.0f / std::sqrt((ss / static_cast<float>(size)) + eps);
+    for (int64_t i = 0; i < size; ++i) out[i] = x[i] * inv_rms * (w ? w[i] : 1.0f);
 }
 
 // The MoE block of forward_token (transformer.cpp:2589-2757) for the listed
@@ -123,7 +176,10 @@ int32_t jxr_moe_forward(const jxo_moe_desc* L, const float* x, int32_t n_tok,
     for (int32_t i = 0; i < cnt; ++i) {
         const int32_t t = token_idx ? token_idx[i] : i;
         if (t < 0 || t >= n_tok) return -2;
-        const float* xn = x + static_cast<size_t>(t) * d;
+        const float* xt = x + static_cast<size_t>(t) * d;
+        std::vector<float> xnorm(d);
+        if (L->residual) ref_rms_norm(xnorm.data(), xt, L->ffn_norm, d, L->rms_eps);  // 2585-2587
+        const float* xn = L->residual ? xnorm.data() : xt;
 
         std::fill(logits.begin(), logits.end(), 0.0f);
         moe::matmul_quant_f32(GGMLType::F32, L->router, xn, logits.data(), E, d);
@@ -156,6 +212,10 @@ int32_t jxr_moe_forward(const jxo_moe_desc* L, const float* x, int32_t n_tok,
                 sh_scale = 1.0f / (1.0f + std::exp(-g_val));
             }
             for (uint32_t j = 0; j < d; ++j) moe_accum[j] += sh_scale * down_buf[j];
+        }
+        if (L->residual) {
+            if (L->post_ffw_norm) ref_rms_norm(moe_accum.data(), moe_accum.data(), L->post_ffw_norm, d, L->rms_eps);
+            for (uint32_t j = 0; j < d; ++j) moe_accum[j] = xt[j] + moe_accum[j];  // 2762-2764
         }
         std::memcpy(out + static_cast<size_t>(i) * d, moe_accum.data(), sizeof(float) * d);
         if (logits_out) std::memcpy(logits_out + static_cast<size_t>(i) * E, logits.data(), sizeof(float) * E);

@@ -45,6 +45,11 @@ CASES = [
     ("toy_gelu", 1, [0]),
     ("toy_gelu", 64, ("tiles", 32, 0)),
 ]
+# the residual-stream form (rms_norm before, post_ffw_norm and the residual add after the block)
+RESID_CASES = [
+    ("toy_norm", 1, [0]),
+    ("toy_norm", 64, ("tiles", 32, 0)),
+]
 
 
 def covering_rows(ids: np.ndarray, n_experts: int, g_routed: int, g_shared: int) -> list[int]:
@@ -87,15 +92,24 @@ def layer_digest(lw) -> str:
                   lw.sh_gate, lw.sh_up, lw.sh_down, lw.sh_gate_inp)
 
 
-def make_case(ref: Oracle, name: str, n: int, rows, tag: str = "") -> str:
+def make_case(ref: Oracle, name: str, n: int, rows, tag: str = "", residual: bool = False) -> str:
     cfg = synth.CONFIGS[name]
     lw = synth.make_layer(cfg)
     x = synth.make_tokens(cfg, n)
+    # the router sees rms_norm(x) in the residual form (restated from transformer.cpp:67-73 on the
+    # reference build's own vec_dot_f32)
+    xr = x
+    if residual:
+        xr = np.empty_like(x)
+        for t in range(n):
+            ss = np.float32(ref.vec_dot_f32(x[t], x[t]))
+            inv = np.float32(1.0) / np.sqrt(ss / np.float32(cfg.d_model) + np.float32(cfg.rms_eps))
+            xr[t] = x[t] * inv * lw.ffn_norm
     ids_all = np.zeros((n, cfg.top_k), np.int32)
     w_all = np.zeros((n, cfg.top_k), np.float32)
     lg_all = np.zeros((n, cfg.n_experts), np.float32)
     for t in range(n):
-        logits = ref.matmul_quant_f32(F.F32, lw.router.view(np.uint8).reshape(-1), x[t],
+        logits = ref.matmul_quant_f32(F.F32, lw.router.view(np.uint8).reshape(-1), xr[t],
                                       cfg.n_experts, cfg.d_model)
         if lw.router_bias is not None:
             logits = (logits + lw.router_bias).astype(np.float32)
@@ -104,13 +118,13 @@ def make_case(ref: Oracle, name: str, n: int, rows, tag: str = "") -> str:
     if isinstance(rows, tuple):  # ("tiles", routed, shared): rows covering every tile of the dispatch
         rows = covering_rows(ids_all, cfg.n_experts, rows[1], rows[2])
     # full MoE-block outputs for `rows`
-    out, ids_r, w_r, lg_r = ref.moe_forward(lw, x, np.asarray(rows, dtype=np.int32))
+    out, ids_r, w_r, lg_r = ref.moe_forward(lw, x, np.asarray(rows, dtype=np.int32), residual=residual)
     assert np.array_equal(ids_all[rows], ids_r) and np.array_equal(w_all[rows].view(np.uint32), w_r.view(np.uint32))
     counts = np.bincount(ids_all.reshape(-1), minlength=cfg.n_experts).astype(np.int32)
     path = os.path.join(OUT, f"{name}_n{n}{tag}.npz")
     np.savez_compressed(
         path,
-        config=name, n=n, rows=np.asarray(rows, np.int32),
+        config=name, n=n, rows=np.asarray(rows, np.int32), residual=residual,
         out=out, topk_ids=ids_all, topk_w=w_all, logits_rows=lg_all[rows], counts=counts,
         layer_sha256=layer_digest(lw), x_sha256=digest(x),
     )
@@ -161,8 +175,54 @@ def make_units(ref: Oracle) -> str:
     return path
 
 
+TOY_GGUF = "/root/reference/models/qwen_run.gguf"
+
+
+def make_gguf_case(ref: Oracle) -> str:
+    """Layer 0 of the reference's toy model file (models/qwen_run.gguf, written by its
+    src/model_forge.cpp:135-339): the layer's tensors as stored in the file (router F32 [128, 8],
+    Q4_0 experts [128, 128, 8], ffn_norm) with their metadata, seeded tokens, and the reference
+    build's MoE block on them -- the fixture the GPU test rebuilds a GGUF file from."""
+    from jxai_amd.gguf import GGUFFile
+    f = GGUFFile(TOY_GGUF)
+    names = ["blk.0.ffn_gate_inp.weight", "blk.0.ffn_gate_exps.weight", "blk.0.ffn_up_exps.weight",
+             "blk.0.ffn_down_exps.weight", "blk.0.ffn_norm.weight"]
+    t = f.tensors()
+    kw = {}
+    for i, nm in enumerate(names):
+        kw[f"t{i}_name"] = nm
+        kw[f"t{i}_dims"] = np.array(t[nm]["dims"][: t[nm]["n_dims"]], np.int64)
+        kw[f"t{i}_type"] = t[nm]["type"]
+        kw[f"t{i}_bytes"] = f.tensor_bytes(nm)
+    arch = f.get_str("general.architecture")
+    meta = {"arch": arch, "top_k": f.get_u32(f"{arch}.expert_used_count"),
+            "n_experts": f.get_u32(f"{arch}.expert_count"),
+            "eps": f.get_f32(f"{arch}.attention.layer_norm_rms_epsilon")}
+    d, E, Fd = 128, 8, 128
+    cfg = synth.LayerConfig("qwen_run_l0", d, E, meta["top_k"], Fd, F.Q4_0)
+    lw = synth.LayerWeights(cfg, kw["t0_bytes"].view(np.float32).reshape(E, d).copy(), None, kw["t1_bytes"],
+                            kw["t2_bytes"], kw["t3_bytes"])
+    n = 64
+    x = synth.make_tokens(cfg, n, seed=5)
+    out, ids, w, lg = ref.moe_forward(lw, x)
+    f.close()
+    path = os.path.join(OUT, "qwen_run_layer0.npz")
+    np.savez_compressed(path, n_tensors=len(names), arch=arch, top_k=meta["top_k"], n_experts=meta["n_experts"],
+                        eps=np.float32(meta["eps"]), x=x, out=out, topk_ids=ids, topk_w=w, logits=lg,
+                        file_sha256=hashlib.sha256(open(TOY_GGUF, "rb").read()).hexdigest(), **kw)
+    return path
+
+
 def main() -> None:
     build(ref=True)
+    if "--gguf" in sys.argv:  # only the toy-model fixture
+        print(make_gguf_case(Oracle("reference", avx512=False)))
+        return
+    if "--resid" in sys.argv:  # only the residual-stream cases
+        ref = Oracle("reference", avx512=False)
+        for name, n, rows in RESID_CASES:
+            print(make_case(ref, name, n, rows, tag="_resid", residual=True))
+        return
     if "--avx512-child" in sys.argv:
         ref = Oracle("reference", avx512=True)
         print(make_case(ref, "toy", 1, [0], tag="_avx512"))
@@ -170,8 +230,11 @@ def main() -> None:
         return
     ref = Oracle("reference", avx512=False)
     print(make_units(ref))
+    print(make_gguf_case(ref))
     for name, n, rows in CASES:
         print(make_case(ref, name, n, rows))
+    for name, n, rows in RESID_CASES:
+        print(make_case(ref, name, n, rows, tag="_resid", residual=True))
     subprocess.run([sys.executable, os.path.abspath(__file__), "--avx512-child"], check=True)
 
 

@@ -43,6 +43,10 @@ EXTRA = {
     # MFMA pair tile (j % 64 // 32) and its part of the 128-pair dispatch tile (j % 128 // 64)
     "e2_mixtral": synth.LayerConfig("e2_mixtral", 4096, 2, 2, 2048, F.Q4_K),
     "e2_dsv2lite": synth.LayerConfig("e2_dsv2lite", 2048, 2, 2, 1408, F.Q4_K),
+    # the residual-stream form with a shared expert (split router rows) and a Mixtral-sized d_model
+    "qwen15_norm": synth.LayerConfig("qwen15_norm", 512, 12, 4, 384, F.Q4_0, d_ff_shared=768, shared_gate=True,
+                                     norms=True),
+    "mixtral_norm": synth.LayerConfig("mixtral_norm", 4096, 8, 2, 1024, F.Q4_K, norms=True),
 }
 
 
@@ -95,7 +99,8 @@ def test_matmul_swiglu_quant_f32(moe, port, qt, rows, cols, use_gelu):
 
 # ------------------------------------------------------------------ layer vs the golden vectors
 GOLDEN_CASES = ["toy_n1", "qwen15moe_n1", "qwen15moe_n64", "mixtral_n1", "mixtral_n512", "mixtral_n2048",
-                "qwen3moe_n2048", "dsv2lite_n32", "toy_gelu_n1", "toy_gelu_n64"]
+                "qwen3moe_n2048", "dsv2lite_n32", "toy_gelu_n1", "toy_gelu_n64", "toy_norm_n1_resid",
+                "toy_norm_n64_resid"]
 
 
 @pytest.mark.parametrize("case", GOLDEN_CASES)
@@ -107,7 +112,7 @@ def test_layer_vs_golden(moe, case):
     x = synth.make_tokens(cfg, n)
     L = moe.MoELayer.from_weights(lw)
     say(f"layer {case}: forward")
-    out, ids, w, counts = L.forward(x)
+    out, ids, w, counts = L.forward(x, residual=bool(z["residual"]))
     assert np.array_equal(ids, z["topk_ids"]), "routing differs"
     assert np.array_equal(counts, z["counts"])
     np.testing.assert_allclose(w, z["topk_w"], rtol=2e-6, atol=0)
@@ -506,3 +511,94 @@ def test_compiled_caller(moe, port, tmp_path):
     assert np.array_equal(ids, ids_o)
     assert rel_err(o, want) <= REL_TOL
     L.close()
+
+
+def test_gguf_toy_layer_on_gpu(moe, tmp_path):
+    """Layer 0 of the reference's toy model (models/qwen_run.gguf), rebuilt as a GGUF file from the
+    committed fixture, through the loader (jx_gguf_open, jx_gguf_moe_layer_desc) and one upload
+    (jx_moe_layer_create): routing exact and outputs within the bar against the reference build, one
+    token (decode) and 64 (matrix-core GEMMs)."""
+    from jxai_amd.gguf import GGUFFile
+    from tests.test_gguf import fixture_file
+    path = str(tmp_path / "l0.gguf")
+    z = fixture_file(path)
+    f = GGUFFile(path)
+    L = f.moe_layer(0)
+    f.close()  # the layer holds its own device copy
+    for n, regime in ((1, None), (2, None), (64, None), (64, "gemv")):
+        say(f"gguf toy layer n={n} regime={regime}")
+        out, ids, w, counts = L.forward(z["x"][:n], regime=regime)
+        assert np.array_equal(ids, z["topk_ids"][:n])
+        np.testing.assert_allclose(w, z["topk_w"][:n], rtol=2e-6, atol=0)
+        err = rel_err(out, z["out"][:n])
+        say(f"gguf toy layer n={n}: max rel err {err:.2e}")
+        assert err <= REL_TOL
+    L.close()
+
+
+@pytest.mark.parametrize("name,n,regime", [("toy_norm", 1, None), ("toy_norm", 2, None), ("toy_norm", 40, "gemv"),
+                                           ("toy_norm", 300, "mfma"), ("qwen15_norm", 1, None),
+                                           ("qwen15_norm", 70, None), ("qwen15_norm", 700, None),
+                                           ("mixtral_norm", 1, None), ("mixtral_norm", 2, None),
+                                           ("mixtral_norm", 200, "mfma")])
+def test_residual_form_vs_oracle(moe, port, name, n, regime):
+    """JX_FWD_RESIDUAL: rms_norm(x, ffn_norm) feeds the router (routing exact), the combine applies
+    post_ffw_norm and adds x, against the oracle's forward_token FFN step."""
+    say(f"residual {name} n={n} regime={regime}")
+    cfg, lw = layer(name)
+    x = synth.make_tokens(cfg, n, seed=17)
+    L = moe.MoELayer.from_weights(lw)
+    out, ids, w, counts = L.forward(x, regime=regime, residual=True)
+    sel = np.unique(np.linspace(0, n - 1, min(n, 6)).astype(np.int32))
+    want, ids_o, w_o, _ = port.moe_forward(lw, x, sel, residual=True)
+    assert np.array_equal(ids[sel], ids_o)
+    np.testing.assert_allclose(w[sel], w_o, rtol=2e-6, atol=0)
+    err = rel_err(out[sel], want)
+    say(f"residual {name} n={n}: max rel err {err:.2e}")
+    assert err <= REL_TOL
+    # in place: out aliasing x, through device pointers
+    xb = moe.DeviceBuffer(x.nbytes).upload(x)
+    from jxai_amd._lib import JX_FWD_DEVICE_PTRS, JX_FWD_RESIDUAL
+    flags = JX_FWD_DEVICE_PTRS | JX_FWD_RESIDUAL | {None: 0, "gemv": 1 << 2, "mfma": 1 << 3}[regime]
+    assert moe.lib().jx_moe_forward(L.handle, xb.ptr, n, xb.ptr, None, None, None, None, flags) == 0
+    got = xb.download(np.empty_like(x))
+    assert np.array_equal(got.view(np.uint32), out.view(np.uint32))
+    xb.free()
+    L.close()
+
+
+@pytest.mark.parametrize("types,cols,rows", [((F.Q4_K, F.Q4_0, F.Q8_0), 512, (256, 4, 4)),
+                                             ((F.Q4_K, F.Q4_K, F.Q4_K), 1408, (64, 32, 32)),
+                                             ((F.Q4_K, F.Q4_K, F.Q4_K), 256, (2, 2, 2)),
+                                             ((F.Q4_0, F.Q4_K, None), 2048, (1024, 512, 0))])
+def test_dense_device_dropins(moe, port, types, cols, rows):
+    """jx_matmul_qkv_quant_f32_dev and jx_matmul_quant_f32_dev on device pointers against the oracle's
+    matmul_qkv_quant_f32 / matmul_quant_f32 (same integer block sums; fp32 order differs)."""
+    say(f"dense drop-ins {types} cols={cols} rows={rows}")
+    mats = [None if t is None else (t, synth.quant_matrix(synth.sub_seed("qkvg", f"{i}{cols}"), t, r, cols), r)
+            for i, (t, r) in enumerate(zip(types, rows))]
+    x = synth.normal_f32(synth.sub_seed("qkvg", f"x{cols}"), cols, 1.0)
+    want = port.matmul_qkv_quant_f32(mats, x)
+    qm = [None if m is None else moe.QMatrix(m[0], m[1], m[2], cols) for m in mats]
+    xb = moe.DeviceBuffer(x.nbytes).upload(x)
+    outs = [None if m is None else moe.DeviceBuffer(m[2] * 4) for m in mats]
+    h = lambda o: None if o is None else o.handle  # noqa: E731
+    p = lambda o: None if o is None else o.ptr  # noqa: E731
+    assert moe.lib().jx_matmul_qkv_quant_f32_dev(h(qm[0]), h(qm[1]), h(qm[2]), xb.ptr, p(outs[0]), p(outs[1]),
+                                                  p(outs[2]), None) == 0, moe.lib().jx_moe_last_error()
+    moe.lib().jx_device_synchronize()
+    for m, o, w in zip(mats, outs, want):
+        if m is None:
+            continue
+        got = o.download(np.empty(m[2], np.float32))
+        assert np.abs(got - w).max() <= 1e-5 * np.abs(w).max()
+        # the single-matrix drop-in on the first matrix's own rule
+    m0 = mats[0]
+    w0 = port.matmul_quant_f32(m0[0], m0[1], x, m0[2], cols)
+    assert moe.lib().jx_matmul_quant_f32_dev(qm[0].handle, xb.ptr, outs[0].ptr, None) == 0
+    moe.lib().jx_device_synchronize()
+    got0 = outs[0].download(np.empty(m0[2], np.float32))
+    assert np.abs(got0 - w0).max() <= 1e-5 * np.abs(w0).max()
+    for m in qm:
+        if m is not None:
+            m.close()

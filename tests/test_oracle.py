@@ -216,6 +216,65 @@ def test_dequantize_row(port, qt, cols):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("d,scale,weighted", [(512, 1.0, True), (4096, 3.0, True), (128, 1e-3, False), (2048, 0.0, True)])
+def test_rms_norm(port, ref, d, scale, weighted):
+    """MoETransformerEngine::rms_norm (transformer.cpp:67-73): against the same three steps in
+    float32 on the reference build's own vec_dot_f32 (bit for bit: IEEE division and square root),
+    and against a float64 closed form (a few ulp)."""
+    x = (synth.normal_f32(synth.sub_seed("rms", f"{d}_{scale}"), d, 1.0) * np.float32(scale)).astype(np.float32)
+    w = (1.0 + synth.normal_f32(synth.sub_seed("rmsw", str(d)), d, 0.1)).astype(np.float32) if weighted else None
+    eps = np.float32(1e-5)
+    got = port.rms_norm(x, w, float(eps))
+    ss = np.float32(ref.vec_dot_f32(x, x))
+    inv = np.float32(1.0) / np.sqrt(ss / np.float32(d) + eps)
+    want = x * inv * (w if w is not None else np.float32(1.0))
+    assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
+    x64 = x.astype(np.float64)
+    exact = x64 / np.sqrt((x64 @ x64) / d + 1e-5) * (w.astype(np.float64) if w is not None else 1.0)
+    assert np.abs(got - exact).max() <= 4 * np.finfo(np.float32).eps * max(np.abs(exact).max(), 1e-30)
+
+
+@pytest.mark.parametrize("name", ["toy_norm", "qwen15_norm"])
+def test_moe_block_residual_live_vs_reference(port, ref, name):
+    """The residual-stream form (rms_norm, block, post_ffw_norm, residual add) bit-exact against the
+    reference build's functions."""
+    cfg = RESID_CFGS[name]
+    lw = synth.make_layer(cfg, seed=5)
+    x = synth.make_tokens(cfg, 5, seed=5)
+    a = port.moe_forward(lw, x, residual=True)
+    b = ref.moe_forward(lw, x, residual=True)
+    for u, v in zip(a, b):
+        assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
+    plain = port.moe_forward(lw, x)[0]
+    assert not np.array_equal(a[0], plain)
+
+
+RESID_CFGS = {
+    "toy_norm": synth.CONFIGS["toy_norm"],
+    "qwen15_norm": synth.LayerConfig("qwen15_norm", 512, 12, 4, 384, F.Q4_0, d_ff_shared=768, shared_gate=True,
+                                     norms=True),
+}
+
+
+QKV_CASES = [((F.Q4_K, F.Q4_0, F.Q8_0), 512, (256, 4, 4)),   # k, v alone under 8 rows: x quantized for all
+             ((F.Q4_K, F.Q4_K, F.Q4_K), 1408, (64, 32, 32)),  # cols % 256 != 0: fp32 Q4_K dots
+             ((F.Q4_K, F.Q4_K, F.Q4_K), 256, (2, 2, 2))]      # 6 rows in all: no quantization
+
+
+@pytest.mark.parametrize("types,cols,rows", QKV_CASES)
+def test_qkv_live_vs_reference(port, ref, types, cols, rows):
+    """matmul_qkv_quant_f32 (src/quant.cpp:3924-3968) bit-exact against the reference build."""
+    mats = [(t, synth.quant_matrix(synth.sub_seed("qkv", f"{i}{cols}"), t, r, cols), r)
+            for i, (t, r) in enumerate(zip(types, rows))]
+    x = synth.normal_f32(synth.sub_seed("qkv", f"x{cols}"), cols, 1.0)
+    for u, v in zip(port.matmul_qkv_quant_f32(mats, x), ref.matmul_qkv_quant_f32(mats, x)):
+        assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
+    # the k and v rows of the first case take the Q8_0 dot as part of the q/k/v set, unlike alone
+    if rows[1] < 8 and sum(rows) >= 8 and cols % 32 == 0:
+        alone = port.matmul_quant_f32(types[2], mats[2][1], x, rows[2], cols) if types[2] == F.Q4_K else None
+        assert alone is None or not np.array_equal(alone, port.matmul_qkv_quant_f32(mats, x)[2])
+
+
 # --------------------------------------------------------------- top-k + softmax
 @pytest.mark.parametrize("E,k", [(8, 2), (60, 4), (128, 8), (64, 6), (5, 5)])
 def test_select_experts_bruteforce(port, E, k):
@@ -242,7 +301,8 @@ def test_select_experts_live_vs_reference(port, ref):
 
 # --------------------------------------------------------------- whole MoE block vs the golden vectors
 GOLDEN_CASES = ["toy_n1", "qwen15moe_n1", "qwen15moe_n64", "mixtral_n1", "mixtral_n512",
-                "mixtral_n2048", "qwen3moe_n2048", "dsv2lite_n32", "toy_gelu_n1", "toy_gelu_n64"]
+                "mixtral_n2048", "qwen3moe_n2048", "dsv2lite_n32", "toy_gelu_n1", "toy_gelu_n64",
+                "toy_norm_n1_resid", "toy_norm_n64_resid"]
 
 
 def _layer(name, n):
@@ -259,13 +319,14 @@ def test_moe_block_golden(port, case):
     assert layer_digest(lw) == str(z["layer_sha256"]), "synthetic generator drifted"
     assert digest(x) == str(z["x_sha256"]), "synthetic generator drifted"
     # routing of every token: bit-exact ids, order, probabilities and counts
-    lg, ids, w = port.route(lw, x)
+    xr = np.stack([port.rms_norm(v, lw.ffn_norm, cfg.rms_eps) for v in x]) if bool(z["residual"]) else x
+    lg, ids, w = port.route(lw, xr)
     assert np.array_equal(ids, z["topk_ids"])
     assert np.array_equal(w.view(np.uint32), z["topk_w"].view(np.uint32))
     assert np.array_equal(np.bincount(ids.reshape(-1), minlength=cfg.n_experts), z["counts"])
     assert int(z["counts"].sum()) == n * cfg.top_k
     # full block output for the stored rows
-    out, ids_r, w_r, lg_r = port.moe_forward(lw, x, z["rows"])
+    out, ids_r, w_r, lg_r = port.moe_forward(lw, x, z["rows"], residual=bool(z["residual"]))
     assert np.array_equal(out.view(np.uint32), z["out"].view(np.uint32))
     assert np.array_equal(lg_r.view(np.uint32), z["logits_rows"].view(np.uint32))
 
