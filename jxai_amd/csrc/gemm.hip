@@ -227,9 +227,10 @@ struct WRaw<T_Q4_K> {
     }
     // PAR: the parity of h (even half-units carry the header, odd ones the min pieces), so each of the
     // two alternating register sets holds only the fields its parity uses
+    __device__ static uint32_t xoff(const QMat&, int, int, int) { return 0; }
     template <int PAR>
-    __device__ void load(const uint8_t* qb, const uint8_t* sb, const uint8_t* mb, uint32_t qo, uint32_t so,
-                         uint32_t mo, int h, int nb) {
+    __device__ void load(const uint8_t* qb, const uint8_t* sb, const uint8_t* mb, const uint8_t*, uint32_t qo,
+                         uint32_t so, uint32_t mo, uint32_t, int h, int nb) {
         (void)nb;
         static_assert(PAR == 0 || PAR == 1, "parity");
         const uint8_t* qh = qb + (size_t)(h >> 1) * 4096 + PAR * 2048;
@@ -245,31 +246,88 @@ struct WRaw<T_Q4_K> {
     }
 };
 
+// Q5_K: the Q4_K fields plus the lane's chunk of fifth bits (qh bytes 16g..16g+15, bit j = sub-block j),
+// loaded with every half-unit.
+template <>
+struct WRaw<T_Q5_K> : WRaw<T_Q4_K> {
+    uint4 qh;
+    __device__ static uint32_t xoff(const QMat& W, int rt, int n, int g) {
+        return (uint32_t)((((size_t)rt * W.nkb * 2 + g) * 32 + n) * 16);
+    }
+    template <int PAR>
+    __device__ void load(const uint8_t* qb, const uint8_t* sb, const uint8_t* mb, const uint8_t* xb, uint32_t qo,
+                         uint32_t so, uint32_t mo, uint32_t xo, int h, int nb) {
+        WRaw<T_Q4_K>::template load<PAR>(qb, sb, mb, xb, qo, so, mo, xo, h, nb);
+        qh = ld16(xb + (size_t)(h >> 1) * 1024 + xo);
+    }
+};
+
+// Q6_K: half-unit h is 128-element half h & 1 of super-block h / 2; lane (n, g) takes elements
+// 16g..16g+15 of its four 32-blocks: ql chunks g and 2 + g and qh chunk 4 + g of that half; the 16
+// int8 scales and d of row n come with the even half-unit.
+template <>
+struct WRaw<T_Q6_K> {
+    uint4 q[3];
+    uint4 sc;
+    uint32_t d;
+    __device__ static uint32_t qoff(const QMat& W, int rt, int n, int g) {
+        return (uint32_t)((size_t)rt * W.nkb * 6144 + g * 512 + n * 16);
+    }
+    __device__ static uint32_t soff(const QMat& W, int rt, int n) {
+        return (uint32_t)(((size_t)rt * W.nkb * 32 + n) * 16);
+    }
+    __device__ static uint32_t moff(const QMat&, int, int) { return 0; }
+    __device__ static uint32_t xoff(const QMat& W, int rt, int n, int) {
+        return (uint32_t)(((size_t)rt * W.nkb * 32 + n) * 2);
+    }
+    template <int PAR>
+    __device__ void load(const uint8_t* qb, const uint8_t* sb, const uint8_t*, const uint8_t* xb, uint32_t qo,
+                         uint32_t so, uint32_t, uint32_t xo, int h, int nb) {
+        (void)nb;
+        const uint8_t* base = qb + (size_t)(h >> 1) * 6144 + (h & 1) * 3072 + qo;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) q[c] = ld16(base + c * 1024);
+        if (PAR == 0) {
+            sc = ld16(sb + (size_t)(h >> 1) * 512 + so);
+            d = *reinterpret_cast<const uint16_t*>(xb + (size_t)(h >> 1) * 64 + xo);
+        }
+    }
+};
+
 template <int TYPE>
-struct WRaw {  // Q4_0 / Q8_0: 16 bytes per 32-block, and row n's fp16 block scales
+struct WRaw {  // Q4_0 / Q5_0 / Q8_0: 16 bytes per 32-block, row n's fp16 block scales (Q5_0: and fifth bits)
+    static constexpr bool Q5 = TYPE == T_Q5_0;
     uint4 q[HB];
     uint32_t d[HB];
+    uint32_t qh[Q5 ? HB : 1];
     __device__ static uint32_t qoff(const QMat& W, int rt, int n, int g) {
-        return TYPE == T_Q4_0 ? (uint32_t)(((size_t)rt * W.nkb * 32 + n) * 16)
+        return TYPE != T_Q8_0 ? (uint32_t)(((size_t)rt * W.nkb * 32 + n) * 16)
                               : (uint32_t)((((size_t)rt * W.nkb * 2 + g) * 32 + n) * 16);
     }
     __device__ static uint32_t soff(const QMat& W, int rt, int n) {
         return (uint32_t)(((size_t)rt * W.nkb * 32 + n) * 2);
     }
     __device__ static uint32_t moff(const QMat&, int, int) { return 0; }
+    __device__ static uint32_t xoff(const QMat& W, int rt, int n, int) {
+        return Q5 ? (uint32_t)(((size_t)rt * W.nkb * 32 + n) * 4) : 0u;
+    }
     template <int PAR>
-    __device__ void load(const uint8_t* qb, const uint8_t* sb, const uint8_t*, uint32_t qo, uint32_t so, uint32_t,
-                         int h, int nb) {
-        constexpr int QB = TYPE == T_Q4_0 ? 512 : 1024;  // bytes per 32-block of a row tile
+    __device__ void load(const uint8_t* qb, const uint8_t* sb, const uint8_t*, const uint8_t* xb, uint32_t qo,
+                         uint32_t so, uint32_t, uint32_t xo, int h, int nb) {
+        constexpr int QB = TYPE != T_Q8_0 ? 512 : 1024;  // bytes per 32-block of a row tile
 #pragma unroll
         for (int j = 0; j < HB; ++j) {
             if (j < nb) {
                 q[j] = ld16(qb + (size_t)(h * HB + j) * QB + qo);
                 d[j] = *reinterpret_cast<const uint16_t*>(sb + (size_t)(h * HB + j) * 64 + so);
+                if constexpr (Q5) qh[j] = *reinterpret_cast<const uint32_t*>(xb + (size_t)(h * HB + j) * 128 + xo);
             }
         }
     }
 };
+
+// Four bits -> bit 0 of four bytes (disjoint shifted copies, no carries).
+__device__ __forceinline__ uint32_t spread4(uint32_t x) { return ((x & 0xFu) * 0x00204081u) & 0x01010101u; }
 
 template <bool V>
 struct Parity {
@@ -299,10 +357,13 @@ __global__ void __launch_bounds__(GW * 64) __attribute__((amdgpu_waves_per_eu(WP
 k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8 hq, float* hf, int hf_ld,
         float* y) {
     constexpr int NTH = GW * 64;
-    constexpr bool Q4K = TYPE == T_Q4_K;
-    // Q4_K: no per-period sums; acc is kept in units of the current
-    // super-block's d (per weight row) and rescaled by d_prev / d_cur at each
-    // super-block (fp32 rounding ~2^-24 per step)
+    // K-quants (Q4_K / Q5_K / Q6_K): acc is kept in units of the current super-block's d (per weight
+    // row) and rescaled by d_prev / d_cur at each super-block (fp32 rounding ~2^-24 per step); Q4_K and
+    // Q5_K carry the min term (Q4K below), Q6_K has none and signed sub-block scales per 16 of K
+    constexpr bool Q4K = TYPE == T_Q4_K || TYPE == T_Q5_K;
+    constexpr bool K6 = TYPE == T_Q6_K;
+    constexpr bool SUPER = Q4K || K6;
+    static_assert(!(K6 && GATEUP), "Q6_K gate/up runs on the GEMVs (its sc * q operand is not exact in fp16)");
     constexpr bool RESCALE = true;
     // Q4_K gate/up: block-unit activations -- the exact quants q as the operand and acc kept in units of
     // the current block's dx per pair, rescaled by u(b-1) / u(b) (one multiply per accumulator element
@@ -400,22 +461,25 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
     const uint8_t* qbase[TM];
     const uint8_t* sbase[TM];
     const uint8_t* mbase[TM];
-    uint32_t qo[TM], so[TM], mo[TM];
+    const uint8_t* xbase[TM];
+    uint32_t qo[TM], so[TM], mo[TM], xo[TM];
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         const QMat& W = (GATEUP && i == 1) ? W1 : W0;
         qbase[i] = W.qs + (size_t)e * W.qs_es;
         sbase[i] = W.sc + (size_t)e * W.sc_es;
         mbase[i] = Q4K ? W.mn + (size_t)e * W.mn_es : nullptr;
+        xbase[i] = W.ex ? W.ex + (size_t)e * W.ex_es : nullptr;
         const int rt = min(GATEUP ? rt0 : rt0 + i, W.nrt - 1);
         qo[i] = WRaw<TYPE>::qoff(W, rt, n, g);
         so[i] = WRaw<TYPE>::soff(W, rt, n);
         mo[i] = WRaw<TYPE>::moff(W, rt, n);
+        xo[i] = WRaw<TYPE>::xoff(W, rt, n, g);
     }
 
-    // Q4_0 / Q8_0 down: two accumulator sets, acc for even 32-blocks and acc2 for odd ones, each in its own
-    // unit (down only: with gate/up's two weight tiles per wave the second set spills, 394 -> 702 us)
-    constexpr bool DUAL = !Q4K && !GATEUP;
+    // Q4_0 / Q5_0 / Q8_0 down: two accumulator sets, acc for even 32-blocks and acc2 for odd ones, each in
+    // its own unit (down only: with gate/up's two weight tiles per wave the second set spills, 394 -> 702 us)
+    constexpr bool DUAL = !SUPER && !GATEUP;
     constexpr int TM2 = DUAL ? TM : 1, TN2 = DUAL ? TN : 1;
     v16f acc[TM][TN], acc2[TM2][TN2];
 #pragma unroll
@@ -428,7 +492,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
         for (int t = 0; t < TN2; ++t) acc2[i][t] = v16f{};
 
     WRaw<TYPE> wa[TM], wb[TM];
-    uint4 hdr[TM];  // Q4_K headers of the current super-block
+    uint4 hdr[TM];  // Q4_K / Q5_K headers (Q6_K: the 16 scales) of the current super-block
     float dl[TM];   // the unit acc is kept in for the lane's row: the current super-block's (Q4_K) or
                     // block's (Q4_0 / Q8_0) weight scale d, 1 where d is zero
     float dl2[TM2]; // the unit of acc2
@@ -443,7 +507,8 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
     for (int i = 0; i < TM2; ++i) dl2[i] = 1.0f;
     if (active)
 #pragma unroll
-        for (int i = 0; i < TM; ++i) wa[i].template load<0>(qbase[i], sbase[i], mbase[i], qo[i], so[i], mo[i], 0, min(HB, KB));
+        for (int i = 0; i < TM; ++i)
+            wa[i].template load<0>(qbase[i], sbase[i], mbase[i], xbase[i], qo[i], so[i], mo[i], xo[i], 0, min(HB, KB));
     stage(0);
 
     // LDS byte offset of this lane's A chunk (hi/lo hl, sub-block j of the half-unit, K-half m) in pair tile 0
@@ -458,17 +523,23 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
             if (active)
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
-                    nxt[i].template load<ODD ? 0 : 1>(qbase[i], sbase[i], mbase[i], qo[i], so[i], mo[i], h + 1,
-                                                      min(HB, KB - (h + 1) * HB));
+                    nxt[i].template load<ODD ? 0 : 1>(qbase[i], sbase[i], mbase[i], xbase[i], qo[i], so[i], mo[i],
+                                                      xo[i], h + 1, min(HB, KB - (h + 1) * HB));
         }
         if (!active) return;
         const uint8_t* sa = sm.st[ODD].q + pg * TN * 32 * PB;
-        if constexpr (Q4K) {
+        if constexpr (SUPER) {
             if (!ODD) {
 #pragma unroll
                 for (int i = 0; i < TM; ++i) {
-                    hdr[i] = cur[i].hd;
-                    const float d = f16_to_f32(hdr[i].x & 0xFFFFu);
+                    float d;
+                    if constexpr (K6) {
+                        hdr[i] = cur[i].sc;
+                        d = f16_to_f32(cur[i].d & 0xFFFFu);
+                    } else {
+                        hdr[i] = cur[i].hd;
+                        d = f16_to_f32(hdr[i].x & 0xFFFFu);
+                    }
                     if constexpr (RESCALE) {
                         dz[i] = d == 0.0f;
                         const float u = dz[i] ? 1.0f : d;  // the unit the min table divides by
@@ -482,7 +553,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
                         (void)d;
                     }
                 }
-            } else {
+            } else if constexpr (Q4K) {
                 // min term, once per super-block: acc += sum_j (dx_j sum q_j) (-dmin m_j / unit) on bf16
                 // 3-piece splits (the activation side in xm, the weight side from the min table); six of
                 // the nine piece products (all above 2^-24 relative) in three MFMAs, (MFMA, lane half) ->
@@ -524,20 +595,47 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
                 if (m == 0) {
 #pragma unroll
                     for (int i = 0; i < TM; ++i) {
-                        int sc, mn;
-                        hdr_scale_min(hdr[i], 4 * ODD + jj, sc, mn);
-                        const _Float16 sv = (_Float16)(RESCALE && dz[i] ? 0.0f : (float)sc);  // exact
-                        const _Float16 s1 = (jj & 1) ? sv * (_Float16)0.0625f : sv;
-                        const _Float16 s0 = (jj & 1) ? sv * (_Float16)-64.0f : sv * (_Float16)-1024.0f;
-                        c1[i] = h2v{s1, s1};
-                        c0[i] = h2v{s0, s0};
+                        if constexpr (K6) {
+                            // sc * (q6 - 32) from v = 4 q6: (1024 + v) * sc / 4 - 288 sc in one fp16 fma (both
+                            // constants exact; the result rounds once, exact up to |sc * (q6 - 32)| <= 2048)
+                            const int k = 8 * ODD + 2 * jj + g;
+                            const uint32_t wsc = k < 4 ? hdr[i].x : (k < 8 ? hdr[i].y : (k < 12 ? hdr[i].z : hdr[i].w));
+                            const float scf = RESCALE && dz[i] ? 0.0f : (float)(int8_t)(uint8_t)(wsc >> (8 * (k & 3)));
+                            c1[i] = splat(scf * 0.25f);
+                            c0[i] = splat(scf * -288.0f);
+                        } else {
+                            int sc, mn;
+                            hdr_scale_min(hdr[i], 4 * ODD + jj, sc, mn);
+                            const _Float16 sv = (_Float16)(RESCALE && dz[i] ? 0.0f : (float)sc);  // exact
+                            // Q5_K quants arrive in the low bits (0..31); Q4_K high nibbles stay in place
+                            const bool hi = TYPE == T_Q4_K && (jj & 1);
+                            const _Float16 s1 = hi ? sv * (_Float16)0.0625f : sv;
+                            const _Float16 s0 = hi ? sv * (_Float16)-64.0f : sv * (_Float16)-1024.0f;
+                            c1[i] = h2v{s1, s1};
+                            c0[i] = h2v{s0, s0};
+                        }
                     }
                 }
-                const uint32_t mask = (jj & 1) ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
 #pragma unroll
                 for (int i = 0; i < TM; ++i) {
-                    const uint4 raw = cur[i].q[jj >> 1];
-                    dst[i] = m ? cvt8(raw.z, raw.w, mask, 0u, c1[i], c0[i]) : cvt8(raw.x, raw.y, mask, 0u, c1[i], c0[i]);
+                    if constexpr (K6) {
+                        const uint4 lo = cur[i].q[jj & 1], hb = cur[i].q[2];
+                        const int sh = (jj >> 1) * 4;
+                        const uint32_t l0 = ((m ? lo.z : lo.x) >> sh) & 0x0F0F0F0Fu, l1 = ((m ? lo.w : lo.y) >> sh) & 0x0F0F0F0Fu;
+                        const uint32_t h0 = ((m ? hb.z : hb.x) >> (2 * jj)) & 0x03030303u;
+                        const uint32_t h1 = ((m ? hb.w : hb.y) >> (2 * jj)) & 0x03030303u;
+                        dst[i] = cvt8((l0 << 2) | (h0 << 6), (l1 << 2) | (h1 << 6), 0xFFFFFFFFu, 0u, c1[i], c0[i]);
+                    } else if constexpr (TYPE == T_Q5_K) {
+                        const uint4 raw = cur[i].q[jj >> 1], qb = cur[i].qh;
+                        const int sh = (jj & 1) * 4, J = 4 * ODD + jj;
+                        const uint32_t w0 = (((m ? raw.z : raw.x) >> sh) & 0x0F0F0F0Fu) | ((((m ? qb.z : qb.x) >> J) & 0x01010101u) << 4);
+                        const uint32_t w1 = (((m ? raw.w : raw.y) >> sh) & 0x0F0F0F0Fu) | ((((m ? qb.w : qb.y) >> J) & 0x01010101u) << 4);
+                        dst[i] = cvt8(w0, w1, 0xFFFFFFFFu, 0u, c1[i], c0[i]);
+                    } else {
+                        const uint32_t mask = (jj & 1) ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+                        const uint4 raw = cur[i].q[jj >> 1];
+                        dst[i] = m ? cvt8(raw.z, raw.w, mask, 0u, c1[i], c0[i]) : cvt8(raw.x, raw.y, mask, 0u, c1[i], c0[i]);
+                    }
                 }
             };
             // block-unit form: each pair tile's 16 unit ratios of a block (register r <-> pair
@@ -679,10 +777,20 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
             // the block's weight scale d (unit 1 and a zeroed weight operand where d is zero), then the
             // block's MFMAs straight into it. With two sets, one set's rescale does not wait for MFMAs
             // still writing the other, and the MFMAs of one block overlap the rescale of the next.
-            const uint32_t mask = TYPE == T_Q8_0 ? 0xFFFFFFFFu : (g ? 0xF0F0F0F0u : 0x0F0F0F0Fu);
+            // operand bytes: Q8_0 q + 128, Q4_0 the lane's nibble half in place, Q5_0 its 5-bit quants
+            // (nibble + fifth bit, built in q5w); then fp16 k1 * (1024 + byte) + k0 = the weight
+            const uint32_t mask = TYPE == T_Q4_0 ? (g ? 0xF0F0F0F0u : 0x0F0F0F0Fu) : 0xFFFFFFFFu;
             const uint32_t flip = TYPE == T_Q8_0 ? 0x80808080u : 0u;
-            const float k1 = TYPE == T_Q8_0 ? 1.0f : (g ? 0.0625f : 1.0f);
-            const float k0 = TYPE == T_Q8_0 ? -1152.0f : (g ? -72.0f : -1032.0f);
+            const float k1 = TYPE == T_Q4_0 && g ? 0.0625f : 1.0f;
+            const float k0 = TYPE == T_Q8_0 ? -1152.0f : (TYPE == T_Q5_0 ? -1040.0f : (g ? -72.0f : -1032.0f));
+            // Q5_0: elements 16g + 8m + i are nibble half g of qs[8m + i] with fifth bit 16g + 8m + i
+            // (dequantize_row_q5_0, src/quant.cpp:1585-1600)
+            auto q5w = [&](const WRaw<TYPE>& w, int j, int m, uint32_t& w0, uint32_t& w1) {
+                const uint4 raw = w.q[j];
+                const uint32_t bits = (w.qh[TYPE == T_Q5_0 ? j : 0] >> (8 * (2 * g + m))) & 0xFFu;
+                w0 = (((m ? raw.z : raw.x) >> (4 * g)) & 0x0F0F0F0Fu) | (spread4(bits) << 4);
+                w1 = (((m ? raw.w : raw.y) >> (4 * g)) & 0x0F0F0F0Fu) | (spread4(bits >> 4) << 4);
+            };
             auto block = [&](int j, auto& A, auto& D) {  // A: an accumulator set, D: its units
                 h2v c1[TM], c0[TM];
 #pragma unroll
@@ -704,9 +812,15 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
                     h8 wv[TM], av[TN][HL];
 #pragma unroll
                     for (int i = 0; i < TM; ++i) {
-                        const uint4 raw = cur[i].q[j];
-                        wv[i] = m ? cvt8(raw.z, raw.w, mask, flip, c1[i], c0[i])
-                                  : cvt8(raw.x, raw.y, mask, flip, c1[i], c0[i]);
+                        if constexpr (TYPE == T_Q5_0) {
+                            uint32_t w0, w1;
+                            q5w(cur[i], j, m, w0, w1);
+                            wv[i] = cvt8(w0, w1, mask, flip, c1[i], c0[i]);
+                        } else {
+                            const uint4 raw = cur[i].q[j];
+                            wv[i] = m ? cvt8(raw.z, raw.w, mask, flip, c1[i], c0[i])
+                                      : cvt8(raw.x, raw.y, mask, flip, c1[i], c0[i]);
+                        }
                     }
 #pragma unroll
                     for (int t = 0; t < TN; ++t)
@@ -1017,14 +1131,18 @@ void launch_mfma_gateup(const QMat& g, const QMat& u, const ActH& xin, const Gro
     const int hf_ld = ((g.rows + 255) / 256) * 256;
     // Q4_K reads the block-unit form, the others the hi/lo form (the caller allocates the forms its
     // matrices need; a missing one is a caller bug, and nothing is launched on null pointers)
-    if (g.type == T_Q4_K ? !(xin.q16 && xin.rx && xin.pu && xin.xu) : !(xin.hl && xin.pe)) return;
+    const bool unit = g.type == T_Q4_K || g.type == T_Q5_K;
+    if (unit ? !(xin.q16 && xin.rx && xin.pu && xin.xu) : !(xin.hl && xin.pe)) return;
     switch (g.type) {
         case T_Q4_0: launch_t<T_Q4_0, true>(g, u, xin, grp, tiles_ub, hq, hf, hf_ld, nullptr, st); break;
         case T_Q8_0: launch_t<T_Q8_0, true>(g, u, xin, grp, tiles_ub, hq, hf, hf_ld, nullptr, st); break;
         case T_Q4_K: launch_t<T_Q4_K, true>(g, u, xin, grp, tiles_ub, hq, hf, hf_ld, nullptr, st); break;
-        default: break;
+        case T_Q5_K: launch_t<T_Q5_K, true>(g, u, xin, grp, tiles_ub, hq, hf, hf_ld, nullptr, st); break;
+        default: break;  // Q5_0 / Q6_K gate/up: GEMV only (gemm_gateup_ok)
     }
 }
+
+bool gemm_gateup_ok(int type) { return type == T_Q4_0 || type == T_Q8_0 || type == T_Q4_K || type == T_Q5_K; }
 
 void launch_mfma_down(const QMat& dn, const ActH& hin, const Groups& grp, int tiles_ub, float* y, hipStream_t st) {
     const ActQ8 none{};
@@ -1032,6 +1150,9 @@ void launch_mfma_down(const QMat& dn, const ActH& hin, const Groups& grp, int ti
         case T_Q4_0: launch_t<T_Q4_0, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st); break;
         case T_Q8_0: launch_t<T_Q8_0, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st); break;
         case T_Q4_K: launch_t<T_Q4_K, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st); break;
+        case T_Q5_0: launch_t<T_Q5_0, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st); break;
+        case T_Q5_K: launch_t<T_Q5_K, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st); break;
+        case T_Q6_K: launch_t<T_Q6_K, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st); break;
         default: break;
     }
 }

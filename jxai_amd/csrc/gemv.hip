@@ -15,9 +15,15 @@
 // x activation scale) as in the reference's vec_dot_*_q8_0 kernels
 // (src/quant.cpp:3307-3573); only the fp32 summation order differs.
 //
-// K-units (four 1 KB wave loads each):
+// K-units (four 1 KB wave loads each, more for the five- and six-bit formats):
 //   Q4_K  one 256-element super-block: 4 pair chunks + the 16-byte header
+//   Q5_K  half a super-block (sub-block pairs 2s, 2s + 1 of super-block u / 2, s = u % 2): 2 pair
+//         chunks, the header and the 16-byte chunk of fifth bits of half h
+//   Q6_K  half a super-block (128 elements, four 32-blocks): lanes of half h take elements
+//         16h..16h+15 of each block (sub-block 2r + h of block r): ql chunks h and 2 + h and qh
+//         chunk 4 + h of that half, its 8 scales and d
 //   Q4_0  eight 32-blocks: lanes of half h take the four blocks of parity h
+//   Q5_0  as Q4_0 + each block's 32 fifth bits (fp32 activations only)
 //   Q8_0  four 32-blocks: lanes of half h take half h of each
 #include <algorithm>
 
@@ -35,6 +41,22 @@ struct RawB {
 struct RawQ4K {
     uint4 q[4];
     uint4 hd;  // d | dmin << 16, then the 12 scale bytes
+};
+struct RawQ5K {
+    uint4 q[2];  // pair chunks 2s, 2s + 1
+    uint4 hd;
+    uint4 qh;    // qh bytes 16h..16h+15 shifted right by 4s: bit j of each byte = fifth bit of sub-block 4s + j
+    int s;       // which half of the super-block
+};
+struct RawQ6K {
+    uint4 q[3];  // of the unit's 128-element half: ql chunks h, 2 + h, then qh chunk 4 + h
+    uint2 sc;    // the half's 8 int8 sub-block scales
+    uint32_t d;  // fp16 bits of d
+};
+struct RawB5 {
+    uint4 q[4];
+    uint32_t d[4];
+    uint32_t qh[4];
 };
 
 template <int TYPE>
@@ -95,9 +117,66 @@ struct Fmt<T_Q4_K> {
     }
 };
 
+template <>
+struct Fmt<T_Q5_0> {
+    using Raw = RawB5;
+    static constexpr int BPU = 8;
+    __device__ static void load(Raw& c, const QMat& W, int e, int rt, int u, int m, int h, bool ok) {
+        const size_t b0 = (size_t)rt * W.nkb + (size_t)u * BPU + h;
+        const uint8_t* qb = W.qs + e * W.qs_es;
+        const uint8_t* sb = W.sc + e * W.sc_es;
+        const uint8_t* xb = W.ex + e * W.ex_es;
+        const int left = W.nkb - u * BPU - h;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const bool v = ok && 2 * i < left;
+            const size_t t = (b0 + 2 * i) * 32 + m;
+            c.q[i] = ld_stream16(v ? qb + t * 16 : W.pad_qs + m * 16);
+            c.d[i] = *reinterpret_cast<const uint16_t*>(v ? sb + t * 2 : W.pad_sc + m * 2);
+            c.qh[i] = *reinterpret_cast<const uint32_t*>(v ? xb + t * 4 : W.pad_ex + m * 4);
+        }
+    }
+};
+
+// Units are halves of super-blocks (unit u: super-block u / 2, sub-blocks 4 (u % 2) .. + 3).
+template <>
+struct Fmt<T_Q5_K> {
+    using Raw = RawQ5K;
+    static constexpr int BPU = 1;
+    __device__ static void load(Raw& c, const QMat& W, int e, int rt, int u, int m, int h, bool ok) {
+        const size_t t = (size_t)rt * W.nkb + (u >> 1);
+        c.s = u & 1;
+        const uint8_t* qb = ok ? W.qs + e * W.qs_es + (t * 8 + 4 * c.s + h) * 512 : W.pad_qs;
+        const uint8_t* hb = ok ? W.sc + e * W.sc_es + t * 512 : W.pad_sc;
+        const uint8_t* xb = ok ? W.ex + e * W.ex_es + (t * 2 + h) * 512 : W.pad_ex;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) c.q[p] = ld_stream16(qb + p * 1024 + m * 16);
+        c.hd = ld_stream16(hb + m * 16);
+        const uint4 v = ld_stream16(xb + m * 16);
+        const int sh = 4 * c.s;
+        c.qh = make_uint4(v.x >> sh, v.y >> sh, v.z >> sh, v.w >> sh);
+    }
+};
+
+// Units are 128-element halves of super-blocks (unit u: super-block u / 2, half u % 2).
+template <>
+struct Fmt<T_Q6_K> {
+    using Raw = RawQ6K;
+    static constexpr int BPU = 1;
+    __device__ static void load(Raw& c, const QMat& W, int e, int rt, int u, int m, int h, bool ok) {
+        const size_t t = (size_t)rt * W.nkb + (u >> 1);
+        const int n = u & 1;
+        const uint8_t* qb = ok ? W.qs + e * W.qs_es + t * 6144 + n * 3072 : W.pad_qs;  // 6 chunks of 512 B per half
+#pragma unroll
+        for (int k = 0; k < 3; ++k) c.q[k] = ld_stream16(qb + (2 * k + h) * 512 + m * 16);
+        c.sc = *reinterpret_cast<const uint2*>((ok ? W.sc + e * W.sc_es + t * 512 + 8 * n : W.pad_sc) + m * 16);
+        c.d = *reinterpret_cast<const uint16_t*>((ok ? W.ex + e * W.ex_es + t * 64 : W.pad_ex) + m * 2);
+    }
+};
+
 template <int TYPE>
 __host__ __device__ constexpr int n_units(int nkb) {
-    return (nkb + Fmt<TYPE>::BPU - 1) / Fmt<TYPE>::BPU;
+    return (TYPE == T_Q6_K || TYPE == T_Q5_K) ? 2 * nkb : (nkb + Fmt<TYPE>::BPU - 1) / Fmt<TYPE>::BPU;
 }
 
 __device__ __forceinline__ uint32_t byte_of(const uint4& v, int i) {
@@ -114,6 +193,50 @@ __device__ __forceinline__ void hd_scale_min(const uint4& hd, int j, int& sc, in
     } else {
         sc = (byte_of(hd, j + 4) & 0x0F) | ((byte_of(hd, j - 4) >> 6) << 4);
         mn = (byte_of(hd, j + 4) >> 4) | ((byte_of(hd, j) >> 6) << 4);
+    }
+}
+
+// Byte k (0..7) of 8 bytes, sign-extended (the Q6_K int8 scales).
+__device__ __forceinline__ int sbyte(const uint2& v, int k) {
+    return (int)(int8_t)(uint8_t)((k < 4 ? v.x : v.y) >> (8 * (k & 3)));
+}
+
+__device__ __forceinline__ uint32_t comp(const uint4& v, int i) { return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w)); }
+
+// Q6_K, 32-block r (0..3) of a unit, this lane's 16 elements as four words of 4 q6 bytes shifted
+// left by 2 (4 q6, 0..252): the low nibble from ql chunk q[r & 1] (high nibble when r >= 2), the
+// two high bits from bits 2r, 2r + 1 of qh chunk q[2] (block_q6_K layout, src/quant.cpp:1389-1428).
+__device__ __forceinline__ void q6_words(const RawQ6K& c, int r, uint32_t (&w)[4]) {
+    const uint4 lo = c.q[r & 1], hi = c.q[2];
+    const int sh = (r >> 1) * 4;
+#pragma unroll
+    for (int z = 0; z < 4; ++z) {
+        const uint32_t l4 = (comp(lo, z) >> sh) & 0x0F0F0F0Fu;
+        const uint32_t h2 = (comp(hi, z) >> (2 * r)) & 0x03030303u;
+        w[z] = (l4 << 2) | (h2 << 6);
+    }
+}
+
+// Q5_K: the 5-bit quants of the unit's sub-block j (0..3; 2p: low nibbles of chunk p, 2p + 1:
+// high) for this lane's 16 elements, fifth bit from bit j of the lane's shifted qh bytes
+// (dequantize_row_q5_K, src/quant.cpp:1345-1387).
+__device__ __forceinline__ void q5k_words(const RawQ5K& c, int j, uint32_t (&w)[4]) {
+    const uint4 v = c.q[j >> 1];
+    const int sh = (j & 1) * 4;
+#pragma unroll
+    for (int z = 0; z < 4; ++z) w[z] = ((comp(v, z) >> sh) & 0x0F0F0F0Fu) | (((comp(c.qh, z) >> j) & 0x01010101u) << 4);
+}
+
+// (scale, min) of sub-blocks 4s .. 4s + 3 of a Q5_K header (constant-index unpacking, then a select
+// on the unit's half s).
+__device__ __forceinline__ void q5k_unit_scales(const uint4& hd, int s, int (&sc)[4], int (&mn)[4]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        int a0, b0, a1, b1;
+        hd_scale_min(hd, k, a0, b0);
+        hd_scale_min(hd, 4 + k, a1, b1);
+        sc[k] = s ? a1 : a0;
+        mn[k] = s ? b1 : b0;
     }
 }
 
@@ -186,23 +309,67 @@ __device__ __forceinline__ void unit_accum(const typename Fmt<TYPE>::Raw& c, con
                 }
             }
         }
-    } else {
+    } else if constexpr (TYPE == T_Q6_K) {
+        // vec_dot_q6_K_q8_0 (src/quant.cpp:3723-3818): per 32-block the exact integer sum
+        // sc * sum((q6 - 32) * y) of this lane's sub-block, scaled by d * dy
+        const float d = f16_to_f32(c.d & 0xFFFFu);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t w[4];
+            q6_words(c, j, w);
+            int wv[4];
+#pragma unroll
+            for (int z = 0; z < 4; ++z) wv[z] = (int)(w[z] ^ 0x80808080u);  // 4 (q6 - 32) as int8
+            const int sc = sbyte(c.sc, 2 * j + h);
+            const int b = u * 4 + j;
+#pragma unroll
+            for (int t = 0; t < TB; ++t) {
+                if (t < nt) {
+                    const uint4 a = lds16(A.q + t * A.K + b * 32 + 16 * h);
+                    int is = sdot4(wv[0], (int)a.x, 0);
+                    is = sdot4(wv[1], (int)a.y, is);
+                    is = sdot4(wv[2], (int)a.z, is);
+                    is = sdot4(wv[3], (int)a.w, is);
+                    acc[t] = __builtin_fmaf(d * A.s[t * KB + b].x, (float)(sc * (is >> 2)), acc[t]);
+                }
+            }
+        }
+    } else {  // Q4_K (whole super-block units) / Q5_K (half super-block units: pairs 2s, 2s + 1)
+        constexpr int NP = TYPE == T_Q5_K ? 2 : 4;
+        const int bb = TYPE == T_Q5_K ? u * 4 : u * 8;  // the unit's first 32-block in K
+        int usc[4], umn[4];
+        if constexpr (TYPE == T_Q5_K) q5k_unit_scales(c.hd, c.s, usc, umn);
         const float d = f16_to_f32(c.hd.x & 0xFFFFu), dmin = f16_to_f32(c.hd.x >> 16);
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
+        for (int p = 0; p < NP; ++p) {
             int s0, m0, s1, m1;
-            hd_scale_min(c.hd, 2 * p, s0, m0);
-            hd_scale_min(c.hd, 2 * p + 1, s1, m1);
+            if constexpr (TYPE == T_Q5_K) {
+                s0 = usc[2 * p], m0 = umn[2 * p], s1 = usc[2 * p + 1], m1 = umn[2 * p + 1];
+            } else {
+                hd_scale_min(c.hd, 2 * p, s0, m0);
+                hd_scale_min(c.hd, 2 * p + 1, s1, m1);
+            }
             const float fs0 = d * (float)s0, fm0 = dmin * (float)m0;
             const float fs1 = d * (float)s1, fm1 = dmin * (float)m1;
-            const uint32_t q[4] = {c.q[p].x, c.q[p].y, c.q[p].z, c.q[p].w};
             int ql[4], qh[4];
+            if constexpr (TYPE == T_Q5_K) {
+                uint32_t wl[4], wh[4];
+                q5k_words(c, 2 * p, wl);
+                q5k_words(c, 2 * p + 1, wh);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                ql[i] = (int)(q[i] & 0x0F0F0F0Fu);
-                qh[i] = (int)((q[i] >> 4) & 0x0F0F0F0Fu);
+                for (int i = 0; i < 4; ++i) {
+                    ql[i] = (int)wl[i];
+                    qh[i] = (int)wh[i];
+                }
+            } else {
+                const uint32_t q[4] = {c.q[p].x, c.q[p].y, c.q[p].z, c.q[p].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    ql[i] = (int)(q[i] & 0x0F0F0F0Fu);
+                    qh[i] = (int)((q[i] >> 4) & 0x0F0F0F0Fu);
+                }
             }
-            const int b0 = u * 8 + 2 * p;
+            const int b0 = bb + 2 * p;
 #pragma unroll
             for (int j = 0; j < TB; ++j) {
                 if (j < nt) {
@@ -231,50 +398,147 @@ __device__ __forceinline__ void unit_accum(const typename Fmt<TYPE>::Raw& c, con
     }
 }
 
-// Q4_K against fp32 activations (the reference's vec_dot_q4_K_f32 fallback,
-// src/quant.cpp:2910-3013, used when K % 256 != 0): rows of y are zero-padded
-// to whole super-blocks, so the partial last super-block needs no masking.
-template <int TB>
-__device__ __forceinline__ void unit_accum_f32(const RawQ4K& c, const ActLds& A, int u, int h, int nt, float* acc) {
-    const float d = f16_to_f32(c.hd.x & 0xFFFFu), dmin = f16_to_f32(c.hd.x >> 16);
+// One row's 32 (or 16) quants against fp32 activations from LDS: sum_i w_i * y_i as an fp32 fma
+// chain, w_i = (float)(byte i of the words) + off.
+template <int NW>
+__device__ __forceinline__ float dot_f32_words(const uint32_t (&w)[NW], const float* y, float off) {
+    float s = 0.0f;
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        int s0, m0, s1, m1;
-        hd_scale_min(c.hd, 2 * p, s0, m0);
-        hd_scale_min(c.hd, 2 * p + 1, s1, m1);
-        const float fs0 = d * (float)s0, fm0 = dmin * (float)m0;
-        const float fs1 = d * (float)s1, fm1 = dmin * (float)m1;
-        const uint32_t q[4] = {c.q[p].x, c.q[p].y, c.q[p].z, c.q[p].w};
+    for (int i = 0; i < NW; ++i) {
+        const float4 v = *reinterpret_cast<const float4*>(y + 4 * i);
+        s = __builtin_fmaf((float)(w[i] & 0xFFu) + off, v.x, s);
+        s = __builtin_fmaf((float)((w[i] >> 8) & 0xFFu) + off, v.y, s);
+        s = __builtin_fmaf((float)((w[i] >> 16) & 0xFFu) + off, v.z, s);
+        s = __builtin_fmaf((float)(w[i] >> 24) + off, v.w, s);
+    }
+    return s;
+}
+
+// Accumulate one K-unit of one weight row against up to TB fp32 activation rows (the reference's
+// vec_dot_quant_f32 dots, src/quant.cpp:3269-3305: vec_dot_q4_0_f32 2780-2827, vec_dot_q8_0_f32
+// 2829-2862, vec_dot_q4_K_f32 2910-3013, vec_dot_q5_K_f32 3069-3085, vec_dot_q6_K_f32 3087-3165,
+// vec_dot_q5_0_f32 3232-3234): each block or sub-block's weights times y as an fp32 chain, scaled
+// once.  K-quant rows of y are zero-padded to whole super-blocks, so a partial last super-block
+// needs no masking; only the fp32 summation order differs from the reference.
+template <int TYPE, int TB>
+__device__ __forceinline__ void unit_accum_f32(const typename Fmt<TYPE>::Raw& c, const ActLds& A, int u, int h,
+                                               int nt, int nkb, float* acc) {
+    if constexpr (TYPE == T_Q4_K || TYPE == T_Q5_K) {
+        constexpr int NP = TYPE == T_Q5_K ? 2 : 4;  // Q5_K: half super-block units (pairs 2s, 2s + 1)
+        const int e0 = TYPE == T_Q5_K ? u * 128 : u * 256;  // the unit's first element
+        int usc[4], umn[4];
+        if constexpr (TYPE == T_Q5_K) q5k_unit_scales(c.hd, c.s, usc, umn);
+        const float d = f16_to_f32(c.hd.x & 0xFFFFu), dmin = f16_to_f32(c.hd.x >> 16);
 #pragma unroll
-        for (int j = 0; j < TB; ++j) {
-            if (j < nt) {
-                const float* ya = A.f + j * A.K + u * 256 + 64 * p + 16 * h;
-                const float* yb = ya + 32;
-                float sa = 0.0f, sb = 0.0f, ta = 0.0f, tb = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float4 va = *reinterpret_cast<const float4*>(ya + 4 * i);
-                    const float4 vb = *reinterpret_cast<const float4*>(yb + 4 * i);
-                    const float fa[4] = {va.x, va.y, va.z, va.w};
-                    const float fb[4] = {vb.x, vb.y, vb.z, vb.w};
-#pragma unroll
-                    for (int z = 0; z < 4; ++z) {
-                        const uint32_t byte = (q[i] >> (8 * z)) & 0xFFu;
-                        sa = __builtin_fmaf((float)(byte & 15u), fa[z], sa);
-                        sb = __builtin_fmaf((float)(byte >> 4), fb[z], sb);
-                        ta = ta + fa[z];
-                        tb = tb + fb[z];
-                    }
-                }
-                float v = acc[j];
-                v = __builtin_fmaf(fs0, sa, v);
-                v = __builtin_fmaf(-fm0, ta, v);
-                v = __builtin_fmaf(fs1, sb, v);
-                v = __builtin_fmaf(-fm1, tb, v);
-                acc[j] = v;
+        for (int p = 0; p < NP; ++p) {
+            int s0, m0, s1, m1;
+            if constexpr (TYPE == T_Q5_K) {
+                s0 = usc[2 * p], m0 = umn[2 * p], s1 = usc[2 * p + 1], m1 = umn[2 * p + 1];
+            } else {
+                hd_scale_min(c.hd, 2 * p, s0, m0);
+                hd_scale_min(c.hd, 2 * p + 1, s1, m1);
             }
-            // one token's 32 activations at a time in registers
-            if constexpr (TB > 1) __builtin_amdgcn_sched_barrier(0);
+            const float fs0 = d * (float)s0, fm0 = dmin * (float)m0;
+            const float fs1 = d * (float)s1, fm1 = dmin * (float)m1;
+            uint32_t q[4];  // Q4_K: the chunk's bytes (low nibble: sub-block 2p, high: 2p + 1)
+            uint32_t q5[4]; // Q5_K: the fifth bits of the lane's 16 elements
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                q[i] = comp(c.q[p], i);
+                if constexpr (TYPE == T_Q5_K) q5[i] = comp(c.qh, i) >> (2 * p);
+            }
+#pragma unroll
+            for (int j = 0; j < TB; ++j) {
+                if (j < nt) {
+                    const float* ya = A.f + j * A.K + e0 + 64 * p + 16 * h;
+                    const float* yb = ya + 32;
+                    float sa = 0.0f, sb = 0.0f, ta = 0.0f, tb = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float4 va = *reinterpret_cast<const float4*>(ya + 4 * i);
+                        const float4 vb = *reinterpret_cast<const float4*>(yb + 4 * i);
+                        const float fa[4] = {va.x, va.y, va.z, va.w};
+                        const float fb[4] = {vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+                        for (int z = 0; z < 4; ++z) {
+                            uint32_t lo = (q[i] >> (8 * z)) & 15u, hi = (q[i] >> (8 * z + 4)) & 15u;
+                            if constexpr (TYPE == T_Q5_K) {
+                                lo |= ((q5[i] >> (8 * z)) & 1u) << 4;
+                                hi |= ((q5[i] >> (8 * z + 1)) & 1u) << 4;
+                            }
+                            sa = __builtin_fmaf((float)lo, fa[z], sa);
+                            sb = __builtin_fmaf((float)hi, fb[z], sb);
+                            ta = ta + fa[z];
+                            tb = tb + fb[z];
+                        }
+                    }
+                    float v = acc[j];
+                    v = __builtin_fmaf(fs0, sa, v);
+                    v = __builtin_fmaf(-fm0, ta, v);
+                    v = __builtin_fmaf(fs1, sb, v);
+                    v = __builtin_fmaf(-fm1, tb, v);
+                    acc[j] = v;
+                }
+                // one token's activations at a time in registers
+                if constexpr (TB > 1) __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    } else if constexpr (TYPE == T_Q6_K) {
+        const float d = f16_to_f32(c.d & 0xFFFFu);
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            uint32_t w[4];
+            q6_words(c, jb, w);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w[i] = (w[i] >> 2) & 0x3F3F3F3Fu;  // q6
+            const float ds = d * (float)sbyte(c.sc, 2 * jb + h);
+#pragma unroll
+            for (int j = 0; j < TB; ++j) {
+                if (j < nt) {
+                    const float* y = A.f + j * A.K + u * 128 + 32 * jb + 16 * h;
+                    acc[j] = __builtin_fmaf(ds, dot_f32_words<4>(w, y, -32.0f), acc[j]);
+                }
+                if constexpr (TB > 1) __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    } else if constexpr (TYPE == T_Q8_0) {  // half h of each of the unit's four blocks
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int b = u * 4 + i;
+            if (b < nkb) {
+                const float dw = f16_to_f32(c.d[i] & 0xFFFFu);
+                uint32_t w[4];
+#pragma unroll
+                for (int z = 0; z < 4; ++z) w[z] = comp(c.q[i], z) ^ 0x80808080u;  // q + 128
+#pragma unroll
+                for (int j = 0; j < TB; ++j)
+                    if (j < nt) acc[j] = __builtin_fmaf(dw, dot_f32_words<4>(w, A.f + j * A.K + b * 32 + 16 * h, -128.0f), acc[j]);
+            }
+        }
+    } else {  // Q4_0 / Q5_0: whole blocks of parity h
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int b = u * 8 + 2 * i + h;
+            if (b < nkb) {
+                const float dw = f16_to_f32(c.d[i] & 0xFFFFu);
+                uint32_t w[8];
+#pragma unroll
+                for (int z = 0; z < 4; ++z) {
+                    w[z] = comp(c.q[i], z) & 0x0F0F0F0Fu;          // elements 4z..4z+3
+                    w[4 + z] = (comp(c.q[i], z) >> 4) & 0x0F0F0F0Fu;  // elements 16 + 4z..
+                }
+                float off = -8.0f;
+                if constexpr (TYPE == T_Q5_0) {  // fifth bit j of element j (dequantize_row_q5_0, 1585-1600)
+                    const uint32_t qh = c.qh[i];
+#pragma unroll
+                    for (int z = 0; z < 8; ++z)
+                        w[z] |= ((((qh >> (4 * z)) & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
+                    off = -16.0f;
+                }
+#pragma unroll
+                for (int j = 0; j < TB; ++j)
+                    if (j < nt) acc[j] = __builtin_fmaf(dw, dot_f32_words<8>(w, A.f + j * A.K + b * 32, off), acc[j]);
+            }
         }
     }
 }
@@ -447,14 +711,23 @@ __device__ __forceinline__ void kloop(const QMat& W0, const QMat& W1, int e, int
 #define JX_GEMV_TB4_WPS 2
 #endif
 #define GEMV_WAVES_PER_SIMD(TB) ((TB) == 1 ? 4 : JX_GEMV_TB4_WPS)
+// The single-token down GEMV's fp32-activation dots other than Q4_K's do not fit 128 VGPRs with two
+// units in flight; they run at 2 waves per SIMD (one 8-wave block per CU, as at 3).
+template <int TYPE, int TB, bool F32ACT>
+constexpr int down_wps() {
+    return TB == 1 && F32ACT && TYPE != T_Q4_K && TYPE != T_Q5_K ? 2 : GEMV_WAVES_PER_SIMD(TB);
+}
 
 // Gate + up + SwiGLU (matmul_swiglu_quant_f32, src/quant.cpp:3970-4009) and
 // the Q8_0 quantization of the result for the down projection
 // (matmul_quant_f32's quantize_row_q8_0, 3908-3914).  The first half of the
-// waves streams the gate tile, the second half the up tile.
-template <int TYPE, int TB, int WAVES, int WPS = GEMV_WAVES_PER_SIMD(TB)>
+// waves streams the gate tile, the second half the up tile.  F32ACT: the
+// fp32-activation dots (types without a Q8_0 form at this K) over xf rows of
+// xf_ld floats, zero-padded to whole K-units, staged straight into LDS.
+template <int TYPE, int TB, int WAVES, int WPS = GEMV_WAVES_PER_SIMD(TB), bool F32ACT = false>
 __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WPS)))
-k_gemv_gateup(QMat G, QMat U, ActQ8 xq, Groups grp, ActQ8 hq, float* hf, int hf_ld, SmallTail tail) {
+k_gemv_gateup(QMat G, QMat U, ActQ8 xq, const float* xf, int xf_ld, Groups grp, ActQ8 hq, float* hf, int hf_ld,
+              SmallTail tail) {
     constexpr int HW = WAVES / 2;  // waves per matrix
     extern __shared__ __align__(16) int8_t smem[];
     __shared__ float red[WAVES][TB][32];
@@ -470,26 +743,38 @@ k_gemv_gateup(QMat G, QMat U, ActQ8 xq, Groups grp, ActQ8 hq, float* hf, int hf_
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 31, h = lane >> 5;
     const int mat = wave / HW, kw = wave % HW;
     const QMat& W = mat ? U : G;
-    const int K = xq.K;
+    const int K = F32ACT ? xf_ld : xq.K;
     const int nu = n_units<TYPE>(G.nkb);
-    const ActLds A{smem, reinterpret_cast<const float2*>(smem + TB * K), nullptr, K};
+    const ActLds A{smem, reinterpret_cast<const float2*>(smem + TB * K), reinterpret_cast<const float*>(smem), K};
     for (int tb0 = 0; tb0 < cnt; tb0 += TB) {
         const int nt = min(TB, cnt - tb0);
         if (tb0) __syncthreads();  // previous group's LDS reads are done
         auto src = [&](int j) { return (size_t)token_of(grp, rec, tb0 + j); };
         StageQ8<WAVES * 64, TB == 1 ? 4 : 8, TB == 1 ? 2 : 4> sg;
-        sg.issue(xq, nt, src, tid);
+        if constexpr (!F32ACT) sg.issue(xq, nt, src, tid);
         float acc[TB];
 #pragma unroll
         for (int j = 0; j < TB; ++j) acc[j] = 0.0f;
         kloop<TYPE, 1>(
             W, W, e, rt, kw, nu, HW, m, h,
             [&] {
-                sg.write(K, TB, nt, smem, tid);
+                if constexpr (F32ACT) {
+                    float* lf = reinterpret_cast<float*>(smem);
+                    for (int i = tid; i < nt * (K / 4); i += WAVES * 64) {
+                        const int j = i / (K / 4), c4 = i - j * (K / 4);
+                        *reinterpret_cast<float4*>(lf + j * K + 4 * c4) =
+                            *reinterpret_cast<const float4*>(xf + src(j) * (size_t)xf_ld + 4 * c4);
+                    }
+                } else {
+                    sg.write(K, TB, nt, smem, tid);
+                }
                 __syncthreads();
             },
             [&](const typename Fmt<TYPE>::Raw& c, const typename Fmt<TYPE>::Raw&, int u) {
-                unit_accum<TYPE, TB>(c, A, u, h, nt, G.nkb, acc);
+                if constexpr (F32ACT)
+                    unit_accum_f32<TYPE, TB>(c, A, u, h, nt, G.nkb, acc);
+                else
+                    unit_accum<TYPE, TB>(c, A, u, h, nt, G.nkb, acc);
             });
 #pragma unroll
         for (int j = 0; j < TB; ++j) {
@@ -516,7 +801,7 @@ k_gemv_gateup(QMat G, QMat U, ActQ8 xq, Groups grp, ActQ8 hq, float* hf, int hf_
 
 // Down projection into y[pair][rows].
 template <int TYPE, int TB, int WAVES, bool F32ACT>
-__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(GEMV_WAVES_PER_SIMD(TB))))
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(down_wps<TYPE, TB, F32ACT>())))
 k_gemv_down(QMat D, ActQ8 hq, const float* hf, int hf_ld, Groups grp, float* y, CombineOut comb) {
     extern __shared__ __align__(16) int8_t smem[];
     __shared__ float red[WAVES][TB][32];
@@ -551,11 +836,11 @@ k_gemv_down(QMat D, ActQ8 hq, const float* hf, int hf_ld, Groups grp, float* y, 
                 __syncthreads();
             },
             [&](const typename Fmt<TYPE>::Raw& c, const typename Fmt<TYPE>::Raw&, int u) {
-                           if constexpr (F32ACT)
-                               unit_accum_f32<TB>(c, A, u, h, nt, acc);
-                           else
-                               unit_accum<TYPE, TB>(c, A, u, h, nt, D.nkb, acc);
-                       });
+                if constexpr (F32ACT)
+                    unit_accum_f32<TYPE, TB>(c, A, u, h, nt, D.nkb, acc);
+                else
+                    unit_accum<TYPE, TB>(c, A, u, h, nt, D.nkb, acc);
+            });
 #pragma unroll
         for (int j = 0; j < TB; ++j) {
             acc[j] += __shfl_xor(acc[j], 32, 64);
@@ -624,6 +909,51 @@ struct Mx<T_Q4_K> {
         hd_scale_min(c.hd, j, sc, mn);
         rs = f16_to_f32(c.hd.x) * (float)sc;
         rmin = -f16_to_f32(c.hd.x >> 16) * (float)mn;
+    }
+};
+
+// Q5_K: as Q4_K with the fifth bits (values 0..31, exact in int8).
+template <>
+struct Mx<T_Q5_K> {
+    static constexpr int BPU = 4;  // half super-block units
+    using Raw = RawQ5K;
+    __device__ static int units(const QMat& W) { return 2 * W.nkb; }
+    __device__ static void load(Raw& c, const QMat& W, int e, int rt, int u, int m, int h, bool ok) {
+        Fmt<T_Q5_K>::load(c, W, e, rt, u, m, h, ok);
+    }
+    __device__ static uint4 bop(const Raw& c, int j, int) {
+        uint32_t w[4];
+        q5k_words(c, j, w);
+        return make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    __device__ static void scales(const Raw& c, int j, float& rs, float& rmin) {
+        int a0, b0, a1, b1;  // sub-block 4s + j (j is a constant after unrolling, s is not)
+        hd_scale_min(c.hd, j, a0, b0);
+        hd_scale_min(c.hd, 4 + j, a1, b1);
+        rs = f16_to_f32(c.hd.x) * (float)(c.s ? a1 : a0);
+        rmin = -f16_to_f32(c.hd.x >> 16) * (float)(c.s ? b1 : b0);
+    }
+};
+
+// Q6_K: lane (m, h) holds sub-block 2j + h of block j (the GEMV's split, half super-block units)
+// as 4 (q6 - 32) in int8; the two sub-blocks of a block have their own scales, so each takes one
+// MFMA with the other half's operand zeroed.
+template <>
+struct Mx<T_Q6_K> {
+    static constexpr int BPU = 4;
+    using Raw = RawQ6K;
+    __device__ static int units(const QMat& W) { return 2 * W.nkb; }
+    __device__ static void load(Raw& c, const QMat& W, int e, int rt, int u, int m, int h, bool ok) {
+        Fmt<T_Q6_K>::load(c, W, e, rt, u, m, h, ok);
+    }
+    __device__ static uint4 bop(const Raw& c, int j, int) {
+        uint32_t w[4];
+        q6_words(c, j, w);
+        return make_uint4(w[0] ^ 0x80808080u, w[1] ^ 0x80808080u, w[2] ^ 0x80808080u, w[3] ^ 0x80808080u);
+    }
+    __device__ static void scales(const Raw& c, int, float& rs, float& rmin) {
+        rs = f16_to_f32(c.d & 0xFFFFu);
+        rmin = 0.0f;
     }
 };
 
@@ -711,7 +1041,8 @@ k_gemv_mx(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_l
             float2 v = make_float2(0.0f, 0.0f);
             if (t < nt) {
                 const float2 sv = act.s[src(t) * KB + b];
-                v = make_float2(sv.x, TYPE == T_Q4_K ? sv.x * sv.y : sv.y);  // Q4_K: scale * sum; Q4_0: sum
+                // Q4_K / Q5_K: scale * sum (min term); Q4_0: sum
+                v = make_float2(sv.x, (TYPE == T_Q4_K || TYPE == T_Q5_K) ? sv.x * sv.y : sv.y);
             }
             msc[i] = v;
         }
@@ -733,10 +1064,19 @@ k_gemv_mx(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_l
 #pragma unroll
             for (int j = 0; j < BPU; ++j) {
                 const int b = u * BPU + j;
-                if (TYPE != T_Q4_K && b >= KB) break;  // wave-uniform; Q4_K units are whole super-blocks
-                const v16i_t D = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i_t, a[j]),
-                                                                       __builtin_bit_cast(v4i_t, X::bop(w, j, h)),
-                                                                       v16i_t{}, 0, 0, 0);
+                if (!is_kquant(TYPE) && b >= KB) break;  // wave-uniform; K-quant units are whole super-blocks
+                const uint4 bw = X::bop(w, j, h);
+                v16i_t D, D2;
+                if constexpr (TYPE == T_Q6_K) {
+                    const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+                    D = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i_t, a[j]),
+                                                              __builtin_bit_cast(v4i_t, h ? z : bw), v16i_t{}, 0, 0, 0);
+                    D2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i_t, a[j]),
+                                                               __builtin_bit_cast(v4i_t, h ? bw : z), v16i_t{}, 0, 0, 0);
+                } else {
+                    D = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i_t, a[j]),
+                                                              __builtin_bit_cast(v4i_t, bw), v16i_t{}, 0, 0, 0);
+                }
                 float rs, rmin;
                 X::scales(w, j, rs, rmin);
                 // tokens of registers 0-3: 4h..4h+3, of 4-7: 8+4h..11+4h (only when the pass has them)
@@ -748,9 +1088,12 @@ k_gemv_mx(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_l
 #pragma unroll
                 for (int r = 0; r < MX_NT / 2; ++r) {
                     if (r >= 4 && !hi8) break;  // pass-uniform
-                    if constexpr (TYPE == T_Q4_K) {
+                    if constexpr (TYPE == T_Q4_K || TYPE == T_Q5_K) {
                         acc[r] = __builtin_fmaf(rs * sx[r], (float)D[r], acc[r]);
                         acc[r] = __builtin_fmaf(rmin, sy[r], acc[r]);
+                    } else if constexpr (TYPE == T_Q6_K) {  // D = 4 sum((q6 - 32) y) per sub-block, exact
+                        const int isum = sbyte(w.sc, 2 * j) * (D[r] >> 2) + sbyte(w.sc, 2 * j + 1) * (D2[r] >> 2);
+                        acc[r] = __builtin_fmaf(rs * sx[r], (float)isum, acc[r]);
                     } else if constexpr (TYPE == T_Q4_0) {
                         const int isum = D[r] - 8 * (int)sy[r];  // weights are nibble - 8; sy exact (|sum| < 2^12)
                         acc[r] = __builtin_fmaf(rs * sx[r], (float)isum, acc[r]);
@@ -811,6 +1154,7 @@ constexpr int DOWN_WAVES = JX_GEMV_DOWN_WAVES;
 // 4 * MF * NTH floats).
 int gemv_max_k(bool gateup, int tb, bool f32) {
     const int nth = 64 * (gateup ? GATEUP_WAVES : DOWN_WAVES);
+    if (f32 && gateup) return (144 * 1024 / 4) / (tb <= 1 ? 1 : 4) / 256 * 256;  // staged straight into LDS
     if (f32) return (tb <= 1 ? 2 : 4) * 4 * nth / (tb <= 1 ? 1 : 4);
     const int mq = tb <= 1 ? 4 : 8, ms = tb <= 1 ? 2 : 4, rows = tb <= 1 ? 1 : 4;
     return std::min(16 * mq * nth, 32 * ms * nth) / rows;
@@ -840,10 +1184,33 @@ static int num_cus() {
 }
 
 template <int TYPE>
-static void gateup_t(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots, int tb,
-                     ActQ8 hq, float* hf, hipStream_t st, const SmallTail& tail) {
+static void gateup_q8(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots, int tb, ActQ8 hq,
+                      float* hf, int hf_ld, dim3 grid, hipStream_t st, const SmallTail& tail);
+
+template <int TYPE>
+static void gateup_t(const QMat& g, const QMat& u, const ActQ8& xq, const float* xf, int xf_ld, const Groups& grp,
+                     int slots, int tb, ActQ8 hq, float* hf, hipStream_t st, const SmallTail& tail) {
     dim3 grid(g.nrt * slots + (tail.on ? 1 : 0));
     const int hf_ld = ((g.rows + 255) / 256) * 256;
+    if (xf) {  // fp32 activations: one token, or groups of 4
+        const int rows = tb <= 1 ? 1 : 4;
+        const size_t lds = act_lds_bytes(rows, xf_ld, true);
+        auto go = [&](auto kern) {
+            lds_optin(kern, lds);
+            hipLaunchKernelGGL(kern, grid, dim3(GATEUP_WAVES * 64), lds, st, g, u, xq, xf, xf_ld, grp, hq, hf, hf_ld,
+                               tail);
+        };
+        if (rows == 1) go(k_gemv_gateup<TYPE, 1, GATEUP_WAVES, 2, true>);
+        else go(k_gemv_gateup<TYPE, 4, GATEUP_WAVES, 2, true>);
+        return;
+    }
+    if constexpr (TYPE != T_Q5_0) gateup_q8<TYPE>(g, u, xq, grp, slots, tb, hq, hf, hf_ld, grid, st, tail);
+}
+
+// The Q8_0-activation forms (not for Q5_0).
+template <int TYPE>
+static void gateup_q8(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots, int tb, ActQ8 hq,
+                      float* hf, int hf_ld, dim3 grid, hipStream_t st, const SmallTail& tail) {
     if (tb <= 1) {
         const size_t lds = act_lds_bytes(1, xq.K, false);
         // every block resident at 3 waves per SIMD: the spill-free build (measured: Qwen3-shaped 32.6 -> 31.0 us,
@@ -851,7 +1218,8 @@ static void gateup_t(const QMat& g, const QMat& u, const ActQ8& xq, const Groups
         const bool w3 = (size_t)grid.x * GATEUP_WAVES <= (size_t)3 * 4 * num_cus();
         auto go = [&](auto kern) {
             lds_optin(kern, lds);
-            hipLaunchKernelGGL(kern, grid, dim3(GATEUP_WAVES * 64), lds, st, g, u, xq, grp, hq, hf, hf_ld, tail);
+            hipLaunchKernelGGL(kern, grid, dim3(GATEUP_WAVES * 64), lds, st, g, u, xq, nullptr, 0, grp, hq, hf, hf_ld,
+                               tail);
         };
         if (w3) go(k_gemv_gateup<TYPE, 1, GATEUP_WAVES, 3>);
         else go(k_gemv_gateup<TYPE, 1, GATEUP_WAVES, 4>);
@@ -859,7 +1227,7 @@ static void gateup_t(const QMat& g, const QMat& u, const ActQ8& xq, const Groups
         const size_t lds = act_lds_bytes(4, xq.K, false);
         lds_optin(k_gemv_gateup<TYPE, 4, GATEUP_WAVES>, lds);
         hipLaunchKernelGGL((k_gemv_gateup<TYPE, 4, GATEUP_WAVES>), grid, dim3(GATEUP_WAVES * 64), lds, st, g, u, xq,
-                           grp, hq, hf, hf_ld, tail);
+                           nullptr, 0, grp, hq, hf, hf_ld, tail);
     } else {  // several tokens per expert: the matrix-core form
         const size_t lds = (size_t)(xq.K / 32) * MX_NT * sizeof(float2);
         lds_optin(k_gemv_mx<TYPE, true, GATEUP_WAVES>, lds);
@@ -869,12 +1237,17 @@ static void gateup_t(const QMat& g, const QMat& u, const ActQ8& xq, const Groups
 }
 
 void launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots, int tb,
-                        ActQ8 hq, float* hf, hipStream_t st, const SmallTail* tail) {
+                        ActQ8 hq, float* hf, hipStream_t st, const SmallTail* tail, const float* xf, int xf_ld) {
     const SmallTail t = tail ? *tail : SmallTail{};
     switch (g.type) {
-        case T_Q4_0: gateup_t<T_Q4_0>(g, u, xq, grp, slots, tb, hq, hf, st, t); break;
-        case T_Q8_0: gateup_t<T_Q8_0>(g, u, xq, grp, slots, tb, hq, hf, st, t); break;
-        case T_Q4_K: gateup_t<T_Q4_K>(g, u, xq, grp, slots, tb, hq, hf, st, t); break;
+        case T_Q4_0: gateup_t<T_Q4_0>(g, u, xq, xf, xf_ld, grp, slots, tb, hq, hf, st, t); break;
+        case T_Q8_0: gateup_t<T_Q8_0>(g, u, xq, xf, xf_ld, grp, slots, tb, hq, hf, st, t); break;
+        case T_Q4_K: gateup_t<T_Q4_K>(g, u, xq, xf, xf_ld, grp, slots, tb, hq, hf, st, t); break;
+        case T_Q5_K: gateup_t<T_Q5_K>(g, u, xq, xf, xf_ld, grp, slots, tb, hq, hf, st, t); break;
+        case T_Q6_K: gateup_t<T_Q6_K>(g, u, xq, xf, xf_ld, grp, slots, tb, hq, hf, st, t); break;
+        case T_Q5_0:  // fp32 activations only
+            if (xf) gateup_t<T_Q5_0>(g, u, xq, xf, xf_ld, grp, slots, tb, hq, hf, st, t);
+            break;
         default: break;
     }
 }
@@ -890,10 +1263,12 @@ static void down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, 
         hipLaunchKernelGGL((k_gemv_down<TYPE, 1, DOWN_WAVES, F32ACT>), grid, dim3(DOWN_WAVES * 64), lds, st, dn, hq,
                            hf, hf_ld, grp, y, comb);
     } else if (tb > 4 && !F32ACT) {  // several tokens per expert: the matrix-core form
-        const size_t lds = (size_t)(K / 32) * MX_NT * sizeof(float2);
-        lds_optin(k_gemv_mx<TYPE, false, DOWN_WAVES>, lds);
-        hipLaunchKernelGGL((k_gemv_mx<TYPE, false, DOWN_WAVES>), grid, dim3(DOWN_WAVES * 64), lds, st, dn, dn, hq,
-                           grp, ActQ8{}, nullptr, 0, y, SmallTail{});
+        if constexpr (!F32ACT) {
+            const size_t lds = (size_t)(K / 32) * MX_NT * sizeof(float2);
+            lds_optin(k_gemv_mx<TYPE, false, DOWN_WAVES>, lds);
+            hipLaunchKernelGGL((k_gemv_mx<TYPE, false, DOWN_WAVES>), grid, dim3(DOWN_WAVES * 64), lds, st, dn, dn,
+                               hq, grp, ActQ8{}, nullptr, 0, y, SmallTail{});
+        }
     } else {
         const size_t lds = act_lds_bytes(4, K, F32ACT);
         lds_optin(k_gemv_down<TYPE, 4, DOWN_WAVES, F32ACT>, lds);
@@ -906,14 +1281,24 @@ void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_l
                       int tb, float* y, hipStream_t st, const CombineOut& comb) {
     // the folded combine is written for the single-token and four-token GEMVs (the few-token path)
     const CombineOut c = tb <= 4 ? comb : CombineOut{};
-    if (hf) {
-        down_t<T_Q4_K, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c);
+    if (hf) {  // fp32 activations
+        switch (dn.type) {
+            case T_Q4_0: down_t<T_Q4_0, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
+            case T_Q5_0: down_t<T_Q5_0, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
+            case T_Q8_0: down_t<T_Q8_0, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
+            case T_Q4_K: down_t<T_Q4_K, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
+            case T_Q5_K: down_t<T_Q5_K, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
+            case T_Q6_K: down_t<T_Q6_K, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
+            default: break;
+        }
         return;
     }
     switch (dn.type) {
         case T_Q4_0: down_t<T_Q4_0, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
         case T_Q8_0: down_t<T_Q8_0, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
         case T_Q4_K: down_t<T_Q4_K, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
+        case T_Q5_K: down_t<T_Q5_K, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
+        case T_Q6_K: down_t<T_Q6_K, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
         default: break;
     }
 }

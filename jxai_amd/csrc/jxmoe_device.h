@@ -6,7 +6,10 @@
 
 namespace jx {
 
-enum : int { T_F32 = 0, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12 };
+enum : int { T_F32 = 0, T_Q4_0 = 2, T_Q5_0 = 6, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14 };
+
+// Super-block formats (256 elements per K-unit, Q4_K-style header for Q4_K and Q5_K).
+__host__ __device__ constexpr bool is_kquant(int t) { return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
 
 constexpr int WAVE = 64;
 constexpr int ROWS_PER_TILE = 32;   // weight rows per repacked tile (= one MFMA M/N edge)

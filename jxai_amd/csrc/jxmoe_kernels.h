@@ -14,13 +14,20 @@ namespace jx {
 //   Q8_0  qs  [e][rt][b][2 halves][32 rows][16 B]  sc  [e][rt][b][32] fp16 d
 //   Q4_K  qs  [e][rt][sb][4 pairs][2 halves][32 rows][16 B]
 //         sc  [e][rt][sb][32 rows][16 B]  = (d, dmin, scales[12]) headers
-// Byte totals of qs+sc equal the GGUF tensor (18/34/144 B per block).
+//   Q5_0  qs  [e][rt][b][32 rows][16 B]           sc  [e][rt][b][32] fp16 d
+//         ex  [e][rt][b][32] u32 qh (fifth bits)
+//   Q5_K  qs, sc as Q4_K;  ex [e][rt][sb][2 halves][32 rows][16 B] = qh bytes 16h..16h+15
+//   Q6_K  qs  [e][rt][sb][2 halves n][6 chunks c][32 rows][16 B]: c < 4 = ql bytes 64n + 16c ..,
+//             c = 4, 5 = qh bytes 32n + 16(c - 4) ..
+//         sc  [e][rt][sb][32 rows][16 B] = the 16 int8 sub-block scales
+//         ex  [e][rt][sb][32] fp16 d
+// Byte totals of qs+sc(+ex) equal the GGUF tensor (18/34/144/22/176/210 B per block).
 struct QMat {
     int type = 0;
     int rows = 0;       // per expert, multiple of 32
     int cols = 0;       // K
     int nrt = 0;        // rows / 32
-    int nkb = 0;        // K-units: 32-blocks (Q4_0/Q8_0) or 256-super-blocks (Q4_K)
+    int nkb = 0;        // K-units: 32-blocks (Q4_0/Q5_0/Q8_0) or 256-super-blocks (Q4_K/Q5_K/Q6_K)
     const uint8_t* qs = nullptr;
     const uint8_t* sc = nullptr;
     size_t qs_es = 0, sc_es = 0;  // per-expert strides (bytes)
@@ -29,7 +36,12 @@ struct QMat {
     // issues for units it will not use read here (uniform instruction streams).
     const uint8_t* pad_qs = nullptr;
     const uint8_t* pad_sc = nullptr;
-    // Q4_K min-term table for the matrix-core GEMMs (launch_min_table; null for
+    // Third region of the five- and six-bit formats (Q5_0 / Q5_K high bits, Q6_K d), its
+    // per-expert stride and zeroed pad; null for the others.
+    const uint8_t* ex = nullptr;
+    size_t ex_es = 0;
+    const uint8_t* pad_ex = nullptr;
+    // Q4_K / Q5_K min-term table for the matrix-core GEMMs (launch_min_table; null for
     // other types and for matrices only the GEMVs read): per (expert, row tile,
     // super-block) 3 x [32 rows][16 B] = the bf16 pieces (hi, mid, lo) of
     // -dmin * m_j / u for the 8 sub-blocks j, u = d (1 where d is zero).
@@ -173,9 +185,12 @@ void chain_rows(const float* rows, int nrows, int d, float* out);
 void launch_dispatch(const int* ids, int nk, int E, int top_k, const DispatchOut& o, hipStream_t st);
 
 // Decode regime: gate+up dequant-GEMV with SwiGLU and Q8_0 re-quantization.
-// Output rows are sorted pairs (routed) or tokens (shared).
+// Output rows are sorted pairs (routed) or tokens (shared).  With xf, the
+// fp32-activation dots over rows of xf_ld floats (zero-padded to whole K-units;
+// one token or groups of 4) instead of the Q8_0 form xq.
 void launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots,
-                        int tb, ActQ8 hq, float* hf, hipStream_t st, const SmallTail* tail = nullptr);
+                        int tb, ActQ8 hq, float* hf, hipStream_t st, const SmallTail* tail = nullptr,
+                        const float* xf = nullptr, int xf_ld = 0);
 // Largest K the GEMVs accept for token groups of `tb` rows (gate/up or down,
 // Q8_0 or fp32 activations).
 int gemv_max_k(bool gateup, int tb, bool f32);
@@ -188,7 +203,10 @@ void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_l
 void launch_mfma_gateup(const QMat& g, const QMat& u, const ActH& xin, const Groups& grp, int tiles_ub,
                         const ActQ8& hq, float* hf, hipStream_t st);
 void launch_mfma_down(const QMat& dn, const ActH& hin, const Groups& grp, int tiles_ub, float* y, hipStream_t st);
-// Fill m.mn (m.n_mats * m.nrt * m.nkb * 1536 bytes) from a repacked Q4_K matrix.
+// Weight types the matrix-core gate/up GEMM takes (Q5_0 has no Q8_0-activation form; Q6_K's sc * q
+// operand is not exact in fp16, and gate/up products must be: h is re-quantized).
+bool gemm_gateup_ok(int type);
+// Fill m.mn (m.n_mats * m.nrt * m.nkb * 1536 bytes) from a repacked Q4_K or Q5_K matrix.
 void launch_min_table(const QMat& m, uint8_t* mn, hipStream_t st);
 
 // acc[t] = sum_s p[t][s] * y[pos(t,s)] (+ shscale[t] * ysh[t]), fma in selection order;
@@ -218,17 +236,18 @@ void launch_route_small(const RouteArgs& a, const DispatchOut& o, hipStream_t st
 
 // Q8_0 of rows x K fp32 (row-major, K % 32 == 0).
 void launch_quantize_q8(const float* x, int rows, int K, ActQ8 out, hipStream_t st);
-// dst[0 .. kpad) = x[0 .. n) then zeros.
-void launch_copy_pad(const float* x, int n, int kpad, float* dst, hipStream_t st);
+// dst[r][0 .. kpad) = x[r][0 .. n) then zeros, for rows r (x rows of n floats).
+void launch_copy_pad(const float* x, int n, int kpad, float* dst, hipStream_t st, int rows = 1);
 
 // Matrix-core form of existing Q8_0 activations (int8 quants + (scale, sum)).
 // lo = false writes only the fp16 hi halves (the down GEMM's operand).
 void launch_q8_to_acth(const ActQ8& in, int rows, ActH out, hipStream_t st, bool lo = true);
-// Matrix-core form (hi only) of fp32 activation rows [rows][ld], ld = out.K % 256 == 0, zero-padded.
+// Matrix-core form (hi only) of fp32 activation rows [rows][ld] (out.K % 128 == 0, columns up to
+// out.K zero-padded).
 void launch_f32_to_acth(const float* h, int ld, int rows, ActH out, hipStream_t st);
 
 // Repack a GGUF block matrix set [n_mats][rows][cols] (already on the device
 // as raw bytes) into the QMat layout.
-void launch_repack(const uint8_t* raw, QMat m, uint8_t* qs, uint8_t* sc, hipStream_t st);
+void launch_repack(const uint8_t* raw, QMat m, uint8_t* qs, uint8_t* sc, uint8_t* ex, hipStream_t st);
 
 }  // namespace jx

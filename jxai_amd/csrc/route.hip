@@ -607,10 +607,11 @@ void launch_q8_to_acth(const ActQ8& in, int rows, ActH out, hipStream_t st, bool
     hipLaunchKernelGGL(k_q8_to_acth, dim3((rows + 3) / 4), dim3(256), 0, st, in, rows, out, lo ? 1 : 0);
 }
 
-// Matrix-core form (fp16 hi only) of fp32 activation rows h [rows][ld], ld =
-// out.K a multiple of 256 with zero padding past the real columns (the
-// reference's fp32-activation products, vec_dot_q4_K_f32, src/quant.cpp:2910-3013,
-// for a down projection whose K is not a multiple of 256).  One block per
+// Matrix-core form (fp16 hi only) of fp32 activation rows h [rows][ld], out.K
+// a multiple of 128 (K-quants: 256, zero padding past the real columns) -- the
+// reference's fp32-activation products (vec_dot_quant_f32, src/quant.cpp:3269-3305)
+// for a down projection without a Q8_0 form (Q5_0, or a K-quant whose K is not
+// a multiple of 256).  One block per
 // row: E = exponent(max |h|) - 14 so every h * 2^-E is below 2^15; hi =
 // fp16(h * 2^-E) (relative error <= 2^-12 per value, as the Q8_0 down operand);
 // the min-term value of each 32-block is its fp32 sum times 2^-E, split into
@@ -1216,11 +1217,13 @@ __global__ void __launch_bounds__(256) k_quant_q8(const float* x, int rows, int 
 // fp32-activation GEMV reads (written by a kernel, so a captured graph holds no memset node).
 __global__ void __launch_bounds__(256) k_copy_pad(const float* x, int n, int kpad, float* dst) {
     const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < kpad) dst[i] = i < n ? x[i] : 0.0f;
+    const size_t row = blockIdx.y;
+    if (i < kpad) dst[row * kpad + i] = i < n ? x[row * n + i] : 0.0f;
 }
 
-void launch_copy_pad(const float* x, int n, int kpad, float* dst, hipStream_t st) {
-    hipLaunchKernelGGL(k_copy_pad, dim3((unsigned)((kpad + 255) / 256)), dim3(256), 0, st, x, n, kpad, dst);
+void launch_copy_pad(const float* x, int n, int kpad, float* dst, hipStream_t st, int rows) {
+    hipLaunchKernelGGL(k_copy_pad, dim3((unsigned)((kpad + 255) / 256), (unsigned)rows), dim3(256), 0, st, x, n, kpad,
+                       dst);
 }
 
 void launch_quantize_q8(const float* x, int rows, int K, ActQ8 out, hipStream_t st) {
@@ -1231,7 +1234,7 @@ void launch_quantize_q8(const float* x, int rows, int K, ActQ8 out, hipStream_t 
 
 // One thread per (matrix, row, K-unit): scatter a GGUF block into the tile
 // layout described in jxmoe_kernels.h.
-__global__ void __launch_bounds__(256) k_repack(const uint8_t* raw, QMat m, uint8_t* qs, uint8_t* sc) {
+__global__ void __launch_bounds__(256) k_repack(const uint8_t* raw, QMat m, uint8_t* qs, uint8_t* sc, uint8_t* ex) {
     const size_t units = (size_t)m.n_mats * m.rows * m.nkb;
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= units) return;
@@ -1255,21 +1258,44 @@ __global__ void __launch_bounds__(256) k_repack(const uint8_t* raw, QMat m, uint
         }
         sc[(tile * 32 + mm) * 2 + 0] = src[0];
         sc[(tile * 32 + mm) * 2 + 1] = src[1];
-    } else {  // Q4_K
-        const uint8_t* src = raw + idx * 144;
+    } else if (m.type == T_Q5_0) {  // block_q5_0: d, qh (u32), qs[16]
+        const uint8_t* src = raw + idx * 22;
+        uint8_t* dq = qs + (tile * 32 + mm) * 16;
+        for (int i = 0; i < 16; ++i) dq[i] = src[6 + i];
+        sc[(tile * 32 + mm) * 2 + 0] = src[0];
+        sc[(tile * 32 + mm) * 2 + 1] = src[1];
+        for (int i = 0; i < 4; ++i) ex[(tile * 32 + mm) * 4 + i] = src[2 + i];
+    } else if (m.type == T_Q6_K) {  // block_q6_K: ql[128], qh[64], scales[16], d
+        const uint8_t* src = raw + idx * 210;
+        for (int n = 0; n < 2; ++n)
+            for (int c = 0; c < 6; ++c) {
+                const uint8_t* s = c < 4 ? src + 64 * n + 16 * c : src + 128 + 32 * n + 16 * (c - 4);
+                uint8_t* dq = qs + (((tile * 2 + n) * 6 + c) * 32 + mm) * 16;
+                for (int i = 0; i < 16; ++i) dq[i] = s[i];
+            }
+        for (int i = 0; i < 16; ++i) sc[(tile * 32 + mm) * 16 + i] = src[192 + i];
+        ex[(tile * 32 + mm) * 2 + 0] = src[208];
+        ex[(tile * 32 + mm) * 2 + 1] = src[209];
+    } else {  // Q4_K (144 B: header, qs[128]) or Q5_K (176 B: header, qh[32], qs[128])
+        const bool q5 = m.type == T_Q5_K;
+        const uint8_t* src = raw + idx * (q5 ? 176 : 144);
+        const uint8_t* sq = src + (q5 ? 48 : 16);
         uint8_t* dh = sc + (tile * 32 + mm) * 16;
         for (int i = 0; i < 16; ++i) dh[i] = src[i];
         for (int p = 0; p < 4; ++p)
             for (int h = 0; h < 2; ++h) {
                 uint8_t* dq = qs + (((tile * 4 + p) * 2 + h) * 32 + mm) * 16;
-                for (int i = 0; i < 16; ++i) dq[i] = src[16 + 32 * p + 16 * h + i];
+                for (int i = 0; i < 16; ++i) dq[i] = sq[32 * p + 16 * h + i];
             }
+        if (q5)
+            for (int h = 0; h < 2; ++h)
+                for (int i = 0; i < 16; ++i) ex[((tile * 2 + h) * 32 + mm) * 16 + i] = src[16 + 16 * h + i];
     }
 }
 
-void launch_repack(const uint8_t* raw, QMat m, uint8_t* qs, uint8_t* sc, hipStream_t st) {
+void launch_repack(const uint8_t* raw, QMat m, uint8_t* qs, uint8_t* sc, uint8_t* ex, hipStream_t st) {
     const size_t units = (size_t)m.n_mats * m.rows * m.nkb;
-    hipLaunchKernelGGL(k_repack, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, st, raw, m, qs, sc);
+    hipLaunchKernelGGL(k_repack, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, st, raw, m, qs, sc, ex);
 }
 
 }  // namespace jx

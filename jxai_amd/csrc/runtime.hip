@@ -50,21 +50,28 @@ int fail(int code, const std::string& msg) {
                         std::string(#expr) + ": " + hipGetErrorString(e_));                       \
     } while (0)
 
-bool expert_type_ok(int t) { return t == jx::T_Q4_0 || t == jx::T_Q8_0 || t == jx::T_Q4_K; }
+bool expert_type_ok(int t) {
+    return t == jx::T_Q4_0 || t == jx::T_Q5_0 || t == jx::T_Q8_0 || t == jx::T_Q4_K || t == jx::T_Q5_K ||
+           t == jx::T_Q6_K;
+}
 
+// ggml_type_size / tensor_byte_size (include/common.h:154-195)
 size_t row_bytes(int t, int64_t cols) {
     switch (t) {
         case jx::T_Q4_0: return (size_t)((cols + 31) / 32) * 18;
+        case jx::T_Q5_0: return (size_t)((cols + 31) / 32) * 22;
         case jx::T_Q8_0: return (size_t)((cols + 31) / 32) * 34;
         case jx::T_Q4_K: return (size_t)((cols + 255) / 256) * 144;
+        case jx::T_Q5_K: return (size_t)((cols + 255) / 256) * 176;
+        case jx::T_Q6_K: return (size_t)((cols + 255) / 256) * 210;
         default: return 0;
     }
 }
 
-// supports_q8_activation (src/quant.cpp:3881-3893)
+// supports_q8_activation (src/quant.cpp:3881-3893): Q5_0 always takes fp32 activations
 bool q8_activation(int t, int64_t cols) {
     if (t == jx::T_Q4_0 || t == jx::T_Q8_0) return cols % 32 == 0;
-    if (t == jx::T_Q4_K) return cols % 256 == 0;
+    if (jx::is_kquant(t)) return cols % 256 == 0;
     return false;
 }
 
@@ -72,20 +79,21 @@ struct DevMat {
     jx::QMat m;
     uint8_t* qs = nullptr;
     uint8_t* sc = nullptr;
-    uint8_t* mn = nullptr;  // Q4_K min-term table (matrix-core GEMMs)
+    uint8_t* ex = nullptr;  // Q5_0 / Q5_K high bits, Q6_K d
+    uint8_t* mn = nullptr;  // Q4_K / Q5_K min-term table (matrix-core GEMMs)
     void release() {
-        if (qs) (void)hipFree(qs);
-        if (sc) (void)hipFree(sc);
-        if (mn) (void)hipFree(mn);
-        qs = sc = mn = nullptr;
+        for (uint8_t* p : {qs, sc, ex, mn})
+            if (p) (void)hipFree(p);
+        qs = sc = ex = mn = nullptr;
     }
 };
 
 // Upload n_mats [rows][cols] block matrices and repack them on the device;
-// with `gemm`, Q4_K matrices also get the matrix-core GEMMs' min-term table.
+// with `gemm`, Q4_K / Q5_K matrices also get the matrix-core GEMMs' min-term table.
 int upload_matrix(int type, int n_mats, int rows, int cols, const void* host, DevMat& out, hipStream_t st,
                   bool gemm = false) {
-    if (!expert_type_ok(type)) return fail(JX_ERR_UNSUPPORTED, "expert weight type must be Q4_0, Q8_0 or Q4_K");
+    if (!expert_type_ok(type))
+        return fail(JX_ERR_UNSUPPORTED, "expert weight type must be Q4_0, Q5_0, Q8_0, Q4_K, Q5_K or Q6_K");
     if (rows % jx::ROWS_PER_TILE != 0) return fail(JX_ERR_UNSUPPORTED, "matrix rows must be a multiple of 32");
     if (cols % 32 != 0) return fail(JX_ERR_UNSUPPORTED, "matrix cols must be a multiple of 32");
     jx::QMat& m = out.m;
@@ -93,13 +101,22 @@ int upload_matrix(int type, int n_mats, int rows, int cols, const void* host, De
     m.rows = rows;
     m.cols = cols;
     m.nrt = rows / jx::ROWS_PER_TILE;
-    m.nkb = type == jx::T_Q4_K ? (cols + 255) / 256 : cols / 32;
+    m.nkb = jx::is_kquant(type) ? (cols + 255) / 256 : cols / 32;
     m.n_mats = n_mats;
     const size_t units = (size_t)rows * m.nkb;
-    const size_t qs_u = type == jx::T_Q4_0 ? 16 : (type == jx::T_Q8_0 ? 32 : 128);
-    const size_t sc_u = type == jx::T_Q4_K ? 16 : 2;
+    // bytes per row and K-unit of each region (qs + sc + ex = the GGUF block)
+    size_t qs_u = 0, sc_u = 0, ex_u = 0;
+    switch (type) {
+        case jx::T_Q4_0: qs_u = 16, sc_u = 2; break;
+        case jx::T_Q5_0: qs_u = 16, sc_u = 2, ex_u = 4; break;
+        case jx::T_Q8_0: qs_u = 32, sc_u = 2; break;
+        case jx::T_Q4_K: qs_u = 128, sc_u = 16; break;
+        case jx::T_Q5_K: qs_u = 128, sc_u = 16, ex_u = 32; break;
+        default: qs_u = 192, sc_u = 16, ex_u = 2; break;  // Q6_K
+    }
     m.qs_es = units * qs_u;
     m.sc_es = units * sc_u;
+    m.ex_es = units * ex_u;
     // the GEMMs address one expert's matrix with 32-bit offsets (min table: 12x the headers)
     if (m.qs_es >= ((size_t)1 << 32) || m.sc_es * 12 >= ((size_t)1 << 32))
         return fail(JX_ERR_UNSUPPORTED, "one expert matrix exceeds 4 GiB");
@@ -111,15 +128,21 @@ int upload_matrix(int type, int n_mats, int rows, int cols, const void* host, De
     HIPCHK(hipMemsetAsync(out.sc + m.sc_es * n_mats, 0, jx::QMAT_PAD, st));
     m.pad_qs = out.qs + m.qs_es * n_mats;
     m.pad_sc = out.sc + m.sc_es * n_mats;
+    if (ex_u) {
+        HIPCHK(hipMalloc(&out.ex, m.ex_es * n_mats + jx::QMAT_PAD));
+        HIPCHK(hipMemsetAsync(out.ex + m.ex_es * n_mats, 0, jx::QMAT_PAD, st));
+        m.pad_ex = out.ex + m.ex_es * n_mats;
+    }
     HIPCHK(hipMalloc(&raw, raw_bytes));
     hipError_t e = hipMemcpyAsync(raw, host, raw_bytes, hipMemcpyHostToDevice, st);
     if (e == hipSuccess) {
         m.qs = out.qs;
         m.sc = out.sc;
-        jx::launch_repack(raw, m, out.qs, out.sc, st);
+        m.ex = out.ex;
+        jx::launch_repack(raw, m, out.qs, out.sc, out.ex, st);
         e = hipGetLastError();
     }
-    if (e == hipSuccess && gemm && type == jx::T_Q4_K) {
+    if (e == hipSuccess && gemm && (type == jx::T_Q4_K || type == jx::T_Q5_K)) {
         m.mn_es = (size_t)m.nrt * m.nkb * 1536;
         e = hipMalloc(&out.mn, m.mn_es * n_mats);
         if (e == hipSuccess) {
@@ -187,6 +210,10 @@ struct jx_moe_layer {
     int device = 0;
     int E = 0, k = 0, d = 0, F = 0, Fs = 0;
     bool shared = false, down_f32 = false, sdown_f32 = false;
+    // gate/up over fp32 activations (no Q8_0 form at d_model: Q5_0, or a K-quant with d_model % 256 != 0),
+    // routed / shared; they read xf, x zero-padded to dpad columns
+    bool gu_f32 = false, sgu_f32 = false;
+    int dpad = 0;
     float* router = nullptr;
     float* ffn_norm = nullptr;   // [d] or null (weight 1)
     float* post_norm = nullptr;  // [d] or null (no post_ffw_norm)
@@ -205,7 +232,7 @@ struct jx_moe_layer {
     int4* slots = nullptr;
     jx::ActQ8 xq, hq, hqs;
     DevActH xh, hh, hhs;  // matrix-core forms of x, h, shared h
-    float *hf = nullptr, *hfs = nullptr, *y = nullptr, *ysh = nullptr;
+    float *hf = nullptr, *hfs = nullptr, *y = nullptr, *ysh = nullptr, *xf = nullptr;
     int last_n = 0;
     Prof prof;
     hipStream_t own = nullptr;  // used when the caller passes the null stream
@@ -249,6 +276,10 @@ struct jx_qmatrix {
 
 namespace {
 
+// K of a down projection's matrix-core activation form: d_ff, or for fp32 h of a K-quant d_ff padded to
+// whole super-blocks (the fp32 rows are stored padded that far).
+int down_h_k(int type, int f, bool f32) { return f32 && jx::is_kquant(type) ? (f + 255) / 256 * 256 : f; }
+
 int ensure_workspace(jx_moe_layer* L, int n) {
     if (n <= L->cap) return JX_OK;
     // captured graphs hold the old buffer addresses
@@ -278,12 +309,14 @@ int ensure_workspace(jx_moe_layer* L, int n) {
     WS(L->n_tiles, 1);
     WS(L->tiles, nk / jx::MFMA_BN + std::min<size_t>(L->E, nk) + 1);
     WS(L->slots, L->E);
-    // h's matrix-core form: K = d_ff, or d_ff padded to whole super-blocks for fp32 h
-    const int hK = L->down_f32 ? (L->F + 255) / 256 * 256 : L->F;
-    const int hKs = L->sdown_f32 ? (L->Fs + 255) / 256 * 256 : L->Fs;
-    // x's forms: block-unit for Q4_K gate/up matrices, hi/lo for the others (routed and shared)
-    const bool xunit = L->gate.m.type == jx::T_Q4_K || (L->shared && L->sgate.m.type == jx::T_Q4_K);
-    const bool xhilo = L->gate.m.type != jx::T_Q4_K || (L->shared && L->sgate.m.type != jx::T_Q4_K);
+    // h's matrix-core form: K = d_ff, or for fp32 h of a K-quant d_ff padded to whole super-blocks
+    const int hK = down_h_k(L->down.m.type, L->F, L->down_f32);
+    const int hKs = L->shared ? down_h_k(L->sdown.m.type, L->Fs, L->sdown_f32) : 0;
+    // x's forms for the gate/up GEMMs: block-unit for Q4_K / Q5_K, hi/lo for Q4_0 / Q8_0 (routed and shared)
+    auto unit_t = [](int t) { return t == jx::T_Q4_K || t == jx::T_Q5_K; };
+    auto hilo_t = [](int t) { return t == jx::T_Q4_0 || t == jx::T_Q8_0; };
+    const bool xunit = unit_t(L->gate.m.type) || (L->shared && unit_t(L->sgate.m.type));
+    const bool xhilo = hilo_t(L->gate.m.type) || (L->shared && hilo_t(L->sgate.m.type));
     if ((r = L->xh.alloc((size_t)cap, L->d, xhilo, xunit)) != JX_OK || (r = L->hh.alloc(nk, hK)) != JX_OK) {
         L->cap = 0;
         return r;
@@ -299,6 +332,10 @@ int ensure_workspace(jx_moe_layer* L, int n) {
     WS(L->hq.s, nk * L->F / 32);
     L->hq.K = L->F;
     WS(L->y, nk * L->d);
+    if (L->gu_f32 || L->sgu_f32) {
+        WS(L->xf, (size_t)cap * L->dpad);
+        HIPCHK(hipMemset(L->xf, 0, (size_t)cap * L->dpad * sizeof(float)));
+    }
     const size_t fpad = ((size_t)L->F + 255) / 256 * 256;
     if (L->down_f32) {
         WS(L->hf, nk * fpad);
@@ -325,7 +362,8 @@ void free_layer(jx_moe_layer* L) {
     for (auto* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown}) m->release();
     void* ptrs[] = {L->router, L->router_cm, L->bias, L->shgate, L->ffn_norm, L->post_norm, L->xn, L->x, L->out, L->probs, L->shscale, L->logits, L->ids,
                     L->counts, L->offs, L->act, L->n_act, L->pair_tok, L->pos_of, L->n_tiles, L->tiles,
-                    L->slots, L->xq.q, L->xq.s, L->hq.q, L->hq.s, L->hqs.q, L->hqs.s, L->hf, L->hfs, L->y, L->ysh};
+                    L->slots, L->xq.q, L->xq.s, L->hq.q, L->hq.s, L->hqs.q, L->hqs.s, L->hf, L->hfs, L->y, L->ysh,
+                    L->xf};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     L->xh.release();
@@ -408,15 +446,26 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     bool mfma = (size_t)nk >= (size_t)min_ppe * E;
     if (flags & JX_FWD_FORCE_GEMV) mfma = false;
     if (flags & JX_FWD_FORCE_MFMA) mfma = true;
-    // the matrix-core GEMMs stage K in 128-element half-units; their Q4_K matrices carry the min table
-    auto ready = [](const DevMat& M) { return M.m.type != jx::T_Q4_K || M.m.mn != nullptr; };
-    const bool mfma_shape = d % 128 == 0 && (L->down_f32 || L->F % 128 == 0) && ready(L->gate) && ready(L->up) &&
-                            ready(L->down);
-    mfma = mfma && mfma_shape;
-    const bool smfma = L->shared && n >= jx::MFMA_MIN_SHARED_TOKENS && !(flags & JX_FWD_FORCE_GEMV) && d % 128 == 0 &&
-                       (L->sdown_f32 || L->Fs % 128 == 0) && ready(L->sgate) && ready(L->sup) && ready(L->sdown);
-    jx::RouteArgs ra{xdev, n, d, E, k, L->router, L->bias, L->shgate, L->xq, (mfma || smfma) ? L->xh.a : jx::ActH{},
-                     L->ids, L->probs, L->shscale, L->logits, L->router_cm};
+    // The matrix-core GEMMs stage K in 128-element half-units; their Q4_K / Q5_K matrices carry the min
+    // table.  Gate/up takes the GEMM only with a Q8_0 form of x and a type whose products stay exact
+    // there (gemm_gateup_ok); otherwise it runs on the GEMVs (the multi-token form at prefill sizes)
+    // and the down projection still decides for itself.
+    auto ready = [](const DevMat& M) {
+        return !(M.m.type == jx::T_Q4_K || M.m.type == jx::T_Q5_K) || M.m.mn != nullptr;
+    };
+    auto gu_gemm = [&](const DevMat& G, const DevMat& U, bool f32) {
+        return !f32 && jx::gemm_gateup_ok(G.m.type) && d % 128 == 0 && ready(G) && ready(U);
+    };
+    auto dn_gemm = [&](const DevMat& D, int f, bool f32) { return down_h_k(D.m.type, f, f32) % 128 == 0 && ready(D); };
+    const bool mfma_gu = mfma && gu_gemm(L->gate, L->up, L->gu_f32);
+    const bool dn_shape = dn_gemm(L->down, L->F, L->down_f32);
+    const bool smfma = L->shared && n >= jx::MFMA_MIN_SHARED_TOKENS && !(flags & JX_FWD_FORCE_GEMV);
+    const bool smfma_gu = smfma && gu_gemm(L->sgate, L->sup, L->sgu_f32);
+    const bool smfma_dn = smfma && dn_gemm(L->sdown, L->Fs, L->sdown_f32);
+    mfma = mfma && (mfma_gu || dn_shape);
+    jx::RouteArgs ra{xdev, n, d, E, k, L->router, L->bias, L->shgate, L->xq,
+                     (mfma_gu || smfma_gu) ? L->xh.a : jx::ActH{}, L->ids, L->probs, L->shscale, L->logits,
+                     L->router_cm};
     const jx::DispatchOut dout{L->counts, L->offs,   L->act,   L->n_act, L->pair_tok,
                                L->pos_of,  L->tiles, L->n_tiles, L->slots};
     // few-token decode: logits on one block per router row, grouping in the GEMVs
@@ -430,10 +479,10 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         return n == 1 ? 1 : (tokens_per_expert_x2 >= (q8w ? 1 : 5) ? 16 : 4);
     };
     const int tb = gemv_tb(2 * nk / E);
-    // fp32 h (Q4_K down with d_ff % 256 != 0) takes the matrix-core down GEMM from 2 tokens on (every
-    // dispatch path writes the MFMA tiles, the few-token one from the gate/up GEMV's tail block): the
-    // fp32 GEMV's multi-token form re-streams the weights per group of 4 tokens in fp32
-    const bool mfma_down = mfma || (L->down_f32 && n >= 2 && mfma_shape);
+    // fp32 h (no Q8_0 form at d_ff) takes the matrix-core down GEMM from 2 tokens on (every dispatch path
+    // writes the MFMA tiles, the few-token one from the gate/up GEMV's tail block): the fp32 GEMV's
+    // multi-token form re-streams the weights per group of 4 tokens in fp32
+    const bool mfma_down = (mfma || (L->down_f32 && n >= 2)) && dn_shape;
     // The weighted combine folds into the down GEMV when the few-token routers run and every output
     // element receives at most two contributions (top_k <= 2, no shared expert; CombineOut).
     const bool fold = jx::route_small_fits(n, d, E) && k <= 2 && !L->shared && !mfma_down && tb <= 4 &&
@@ -450,7 +499,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
             Launch l(L, "route_dispatch", st);
             jx::launch_route_small(ra, dout, st);
         }
-        if (mfma || smfma) {
+        if (mfma_gu || smfma_gu) {
             Launch l(L, "to_matrix_form", st);
             jx::launch_q8_to_acth(L->xq, n, L->xh.a, st);
         }
@@ -477,6 +526,10 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     const int tbs = n == 1 ? 1 : (n >= 3 ? 16 : 4);  // the shared expert sees every token
     const int tiles_ub = nk / jx::MFMA_BN + slots;
     const size_t fpad = ((size_t)L->F + 255) / 256 * 256;
+    if (L->gu_f32 || L->sgu_f32) {  // fp32 x zero-padded for the fp32-activation gate/up
+        Launch l(L, "x_pad", st);
+        jx::launch_copy_pad(xdev, d, L->dpad, L->xf, st, n);
+    }
     // shared expert on the side stream, concurrent with the routed gate/up
     if (L->shared) {
         HIPCHK(hipEventRecord(L->ev_fork, st));
@@ -487,13 +540,17 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         sg.n_tok = n;
         sg.top_k = 1;
         const size_t fspad = ((size_t)L->Fs + 255) / 256 * 256;
-        if (smfma) {
-            const int st_ub = (n + jx::MFMA_BN - 1) / jx::MFMA_BN;
-            {
-                Launch l(L, "shared_gateup_mfma", ss);
-                jx::launch_mfma_gateup(L->sgate.m, L->sup.m, L->xh.a, sg, st_ub, L->sdown_f32 ? jx::ActQ8{} : L->hqs,
-                                       L->sdown_f32 ? L->hfs : nullptr, ss);
-            }
+        const int st_ub = (n + jx::MFMA_BN - 1) / jx::MFMA_BN;
+        if (smfma_gu) {
+            Launch l(L, "shared_gateup_mfma", ss);
+            jx::launch_mfma_gateup(L->sgate.m, L->sup.m, L->xh.a, sg, st_ub, L->sdown_f32 ? jx::ActQ8{} : L->hqs,
+                                   L->sdown_f32 ? L->hfs : nullptr, ss);
+        } else {
+            Launch l(L, "shared_gateup_gemv", ss);
+            jx::launch_gemv_gateup(L->sgate.m, L->sup.m, L->xq, sg, 1, tbs, L->hqs, L->sdown_f32 ? L->hfs : nullptr, ss,
+                                   nullptr, L->sgu_f32 ? L->xf : nullptr, L->dpad);
+        }
+        if (smfma_dn) {
             Launch l(L, "shared_down", ss);
             if (L->sdown_f32)
                 jx::launch_f32_to_acth(L->hfs, (int)fspad, n, L->hhs.a, ss);
@@ -501,18 +558,14 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
                 jx::launch_q8_to_acth(L->hqs, n, L->hhs.a, ss, false);
             jx::launch_mfma_down(L->sdown.m, L->hhs.a, sg, st_ub, L->ysh, ss);
         } else {
-            {
-                Launch l(L, "shared_gateup_gemv", ss);
-                jx::launch_gemv_gateup(L->sgate.m, L->sup.m, L->xq, sg, 1, tbs, L->hqs, L->sdown_f32 ? L->hfs : nullptr,
-                                       ss);
-            }
             Launch l(L, "shared_down", ss);
             jx::launch_gemv_down(L->sdown.m, L->hqs, L->sdown_f32 ? L->hfs : nullptr, (int)fspad, sg, 1, tbs, L->ysh,
                                  ss);
         }
         HIPCHK(hipEventRecord(L->ev_join, ss));
     }
-    if (mfma) {
+    const float* gxf = L->gu_f32 ? L->xf : nullptr;
+    if (mfma_gu) {
         Launch l(L, "gateup_mfma", st);
         jx::launch_mfma_gateup(L->gate.m, L->up.m, L->xh.a, grp, tiles_ub, L->down_f32 ? jx::ActQ8{} : L->hq,
                                L->down_f32 ? L->hf : nullptr, st);
@@ -526,10 +579,11 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         tail.on = 1;
         Launch l(L, "gateup_gemv", st);
         jx::launch_gemv_gateup(L->gate.m, L->up.m, L->xq, lg, slots, tb, L->hq, L->down_f32 ? L->hf : nullptr, st,
-                               &tail);
+                               &tail, gxf, L->dpad);
     } else {
         Launch l(L, "gateup_gemv", st);
-        jx::launch_gemv_gateup(L->gate.m, L->up.m, L->xq, grp, slots, tb, L->hq, L->down_f32 ? L->hf : nullptr, st);
+        jx::launch_gemv_gateup(L->gate.m, L->up.m, L->xq, grp, slots, tb, L->hq, L->down_f32 ? L->hf : nullptr, st,
+                               nullptr, gxf, L->dpad);
     }
     if (L->shared) HIPCHK(hipStreamWaitEvent(st, L->ev_join, 0));
     if (mfma_down) {
@@ -551,8 +605,8 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
             comb.k = k;
         }
         Launch l(L, fold ? "down_gemv_combine" : (L->down_f32 ? "down_gemv_f32" : "down_gemv"), st);
-        jx::launch_gemv_down(L->down.m, L->hq, L->down_f32 ? L->hf : nullptr, (int)fpad, grp, slots, mfma ? 4 : tb,
-                             L->y, st, comb);
+        jx::launch_gemv_down(L->down.m, L->hq, L->down_f32 ? L->hf : nullptr, (int)fpad, grp, slots, tb, L->y, st,
+                             comb);
     }
     if (!fold) {
         Launch l(L, "combine", st);
@@ -647,27 +701,23 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
     if (D->activation != JX_ACT_SILU && D->activation != JX_ACT_GELU_TANH)
         return fail(JX_ERR_INVALID, "activation must be JX_ACT_SILU or JX_ACT_GELU_TANH");
     if (D->gate_type != D->up_type) return fail(JX_ERR_UNSUPPORTED, "gate and up must share a type");
-    // gate/up consume Q8_0 activations (cols = d_model); the fp32-activation
-    // fallback of the reference is only implemented for Q4_K down projections.
-    if (!q8_activation(D->gate_type, D->d_model))
-        return fail(JX_ERR_UNSUPPORTED, "gate/up need Q8_0 activations (Q4_K requires d_model % 256 == 0)");
-    if (!q8_activation(D->down_type, D->d_ff) && D->down_type != jx::T_Q4_K)
-        return fail(JX_ERR_UNSUPPORTED, "down projection shape not covered");
-    if (D->d_ff_shared > 0) {
+    const bool has_sh = D->d_ff_shared > 0;
+    for (int t : {D->gate_type, D->down_type, has_sh ? D->sh_gate_type : D->gate_type, has_sh ? D->sh_down_type : D->down_type})
+        if (!expert_type_ok(t))
+            return fail(JX_ERR_UNSUPPORTED, "expert weight type must be Q4_0, Q5_0, Q8_0, Q4_K, Q5_K or Q6_K");
+    if (has_sh) {
         if (D->d_ff_shared % 32 != 0) return fail(JX_ERR_UNSUPPORTED, "d_ff_shared must be a multiple of 32");
         if (!D->sh_gate || !D->sh_up || !D->sh_down) return fail(JX_ERR_INVALID, "missing shared expert tensor");
         if (D->sh_gate_type != D->sh_up_type) return fail(JX_ERR_UNSUPPORTED, "shared gate and up must share a type");
-        if (!q8_activation(D->sh_gate_type, D->d_model))
-            return fail(JX_ERR_UNSUPPORTED, "shared gate/up need Q8_0 activations");
-        if (!q8_activation(D->sh_down_type, D->d_ff_shared) && D->sh_down_type != jx::T_Q4_K)
-            return fail(JX_ERR_UNSUPPORTED, "shared down projection shape not covered");
     }
-    {  // the GEMVs stage up to 4 token rows of activations in LDS
-        auto down_k = [](int t, int f) { return q8_activation(t, f) ? f : (f + 255) / 256 * 256; };
-        if (D->d_model > jx::gemv_max_k(true, 4, false) ||
-            down_k(D->down_type, D->d_ff) > jx::gemv_max_k(false, 4, !q8_activation(D->down_type, D->d_ff)) ||
-            (D->d_ff_shared > 0 && down_k(D->sh_down_type, D->d_ff_shared) >
-                                       jx::gemv_max_k(false, 4, !q8_activation(D->sh_down_type, D->d_ff_shared))))
+    {  // the GEMVs stage up to 4 token rows of activations in LDS: Q8_0 forms at K, fp32 rows padded
+        // to whole super-blocks (K-quants) where the reference keeps fp32 activations
+        auto act_k = [](int t, int f) { return q8_activation(t, f) || !jx::is_kquant(t) ? f : (f + 255) / 256 * 256; };
+        auto fits = [&](bool gateup, int t, int f) {
+            return act_k(t, f) <= jx::gemv_max_k(gateup, 4, !q8_activation(t, f));
+        };
+        if (!fits(true, D->gate_type, D->d_model) || !fits(false, D->down_type, D->d_ff) ||
+            (has_sh && (!fits(true, D->sh_gate_type, D->d_model) || !fits(false, D->sh_down_type, D->d_ff_shared))))
             return fail(JX_ERR_UNSUPPORTED, "d_model / d_ff exceed the GEMVs' staged activation capacity");
     }
     auto* L = new jx_moe_layer();
@@ -678,10 +728,14 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
     L->F = D->d_ff;
     L->Fs = D->d_ff_shared;
     L->shared = D->d_ff_shared > 0;
-    // rows >= 8 always holds here, so the reference uses Q8_0 down activations
-    // exactly when supports_q8_activation allows (matmul_quant_f32, 3908-3914)
+    // rows >= 8 always holds here, so the reference uses Q8_0 activations exactly when
+    // supports_q8_activation allows (matmul_quant_f32, 3908-3914; matmul_swiglu_quant_f32, 3985-3991,
+    // whose Q8_0 x is used by the rows of types that support it)
     L->down_f32 = !q8_activation(D->down_type, D->d_ff);
     L->sdown_f32 = L->shared && !q8_activation(D->sh_down_type, D->d_ff_shared);
+    L->gu_f32 = !q8_activation(D->gate_type, D->d_model);
+    L->sgu_f32 = L->shared && !q8_activation(D->sh_gate_type, D->d_model);
+    L->dpad = (D->d_model + 255) / 256 * 256;
     hipStream_t st = nullptr;
     int r = JX_OK;
     auto bail = [&](int code) {
@@ -925,7 +979,6 @@ void jx_qmatrix_destroy(jx_qmatrix* m) {
 // zero-padded fp32 copy xf of the same activation row.
 static int dev_gemv(jx_qmatrix* W, bool q8, const jx::ActQ8& xq, float* xf, float* out, hipStream_t st) {
     const size_t kpad = ((size_t)W->cols + 255) / 256 * 256;
-    if (!q8 && W->type != jx::T_Q4_K) return fail(JX_ERR_UNSUPPORTED, "fp32-activation dot only implemented for Q4_K");
     if (kpad > (size_t)jx::gemv_max_k(false, 1, !q8))
         return fail(JX_ERR_UNSUPPORTED, "cols exceeds the GEMV's staged activation capacity");
     jx::Groups g;
@@ -999,8 +1052,6 @@ int jx_matmul_quant_f32(jx_qmatrix* W, const float* x, float* out) {
     HIPCHK(hipSetDevice(W->device));
     const int rows = W->rows, cols = W->cols;
     const bool q8 = rows >= 8 && q8_activation(W->type, cols);
-    if (!q8 && W->type != jx::T_Q4_K)
-        return fail(JX_ERR_UNSUPPORTED, "fp32-activation dot only implemented for Q4_K");
     if (((size_t)cols + 255) / 256 * 256 > (size_t)jx::gemv_max_k(false, 1, !q8))
         return fail(JX_ERR_UNSUPPORTED, "cols exceeds the GEMV's staged activation capacity");
     Scratch s;
@@ -1034,8 +1085,6 @@ int jx_matmul_quant_f32_noalloc(jx_qmatrix* W, const float* x_dev, float* out_de
     if (!W || !x_dev || !out_dev) return fail(JX_ERR_INVALID, "null argument");
     const int rows = W->rows, cols = W->cols;
     const bool q8 = rows >= 8 && q8_activation(W->type, cols);
-    if (!q8 && W->type != jx::T_Q4_K)
-        return fail(JX_ERR_UNSUPPORTED, "fp32-activation dot only implemented for Q4_K");
     const size_t kpad = ((size_t)cols + 255) / 256 * 256;
     if (kpad > NOALLOC_MAX_COLS)
         return fail(JX_ERR_UNSUPPORTED, "cols exceed the no-allocation scratch (" + std::to_string(NOALLOC_MAX_COLS) +
@@ -1073,12 +1122,13 @@ int jx_matmul_swiglu_quant_f32(jx_qmatrix* Wg, jx_qmatrix* Wu, const float* x, f
         return fail(JX_ERR_UNSUPPORTED, "gate and up must share shape and type");
     HIPCHK(hipSetDevice(Wg->device));
     const int rows = Wg->rows, cols = Wg->cols;
-    if (!(rows >= 8 && cols % 32 == 0 && q8_activation(Wg->type, cols)))
-        return fail(JX_ERR_UNSUPPORTED, "fp32-activation gate/up not implemented");
-    if (cols > jx::gemv_max_k(true, 1, false))
+    // Q8_0 x iff exp_dim >= 8 and cols % 32 == 0 (quant.cpp:3985-3991), used by rows whose type allows it
+    const bool q8 = rows >= 8 && cols % 32 == 0 && q8_activation(Wg->type, cols);
+    const size_t kpad = ((size_t)cols + 255) / 256 * 256;
+    if ((q8 ? (size_t)cols : kpad) > (size_t)jx::gemv_max_k(true, 1, !q8))
         return fail(JX_ERR_UNSUPPORTED, "cols exceeds the GEMV's staged activation capacity");
     Scratch s;
-    float* xd = s.get<float>(cols);
+    float* xd = s.get<float>(kpad);
     const size_t fpad = ((size_t)rows + 255) / 256 * 256;
     float* hf = s.get<float>(fpad);
     jx::ActQ8 a, hq;
@@ -1086,15 +1136,16 @@ int jx_matmul_swiglu_quant_f32(jx_qmatrix* Wg, jx_qmatrix* Wu, const float* x, f
     a.s = s.get<float2>(cols / 32);
     a.K = cols;
     if (!xd || !hf || !a.q || !a.s) return fail(JX_ERR_NOMEM, "scratch allocation");
+    HIPCHK(hipMemset(xd, 0, kpad * 4));
     HIPCHK(hipMemcpy(xd, x, (size_t)cols * 4, hipMemcpyHostToDevice));
-    jx::launch_quantize_q8(xd, 1, cols, a, nullptr);
+    if (q8) jx::launch_quantize_q8(xd, 1, cols, a, nullptr);
     jx::Groups g;
     g.identity = 1;
     g.n_tok = 1;
     hq.K = rows;  // q == nullptr: no Q8_0 output wanted
     jx::QMat gm = Wg->w.m;
     gm.act = use_gelu ? jx::ACT_GELU_TANH : jx::ACT_SILU;
-    jx::launch_gemv_gateup(gm, Wu->w.m, a, g, 1, 1, hq, hf, nullptr);
+    jx::launch_gemv_gateup(gm, Wu->w.m, a, g, 1, 1, hq, hf, nullptr, nullptr, q8 ? nullptr : xd, (int)kpad);
     HIPCHK(hipGetLastError());
     HIPCHK(hipMemcpy(out, hf, (size_t)rows * 4, hipMemcpyDeviceToHost));
     return JX_OK;

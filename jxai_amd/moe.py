@@ -112,7 +112,8 @@ class MoELayer:
         gt, ut, dt = lw.types
         kw = {}
         if cfg.has_shared:
-            kw = dict(d_ff_shared=cfg.d_ff_shared, sh_gate_type=gt, sh_up_type=ut, sh_down_type=dt,
+            sgt, sut, sdt = lw.sh_types
+            kw = dict(d_ff_shared=cfg.d_ff_shared, sh_gate_type=sgt, sh_up_type=sut, sh_down_type=sdt,
                       sh_gate=lw.sh_gate, sh_up=lw.sh_up, sh_down=lw.sh_down, sh_gate_inp=lw.sh_gate_inp)
         return cls(n_experts=cfg.n_experts, top_k=cfg.top_k, d_model=cfg.d_model, d_ff=cfg.d_ff,
                    gate_type=gt, up_type=ut, down_type=dt, router=lw.router, router_bias=lw.router_bias,

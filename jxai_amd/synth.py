@@ -118,13 +118,28 @@ def quant_matrix(seed: int, qtype: int, rows: int, cols: int,
         d = fp16_uniform(seed ^ 0x1, nblocks, scale_lo, scale_hi)
         out[:, 0:2] = d.view(np.uint8).reshape(nblocks, 2)
         out[:, 2:34] = int8_pm127(seed ^ 0x2, nblocks * 32).reshape(nblocks, 32)
-    elif qtype == F.Q4_K:
-        d = fp16_uniform(seed ^ 0x1, nblocks, scale_lo, scale_hi)
-        dmin = fp16_uniform(seed ^ 0x3, nblocks, scale_lo, scale_hi)
+    elif qtype in (F.Q4_K, F.Q5_K):
+        # Q5_K quants reach 31: half the scale range keeps the weights' spread near Q4_K's
+        k = 0.5 if qtype == F.Q5_K else 1.0
+        d = fp16_uniform(seed ^ 0x1, nblocks, k * scale_lo, k * scale_hi)
+        dmin = fp16_uniform(seed ^ 0x3, nblocks, k * scale_lo, k * scale_hi)
         out[:, 0:2] = d.view(np.uint8).reshape(nblocks, 2)
         out[:, 2:4] = dmin.view(np.uint8).reshape(nblocks, 2)
         out[:, 4:16] = random_bytes(seed ^ 0x4, nblocks * 12).reshape(nblocks, 12)
-        out[:, 16:144] = random_bytes(seed ^ 0x2, nblocks * 128).reshape(nblocks, 128)
+        q0 = 48 if qtype == F.Q5_K else 16
+        out[:, q0:q0 + 128] = random_bytes(seed ^ 0x2, nblocks * 128).reshape(nblocks, 128)
+        if qtype == F.Q5_K:
+            out[:, 16:48] = random_bytes(seed ^ 0x5, nblocks * 32).reshape(nblocks, 32)
+    elif qtype == F.Q6_K:
+        # ql[128], qh[64], int8 scales[16] over the full range (sign and |sc| > 64 included), d
+        out[:, 0:192] = random_bytes(seed ^ 0x2, nblocks * 192).reshape(nblocks, 192)
+        out[:, 192:208] = random_bytes(seed ^ 0x4, nblocks * 16).reshape(nblocks, 16)
+        d = fp16_uniform(seed ^ 0x1, nblocks, scale_lo / 16, scale_hi / 16)
+        out[:, 208:210] = d.view(np.uint8).reshape(nblocks, 2)
+    elif qtype == F.Q5_0:
+        d = fp16_uniform(seed ^ 0x1, nblocks, scale_lo / 2, scale_hi / 2)
+        out[:, 0:2] = d.view(np.uint8).reshape(nblocks, 2)
+        out[:, 2:22] = random_bytes(seed ^ 0x2, nblocks * 20).reshape(nblocks, 20)
     else:
         raise ValueError(f"unsupported expert weight type {qtype}")
     return out.reshape(-1)
@@ -143,6 +158,8 @@ class LayerConfig:
     d_ff: int
     wtype: int
     d_ff_shared: int = 0
+    down_wtype: int | None = None     # routed down type when it differs (Q4_K_M files: Q6_K / Q5_0 downs)
+    sh_down_wtype: int | None = None  # shared down type (default: the routed down type)
     shared_gate: bool = False
     zipf_gamma: float = 0.0
     act: int = 0  # gated activation: 0 SiLU, 1 GELU-tanh (the reference's use_gelu)
@@ -154,6 +171,14 @@ class LayerConfig:
     @property
     def has_shared(self) -> bool:
         return self.d_ff_shared > 0
+
+    @property
+    def down_t(self) -> int:
+        return self.wtype if self.down_wtype is None else self.down_wtype
+
+    @property
+    def sh_down_t(self) -> int:
+        return self.down_t if self.sh_down_wtype is None else self.sh_down_wtype
 
 
 CONFIGS = {
@@ -176,6 +201,22 @@ CONFIGS = {
     "dsv2lite": LayerConfig("dsv2lite", 2048, 64, 6, 1408, F.Q4_K, d_ff_shared=2816,
                             decode_tokens=(32,),
                             describe="DeepSeek-V2-Lite-shaped d2048 E64 top-6 F1408 Q4_K + 2x1408 shared"),
+    # the mixed-type layers of real Q4_K_M files: Q6_K downs on the layers llama.cpp gives more bits,
+    # Q5_0 where d_ff % 256 != 0 rules out the K-quants (its fallback for Q4_K), Q6_K shared down
+    "mixtral_q6k": LayerConfig("mixtral_q6k", 4096, 8, 2, 14336, F.Q4_K, down_wtype=F.Q6_K,
+                               decode_tokens=(1, 512, 2048),
+                               describe="Mixtral-8x7B-shaped Q4_K_M layer: Q4_K gate/up, Q6_K down"),
+    "dsv2lite_q50": LayerConfig("dsv2lite_q50", 2048, 64, 6, 1408, F.Q4_K, d_ff_shared=2816,
+                                down_wtype=F.Q5_0, sh_down_wtype=F.Q6_K, decode_tokens=(1, 32, 512),
+                                describe="DeepSeek-V2-Lite-shaped Q4_K_M layer: Q4_K gate/up, Q5_0 routed down "
+                                         "(fp32 activations), Q6_K shared down"),
+    # single-format toy layers: every kernel form of each type (Q5_0 gate/up takes fp32 x)
+    "toy_q5k": LayerConfig("toy_q5k", 512, 8, 2, 1024, F.Q5_K, decode_tokens=(1, 2, 64, 512),
+                           describe="Toy MoE FFN d512 E8 top-2 F1024 Q5_K"),
+    "toy_q6k": LayerConfig("toy_q6k", 512, 8, 2, 1024, F.Q6_K, decode_tokens=(1, 2, 64, 512),
+                           describe="Toy MoE FFN d512 E8 top-2 F1024 Q6_K"),
+    "toy_q50": LayerConfig("toy_q50", 512, 8, 2, 1024, F.Q5_0, decode_tokens=(1, 2, 64, 512),
+                           describe="Toy MoE FFN d512 E8 top-2 F1024 Q5_0 (fp32 activations throughout)"),
 }
 
 
@@ -206,7 +247,12 @@ class LayerWeights:
     @property
     def types(self):
         t = self.cfg.wtype
-        return t, t, t
+        return t, t, self.cfg.down_t
+
+    @property
+    def sh_types(self):
+        t = self.cfg.wtype
+        return t, t, self.cfg.sh_down_t
 
 
 def make_layer(cfg: LayerConfig, seed: int = BASE_SEED) -> LayerWeights:
@@ -216,13 +262,13 @@ def make_layer(cfg: LayerConfig, seed: int = BASE_SEED) -> LayerWeights:
     bias = zipf_bias(cfg, seed) if cfg.zipf_gamma > 0 else None
     gate = quant_matrix(s("gate_exps"), cfg.wtype, E * Fd, d)
     up = quant_matrix(s("up_exps"), cfg.wtype, E * Fd, d)
-    down = quant_matrix(s("down_exps"), cfg.wtype, E * d, Fd)
+    down = quant_matrix(s("down_exps"), cfg.down_t, E * d, Fd)
     lw = LayerWeights(cfg, router, bias, gate, up, down)
     if cfg.has_shared:
         Fs = cfg.d_ff_shared
         lw.sh_gate = quant_matrix(s("gate_shexp"), cfg.wtype, Fs, d)
         lw.sh_up = quant_matrix(s("up_shexp"), cfg.wtype, Fs, d)
-        lw.sh_down = quant_matrix(s("down_shexp"), cfg.wtype, d, Fs)
+        lw.sh_down = quant_matrix(s("down_shexp"), cfg.sh_down_t, d, Fs)
         if cfg.shared_gate:
             lw.sh_gate_inp = normal_f32(s("gate_inp_shexp"), d, 0.02)
     if cfg.norms:  # RMSNorm weights around 1
@@ -239,7 +285,7 @@ def make_tokens(cfg: LayerConfig, n: int, seed: int = BASE_SEED) -> np.ndarray:
 def expert_bytes(cfg: LayerConfig) -> int:
     """gate+up+down bytes of one routed expert."""
     t = cfg.wtype
-    return 2 * F.matrix_bytes(t, cfg.d_ff, cfg.d_model) + F.matrix_bytes(t, cfg.d_model, cfg.d_ff)
+    return 2 * F.matrix_bytes(t, cfg.d_ff, cfg.d_model) + F.matrix_bytes(cfg.down_t, cfg.d_model, cfg.d_ff)
 
 
 def shared_bytes(cfg: LayerConfig) -> int:
@@ -247,4 +293,4 @@ def shared_bytes(cfg: LayerConfig) -> int:
         return 0
     t = cfg.wtype
     Fs = cfg.d_ff_shared
-    return 2 * F.matrix_bytes(t, Fs, cfg.d_model) + F.matrix_bytes(t, cfg.d_model, Fs)
+    return 2 * F.matrix_bytes(t, Fs, cfg.d_model) + F.matrix_bytes(cfg.sh_down_t, cfg.d_model, Fs)

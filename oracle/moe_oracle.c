@@ -83,6 +83,9 @@ int64_t jxo_row_bytes(int32_t type, int64_t cols) {
         case JXO_Q4_0: return ((cols + 31) / 32) * 18;
         case JXO_Q8_0: return ((cols + 31) / 32) * 34;
         case JXO_Q4_K: return ((cols + 255) / 256) * 144;
+        case JXO_Q5_0: return ((cols + 31) / 32) * 22;
+        case JXO_Q5_K: return ((cols + 255) / 256) * 176;
+        case JXO_Q6_K: return ((cols + 255) / 256) * 210;
         default: return -1;
     }
 }
@@ -160,8 +163,94 @@ static void dequant_q4_K(const uint8_t* x, float* y, int64_t k) {
     }
 }
 
+/* dequantize_row_q5_K (src/quant.cpp:1345-1387), block_q5_K (include/quant.h:36-42: d, dmin,
+ * scales[12], qh[32], qs[128]): in 64-element chunk c, element l of the low half takes the low
+ * nibble of qs[32c + l] and bit 2c of qh[l], element 32 + l the high nibble and bit 2c + 1;
+ * value d*sc*q - dmin*m (d*sc*q is exact, so contracting it changes nothing). */
+static void dequant_q5_K(const uint8_t* x, float* y, int64_t k) {
+    const int64_t nb = k / 256;
+    for (int64_t i = 0; i < nb; ++i) {
+        const uint8_t* blk = x + i * 176;
+        const float d = ld_f16(blk), dmin = ld_f16(blk + 2);
+        const uint8_t* sc = blk + 4;
+        const uint8_t* qh = blk + 16;
+        const uint8_t* q = blk + 48;
+        float* yb = y + i * 256;
+        for (int c = 0; c < 4; ++c) {
+            uint8_t s, m;
+            scale_min_k4(2 * c, sc, &s, &m);
+            const float d1 = d * (float)s, m1 = dmin * (float)m;
+            scale_min_k4(2 * c + 1, sc, &s, &m);
+            const float d2 = d * (float)s, m2 = dmin * (float)m;
+            for (int l = 0; l < 32; ++l) {
+                const int q0 = (q[32 * c + l] & 0x0F) | (((qh[l] >> (2 * c)) & 1) << 4);
+                const int q1 = (q[32 * c + l] >> 4) | (((qh[l] >> (2 * c + 1)) & 1) << 4);
+                yb[64 * c + l] = fmaf(d1, (float)q0, -m1);
+                yb[64 * c + 32 + l] = fmaf(d2, (float)q1, -m2);
+            }
+        }
+    }
+    const int64_t rem = k - nb * 256;
+    if (rem > 0) {
+        float tmp[256];
+        dequant_q5_K(x + nb * 176, tmp, 256);
+        memcpy(y + nb * 256, tmp, (size_t)rem * 4);
+    }
+}
+
+/* The 6-bit quant of element e (0..255) of a block_q6_K (include/quant.h:45-50: ql[128],
+ * qh[64], scales[16], d) minus 32, in dequantize_row_q6_K's layout (src/quant.cpp:1389-1428):
+ * 128-element half n, quarter r = (e % 128) / 32, l = e % 32 -> nibble (r / 2) of
+ * ql[64n + 32 (r % 2) + l] and bits 2r..2r+1 of qh[32n + l]. */
+static inline int q6_val(const uint8_t* blk, int e) {
+    const int n = e >> 7, r = (e >> 5) & 3, l = e & 31;
+    const uint8_t lo = blk[64 * n + 32 * (r & 1) + l];
+    const int nib = (r >> 1) ? (lo >> 4) : (lo & 0x0F);
+    const int hb = (blk[128 + 32 * n + l] >> (2 * r)) & 3;
+    return (nib | (hb << 4)) - 32;
+}
+
+/* dequantize_row_q6_K (src/quant.cpp:1389-1428): (d * sc) * q, sc = scales[e / 16]; both
+ * products are exact (11-bit d, 8-bit sc, 6-bit q). */
+static void dequant_q6_K(const uint8_t* x, float* y, int64_t k) {
+    const int64_t nb = k / 256;
+    for (int64_t i = 0; i < nb; ++i) {
+        const uint8_t* blk = x + i * 210;
+        const float d = ld_f16(blk + 208);
+        for (int e = 0; e < 256; ++e)
+            y[i * 256 + e] = d * (float)(int8_t)blk[192 + e / 16] * (float)q6_val(blk, e);
+    }
+    const int64_t rem = k - nb * 256;
+    if (rem > 0) {
+        float tmp[256];
+        dequant_q6_K(x + nb * 210, tmp, 256);
+        memcpy(y + nb * 256, tmp, (size_t)rem * 4);
+    }
+}
+
+/* dequantize_row_q5_0 (src/quant.cpp:1585-1600), block_q5_0 (include/quant.h:60-66: d,
+ * qh as a little-endian u32, qs[16]): element j < 16 = low nibble of qs[j] with bit j of qh as
+ * its fifth bit, element 16 + j = high nibble with bit 16 + j; value (q - 16) * d (exact). */
+static void dequant_q5_0(const uint8_t* x, float* y, int64_t nb) {
+    for (int64_t i = 0; i < nb; ++i) {
+        const uint8_t* b = x + i * 22;
+        const float d = ld_f16(b);
+        uint32_t qh;
+        memcpy(&qh, b + 2, 4);
+        for (int j = 0; j < 16; ++j) {
+            const int lo = (b[6 + j] & 0x0F) | (int)(((qh >> j) & 1u) << 4);
+            const int hi = (b[6 + j] >> 4) | (int)(((qh >> (j + 16)) & 1u) << 4);
+            y[i * 32 + j] = (float)(lo - 16) * d;
+            y[i * 32 + 16 + j] = (float)(hi - 16) * d;
+        }
+    }
+}
+
 void jxo_dequantize_row(int32_t type, const uint8_t* w, float* y, int64_t k) {
     if (type == JXO_Q4_K) { dequant_q4_K(w, y, k); return; }
+    if (type == JXO_Q5_K) { dequant_q5_K(w, y, k); return; }
+    if (type == JXO_Q6_K) { dequant_q6_K(w, y, k); return; }
+    if (type == JXO_Q5_0) { dequant_q5_0(w, y, k / 32); return; }
     const int64_t nb = k / 32;
     for (int64_t i = 0; i < nb; ++i) {
         if (type == JXO_Q4_0) {  /* dequantize_row_q4_0 (quant.cpp:1014-1027) */
@@ -255,6 +344,114 @@ float jxo_vec_dot_q4_K_f32(const uint8_t* x, const float* y, int64_t k) {
         total += jxo_vec_dot_f32(deq, y + nb * 256, rem);
     }
     return total;
+}
+
+/* vec_dot_q4_0_f32 (src/quant.cpp:2780-2827) and vec_dot_q8_0_f32 (2829-2862), AVX2 order:
+ * per 32-block an 8-lane sum bsum (Q4_0: lane t = ((lo[t] * y[t] + lo[8+t] * y[8+t]) +
+ * hi[t] * y[16+t]) + hi[8+t] * y[24+t] as one multiply and three fmas, weights q - 8; Q8_0:
+ * four fmas from zero over 8-element chunks), acc_t = fma(d, bsum_t, acc_t), the 8 lanes
+ * summed in order.  Whole blocks only (k / 32). */
+static float dot_q4_0_f32(const uint8_t* x, const float* y, int64_t k) {
+    float acc[8] = {0};
+    for (int64_t i = 0; i < k / 32; ++i) {
+        const uint8_t* b = x + i * 18;
+        const float d = ld_f16(b);
+        const float* yb = y + i * 32;
+        for (int t = 0; t < 8; ++t) {
+            float bs = (float)((b[2 + t] & 0x0F) - 8) * yb[t];
+            bs = fmaf((float)((b[2 + 8 + t] & 0x0F) - 8), yb[8 + t], bs);
+            bs = fmaf((float)((b[2 + t] >> 4) - 8), yb[16 + t], bs);
+            bs = fmaf((float)((b[2 + 8 + t] >> 4) - 8), yb[24 + t], bs);
+            acc[t] = fmaf(d, bs, acc[t]);
+        }
+    }
+    float total = 0.0f;
+    for (int t = 0; t < 8; ++t) total += acc[t];
+    return total;
+}
+
+static float dot_q8_0_f32(const uint8_t* x, const float* y, int64_t k) {
+    float acc[8] = {0};
+    for (int64_t i = 0; i < k / 32; ++i) {
+        const uint8_t* b = x + i * 34;
+        const float d = ld_f16(b);
+        for (int t = 0; t < 8; ++t) {
+            float bs = 0.0f;
+            for (int c = 0; c < 4; ++c) bs = fmaf((float)(int8_t)b[2 + 8 * c + t], y[i * 32 + 8 * c + t], bs);
+            acc[t] = fmaf(d, bs, acc[t]);
+        }
+    }
+    float total = 0.0f;
+    for (int t = 0; t < 8; ++t) total += acc[t];
+    return total;
+}
+
+/* vec_dot_deq_f32 (src/quant.cpp:3208-3229) as vec_dot_q5_0_f32 uses it (3232-3234), and
+ * vec_dot_q5_K_f32 (3069-3085): each block dequantized, vec_dot_f32 over it, the block dots
+ * added in order; a partial last block is dequantized whole and dotted over its valid
+ * elements. */
+static float dot_deq_f32(int32_t type, const uint8_t* x, const float* y, int64_t k) {
+    const int blk = type == JXO_Q5_0 ? 32 : 256;
+    const int64_t bytes = jxo_row_bytes(type, blk);
+    const int64_t nb = k / blk, rem = k - nb * blk;
+    float deq[256];
+    float sum = 0.0f;
+    for (int64_t i = 0; i < nb; ++i) {
+        jxo_dequantize_row(type, x + i * bytes, deq, blk);
+        sum += jxo_vec_dot_f32(deq, y + i * blk, blk);
+    }
+    if (rem > 0) {
+        jxo_dequantize_row(type, x + nb * bytes, deq, blk);
+        sum += jxo_vec_dot_f32(deq, y + nb * blk, rem);
+    }
+    return sum;
+}
+
+/* vec_dot_q6_K_f32 (src/quant.cpp:3087-3165), AVX2 order: per 128-element half and 16-element
+ * step is (0, 1), for the four quarters r in order an 8-lane product p_t = fma(q[8+t], y[8+t],
+ * q[t] * y[t]) over elements 32 r + 16 is .. + 15 of the half, then acc_t = fma(d * sc, p_t,
+ * acc_t) with sc = scales[8 n + 2 r + is]; the 8 lanes summed in order; a partial last block
+ * dequantized and dotted with vec_dot_f32. */
+static float dot_q6_K_f32(const uint8_t* x, const float* y, int64_t k) {
+    const int64_t nb = k / 256;
+    float acc[8] = {0};
+    for (int64_t i = 0; i < nb; ++i) {
+        const uint8_t* blk = x + i * 210;
+        const float d = ld_f16(blk + 208);
+        for (int n = 0; n < 2; ++n)
+            for (int is = 0; is < 2; ++is)
+                for (int r = 0; r < 4; ++r) {
+                    const int e0 = 128 * n + 32 * r + 16 * is;
+                    const float* yb = y + i * 256 + e0;
+                    const float ds = d * (float)(int8_t)blk[192 + 8 * n + 2 * r + is];
+                    for (int t = 0; t < 8; ++t) {
+                        const float p = fmaf((float)q6_val(blk, e0 + 8 + t), yb[8 + t], (float)q6_val(blk, e0 + t) * yb[t]);
+                        acc[t] = fmaf(ds, p, acc[t]);
+                    }
+                }
+    }
+    float total = 0.0f;
+    for (int t = 0; t < 8; ++t) total += acc[t];
+    const int64_t rem = k - nb * 256;
+    if (rem > 0) {
+        float deq[256];
+        dequant_q6_K(x + nb * 210, deq, 256);
+        total += jxo_vec_dot_f32(deq, y + nb * 256, rem);
+    }
+    return total;
+}
+
+float jxo_vec_dot_quant_f32(int32_t type, const uint8_t* w, const float* y, int64_t k) {
+    switch (type) {
+        case JXO_F32: return jxo_vec_dot_f32((const float*)(const void*)w, y, k);
+        case JXO_Q4_0: return dot_q4_0_f32(w, y, k);
+        case JXO_Q8_0: return dot_q8_0_f32(w, y, k);
+        case JXO_Q4_K: return jxo_vec_dot_q4_K_f32(w, y, k);
+        case JXO_Q5_0:
+        case JXO_Q5_K: return dot_deq_f32(type, w, y, k);
+        case JXO_Q6_K: return dot_q6_K_f32(w, y, k);
+        default: abort();
+    }
 }
 
 /* --------------------------------------------- Q8_0-activation dots -- */
@@ -404,8 +601,112 @@ static float dot_q4K_q8(const uint8_t* x, const uint8_t* y, int64_t k, int32_t o
     return total;
 }
 
+/* vec_dot_q5_K_q8_0 (src/quant.cpp:3648-3721; AVX2 only, no AVX-512 variant): as the Q4_K
+ * AVX2 dot with 5-bit quants -- per 64-element chunk c, lane t of each 32-block takes the exact
+ * integer dot of elements 4t..4t+3 and the sum of their activation quants, then
+ * acc_t = fma(d1 dy0, dot0_t), fma(-(m1 dy0), sum0_t), fma(d2 dy1, dot1_t), fma(-(m2 dy1), sum1_t);
+ * the 8 lanes summed in order; a partial last block as in dot_q4K_q8. */
+static float dot_q5K_q8(const uint8_t* x, const uint8_t* y, int64_t k) {
+    const int64_t nb = k / 256;
+    float acc[8] = {0};
+    for (int64_t i = 0; i < nb; ++i) {
+        const uint8_t* blk = x + i * 176;
+        const float d = ld_f16(blk), dmin = ld_f16(blk + 2);
+        const uint8_t* scs = blk + 4;
+        const uint8_t* qh = blk + 16;
+        const uint8_t* q = blk + 48;
+        const uint8_t* yb = y + i * 8 * 34;
+        for (int c = 0; c < 4; ++c) {
+            uint8_t s, m;
+            scale_min_k4(2 * c, scs, &s, &m);
+            const float d1 = d * (float)s, m1 = dmin * (float)m;
+            scale_min_k4(2 * c + 1, scs, &s, &m);
+            const float d2 = d * (float)s, m2 = dmin * (float)m;
+            const uint8_t* ya = yb + (2 * c) * 34;
+            const uint8_t* yc = yb + (2 * c + 1) * 34;
+            const float dy0 = ld_f16(ya), dy1 = ld_f16(yc);
+            for (int t = 0; t < 8; ++t) {
+                int32_t a = 0, b = 0, cc = 0, e = 0;
+                for (int l = 4 * t; l < 4 * t + 4; ++l) {
+                    const int q0 = (q[32 * c + l] & 0x0F) | (((qh[l] >> (2 * c)) & 1) << 4);
+                    const int q1 = (q[32 * c + l] >> 4) | (((qh[l] >> (2 * c + 1)) & 1) << 4);
+                    a += q0 * (int8_t)ya[2 + l];
+                    b += (int8_t)ya[2 + l];
+                    cc += q1 * (int8_t)yc[2 + l];
+                    e += (int8_t)yc[2 + l];
+                }
+                acc[t] = fmaf(d1 * dy0, (float)a, acc[t]);
+                acc[t] = fmaf(-(m1 * dy0), (float)b, acc[t]);
+                acc[t] = fmaf(d2 * dy1, (float)cc, acc[t]);
+                acc[t] = fmaf(-(m2 * dy1), (float)e, acc[t]);
+            }
+        }
+    }
+    float total = 0.0f;
+    for (int t = 0; t < 8; ++t) total += acc[t];
+    const int64_t rem = k - nb * 256;
+    if (rem > 0) {
+        float deq[256], yf[256];
+        dequant_q5_K(x + nb * 176, deq, 256);
+        jxo_dequantize_row(JXO_Q8_0, y + nb * 8 * 34, yf, 256);
+        total += jxo_vec_dot_f32(deq, yf, rem);
+    }
+    return total;
+}
+
+/* vec_dot_q6_K_q8_0 (src/quant.cpp:3723-3818; AVX2 only): per 128-element half n and quarter r
+ * (the half's 32-block r), four int32 lanes s_r[t] = sc[8n + 2r] * (dot of elements 4t..4t+3)
+ * + sc[8n + 2r + 1] * (dot of elements 16 + 4t..16 + 4t+3), exact; lanes 0-3 of acc take
+ * fma(d * dy_0, s_0[t]) then fma(d * dy_2, s_2[t]), lanes 4-7 fma(d * dy_1, s_1[t]) then
+ * fma(d * dy_3, s_3[t]); the 8 lanes summed in order; a partial last block dequantized. */
+static float dot_q6K_q8(const uint8_t* x, const uint8_t* y, int64_t k) {
+    const int64_t nb = k / 256;
+    float acc[8] = {0};
+    for (int64_t i = 0; i < nb; ++i) {
+        const uint8_t* blk = x + i * 210;
+        const float d = ld_f16(blk + 208);
+        for (int n = 0; n < 2; ++n) {
+            int32_t sr[4][4];
+            float dy[4];
+            for (int r = 0; r < 4; ++r) {
+                const uint8_t* yq = y + (i * 8 + 4 * n + r) * 34;
+                dy[r] = d * ld_f16(yq);
+                const int sa = (int8_t)blk[192 + 8 * n + 2 * r], sb = (int8_t)blk[192 + 8 * n + 2 * r + 1];
+                for (int t = 0; t < 4; ++t) {
+                    int32_t a = 0, b = 0;
+                    for (int l = 4 * t; l < 4 * t + 4; ++l) {
+                        a += q6_val(blk, 128 * n + 32 * r + l) * (int8_t)yq[2 + l];
+                        b += q6_val(blk, 128 * n + 32 * r + 16 + l) * (int8_t)yq[2 + 16 + l];
+                    }
+                    sr[r][t] = sa * a + sb * b;
+                }
+            }
+            for (int t = 0; t < 4; ++t) {
+                acc[t] = fmaf(dy[0], (float)sr[0][t], acc[t]);
+                acc[4 + t] = fmaf(dy[1], (float)sr[1][t], acc[4 + t]);
+            }
+            for (int t = 0; t < 4; ++t) {
+                acc[t] = fmaf(dy[2], (float)sr[2][t], acc[t]);
+                acc[4 + t] = fmaf(dy[3], (float)sr[3][t], acc[4 + t]);
+            }
+        }
+    }
+    float total = 0.0f;
+    for (int t = 0; t < 8; ++t) total += acc[t];
+    const int64_t rem = k - nb * 256;
+    if (rem > 0) {
+        float deq[256], yf[256];
+        dequant_q6_K(x + nb * 210, deq, 256);
+        jxo_dequantize_row(JXO_Q8_0, y + nb * 8 * 34, yf, 256);
+        total += jxo_vec_dot_f32(deq, yf, rem);
+    }
+    return total;
+}
+
 float jxo_vec_dot_q8(int32_t type, const uint8_t* w, const uint8_t* xq8, int64_t k, int32_t order) {
     if (type == JXO_Q4_K) return dot_q4K_q8(w, xq8, k, order);
+    if (type == JXO_Q5_K) return dot_q5K_q8(w, xq8, k);
+    if (type == JXO_Q6_K) return dot_q6K_q8(w, xq8, k);
     const int64_t nb = k / 32;
     if (order == JXO_ORDER_AVX512) return dot_q4q8_32_avx512(type, w, xq8, nb);
     return dot_q4q8_32(type, w, xq8, nb);
@@ -416,24 +717,18 @@ float jxo_vec_dot_q8(int32_t type, const uint8_t* w, const uint8_t* xq8, int64_t
 static int supports_q8_act(int32_t type, int64_t cols) {
     /* supports_q8_activation (src/quant.cpp:3881-3893) */
     if (type == JXO_Q4_0 || type == JXO_Q8_0) return cols % 32 == 0;
-    if (type == JXO_Q4_K) return cols % 256 == 0;
+    if (type == JXO_Q4_K || type == JXO_Q5_K || type == JXO_Q6_K) return cols % 256 == 0;
     return 0;
 }
 
-/* vec_dot_row_with_q8 (src/quant.cpp:3841-3879) for the three expert
- * formats, falling back to the fp32-activation dot (vec_dot_quant_f32,
- * 3269-3305) when no Q8_0 activation applies. */
+/* vec_dot_row_with_q8 (src/quant.cpp:3841-3879): the Q8_0-activation dot where a Q8_0 x
+ * exists and the type/cols rule allows it, else the fp32-activation dot (vec_dot_quant_f32,
+ * 3269-3305). */
 static float row_dot(int32_t type, const uint8_t* row, const float* x, const uint8_t* xq8,
                      int64_t cols, int32_t order) {
-    if (xq8) {
-        if ((type == JXO_Q4_0 || type == JXO_Q8_0) && cols % 32 == 0)
-            return jxo_vec_dot_q8(type, row, xq8, cols, order);
-        if (type == JXO_Q4_K && cols % 256 == 0)
-            return jxo_vec_dot_q8(type, row, xq8, cols, order);
-    }
-    if (type == JXO_F32) return jxo_vec_dot_f32((const float*)(const void*)row, x, cols);
-    if (type == JXO_Q4_K) return jxo_vec_dot_q4_K_f32(row, x, cols);
-    abort(); /* Q4_0/Q8_0 with fp32 activations: not on any configured path */
+    if (xq8 && type != JXO_F32 && type != JXO_Q5_0 && supports_q8_act(type, cols))
+        return jxo_vec_dot_q8(type, row, xq8, cols, order);
+    return jxo_vec_dot_quant_f32(type, row, x, cols);
 }
 
 /* matmul_quant_f32 (src/quant.cpp:3895-3922): Q8_0 activations iff rows >= 8

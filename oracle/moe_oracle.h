@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-enum { JXO_F32 = 0, JXO_Q4_0 = 2, JXO_Q8_0 = 8, JXO_Q4_K = 12 };
+enum { JXO_F32 = 0, JXO_Q4_0 = 2, JXO_Q5_0 = 6, JXO_Q8_0 = 8, JXO_Q4_K = 12, JXO_Q5_K = 13, JXO_Q6_K = 14 };
 enum { JXO_ORDER_AVX2 = 0, JXO_ORDER_AVX512 = 1 };
 
 typedef struct {
@@ -54,6 +54,8 @@ float jxo_vec_dot_f32(const float* a, const float* b, int64_t k);
 void jxo_rms_norm(float* out, const float* x, const float* weight, int64_t size, float eps);
 float jxo_vec_dot_q8(int32_t type, const uint8_t* w, const uint8_t* xq8, int64_t k, int32_t order);
 float jxo_vec_dot_q4_K_f32(const uint8_t* w, const float* y, int64_t k);
+/* vec_dot_quant_f32 (src/quant.cpp:3269-3305) for F32, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K. */
+float jxo_vec_dot_quant_f32(int32_t type, const uint8_t* w, const float* y, int64_t k);
 void jxo_matmul_quant_f32(int32_t type, const uint8_t* W, const float* x, float* out,
                           int64_t rows, int64_t cols, int32_t order);
 void jxo_matmul_swiglu_quant_f32(int32_t gate_type, const uint8_t* Wg, int32_t up_type, const uint8_t* Wu,

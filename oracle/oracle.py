@@ -78,6 +78,8 @@ class Oracle:
         getattr(L, p + "vec_dot_q4_K_f32").restype = C.c_float
         getattr(L, p + "vec_dot_q4_K_f32").argtypes = [_u8, _fp, C.c_int64]
         getattr(L, p + "vec_dot_q8").restype = C.c_float
+        getattr(L, p + "vec_dot_quant_f32").restype = C.c_float
+        getattr(L, p + "vec_dot_quant_f32").argtypes = [C.c_int32, _u8, _fp, C.c_int64]
         getattr(L, p + "select_experts").restype = C.c_int32
         getattr(L, p + "select_experts").argtypes = [_fp, C.c_int32, C.c_int32, _i32, _fp]
         getattr(L, p + "moe_forward").restype = C.c_int32
@@ -126,6 +128,12 @@ class Oracle:
         w = np.ascontiguousarray(w, dtype=np.uint8)
         y = np.ascontiguousarray(y, dtype=np.float32)
         return getattr(self.lib, self.p + "vec_dot_q4_K_f32")(_ptr(w, _u8), _ptr(y, _fp), y.size)
+
+    def vec_dot_quant_f32(self, qtype: int, w, y, k: int | None = None) -> float:
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        y = np.ascontiguousarray(y, dtype=np.float32)
+        return getattr(self.lib, self.p + "vec_dot_quant_f32")(qtype, _ptr(w, _u8), _ptr(y, _fp),
+                                                               y.size if k is None else k)
 
     def vec_dot_q8(self, qtype: int, w, xq8, k: int) -> float:
         w = np.ascontiguousarray(w, dtype=np.uint8)
@@ -201,10 +209,11 @@ class Oracle:
             return a.ctypes.data_as(t)
 
         gt, ut, dt = lw.types
+        sgt, sut, sdt = lw.sh_types
         D = MoeDesc(cfg.n_experts, cfg.top_k, cfg.d_model, cfg.d_ff, gt, ut, dt,
                     P(lw.router, _fp), P(lw.router_bias, _fp),
                     P(lw.gate, _u8), P(lw.up, _u8), P(lw.down, _u8),
-                    cfg.d_ff_shared, gt, ut, dt,
+                    cfg.d_ff_shared, sgt, sut, sdt,
                     P(lw.sh_gate, _u8), P(lw.sh_up, _u8), P(lw.sh_down, _u8),
                     P(lw.sh_gate_inp, _fp), cfg.act, P(lw.ffn_norm, _fp), P(lw.post_ffw_norm, _fp),
                     cfg.rms_eps, 0)

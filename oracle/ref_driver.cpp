@@ -48,8 +48,14 @@ float jxr_vec_dot_q8(int32_t type, const uint8_t* w, const uint8_t* xq8, int64_t
         case JXO_Q4_0: return moe::vec_dot_q4_0_q8_0(w, y, k);
         case JXO_Q8_0: return moe::vec_dot_q8_0_q8_0(w, y, k);
         case JXO_Q4_K: return moe::vec_dot_q4_K_q8_0(w, y, k);
+        case JXO_Q5_K: return moe::vec_dot_q5_K_q8_0(w, y, k);
+        case JXO_Q6_K: return moe::vec_dot_q6_K_q8_0(w, y, k);
         default: return 0.0f;
     }
+}
+
+float jxr_vec_dot_quant_f32(int32_t type, const uint8_t* w, const float* y, int64_t k) {
+    return moe::vec_dot_quant_f32(static_cast<GGMLType>(type), w, y, k);
 }
 
 void jxr_matmul_quant_f32(int32_t type, const uint8_t* W, const float* x, float* out, int64_t rows, int64_t cols) {

@@ -45,6 +45,19 @@ CASES = [
     ("toy_gelu", 1, [0]),
     ("toy_gelu", 64, ("tiles", 32, 0)),
 ]
+# the five- and six-bit formats (Q4_K_M mixes; whole toy layers of each type, every row stored)
+F3_CASES = [
+    ("toy_q5k", 1, [0]),
+    ("toy_q5k", 64, list(range(64))),
+    ("toy_q6k", 1, [0]),
+    ("toy_q6k", 64, list(range(64))),
+    ("toy_q50", 1, [0]),
+    ("toy_q50", 64, list(range(64))),
+    ("mixtral_q6k", 1, [0]),
+    ("mixtral_q6k", 512, ("tiles", 32, 0)),
+    ("dsv2lite_q50", 1, [0]),
+    ("dsv2lite_q50", 32, ("tiles", 16, 16)),
+]
 # the residual-stream form (rms_norm before, post_ffw_norm and the residual add after the block)
 RESID_CASES = [
     ("toy_norm", 1, [0]),
@@ -175,6 +188,44 @@ def make_units(ref: Oracle) -> str:
     return path
 
 
+def make_units_f3(ref: Oracle) -> str:
+    """Function-level vectors of the five- and six-bit formats (Q5_0, Q5_K, Q6_K) and of the fp32-activation
+    dots of every expert format: dequantize_row, vec_dot_quant_f32, the Q8_0-activation dots and the two
+    matmul dispatchers over both activation forms."""
+    kw = {}
+    for qt in (F.Q5_0, F.Q5_K, F.Q6_K):  # dequantize_row, two rows (all scale bytes / fifth bits exercised)
+        cols = 512
+        w = synth.quant_matrix(synth.sub_seed("units_f3", f"deq{qt}"), qt, 2, cols)
+        kw[f"deq_w_{qt}"] = w
+        kw[f"deq_o_{qt}"] = np.concatenate([ref.dequantize_row(qt, w[r * F.row_bytes(qt, cols):], cols) for r in range(2)])
+    # matmul_quant_f32: K-quants at 2048 (Q8_0 activations) and 896 / 1408 (fp32, partial super-block);
+    # Q5_0 (fp32 always); Q4_0 / Q8_0 with 4 rows (fp32: matmul_quant_f32 quantizes x only from 8 rows)
+    for qt, rows, cols in ((F.Q5_K, 16, 2048), (F.Q6_K, 16, 2048), (F.Q5_K, 16, 896), (F.Q6_K, 16, 1408),
+                           (F.Q5_0, 16, 1408), (F.Q4_0, 4, 512), (F.Q8_0, 4, 512), (F.Q4_K, 4, 512)):
+        key = f"{qt}_{rows}_{cols}"
+        w = synth.quant_matrix(synth.sub_seed("units_f3", f"w{key}"), qt, rows, cols)
+        y = synth.normal_f32(synth.sub_seed("units_f3", f"y{key}"), cols, 1.0)
+        kw[f"mm_w_{key}"], kw[f"mm_y_{key}"] = w, y
+        kw[f"mm_o_{key}"] = ref.matmul_quant_f32(qt, w, y, rows, cols)
+        rb = F.row_bytes(qt, cols)
+        kw[f"f32_o_{key}"] = np.array([ref.vec_dot_quant_f32(qt, w[r * rb:(r + 1) * rb], y) for r in range(rows)],
+                                      np.float32)
+        if qt in (F.Q5_K, F.Q6_K):  # the Q8_0-activation block dot directly, partial super-block included
+            yq = ref.quantize_row_q8_0(np.concatenate([y, np.zeros((-cols) % 256, np.float32)]))
+            kw[f"q8_o_{key}"] = np.array([ref.vec_dot_q8(qt, w[r * rb:(r + 1) * rb], yq, cols) for r in range(rows)],
+                                         np.float32)
+    # matmul_swiglu_quant_f32 with fp32 x (Q5_0) and Q8_0 x (Q6_K, Q5_K)
+    for qt in (F.Q5_0, F.Q6_K, F.Q5_K):
+        g = synth.quant_matrix(synth.sub_seed("units_f3", f"swg{qt}"), qt, 64, 512)
+        u = synth.quant_matrix(synth.sub_seed("units_f3", f"swu{qt}"), qt, 64, 512)
+        x = synth.normal_f32(synth.sub_seed("units_f3", f"swx{qt}"), 512, 1.0)
+        kw[f"sw_g_{qt}"], kw[f"sw_u_{qt}"], kw[f"sw_x_{qt}"] = g, u, x
+        kw[f"sw_o_{qt}"] = ref.matmul_swiglu_quant_f32(qt, g, qt, u, x, 64, 512)
+    path = os.path.join(OUT, "units_f3.npz")
+    np.savez_compressed(path, **kw)
+    return path
+
+
 TOY_GGUF = "/root/reference/models/qwen_run.gguf"
 
 
@@ -218,6 +269,12 @@ def main() -> None:
     if "--gguf" in sys.argv:  # only the toy-model fixture
         print(make_gguf_case(Oracle("reference", avx512=False)))
         return
+    if "--f3" in sys.argv:  # only the five- and six-bit format fixtures
+        ref = Oracle("reference", avx512=False)
+        print(make_units_f3(ref))
+        for name, n, rows in F3_CASES:
+            print(make_case(ref, name, n, rows))
+        return
     if "--resid" in sys.argv:  # only the residual-stream cases
         ref = Oracle("reference", avx512=False)
         for name, n, rows in RESID_CASES:
@@ -235,6 +292,9 @@ def main() -> None:
         print(make_case(ref, name, n, rows))
     for name, n, rows in RESID_CASES:
         print(make_case(ref, name, n, rows, tag="_resid", residual=True))
+    print(make_units_f3(ref))
+    for name, n, rows in F3_CASES:
+        print(make_case(ref, name, n, rows))
     subprocess.run([sys.executable, os.path.abspath(__file__), "--avx512-child"], check=True)
 
 

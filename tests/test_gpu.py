@@ -570,7 +570,12 @@ def test_residual_form_vs_oracle(moe, port, name, n, regime):
 @pytest.mark.parametrize("types,cols,rows", [((F.Q4_K, F.Q4_0, F.Q8_0), 512, (256, 4, 4)),
                                              ((F.Q4_K, F.Q4_K, F.Q4_K), 1408, (64, 32, 32)),
                                              ((F.Q4_K, F.Q4_K, F.Q4_K), 256, (2, 2, 2)),
-                                             ((F.Q4_0, F.Q4_K, None), 2048, (1024, 512, 0))])
+                                             ((F.Q4_0, F.Q4_K, None), 2048, (1024, 512, 0)),
+                                             # Q4_K_M attention blocks: Q5_0 q/k with a Q6_K v at 896 columns
+                                             # (fp32 activations throughout), Q6_K v at 2048 (Q8_0)
+                                             ((F.Q5_0, F.Q5_0, F.Q6_K), 896, (896, 128, 128)),
+                                             ((F.Q4_K, F.Q4_K, F.Q6_K), 2048, (2048, 256, 256)),
+                                             ((F.Q6_K, None, F.Q5_K), 4096, (4096, 0, 64))])
 def test_dense_device_dropins(moe, port, types, cols, rows):
     """jx_matmul_qkv_quant_f32_dev and jx_matmul_quant_f32_dev on device pointers against the oracle's
     matmul_qkv_quant_f32 / matmul_quant_f32 (same integer block sums; fp32 order differs)."""

@@ -45,7 +45,24 @@ def deq_matrix(qt: int, w: np.ndarray, rows: int, cols: int) -> np.ndarray:
     if qt == F.Q8_0:
         d = b[:, :, 0:2].copy().view(np.float16).astype(np.float64)
         return (b[:, :, 2:34].view(np.int8).astype(np.float64) * d).reshape(rows, nb * 32)[:, :cols]
-    # Q4_K: d, dmin, 12 bytes of 6-bit (scale, min) pairs, 128 bytes of nibbles
+    if qt == F.Q5_0:  # d, qh (u32 LE: bit j = fifth bit of element j), qs: low nibbles 0..15, high 16..31
+        d = b[:, :, 0:2].copy().view(np.float16).astype(np.float64)
+        qh = b[:, :, 2:6].copy().view("<u4").astype(np.int64)
+        qs = b[:, :, 6:22].astype(np.int64)
+        bits = (qh >> np.arange(32)) & 1
+        vals = np.concatenate([qs & 15, qs >> 4], axis=2) + 16 * bits - 16
+        return (vals * d).reshape(rows, nb * 32)[:, :cols]
+    if qt == F.Q6_K:  # ql[128], qh[64], int8 scales[16], d; element 128n + 32r + l
+        ql = b[:, :, 0:128].astype(np.int64).reshape(rows, nb, 2, 2, 32)   # [n][r % 2][l]
+        qh = b[:, :, 128:192].astype(np.int64).reshape(rows, nb, 2, 1, 32)  # [n][l]
+        sc = b[:, :, 192:208].view(np.int8).astype(np.float64)
+        d = b[:, :, 208:210].copy().view(np.float16).astype(np.float64)
+        r = np.arange(4).reshape(1, 1, 1, 4, 1)
+        nib = (np.take_along_axis(ql, np.broadcast_to(r % 2, (rows, nb, 2, 4, 1)), axis=3) >> (4 * (r // 2))) & 15
+        q = (nib | (((qh >> (2 * r)) & 3) << 4)) - 32  # [rows][nb][n][r][l]
+        vals = q.reshape(rows, nb, 256) * np.repeat(sc, 16, axis=2) * d
+        return vals.reshape(rows, nb * 256)[:, :cols]
+    # Q4_K / Q5_K: d, dmin, 12 bytes of 6-bit (scale, min) pairs (Q5_K: then qh[32]), 128 bytes of nibbles
     d = b[:, :, 0:2].copy().view(np.float16).astype(np.float64)[..., 0]
     dmin = b[:, :, 2:4].copy().view(np.float16).astype(np.float64)[..., 0]
     s = b[:, :, 4:16].astype(np.int64)
@@ -55,8 +72,12 @@ def deq_matrix(qt: int, w: np.ndarray, rows: int, cols: int) -> np.ndarray:
     mn[..., :4] = s[..., 4:8] & 63
     sc[..., 4:] = (s[..., 8:12] & 15) | ((s[..., 0:4] >> 6) << 4)
     mn[..., 4:] = (s[..., 8:12] >> 4) | ((s[..., 4:8] >> 6) << 4)
-    qs = b[:, :, 16:144].astype(np.int64).reshape(rows, nb, 4, 32)
+    q0 = 48 if qt == F.Q5_K else 16
+    qs = b[:, :, q0:q0 + 128].astype(np.int64).reshape(rows, nb, 4, 32)
     nib = np.stack([qs & 15, qs >> 4], axis=3).reshape(rows, nb, 8, 32)  # sub-block 2j: low, 2j+1: high
+    if qt == F.Q5_K:  # fifth bit of element l of sub-block j: bit j of qh[l]
+        qh = b[:, :, 16:48].astype(np.int64)
+        nib = nib + 16 * ((qh[:, :, None, :] >> np.arange(8).reshape(1, 1, 8, 1)) & 1)
     w_ = d[..., None, None] * sc[..., None] * nib - dmin[..., None, None] * mn[..., None]
     return w_.reshape(rows, nb * 256)[:, :cols]
 
@@ -200,6 +221,82 @@ def test_gelu_gate_live_vs_reference(port, ref, qt, rows, cols):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+# --------------------------------------------------------------- the five- and six-bit formats
+F3_MM = ["13_16_2048", "14_16_2048", "13_16_896", "14_16_1408", "6_16_1408", "2_4_512", "8_4_512", "12_4_512"]
+
+
+@pytest.mark.parametrize("qt", [F.Q5_0, F.Q5_K, F.Q6_K])
+def test_f3_dequantize_golden(port, qt):
+    """dequantize_row_q5_0 / _q5_K / _q6_K (src/quant.cpp:1585-1600, 1345-1387, 1389-1428) bit for bit
+    against the reference build's vectors and exactly against the closed-form decode (every value is
+    exact in fp32: d * sc * q products of at most 22 bits)."""
+    z = load("units_f3.npz")
+    w, cols = z[f"deq_w_{qt}"], 512
+    rb = F.row_bytes(qt, cols)
+    got = np.concatenate([port.dequantize_row(qt, w[r * rb:], cols) for r in range(2)])
+    assert np.array_equal(got.view(np.uint32), z[f"deq_o_{qt}"].view(np.uint32))
+    assert np.array_equal(got.astype(np.float64), deq_matrix(qt, w, 2, cols).reshape(-1))
+
+
+@pytest.mark.parametrize("key", F3_MM)
+def test_f3_dots_golden_and_float64(port, key):
+    """matmul_quant_f32 (Q8_0 x from 8 rows where the type allows, fp32 otherwise), vec_dot_quant_f32 and
+    the Q5_K / Q6_K Q8_0-activation dots (src/quant.cpp:3648-3818) against the reference build's vectors,
+    then against the float64 closed form with the activations each path uses."""
+    z = load("units_f3.npz")
+    qt, rows, cols = map(int, key.split("_"))
+    w, y = z[f"mm_w_{key}"], z[f"mm_y_{key}"]
+    got = port.matmul_quant_f32(qt, w, y, rows, cols)
+    assert np.array_equal(got.view(np.uint32), z[f"mm_o_{key}"].view(np.uint32))
+    rb = F.row_bytes(qt, cols)
+    f32 = np.array([port.vec_dot_quant_f32(qt, w[r * rb:(r + 1) * rb], y) for r in range(rows)], np.float32)
+    assert np.array_equal(f32.view(np.uint32), z[f"f32_o_{key}"].view(np.uint32))
+    W = deq_matrix(qt, w, rows, cols)
+    y64 = y.astype(np.float64)
+    assert np.all(np.abs(f32 - W @ y64) <= 2e-6 * (np.abs(W) @ np.abs(y64)) + 1e-30)
+    if qt in (F.Q5_K, F.Q6_K):
+        yq = port.quantize_row_q8_0(np.concatenate([y, np.zeros((-cols) % 256, np.float32)]))
+        q8 = np.array([port.vec_dot_q8(qt, w[r * rb:(r + 1) * rb], yq, cols) for r in range(rows)], np.float32)
+        assert np.array_equal(q8.view(np.uint32), z[f"q8_o_{key}"].view(np.uint32))
+        ya = deq_q8_blocks(yq)[:cols]
+        assert np.all(np.abs(q8 - W @ ya) <= 2e-6 * (np.abs(W) @ np.abs(ya)) + 1e-30)
+    # the dispatcher's activation form (supports_q8_activation, quant.cpp:3881-3893, from 8 rows): here
+    # every case without Q8_0 activations must equal the fp32 dots, and every Q5_K / Q6_K one with them
+    # the Q8_0 dots
+    if not (rows >= 8 and F.supports_q8_activation(qt, cols)):
+        assert np.array_equal(got.view(np.uint32), f32.view(np.uint32))
+    elif qt in (F.Q5_K, F.Q6_K):
+        assert np.array_equal(got.view(np.uint32), q8.view(np.uint32))
+
+
+@pytest.mark.parametrize("qt", [F.Q5_0, F.Q6_K, F.Q5_K])
+def test_f3_swiglu_golden(port, qt):
+    """matmul_swiglu_quant_f32 over fp32 x (Q5_0: no Q8_0 form) and Q8_0 x (Q5_K, Q6_K)."""
+    z = load("units_f3.npz")
+    g, u, x = z[f"sw_g_{qt}"], z[f"sw_u_{qt}"], z[f"sw_x_{qt}"]
+    got = port.matmul_swiglu_quant_f32(qt, g, qt, u, x, 64, 512)
+    assert np.array_equal(got.view(np.uint32), z[f"sw_o_{qt}"].view(np.uint32))
+    xa = x.astype(np.float64) if qt == F.Q5_0 else deq_q8_blocks(port.quantize_row_q8_0(x))
+    gv, uv = deq_matrix(qt, g, 64, 512) @ xa, deq_matrix(qt, u, 64, 512) @ xa
+    np.testing.assert_allclose(got, gv / (1 + np.exp(-gv)) * uv, rtol=1e-5, atol=1e-6 * np.abs(got).max())
+
+
+def test_f3_q6k_scale_extremes(port, ref):
+    """Q6_K with every sub-block scale at -128 or 127 and quants at 0 / 63 (the largest |sc * (q - 32)|),
+    both dots, against the reference build."""
+    rows, cols = 8, 512
+    w = synth.quant_matrix(synth.sub_seed("q6x", "w"), F.Q6_K, rows, cols).reshape(rows * 2, 210)
+    w[:, 192:208] = np.where(np.arange(16) % 2, 0x80, 0x7F).astype(np.uint8)
+    w[0::2, 0:192] = 0xFF
+    w[1::2, 0:192] = 0x00
+    w = w.reshape(-1)
+    y = synth.normal_f32(synth.sub_seed("q6x", "y"), cols, 50.0)
+    for rr in (rows, 4):  # Q8_0 and fp32 activations
+        a = port.matmul_quant_f32(F.Q6_K, w, y, rr, cols)
+        b = ref.matmul_quant_f32(F.Q6_K, w, y, rr, cols)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 @pytest.mark.parametrize("qt,cols", [(F.Q4_0, 512), (F.Q8_0, 512), (F.Q4_K, 1024)])
 def test_dequantize_row(port, qt, cols):
     """dequantize_row_q4_0 / _q8_0 / _q4_K (src/quant.cpp:1014-1057, 1209-1249) against the formats'
@@ -300,7 +397,9 @@ def test_select_experts_live_vs_reference(port, ref):
 
 
 # --------------------------------------------------------------- whole MoE block vs the golden vectors
-GOLDEN_CASES = ["toy_n1", "qwen15moe_n1", "qwen15moe_n64", "mixtral_n1", "mixtral_n512",
+F3_GOLDEN_CASES = ["toy_q5k_n1", "toy_q5k_n64", "toy_q6k_n1", "toy_q6k_n64", "toy_q50_n1", "toy_q50_n64",
+                   "mixtral_q6k_n1", "mixtral_q6k_n512", "dsv2lite_q50_n1", "dsv2lite_q50_n32"]
+GOLDEN_CASES = F3_GOLDEN_CASES + ["toy_n1", "qwen15moe_n1", "qwen15moe_n64", "mixtral_n1", "mixtral_n512",
                 "mixtral_n2048", "qwen3moe_n2048", "dsv2lite_n32", "toy_gelu_n1", "toy_gelu_n64",
                 "toy_norm_n1_resid", "toy_norm_n64_resid"]
 
@@ -347,7 +446,10 @@ def test_moe_block_live_vs_reference(port, ref):
                                            (F.Q8_0, 16, 4, 256, 320, 0, False, 0),
                                            (F.Q4_K, 8, 3, 512, 768, 512, True, 0),
                                            (F.Q4_K, 6, 2, 256, 1408, 1408, False, 0),
-                                           (F.Q4_K, 8, 2, 512, 768, 512, True, 1)]:
+                                           (F.Q4_K, 8, 2, 512, 768, 512, True, 1),
+                                           (F.Q5_K, 8, 2, 512, 768, 512, True, 0),
+                                           (F.Q6_K, 8, 3, 256, 640, 0, False, 1),
+                                           (F.Q5_0, 8, 2, 256, 640, 320, True, 0)]:
         cfg = synth.LayerConfig(f"live{qt}_{Fd}_{act}", d, E, k, Fd, qt, d_ff_shared=Fs, shared_gate=gate, act=act)
         lw = synth.make_layer(cfg, seed=99)
         x = synth.make_tokens(cfg, 6, seed=99)
@@ -361,33 +463,36 @@ def test_moe_block_live_vs_reference(port, ref):
 def _block_float64(port, lw, x, ids, probs):
     cfg = lw.cfg
     d, Fd, E = cfg.d_model, cfg.d_ff, cfg.n_experts
-    t = cfg.wtype
+    t, td, tsd = cfg.wtype, cfg.down_t, cfg.sh_down_t
     G = deq_matrix(t, lw.gate, E * Fd, d).reshape(E, Fd, d)
     U = deq_matrix(t, lw.up, E * Fd, d).reshape(E, Fd, d)
-    D = deq_matrix(t, lw.down, E * d, Fd).reshape(E, d, Fd)
+    D = deq_matrix(td, lw.down, E * d, Fd).reshape(E, d, Fd)
+
+    def act_in(v, qt, k):  # the activations each path uses: Q8_0 where the type allows, fp32 otherwise
+        return deq_q8_blocks(port.quantize_row_q8_0(v)) if F.supports_q8_activation(qt, k) else v.astype(np.float64)
+
     out = np.zeros((x.shape[0], d))
     for i in range(x.shape[0]):
-        xa = deq_q8_blocks(port.quantize_row_q8_0(x[i]))
+        xa = act_in(x[i], t, d)
         for s in range(cfg.top_k):
             e = ids[i, s]
             g, u = G[e] @ xa, U[e] @ xa
             h = ((_gelu64(g) if cfg.act else g / (1 + np.exp(-g))) * u).astype(np.float32)
-            ha = deq_q8_blocks(port.quantize_row_q8_0(h)) if F.supports_q8_activation(t, Fd) else h.astype(np.float64)
-            out[i] += probs[i, s] * (D[e] @ ha)
+            out[i] += probs[i, s] * (D[e] @ act_in(h, td, Fd))
         if cfg.has_shared:
             Fs = cfg.d_ff_shared
             g = deq_matrix(t, lw.sh_gate, Fs, d) @ xa
             u = deq_matrix(t, lw.sh_up, Fs, d) @ xa
             h = ((_gelu64(g) if cfg.act else g / (1 + np.exp(-g))) * u).astype(np.float32)
-            ha = deq_q8_blocks(port.quantize_row_q8_0(h)) if F.supports_q8_activation(t, Fs) else h.astype(np.float64)
             sh = 1.0
             if lw.sh_gate_inp is not None:
                 sh = 1 / (1 + np.exp(-(lw.sh_gate_inp.astype(np.float64) @ x[i].astype(np.float64))))
-            out[i] += sh * (deq_matrix(t, lw.sh_down, d, Fs) @ ha)
+            out[i] += sh * (deq_matrix(tsd, lw.sh_down, d, Fs) @ act_in(h, tsd, Fs))
     return out
 
 
-@pytest.mark.parametrize("name,n", [("toy", 3), ("dsv2lite", 2), ("qwen15moe", 2), ("toy_gelu", 3)])
+@pytest.mark.parametrize("name,n", [("toy", 3), ("dsv2lite", 2), ("qwen15moe", 2), ("toy_gelu", 3), ("toy_q5k", 3),
+                                    ("toy_q6k", 3), ("toy_q50", 3), ("dsv2lite_q50", 2)])
 def test_moe_block_float64_restatement(port, name, n):
     cfg, lw, x = _layer(name, 64 if name == "qwen15moe" else n)
     x = x[:n]
