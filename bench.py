@@ -47,7 +47,9 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "mixtral_layer_traffic.json")
 
 # every configured point: (config, tokens)
 POINTS = [("toy", 1), ("qwen15moe", 1), ("qwen15moe", 64), ("mixtral", 1), ("mixtral", 512), ("mixtral", 2048),
-          ("qwen3moe", 2048), ("dsv2lite", 32)]
+          ("qwen3moe", 2048), ("dsv2lite", 32),
+          # the mixed-format layers of Q4_K_M files (Q6_K down; Q5_0 routed down, Q6_K shared down)
+          ("mixtral_q6k", 1), ("mixtral_q6k", 2048), ("dsv2lite_q50", 1), ("dsv2lite_q50", 32), ("dsv2lite_q50", 2048)]
 
 
 class Hip:
@@ -135,7 +137,7 @@ def algorithmic(cfg, n, counts):
     d, Fd, E = cfg.d_model, cfg.d_ff, cfg.n_experts
     distinct = int((np.asarray(counts) > 0).sum())
     gu_bytes = 2 * F.matrix_bytes(t, Fd, d)
-    dn_bytes = F.matrix_bytes(t, d, Fd)
+    dn_bytes = F.matrix_bytes(cfg.down_t, d, Fd)
     nbytes = distinct * (gu_bytes + dn_bytes) + synth.shared_bytes(cfg)
     nbytes += E * d * 4 + (d * 4 if cfg.shared_gate else 0) + n * d * 4 * 2
     ops = 2 * n * cfg.top_k * 3 * d * Fd + 2 * n * 3 * d * cfg.d_ff_shared

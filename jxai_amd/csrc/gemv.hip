@@ -23,7 +23,8 @@
 //         16h..16h+15 of each block (sub-block 2r + h of block r): ql chunks h and 2 + h and qh
 //         chunk 4 + h of that half, its 8 scales and d
 //   Q4_0  eight 32-blocks: lanes of half h take the four blocks of parity h
-//   Q5_0  as Q4_0 + each block's 32 fifth bits (fp32 activations only)
+//   Q5_0  four 32-blocks: lanes of half h take the two blocks of parity h, with their 32 fifth
+//         bits (fp32 activations only)
 //   Q8_0  four 32-blocks: lanes of half h take half h of each
 #include <algorithm>
 
@@ -54,9 +55,9 @@ struct RawQ6K {
     uint32_t d;  // fp16 bits of d
 };
 struct RawB5 {
-    uint4 q[4];
-    uint32_t d[4];
-    uint32_t qh[4];
+    uint4 q[2];
+    uint32_t d[2];
+    uint32_t qh[2];
 };
 
 template <int TYPE>
@@ -120,7 +121,7 @@ struct Fmt<T_Q4_K> {
 template <>
 struct Fmt<T_Q5_0> {
     using Raw = RawB5;
-    static constexpr int BPU = 8;
+    static constexpr int BPU = 4;
     __device__ static void load(Raw& c, const QMat& W, int e, int rt, int u, int m, int h, bool ok) {
         const size_t b0 = (size_t)rt * W.nkb + (size_t)u * BPU + h;
         const uint8_t* qb = W.qs + e * W.qs_es;
@@ -128,7 +129,7 @@ struct Fmt<T_Q5_0> {
         const uint8_t* xb = W.ex + e * W.ex_es;
         const int left = W.nkb - u * BPU - h;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 2; ++i) {
             const bool v = ok && 2 * i < left;
             const size_t t = (b0 + 2 * i) * 32 + m;
             c.q[i] = ld_stream16(v ? qb + t * 16 : W.pad_qs + m * 16);
@@ -516,28 +517,34 @@ __device__ __forceinline__ void unit_accum_f32(const typename Fmt<TYPE>::Raw& c,
             }
         }
     } else {  // Q4_0 / Q5_0: whole blocks of parity h
+        constexpr int NB = Fmt<TYPE>::BPU / 2;  // blocks per lane
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int b = u * 8 + 2 * i + h;
+        for (int i = 0; i < NB; ++i) {
+            const int b = u * Fmt<TYPE>::BPU + 2 * i + h;
             if (b < nkb) {
                 const float dw = f16_to_f32(c.d[i] & 0xFFFFu);
-                uint32_t w[8];
+                const float off = TYPE == T_Q5_0 ? -16.0f : -8.0f;
 #pragma unroll
-                for (int z = 0; z < 4; ++z) {
-                    w[z] = comp(c.q[i], z) & 0x0F0F0F0Fu;          // elements 4z..4z+3
-                    w[4 + z] = (comp(c.q[i], z) >> 4) & 0x0F0F0F0Fu;  // elements 16 + 4z..
+                for (int j = 0; j < TB; ++j) {
+                    if (j < nt) {
+                        // the low nibbles (elements 0..15), then the high ones (16..31), one half's
+                        // activations in registers at a time
+                        float s2[2];
+#pragma unroll
+                        for (int hb = 0; hb < 2; ++hb) {
+                            uint32_t w[4];
+#pragma unroll
+                            for (int z = 0; z < 4; ++z) {
+                                w[z] = (comp(c.q[i], z) >> (4 * hb)) & 0x0F0F0F0Fu;
+                                if constexpr (TYPE == T_Q5_0)  // fifth bit e of element e (dequantize_row_q5_0)
+                                    w[z] |= ((((c.qh[i] >> (16 * hb + 4 * z)) & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
+                            }
+                            s2[hb] = dot_f32_words<4>(w, A.f + j * A.K + b * 32 + 16 * hb, off);
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                        acc[j] = __builtin_fmaf(dw, s2[0] + s2[1], acc[j]);
+                    }
                 }
-                float off = -8.0f;
-                if constexpr (TYPE == T_Q5_0) {  // fifth bit j of element j (dequantize_row_q5_0, 1585-1600)
-                    const uint32_t qh = c.qh[i];
-#pragma unroll
-                    for (int z = 0; z < 8; ++z)
-                        w[z] |= ((((qh >> (4 * z)) & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
-                    off = -16.0f;
-                }
-#pragma unroll
-                for (int j = 0; j < TB; ++j)
-                    if (j < nt) acc[j] = __builtin_fmaf(dw, dot_f32_words<8>(w, A.f + j * A.K + b * 32, off), acc[j]);
             }
         }
     }
@@ -711,11 +718,12 @@ __device__ __forceinline__ void kloop(const QMat& W0, const QMat& W1, int e, int
 #define JX_GEMV_TB4_WPS 2
 #endif
 #define GEMV_WAVES_PER_SIMD(TB) ((TB) == 1 ? 4 : JX_GEMV_TB4_WPS)
-// The single-token down GEMV's fp32-activation dots other than Q4_K's do not fit 128 VGPRs with two
-// units in flight; they run at 2 waves per SIMD (one 8-wave block per CU, as at 3).
+// The single-token down GEMV's fp32-activation dots of Q8_0 and Q6_K (matrices under 8 rows; Q6_K with
+// K % 256 != 0) do not fit 128 VGPRs with two units in flight; they run at 2 waves per SIMD (one 8-wave
+// block per CU).
 template <int TYPE, int TB, bool F32ACT>
 constexpr int down_wps() {
-    return TB == 1 && F32ACT && TYPE != T_Q4_K && TYPE != T_Q5_K ? 2 : GEMV_WAVES_PER_SIMD(TB);
+    return TB == 1 && F32ACT && (TYPE == T_Q8_0 || TYPE == T_Q6_K) ? 2 : GEMV_WAVES_PER_SIMD(TB);
 }
 
 // Gate + up + SwiGLU (matmul_swiglu_quant_f32, src/quant.cpp:3970-4009) and
