@@ -97,10 +97,10 @@ class Hip:
 
 
 def measured_traffic(role, tokens):
-    """HBM bytes per launch of the kernel timed as `role` (gateup_mfma, down_mfma, gateup_gemv,
-    down_gemv) at `tokens` tokens from the rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE in
-    KiB per dispatch, each scaled by what the counter reads for a plain device copy of known size),
-    or None when no summary covers it."""
+    """Memory bytes per launch of the kernel timed as `role` (gateup_mfma, down_mfma, gateup_gemv,
+    down_gemv) at `tokens` tokens from the rocprofv3 --pmc summary: the L2's read and write requests
+    to memory times their sizes (exact on a plain device copy of known size), or None when no
+    summary covers it."""
     try:
         with open(TRAFFIC_FILE) as f:
             t = json.load(f)
@@ -109,7 +109,7 @@ def measured_traffic(role, tokens):
     k = t.get("kernels", {}).get(f"{role}@{tokens}")
     if not k:
         return None
-    return 1024.0 * (k["fetch_kib"] * t["fetch_scale"] + k["write_kib"] * t["write_scale"])
+    return k["read_bytes"] + k["write_bytes"]
 
 
 def copy_calibration():

@@ -32,8 +32,13 @@ enum {
     JX_ERR_NODEVICE = 5      /* no gfx950 device / init not done              */
 };
 
-/* GGML tensor type codes, as GGMLType in include/common.h:45-77. */
-enum { JX_TYPE_F32 = 0, JX_TYPE_Q4_0 = 2, JX_TYPE_Q8_0 = 8, JX_TYPE_Q4_K = 12 };
+/* GGML tensor type codes, as GGMLType in include/common.h:45-77.  Expert and
+ * qmatrix weights take the six block formats below; activations are Q8_0 where
+ * supports_q8_activation allows (src/quant.cpp:3881-3893: Q4_0 / Q8_0 with
+ * cols % 32 == 0, Q4_K / Q5_K / Q6_K with cols % 256 == 0), fp32 otherwise
+ * (Q5_0 always), as the reference's dots. */
+enum { JX_TYPE_F32 = 0, JX_TYPE_Q4_0 = 2, JX_TYPE_Q5_0 = 6, JX_TYPE_Q8_0 = 8, JX_TYPE_Q4_K = 12, JX_TYPE_Q5_K = 13,
+       JX_TYPE_Q6_K = 14 };
 
 /* Gated activation of the expert FFN (hp_.use_gelu, src/transformer.cpp:1995,
  * passed to matmul_swiglu_quant_f32 at 2724; src/quant.cpp:3999-4007). */
@@ -58,7 +63,7 @@ typedef struct jx_moe_layer_desc {
     int32_t top_k;         /* k        (hp_.n_experts_used)                     */
     int32_t d_model;       /* d        (hp_.dim)                                */
     int32_t d_ff;          /* F        (hp_.moe_expert_dim)                     */
-    int32_t gate_type, up_type, down_type;  /* Q4_0 / Q8_0 / Q4_K            */
+    int32_t gate_type, up_type, down_type;  /* JX_TYPE_Q*; gate == up      */
     const float* router;   /* [E][d] fp32, blk.L.ffn_gate_inp.weight            */
     const float* router_bias; /* [E] fp32 added to the logits, or NULL          */
     const void* gate_exps;
