@@ -11,9 +11,10 @@ timed region).  Headline workload: the Mixtral-8x7B-shaped Q4_K MoE layer
 and `configs`, every configured layer shape at its token counts, each with the
 algorithmic bytes and int8 ops of the pass and their roofline fractions.
 
-Timing: K steps between two device synchronizations give `value` and
-`ms_per_step`; HIP events recorded on the forward's stream around each step in
-the same timed region give the per-step median and p10/p90.  Before timing,
+Timing: K steps back to back between two device synchronizations give `value`
+and `ms_per_step` (nothing else is enqueued in that region: a timing event costs
+the GPU 3-5 us); a second pass with one HIP event after each step on the
+forward's stream gives the per-step median and p10/p90.  Before timing,
 the device-pointer asynchronous path (the one timed) is checked bit for bit
 against the host-pointer path.  Kernel durations for the rooflines come from a
 second pass with HIP events around every launch.  The prefill GEMMs run
@@ -150,7 +151,8 @@ def pct(a, q):
 
 
 def run_gpu(hip, L, cfg, n, steps, warmup, regime=None):
-    """Warm-up, a bit-exact check of the timed path, K timed steps, then a profiled pass."""
+    """Warm-up, a bit-exact check of the timed path, K timed steps, a pass with one timing event per
+    step (the per-step distribution), then a profiled pass."""
     from jxai_amd import moe
     x = synth.make_tokens(cfg, n)
     xb = moe.DeviceBuffer(x.nbytes).upload(x)
@@ -162,18 +164,24 @@ def run_gpu(hip, L, cfg, n, steps, warmup, regime=None):
     got = ob.download(np.empty_like(x))
     if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
         raise SystemExit(f"bench: the timed device path differs from the host path ({cfg.name}, n={n})")
-    evs = hip.events(2 * steps)
     moe.lib().jx_device_synchronize()
-    # timed region: the production path (graph replays for small batches), events between steps only
+    # timed region: K steps of the production path back to back between two device synchronizations,
+    # nothing else in the stream (a timing event costs the GPU 3-5 us, a tenth of a decode step)
     t0 = time.perf_counter()
-    for i in range(steps):
-        hip.record(evs[2 * i])
+    for _ in range(steps):
         L.forward_device(xb, n, ob, sync=False, regime=regime, stream=hip.stream)
-        hip.record(evs[2 * i + 1])
     hip.sync()
     moe.lib().jx_device_synchronize()
     t1 = time.perf_counter()
-    step_ms = [hip.elapsed_ms(evs[2 * i], evs[2 * i + 1]) for i in range(steps)]
+    # per-step distribution: the same steps with one timing event after each (step i = e[i] - e[i-1];
+    # each interval includes one event's cost)
+    evs = hip.events(steps + 1)
+    hip.record(evs[0])
+    for i in range(steps):
+        L.forward_device(xb, n, ob, sync=False, regime=regime, stream=hip.stream)
+        hip.record(evs[i + 1])
+    hip.sync()
+    step_ms = [hip.elapsed_ms(evs[i], evs[i + 1]) for i in range(steps)]
     hip.free(evs)
     # kernel durations: the same steps again with HIP events around every launch
     L.profile(True)
@@ -188,14 +196,17 @@ def run_gpu(hip, L, cfg, n, steps, warmup, regime=None):
 
 
 def step_stats(r):
+    """Per-step distribution (one timing event per step, included) beside the timed region's mean."""
     s = r["step_ms"]
-    return {"median": float(np.median(s)), "p10": pct(s, 10), "p90": pct(s, 90), "mean_wall": r["wall_s"] * 1e3}
+    return {"median": float(np.median(s)), "p10": pct(s, 10), "p90": pct(s, 90), "mean_wall": r["wall_s"] * 1e3,
+            "note": "median/p10/p90 from a second pass with one hipEvent per step (its cost, 3-5 us, included); "
+                    "mean_wall = the timed region (K steps back to back between synchronizations) / K"}
 
 
 def point_line(cfg, n, r):
     """tok/s, algorithmic work and roofline fractions of one configured point."""
     a = algorithmic(cfg, n, r["counts"])
-    t = float(np.median(r["step_ms"])) / 1e3
+    t = r["wall_s"]
     return {"tokens": n, "tok_s": n / t, "step_ms": step_stats(r), "bytes": a["bytes"], "int8_ops": a["ops"],
             "distinct_experts": a["distinct"], "hbm_frac": a["bytes"] / t / 1e9 / HBM_PEAK_GBS,
             "int8_frac": a["ops"] / t / 1e12 / INT8_PEAK_TOPS,

@@ -794,7 +794,14 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
                       hipEventCreateWithFlags(&L->ev_fork, hipEventDisableTiming) != hipSuccess ||
                       hipEventCreateWithFlags(&L->ev_join, hipEventDisableTiming) != hipSuccess))
         return bail(fail(JX_ERR_HIP, "shared-expert stream create"));
-    if (const char* g = std::getenv("JX_NO_GRAPH")) L->use_graphs = std::strcmp(g, "0") == 0;
+    // Graph replays pay where the forward forks the shared expert onto its second stream (the fork and
+    // join become graph edges instead of event waits): measured per decode step with the host running
+    // ahead, Qwen1.5-shaped 53.2 -> 41.6 us, DeepSeek-V2-Lite-shaped 50.1 -> 41.6 us.  Without a shared
+    // expert direct launches are faster (Mixtral-shaped 49.5 -> 46.4 us, Qwen3-shaped 30.8 -> 26.0 us).
+    // JX_NO_GRAPH=1 / JX_GRAPHS=1 force either way (A/B measurement).
+    L->use_graphs = L->shared;
+    if (const char* g = std::getenv("JX_NO_GRAPH")) L->use_graphs = L->use_graphs && std::strcmp(g, "0") == 0;
+    if (const char* g = std::getenv("JX_GRAPHS")) L->use_graphs = std::strcmp(g, "0") != 0;
     if (const char* f = std::getenv("JX_NO_FOLD")) L->fold_combine = std::strcmp(f, "0") == 0;
     *out = L;
     return JX_OK;

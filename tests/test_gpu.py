@@ -327,13 +327,17 @@ def test_decode_two_tokens_same_experts(moe, port, name):
     L.close()
 
 
-def test_graph_replays_match_eager(moe, monkeypatch):
-    """Captured-graph replays, interleaved with eager launches and syncs, equal the eager result bit for bit."""
-    cfg, lw = layer("dsv2lite")
+@pytest.mark.parametrize("name", ["dsv2lite", "toy"])
+def test_graph_replays_match_eager(moe, monkeypatch, name):
+    """Captured-graph replays, interleaved with eager launches and syncs, equal the eager result bit for bit
+    (layers with a shared expert replay graphs by default; the toy layer is forced to)."""
+    cfg, lw = layer(name)
     monkeypatch.setenv("JX_NO_GRAPH", "1")
     eager = moe.MoELayer.from_weights(lw)
     monkeypatch.delenv("JX_NO_GRAPH")
+    monkeypatch.setenv("JX_GRAPHS", "1")
     graphed = moe.MoELayer.from_weights(lw)
+    monkeypatch.delenv("JX_GRAPHS")
     for n in (1, 32, 1):
         x = synth.make_tokens(cfg, n, seed=n + 11)
         want = eager.forward(x)
