@@ -151,19 +151,22 @@ def pct(a, q):
 
 
 def run_gpu(hip, L, cfg, n, steps, warmup, regime=None):
-    """Warm-up, a bit-exact check of the timed path, K timed steps, a pass with one timing event per
+    """A bit-exact check of the timed path, warm-up, K timed steps, a pass with one timing event per
     step (the per-step distribution), then a profiled pass."""
     from jxai_amd import moe
     x = synth.make_tokens(cfg, n)
     xb = moe.DeviceBuffer(x.nbytes).upload(x)
     ob = moe.DeviceBuffer(x.nbytes)
     want, ids, w, counts = L.forward(x, regime=regime)  # host-pointer path; routing of this batch
-    for _ in range(warmup):
-        L.forward_device(xb, n, ob, sync=False, regime=regime, stream=hip.stream)
+    L.forward_device(xb, n, ob, sync=False, regime=regime, stream=hip.stream)
     hip.sync()
     got = ob.download(np.empty_like(x))
     if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
         raise SystemExit(f"bench: the timed device path differs from the host path ({cfg.name}, n={n})")
+    # warm-up right before the timed region (the check above leaves the GPU idle for a while)
+    for _ in range(warmup):
+        L.forward_device(xb, n, ob, sync=False, regime=regime, stream=hip.stream)
+    hip.sync()
     moe.lib().jx_device_synchronize()
     # timed region: K steps of the production path back to back between two device synchronizations,
     # nothing else in the stream (a timing event costs the GPU 3-5 us, a tenth of a decode step)

@@ -37,8 +37,8 @@ enum {
  * supports_q8_activation allows (src/quant.cpp:3881-3893: Q4_0 / Q8_0 with
  * cols % 32 == 0, Q4_K / Q5_K / Q6_K with cols % 256 == 0), fp32 otherwise
  * (Q5_0 always), as the reference's dots. */
-enum { JX_TYPE_F32 = 0, JX_TYPE_Q4_0 = 2, JX_TYPE_Q5_0 = 6, JX_TYPE_Q8_0 = 8, JX_TYPE_Q4_K = 12, JX_TYPE_Q5_K = 13,
-       JX_TYPE_Q6_K = 14 };
+enum { JX_TYPE_F32 = 0, JX_TYPE_F16 = 1, JX_TYPE_Q4_0 = 2, JX_TYPE_Q5_0 = 6, JX_TYPE_Q8_0 = 8, JX_TYPE_Q4_K = 12,
+       JX_TYPE_Q5_K = 13, JX_TYPE_Q6_K = 14, JX_TYPE_BF16 = 30 };
 
 /* Gated activation of the expert FFN (hp_.use_gelu, src/transformer.cpp:1995,
  * passed to matmul_swiglu_quant_f32 at 2724; src/quant.cpp:3999-4007). */
@@ -64,7 +64,7 @@ typedef struct jx_moe_layer_desc {
     int32_t d_model;       /* d        (hp_.dim)                                */
     int32_t d_ff;          /* F        (hp_.moe_expert_dim)                     */
     int32_t gate_type, up_type, down_type;  /* JX_TYPE_Q*; gate == up      */
-    const float* router;   /* [E][d] fp32, blk.L.ffn_gate_inp.weight            */
+    const void* router;    /* [E][d] blk.L.ffn_gate_inp.weight, of router_type  */
     const float* router_bias; /* [E] fp32 added to the logits, or NULL          */
     const void* gate_exps;
     const void* up_exps;
@@ -76,11 +76,13 @@ typedef struct jx_moe_layer_desc {
     const void* sh_down;
     const float* sh_gate_inp; /* [d] fp32 ffn_gate_inp_shexp, or NULL (scale 1) */
     int32_t activation;    /* JX_ACT_SILU or JX_ACT_GELU_TANH (hp_.use_gelu)     */
-    int32_t router_type;   /* type of `router`: JX_TYPE_F32 (0).  The reference
-                              also accepts F16/BF16 routers through
-                              matmul_quant_f32 (transformer.cpp:2591), whose
-                              8-lane dot order (quant.cpp:3015-3055) this
-                              library does not reproduce: JX_ERR_UNSUPPORTED */
+    int32_t router_type;   /* type of `router`: JX_TYPE_F32, JX_TYPE_F16 or
+                              JX_TYPE_BF16 (the reference routes through
+                              matmul_quant_f32(lw.router_gate->type, ...),
+                              transformer.cpp:2591: vec_dot_f32 for F32,
+                              vec_dot_{f16,bf16}_f32's 8-lane order for the
+                              others, quant.cpp:3015-3055); other types:
+                              JX_ERR_UNSUPPORTED */
     /* The steps either side of the block, used with JX_FWD_RESIDUAL
      * (src/transformer.cpp:2585-2587, 2758-2764): */
     const float* ffn_norm;      /* [d] fp32 blk.L.ffn_norm, or NULL (weight 1)       */

@@ -141,7 +141,7 @@ struct CombineOut {
 struct RouteArgs {
     const float* x;        // [n][d]
     int n, d, E, k;
-    const float* router;   // [E][d]
+    const float* router;   // [E][d] fp32 (F16 / BF16 routers converted exactly at upload)
     const float* bias;     // [E] or null
     const float* shgate;   // [d] or null
     ActQ8 xq;              // out: Q8_0 of x (int8 + (scale, sum))
@@ -153,6 +153,7 @@ struct RouteArgs {
     const float* router_cm;  // the router rows, then the shared gate, chain-major (chain_rows)
     float* zero_out = nullptr;  // few-token routers: zero this many floats here first (the folded
     int zero_count = 0;         // combine's output; CombineOut)
+    int chain8 = 0;             // router rows (not the shared gate) in the F16 / BF16 dot order
 };
 
 // Outputs of the token -> expert dispatch (the device side of Groups).

@@ -157,6 +157,18 @@ __device__ void write_acth_row(const int8_t* q, const float2* sc, int K, const A
     }
 }
 
+// The end of a 16-lane router chain group: vec_dot_f32 (src/quant.cpp:2756-2778) adds lane j + 8
+// (the reference's acc1) to lane j < 8 (acc0), then sums lanes 0..7 in order from zero; the F16 /
+// BF16 dots (src/quant.cpp:3015-3055) have the 8 lanes only.
+__device__ __forceinline__ float chain_sum(float acc, bool c8) {
+    const float hi = __shfl_down(acc, 8, 16);
+    const float v = c8 ? acc : acc + hi;
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) s += __shfl(v, q, 16);
+    return s;
+}
+
 // Chain-major rows: element 16 i + j of a row at j * S + i, so lane j of a
 // vec_dot_f32 chain reads its operands four at a time.  In LDS the stride is
 // padded to a multiple of 4 floats plus 4 against bank conflicts; the router
@@ -341,40 +353,69 @@ __global__ void __launch_bounds__(RT_THREADS) k_route(RouteArgs a, int nsplit, i
         const int r1 = min(R, (split + 1) * rpb);
         const int m = d / 16, m4 = m & ~3, Sg = chain_stride_of(d);
         for (int r = split * rpb + grp; r < r1; r += RT_GROUPS) {
-            const float* wr = a.router_cm + (size_t)r * 16 * Sg + j * Sg;
+            // F16 / BF16 router rows: vec_dot_{f16,bf16}_f32's order (src/quant.cpp:3015-3055), one chain
+            // per lane jc < 8 over elements 8 i + jc, i.e. chain-major columns jc and jc + 8 interleaved
+            // step by step (lanes 8-15 repeat lanes 0-7); the shared gate row stays fp32
+            const bool c8 = a.chain8 && r < E;
+            const int jc = c8 ? (j & 7) : j;
+            const float* wr = a.router_cm + (size_t)r * 16 * Sg + jc * Sg;
             // token rows of the chains: tokens past nt (last block) repeat the last one, results dropped,
             // so the loop has no branches and the router loads can run ahead
             const float* xr[T];
 #pragma unroll
-            for (int t = 0; t < T; ++t) xr[t] = xs + min(t, nt - 1) * RS + j * S;
+            for (int t = 0; t < T; ++t) xr[t] = xs + min(t, nt - 1) * RS + jc * S;
             float acc[T];
 #pragma unroll
             for (int t = 0; t < T; ++t) acc[t] = 0.0f;
-#pragma unroll RT_UNROLL
-            for (int i = 0; i < m4; i += 4) {
-                const float4 w4 = *reinterpret_cast<const float4*>(wr + i);
+            if (c8) {
+                const float* wr8 = wr + 8 * Sg;
+                for (int i = 0; i < m4; i += 4) {
+                    const float4 w4 = *reinterpret_cast<const float4*>(wr + i);
+                    const float4 w8 = *reinterpret_cast<const float4*>(wr8 + i);
 #pragma unroll
-                for (int t = 0; t < T; ++t) {
-                    const float4 x4 = *reinterpret_cast<const float4*>(xr[t] + i);
-                    acc[t] = __builtin_fmaf(w4.x, x4.x, acc[t]);
-                    acc[t] = __builtin_fmaf(w4.y, x4.y, acc[t]);
-                    acc[t] = __builtin_fmaf(w4.z, x4.z, acc[t]);
-                    acc[t] = __builtin_fmaf(w4.w, x4.w, acc[t]);
+                    for (int t = 0; t < T; ++t) {
+                        const float4 x4 = *reinterpret_cast<const float4*>(xr[t] + i);
+                        const float4 x8 = *reinterpret_cast<const float4*>(xr[t] + 8 * S + i);
+                        acc[t] = __builtin_fmaf(w4.x, x4.x, acc[t]);
+                        acc[t] = __builtin_fmaf(w8.x, x8.x, acc[t]);
+                        acc[t] = __builtin_fmaf(w4.y, x4.y, acc[t]);
+                        acc[t] = __builtin_fmaf(w8.y, x8.y, acc[t]);
+                        acc[t] = __builtin_fmaf(w4.z, x4.z, acc[t]);
+                        acc[t] = __builtin_fmaf(w8.z, x8.z, acc[t]);
+                        acc[t] = __builtin_fmaf(w4.w, x4.w, acc[t]);
+                        acc[t] = __builtin_fmaf(w8.w, x8.w, acc[t]);
+                    }
                 }
-            }
-            for (int i = m4; i < m; ++i) {
-                const float wv = wr[i];
+                for (int i = m4; i < m; ++i) {
 #pragma unroll
-                for (int t = 0; t < T; ++t) acc[t] = __builtin_fmaf(wv, xr[t][i], acc[t]);
+                    for (int t = 0; t < T; ++t) {
+                        acc[t] = __builtin_fmaf(wr[i], xr[t][i], acc[t]);
+                        acc[t] = __builtin_fmaf(wr8[i], xr[t][8 * S + i], acc[t]);
+                    }
+                }
+            } else {
+#pragma unroll RT_UNROLL
+                for (int i = 0; i < m4; i += 4) {
+                    const float4 w4 = *reinterpret_cast<const float4*>(wr + i);
+#pragma unroll
+                    for (int t = 0; t < T; ++t) {
+                        const float4 x4 = *reinterpret_cast<const float4*>(xr[t] + i);
+                        acc[t] = __builtin_fmaf(w4.x, x4.x, acc[t]);
+                        acc[t] = __builtin_fmaf(w4.y, x4.y, acc[t]);
+                        acc[t] = __builtin_fmaf(w4.z, x4.z, acc[t]);
+                        acc[t] = __builtin_fmaf(w4.w, x4.w, acc[t]);
+                    }
+                }
+                for (int i = m4; i < m; ++i) {
+                    const float wv = wr[i];
+#pragma unroll
+                    for (int t = 0; t < T; ++t) acc[t] = __builtin_fmaf(wv, xr[t][i], acc[t]);
+                }
             }
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 if (t < nt) {
-                    const float hi = __shfl_down(acc[t], 8, 16);
-                    const float v = acc[t] + hi;  // acc0[j] + acc1[j] for j < 8
-                    float s = 0.0f;
-#pragma unroll
-                    for (int q = 0; q < 8; ++q) s += __shfl(v, q, 16);
+                    const float s = chain_sum(acc[t], c8);
                     if (j == 0) {
                         const size_t tok = (size_t)(t0 + t);
                         if (r < E) {
@@ -545,7 +586,9 @@ static bool route_rows_fits(const RouteArgs& a) {
 #ifndef JX_RR_MIN_N
 #define JX_RR_MIN_N 512
 #endif
-    return R > RT_GROUPS && a.d % 64 == 0 && (m4 == 8 || m4 == 16 || m4 == 24 || m4 == 32) && a.n >= JX_RR_MIN_N;
+    // (F16 / BF16 routers: two chain columns per lane would not fit the register-resident rows)
+    return R > RT_GROUPS && a.d % 64 == 0 && (m4 == 8 || m4 == 16 || m4 == 24 || m4 == 32) && a.n >= JX_RR_MIN_N &&
+           !a.chain8;
 }
 
 void launch_route(const RouteArgs& a, hipStream_t st) {
@@ -726,25 +769,45 @@ k_route_small(RouteArgs a) {
         // tails)
         const int t = lane >> 4, j = lane & 15;
         if (t < n) {
-            const float* wr = lds + j * S;
-            const float* xr = lds + (1 + t) * RS + j * S;
+            // F16 / BF16 router rows: columns jc and jc + 8 interleaved (as k_route); the shared gate fp32
+            const bool c8 = a.chain8 && r < E;
+            const int jc = c8 ? (j & 7) : j;
+            const float* wr = lds + jc * S;
+            const float* xr = lds + (1 + t) * RS + jc * S;
             const int m = d / 16, m4 = m & ~3;
             float acc = 0.0f;
+            if (c8) {
+                for (int i = 0; i < m4; i += 4) {
+                    const float4 p = *reinterpret_cast<const float4*>(wr + i);
+                    const float4 p8 = *reinterpret_cast<const float4*>(wr + 8 * S + i);
+                    const float4 q = *reinterpret_cast<const float4*>(xr + i);
+                    const float4 q8 = *reinterpret_cast<const float4*>(xr + 8 * S + i);
+                    acc = __builtin_fmaf(p.x, q.x, acc);
+                    acc = __builtin_fmaf(p8.x, q8.x, acc);
+                    acc = __builtin_fmaf(p.y, q.y, acc);
+                    acc = __builtin_fmaf(p8.y, q8.y, acc);
+                    acc = __builtin_fmaf(p.z, q.z, acc);
+                    acc = __builtin_fmaf(p8.z, q8.z, acc);
+                    acc = __builtin_fmaf(p.w, q.w, acc);
+                    acc = __builtin_fmaf(p8.w, q8.w, acc);
+                }
+                for (int i = m4; i < m; ++i) {
+                    acc = __builtin_fmaf(wr[i], xr[i], acc);
+                    acc = __builtin_fmaf(wr[8 * S + i], xr[8 * S + i], acc);
+                }
+            } else {
 #pragma unroll 8
-            for (int i = 0; i < m4; i += 4) {
-                const float4 p = *reinterpret_cast<const float4*>(wr + i);
-                const float4 q = *reinterpret_cast<const float4*>(xr + i);
-                acc = __builtin_fmaf(p.x, q.x, acc);
-                acc = __builtin_fmaf(p.y, q.y, acc);
-                acc = __builtin_fmaf(p.z, q.z, acc);
-                acc = __builtin_fmaf(p.w, q.w, acc);
+                for (int i = 0; i < m4; i += 4) {
+                    const float4 p = *reinterpret_cast<const float4*>(wr + i);
+                    const float4 q = *reinterpret_cast<const float4*>(xr + i);
+                    acc = __builtin_fmaf(p.x, q.x, acc);
+                    acc = __builtin_fmaf(p.y, q.y, acc);
+                    acc = __builtin_fmaf(p.z, q.z, acc);
+                    acc = __builtin_fmaf(p.w, q.w, acc);
+                }
+                for (int i = m4; i < m; ++i) acc = __builtin_fmaf(wr[i], xr[i], acc);
             }
-            for (int i = m4; i < m; ++i) acc = __builtin_fmaf(wr[i], xr[i], acc);
-            const float hi = __shfl_down(acc, 8, 16);
-            const float v = acc + hi;
-            float s = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 8; ++q) s += __shfl(v, q, 16);
+            const float s = chain_sum(acc, c8);
             if (j == 0) {
                 if (r < E) a.logits[(size_t)t * E + r] = a.bias ? s + a.bias[r] : s;
                 else a.shscale[t] = s;  // raw shared-gate logit; the top-k step applies the sigmoid
@@ -830,14 +893,18 @@ __global__ void __launch_bounds__(R1_THREADS) k_route_one(RouteArgs a, DispatchO
         const int t = c / rows, r = c % rows, j = tid & 15;
         const float* w = lds + (size_t)r * d;
         const float* xt = xs + (size_t)t * d;
+        // F16 / BF16 router rows: 8 chains over 8-element steps (lanes 8-15 repeat lanes 0-7)
+        const bool c8 = a.chain8 && r < E;
         float acc = 0.0f;
+        if (c8) {
+            const int jc = j & 7;
 #pragma unroll 32
-        for (int i = 0; i < d; i += 16) acc = __builtin_fmaf(w[i + j], xt[i + j], acc);
-        const float hi = __shfl_down(acc, 8, 16);
-        const float v = acc + hi;
-        float s = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) s += __shfl(v, q, 16);
+            for (int i = 0; i < d; i += 8) acc = __builtin_fmaf(w[i + jc], xt[i + jc], acc);
+        } else {
+#pragma unroll 32
+            for (int i = 0; i < d; i += 16) acc = __builtin_fmaf(w[i + j], xt[i + j], acc);
+        }
+        const float s = chain_sum(acc, c8);
         if (j == 0) {
             if (r < E) {
                 const float l = a.bias ? s + a.bias[r] : s;

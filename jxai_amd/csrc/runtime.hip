@@ -50,6 +50,39 @@ int fail(int code, const std::string& msg) {
                         std::string(#expr) + ": " + hipGetErrorString(e_));                       \
     } while (0)
 
+// IEEE half / bfloat16 bits -> float, exact for every input (the reference's fp16_to_fp32 and
+// bf16_to_fp32, src/quant.cpp:876-932; F16C's conversion keeps NaN payloads, as this does).
+float half_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu, bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {  // subnormal: normalise
+            int k = 0;
+            while (!(m & 0x400u)) {
+                m <<= 1;
+                ++k;
+            }
+            bits = sign | ((uint32_t)(113 - k) << 23) | ((m & 0x3FFu) << 13);
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7F800000u | (m << 13);
+    } else {
+        bits = sign | ((e + 112) << 23) | (m << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+float bf16_to_float(uint16_t b) {
+    const uint32_t bits = (uint32_t)b << 16;
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
 bool expert_type_ok(int t) {
     return t == jx::T_Q4_0 || t == jx::T_Q5_0 || t == jx::T_Q8_0 || t == jx::T_Q4_K || t == jx::T_Q5_K ||
            t == jx::T_Q6_K;
@@ -262,6 +295,7 @@ struct jx_moe_layer {
     uint64_t graph_clock = 0;
     bool use_graphs = true;
     bool fold_combine = true;  // JX_NO_FOLD=1 keeps the separate combine launch (A/B measurement)
+    bool chain8 = false;       // F16 / BF16 router: the 8-lane dot order
 };
 
 struct jx_qmatrix {
@@ -466,6 +500,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     jx::RouteArgs ra{xdev, n, d, E, k, L->router, L->bias, L->shgate, L->xq,
                      (mfma_gu || smfma_gu) ? L->xh.a : jx::ActH{}, L->ids, L->probs, L->shscale, L->logits,
                      L->router_cm};
+    ra.chain8 = L->chain8 ? 1 : 0;
     const jx::DispatchOut dout{L->counts, L->offs,   L->act,   L->n_act, L->pair_tok,
                                L->pos_of,  L->tiles, L->n_tiles, L->slots};
     // few-token decode: logits on one block per router row, grouping in the GEMVs
@@ -696,8 +731,8 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
         return fail(JX_ERR_UNSUPPORTED, "d_model must be a multiple of 32, at most 8192");
     if (D->d_ff < 32 || D->d_ff % 32 != 0) return fail(JX_ERR_UNSUPPORTED, "d_ff must be a multiple of 32");
     if (!D->router || !D->gate_exps || !D->up_exps || !D->down_exps) return fail(JX_ERR_INVALID, "missing tensor");
-    if (D->router_type != JX_TYPE_F32)
-        return fail(JX_ERR_UNSUPPORTED, "router must be F32 (the F16/BF16 dot order of matmul_quant_f32 is not reproduced)");
+    if (D->router_type != JX_TYPE_F32 && D->router_type != JX_TYPE_F16 && D->router_type != JX_TYPE_BF16)
+        return fail(JX_ERR_UNSUPPORTED, "router must be F32, F16 or BF16");
     if (D->activation != JX_ACT_SILU && D->activation != JX_ACT_GELU_TANH)
         return fail(JX_ERR_INVALID, "activation must be JX_ACT_SILU or JX_ACT_GELU_TANH");
     if (D->gate_type != D->up_type) return fail(JX_ERR_UNSUPPORTED, "gate and up must share a type");
@@ -744,8 +779,19 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
     };
     if (hipSetDevice(L->device) != hipSuccess) return bail(fail(JX_ERR_HIP, "hipSetDevice"));
     const size_t E = L->E, d = L->d;
+    // F16 / BF16 routers widen to fp32 exactly (fp16_to_fp32 / bf16_to_fp32, src/quant.cpp:876-932); the
+    // router kernels then take their products in the F16 / BF16 dot order (RouteArgs::chain8)
+    std::vector<float> router_f32(E * d);
+    L->chain8 = D->router_type != JX_TYPE_F32;
+    if (D->router_type == JX_TYPE_F32) {
+        std::copy(static_cast<const float*>(D->router), static_cast<const float*>(D->router) + E * d, router_f32.begin());
+    } else {
+        const uint16_t* h = static_cast<const uint16_t*>(D->router);
+        for (size_t i = 0; i < E * d; ++i)
+            router_f32[i] = D->router_type == JX_TYPE_F16 ? half_to_float(h[i]) : bf16_to_float(h[i]);
+    }
     if ((r = dalloc(L->router, E * d)) != JX_OK) return bail(r);
-    if (hipMemcpy(L->router, D->router, E * d * 4, hipMemcpyHostToDevice) != hipSuccess)
+    if (hipMemcpy(L->router, router_f32.data(), E * d * 4, hipMemcpyHostToDevice) != hipSuccess)
         return bail(fail(JX_ERR_HIP, "router upload"));
     if (D->router_bias) {
         if ((r = dalloc(L->bias, E)) != JX_OK) return bail(r);
@@ -781,7 +827,7 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
     {  // chain-major router copy for the many-token router
         const int R = L->E + (L->shgate ? 1 : 0);
         std::vector<float> rows((size_t)R * d), cm((size_t)R * 16 * jx::chain_stride((int)d));
-        std::copy(D->router, D->router + E * d, rows.begin());
+        std::copy(router_f32.begin(), router_f32.end(), rows.begin());
         if (L->shgate) std::copy(D->sh_gate_inp, D->sh_gate_inp + d, rows.begin() + E * d);
         jx::chain_rows(rows.data(), R, (int)d, cm.data());
         if ((r = dalloc(L->router_cm, cm.size())) != JX_OK) return bail(r);

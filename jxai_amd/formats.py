@@ -17,16 +17,18 @@ Q8_0 = 8
 Q4_K = 12
 Q5_K = 13
 Q6_K = 14
+BF16 = 30
 
 NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K",
-         Q6_K: "Q6_K"}
+         Q6_K: "Q6_K", BF16: "BF16"}
 BY_NAME = {v: k for k, v in NAMES.items()}
 
 # elements per block, bytes per block (include/common.h:154-189)
 BLOCK = {F32: (1, 4), F16: (1, 2), Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144),
-         Q5_K: (256, 176), Q6_K: (256, 210)}
+         Q5_K: (256, 176), Q6_K: (256, 210), BF16: (1, 2)}
 
 EXPERT_TYPES = (Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)
+ROUTER_TYPES = (F32, F16, BF16)  # the router GEMV goes through matmul_quant_f32 (transformer.cpp:2591)
 K_QUANTS = (Q4_K, Q5_K, Q6_K)
 
 

@@ -78,8 +78,8 @@ class MoELayer:
                           ffn_norm, post_ffw_norm)]
         (router, router_bias, gate_exps, up_exps, down_exps, sh_gate, sh_up, sh_down, sh_gate_inp, ffn_norm,
          post_ffw_norm) = keep
-        if router_type == F.F32:
-            assert router.dtype == np.float32 and router.size == n_experts * d_model
+        if router.size != n_experts * d_model or router.dtype != (np.float32 if router_type == F.F32 else np.uint16):
+            raise JxError("router must hold E x d_model fp32 values (F32) or half / bfloat16 bits (F16 / BF16)")
         for name, a, t, rows, cols in (("gate", gate_exps, gate_type, d_ff, d_model),
                                        ("up", up_exps, up_type, d_ff, d_model),
                                        ("down", down_exps, down_type, d_model, d_ff)):
@@ -119,7 +119,7 @@ class MoELayer:
                    gate_type=gt, up_type=ut, down_type=dt, router=lw.router, router_bias=lw.router_bias,
                    gate_exps=lw.gate, up_exps=lw.up, down_exps=lw.down, activation=cfg.act,
                    ffn_norm=lw.ffn_norm, post_ffw_norm=lw.post_ffw_norm, rms_norm_eps=cfg.rms_eps,
-                   device=device, **kw)
+                   router_type=cfg.router_type, device=device, **kw)
 
     def forward(self, x: np.ndarray, regime: str | None = None, residual: bool = False):
         """MoE block over host activations [n][d] -> (out [n][d], topk_ids, topk_w, counts).

@@ -164,6 +164,7 @@ class LayerConfig:
     zipf_gamma: float = 0.0
     act: int = 0  # gated activation: 0 SiLU, 1 GELU-tanh (the reference's use_gelu)
     norms: bool = False  # ffn_norm and post_ffw_norm weights for the residual-stream form
+    router_type: int = F.F32  # F16 / BF16: the router rows stored as half / bfloat16 bits
     rms_eps: float = 1e-5
     decode_tokens: tuple = field(default_factory=tuple)
     describe: str = ""
@@ -217,6 +218,14 @@ CONFIGS = {
                            describe="Toy MoE FFN d512 E8 top-2 F1024 Q6_K"),
     "toy_q50": LayerConfig("toy_q50", 512, 8, 2, 1024, F.Q5_0, decode_tokens=(1, 2, 64, 512),
                            describe="Toy MoE FFN d512 E8 top-2 F1024 Q5_0 (fp32 activations throughout)"),
+    # routers stored as F16 / BF16 (the reference's matmul_quant_f32 takes any router type): the toy
+    # layer, and a 24-expert layer (split routers) with a sigmoid-gated shared expert whose fp32 gate
+    # keeps vec_dot_f32's order beside the BF16 router rows
+    "toy_f16r": LayerConfig("toy_f16r", 512, 8, 2, 1024, F.Q4_0, router_type=F.F16, decode_tokens=(1, 64),
+                            describe="Toy MoE FFN d512 E8 top-2 F1024 Q4_0, F16 router"),
+    "toy_bf16r_sh": LayerConfig("toy_bf16r_sh", 512, 24, 4, 512, F.Q4_K, d_ff_shared=512, shared_gate=True,
+                                router_type=F.BF16, decode_tokens=(1, 64),
+                                describe="d512 E24 top-4 F512 Q4_K + shared 512 (sigmoid gate), BF16 router"),
 }
 
 
@@ -229,10 +238,21 @@ def zipf_bias(cfg: LayerConfig, seed: int = BASE_SEED) -> np.ndarray:
     return np.array([-1.1 * cfg.zipf_gamma * math.log(float(r)) for r in rank], dtype=np.float32)
 
 
+def to_f16_bits(v: np.ndarray) -> np.ndarray:
+    """fp32 -> IEEE half bits, round to nearest even (numpy's conversion)."""
+    return np.ascontiguousarray(v, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def to_bf16_bits(v: np.ndarray) -> np.ndarray:
+    """fp32 -> bfloat16 bits, round to nearest even (fp32_to_bf16, src/quant.cpp:934-939; finite inputs)."""
+    b = np.ascontiguousarray(v, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+
 @dataclass
 class LayerWeights:
     cfg: LayerConfig
-    router: np.ndarray              # fp32 [E][d]
+    router: np.ndarray              # [E][d]: fp32, or uint16 half / bfloat16 bits (cfg.router_type)
     router_bias: np.ndarray | None  # fp32 [E]
     gate: np.ndarray                # bytes, [E][F] rows of d
     up: np.ndarray
@@ -259,6 +279,10 @@ def make_layer(cfg: LayerConfig, seed: int = BASE_SEED) -> LayerWeights:
     d, E, Fd = cfg.d_model, cfg.n_experts, cfg.d_ff
     s = lambda name: sub_seed(cfg.name, name, seed)  # noqa: E731
     router = normal_f32(s("router"), E * d, 0.02).reshape(E, d)
+    if cfg.router_type == F.F16:
+        router = to_f16_bits(router)
+    elif cfg.router_type == F.BF16:
+        router = to_bf16_bits(router)
     bias = zipf_bias(cfg, seed) if cfg.zipf_gamma > 0 else None
     gate = quant_matrix(s("gate_exps"), cfg.wtype, E * Fd, d)
     up = quant_matrix(s("up_exps"), cfg.wtype, E * Fd, d)

@@ -80,6 +80,8 @@ static inline float ld_f16(const uint8_t* p) {
 int64_t jxo_row_bytes(int32_t type, int64_t cols) {
     switch (type) {
         case JXO_F32: return cols * 4;
+        case JXO_F16:
+        case JXO_BF16: return cols * 2;
         case JXO_Q4_0: return ((cols + 31) / 32) * 18;
         case JXO_Q8_0: return ((cols + 31) / 32) * 34;
         case JXO_Q4_K: return ((cols + 255) / 256) * 144;
@@ -441,9 +443,43 @@ static float dot_q6_K_f32(const uint8_t* x, const float* y, int64_t k) {
     return total;
 }
 
+/* vec_dot_f16_f32 / vec_dot_bf16_f32 (src/quant.cpp:3015-3055), AVX2 order: one 8-lane accumulator
+ * over 8-element steps, acc_j = fma(w[i + j], y[i + j], acc_j) with the weight widened exactly
+ * (fp16_to_fp32 / bf16_to_fp32, src/quant.cpp:876-932), the 8 lanes summed in order from zero, then
+ * the scalar tail contracted like vec_dot_f32's. */
+static float h16_to_f32(int32_t type, uint16_t h) {
+    if (type == JXO_F16) return jxo_fp16_to_fp32(h);
+    const uint32_t bits = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+float jxo_vec_dot_h16_f32(int32_t type, const uint16_t* w, const float* y, int64_t k) {
+    float acc[8] = {0};
+    int64_t i = 0;
+    for (; i + 8 <= k; i += 8)
+        for (int j = 0; j < 8; ++j) acc[j] = fmaf(h16_to_f32(type, w[i + j]), y[i + j], acc[j]);
+    float total = 0.0f;
+    for (int j = 0; j < 8; ++j) total += acc[j];
+    for (; i < k; ++i) total = fmaf(h16_to_f32(type, w[i]), y[i], total);
+    return total;
+}
+
+/* One router row's logit (matmul_quant_f32(lw.router_gate->type, ...), transformer.cpp:2591: with
+ * E < 8 rows or a non-Q8 type, vec_dot_quant_f32 of the row). */
+static float router_dot(const jxo_moe_desc* L, int32_t e, const float* x) {
+    const int64_t d = L->d_model;
+    if (L->router_type == JXO_F16 || L->router_type == JXO_BF16)
+        return jxo_vec_dot_h16_f32(L->router_type, (const uint16_t*)L->router + e * d, x, d);
+    return jxo_vec_dot_f32((const float*)L->router + e * d, x, d);
+}
+
 float jxo_vec_dot_quant_f32(int32_t type, const uint8_t* w, const float* y, int64_t k) {
     switch (type) {
         case JXO_F32: return jxo_vec_dot_f32((const float*)(const void*)w, y, k);
+        case JXO_F16:
+        case JXO_BF16: return jxo_vec_dot_h16_f32(type, (const uint16_t*)(const void*)w, y, k);
         case JXO_Q4_0: return dot_q4_0_f32(w, y, k);
         case JXO_Q8_0: return dot_q8_0_f32(w, y, k);
         case JXO_Q4_K: return jxo_vec_dot_q4_K_f32(w, y, k);
@@ -837,15 +873,15 @@ int32_t jxo_select_experts(const float* logits, int32_t E, int32_t k, int32_t* i
     return ties;
 }
 
-/* Router GEMV (transformer.cpp:2589-2594 -> matmul_quant_f32(F32) ->
- * vec_dot_f32), optional per-expert bias added after the GEMV, then top-k. */
+/* Router GEMV (transformer.cpp:2589-2594 -> matmul_quant_f32(router type) -> vec_dot_f32 or the
+ * F16 / BF16 dots), optional per-expert bias added after the GEMV, then top-k. */
 void jxo_route(const jxo_moe_desc* L, const float* x, int32_t n_tok,
                float* logits, int32_t* topk_ids, float* topk_w) {
     const int32_t E = L->n_experts, d = L->d_model, k = L->top_k;
     for (int32_t t = 0; t < n_tok; ++t) {
         float* lg = logits + (int64_t)t * E;
         for (int32_t e = 0; e < E; ++e) {
-            lg[e] = jxo_vec_dot_f32(L->router + (int64_t)e * d, x + (int64_t)t * d, d);
+            lg[e] = router_dot(L, e, x + (int64_t)t * d);
             if (L->router_bias) lg[e] = lg[e] + L->router_bias[e];
         }
         jxo_select_experts(lg, E, k, topk_ids + (int64_t)t * k, topk_w + (int64_t)t * k);
@@ -871,7 +907,7 @@ static void moe_token(const jxo_moe_desc* L, const float* x, float* out, int32_t
                       float* logits, int32_t order, float* h, float* y) {
     const int32_t E = L->n_experts, d = L->d_model, Fd = L->d_ff, k = L->top_k;
     for (int32_t e = 0; e < E; ++e) {
-        logits[e] = jxo_vec_dot_f32(L->router + (int64_t)e * d, x, d);
+        logits[e] = router_dot(L, e, x);
         if (L->router_bias) logits[e] = logits[e] + L->router_bias[e];
     }
     jxo_select_experts(logits, E, k, ids, probs);

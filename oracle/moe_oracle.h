@@ -21,13 +21,14 @@
 extern "C" {
 #endif
 
-enum { JXO_F32 = 0, JXO_Q4_0 = 2, JXO_Q5_0 = 6, JXO_Q8_0 = 8, JXO_Q4_K = 12, JXO_Q5_K = 13, JXO_Q6_K = 14 };
+enum { JXO_F32 = 0, JXO_F16 = 1, JXO_Q4_0 = 2, JXO_Q5_0 = 6, JXO_Q8_0 = 8, JXO_Q4_K = 12, JXO_Q5_K = 13,
+       JXO_Q6_K = 14, JXO_BF16 = 30 };
 enum { JXO_ORDER_AVX2 = 0, JXO_ORDER_AVX512 = 1 };
 
 typedef struct {
     int32_t n_experts, top_k, d_model, d_ff;
     int32_t gate_type, up_type, down_type;
-    const float* router;       /* [E][d] fp32                               */
+    const void* router;        /* [E][d] of router_type (F32, F16 or BF16)   */
     const float* router_bias;  /* [E] fp32 added after the GEMV, or NULL     */
     const uint8_t* gate;       /* [E][d_ff] rows of d_model, block layout     */
     const uint8_t* up;
@@ -43,6 +44,7 @@ typedef struct {
     const float* post_ffw_norm;/* [d] fp32 or NULL (none)                    */
     float rms_eps;
     int32_t residual;          /* x is the residual stream: out = x + post(block(rms_norm(x))) */
+    int32_t router_type;       /* JXO_F32, JXO_F16 or JXO_BF16                */
 } jxo_moe_desc;
 
 uint16_t jxo_fp32_to_fp16(float f);
@@ -54,7 +56,9 @@ float jxo_vec_dot_f32(const float* a, const float* b, int64_t k);
 void jxo_rms_norm(float* out, const float* x, const float* weight, int64_t size, float eps);
 float jxo_vec_dot_q8(int32_t type, const uint8_t* w, const uint8_t* xq8, int64_t k, int32_t order);
 float jxo_vec_dot_q4_K_f32(const uint8_t* w, const float* y, int64_t k);
-/* vec_dot_quant_f32 (src/quant.cpp:3269-3305) for F32, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K. */
+/* vec_dot_f16_f32 / vec_dot_bf16_f32 (src/quant.cpp:3015-3055): w holds half / bfloat16 bits. */
+float jxo_vec_dot_h16_f32(int32_t type, const uint16_t* w, const float* y, int64_t k);
+/* vec_dot_quant_f32 (src/quant.cpp:3269-3305) for F32, F16, BF16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K. */
 float jxo_vec_dot_quant_f32(int32_t type, const uint8_t* w, const float* y, int64_t k);
 void jxo_matmul_quant_f32(int32_t type, const uint8_t* W, const float* x, float* out,
                           int64_t rows, int64_t cols, int32_t order);

@@ -27,7 +27,7 @@ class MoeDesc(C.Structure):
     _fields_ = [
         ("n_experts", C.c_int32), ("top_k", C.c_int32), ("d_model", C.c_int32), ("d_ff", C.c_int32),
         ("gate_type", C.c_int32), ("up_type", C.c_int32), ("down_type", C.c_int32),
-        ("router", _fp), ("router_bias", _fp),
+        ("router", C.c_void_p), ("router_bias", _fp),
         ("gate", _u8), ("up", _u8), ("down", _u8),
         ("d_ff_shared", C.c_int32),
         ("sh_gate_type", C.c_int32), ("sh_up_type", C.c_int32), ("sh_down_type", C.c_int32),
@@ -35,6 +35,7 @@ class MoeDesc(C.Structure):
         ("sh_gate_inp", _fp),
         ("activation", C.c_int32),
         ("ffn_norm", _fp), ("post_ffw_norm", _fp), ("rms_eps", C.c_float), ("residual", C.c_int32),
+        ("router_type", C.c_int32),
     ]
 
 
@@ -211,12 +212,12 @@ class Oracle:
         gt, ut, dt = lw.types
         sgt, sut, sdt = lw.sh_types
         D = MoeDesc(cfg.n_experts, cfg.top_k, cfg.d_model, cfg.d_ff, gt, ut, dt,
-                    P(lw.router, _fp), P(lw.router_bias, _fp),
+                    P(lw.router, C.c_void_p), P(lw.router_bias, _fp),
                     P(lw.gate, _u8), P(lw.up, _u8), P(lw.down, _u8),
                     cfg.d_ff_shared, sgt, sut, sdt,
                     P(lw.sh_gate, _u8), P(lw.sh_up, _u8), P(lw.sh_down, _u8),
                     P(lw.sh_gate_inp, _fp), cfg.act, P(lw.ffn_norm, _fp), P(lw.post_ffw_norm, _fp),
-                    cfg.rms_eps, 0)
+                    cfg.rms_eps, 0, cfg.router_type)
         return D, keep
 
     def rms_norm(self, x, w, eps: float) -> np.ndarray:

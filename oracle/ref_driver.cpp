@@ -188,7 +188,7 @@ int32_t jxr_moe_forward(const jxo_moe_desc* L, const float* x, int32_t n_tok,
         const float* xn = L->residual ? xnorm.data() : xt;
 
         std::fill(logits.begin(), logits.end(), 0.0f);
-        moe::matmul_quant_f32(GGMLType::F32, L->router, xn, logits.data(), E, d);
+        moe::matmul_quant_f32(static_cast<GGMLType>(L->router_type), L->router, xn, logits.data(), E, d);
         if (L->router_bias)
             for (uint32_t e = 0; e < E; ++e) logits[e] = logits[e] + L->router_bias[e];
         auto selected = tier.select_experts_cache_aware(0, logits.data(), E, k);

@@ -64,6 +64,14 @@ RESID_CASES = [
     ("toy_norm", 64, ("tiles", 32, 0)),
 ]
 
+# F16 / BF16 routers (the router GEMV through matmul_quant_f32 of the router's own type)
+ROUTER16_CASES = [
+    ("toy_f16r", 1, [0]),
+    ("toy_f16r", 64, list(range(64))),
+    ("toy_bf16r_sh", 1, [0]),
+    ("toy_bf16r_sh", 64, list(range(64))),
+]
+
 
 def covering_rows(ids: np.ndarray, n_experts: int, g_routed: int, g_shared: int) -> list[int]:
     """Tokens whose output rows together touch every tile of the grouped kernels.
@@ -122,7 +130,7 @@ def make_case(ref: Oracle, name: str, n: int, rows, tag: str = "", residual: boo
     w_all = np.zeros((n, cfg.top_k), np.float32)
     lg_all = np.zeros((n, cfg.n_experts), np.float32)
     for t in range(n):
-        logits = ref.matmul_quant_f32(F.F32, lw.router.view(np.uint8).reshape(-1), xr[t],
+        logits = ref.matmul_quant_f32(cfg.router_type, lw.router.view(np.uint8).reshape(-1), xr[t],
                                       cfg.n_experts, cfg.d_model)
         if lw.router_bias is not None:
             logits = (logits + lw.router_bias).astype(np.float32)
@@ -226,6 +234,28 @@ def make_units_f3(ref: Oracle) -> str:
     return path
 
 
+def make_units_router16(ref: Oracle) -> str:
+    """vec_dot_f16_f32 / vec_dot_bf16_f32 (src/quant.cpp:3015-3055) through vec_dot_quant_f32, with and
+    without a scalar tail (k % 8 != 0), and matmul_quant_f32 over an E x d router of each type."""
+    kw = {}
+    for t in (F.F16, F.BF16):
+        for k in (37, 512, 4101):
+            v = synth.normal_f32(synth.sub_seed("units_r16", f"w{t}_{k}"), k, 0.05)
+            w = synth.to_f16_bits(v) if t == F.F16 else synth.to_bf16_bits(v)
+            y = synth.normal_f32(synth.sub_seed("units_r16", f"y{t}_{k}"), k, 1.0)
+            kw[f"dot_w_{t}_{k}"], kw[f"dot_y_{t}_{k}"] = w, y
+            kw[f"dot_o_{t}_{k}"] = np.float32(ref.vec_dot_quant_f32(t, w.view(np.uint8), y))
+        E, d = 24, 2048
+        v = synth.normal_f32(synth.sub_seed("units_r16", f"router{t}"), E * d, 0.02)
+        w = synth.to_f16_bits(v) if t == F.F16 else synth.to_bf16_bits(v)
+        x = synth.normal_f32(synth.sub_seed("units_r16", f"x{t}"), d, 1.0)
+        kw[f"mm_w_{t}"], kw[f"mm_x_{t}"] = w, x
+        kw[f"mm_o_{t}"] = ref.matmul_quant_f32(t, w.view(np.uint8), x, E, d)
+    path = os.path.join(OUT, "units_router16.npz")
+    np.savez_compressed(path, **kw)
+    return path
+
+
 TOY_GGUF = "/root/reference/models/qwen_run.gguf"
 
 
@@ -275,6 +305,12 @@ def main() -> None:
         for name, n, rows in F3_CASES:
             print(make_case(ref, name, n, rows))
         return
+    if "--router16" in sys.argv:  # only the F16 / BF16 router fixtures
+        ref = Oracle("reference", avx512=False)
+        print(make_units_router16(ref))
+        for name, n, rows in ROUTER16_CASES:
+            print(make_case(ref, name, n, rows))
+        return
     if "--resid" in sys.argv:  # only the residual-stream cases
         ref = Oracle("reference", avx512=False)
         for name, n, rows in RESID_CASES:
@@ -294,6 +330,9 @@ def main() -> None:
         print(make_case(ref, name, n, rows, tag="_resid", residual=True))
     print(make_units_f3(ref))
     for name, n, rows in F3_CASES:
+        print(make_case(ref, name, n, rows))
+    print(make_units_router16(ref))
+    for name, n, rows in ROUTER16_CASES:
         print(make_case(ref, name, n, rows))
     subprocess.run([sys.executable, os.path.abspath(__file__), "--avx512-child"], check=True)
 

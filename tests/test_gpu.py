@@ -474,12 +474,17 @@ def test_batch_limit_refused(moe):
 
 
 def test_layer_desc_refusals(moe):
-    """Router types other than F32 and unknown activations are refused with a message."""
+    """Router types other than F32 / F16 / BF16, router arrays that do not match their type, and unknown
+    activations are refused with a message."""
     cfg, lw = layer("toy")
     from jxai_amd._lib import JxError
-    with pytest.raises(JxError, match="router must be F32"):
+    with pytest.raises(JxError, match="router must be F32, F16 or BF16"):
         moe.MoELayer(n_experts=8, top_k=2, d_model=512, d_ff=1024, gate_type=F.Q4_0, up_type=F.Q4_0,
-                     down_type=F.Q4_0, router=lw.router.astype(np.float16), gate_exps=lw.gate, up_exps=lw.up,
+                     down_type=F.Q4_0, router=synth.to_f16_bits(lw.router), gate_exps=lw.gate, up_exps=lw.up,
+                     down_exps=lw.down, router_type=F.Q8_0)
+    with pytest.raises(JxError, match="half / bfloat16 bits"):
+        moe.MoELayer(n_experts=8, top_k=2, d_model=512, d_ff=1024, gate_type=F.Q4_0, up_type=F.Q4_0,
+                     down_type=F.Q4_0, router=lw.router, gate_exps=lw.gate, up_exps=lw.up,
                      down_exps=lw.down, router_type=F.F16)
     with pytest.raises(JxError, match="activation"):
         moe.MoELayer(n_experts=8, top_k=2, d_model=512, d_ff=1024, gate_type=F.Q4_0, up_type=F.Q4_0,

@@ -269,6 +269,55 @@ def test_f3_dots_golden_and_float64(port, key):
         assert np.array_equal(got.view(np.uint32), q8.view(np.uint32))
 
 
+def _h16_values(t, w):
+    """Half / bfloat16 bits -> exact float64 values."""
+    if t == F.F16:
+        return w.view(np.float16).astype(np.float64)
+    return (w.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+@pytest.mark.parametrize("t", [F.F16, F.BF16])
+def test_router16_dots_golden_and_float64(port, t):
+    """vec_dot_f16_f32 / vec_dot_bf16_f32 (src/quant.cpp:3015-3055): the reference build's values bit for
+    bit (with and without the scalar tail), the float64 closed form of the widened weights, and the
+    lane structure itself: the 16-lane vec_dot_f32 order over the same values differs from the golden
+    (so a router kernel left in the fp32 order would be caught)."""
+    z = load("units_router16.npz")
+    for k in (37, 512, 4101):
+        w, y = z[f"dot_w_{t}_{k}"], z[f"dot_y_{t}_{k}"]
+        got = np.float32(port.vec_dot_quant_f32(t, w.view(np.uint8), y))
+        assert got.view(np.uint32) == z[f"dot_o_{t}_{k}"].view(np.uint32), (t, k)
+        w64 = _h16_values(t, w)
+        assert abs(float(got) - float(w64 @ y.astype(np.float64))) <= 2e-6 * float(np.abs(w64) @ np.abs(y)) + 1e-30
+    w, y = z[f"dot_w_{t}_4101"], z[f"dot_y_{t}_4101"]
+    wrong = np.float32(port.vec_dot_f32(_h16_values(t, w).astype(np.float32), y))
+    assert wrong.view(np.uint32) != z[f"dot_o_{t}_4101"].view(np.uint32)
+    E, d = 24, 2048
+    mw, mx = z[f"mm_w_{t}"], z[f"mm_x_{t}"]
+    got = port.matmul_quant_f32(t, mw.view(np.uint8), mx, E, d)
+    assert np.array_equal(got.view(np.uint32), z[f"mm_o_{t}"].view(np.uint32))
+
+
+@pytest.mark.parametrize("t", [F.F16, F.BF16])
+def test_router16_live_vs_reference(port, ref, t):
+    """Seeded rows of assorted lengths through both builds, bit for bit, and a layer's routing."""
+    import dataclasses
+    rng = np.random.default_rng(11 + t)
+    for k in (8, 24, 64, 136, 1000, 2048, 8192):
+        v = (rng.standard_normal(k) * 0.05).astype(np.float32)
+        w = synth.to_f16_bits(v) if t == F.F16 else synth.to_bf16_bits(v)
+        y = rng.standard_normal(k).astype(np.float32)
+        a = np.float32(port.vec_dot_quant_f32(t, w.view(np.uint8), y))
+        b = np.float32(ref.vec_dot_quant_f32(t, w.view(np.uint8), y))
+        assert a.view(np.uint32) == b.view(np.uint32), (t, k)
+    cfg = dataclasses.replace(synth.CONFIGS["toy"], name="toy_live_r16", router_type=t)
+    lw, x = synth.make_layer(cfg), synth.make_tokens(synth.CONFIGS["toy"], 6)
+    o1, i1, w1, l1 = port.moe_forward(lw, x)
+    o2, i2, w2, l2 = ref.moe_forward(lw, x)
+    assert np.array_equal(l1.view(np.uint32), l2.view(np.uint32)) and np.array_equal(i1, i2)
+    assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32))
+
+
 @pytest.mark.parametrize("qt", [F.Q5_0, F.Q6_K, F.Q5_K])
 def test_f3_swiglu_golden(port, qt):
     """matmul_swiglu_quant_f32 over fp32 x (Q5_0: no Q8_0 form) and Q8_0 x (Q5_K, Q6_K)."""
@@ -399,7 +448,8 @@ def test_select_experts_live_vs_reference(port, ref):
 # --------------------------------------------------------------- whole MoE block vs the golden vectors
 F3_GOLDEN_CASES = ["toy_q5k_n1", "toy_q5k_n64", "toy_q6k_n1", "toy_q6k_n64", "toy_q50_n1", "toy_q50_n64",
                    "mixtral_q6k_n1", "mixtral_q6k_n512", "dsv2lite_q50_n1", "dsv2lite_q50_n32"]
-GOLDEN_CASES = F3_GOLDEN_CASES + ["toy_n1", "qwen15moe_n1", "qwen15moe_n64", "mixtral_n1", "mixtral_n512",
+ROUTER16_GOLDEN_CASES = ["toy_f16r_n1", "toy_f16r_n64", "toy_bf16r_sh_n1", "toy_bf16r_sh_n64"]
+GOLDEN_CASES = F3_GOLDEN_CASES + ROUTER16_GOLDEN_CASES + ["toy_n1", "qwen15moe_n1", "qwen15moe_n64", "mixtral_n1", "mixtral_n512",
                 "mixtral_n2048", "qwen3moe_n2048", "dsv2lite_n32", "toy_gelu_n1", "toy_gelu_n64",
                 "toy_norm_n1_resid", "toy_norm_n64_resid"]
 
