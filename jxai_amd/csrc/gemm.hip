@@ -204,6 +204,7 @@ __device__ __forceinline__ void work_item(int L, int n_items, int R, int S, int 
 }
 
 // ---------------------------------------------------------------- weights
+
 // Raw weight bytes of one half-unit for lane (n, g) of one row tile: the lane
 // reads row n.  off() is the lane's byte offset of its row in the tile layout
 // (jxmoe_kernels.h), at() the half-unit's offset, the same for every lane.
@@ -214,8 +215,9 @@ template <>
 struct WRaw<T_Q4_K> {
     uint4 q[2];   // sub-block pairs 2s, 2s+1 of super-block h/2 (s = h&1), half g: elements
                   // 16g..16g+15 of sub-blocks 2p (low nibbles) and 2p+1 (high nibbles)
-    uint4 hd;     // header of row n (d | dmin << 16, scales[12]); loaded with the even half
+    uint32_t hd;  // d | dmin << 16 of row n's header; loaded with the even half
     uint4 mn[3];  // min-term pieces of row n (hi, mid, lo; QMat::mn); loaded with the odd half
+    uint4 cs;     // the 8 sub-blocks' fp16 operand scales s1 of row n (QMat::mn); loaded with the even half
     __device__ static uint32_t qoff(const QMat& W, int rt, int n, int g) {
         return (uint32_t)((((size_t)rt * W.nkb * 8 + g) * 32 + n) * 16);
     }
@@ -223,7 +225,7 @@ struct WRaw<T_Q4_K> {
         return (uint32_t)(((size_t)rt * W.nkb * 32 + n) * 16);
     }
     __device__ static uint32_t moff(const QMat& W, int rt, int n) {
-        return (uint32_t)(((size_t)rt * W.nkb * 96 + n) * 16);
+        return (uint32_t)(((size_t)rt * W.nkb * (MN_SB / 16) + n) * 16);
     }
     // PAR: the parity of h (even half-units carry the header, odd ones the min pieces), so each of the
     // two alternating register sets holds only the fields its parity uses
@@ -236,10 +238,11 @@ struct WRaw<T_Q4_K> {
         const uint8_t* qh = qb + (size_t)(h >> 1) * 4096 + PAR * 2048;
 #pragma unroll
         for (int p = 0; p < 2; ++p) q[p] = ld16(qh + p * 1024 + qo);
+        const uint8_t* mh = mb + (size_t)(h >> 1) * MN_SB + mo;
         if (PAR == 0) {
-            hd = ld16(sb + (size_t)(h >> 1) * 512 + so);
+            hd = *reinterpret_cast<const uint32_t*>(sb + (size_t)(h >> 1) * 512 + so);
+            cs = ld16(mh + MN_CS);
         } else {
-            const uint8_t* mh = mb + (size_t)(h >> 1) * 1536 + mo;
 #pragma unroll
             for (int c = 0; c < 3; ++c) mn[c] = ld16(mh + c * 512);
         }
@@ -492,7 +495,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
         for (int t = 0; t < TN2; ++t) acc2[i][t] = v16f{};
 
     WRaw<TYPE> wa[TM], wb[TM];
-    uint4 hdr[TM];  // Q4_K / Q5_K headers (Q6_K: the 16 scales) of the current super-block
+    uint4 hdr[TM];  // the current super-block's sub-block scales: Q6_K's 16 int8, Q4_K / Q5_K's 8 fp16 s1
     float dl[TM];   // the unit acc is kept in for the lane's row: the current super-block's (Q4_K) or
                     // block's (Q4_0 / Q8_0) weight scale d, 1 where d is zero
     float dl2[TM2]; // the unit of acc2
@@ -537,8 +540,8 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
                         hdr[i] = cur[i].sc;
                         d = f16_to_f32(cur[i].d & 0xFFFFu);
                     } else {
-                        hdr[i] = cur[i].hd;
-                        d = f16_to_f32(hdr[i].x & 0xFFFFu);
+                        hdr[i] = cur[i].cs;  // the super-block's operand scales, for both halves
+                        d = f16_to_f32(cur[i].hd & 0xFFFFu);
                     }
                     if constexpr (RESCALE) {
                         dz[i] = d == 0.0f;
@@ -604,14 +607,12 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
                             c1[i] = splat(scf * 0.25f);
                             c0[i] = splat(scf * -288.0f);
                         } else {
-                            int sc, mn;
-                            hdr_scale_min(hdr[i], 4 * ODD + jj, sc, mn);
-                            const _Float16 sv = (_Float16)(RESCALE && dz[i] ? 0.0f : (float)sc);  // exact
-                            // Q5_K quants arrive in the low bits (0..31); Q4_K high nibbles stay in place
-                            const bool hi = TYPE == T_Q4_K && (jj & 1);
-                            const _Float16 s1 = hi ? sv * (_Float16)0.0625f : sv;
-                            const _Float16 s0 = hi ? sv * (_Float16)-64.0f : sv * (_Float16)-1024.0f;
+                            // sub-block J = 4 ODD + jj's scale s1 from the table built at upload (k_min_table;
+                            // zero where d is zero) and s0 = -1024 s1 (exact)
+                            const uint32_t w2 = ODD ? (jj < 2 ? hdr[i].z : hdr[i].w) : (jj < 2 ? hdr[i].x : hdr[i].y);
+                            const _Float16 s1 = as_h2(w2)[jj & 1];
                             c1[i] = h2v{s1, s1};
+                            const _Float16 s0 = s1 * (_Float16)-1024.0f;
                             c0[i] = h2v{s0, s0};
                         }
                     }
@@ -1034,6 +1035,11 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
 // zero) for the 8 sub-blocks, in the unit the GEMM's accumulator uses for that
 // super-block.  -dmin * m_j is exact in fp32 (11-bit x 6-bit); the division
 // rounds once; the split is exact.
+// Also the GEMM's A-operand scale of each sub-block J (fp16, exact): the weight fragment holds 1024 + v
+// with v = q for Q5_K and Q4_K low nibbles, v = 16 q for Q4_K high nibbles, and s1 (1024 + v) - 1024 s1 =
+// sc_J q in one fused fp16 fma, with s1 = sc_J (sc_J / 16 for high nibbles), zero where d is zero.
+// Converting the 6-bit scales in the kernel cost ~90 VALU instructions per super-block and wave of the
+// gate/up GEMM.
 __global__ void __launch_bounds__(256) k_min_table(QMat m, uint8_t* mn) {
     const size_t n = (size_t)m.n_mats * m.nrt * m.nkb * 32;
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -1042,7 +1048,7 @@ __global__ void __launch_bounds__(256) k_min_table(QMat m, uint8_t* mn) {
     const uint4 hd = ld16(m.sc + (t * 32 + row) * 16);
     const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
     const float u = d == 0.0f ? 1.0f : d;
-    uint32_t pw[3][4];
+    uint32_t pw[3][4], cw[4];
 #pragma unroll
     for (int j = 0; j < 8; j += 2) {
         uint16_t p[3][2];
@@ -1051,13 +1057,20 @@ __global__ void __launch_bounds__(256) k_min_table(QMat m, uint8_t* mn) {
             int sc, mv;
             hdr_scale_min(hd, j + k, sc, mv);
             split3((-dmin * (float)mv) / u, p[0][k], p[1][k], p[2][k]);
+            const bool hi = m.type == T_Q4_K && ((j + k) & 1);
+            const float sv = d == 0.0f ? 0.0f : (float)sc;
+            const _Float16 s1 = (_Float16)(hi ? sv * 0.0625f : sv);
+            if (k == 0) cw[j / 2] = __builtin_bit_cast(uint16_t, s1);
+            else cw[j / 2] |= (uint32_t)__builtin_bit_cast(uint16_t, s1) << 16;
         }
 #pragma unroll
         for (int c = 0; c < 3; ++c) pw[c][j / 2] = (uint32_t)p[c][0] | ((uint32_t)p[c][1] << 16);
     }
+    uint8_t* base = mn + t * MN_SB + row * 16;
 #pragma unroll
     for (int c = 0; c < 3; ++c)
-        *reinterpret_cast<uint4*>(mn + ((t * 3 + c) * 32 + row) * 16) = make_uint4(pw[c][0], pw[c][1], pw[c][2], pw[c][3]);
+        *reinterpret_cast<uint4*>(base + c * 512) = make_uint4(pw[c][0], pw[c][1], pw[c][2], pw[c][3]);
+    *reinterpret_cast<uint4*>(base + MN_CS) = make_uint4(cw[0], cw[1], cw[2], cw[3]);
 }
 
 void launch_min_table(const QMat& m, uint8_t* mn, hipStream_t st) {

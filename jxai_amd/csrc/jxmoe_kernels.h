@@ -22,6 +22,8 @@ namespace jx {
 //         sc  [e][rt][sb][32 rows][16 B] = the 16 int8 sub-block scales
 //         ex  [e][rt][sb][32] fp16 d
 // Byte totals of qs+sc(+ex) equal the GGUF tensor (18/34/144/22/176/210 B per block).
+constexpr int MN_SB = 2048, MN_CS = 1536;  // QMat::mn bytes per (row tile, super-block); scales offset
+
 struct QMat {
     int type = 0;
     int rows = 0;       // per expert, multiple of 32
@@ -41,10 +43,11 @@ struct QMat {
     const uint8_t* ex = nullptr;
     size_t ex_es = 0;
     const uint8_t* pad_ex = nullptr;
-    // Q4_K / Q5_K min-term table for the matrix-core GEMMs (launch_min_table; null for
-    // other types and for matrices only the GEMVs read): per (expert, row tile,
-    // super-block) 3 x [32 rows][16 B] = the bf16 pieces (hi, mid, lo) of
-    // -dmin * m_j / u for the 8 sub-blocks j, u = d (1 where d is zero).
+    // Q4_K / Q5_K table for the matrix-core GEMMs (launch_min_table; null for other types
+    // and for matrices only the GEMVs read): per (expert, row tile, super-block) MN_SB
+    // bytes, 3 x [32 rows][16 B] = the bf16 pieces (hi, mid, lo) of -dmin * m_j / u for
+    // the 8 sub-blocks j, u = d (1 where d is zero), then at MN_CS [32 rows][16 B] = the
+    // fp16 A-operand scales s1 of the 8 sub-blocks.
     const uint8_t* mn = nullptr;
     size_t mn_es = 0;  // per-expert stride (bytes)
     // Gated activation applied to this matrix's outputs when it is the gate of
@@ -207,7 +210,7 @@ void launch_mfma_down(const QMat& dn, const ActH& hin, const Groups& grp, int ti
 // Weight types the matrix-core gate/up GEMM takes (Q5_0 has no Q8_0-activation form; Q6_K's sc * q
 // operand is not exact in fp16, and gate/up products must be: h is re-quantized).
 bool gemm_gateup_ok(int type);
-// Fill m.mn (m.n_mats * m.nrt * m.nkb * 1536 bytes) from a repacked Q4_K or Q5_K matrix.
+// Fill m.mn (m.n_mats * m.nrt * m.nkb * MN_SB bytes) from a repacked Q4_K or Q5_K matrix.
 void launch_min_table(const QMat& m, uint8_t* mn, hipStream_t st);
 
 // acc[t] = sum_s p[t][s] * y[pos(t,s)] (+ shscale[t] * ysh[t]), fma in selection order;

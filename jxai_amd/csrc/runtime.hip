@@ -150,8 +150,8 @@ int upload_matrix(int type, int n_mats, int rows, int cols, const void* host, De
     m.qs_es = units * qs_u;
     m.sc_es = units * sc_u;
     m.ex_es = units * ex_u;
-    // the GEMMs address one expert's matrix with 32-bit offsets (min table: 12x the headers)
-    if (m.qs_es >= ((size_t)1 << 32) || m.sc_es * 12 >= ((size_t)1 << 32))
+    // the GEMMs address one expert's matrix with 32-bit offsets (the GEMM table: 4x the headers)
+    if (m.qs_es >= ((size_t)1 << 32) || m.sc_es * 4 >= ((size_t)1 << 32))
         return fail(JX_ERR_UNSUPPORTED, "one expert matrix exceeds 4 GiB");
     const size_t raw_bytes = (size_t)n_mats * rows * row_bytes(type, cols);
     uint8_t* raw = nullptr;
@@ -176,7 +176,7 @@ int upload_matrix(int type, int n_mats, int rows, int cols, const void* host, De
         e = hipGetLastError();
     }
     if (e == hipSuccess && gemm && (type == jx::T_Q4_K || type == jx::T_Q5_K)) {
-        m.mn_es = (size_t)m.nrt * m.nkb * 1536;
+        m.mn_es = (size_t)m.nrt * m.nkb * jx::MN_SB;
         e = hipMalloc(&out.mn, m.mn_es * n_mats);
         if (e == hipSuccess) {
             m.mn = out.mn;
