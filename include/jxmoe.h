@@ -50,8 +50,11 @@ enum {
     JX_FWD_ASYNC = 1u << 1,       /* return after enqueueing (device ptrs only)   */
     JX_FWD_FORCE_GEMV = 1u << 2,  /* force the decode (dequant-GEMV) regime       */
     JX_FWD_FORCE_MFMA = 1u << 3,  /* force the prefill (matrix-core GEMM) regime  */
-    JX_FWD_RESIDUAL = 1u << 4     /* x is the residual stream before ffn_norm: the
+    JX_FWD_RESIDUAL = 1u << 4,    /* x is the residual stream before ffn_norm: the
                                      whole FFN step of forward_token (see below)   */
+    JX_FWD_UNFUSED = 1u << 5      /* one-token steps as separate router, gate/up and
+                                     down launches instead of the single fused
+                                     launch (same results; for comparison)          */
 };
 
 /* One MoE layer, as bound by bind_tensors (src/transformer.cpp:2142-2186).

@@ -18,6 +18,7 @@ JX_FWD_ASYNC = 1 << 1
 JX_FWD_FORCE_GEMV = 1 << 2
 JX_FWD_FORCE_MFMA = 1 << 3
 JX_FWD_RESIDUAL = 1 << 4
+JX_FWD_UNFUSED = 1 << 5
 
 JX_ACT_SILU = 0
 JX_ACT_GELU_TANH = 1

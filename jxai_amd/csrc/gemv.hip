@@ -651,16 +651,11 @@ struct StageF32 {
 
 // Q8_0 of one 32-row block of h held by lanes 0..31 (quantize_row_q8_0).
 __device__ __forceinline__ void store_q8_block(float hv, int m, bool writer, ActQ8& hq, size_t row, int blk) {
-    const float amax = wave_max32(__builtin_fabsf(hv));
-    const float dd = amax / 127.0f;
-    const float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
-    float r = round_away(hv * id);
-    r = fminf(fmaxf(r, -127.0f), 127.0f);
-    const int q = (int)r;
-    const int s = wave_sum32i(q);
+    float2 sv;
+    const int q = q8_block_vals(hv, sv);
     if (writer) {
         hq.q[row * hq.K + blk * 32 + m] = (int8_t)q;
-        if (m == 0) hq.s[row * (hq.K / 32) + blk] = make_float2(f16_to_f32(f32_to_f16_trunc(dd)), (float)s);
+        if (m == 0) hq.s[row * (hq.K / 32) + blk] = sv;
     }
 }
 
@@ -1283,6 +1278,321 @@ static void down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, 
         hipLaunchKernelGGL((k_gemv_down<TYPE, 4, DOWN_WAVES, F32ACT>), grid, dim3(DOWN_WAVES * 64), lds, st, dn, hq,
                            hf, hf_ld, grp, y, comb);
     }
+}
+
+// ---------------------------------------------------------------- one-token step in one launch
+// A one-token decode step of a layer without a shared expert (even top-k, Q8_0 activations on both
+// sides) as one grid of 512-thread blocks, in index order:
+//   [0, E)     router rows: block r stages its row and the token chain-major in LDS, runs the
+//              vec_dot_f32 chain (as k_route_small) and publishes the logit as one device-coherent
+//              64-bit word (epoch << 32 | bits).  Block 0 first zeroes the folded combine's output.
+//   E          once every logit of this launch is out: the dispatch tables (topk_dispatch_wave) and
+//              the Q8_0 of x, for the caller.
+//   gate/up    row tile rt of slots 2s and 2s + 1, waves 0-3 and 4-7 each the 4-wave single-token
+//              gate/up GEMV: the Q8_0 of x is formed in LDS while the router runs, the slot's expert
+//              follows from the logits (small_group), and h's Q8_0 block is stored device-coherently,
+//              its quants first, then its scale word carrying the launch's tag.
+//   down       row tile rt of one slot, the 8-wave single-token down GEMV: its first weight units
+//              are in flight before it waits for every scale word of the slot's h to carry the tag;
+//              the quants are then read device-coherently.
+// The arithmetic is that of the separate launches (same chains, quantization, unit order and
+// reductions), so the results are bit-identical to them.  A block waits only on blocks with smaller
+// indices, which the dispatcher starts first, so every wait ends; each is bounded anyway (giving up
+// sets sync->err, and the block goes on with in-bounds reads).  The launch number tags the logits
+// (32 bits) and h's scales (htag, 13 bits: an fp16 scale widened to fp32 has its low 13 mantissa
+// bits zero), so nothing is reset between launches and no two blocks update one word (atomic
+// read-modify-writes on one line serialize at the memory side).  Blocks hand over through
+// device-scope atomic loads and stores only (a device-scope fence writes back the whole L2 on this
+// part).  Calls on one layer must be stream-ordered.
+constexpr int DEC_THREADS = 512;
+constexpr int DEC_SPIN_LIMIT = 1 << 18;  // polls (each a device-coherent round trip) before giving up
+
+__device__ __forceinline__ void dec_fail(DecodeSync* s) {
+    __hip_atomic_store(&s->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wave 0: wait until all E logits carry this launch's tag, then put them in lg (LDS); the caller
+// synchronizes the block.
+__device__ void dec_wait_logits(const Decode1Args& a, float* lg) {
+    const int lane = threadIdx.x & 63;
+    for (int it = 0;; ++it) {
+        uint64_t w0 = 0, w1 = 0;
+        bool ok = true;
+        if (lane < a.E) {
+            w0 = __hip_atomic_load(a.sync->tag + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ok = (uint32_t)(w0 >> 32) == a.epoch;
+        }
+        if (64 + lane < a.E) {
+            w1 = __hip_atomic_load(a.sync->tag + 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ok = ok && (uint32_t)(w1 >> 32) == a.epoch;
+        }
+        const bool all = __all(ok);
+        if (all || it >= DEC_SPIN_LIMIT) {
+            if (!all && lane == 0) dec_fail(a.sync);
+            if (lane < a.E) lg[lane] = __uint_as_float((uint32_t)w0);
+            if (64 + lane < a.E) lg[64 + lane] = __uint_as_float((uint32_t)w1);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+constexpr uint32_t DEC_HTAG_MASK = 0x1FFFu;  // low mantissa bits of h's stored scale
+
+template <int TG, int TD>
+__global__ void __launch_bounds__(DEC_THREADS) __attribute__((amdgpu_waves_per_eu(GEMV_WAVES_PER_SIMD(1))))
+k_decode1(Decode1Args a) {
+    extern __shared__ __align__(16) int8_t smem[];
+    __shared__ float lg[SMALL_GROUP_MAX_E];
+    __shared__ float red[DEC_THREADS / 64][32];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 31, h = lane >> 5;
+    const int E = a.E, d = a.d;
+    const int ng = a.G.nrt * (a.k / 2);  // gate/up blocks
+    const int blk = blockIdx.x;
+    Groups grp;  // the slot records follow from the logits (small_group)
+    grp.logits = lg;
+    grp.n_experts = E;
+    grp.top_k = a.k;
+    grp.n_tok = 1;
+
+    if (blk < E) {  // ---- router row blk
+        float* lds = reinterpret_cast<float*>(smem);
+        const int S = rs_stride(d), RS = 16 * S;
+        if (blk == 0 && a.out) {  // the folded combine's output starts at zero
+            for (int i = tid; i < d; i += DEC_THREADS)
+                __hip_atomic_store(reinterpret_cast<uint32_t*>(a.out) + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // complete before the logit is out
+        }
+        {  // row + token -> LDS, chain-major, every load in flight before the first store
+            constexpr int PER = 2 * 8192 / 4 / DEC_THREADS;  // d <= 8192
+            const int c4 = d / 4, tot = 2 * c4;
+            float4 v[PER];
+#pragma unroll
+            for (int q = 0; q < PER; ++q) {
+                const int i = tid + q * DEC_THREADS;
+                if (i >= tot) break;
+                const int row = i / c4, c = i - row * c4;
+                v[q] = *reinterpret_cast<const float4*>((row == 0 ? a.router + (size_t)blk * d : a.x) + 4 * c);
+            }
+#pragma unroll
+            for (int q = 0; q < PER; ++q) {
+                const int i = tid + q * DEC_THREADS;
+                if (i >= tot) break;
+                const int row = i / c4, c = i - row * c4;
+                float* dst = lds + row * RS + 4 * (c & 3) * S + (c >> 2);
+                dst[0] = v[q].x;
+                dst[S] = v[q].y;
+                dst[2 * S] = v[q].z;
+                dst[3 * S] = v[q].w;
+            }
+        }
+        __syncthreads();
+        if (wave == 0 && lane < 16) {
+            const bool c8 = a.chain8 != 0;
+            const float s = chain_sum(chain_dot_lds(lds, lds + RS, S, d, lane, c8), c8);
+            if (lane == 0) {
+                const float l = a.bias ? s + a.bias[blk] : s;
+                a.ra.logits[blk] = l;
+                __hip_atomic_store(a.sync->tag + blk, ((uint64_t)a.epoch << 32) | __float_as_uint(l), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        return;
+    }
+
+    if (blk == E) {  // ---- the caller's dispatch tables and Q8_0 of x
+        if (wave == 0) dec_wait_logits(a, lg);
+        __syncthreads();
+        if (wave == 0) {
+            topk_dispatch_wave<SMALL_GROUP_MAX_E / 64>(a.ra, a.o, lg, nullptr);
+        } else {
+            const int nb = d / 32, hw = 2 * (wave - 1) + h;
+            for (int b = hw; b < nb; b += 2 * (DEC_THREADS / 64 - 1)) {  // half-wave uniform
+                float2 sv;
+                a.xq.q[b * 32 + m] = (int8_t)q8_block_vals(a.x[b * 32 + m], sv);
+                if (m == 0) a.xq.s[b] = sv;
+            }
+        }
+        return;
+    }
+
+    if (blk < E + 1 + ng) {  // ---- gate/up: row tile rt of slots 2 sp, 2 sp + 1
+        const int b = blk - (E + 1), rt = b % a.G.nrt, sp = b / a.G.nrt;
+        const int half = wave >> 2, lw = wave & 3, mat = lw >> 1, kw = lw & 1, slot = 2 * sp + half;
+        const int K = d, KB = K / 32;
+        int8_t* xq = smem;                                     // [K] quants
+        float2* xs = reinterpret_cast<float2*>(smem + K);      // [K / 32] (scale, sum)
+        {  // Q8_0 of x while the router runs, one 32-block per half-wave and step (as the router kernels)
+            constexpr int XPER = 8192 / 32 / (2 * DEC_THREADS / 64);  // d <= 8192
+            const int hw = 2 * wave + h;
+            float xv[XPER];
+#pragma unroll
+            for (int q = 0; q < XPER; ++q) {
+                const int bb = hw + q * (2 * DEC_THREADS / 64);
+                xv[q] = bb < KB ? a.x[bb * 32 + m] : 0.0f;
+            }
+#pragma unroll
+            for (int q = 0; q < XPER; ++q) {
+                const int bb = hw + q * (2 * DEC_THREADS / 64);
+                if (bb < KB) {  // half-wave uniform
+                    float2 sv;
+                    xq[bb * 32 + m] = (int8_t)q8_block_vals(xv[q], sv);
+                    if (m == 0) xs[bb] = sv;
+                }
+            }
+        }
+        if (wave == 0) dec_wait_logits(a, lg);
+        __syncthreads();  // the logits and the Q8_0 of x
+        const int4 rec = small_group(grp, slot);
+        const int e = rec.x, p0 = rec.y;
+        const ActLds A{xq, xs, nullptr, K};
+        const QMat& W = mat ? a.U : a.G;
+        const int nu = n_units<TG>(a.G.nkb);
+        float acc[1] = {0.0f};
+        kloop<TG, 1>(
+            W, W, e, rt, kw, nu, 2, m, h, [] {},
+            [&](const typename Fmt<TG>::Raw& c, const typename Fmt<TG>::Raw&, int u) {
+                unit_accum<TG, 1>(c, A, u, h, 1, a.G.nkb, acc);
+            });
+        acc[0] += __shfl_xor(acc[0], 32, 64);
+        if (h == 0) red[wave][m] = acc[0];
+        __syncthreads();
+        if (lw == 0) {  // waves 0 and 4: SwiGLU and the Q8_0 block of h (as k_gemv_gateup)
+            float gv = 0.0f, uv = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+                gv += red[4 * half + w][m];
+                uv += red[4 * half + 2 + w][m];
+            }
+            float2 sv;
+            const int q = q8_block_vals(gated(gv, uv, a.G.act), sv);
+            const uint32_t q1 = (uint32_t)__shfl_down(q, 1, 64), q2 = (uint32_t)__shfl_down(q, 2, 64),
+                           q3 = (uint32_t)__shfl_down(q, 3, 64);
+            const uint32_t word = ((uint32_t)q & 0xFFu) | ((q1 & 0xFFu) << 8) | ((q2 & 0xFFu) << 16) | (q3 << 24);
+            if (h == 0 && (m & 3) == 0)
+                __hip_atomic_store(reinterpret_cast<uint32_t*>(a.hq.q + (size_t)p0 * a.hq.K + rt * 32 + m), word,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the quants are out before the tagged scale
+            if (lane == 0)
+                __hip_atomic_store(reinterpret_cast<uint64_t*>(a.hq.s + (size_t)p0 * (a.hq.K / 32) + rt),
+                                   ((uint64_t)__float_as_uint(sv.y) << 32) | __float_as_uint(sv.x) | a.htag,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
+
+    {  // ---- down: row tile rt of one slot
+        const int b = blk - (E + 1 + ng), rt = b % a.D.nrt, slot = b / a.D.nrt;
+        if (wave == 0) dec_wait_logits(a, lg);
+        __syncthreads();
+        const int4 rec = small_group(grp, slot);
+        const int e = rec.x, p0 = rec.y;
+        const int K = a.hq.K, KB = K / 32;
+        const ActLds A{smem, reinterpret_cast<const float2*>(smem + K), nullptr, K};
+        const int nu = n_units<TD>(a.D.nkb);
+        float acc[1] = {0.0f};
+        kloop<TD, 1>(
+            a.D, a.D, e, rt, wave, nu, DEC_THREADS / 64, m, h,
+            [&] {  // after the first two units' loads: wait until every scale word of the slot's h carries
+                   // this launch's tag (its quants were stored before it), then stage h
+                const uint64_t* ss = reinterpret_cast<const uint64_t*>(a.hq.s + (size_t)p0 * KB);
+                uint64_t sv = 0;
+                for (int it = 0;; ++it) {
+                    if (tid < KB) sv = __hip_atomic_load(ss + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    const bool ok = tid >= KB || ((uint32_t)sv & DEC_HTAG_MASK) == a.htag;
+                    if (__syncthreads_and(ok)) break;  // block-uniform
+                    if (it >= DEC_SPIN_LIMIT) {
+                        if (tid == 0) dec_fail(a.sync);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                constexpr int QPER = 16384 / 4 / DEC_THREADS;  // d_ff <= 16384
+                const uint32_t* qs = reinterpret_cast<const uint32_t*>(a.hq.q + (size_t)p0 * K);
+                uint32_t qv[QPER];
+#pragma unroll
+                for (int q = 0; q < QPER; ++q) {
+                    const int i = tid + q * DEC_THREADS;
+                    qv[q] = i < K / 4 ? __hip_atomic_load(qs + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+                }
+#pragma unroll
+                for (int q = 0; q < QPER; ++q) {
+                    const int i = tid + q * DEC_THREADS;
+                    if (i < K / 4) reinterpret_cast<uint32_t*>(smem)[i] = qv[q];
+                }
+                if (tid < KB) reinterpret_cast<uint64_t*>(smem + K)[tid] = sv & ~(uint64_t)DEC_HTAG_MASK;
+                __syncthreads();
+            },
+            [&](const typename Fmt<TD>::Raw& c, const typename Fmt<TD>::Raw&, int u) {
+                unit_accum<TD, 1>(c, A, u, h, 1, a.D.nkb, acc);
+            });
+        acc[0] += __shfl_xor(acc[0], 32, 64);
+        if (h == 0) red[wave][m] = acc[0];
+        __syncthreads();
+        if (wave == 0) {
+            float p = 0.0f;
+            if (a.out) {  // this slot's weight: the softmax of topk_token_wave, as in the tables
+                RouteArgs r = a.ra;
+                r.ids = nullptr;
+                r.probs = nullptr;
+                r.shscale = nullptr;
+                uint64_t msk[SMALL_GROUP_MAX_E / 64];
+                float myp = 0.0f;
+                const int myid = topk_token_wave<SMALL_GROUP_MAX_E / 64>(r, lg, 0, nullptr, msk, &myp);
+                for (int q = 0; q < a.k; ++q) {
+                    const int id = __shfl(myid, q, 64);
+                    const float pq = __shfl(myp, q, 64);
+                    if (id == e) p = pq;
+                }
+            }
+            if (h == 0) {
+                float s = 0.0f;
+#pragma unroll
+                for (int w = 0; w < DEC_THREADS / 64; ++w) s += red[w][m];
+                const int row = rt * 32 + m;
+                if (!(a.D.valid_rows && row >= a.D.valid_rows)) {
+                    if (a.out) atomicAdd(a.out + row, p * s);
+                    else a.y[(size_t)p0 * a.D.rows + row] = s;
+                }
+            }
+        }
+    }
+}
+
+static bool fmt_q8(int t) { return t == T_Q4_0 || t == T_Q8_0 || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
+
+bool decode1_fits(int gtype, int dtype, int d, int f, int E, int k) {
+    // built: one format on both sides, or a K-quant gate/up with a Q6_K down (the _M mixes)
+    const bool built = fmt_q8(gtype) && (gtype == dtype || ((gtype == T_Q4_K || gtype == T_Q5_K) && dtype == T_Q6_K));
+    return built && E >= 1 && E <= SMALL_GROUP_MAX_E && k >= 2 && k % 2 == 0 && k <= MAX_SLOTS_DEC && k <= E &&
+           d % 32 == 0 && d <= 8192 && f % 32 == 0 && f <= 16384;
+}
+
+// The fused launch pays where its gate/up blocks fit one per CU.  Larger gate/up phases leave the
+// down blocks to the slots the gate/up blocks free, unevenly (measured, Mixtral-shaped: 64 CUs run two
+// down blocks while 64 run none), and the separate launches are faster there.  Measured per step:
+// toy 15.9 -> 11.2 us, Qwen3-shaped 26.1 -> 24.9 us, Mixtral-shaped 46.1 -> 48.6 us (not taken).
+bool decode1_pays(int gate_nrt, int k) { return gate_nrt * (k / 2) <= num_cus(); }
+
+void launch_decode1(const Decode1Args& a, int gtype, int dtype, hipStream_t st) {
+    const dim3 grid(a.E + 1 + a.G.nrt * (a.k / 2) + a.D.nrt * a.k);
+    // LDS: router row + token chain-major, or a gate/up's Q8_0 of x, or a down's Q8_0 of h
+    const size_t lds = std::max({(size_t)2 * 16 * rs_stride(a.d) * sizeof(float),
+                                 act_lds_bytes(1, a.d, false), act_lds_bytes(1, a.hq.K, false)});
+    auto go = [&](auto kern) {
+        lds_optin(kern, lds);
+        hipLaunchKernelGGL(kern, grid, dim3(DEC_THREADS), lds, st, a);
+    };
+#define JX_DEC1(G, D) \
+    if (gtype == G && dtype == D) return go(k_decode1<G, D>);
+    JX_DEC1(T_Q4_0, T_Q4_0)
+    JX_DEC1(T_Q8_0, T_Q8_0)
+    JX_DEC1(T_Q4_K, T_Q4_K)
+    JX_DEC1(T_Q5_K, T_Q5_K)
+    JX_DEC1(T_Q6_K, T_Q6_K)
+    JX_DEC1(T_Q4_K, T_Q6_K)
+    JX_DEC1(T_Q5_K, T_Q6_K)
+#undef JX_DEC1
 }
 
 void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp, int slots,

@@ -11,6 +11,89 @@ namespace jx {
 constexpr int MAX_E = 512;
 constexpr int MAX_K = 32;
 
+// Q8_0 of one 32-block held one value per lane of a half-wave
+// (quantize_row_q8_0, src/quant.cpp:1029-1045): amax, d = amax/127 (IEEE
+// division), id = 1/d, q = clamp(round-half-away(x*id)), stored scale =
+// truncated fp16 of d, and the block sum of q (for the Q4_0 -8 offset and the
+// K-quant min terms).  Returns the lane's q; sv = (stored scale, sum).
+__device__ __forceinline__ int q8_block_vals(float v, float2& sv) {
+    const float amax = wave_max32(__builtin_fabsf(v));
+    const float dd = amax / 127.0f;
+    const float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
+    float r = round_away(v * id);
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    const int q = (int)r;
+    sv = make_float2(f16_to_f32(f32_to_f16_trunc(dd)), (float)wave_sum32i(q));
+    return q;
+}
+
+// Chain-major rows: element 16 i + j of a row at j * S + i, so lane j of a
+// vec_dot_f32 chain reads its operands four at a time.  In LDS the stride is
+// padded to a multiple of 4 floats plus 4 against bank conflicts; the router
+// copy in global memory (chain_rows) uses the bare multiple of 4, and each
+// lane's run of steps then sits in a few L1 lines it revisits (measured
+// faster than interleaving the 16 chains for contiguous group loads).
+__host__ __device__ constexpr int rs_stride(int d) { return ((d / 16 + 3) & ~3) + 4; }
+__host__ __device__ constexpr int chain_stride_of(int d) { return (d / 16 + 3) & ~3; }
+
+// Lane j (0..15) of one router row's chain group against one token, both
+// chain-major in LDS with stride S: vec_dot_f32's fp32 FMA chain over elements
+// 16 i + j (src/quant.cpp:2756-2778).  c8: an F16 / BF16 router row, whose
+// dots (src/quant.cpp:3015-3055) run 8 chains over 8-element steps, i.e.
+// chain-major columns jc and jc + 8 interleaved step by step (lanes 8-15
+// repeat lanes 0-7).  d % 16 == 0.
+__device__ __forceinline__ float chain_dot_lds(const float* w, const float* x, int S, int d, int j, bool c8) {
+    const int jc = c8 ? (j & 7) : j;
+    const float* wr = w + jc * S;
+    const float* xr = x + jc * S;
+    const int m = d / 16, m4 = m & ~3;
+    float acc = 0.0f;
+    if (c8) {
+        for (int i = 0; i < m4; i += 4) {
+            const float4 p = *reinterpret_cast<const float4*>(wr + i);
+            const float4 p8 = *reinterpret_cast<const float4*>(wr + 8 * S + i);
+            const float4 q = *reinterpret_cast<const float4*>(xr + i);
+            const float4 q8 = *reinterpret_cast<const float4*>(xr + 8 * S + i);
+            acc = __builtin_fmaf(p.x, q.x, acc);
+            acc = __builtin_fmaf(p8.x, q8.x, acc);
+            acc = __builtin_fmaf(p.y, q.y, acc);
+            acc = __builtin_fmaf(p8.y, q8.y, acc);
+            acc = __builtin_fmaf(p.z, q.z, acc);
+            acc = __builtin_fmaf(p8.z, q8.z, acc);
+            acc = __builtin_fmaf(p.w, q.w, acc);
+            acc = __builtin_fmaf(p8.w, q8.w, acc);
+        }
+        for (int i = m4; i < m; ++i) {
+            acc = __builtin_fmaf(wr[i], xr[i], acc);
+            acc = __builtin_fmaf(wr[8 * S + i], xr[8 * S + i], acc);
+        }
+    } else {
+#pragma unroll 8
+        for (int i = 0; i < m4; i += 4) {
+            const float4 p = *reinterpret_cast<const float4*>(wr + i);
+            const float4 q = *reinterpret_cast<const float4*>(xr + i);
+            acc = __builtin_fmaf(p.x, q.x, acc);
+            acc = __builtin_fmaf(p.y, q.y, acc);
+            acc = __builtin_fmaf(p.z, q.z, acc);
+            acc = __builtin_fmaf(p.w, q.w, acc);
+        }
+        for (int i = m4; i < m; ++i) acc = __builtin_fmaf(wr[i], xr[i], acc);
+    }
+    return acc;
+}
+
+// The end of a 16-lane router chain group: vec_dot_f32 (src/quant.cpp:2756-2778) adds lane j + 8
+// (the reference's acc1) to lane j < 8 (acc0), then sums lanes 0..7 in order from zero; the F16 /
+// BF16 dots (src/quant.cpp:3015-3055) have the 8 lanes only.
+__device__ __forceinline__ float chain_sum(float acc, bool c8) {
+    const float hi = __shfl_down(acc, 8, 16);
+    const float v = c8 ? acc : acc + hi;
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) s += __shfl(v, q, 16);
+    return s;
+}
+
 // Selection order of select_experts_cache_aware (src/tier.cpp:144-146):
 // descending logit; exact ties are ordered by expert index (the reference's
 // std::sort leaves them unspecified).  NaN ranks as -inf, so the order is
@@ -98,12 +181,12 @@ __device__ __forceinline__ uint64_t wave_max_key(uint64_t x) {
 // its raw shared-gate logit (null: no shared gate).  k rounds of the wave
 // argmax (order: logit descending, index ascending, NaN as -inf) give the
 // selection in rank order; the softmax folds the max and the sum in that
-// order as the reference does.  Writes ids, probs and the shared-gate scale
-// of token t; returns the selection mask and, on lane r < k, the expert of
-// rank r.
+// order as the reference does.  Writes ids, probs (a.ids non-null) and the
+// shared-gate scale (a.shscale non-null) of token t; returns the selection mask
+// and, on lane r < k, the expert of rank r (and in *myprob its weight).
 template <int NC>
 __device__ __forceinline__ int topk_token_wave(const RouteArgs& a, const float* lt, size_t t, const float* shl,
-                                               uint64_t (&msk)[NC]) {
+                                               uint64_t (&msk)[NC], float* myprob = nullptr) {
     static_assert(NC * 64 <= MAX_E, "expert chunks");
     constexpr float NEG = -__builtin_inff();
     const int lane = threadIdx.x & 63, E = a.E, k = a.k;
@@ -143,10 +226,11 @@ __device__ __forceinline__ int topk_token_wave(const RouteArgs& a, const float* 
     float sum = 0.0f;
     for (int r = 0; r < k; ++r) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), r));
     const float inv = (sum > 0.0f) ? 1.0f / sum : 1.0f / (float)k;
-    if (lane < k) {
+    if (lane < k && a.ids) {
         a.ids[t * k + lane] = myid;
         a.probs[t * k + lane] = p * inv;
     }
+    if (myprob) *myprob = p * inv;
     if (lane == 0 && a.shscale) a.shscale[t] = shl ? 1.0f / (1.0f + expf(-shl[t])) : 1.0f;
     return myid;
 }

@@ -122,6 +122,7 @@ struct Groups {
     int n_experts = 0;
 };
 constexpr int SMALL_GROUP_MAX_E = 128;
+constexpr int MAX_SLOTS_DEC = 16;  // routed slots (top_k) of the fused one-token step
 
 constexpr int MFMA_BN = 128;  // pairs per matrix-core GEMM tile
 // shared expert on the matrix cores from this many tokens (one dense expert fills few GEMM
@@ -237,6 +238,39 @@ void launch_route_logits(const RouteArgs& a, hipStream_t st);
 constexpr int ROUTE_SMALL_MAX_N = 2;
 bool route_small_fits(int n, int d, int E);
 void launch_route_small(const RouteArgs& a, const DispatchOut& o, hipStream_t st);
+
+// One-token step in one launch (k_decode1): router rows, dispatch tables, gate/up + SwiGLU + Q8_0
+// of h, down (+ the folded combine) as blocks of one grid that hand over through device-coherent
+// words.  DecodeSync is the layer's device state, zeroed once at creation; the host counts the
+// fused launches of the layer (epoch = 1, 2, ...) and passes the count.
+struct DecodeSync {
+    uint64_t tag[SMALL_GROUP_MAX_E];  // router row r: (epoch << 32) | bits of its logit
+    uint32_t err;                     // nonzero: a bounded wait gave up
+    uint32_t pad;
+};
+
+struct Decode1Args {
+    QMat G, U, D;               // gate, up (d_ff x d), down (d x d_ff); Q8_0-activation formats
+    const float* x;             // [d] the token (normalized when the step carries the residual)
+    const float* router;        // [E][d] fp32 rows (F16 / BF16 widened exactly at upload)
+    const float* bias;          // [E] or null
+    int d = 0, E = 0, k = 0, chain8 = 0;
+    ActQ8 xq;                   // out: Q8_0 of x (for the caller)
+    ActQ8 hq;                   // [k][d_ff] Q8_0 of h, row = slot
+    RouteArgs ra;               // logits, ids, probs, shscale of the caller (n = 1)
+    DispatchOut o;              // the dispatch tables of the caller
+    float* out = nullptr;       // folded combine: [d] zeroed here, p * y added by the down blocks
+    float* y = nullptr;         // otherwise: [k][d] per slot, for launch_combine
+    DecodeSync* sync = nullptr;
+    uint32_t epoch = 0;         // this launch's number among the layer's fused launches (from 1)
+    uint32_t htag = 0;          // 1 + epoch % 8191: the tag in the low 13 bits of h's stored scales
+};
+// Whether k_decode1 is built for this shape: E <= SMALL_GROUP_MAX_E, even k <= MAX_SLOTS_DEC,
+// d % 32 == 0 and d <= 8192, d_ff <= 16384, gate/up and down formats with Q8_0 activations.
+bool decode1_fits(int gtype, int dtype, int d, int f, int E, int k);
+// Whether the fused launch is the faster one for gate/up matrices of gate_nrt row tiles at top-k.
+bool decode1_pays(int gate_nrt, int k);
+void launch_decode1(const Decode1Args& a, int gtype, int dtype, hipStream_t st);
 
 // Q8_0 of rows x K fp32 (row-major, K % 32 == 0).
 void launch_quantize_q8(const float* x, int rows, int K, ActQ8 out, hipStream_t st);

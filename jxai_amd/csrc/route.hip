@@ -9,22 +9,13 @@
 
 namespace jx {
 
-// Q8_0 of one 32-block held one value per lane of a half-wave
-// (quantize_row_q8_0, src/quant.cpp:1029-1045): amax, d = amax/127 (IEEE
-// division), id = 1/d, q = clamp(round-half-away(x*id)), stored scale =
-// truncated fp16 of d.  Writes the int8 quants and (scale, block sum of q);
-// the sum feeds the Q4_0 -8 offset and the Q4_K min term.  Returns q.
+// Q8_0 of one 32-block held one value per lane of a half-wave (q8_block_vals),
+// stored to o8 when ok: the int8 quants and (scale, block sum of q).  Returns q.
 __device__ __forceinline__ int quant_block(float v, int l32, bool ok, const ActQ8& o8, size_t row, int b,
                                            float2* scale_out = nullptr) {
-    const float amax = wave_max32(__builtin_fabsf(v));
-    const float dd = amax / 127.0f;
-    const float id = (dd != 0.0f) ? 1.0f / dd : 0.0f;
-    float r = round_away(v * id);
-    r = fminf(fmaxf(r, -127.0f), 127.0f);
-    const int q = (int)r;
-    const int s = wave_sum32i(q);
+    float2 sv;
+    const int q = q8_block_vals(v, sv);
     if (ok) {
-        const float2 sv = make_float2(f16_to_f32(f32_to_f16_trunc(dd)), (float)s);
         o8.q[row * o8.K + b * 32 + l32] = (int8_t)q;
         if (l32 == 0) {
             o8.s[row * (o8.K / 32) + b] = sv;
@@ -157,26 +148,6 @@ __device__ void write_acth_row(const int8_t* q, const float2* sc, int K, const A
     }
 }
 
-// The end of a 16-lane router chain group: vec_dot_f32 (src/quant.cpp:2756-2778) adds lane j + 8
-// (the reference's acc1) to lane j < 8 (acc0), then sums lanes 0..7 in order from zero; the F16 /
-// BF16 dots (src/quant.cpp:3015-3055) have the 8 lanes only.
-__device__ __forceinline__ float chain_sum(float acc, bool c8) {
-    const float hi = __shfl_down(acc, 8, 16);
-    const float v = c8 ? acc : acc + hi;
-    float s = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) s += __shfl(v, q, 16);
-    return s;
-}
-
-// Chain-major rows: element 16 i + j of a row at j * S + i, so lane j of a
-// vec_dot_f32 chain reads its operands four at a time.  In LDS the stride is
-// padded to a multiple of 4 floats plus 4 against bank conflicts; the router
-// copy in global memory (chain_rows) uses the bare multiple of 4, and each
-// lane's run of steps then sits in a few L1 lines it revisits (measured
-// faster than interleaving the 16 chains for contiguous group loads).
-__host__ __device__ constexpr int rs_stride(int d) { return ((d / 16 + 3) & ~3) + 4; }
-__host__ __device__ constexpr int chain_stride_of(int d) { return (d / 16 + 3) & ~3; }
 int chain_stride(int d) { return chain_stride_of(d); }
 
 void chain_rows(const float* rows, int nrows, int d, float* out) {
@@ -771,43 +742,7 @@ k_route_small(RouteArgs a) {
         if (t < n) {
             // F16 / BF16 router rows: columns jc and jc + 8 interleaved (as k_route); the shared gate fp32
             const bool c8 = a.chain8 && r < E;
-            const int jc = c8 ? (j & 7) : j;
-            const float* wr = lds + jc * S;
-            const float* xr = lds + (1 + t) * RS + jc * S;
-            const int m = d / 16, m4 = m & ~3;
-            float acc = 0.0f;
-            if (c8) {
-                for (int i = 0; i < m4; i += 4) {
-                    const float4 p = *reinterpret_cast<const float4*>(wr + i);
-                    const float4 p8 = *reinterpret_cast<const float4*>(wr + 8 * S + i);
-                    const float4 q = *reinterpret_cast<const float4*>(xr + i);
-                    const float4 q8 = *reinterpret_cast<const float4*>(xr + 8 * S + i);
-                    acc = __builtin_fmaf(p.x, q.x, acc);
-                    acc = __builtin_fmaf(p8.x, q8.x, acc);
-                    acc = __builtin_fmaf(p.y, q.y, acc);
-                    acc = __builtin_fmaf(p8.y, q8.y, acc);
-                    acc = __builtin_fmaf(p.z, q.z, acc);
-                    acc = __builtin_fmaf(p8.z, q8.z, acc);
-                    acc = __builtin_fmaf(p.w, q.w, acc);
-                    acc = __builtin_fmaf(p8.w, q8.w, acc);
-                }
-                for (int i = m4; i < m; ++i) {
-                    acc = __builtin_fmaf(wr[i], xr[i], acc);
-                    acc = __builtin_fmaf(wr[8 * S + i], xr[8 * S + i], acc);
-                }
-            } else {
-#pragma unroll 8
-                for (int i = 0; i < m4; i += 4) {
-                    const float4 p = *reinterpret_cast<const float4*>(wr + i);
-                    const float4 q = *reinterpret_cast<const float4*>(xr + i);
-                    acc = __builtin_fmaf(p.x, q.x, acc);
-                    acc = __builtin_fmaf(p.y, q.y, acc);
-                    acc = __builtin_fmaf(p.z, q.z, acc);
-                    acc = __builtin_fmaf(p.w, q.w, acc);
-                }
-                for (int i = m4; i < m; ++i) acc = __builtin_fmaf(wr[i], xr[i], acc);
-            }
-            const float s = chain_sum(acc, c8);
+            const float s = chain_sum(chain_dot_lds(lds, lds + (1 + t) * RS, S, d, j, c8), c8);
             if (j == 0) {
                 if (r < E) a.logits[(size_t)t * E + r] = a.bias ? s + a.bias[r] : s;
                 else a.shscale[t] = s;  // raw shared-gate logit; the top-k step applies the sigmoid

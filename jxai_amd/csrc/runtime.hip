@@ -296,6 +296,13 @@ struct jx_moe_layer {
     bool use_graphs = true;
     bool fold_combine = true;  // JX_NO_FOLD=1 keeps the separate combine launch (A/B measurement)
     bool chain8 = false;       // F16 / BF16 router: the 8-lane dot order
+    // one-token steps in one launch (k_decode1): its device state, zeroed at creation, and the number
+    // of such launches so far (JX_NO_FUSED=1 keeps the separate launches: A/B measurement)
+    jx::DecodeSync* dsync = nullptr;
+    uint32_t dec_epoch = 0;
+    bool fused_decode = true;
+    bool force_fused = false;  // JX_FUSED=1: also where the separate launches measured faster
+    bool dec_used = false;     // the last forward took the fused launch
 };
 
 struct jx_qmatrix {
@@ -364,6 +371,8 @@ int ensure_workspace(jx_moe_layer* L, int n) {
     L->xq.K = L->d;
     WS(L->hq.q, nk * L->F);
     WS(L->hq.s, nk * L->F / 32);
+    // the fused one-token step polls the low bits of h's scale words for its launch's tag: start untagged
+    HIPCHK(hipMemset(L->hq.s, 0, nk * L->F / 32 * sizeof(float2)));
     L->hq.K = L->F;
     WS(L->y, nk * L->d);
     if (L->gu_f32 || L->sgu_f32) {
@@ -397,7 +406,7 @@ void free_layer(jx_moe_layer* L) {
     void* ptrs[] = {L->router, L->router_cm, L->bias, L->shgate, L->ffn_norm, L->post_norm, L->xn, L->x, L->out, L->probs, L->shscale, L->logits, L->ids,
                     L->counts, L->offs, L->act, L->n_act, L->pair_tok, L->pos_of, L->n_tiles, L->tiles,
                     L->slots, L->xq.q, L->xq.s, L->hq.q, L->hq.s, L->hqs.q, L->hqs.s, L->hf, L->hfs, L->y, L->ysh,
-                    L->xf};
+                    L->xf, L->dsync};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     L->xh.release();
@@ -525,6 +534,53 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     if (fold) {
         ra.zero_out = outdev;
         ra.zero_count = n * d;
+    }
+    // one token, no shared expert: router, gate/up and down (and the folded combine) in one launch
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    HIPCHK(hipStreamIsCapturing(st, &cap));
+    L->dec_used = n == 1 && small_logits && !L->shared && L->fused_decode && !(flags & JX_FWD_UNFUSED) &&
+                  cap == hipStreamCaptureStatusNone && !L->gu_f32 && !L->down_f32 && tb == 1 &&
+                  L->up.m.type == L->gate.m.type &&
+                  jx::decode1_fits(L->gate.m.type, L->down.m.type, d, L->F, E, k) &&
+                  (L->force_fused || jx::decode1_pays(L->gate.m.nrt, k));
+    if (L->dec_used) {
+        if (++L->dec_epoch == 0) {  // 2^32 launches: start the counts over
+            HIPCHK(hipMemsetAsync(L->dsync, 0, sizeof(jx::DecodeSync), st));
+            L->dec_epoch = 1;
+        }
+        jx::Decode1Args a;
+        a.G = L->gate.m;
+        a.U = L->up.m;
+        a.D = L->down.m;
+        a.x = xdev;
+        a.router = L->router;
+        a.bias = L->bias;
+        a.d = d;
+        a.E = E;
+        a.k = k;
+        a.chain8 = L->chain8 ? 1 : 0;
+        a.xq = L->xq;
+        a.hq = L->hq;
+        a.ra = ra;
+        a.ra.zero_out = nullptr;
+        a.ra.zero_count = 0;
+        a.o = dout;
+        a.out = fold ? outdev : nullptr;
+        a.y = L->y;
+        a.sync = L->dsync;
+        a.epoch = L->dec_epoch;
+        a.htag = 1u + L->dec_epoch % 8191u;  // never 0, the low bits of every untagged scale
+        {
+            Launch l(L, fold ? "decode_fused" : "decode_fused_y", st);
+            jx::launch_decode1(a, L->gate.m.type, L->down.m.type, st);
+        }
+        if (!fold) {
+            Launch l(L, "combine", st);
+            jx::launch_combine(n, d, k, L->probs, L->pos_of, L->y, nullptr, L->shscale, outdev, st,
+                               resid ? xres : nullptr, resid ? L->post_norm : nullptr, L->eps);
+        }
+        HIPCHK(hipGetLastError());
+        return JX_OK;
     }
     if (small_logits) {
         Launch l(L, "route", st);
@@ -849,6 +905,10 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
     if (const char* g = std::getenv("JX_NO_GRAPH")) L->use_graphs = L->use_graphs && std::strcmp(g, "0") == 0;
     if (const char* g = std::getenv("JX_GRAPHS")) L->use_graphs = std::strcmp(g, "0") != 0;
     if (const char* f = std::getenv("JX_NO_FOLD")) L->fold_combine = std::strcmp(f, "0") == 0;
+    if (const char* f = std::getenv("JX_NO_FUSED")) L->fused_decode = std::strcmp(f, "0") == 0;
+    if (const char* f = std::getenv("JX_FUSED")) L->force_fused = std::strcmp(f, "0") != 0;
+    if ((r = dalloc(L->dsync, 1)) != JX_OK) return bail(r);
+    if (hipMemset(L->dsync, 0, sizeof(jx::DecodeSync)) != hipSuccess) return bail(fail(JX_ERR_HIP, "decode state"));
     *out = L;
     return JX_OK;
 }
@@ -930,6 +990,15 @@ int jx_moe_forward(jx_moe_layer* L, const float* x, int32_t n_tok, float* out, i
     if (!(flags & JX_FWD_ASYNC)) {
         HIPCHK(hipStreamSynchronize(st));
         if (L->prof.on && (r = resolve_profile(L)) != JX_OK) return r;
+        if (L->dec_used) {  // a bounded wait of the fused one-token launch gave up: start its state over
+            uint32_t err = 0;
+            HIPCHK(hipMemcpy(&err, &L->dsync->err, sizeof(err), hipMemcpyDeviceToHost));
+            if (err) {
+                HIPCHK(hipMemset(L->dsync, 0, sizeof(jx::DecodeSync)));
+                L->dec_epoch = 0;
+                return fail(JX_ERR_HIP, "fused one-token step: a wait between its blocks timed out");
+            }
+        }
     }
     return JX_OK;
 }

@@ -18,6 +18,7 @@ import numpy as np
 
 from . import formats as F
 from ._lib import (JX_FWD_DEVICE_PTRS, JX_FWD_ASYNC, JX_FWD_FORCE_GEMV, JX_FWD_FORCE_MFMA, JX_FWD_RESIDUAL,  # noqa: F401
+                   JX_FWD_UNFUSED,
                    JxError, LayerDesc, check, lib)
 
 _inited = {}
@@ -121,9 +122,10 @@ class MoELayer:
                    ffn_norm=lw.ffn_norm, post_ffw_norm=lw.post_ffw_norm, rms_norm_eps=cfg.rms_eps,
                    router_type=cfg.router_type, device=device, **kw)
 
-    def forward(self, x: np.ndarray, regime: str | None = None, residual: bool = False):
+    def forward(self, x: np.ndarray, regime: str | None = None, residual: bool = False, fused: bool = True):
         """MoE block over host activations [n][d] -> (out [n][d], topk_ids, topk_w, counts).
-        residual: x is the residual stream and out = x + the block on rms_norm(x) (JX_FWD_RESIDUAL)."""
+        residual: x is the residual stream and out = x + the block on rms_norm(x) (JX_FWD_RESIDUAL).
+        fused=False: a one-token step as separate launches (JX_FWD_UNFUSED; same results)."""
         x = np.ascontiguousarray(x, dtype=np.float32)
         n = x.shape[0]
         out = np.empty((n, self.d), np.float32)
@@ -132,15 +134,16 @@ class MoELayer:
         counts = np.empty(self.E, np.int32)
         flags = {None: 0, "gemv": JX_FWD_FORCE_GEMV, "mfma": JX_FWD_FORCE_MFMA}[regime]
         flags |= JX_FWD_RESIDUAL if residual else 0
+        flags |= 0 if fused else JX_FWD_UNFUSED
         check(lib().jx_moe_forward(self.handle, _p(x), n, _p(out), _p(ids), _p(w), _p(counts), None, flags),
               "jx_moe_forward")
         return out, ids, w, counts
 
     def forward_device(self, x: DeviceBuffer, n: int, out: DeviceBuffer, sync: bool = True, regime=None,
-                       stream=None) -> None:
+                       stream=None, fused: bool = True) -> None:
         """MoE block over device-resident activations (no host copies), enqueued on `stream`
         (a hipStream_t as an integer; None: the layer's own stream)."""
-        flags = JX_FWD_DEVICE_PTRS | (0 if sync else JX_FWD_ASYNC)
+        flags = JX_FWD_DEVICE_PTRS | (0 if sync else JX_FWD_ASYNC) | (0 if fused else JX_FWD_UNFUSED)
         flags |= {None: 0, "gemv": JX_FWD_FORCE_GEMV, "mfma": JX_FWD_FORCE_MFMA}[regime]
         st = None if stream is None else C.c_void_p(stream)
         check(lib().jx_moe_forward(self.handle, x.ptr, n, out.ptr, None, None, None, st, flags), "jx_moe_forward")

@@ -1,0 +1,124 @@
+"""GPU parity of the fused one-token step (k_decode1: router rows, gate/up, down and the folded
+combine in one launch whose blocks hand over through device-coherent words) against the separate
+launches (JX_FWD_UNFUSED).  Both run the same arithmetic in the same order, so the bar is bit-exact:
+outputs, router logits, ids, weights, counts and the Q8_0 of x.  The layer's launch count tags each
+launch's logits and h's scale words (blocks poll for the tag), so the cases run many fused steps in
+a row, interleaved with separate and multi-token calls, on one layer.  The layer outputs
+themselves are held to the reference by the golden and oracle tests of test_gpu.py, whose one-token
+cases take the fused launch where it is chosen (gate/up blocks at most one per CU); here JX_FUSED=1
+forces it on every shape it is built for, the Mixtral-sized ones included.
+"""
+import numpy as np
+import pytest
+
+from jxai_amd import formats as F
+from jxai_amd import synth
+from tests.test_gpu import REL_TOL, rel_err, say
+
+pytestmark = pytest.mark.gpu
+
+_LAYERS = {}
+
+EXTRA = {
+    # the residual-stream form (combine after the fused launch) at a Mixtral-sized d_model
+    "mixtral_norm": synth.LayerConfig("mixtral_norm", 4096, 8, 2, 1024, F.Q4_K, norms=True),
+    # top-4 without a shared expert: two gate/up block pairs, the combine after the fused launch
+    "toy_k4": synth.LayerConfig("toy_k4", 512, 16, 4, 768, F.Q8_0),
+}
+
+FUSED = ["toy", "toy_gelu", "toy_f16r", "toy_q5k", "toy_q6k", "toy_k4", "qwen3moe", "mixtral_norm", "mixtral",
+         "mixtral_q6k"]
+
+
+@pytest.fixture(scope="module")
+def moe():
+    from jxai_amd import moe as M
+    M.init(0)
+    return M
+
+
+def layer(name):
+    if name not in _LAYERS:
+        _LAYERS.clear()
+        cfg = synth.CONFIGS[name] if name in synth.CONFIGS else EXTRA[name]
+        _LAYERS[name] = (cfg, synth.make_layer(cfg))
+    return _LAYERS[name]
+
+
+def same(a, b):
+    return np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
+
+
+@pytest.fixture(autouse=True)
+def force_fused(monkeypatch):
+    monkeypatch.setenv("JX_FUSED", "1")  # read when a layer is created
+
+
+def took_fused(L, x, residual):
+    L.profile(True)
+    L.forward(x, residual=residual)
+    names = set(L.profile_read())
+    L.profile(False)
+    return bool(names & {"decode_fused", "decode_fused_y"})
+
+
+def step(L, x, fused, residual):
+    out, ids, w, counts = L.forward(x, fused=fused, residual=residual)
+    return out, ids, w, counts, L.last_logits(x.shape[0]), L.last_xq8(x.shape[0])
+
+
+@pytest.mark.parametrize("name", FUSED)
+def test_fused_step_matches_separate_launches(moe, port, name):
+    cfg, lw = layer(name)
+    residual = cfg.norms
+    L = moe.MoELayer.from_weights(lw)
+    xs = synth.make_tokens(cfg, 6, seed=23)
+    x2 = synth.make_tokens(cfg, 2, seed=29)
+    assert took_fused(L, xs[:1], residual)
+    for i in range(6):
+        x = xs[i:i + 1]
+        say(f"{name} token {i}: fused vs separate")
+        got = step(L, x, True, residual)
+        want = step(L, x, False, residual)
+        for g, w_, what in zip(got, want, ("out", "ids", "weights", "counts", "logits", "xq8")):
+            assert same(g, w_) if g.dtype != np.uint8 else np.array_equal(g, w_), f"token {i}: {what}"
+        if i == 2:  # a two-token step (the separate few-token launches) between fused ones
+            L.forward(x2, residual=residual)
+    # the fused path against the reference's algorithm (the CPU restatement) on the last token
+    x = xs[5:6]
+    out = L.forward(x, residual=residual)[0]
+    want, ids_o, _, _ = port.moe_forward(lw, x, np.array([0], np.int32), residual=residual)
+    err = rel_err(out, want)
+    say(f"{name}: fused step vs oracle max rel err {err:.2e}")
+    assert err <= REL_TOL
+    L.close()
+
+
+@pytest.mark.parametrize("name", ["toy", "mixtral"])
+def test_fused_steps_back_to_back(moe, name):
+    """Hundreds of fused launches queued without host synchronization (the launch count, and with
+    it the tags of the logits and of h's scales, advances every step), then the last outputs against
+    separate-launch steps."""
+    cfg, lw = layer(name)
+    L = moe.MoELayer.from_weights(lw)
+    xs = synth.make_tokens(cfg, 2, seed=41)
+    assert took_fused(L, xs[:1], False)
+    xa, xb_ = xs[0:1], xs[1:2]
+    want_a = L.forward(xa, fused=False)[0]
+    want_b = L.forward(xb_, fused=False)[0]
+    da = moe.DeviceBuffer(xa.nbytes).upload(xa)
+    db = moe.DeviceBuffer(xb_.nbytes).upload(xb_)
+    oa = moe.DeviceBuffer(xa.nbytes)
+    ob = moe.DeviceBuffer(xb_.nbytes)
+    say(f"{name}: 400 fused steps back to back")
+    for i in range(200):
+        L.forward_device(da, 1, oa, sync=False)
+        L.forward_device(db, 1, ob, sync=False)
+    moe.lib().jx_device_synchronize()
+    assert same(oa.download(np.empty_like(xa)), want_a)
+    assert same(ob.download(np.empty_like(xb_)), want_b)
+    # a synchronous fused step reports no timed-out wait
+    assert same(L.forward(xa)[0], want_a)
+    for buf in (da, db, oa, ob):
+        buf.free()
+    L.close()
