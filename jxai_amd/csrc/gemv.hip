@@ -1355,6 +1355,82 @@ k_decode1(Decode1Args a) {
     grp.top_k = a.k;
     grp.n_tok = 1;
 
+    // down row tile bd % D.nrt of slot bd / D.nrt, the logits in lg
+    auto down_tile = [&](int bd) {
+        const int rt = bd % a.D.nrt, slot = bd / a.D.nrt;
+        const int4 rec = small_group(grp, slot);
+        const int e = rec.x, p0 = rec.y;
+        const int K = a.hq.K, KB = K / 32;
+        const ActLds A{smem, reinterpret_cast<const float2*>(smem + K), nullptr, K};
+        const int nu = n_units<TD>(a.D.nkb);
+        float acc[1] = {0.0f};
+        kloop<TD, 1>(
+            a.D, a.D, e, rt, wave, nu, DEC_THREADS / 64, m, h,
+            [&] {  // after the first two units' loads: wait until every scale word of the slot's h carries
+                   // this launch's tag (its quants were stored before it), then stage h
+                const uint64_t* ss = reinterpret_cast<const uint64_t*>(a.hq.s + (size_t)p0 * KB);
+                uint64_t sv = 0;
+                for (int it = 0;; ++it) {
+                    if (tid < KB) sv = __hip_atomic_load(ss + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    const bool ok = tid >= KB || ((uint32_t)sv & DEC_HTAG_MASK) == a.htag;
+                    if (__syncthreads_and(ok)) break;  // block-uniform
+                    if (it >= DEC_SPIN_LIMIT) {
+                        if (tid == 0) dec_fail(a.sync);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                constexpr int QPER = 16384 / 4 / DEC_THREADS;  // d_ff <= 16384
+                const uint32_t* qs = reinterpret_cast<const uint32_t*>(a.hq.q + (size_t)p0 * K);
+                uint32_t qv[QPER];
+#pragma unroll
+                for (int q = 0; q < QPER; ++q) {
+                    const int i = tid + q * DEC_THREADS;
+                    qv[q] = i < K / 4 ? __hip_atomic_load(qs + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+                }
+#pragma unroll
+                for (int q = 0; q < QPER; ++q) {
+                    const int i = tid + q * DEC_THREADS;
+                    if (i < K / 4) reinterpret_cast<uint32_t*>(smem)[i] = qv[q];
+                }
+                if (tid < KB) reinterpret_cast<uint64_t*>(smem + K)[tid] = sv & ~(uint64_t)DEC_HTAG_MASK;
+                __syncthreads();
+            },
+            [&](const typename Fmt<TD>::Raw& c, const typename Fmt<TD>::Raw&, int u) {
+                unit_accum<TD, 1>(c, A, u, h, 1, a.D.nkb, acc);
+            });
+        acc[0] += __shfl_xor(acc[0], 32, 64);
+        if (h == 0) red[wave][m] = acc[0];
+        __syncthreads();
+        if (wave == 0) {
+            float p = 0.0f;
+            if (a.out) {  // this slot's weight: the softmax of topk_token_wave, as in the tables
+                RouteArgs r = a.ra;
+                r.ids = nullptr;
+                r.probs = nullptr;
+                r.shscale = nullptr;
+                uint64_t msk[SMALL_GROUP_MAX_E / 64];
+                float myp = 0.0f;
+                const int myid = topk_token_wave<SMALL_GROUP_MAX_E / 64>(r, lg, 0, nullptr, msk, &myp);
+                for (int q = 0; q < a.k; ++q) {
+                    const int id = __shfl(myid, q, 64);
+                    const float pq = __shfl(myp, q, 64);
+                    if (id == e) p = pq;
+                }
+            }
+            if (h == 0) {
+                float s = 0.0f;
+#pragma unroll
+                for (int w = 0; w < DEC_THREADS / 64; ++w) s += red[w][m];
+                const int row = rt * 32 + m;
+                if (!(a.D.valid_rows && row >= a.D.valid_rows)) {
+                    if (a.out) atomicAdd(a.out + row, p * s);
+                    else a.y[(size_t)p0 * a.D.rows + row] = s;
+                }
+            }
+        }
+    };
+
     if (blk < E) {  // ---- router row blk
         float* lds = reinterpret_cast<float*>(smem);
         const int S = rs_stride(d), RS = 16 * S;
@@ -1481,81 +1557,10 @@ k_decode1(Decode1Args a) {
         return;
     }
 
-    {  // ---- down: row tile rt of one slot
-        const int b = blk - (E + 1 + ng), rt = b % a.D.nrt, slot = b / a.D.nrt;
+    {  // ---- down blocks
         if (wave == 0) dec_wait_logits(a, lg);
         __syncthreads();
-        const int4 rec = small_group(grp, slot);
-        const int e = rec.x, p0 = rec.y;
-        const int K = a.hq.K, KB = K / 32;
-        const ActLds A{smem, reinterpret_cast<const float2*>(smem + K), nullptr, K};
-        const int nu = n_units<TD>(a.D.nkb);
-        float acc[1] = {0.0f};
-        kloop<TD, 1>(
-            a.D, a.D, e, rt, wave, nu, DEC_THREADS / 64, m, h,
-            [&] {  // after the first two units' loads: wait until every scale word of the slot's h carries
-                   // this launch's tag (its quants were stored before it), then stage h
-                const uint64_t* ss = reinterpret_cast<const uint64_t*>(a.hq.s + (size_t)p0 * KB);
-                uint64_t sv = 0;
-                for (int it = 0;; ++it) {
-                    if (tid < KB) sv = __hip_atomic_load(ss + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    const bool ok = tid >= KB || ((uint32_t)sv & DEC_HTAG_MASK) == a.htag;
-                    if (__syncthreads_and(ok)) break;  // block-uniform
-                    if (it >= DEC_SPIN_LIMIT) {
-                        if (tid == 0) dec_fail(a.sync);
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(1);
-                }
-                constexpr int QPER = 16384 / 4 / DEC_THREADS;  // d_ff <= 16384
-                const uint32_t* qs = reinterpret_cast<const uint32_t*>(a.hq.q + (size_t)p0 * K);
-                uint32_t qv[QPER];
-#pragma unroll
-                for (int q = 0; q < QPER; ++q) {
-                    const int i = tid + q * DEC_THREADS;
-                    qv[q] = i < K / 4 ? __hip_atomic_load(qs + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
-                }
-#pragma unroll
-                for (int q = 0; q < QPER; ++q) {
-                    const int i = tid + q * DEC_THREADS;
-                    if (i < K / 4) reinterpret_cast<uint32_t*>(smem)[i] = qv[q];
-                }
-                if (tid < KB) reinterpret_cast<uint64_t*>(smem + K)[tid] = sv & ~(uint64_t)DEC_HTAG_MASK;
-                __syncthreads();
-            },
-            [&](const typename Fmt<TD>::Raw& c, const typename Fmt<TD>::Raw&, int u) {
-                unit_accum<TD, 1>(c, A, u, h, 1, a.D.nkb, acc);
-            });
-        acc[0] += __shfl_xor(acc[0], 32, 64);
-        if (h == 0) red[wave][m] = acc[0];
-        __syncthreads();
-        if (wave == 0) {
-            float p = 0.0f;
-            if (a.out) {  // this slot's weight: the softmax of topk_token_wave, as in the tables
-                RouteArgs r = a.ra;
-                r.ids = nullptr;
-                r.probs = nullptr;
-                r.shscale = nullptr;
-                uint64_t msk[SMALL_GROUP_MAX_E / 64];
-                float myp = 0.0f;
-                const int myid = topk_token_wave<SMALL_GROUP_MAX_E / 64>(r, lg, 0, nullptr, msk, &myp);
-                for (int q = 0; q < a.k; ++q) {
-                    const int id = __shfl(myid, q, 64);
-                    const float pq = __shfl(myp, q, 64);
-                    if (id == e) p = pq;
-                }
-            }
-            if (h == 0) {
-                float s = 0.0f;
-#pragma unroll
-                for (int w = 0; w < DEC_THREADS / 64; ++w) s += red[w][m];
-                const int row = rt * 32 + m;
-                if (!(a.D.valid_rows && row >= a.D.valid_rows)) {
-                    if (a.out) atomicAdd(a.out + row, p * s);
-                    else a.y[(size_t)p0 * a.D.rows + row] = s;
-                }
-            }
-        }
+        down_tile(blk - (E + 1 + ng));
     }
 }
 
@@ -1570,8 +1575,10 @@ bool decode1_fits(int gtype, int dtype, int d, int f, int E, int k) {
 
 // The fused launch pays where its gate/up blocks fit one per CU.  Larger gate/up phases leave the
 // down blocks to the slots the gate/up blocks free, unevenly (measured, Mixtral-shaped: 64 CUs run two
-// down blocks while 64 run none), and the separate launches are faster there.  Measured per step:
-// toy 15.9 -> 11.2 us, Qwen3-shaped 26.1 -> 24.9 us, Mixtral-shaped 46.1 -> 48.6 us (not taken).
+// down blocks while 64 run none).  Measured per step: toy 15.9 -> 11.2 us, Qwen3-shaped 26.1 -> 24.9
+// us, Mixtral-shaped 46.1 -> 48.6 us (not taken).
+// (Measured and dropped: a cooperative launch whose first gate/up blocks, one per CU, go on with the
+// down tiles, so that the down work is spread evenly: Mixtral-shaped 64 us per step.)
 bool decode1_pays(int gate_nrt, int k) { return gate_nrt * (k / 2) <= num_cus(); }
 
 void launch_decode1(const Decode1Args& a, int gtype, int dtype, hipStream_t st) {

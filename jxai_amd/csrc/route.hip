@@ -617,7 +617,69 @@ __global__ void __launch_bounds__(256) k_q8_to_acth(ActQ8 in, int rows, ActH out
     write_acth_row(in.q + row * in.K, in.s + row * (in.K / 32), in.K, out, row, threadIdx.x & 63, lo != 0);
 }
 
+__device__ __forceinline__ uint32_t comp4(const uint4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+
+// The hi-only form (the down GEMM's operand, no block-unit form) of Q8_0 rows, one wave per row:
+// every quant and scale load of the row is in flight before the first conversion (16 quants per lane
+// and chunk, NC chunks per lane), and the row exponent comes from the scales already loaded.  The
+// values are those of acth_chunk_v: fp16(dx * 2^-E * q), 2^E per half-unit, the min-term pieces of
+// dx * sum(q) * 2^-E.
+template <int NC>
+__global__ void __launch_bounds__(256) k_q8_to_acth_hi(ActQ8 in, int rows, ActH o) {
+    const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= (size_t)rows) return;  // wave-uniform
+    const int lane = threadIdx.x & 63, K = in.K, n16 = K / 16, KH = K / 128;
+    const int8_t* q = in.q + row * K;
+    const float2* sc = in.s + row * (K / 32);
+    uint4 qv[NC];
+    float2 sv[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int i = min(lane + 64 * c, n16 - 1);  // clamped duplicates are loaded, not stored
+        qv[c] = ld16(q + 16 * i);
+        sv[c] = sc[i >> 1];
+    }
+    float M = 0.0f;  // chunks 2b and 2b + 1 carry block b's scale, so this covers every block
+#pragma unroll
+    for (int c = 0; c < NC; ++c) M = fmaxf(M, sv[c].x);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    const int E = acth_exponent(M);
+    const float dn = __uint_as_float((uint32_t)(127 - E) << 23), up = __uint_as_float((uint32_t)(127 + E) << 23);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int i = lane + 64 * c;
+        if (i >= n16) break;
+        const int e = 16 * i, b = e >> 5, hh = e >> 7;
+        const float s = sv[c].x * dn;  // exact: power-of-two scaling
+        uint32_t hw[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const uint32_t word = comp4(qv[c], u >> 1);
+            const int q0 = (int)(int8_t)(word >> (16 * (u & 1))), q1 = (int)(int8_t)(word >> (16 * (u & 1) + 8));
+            const _Float16 h0 = (_Float16)(s * (float)q0), h1 = (_Float16)(s * (float)q1);  // products exact
+            hw[u] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+        }
+        uint4* hl = reinterpret_cast<uint4*>(o.hl + row * (size_t)KH * 256 + hh * 256 + (e & 127));
+        hl[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        hl[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+        if ((e & 127) == 0) o.pe[row * (size_t)KH + hh] = up;
+        if ((e & 31) == 0)  // exact: 11-bit scale x |sum| < 2^12, times 2^-E
+            store_pieces3(o.xm + row * (size_t)o.KU * 24 + (b / 8) * 24 + (b % 8), sv[c].x * sv[c].y * dn);
+    }
+}
+
 void launch_q8_to_acth(const ActQ8& in, int rows, ActH out, hipStream_t st, bool lo) {
+    const int nc = (in.K / 16 + 63) / 64;
+    if (!lo && !out.q16 && in.K % 128 == 0 && nc <= 16) {
+        const dim3 grid((rows + 3) / 4);
+        if (nc <= 1) hipLaunchKernelGGL(k_q8_to_acth_hi<1>, grid, dim3(256), 0, st, in, rows, out);
+        else if (nc <= 2) hipLaunchKernelGGL(k_q8_to_acth_hi<2>, grid, dim3(256), 0, st, in, rows, out);
+        else if (nc <= 4) hipLaunchKernelGGL(k_q8_to_acth_hi<4>, grid, dim3(256), 0, st, in, rows, out);
+        else if (nc <= 8) hipLaunchKernelGGL(k_q8_to_acth_hi<8>, grid, dim3(256), 0, st, in, rows, out);
+        else hipLaunchKernelGGL(k_q8_to_acth_hi<16>, grid, dim3(256), 0, st, in, rows, out);
+        return;
+    }
     hipLaunchKernelGGL(k_q8_to_acth, dim3((rows + 3) / 4), dim3(256), 0, st, in, rows, out, lo ? 1 : 0);
 }
 
