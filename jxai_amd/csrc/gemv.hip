@@ -1281,20 +1281,25 @@ static void down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, 
 }
 
 // ---------------------------------------------------------------- one-token step in one launch
-// A one-token decode step of a layer without a shared expert (even top-k, Q8_0 activations on both
-// sides) as one grid of 512-thread blocks, in index order:
-//   [0, E)     router rows: block r stages its row and the token chain-major in LDS, runs the
-//              vec_dot_f32 chain (as k_route_small) and publishes the logit as one device-coherent
-//              64-bit word (epoch << 32 | bits).  Block 0 first zeroes the folded combine's output.
-//   E          once every logit of this launch is out: the dispatch tables (topk_dispatch_wave) and
-//              the Q8_0 of x, for the caller.
-//   gate/up    row tile rt of slots 2s and 2s + 1, waves 0-3 and 4-7 each the 4-wave single-token
-//              gate/up GEMV: the Q8_0 of x is formed in LDS while the router runs, the slot's expert
-//              follows from the logits (small_group), and h's Q8_0 block is stored device-coherently,
-//              its quants first, then its scale word carrying the launch's tag.
-//   down       row tile rt of one slot, the 8-wave single-token down GEMV: its first weight units
-//              are in flight before it waits for every scale word of the slot's h to carry the tag;
-//              the quants are then read device-coherently.
+// A one-token decode step (even top-k, Q8_0 activations on both sides, a shared expert of the routed
+// formats or none) as one grid of 512-thread blocks, in index order:
+//   router     one block per router row (and the shared-expert gate row): the row and the token staged
+//              chain-major in LDS, the vec_dot_f32 chain (as k_route_small), the logit published as
+//              one device-coherent 64-bit word (epoch << 32 | bits).  Block 0 first zeroes the folded
+//              combine's output.
+//   tables     once every logit of this launch is out: the dispatch tables (topk_dispatch_wave,
+//              with the shared-expert gate) and the Q8_0 of x, for the caller.
+//   shared g/u two row tiles of the shared expert's gate/up per block (waves 0-3 and 4-7, each the
+//              4-wave single-token GEMV); they need no routing and stream from the start.
+//   gate/up    row tile rt of slots 2s and 2s + 1 likewise, each slot's expert from the published
+//              logits (small_group).  Every gate/up block forms the Q8_0 of x in LDS itself and
+//              stores its Q8_0 block of h device-coherently: the quants, then the scale word carrying
+//              the launch's tag.
+//   down       row tile rt of one routed slot, then of the shared expert: the 8-wave single-token down
+//              GEMV, its first weight units in flight before it waits for every scale word of its h to
+//              carry the tag; the quants are then read device-coherently.  Top-2 without a shared
+//              expert adds p * y into the output (the folded combine); otherwise y and ysh are
+//              written for launch_combine.
 // The arithmetic is that of the separate launches (same chains, quantization, unit order and
 // reductions), so the results are bit-identical to them.  A block waits only on blocks with smaller
 // indices, which the dispatcher starts first, so every wait ends; each is bounded anyway (giving up
@@ -1311,26 +1316,26 @@ __device__ __forceinline__ void dec_fail(DecodeSync* s) {
     __hip_atomic_store(&s->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Wave 0: wait until all E logits carry this launch's tag, then put them in lg (LDS); the caller
-// synchronizes the block.
-__device__ void dec_wait_logits(const Decode1Args& a, float* lg) {
+// Wave 0: wait until the first n logit words carry this launch's tag, then put the logits in lg
+// (LDS); the caller synchronizes the block.
+__device__ void dec_wait_logits(const Decode1Args& a, int n, float* lg) {
     const int lane = threadIdx.x & 63;
     for (int it = 0;; ++it) {
         uint64_t w0 = 0, w1 = 0;
         bool ok = true;
-        if (lane < a.E) {
+        if (lane < n) {
             w0 = __hip_atomic_load(a.sync->tag + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             ok = (uint32_t)(w0 >> 32) == a.epoch;
         }
-        if (64 + lane < a.E) {
+        if (64 + lane < n) {
             w1 = __hip_atomic_load(a.sync->tag + 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             ok = ok && (uint32_t)(w1 >> 32) == a.epoch;
         }
         const bool all = __all(ok);
         if (all || it >= DEC_SPIN_LIMIT) {
             if (!all && lane == 0) dec_fail(a.sync);
-            if (lane < a.E) lg[lane] = __uint_as_float((uint32_t)w0);
-            if (64 + lane < a.E) lg[64 + lane] = __uint_as_float((uint32_t)w1);
+            if (lane < n) lg[lane] = __uint_as_float((uint32_t)w0);
+            if (64 + lane < n) lg[64 + lane] = __uint_as_float((uint32_t)w1);
             return;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -1347,7 +1352,11 @@ k_decode1(Decode1Args a) {
     __shared__ float red[DEC_THREADS / 64][32];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 31, h = lane >> 5;
     const int E = a.E, d = a.d;
-    const int ng = a.G.nrt * (a.k / 2);  // gate/up blocks
+    const int R = E + (a.shgate ? 1 : 0);                       // router rows
+    const int ngs = a.sh ? (a.SG.nrt + 1) / 2 : 0;              // shared gate/up blocks
+    const int ng = a.G.nrt * (a.k / 2);                         // routed gate/up blocks
+    const int nd = a.D.nrt * a.k;                               // routed down blocks
+    const int b_sg = R + 1, b_gu = b_sg + ngs, b_dn = b_gu + ng, b_sd = b_dn + nd;
     const int blk = blockIdx.x;
     Groups grp;  // the slot records follow from the logits (small_group)
     grp.logits = lg;
@@ -1355,20 +1364,57 @@ k_decode1(Decode1Args a) {
     grp.top_k = a.k;
     grp.n_tok = 1;
 
-    // down row tile bd % D.nrt of slot bd / D.nrt, the logits in lg
-    auto down_tile = [&](int bd) {
-        const int rt = bd % a.D.nrt, slot = bd / a.D.nrt;
-        const int4 rec = small_group(grp, slot);
-        const int e = rec.x, p0 = rec.y;
-        const int K = a.hq.K, KB = K / 32;
+    // One gate/up row tile per half (waves 0-3, 4-7): expert e's rows 32 rt.. of Wg / Wu against the
+    // Q8_0 of x in LDS; SwiGLU and h's Q8_0 block into row p0 of hout, device-coherently, the tagged
+    // scale last.  An inactive half loads the pad and stores nothing (both halves meet every barrier).
+    auto gateup_tile = [&](const QMat& Wg, const QMat& Wu, int e, int rt, int p0, const ActQ8& hout, bool active) {
+        const int half = wave >> 2, lw = wave & 3, mat = lw >> 1, kw = lw & 1;
+        const ActLds A{smem, reinterpret_cast<const float2*>(smem + d), nullptr, d};
+        const QMat& W = mat ? Wu : Wg;
+        const int nu = active ? n_units<TG>(Wg.nkb) : 0;
+        float acc[1] = {0.0f};
+        kloop<TG, 1>(
+            W, W, e, rt, kw, nu, 2, m, h, [] {},
+            [&](const typename Fmt<TG>::Raw& c, const typename Fmt<TG>::Raw&, int u) {
+                unit_accum<TG, 1>(c, A, u, h, 1, Wg.nkb, acc);
+            });
+        acc[0] += __shfl_xor(acc[0], 32, 64);
+        if (h == 0) red[wave][m] = acc[0];
+        __syncthreads();
+        if (lw == 0 && active) {  // waves 0 and 4: SwiGLU and the Q8_0 block of h (as k_gemv_gateup)
+            float gv = 0.0f, uv = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+                gv += red[4 * half + w][m];
+                uv += red[4 * half + 2 + w][m];
+            }
+            float2 sv;
+            const int q = q8_block_vals(gated(gv, uv, Wg.act), sv);
+            const uint32_t q1 = (uint32_t)__shfl_down(q, 1, 64), q2 = (uint32_t)__shfl_down(q, 2, 64),
+                           q3 = (uint32_t)__shfl_down(q, 3, 64);
+            const uint32_t word = ((uint32_t)q & 0xFFu) | ((q1 & 0xFFu) << 8) | ((q2 & 0xFFu) << 16) | (q3 << 24);
+            if (h == 0 && (m & 3) == 0)
+                __hip_atomic_store(reinterpret_cast<uint32_t*>(hout.q + (size_t)p0 * hout.K + rt * 32 + m), word,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the quants are out before the tagged scale
+            if (lane == 0)
+                __hip_atomic_store(reinterpret_cast<uint64_t*>(hout.s + (size_t)p0 * (hout.K / 32) + rt),
+                                   ((uint64_t)__float_as_uint(sv.y) << 32) | __float_as_uint(sv.x) | a.htag,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    };
+
+    // Down row tile rt of expert e of Wd against row p0 of hin (once every scale word of that row
+    // carries this launch's tag): y_out[row] = s, or p * s added into the output (folded combine).
+    auto down_tile = [&](const QMat& Wd, int e, int rt, int p0, const ActQ8& hin, float* y_out, float p) {
+        const int K = hin.K, KB = K / 32;
         const ActLds A{smem, reinterpret_cast<const float2*>(smem + K), nullptr, K};
-        const int nu = n_units<TD>(a.D.nkb);
+        const int nu = n_units<TD>(Wd.nkb);
         float acc[1] = {0.0f};
         kloop<TD, 1>(
-            a.D, a.D, e, rt, wave, nu, DEC_THREADS / 64, m, h,
-            [&] {  // after the first two units' loads: wait until every scale word of the slot's h carries
-                   // this launch's tag (its quants were stored before it), then stage h
-                const uint64_t* ss = reinterpret_cast<const uint64_t*>(a.hq.s + (size_t)p0 * KB);
+            Wd, Wd, e, rt, wave, nu, DEC_THREADS / 64, m, h,
+            [&] {  // after the first two units' loads: wait for the tags, then stage h
+                const uint64_t* ss = reinterpret_cast<const uint64_t*>(hin.s + (size_t)p0 * KB);
                 uint64_t sv = 0;
                 for (int it = 0;; ++it) {
                     if (tid < KB) sv = __hip_atomic_load(ss + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1381,7 +1427,7 @@ k_decode1(Decode1Args a) {
                     __builtin_amdgcn_s_sleep(1);
                 }
                 constexpr int QPER = 16384 / 4 / DEC_THREADS;  // d_ff <= 16384
-                const uint32_t* qs = reinterpret_cast<const uint32_t*>(a.hq.q + (size_t)p0 * K);
+                const uint32_t* qs = reinterpret_cast<const uint32_t*>(hin.q + (size_t)p0 * K);
                 uint32_t qv[QPER];
 #pragma unroll
                 for (int q = 0; q < QPER; ++q) {
@@ -1397,41 +1443,48 @@ k_decode1(Decode1Args a) {
                 __syncthreads();
             },
             [&](const typename Fmt<TD>::Raw& c, const typename Fmt<TD>::Raw&, int u) {
-                unit_accum<TD, 1>(c, A, u, h, 1, a.D.nkb, acc);
+                unit_accum<TD, 1>(c, A, u, h, 1, Wd.nkb, acc);
             });
         acc[0] += __shfl_xor(acc[0], 32, 64);
         if (h == 0) red[wave][m] = acc[0];
         __syncthreads();
-        if (wave == 0) {
-            float p = 0.0f;
-            if (a.out) {  // this slot's weight: the softmax of topk_token_wave, as in the tables
-                RouteArgs r = a.ra;
-                r.ids = nullptr;
-                r.probs = nullptr;
-                r.shscale = nullptr;
-                uint64_t msk[SMALL_GROUP_MAX_E / 64];
-                float myp = 0.0f;
-                const int myid = topk_token_wave<SMALL_GROUP_MAX_E / 64>(r, lg, 0, nullptr, msk, &myp);
-                for (int q = 0; q < a.k; ++q) {
-                    const int id = __shfl(myid, q, 64);
-                    const float pq = __shfl(myp, q, 64);
-                    if (id == e) p = pq;
-                }
-            }
-            if (h == 0) {
-                float s = 0.0f;
+        if (wave == 0 && h == 0) {
+            float s = 0.0f;
 #pragma unroll
-                for (int w = 0; w < DEC_THREADS / 64; ++w) s += red[w][m];
-                const int row = rt * 32 + m;
-                if (!(a.D.valid_rows && row >= a.D.valid_rows)) {
-                    if (a.out) atomicAdd(a.out + row, p * s);
-                    else a.y[(size_t)p0 * a.D.rows + row] = s;
-                }
+            for (int w = 0; w < DEC_THREADS / 64; ++w) s += red[w][m];
+            const int row = rt * 32 + m;
+            if (!(Wd.valid_rows && row >= Wd.valid_rows)) {
+                if (y_out) y_out[row] = s;
+                else atomicAdd(a.out + row, p * s);
             }
         }
     };
 
-    if (blk < E) {  // ---- router row blk
+    // Q8_0 of x into LDS (the gate/up blocks' activations), one 32-block per half-wave and step, as
+    // the router kernels form it
+    auto quantize_x = [&] {
+        int8_t* xq = smem;
+        float2* xs = reinterpret_cast<float2*>(smem + d);
+        constexpr int XPER = 8192 / 32 / (2 * DEC_THREADS / 64);  // d <= 8192
+        const int KB = d / 32, hw = 2 * wave + h;
+        float xv[XPER];
+#pragma unroll
+        for (int q = 0; q < XPER; ++q) {
+            const int bb = hw + q * (2 * DEC_THREADS / 64);
+            xv[q] = bb < KB ? a.x[bb * 32 + m] : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < XPER; ++q) {
+            const int bb = hw + q * (2 * DEC_THREADS / 64);
+            if (bb < KB) {  // half-wave uniform
+                float2 sv;
+                xq[bb * 32 + m] = (int8_t)q8_block_vals(xv[q], sv);
+                if (m == 0) xs[bb] = sv;
+            }
+        }
+    };
+
+    if (blk < R) {  // ---- router row blk (row E: the shared-expert gate, fp32 order)
         float* lds = reinterpret_cast<float*>(smem);
         const int S = rs_stride(d), RS = 16 * S;
         if (blk == 0 && a.out) {  // the folded combine's output starts at zero
@@ -1439,6 +1492,7 @@ k_decode1(Decode1Args a) {
                 __hip_atomic_store(reinterpret_cast<uint32_t*>(a.out) + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // complete before the logit is out
         }
+        const float* wrow = blk < E ? a.router + (size_t)blk * d : a.shgate;
         {  // row + token -> LDS, chain-major, every load in flight before the first store
             constexpr int PER = 2 * 8192 / 4 / DEC_THREADS;  // d <= 8192
             const int c4 = d / 4, tot = 2 * c4;
@@ -1448,7 +1502,7 @@ k_decode1(Decode1Args a) {
                 const int i = tid + q * DEC_THREADS;
                 if (i >= tot) break;
                 const int row = i / c4, c = i - row * c4;
-                v[q] = *reinterpret_cast<const float4*>((row == 0 ? a.router + (size_t)blk * d : a.x) + 4 * c);
+                v[q] = *reinterpret_cast<const float4*>((row == 0 ? wrow : a.x) + 4 * c);
             }
 #pragma unroll
             for (int q = 0; q < PER; ++q) {
@@ -1464,11 +1518,11 @@ k_decode1(Decode1Args a) {
         }
         __syncthreads();
         if (wave == 0 && lane < 16) {
-            const bool c8 = a.chain8 != 0;
+            const bool c8 = a.chain8 != 0 && blk < E;
             const float s = chain_sum(chain_dot_lds(lds, lds + RS, S, d, lane, c8), c8);
             if (lane == 0) {
-                const float l = a.bias ? s + a.bias[blk] : s;
-                a.ra.logits[blk] = l;
+                const float l = (blk < E && a.bias) ? s + a.bias[blk] : s;
+                if (blk < E) a.ra.logits[blk] = l;
                 __hip_atomic_store(a.sync->tag + blk, ((uint64_t)a.epoch << 32) | __float_as_uint(l), __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
             }
@@ -1476,11 +1530,11 @@ k_decode1(Decode1Args a) {
         return;
     }
 
-    if (blk == E) {  // ---- the caller's dispatch tables and Q8_0 of x
-        if (wave == 0) dec_wait_logits(a, lg);
+    if (blk == R) {  // ---- the caller's dispatch tables and Q8_0 of x
+        if (wave == 0) dec_wait_logits(a, R, lg);
         __syncthreads();
         if (wave == 0) {
-            topk_dispatch_wave<SMALL_GROUP_MAX_E / 64>(a.ra, a.o, lg, nullptr);
+            topk_dispatch_wave<SMALL_GROUP_MAX_E / 64>(a.ra, a.o, lg, a.shgate ? lg + E : nullptr);
         } else {
             const int nb = d / 32, hw = 2 * (wave - 1) + h;
             for (int b = hw; b < nb; b += 2 * (DEC_THREADS / 64 - 1)) {  // half-wave uniform
@@ -1492,85 +1546,59 @@ k_decode1(Decode1Args a) {
         return;
     }
 
-    if (blk < E + 1 + ng) {  // ---- gate/up: row tile rt of slots 2 sp, 2 sp + 1
-        const int b = blk - (E + 1), rt = b % a.G.nrt, sp = b / a.G.nrt;
-        const int half = wave >> 2, lw = wave & 3, mat = lw >> 1, kw = lw & 1, slot = 2 * sp + half;
-        const int K = d, KB = K / 32;
-        int8_t* xq = smem;                                     // [K] quants
-        float2* xs = reinterpret_cast<float2*>(smem + K);      // [K / 32] (scale, sum)
-        {  // Q8_0 of x while the router runs, one 32-block per half-wave and step (as the router kernels)
-            constexpr int XPER = 8192 / 32 / (2 * DEC_THREADS / 64);  // d <= 8192
-            const int hw = 2 * wave + h;
-            float xv[XPER];
-#pragma unroll
-            for (int q = 0; q < XPER; ++q) {
-                const int bb = hw + q * (2 * DEC_THREADS / 64);
-                xv[q] = bb < KB ? a.x[bb * 32 + m] : 0.0f;
-            }
-#pragma unroll
-            for (int q = 0; q < XPER; ++q) {
-                const int bb = hw + q * (2 * DEC_THREADS / 64);
-                if (bb < KB) {  // half-wave uniform
-                    float2 sv;
-                    xq[bb * 32 + m] = (int8_t)q8_block_vals(xv[q], sv);
-                    if (m == 0) xs[bb] = sv;
-                }
-            }
-        }
-        if (wave == 0) dec_wait_logits(a, lg);
-        __syncthreads();  // the logits and the Q8_0 of x
-        const int4 rec = small_group(grp, slot);
-        const int e = rec.x, p0 = rec.y;
-        const ActLds A{xq, xs, nullptr, K};
-        const QMat& W = mat ? a.U : a.G;
-        const int nu = n_units<TG>(a.G.nkb);
-        float acc[1] = {0.0f};
-        kloop<TG, 1>(
-            W, W, e, rt, kw, nu, 2, m, h, [] {},
-            [&](const typename Fmt<TG>::Raw& c, const typename Fmt<TG>::Raw&, int u) {
-                unit_accum<TG, 1>(c, A, u, h, 1, a.G.nkb, acc);
-            });
-        acc[0] += __shfl_xor(acc[0], 32, 64);
-        if (h == 0) red[wave][m] = acc[0];
+    if (blk < b_gu) {  // ---- shared gate/up: row tiles 2 b, 2 b + 1
+        const int rt = 2 * (blk - b_sg) + (wave >> 2);
+        quantize_x();
         __syncthreads();
-        if (lw == 0) {  // waves 0 and 4: SwiGLU and the Q8_0 block of h (as k_gemv_gateup)
-            float gv = 0.0f, uv = 0.0f;
-#pragma unroll
-            for (int w = 0; w < 2; ++w) {
-                gv += red[4 * half + w][m];
-                uv += red[4 * half + 2 + w][m];
-            }
-            float2 sv;
-            const int q = q8_block_vals(gated(gv, uv, a.G.act), sv);
-            const uint32_t q1 = (uint32_t)__shfl_down(q, 1, 64), q2 = (uint32_t)__shfl_down(q, 2, 64),
-                           q3 = (uint32_t)__shfl_down(q, 3, 64);
-            const uint32_t word = ((uint32_t)q & 0xFFu) | ((q1 & 0xFFu) << 8) | ((q2 & 0xFFu) << 16) | (q3 << 24);
-            if (h == 0 && (m & 3) == 0)
-                __hip_atomic_store(reinterpret_cast<uint32_t*>(a.hq.q + (size_t)p0 * a.hq.K + rt * 32 + m), word,
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the quants are out before the tagged scale
-            if (lane == 0)
-                __hip_atomic_store(reinterpret_cast<uint64_t*>(a.hq.s + (size_t)p0 * (a.hq.K / 32) + rt),
-                                   ((uint64_t)__float_as_uint(sv.y) << 32) | __float_as_uint(sv.x) | a.htag,
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        gateup_tile(a.SG, a.SU, 0, rt < a.SG.nrt ? rt : 0, 0, a.hqs, rt < a.SG.nrt);
         return;
     }
 
-    {  // ---- down blocks
-        if (wave == 0) dec_wait_logits(a, lg);
-        __syncthreads();
-        down_tile(blk - (E + 1 + ng));
+    if (blk < b_dn) {  // ---- routed gate/up: row tile rt of slots 2 sp, 2 sp + 1
+        const int b = blk - b_gu, rt = b % a.G.nrt, sp = b / a.G.nrt;
+        quantize_x();  // while the router runs
+        if (wave == 0) dec_wait_logits(a, E, lg);
+        __syncthreads();  // the logits and the Q8_0 of x
+        const int4 rec = small_group(grp, 2 * sp + (wave >> 2));
+        gateup_tile(a.G, a.U, rec.x, rt, rec.y, a.hq, true);
+        return;
     }
+
+    if (blk < b_sd) {  // ---- routed down: row tile rt of one slot
+        const int b = blk - b_dn, rt = b % a.D.nrt, slot = b / a.D.nrt;
+        if (wave == 0) dec_wait_logits(a, E, lg);
+        __syncthreads();
+        const int4 rec = small_group(grp, slot);
+        float p = 0.0f;
+        if (a.out) {  // this slot's weight: the softmax of topk_token_wave, as in the tables
+            RouteArgs r = a.ra;
+            r.ids = nullptr;
+            r.probs = nullptr;
+            r.shscale = nullptr;
+            uint64_t msk[SMALL_GROUP_MAX_E / 64];
+            float myp = 0.0f;
+            const int myid = topk_token_wave<SMALL_GROUP_MAX_E / 64>(r, lg, 0, nullptr, msk, &myp);
+            for (int q = 0; q < a.k; ++q) {
+                const int id = __shfl(myid, q, 64);
+                const float pq = __shfl(myp, q, 64);
+                if (id == rec.x) p = pq;
+            }
+        }
+        down_tile(a.D, rec.x, rt, rec.y, a.hq, a.out ? nullptr : a.y + (size_t)rec.y * a.D.rows, p);
+        return;
+    }
+
+    // ---- shared down: row tile rt
+    down_tile(a.SD, 0, blk - b_sd, 0, a.hqs, a.ysh, 0.0f);
 }
 
 static bool fmt_q8(int t) { return t == T_Q4_0 || t == T_Q8_0 || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
 
-bool decode1_fits(int gtype, int dtype, int d, int f, int E, int k) {
+bool decode1_fits(int gtype, int dtype, int d, int f, int E, int k, int fs, bool shgate) {
     // built: one format on both sides, or a K-quant gate/up with a Q6_K down (the _M mixes)
     const bool built = fmt_q8(gtype) && (gtype == dtype || ((gtype == T_Q4_K || gtype == T_Q5_K) && dtype == T_Q6_K));
-    return built && E >= 1 && E <= SMALL_GROUP_MAX_E && k >= 2 && k % 2 == 0 && k <= MAX_SLOTS_DEC && k <= E &&
-           d % 32 == 0 && d <= 8192 && f % 32 == 0 && f <= 16384;
+    return built && E >= 1 && E + (shgate ? 1 : 0) <= SMALL_GROUP_MAX_E && k >= 2 && k % 2 == 0 && k <= MAX_SLOTS_DEC && k <= E &&
+           d % 32 == 0 && d <= 8192 && f % 32 == 0 && f <= 16384 && fs % 32 == 0 && fs <= 16384;
 }
 
 // The fused launch pays where its gate/up blocks fit one per CU.  Larger gate/up phases leave the
@@ -1579,13 +1607,16 @@ bool decode1_fits(int gtype, int dtype, int d, int f, int E, int k) {
 // us, Mixtral-shaped 46.1 -> 48.6 us (not taken).
 // (Measured and dropped: a cooperative launch whose first gate/up blocks, one per CU, go on with the
 // down tiles, so that the down work is spread evenly: Mixtral-shaped 64 us per step.)
-bool decode1_pays(int gate_nrt, int k) { return gate_nrt * (k / 2) <= num_cus(); }
+bool decode1_pays(int gate_nrt, int k, int sgate_nrt) {
+    return gate_nrt * (k / 2) + (sgate_nrt + 1) / 2 <= num_cus();
+}
 
 void launch_decode1(const Decode1Args& a, int gtype, int dtype, hipStream_t st) {
-    const dim3 grid(a.E + 1 + a.G.nrt * (a.k / 2) + a.D.nrt * a.k);
+    const dim3 grid(a.E + (a.shgate ? 1 : 0) + 1 + (a.sh ? (a.SG.nrt + 1) / 2 + a.SD.nrt : 0) +
+                    a.G.nrt * (a.k / 2) + a.D.nrt * a.k);
     // LDS: router row + token chain-major, or a gate/up's Q8_0 of x, or a down's Q8_0 of h
-    const size_t lds = std::max({(size_t)2 * 16 * rs_stride(a.d) * sizeof(float),
-                                 act_lds_bytes(1, a.d, false), act_lds_bytes(1, a.hq.K, false)});
+    const size_t lds = std::max({(size_t)2 * 16 * rs_stride(a.d) * sizeof(float), act_lds_bytes(1, a.d, false),
+                                 act_lds_bytes(1, a.hq.K, false), act_lds_bytes(1, a.sh ? a.hqs.K : 0, false)});
     auto go = [&](auto kern) {
         lds_optin(kern, lds);
         hipLaunchKernelGGL(kern, grid, dim3(DEC_THREADS), lds, st, a);

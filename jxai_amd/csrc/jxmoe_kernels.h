@@ -264,12 +264,20 @@ struct Decode1Args {
     DecodeSync* sync = nullptr;
     uint32_t epoch = 0;         // this launch's number among the layer's fused launches (from 1)
     uint32_t htag = 0;          // 1 + epoch % 8191: the tag in the low 13 bits of h's stored scales
+    int sh = 0;                 // a shared expert of the routed formats:
+    QMat SG, SU, SD;            //   its gate, up (d_ff_shared x d) and down (d x d_ff_shared)
+    const float* shgate = nullptr;  // [d] its fp32 gate row (sigmoid weight), or null (weight 1)
+    ActQ8 hqs;                  //   [1][d_ff_shared] Q8_0 of its h
+    float* ysh = nullptr;       //   [d] its output, for launch_combine
 };
-// Whether k_decode1 is built for this shape: E <= SMALL_GROUP_MAX_E, even k <= MAX_SLOTS_DEC,
-// d % 32 == 0 and d <= 8192, d_ff <= 16384, gate/up and down formats with Q8_0 activations.
-bool decode1_fits(int gtype, int dtype, int d, int f, int E, int k);
-// Whether the fused launch is the faster one for gate/up matrices of gate_nrt row tiles at top-k.
-bool decode1_pays(int gate_nrt, int k);
+// Whether k_decode1 is built for this shape: E router rows (+ the shared-expert gate row) <=
+// SMALL_GROUP_MAX_E, even k <= MAX_SLOTS_DEC, d % 32 == 0 and d <= 8192, d_ff and the shared d_ff
+// (fs, 0: none) <= 16384, gate/up and down formats with Q8_0 activations (a shared expert: the same
+// formats as the routed ones).
+bool decode1_fits(int gtype, int dtype, int d, int f, int E, int k, int fs, bool shgate);
+// Whether the fused launch is the faster one for routed gate/up matrices of gate_nrt row tiles at
+// top-k and a shared gate/up of sgate_nrt (0: none).
+bool decode1_pays(int gate_nrt, int k, int sgate_nrt);
 void launch_decode1(const Decode1Args& a, int gtype, int dtype, hipStream_t st);
 
 // Q8_0 of rows x K fp32 (row-major, K % 32 == 0).

@@ -472,6 +472,22 @@ constexpr int MFMA_MIN_PAIRS_PER_EXPERT_Q4_LARGE = 16;
 constexpr int MFMA_MIN_PAIRS_PER_EXPERT_Q8 = 4;
 constexpr size_t LARGE_EXPERT_ELEMS = (size_t)1 << 25;  // d * d_ff per matrix
 
+// Whether a call takes the fused one-token launch (k_decode1), apart from stream capture: one token in
+// the GEMV regime, Q8_0 activations on both sides, a shared expert (if any) in the routed formats, a
+// shape the kernel is built for, and one where it measured faster (or JX_FUSED=1).
+bool decode1_wanted(const jx_moe_layer* L, int n, uint32_t flags) {
+    if (n != 1 || !L->fused_decode || (flags & (JX_FWD_UNFUSED | JX_FWD_FORCE_MFMA))) return false;
+    if (L->gu_f32 || L->down_f32 || L->up.m.type != L->gate.m.type) return false;
+    if (L->shared && (L->sgu_f32 || L->sdown_f32 || L->sgate.m.type != L->gate.m.type ||
+                      L->sup.m.type != L->gate.m.type || L->sdown.m.type != L->down.m.type))
+        return false;
+    if (L->E > jx::SMALL_GROUP_MAX_E || !jx::route_small_fits(1, L->d, L->E)) return false;
+    if (!jx::decode1_fits(L->gate.m.type, L->down.m.type, L->d, L->F, L->E, L->k, L->shared ? L->Fs : 0,
+                          L->shgate != nullptr))
+        return false;
+    return L->force_fused || jx::decode1_pays(L->gate.m.nrt, L->k, L->shared ? L->sgate.m.nrt : 0);
+}
+
 int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStream_t st, uint32_t flags) {
     const int E = L->E, k = L->k, d = L->d;
     // the residual-stream form: x_norm = rms_norm(x, ffn_norm) feeds the router; x is added back in the combine
@@ -538,11 +554,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     // one token, no shared expert: router, gate/up and down (and the folded combine) in one launch
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     HIPCHK(hipStreamIsCapturing(st, &cap));
-    L->dec_used = n == 1 && small_logits && !L->shared && L->fused_decode && !(flags & JX_FWD_UNFUSED) &&
-                  cap == hipStreamCaptureStatusNone && !L->gu_f32 && !L->down_f32 && tb == 1 &&
-                  L->up.m.type == L->gate.m.type &&
-                  jx::decode1_fits(L->gate.m.type, L->down.m.type, d, L->F, E, k) &&
-                  (L->force_fused || jx::decode1_pays(L->gate.m.nrt, k));
+    L->dec_used = small_logits && tb == 1 && cap == hipStreamCaptureStatusNone && decode1_wanted(L, n, flags);
     if (L->dec_used) {
         if (++L->dec_epoch == 0) {  // 2^32 launches: start the counts over
             HIPCHK(hipMemsetAsync(L->dsync, 0, sizeof(jx::DecodeSync), st));
@@ -570,14 +582,23 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         a.sync = L->dsync;
         a.epoch = L->dec_epoch;
         a.htag = 1u + L->dec_epoch % 8191u;  // never 0, the low bits of every untagged scale
+        if (L->shared) {
+            a.sh = 1;
+            a.SG = L->sgate.m;
+            a.SU = L->sup.m;
+            a.SD = L->sdown.m;
+            a.shgate = L->shgate;
+            a.hqs = L->hqs;
+            a.ysh = L->ysh;
+        }
         {
             Launch l(L, fold ? "decode_fused" : "decode_fused_y", st);
             jx::launch_decode1(a, L->gate.m.type, L->down.m.type, st);
         }
         if (!fold) {
             Launch l(L, "combine", st);
-            jx::launch_combine(n, d, k, L->probs, L->pos_of, L->y, nullptr, L->shscale, outdev, st,
-                               resid ? xres : nullptr, resid ? L->post_norm : nullptr, L->eps);
+            jx::launch_combine(n, d, k, L->probs, L->pos_of, L->y, L->shared ? L->ysh : nullptr, L->shscale, outdev,
+                               st, resid ? xres : nullptr, resid ? L->post_norm : nullptr, L->eps);
         }
         HIPCHK(hipGetLastError());
         return JX_OK;
@@ -947,7 +968,9 @@ int jx_moe_forward(jx_moe_layer* L, const float* x, int32_t n_tok, float* out, i
     // Graphs pay off where launch overhead is a large share of the step: batches up to GRAPH_MAX_N
     // tokens (decode and batched decode).  Larger batches (prefill: milliseconds of GEMM, and a new
     // length per prompt) launch directly instead of capturing a graph for every length.
-    if (L->use_graphs && !L->prof.on && cap == hipStreamCaptureStatusNone && n_tok <= jx_moe_layer::GRAPH_MAX_N) {
+    // (the fused one-token launch is one kernel: nothing for a graph to save)
+    if (L->use_graphs && !L->prof.on && cap == hipStreamCaptureStatusNone && n_tok <= jx_moe_layer::GRAPH_MAX_N &&
+        !decode1_wanted(L, n_tok, flags)) {
         // the launch sequence depends only on (n, buffers, regime flags): replay a captured graph
         const jx_moe_layer::GraphKey key{n_tok, xin, outp,
                                          flags & (JX_FWD_FORCE_GEMV | JX_FWD_FORCE_MFMA | JX_FWD_RESIDUAL)};

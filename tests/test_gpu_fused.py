@@ -24,10 +24,17 @@ EXTRA = {
     "mixtral_norm": synth.LayerConfig("mixtral_norm", 4096, 8, 2, 1024, F.Q4_K, norms=True),
     # top-4 without a shared expert: two gate/up block pairs, the combine after the fused launch
     "toy_k4": synth.LayerConfig("toy_k4", 512, 16, 4, 768, F.Q8_0),
+    # shared experts: GELU gate with a sigmoid-gated shared expert, and the residual-stream form
+    "gelu_q4k": synth.LayerConfig("gelu_q4k", 512, 8, 2, 768, F.Q4_K, d_ff_shared=512, shared_gate=True, act=1),
+    "qwen15_norm": synth.LayerConfig("qwen15_norm", 512, 12, 4, 384, F.Q4_0, d_ff_shared=768, shared_gate=True,
+                                     norms=True),
+    # a shared expert without a gate (weight 1) and of an odd row-tile count (17: one shared gate/up
+    # block runs a single tile)
+    "toy_sh_nogate": synth.LayerConfig("toy_sh_nogate", 512, 8, 2, 1024, F.Q8_0, d_ff_shared=544),
 }
 
-FUSED = ["toy", "toy_gelu", "toy_f16r", "toy_q5k", "toy_q6k", "toy_k4", "qwen3moe", "mixtral_norm", "mixtral",
-         "mixtral_q6k"]
+FUSED = ["toy", "toy_gelu", "toy_f16r", "toy_q5k", "toy_q6k", "toy_k4", "qwen3moe", "gelu_q4k", "qwen15_norm",
+         "toy_sh_nogate", "toy_bf16r_sh", "qwen15moe", "mixtral_norm", "mixtral", "mixtral_q6k"]
 
 
 @pytest.fixture(scope="module")
@@ -94,7 +101,7 @@ def test_fused_step_matches_separate_launches(moe, port, name):
     L.close()
 
 
-@pytest.mark.parametrize("name", ["toy", "mixtral"])
+@pytest.mark.parametrize("name", ["toy", "qwen15moe", "mixtral"])
 def test_fused_steps_back_to_back(moe, name):
     """Hundreds of fused launches queued without host synchronization (the launch count, and with
     it the tags of the logits and of h's scales, advances every step), then the last outputs against
