@@ -556,7 +556,11 @@ __device__ __forceinline__ void unit_accum_f32(const typename Fmt<TYPE>::Raw& c,
 // With router logits instead of tables (few-token decode), every wave derives
 // the record itself.
 __device__ __forceinline__ int4 group_of(const Groups& g, int slot) {
-    if (g.identity) return make_int4(0, 0, slot == 0 ? g.n_tok : 0, 0);
+    if (g.identity) {
+        if (!g.chunk) return make_int4(0, 0, slot == 0 ? g.n_tok : 0, 0);
+        const int p = slot * g.chunk;
+        return make_int4(0, p, max(0, min(g.chunk, g.n_tok - p)), p);
+    }
     if (g.logits) return small_group(g, slot);
     return g.slots[slot];
 }

@@ -113,7 +113,8 @@ struct Groups {
     const int4* tiles = nullptr;  // [T] (expert, first pair, pair count, 0) MFMA tiles
     const int* n_tiles = nullptr; // [1]
     int top_k = 1;
-    int identity = 0;             // shared expert: pair p is token p, one group of n_tok
+    int identity = 0;             // shared expert: pair p is token p, one group of n_tok (chunk 0) or
+    int chunk = 0;                // groups of `chunk` tokens, group s from token s * chunk
     int n_tok = 0;
     // Few-token decode (n_tok <= ROUTE_SMALL_MAX_N, n_experts <= SMALL_GROUP_MAX_E): when set,
     // each block derives its slot's group from the router logits [n_tok][n_experts] itself

@@ -302,6 +302,7 @@ struct jx_moe_layer {
     uint32_t dec_epoch = 0;
     bool fused_decode = true;
     bool force_fused = false;  // JX_FUSED=1: also where the separate launches measured faster
+    int smfma_min = jx::MFMA_MIN_SHARED_TOKENS;  // JX_SMFMA_MIN: shared expert's GEMM threshold (A/B)
     bool dec_used = false;     // the last forward took the fused launch
 };
 
@@ -518,7 +519,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     auto dn_gemm = [&](const DevMat& D, int f, bool f32) { return down_h_k(D.m.type, f, f32) % 128 == 0 && ready(D); };
     const bool mfma_gu = mfma && gu_gemm(L->gate, L->up, L->gu_f32);
     const bool dn_shape = dn_gemm(L->down, L->F, L->down_f32);
-    const bool smfma = L->shared && n >= jx::MFMA_MIN_SHARED_TOKENS && !(flags & JX_FWD_FORCE_GEMV);
+    const bool smfma = L->shared && n >= L->smfma_min && !(flags & JX_FWD_FORCE_GEMV);
     const bool smfma_gu = smfma && gu_gemm(L->sgate, L->sup, L->sgu_f32);
     const bool smfma_dn = smfma && dn_gemm(L->sdown, L->Fs, L->sdown_f32);
     mfma = mfma && (mfma_gu || dn_shape);
@@ -651,6 +652,11 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         sg.identity = 1;
         sg.n_tok = n;
         sg.top_k = 1;
+        // the GEMVs' 16-token form: one group per 16 tokens, so the dense expert's row tiles spread
+        // over n / 16 times as many blocks as one group of all tokens (which each block streams pass
+        // by pass)
+        const int sslots = tbs == 16 ? (n + 15) / 16 : 1;
+        if (tbs == 16) sg.chunk = 16;
         const size_t fspad = ((size_t)L->Fs + 255) / 256 * 256;
         const int st_ub = (n + jx::MFMA_BN - 1) / jx::MFMA_BN;
         if (smfma_gu) {
@@ -659,7 +665,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
                                    L->sdown_f32 ? L->hfs : nullptr, ss);
         } else {
             Launch l(L, "shared_gateup_gemv", ss);
-            jx::launch_gemv_gateup(L->sgate.m, L->sup.m, L->xq, sg, 1, tbs, L->hqs, L->sdown_f32 ? L->hfs : nullptr, ss,
+            jx::launch_gemv_gateup(L->sgate.m, L->sup.m, L->xq, sg, sslots, tbs, L->hqs, L->sdown_f32 ? L->hfs : nullptr, ss,
                                    nullptr, L->sgu_f32 ? L->xf : nullptr, L->dpad);
         }
         if (smfma_dn) {
@@ -671,7 +677,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
             jx::launch_mfma_down(L->sdown.m, L->hhs.a, sg, st_ub, L->ysh, ss);
         } else {
             Launch l(L, "shared_down", ss);
-            jx::launch_gemv_down(L->sdown.m, L->hqs, L->sdown_f32 ? L->hfs : nullptr, (int)fspad, sg, 1, tbs, L->ysh,
+            jx::launch_gemv_down(L->sdown.m, L->hqs, L->sdown_f32 ? L->hfs : nullptr, (int)fspad, sg, sslots, tbs, L->ysh,
                                  ss);
         }
         HIPCHK(hipEventRecord(L->ev_join, ss));
@@ -928,6 +934,7 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
     if (const char* f = std::getenv("JX_NO_FOLD")) L->fold_combine = std::strcmp(f, "0") == 0;
     if (const char* f = std::getenv("JX_NO_FUSED")) L->fused_decode = std::strcmp(f, "0") == 0;
     if (const char* f = std::getenv("JX_FUSED")) L->force_fused = std::strcmp(f, "0") != 0;
+    if (const char* f = std::getenv("JX_SMFMA_MIN")) L->smfma_min = std::max(1, std::atoi(f));
     if ((r = dalloc(L->dsync, 1)) != JX_OK) return bail(r);
     if (hipMemset(L->dsync, 0, sizeof(jx::DecodeSync)) != hipSuccess) return bail(fail(JX_ERR_HIP, "decode state"));
     *out = L;
