@@ -1013,8 +1013,14 @@ struct Mx<T_Q4_0> {
 
 // Gate + up (+ SwiGLU + Q8_0 of h) or down for up to MX_NT tokens per pass of one expert's row tile.
 // Gate/up: the first half of the waves streams the gate tile, the second half the up tile.
+// Waves per SIMD the form is compiled for: 3 where it fits 168 VGPRs without spills (Q4_0, Q8_0,
+// Q5_K), 2 for Q4_K and Q6_K (measured: Qwen3-shaped 32-token gate/up 66.7 -> 60.9 us; the
+// Qwen1.5-shaped routed gate/up at 64 tokens 116 -> 100 us).
+template <int TYPE>
+constexpr int mx_wps() { return (TYPE == T_Q4_K || TYPE == T_Q6_K) ? 2 : 3; }
+
 template <int TYPE, bool GATEUP, int WAVES>
-__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(mx_wps<TYPE>())))
 k_gemv_mx(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_ld, float* y, SmallTail tail) {
     using X = Mx<TYPE>;
     using Raw = typename X::Raw;
@@ -1271,10 +1277,17 @@ static void down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, 
                            hf, hf_ld, grp, y, comb);
     } else if (tb > 4 && !F32ACT) {  // several tokens per expert: the matrix-core form
         if constexpr (!F32ACT) {
+            // 4-wave blocks (more of them resident per CU) unless the grid is too small to fill half
+            // the CUs (one dense matrix, few tokens); measured: Qwen1.5-shaped 64 tokens routed down
+            // 75 -> 44 us, Qwen3-shaped 32 tokens 62 -> 33 us
             const size_t lds = (size_t)(K / 32) * MX_NT * sizeof(float2);
-            lds_optin(k_gemv_mx<TYPE, false, DOWN_WAVES>, lds);
-            hipLaunchKernelGGL((k_gemv_mx<TYPE, false, DOWN_WAVES>), grid, dim3(DOWN_WAVES * 64), lds, st, dn, dn,
-                               hq, grp, ActQ8{}, nullptr, 0, y, SmallTail{});
+            auto go = [&](auto kern, int waves) {
+                lds_optin(kern, lds);
+                hipLaunchKernelGGL(kern, grid, dim3(waves * 64), lds, st, dn, dn, hq, grp, ActQ8{}, nullptr, 0, y,
+                                   SmallTail{});
+            };
+            if (2 * (int)grid.x < num_cus()) go(k_gemv_mx<TYPE, false, 8>, 8);
+            else go(k_gemv_mx<TYPE, false, 4>, 4);
         }
     } else {
         const size_t lds = act_lds_bytes(4, K, F32ACT);

@@ -127,9 +127,12 @@ constexpr int MAX_SLOTS_DEC = 16;  // routed slots (top_k) of the fused one-toke
 
 constexpr int MFMA_BN = 128;  // pairs per matrix-core GEMM tile
 // shared expert on the matrix cores from this many tokens (one dense expert fills few GEMM
-// workgroups below that; against the 16-token matrix-core GEMV the crossover measured 32-128 tokens
-// on the Qwen1.5- and DeepSeek-V2-Lite-shaped layers)
-constexpr int MFMA_MIN_SHARED_TOKENS = 64;
+// workgroups below that: 44 gate/up and 16 down workgroups for a 5632 x 2048 expert at 64 tokens).
+// The 16-token matrix-core GEMV in one group per 16 tokens is faster up to 256 tokens for the formats
+// it runs at 3 waves per SIMD (Qwen1.5-shaped, Q4_0: 64 tokens 233 -> 177 us per step), up to 64 for
+// Q4_K / Q6_K (2 waves per SIMD; DeepSeek-V2-Lite-shaped).
+constexpr int MFMA_MIN_SHARED_TOKENS = 256;
+constexpr int MFMA_MIN_SHARED_TOKENS_KQ = 64;  // Q4_K / Q6_K shared experts
 
 // The weighted combine folded into the down GEMV (few-token decode with at most two
 // contributions per output element: top_k <= 2 and no shared expert): out [n][d] is

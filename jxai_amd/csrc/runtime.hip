@@ -302,7 +302,7 @@ struct jx_moe_layer {
     uint32_t dec_epoch = 0;
     bool fused_decode = true;
     bool force_fused = false;  // JX_FUSED=1: also where the separate launches measured faster
-    int smfma_min = jx::MFMA_MIN_SHARED_TOKENS;  // JX_SMFMA_MIN: shared expert's GEMM threshold (A/B)
+    int smfma_min = 0;         // shared expert's GEMM threshold (JX_SMFMA_MIN overrides it: A/B)
     bool dec_used = false;     // the last forward took the fused launch
 };
 
@@ -934,6 +934,9 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
     if (const char* f = std::getenv("JX_NO_FOLD")) L->fold_combine = std::strcmp(f, "0") == 0;
     if (const char* f = std::getenv("JX_NO_FUSED")) L->fused_decode = std::strcmp(f, "0") == 0;
     if (const char* f = std::getenv("JX_FUSED")) L->force_fused = std::strcmp(f, "0") != 0;
+    L->smfma_min = (L->shared && (L->sgate.m.type == jx::T_Q4_K || L->sgate.m.type == jx::T_Q6_K))
+                       ? jx::MFMA_MIN_SHARED_TOKENS_KQ
+                       : jx::MFMA_MIN_SHARED_TOKENS;
     if (const char* f = std::getenv("JX_SMFMA_MIN")) L->smfma_min = std::max(1, std::atoi(f));
     if ((r = dalloc(L->dsync, 1)) != JX_OK) return bail(r);
     if (hipMemset(L->dsync, 0, sizeof(jx::DecodeSync)) != hipSuccess) return bail(fail(JX_ERR_HIP, "decode state"));
