@@ -358,7 +358,7 @@ struct Arr {
 template <int TYPE, bool GATEUP, int GW, int TM, int TN, int WPE, int BN>
 __global__ void __launch_bounds__(GW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8 hq, float* hf, int hf_ld,
-        float* y) {
+        float* y, int KS, size_t ystride) {
     constexpr int NTH = GW * 64;
     // K-quants (Q4_K / Q5_K / Q6_K): acc is kept in units of the current super-block's d (per weight
     // row) and rescaled by d_prev / d_cur at each super-block (fp32 rounding ~2^-24 per step); Q4_K and
@@ -388,8 +388,11 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
     // tiles would idle)
     int n_eff = n_items;
     if (!grp.identity) n_eff = min(n_items, R * *grp.n_tiles * (MFMA_BN / BN));
-    if ((int)(blockIdx.x >> 3) >= (n_eff >> 3) + ((int)(blockIdx.x & 7) < (n_eff & 7) ? 1 : 0)) return;
-    work_item(blockIdx.x, n_eff, R, MFMA_BN / BN, RC, ti, sub, rg);
+    // down over a long K: KS adjacent workgroups per item (on different XCDs), each a range of K writing
+    // its own part of y
+    const int kp = GATEUP ? 0 : (int)(blockIdx.x % KS), LB = GATEUP ? (int)blockIdx.x : (int)(blockIdx.x / KS);
+    if ((LB >> 3) >= (n_eff >> 3) + ((LB & 7) < (n_eff & 7) ? 1 : 0)) return;
+    work_item(LB, n_eff, R, MFMA_BN / BN, RC, ti, sub, rg);
     int e, p0, cnt;
     if (!pair_tile(grp, ti, e, p0, cnt)) return;  // whole workgroup
     p0 += sub * BN;  // this workgroup's part of the tile
@@ -414,6 +417,8 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
 
     const int H = in.KH;
     const int KB = in.K / 32;
+    // this workgroup's half-units [h0, h1): whole super-blocks (an even count), the last part the rest
+    const int HP = ((H + KS - 1) / KS + 1) & ~1, h0 = GATEUP ? 0 : kp * HP, h1 = GATEUP ? H : min(H, h0 + HP);
     // Source rows ascend within a tile (an expert's pairs are in token order; down rows are
     // consecutive pairs), so the workgroup's buffers are based at its first source row in 64 bits
     // and every per-lane offset is relative to it: below 2^32 whenever n_tok rows of the activation
@@ -511,8 +516,9 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
     if (active)
 #pragma unroll
         for (int i = 0; i < TM; ++i)
-            wa[i].template load<0>(qbase[i], sbase[i], mbase[i], xbase[i], qo[i], so[i], mo[i], xo[i], 0, min(HB, KB));
-    stage(0);
+            wa[i].template load<0>(qbase[i], sbase[i], mbase[i], xbase[i], qo[i], so[i], mo[i], xo[i], h0,
+                                   min(HB, KB - h0 * HB));
+    stage(h0);
 
     // LDS byte offset of this lane's A chunk (hi/lo hl, sub-block j of the half-unit, K-half m) in pair tile 0
     auto boff = [&](int hl, int j, int m) { return n * PB + (((16 * hl + 4 * j + 2 * g + m) ^ (n % CPP)) << 4); };
@@ -521,7 +527,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
         constexpr bool ODD = decltype(parity)::value;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (h + 1 < H) {
+        if (h + 1 < h1) {
             stage(h + 1);
             if (active)
 #pragma unroll
@@ -926,14 +932,14 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
         }
     };
 
-    for (int h = 0; h < H; h += 2) {
+    for (int h = h0; h < h1; h += 2) {
         half(h, Parity<false>{}, wa, wb);
-        if (h + 1 < H) half(h + 1, Parity<true>{}, wb, wa);
+        if (h + 1 < h1) half(h + 1, Parity<true>{}, wb, wa);
     }
 
     // ------------------------------------------------------------ epilogue
     if (active) {  // back to natural units: the row's unit (RESCALE) and the token's exponent
-        const float* pe = sm.st[(H - 1) & 1].pe + pbase;
+        const float* pe = sm.st[(h1 - 1) & 1].pe + pbase;
 #pragma unroll
         for (int t = 0; t < TN; ++t)
 #pragma unroll
@@ -1024,7 +1030,7 @@ k_wgemm(QMat W0, QMat W1, ActH in, Groups grp, int R, int n_items, int RC, ActQ8
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int pr = pbase + 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
-                    if (pr < cnt) y[(size_t)(p0 + pr) * W0.rows + rt * 32 + n] = acc[i][t][r];
+                    if (pr < cnt) y[(size_t)kp * ystride + (size_t)(p0 + pr) * W0.rows + rt * 32 + n] = acc[i][t][r];
                 }
         }
     }
@@ -1128,15 +1134,16 @@ struct Shape {
 
 template <int TYPE, bool GATEUP>
 static void launch_t(const QMat& w0, const QMat& w1, const ActH& in, const Groups& grp, int tiles_ub, const ActQ8& hq,
-                     float* hf, int hf_ld, float* y, hipStream_t st) {
+                     float* hf, int hf_ld, float* y, hipStream_t st, int KS = 1, size_t ystride = 0) {
     using S = Shape<TYPE, GATEUP>;
     constexpr int rows_per_wg = Arr<GATEUP, S::GW, S::TM, S::TN, S::BN>::WROWS;  // row tiles of each matrix per workgroup
     const int R = (w0.nrt + rows_per_wg - 1) / rows_per_wg;
     const int n_items = R * tiles_ub * (MFMA_BN / S::BN);
     if (n_items <= 0) return;
     const int RC = S::RC > 0 ? std::min(S::RC, R) : R;
-    hipLaunchKernelGGL((k_wgemm<TYPE, GATEUP, S::GW, S::TM, S::TN, S::WPE, S::BN>), dim3(n_items), dim3(S::GW * 64), 0, st,
-                       w0, w1, in, grp, R, n_items, RC, hq, hf, hf_ld, y);
+    const int grid = n_items * KS;
+    hipLaunchKernelGGL((k_wgemm<TYPE, GATEUP, S::GW, S::TM, S::TN, S::WPE, S::BN>), dim3(grid), dim3(S::GW * 64), 0, st,
+                       w0, w1, in, grp, R, n_items, RC, hq, hf, hf_ld, y, KS, ystride);
 }
 
 void launch_mfma_gateup(const QMat& g, const QMat& u, const ActH& xin, const Groups& grp, int tiles_ub,
@@ -1157,15 +1164,18 @@ void launch_mfma_gateup(const QMat& g, const QMat& u, const ActH& xin, const Gro
 
 bool gemm_gateup_ok(int type) { return type == T_Q4_0 || type == T_Q8_0 || type == T_Q4_K || type == T_Q5_K; }
 
-void launch_mfma_down(const QMat& dn, const ActH& hin, const Groups& grp, int tiles_ub, float* y, hipStream_t st) {
+int mfma_down_ksplit(int K) { return K >= MFMA_DOWN_KSPLIT_MIN_K ? 2 : 1; }
+
+void launch_mfma_down(const QMat& dn, const ActH& hin, const Groups& grp, int tiles_ub, float* y, hipStream_t st,
+                      int KS, size_t ystride) {
     const ActQ8 none{};
     switch (dn.type) {
-        case T_Q4_0: launch_t<T_Q4_0, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st); break;
-        case T_Q8_0: launch_t<T_Q8_0, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st); break;
-        case T_Q4_K: launch_t<T_Q4_K, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st); break;
-        case T_Q5_0: launch_t<T_Q5_0, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st); break;
-        case T_Q5_K: launch_t<T_Q5_K, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st); break;
-        case T_Q6_K: launch_t<T_Q6_K, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st); break;
+        case T_Q4_0: launch_t<T_Q4_0, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st, KS, ystride); break;
+        case T_Q8_0: launch_t<T_Q8_0, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st, KS, ystride); break;
+        case T_Q4_K: launch_t<T_Q4_K, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st, KS, ystride); break;
+        case T_Q5_0: launch_t<T_Q5_0, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st, KS, ystride); break;
+        case T_Q5_K: launch_t<T_Q5_K, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st, KS, ystride); break;
+        case T_Q6_K: launch_t<T_Q6_K, false>(dn, dn, hin, grp, tiles_ub, none, nullptr, 0, y, st, KS, ystride); break;
         default: break;
     }
 }

@@ -211,19 +211,28 @@ void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_l
 // launch_q8_to_acth) and/or fp32 (hf != null).
 void launch_mfma_gateup(const QMat& g, const QMat& u, const ActH& xin, const Groups& grp, int tiles_ub,
                         const ActQ8& hq, float* hf, hipStream_t st);
-void launch_mfma_down(const QMat& dn, const ActH& hin, const Groups& grp, int tiles_ub, float* y, hipStream_t st);
+// KS > 1: the K range split over KS workgroups per item (whole super-blocks each), part q of the
+// output at y + q * ystride (the combine adds the parts in order).
+void launch_mfma_down(const QMat& dn, const ActH& hin, const Groups& grp, int tiles_ub, float* y, hipStream_t st,
+                      int KS = 1, size_t ystride = 0);
+// K-split of the down GEMM for a K of K: two parts from MFMA_DOWN_KSPLIT_MIN_K on (twice the
+// workgroups, finer rounds; measured Mixtral-shaped, K 14336: 2048 tokens 634 -> 575 us, 256 tokens
+// 155 -> 133 us; at K 768 - 1408 the per-workgroup overhead makes it slower).
+constexpr int MFMA_DOWN_KSPLIT_MIN_K = 8192;
+int mfma_down_ksplit(int K);
 // Weight types the matrix-core gate/up GEMM takes (Q5_0 has no Q8_0-activation form; Q6_K's sc * q
 // operand is not exact in fp16, and gate/up products must be: h is re-quantized).
 bool gemm_gateup_ok(int type);
 // Fill m.mn (m.n_mats * m.nrt * m.nkb * MN_SB bytes) from a repacked Q4_K or Q5_K matrix.
 void launch_min_table(const QMat& m, uint8_t* mn, hipStream_t st);
 
-// acc[t] = sum_s p[t][s] * y[pos(t,s)] (+ shscale[t] * ysh[t]), fma in selection order;
+// acc[t] = sum_s p[t][s] * y[pos(t,s)] (+ shscale[t] * ysh[t]), fma in selection order (y2 != null:
+// each y row is y[p] + y2[p], the K-split down GEMM's two parts added in that order);
 // out[t] = acc[t], or resid[t] + acc[t] (resid != null), or with post_w:
 // (resid[t] +) rms_norm(acc[t], post_w, eps) (post_ffw_norm, transformer.cpp:2758-2764).
 void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
                     const float* shscale, float* out, hipStream_t st, const float* resid = nullptr,
-                    const float* post_w = nullptr, float eps = 0.0f);
+                    const float* post_w = nullptr, float eps = 0.0f, const float* y2 = nullptr);
 // MoETransformerEngine::rms_norm (transformer.cpp:67-73) of rows x d floats: out = x * inv * w.
 void launch_rms_norm(const float* x, const float* w, int rows, int d, float eps, float* out, hipStream_t st);
 

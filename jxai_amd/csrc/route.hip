@@ -1169,7 +1169,7 @@ void launch_rms_norm(const float* x, const float* w, int rows, int d, float eps,
 template <int KU>  // slots whose loads go out together (the fma order stays the selection order)
 __global__ void __launch_bounds__(256)
 k_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
-          const float* shscale, const float* resid, float* out) {
+          const float* shscale, const float* resid, float* out, const float* y2) {
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;  // float4 index
     const int d4 = d / 4;
     if (idx >= (size_t)n * d4) return;
@@ -1187,6 +1187,13 @@ k_combine(int n, int d, int k, const float* probs, const int* pos_of, const floa
         }
 #pragma unroll
         for (int u = 0; u < KU; ++u) v[u] = *reinterpret_cast<const float4*>(y + (size_t)p[u] * d + i);
+        if (y2) {  // the K-split down GEMM's second part
+#pragma unroll
+            for (int u = 0; u < KU; ++u) {
+                const float4 b = *reinterpret_cast<const float4*>(y2 + (size_t)p[u] * d + i);
+                v[u] = make_float4(v[u].x + b.x, v[u].y + b.y, v[u].z + b.z, v[u].w + b.w);
+            }
+        }
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
             if (s0 + u < k) {
@@ -1218,7 +1225,7 @@ k_combine(int n, int d, int k, const float* probs, const int* pos_of, const floa
 // computes it, staged chain-major for the exact vec_dot_f32 order of the norm.
 __global__ void __launch_bounds__(256)
 k_combine_norm(int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
-               const float* shscale, const float* post_w, float eps, const float* resid, float* out) {
+               const float* shscale, const float* post_w, float eps, const float* resid, float* out, const float* y2) {
     extern __shared__ float as[];  // chain-major acc row
     __shared__ float inv_s;
     const int t = blockIdx.x, tid = threadIdx.x, S = d / 16 + 1;
@@ -1226,7 +1233,8 @@ k_combine_norm(int d, int k, const float* probs, const int* pos_of, const float*
         float acc = 0.0f;
         for (int s = 0; s < k; ++s) {
             const float w = probs[(size_t)t * k + s];
-            acc = __builtin_fmaf(w, y[(size_t)pos_of[(size_t)t * k + s] * d + i], acc);
+            const size_t o = (size_t)pos_of[(size_t)t * k + s] * d + i;
+            acc = __builtin_fmaf(w, y2 ? y[o] + y2[o] : y[o], acc);
         }
         if (ysh) acc = __builtin_fmaf(shscale[t], ysh[(size_t)t * d + i], acc);
         as[(i & 15) * S + (i >> 4)] = acc;
@@ -1246,24 +1254,27 @@ k_combine_norm(int d, int k, const float* probs, const int* pos_of, const float*
 
 void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
                     const float* shscale, float* out, hipStream_t st, const float* resid, const float* post_w,
-                    float eps) {
+                    float eps, const float* y2) {
     if (post_w) {
         const size_t lds = (size_t)16 * (d / 16 + 1) * sizeof(float);
         if (lds > 65536)
             (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_combine_norm),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         hipLaunchKernelGGL(k_combine_norm, dim3((unsigned)n), dim3(256), lds, st, d, k, probs, pos_of, y, ysh, shscale,
-                           post_w, eps, resid, out);
+                           post_w, eps, resid, out, y2);
         return;
     }
     const size_t tot = (size_t)n * (d / 4);
     const dim3 grid((unsigned)((tot + 255) / 256));
     if (k <= 2)
-        hipLaunchKernelGGL(k_combine<2>, grid, dim3(256), 0, st, n, d, k, probs, pos_of, y, ysh, shscale, resid, out);
+        hipLaunchKernelGGL(k_combine<2>, grid, dim3(256), 0, st, n, d, k, probs, pos_of, y, ysh, shscale, resid, out,
+                           y2);
     else if (k <= 4)
-        hipLaunchKernelGGL(k_combine<4>, grid, dim3(256), 0, st, n, d, k, probs, pos_of, y, ysh, shscale, resid, out);
+        hipLaunchKernelGGL(k_combine<4>, grid, dim3(256), 0, st, n, d, k, probs, pos_of, y, ysh, shscale, resid, out,
+                           y2);
     else
-        hipLaunchKernelGGL(k_combine<8>, grid, dim3(256), 0, st, n, d, k, probs, pos_of, y, ysh, shscale, resid, out);
+        hipLaunchKernelGGL(k_combine<8>, grid, dim3(256), 0, st, n, d, k, probs, pos_of, y, ysh, shscale, resid, out,
+                           y2);
 }
 
 // Q8_0 of `rows` rows of K fp32 values (quantize_row_q8_0, src/quant.cpp:1029-1045),

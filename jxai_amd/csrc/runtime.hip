@@ -266,6 +266,7 @@ struct jx_moe_layer {
     jx::ActQ8 xq, hq, hqs;
     DevActH xh, hh, hhs;  // matrix-core forms of x, h, shared h
     float *hf = nullptr, *hfs = nullptr, *y = nullptr, *ysh = nullptr, *xf = nullptr;
+    size_t ystride = 0;  // floats per part of y (the K-split down GEMM's second part follows the first)
     int last_n = 0;
     Prof prof;
     hipStream_t own = nullptr;  // used when the caller passes the null stream
@@ -375,7 +376,9 @@ int ensure_workspace(jx_moe_layer* L, int n) {
     // the fused one-token step polls the low bits of h's scale words for its launch's tag: start untagged
     HIPCHK(hipMemset(L->hq.s, 0, nk * L->F / 32 * sizeof(float2)));
     L->hq.K = L->F;
-    WS(L->y, nk * L->d);
+    // y: the routed down output per pair; a K-split down GEMM writes its second part ystride floats on
+    L->ystride = nk * L->d;
+    WS(L->y, (size_t)jx::mfma_down_ksplit(hK) * nk * L->d);
     if (L->gu_f32 || L->sgu_f32) {
         WS(L->xf, (size_t)cap * L->dpad);
         HIPCHK(hipMemset(L->xf, 0, (size_t)cap * L->dpad * sizeof(float)));
@@ -704,6 +707,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
                                nullptr, gxf, L->dpad);
     }
     if (L->shared) HIPCHK(hipStreamWaitEvent(st, L->ev_join, 0));
+    int ks = 1;  // parts of the down GEMM's K (the combine adds them)
     if (mfma_down) {
         {
             Launch l(L, "h_to_matrix_form", st);
@@ -713,7 +717,8 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
                 jx::launch_q8_to_acth(L->hq, nk, L->hh.a, st, false);
         }
         Launch l(L, "down_mfma", st);
-        jx::launch_mfma_down(L->down.m, L->hh.a, grp, tiles_ub, L->y, st);
+        ks = jx::mfma_down_ksplit(L->hh.a.K);
+        jx::launch_mfma_down(L->down.m, L->hh.a, grp, tiles_ub, L->y, st, ks, L->ystride);
     } else {
         jx::CombineOut comb;
         if (fold) {
@@ -729,7 +734,8 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     if (!fold) {
         Launch l(L, "combine", st);
         jx::launch_combine(n, d, k, L->probs, L->pos_of, L->y, L->shared ? L->ysh : nullptr, L->shscale, outdev, st,
-                           resid ? xres : nullptr, resid ? L->post_norm : nullptr, L->eps);
+                           resid ? xres : nullptr, resid ? L->post_norm : nullptr, L->eps,
+                           ks > 1 ? L->y + L->ystride : nullptr);
     }
     HIPCHK(hipGetLastError());
     return JX_OK;
