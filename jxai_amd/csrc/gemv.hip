@@ -708,6 +708,28 @@ __device__ __forceinline__ void kloop(const QMat& W0, const QMat& W1, int e, int
 #endif
 }
 
+// kloop with DEPTH units in flight per wave (a ring of register sets): the same units in the same
+// order, so the same sums as kloop's.  pre() runs after the first DEPTH units' loads are issued.
+template <int TYPE, int DEPTH, typename Pre, typename Acc>
+__device__ __forceinline__ void kloop_d(const QMat& W, int e, int rt, int lo, int nu, int stride, int m, int h,
+                                        Pre&& pre, Acc&& accum) {
+    using F = Fmt<TYPE>;
+    typename F::Raw r[DEPTH];
+#pragma unroll
+    for (int i = 0; i < DEPTH; ++i) F::load(r[i], W, e, rt, lo + i * stride, m, h, lo + i * stride < nu);
+    pre();
+    for (int u = lo; u < nu; u += DEPTH * stride) {
+#pragma unroll
+        for (int i = 0; i < DEPTH; ++i) {
+            const int ui = u + i * stride;
+            if (ui >= nu) break;  // wave-uniform
+            accum(r[i], ui);
+            const int un = ui + DEPTH * stride;
+            F::load(r[i], W, e, rt, un, m, h, un < nu);
+        }
+    }
+}
+
 // Resident waves per SIMD the GEMVs are compiled for (single-token groups:
 // <= 128 VGPRs, every block of a decode step resident at once with enough
 // 1 KB weight loads in flight per CU to cover HBM latency).  The single-token
@@ -1648,6 +1670,299 @@ void launch_decode1(const Decode1Args& a, int gtype, int dtype, hipStream_t st) 
     JX_DEC1(T_Q4_K, T_Q6_K)
     JX_DEC1(T_Q5_K, T_Q6_K)
 #undef JX_DEC1
+}
+
+// ---------------------------------------------------------------- one-token step, one block per CU
+// Layers whose gate/up row tiles outnumber the CUs several times (Mixtral-shaped: 896 tiles on 256
+// CUs; k_decode1 leaves its down blocks to the CUs its gate/up blocks free, unevenly) as one grid of
+// one 1024-thread block per CU:
+//   route    the last E blocks run one router row each (the row and the token chain-major in LDS, the
+//            vec_dot_f32 chains of k_route_small) and publish the logit as a tagged word; every block
+//            forms the Q8_0 of x in LDS meanwhile, then selects the experts from the logits (the same
+//            selection in every block).  Block 0 writes the logits, the Q8_0 of x and the dispatch
+//            tables for the caller; each block first zeroes the output rows of its first-slot down
+//            tile (the folded combine adds into them).
+//   gate/up  (slot, row tile) tiles b, b + G, b + 2G, b + 3G of the G blocks, one per group of four
+//            waves (the 4-wave single-token GEMV), so every CU streams about the same bytes.  h's
+//            Q8_0 quants go out as 64-bit words carrying the launch number, its scales with the
+//            launch's tag in their low mantissa bits, so no store waits for another.
+//   down     the block's down tiles b, b + G on waves 0 .. DOWN_WAVES - 1 (the single-token down
+//            GEMV's unit split and wave-order sum): the first weight units in flight, then h read
+//            until every word of the slot carries this launch's number or tag, and p * y added into
+//            the output (two adds onto an exact zero per element).
+// The step is bit-identical to the separate launches.  Every block waits on others, so the grid must
+// be resident at once: one block per CU (its LDS leaves no room for a second) and a grid of one block
+// per CU; every wait is bounded anyway (giving up sets sync->err, which the synchronous forward
+// reports).  The zeroing of a row is ordered before the block's own slot-1 h stores, which the other
+// down tile of that row waits for (decodep_fits checks the tile layout gives every zeroing block one).
+// Measured Mixtral-shaped, host clock over 300 queued steps: 42.2 us per step against 46.3 us for the
+// separate launches (route, gate/up GEMV, down GEMV).
+constexpr int DP_THREADS = 1024, DP_WAVES = DP_THREADS / 64, DP_GROUPS = DP_WAVES / 4;
+// Units in flight per wave (kloop_d).  Measured Mixtral-shaped: 2 -> 42.2 us per step, 3 -> 45, 4 -> 54
+// (more requests in flight slow the stream); likewise four gate/up groups streaming at once against two
+// (42.2 / 42.2 us) or one (51 us), and 16 down waves against 8 (42.4 / 42.2 us).
+constexpr int DP_DEPTH = 2;
+constexpr size_t DP_LDS_MAX = 156 * 1024;
+
+__host__ __device__ inline size_t decodep_route_bytes(int d, int E) {
+    (void)E;
+    return (size_t)2 * 16 * rs_stride(d) * sizeof(float);  // a router row and the token, chain-major
+}
+// LDS offset of the Q8_0 of x, above the router staging and the down projection's staged h
+__host__ __device__ inline size_t decodep_xoff(int d, int f, int E) {
+    const size_t r = decodep_route_bytes(d, E), hb = act_lds_bytes(1, f, false);
+    return r > hb ? r : hb;
+}
+
+// Dynamic LDS of k_decode_p: the router staging or the down projection's h, then the Q8_0 of x, and at
+// least 96 KB so that no CU holds two of the blocks (each waits on the others).
+static size_t decodep_lds(int d, int f, int E) {
+    return std::max<size_t>(decodep_xoff(d, f, E) + act_lds_bytes(1, d, false), 96 * 1024);
+}
+
+template <int TG, int TD>
+__global__ void __launch_bounds__(DP_THREADS) __attribute__((amdgpu_waves_per_eu(DP_WAVES / 4)))
+k_decode_p(Decode1Args a) {
+    extern __shared__ __align__(16) int8_t smem[];
+    __shared__ float lg[SMALL_GROUP_MAX_E];
+    __shared__ float red[DP_WAVES][32];
+    __shared__ int s_e[MAX_SLOTS_DEC];
+    __shared__ float s_p[MAX_SLOTS_DEC];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 31, h = lane >> 5;
+    const int E = a.E, d = a.d, k = a.k, NB = gridDim.x, b = blockIdx.x;
+    const int ng = a.G.nrt * k, nd = a.D.nrt * k;
+    int8_t* xq = smem + decodep_xoff(d, a.hq.K, E);  // Q8_0 of x: quants [d], then (scale, sum) [d / 32]
+    float2* xs = reinterpret_cast<float2*>(xq + d);
+
+    // ---- route
+    for (int j = 0; j < 2; ++j) {  // the output rows of this block's first-slot down tiles start at zero
+        const int t = b + j * NB;
+        if (t < a.D.nrt && tid < 32)
+            __hip_atomic_store(reinterpret_cast<uint32_t*>(a.out) + t * 32 + tid, 0u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // complete before the block's h stores (the barriers below)
+    const int rr = NB - 1 - b;  // router row of this block: the last E blocks hold the fewest gate/up tiles
+    if (rr < E) {  // router row rr against the token, chain-major in LDS (as k_decode1's router blocks)
+        float* lds = reinterpret_cast<float*>(smem);
+        const int S = rs_stride(d), RS = 16 * S;
+        {
+            constexpr int PER = 2 * 8192 / 4 / DP_THREADS;  // d <= 8192
+            const int c4 = d / 4, tot = 2 * c4;
+            float4 v[PER];
+#pragma unroll
+            for (int q = 0; q < PER; ++q) {
+                const int i = tid + q * DP_THREADS;
+                if (i >= tot) break;
+                const int row = i / c4, c = i - row * c4;
+                v[q] = *reinterpret_cast<const float4*>((row == 0 ? a.router + (size_t)rr * d : a.x) + 4 * c);
+            }
+#pragma unroll
+            for (int q = 0; q < PER; ++q) {
+                const int i = tid + q * DP_THREADS;
+                if (i >= tot) break;
+                const int row = i / c4, c = i - row * c4;
+                float* dst = lds + row * RS + 4 * (c & 3) * S + (c >> 2);
+                dst[0] = v[q].x;
+                dst[S] = v[q].y;
+                dst[2 * S] = v[q].z;
+                dst[3 * S] = v[q].w;
+            }
+        }
+        __syncthreads();
+        if (wave == 0 && lane < 16) {
+            const bool c8 = a.chain8 != 0;
+            const float s = chain_sum(chain_dot_lds(lds, lds + RS, S, d, lane, c8), c8);
+            if (lane == 0)
+                __hip_atomic_store(a.sync->tag + rr, ((uint64_t)a.epoch << 32) | __float_as_uint(a.bias ? s + a.bias[rr] : s),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    {  // Q8_0 of x from the token row, one 32-block per half-wave and step, as the router kernels form it
+        constexpr int XPER = 8192 / 32 / (2 * DP_WAVES);  // d <= 8192
+        const int nb = d / 32, hw = 2 * wave + h;
+        float xv[XPER];
+#pragma unroll
+        for (int q = 0; q < XPER; ++q) {
+            const int bb = hw + q * (2 * DP_WAVES);
+            xv[q] = bb < nb ? a.x[bb * 32 + m] : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < XPER; ++q) {
+            const int bb = hw + q * (2 * DP_WAVES);
+            if (bb < nb) {  // half-wave uniform
+                float2 sv;
+                const int v = q8_block_vals(xv[q], sv);
+                xq[bb * 32 + m] = (int8_t)v;
+                if (m == 0) xs[bb] = sv;
+                if (b == 0) {
+                    a.xq.q[bb * 32 + m] = (int8_t)v;
+                    if (m == 0) a.xq.s[bb] = sv;
+                }
+            }
+        }
+    }
+    if (wave == 0) dec_wait_logits(a, E, lg);
+    __syncthreads();
+    if (wave == 0) {  // this launch's experts and weights in selection order (every block alike)
+        RouteArgs r = a.ra;
+        r.ids = nullptr;
+        r.probs = nullptr;
+        r.shscale = nullptr;
+        uint64_t msk[SMALL_GROUP_MAX_E / 64];
+        float myp = 0.0f;
+        const int myid = topk_token_wave<SMALL_GROUP_MAX_E / 64>(r, lg, 0, nullptr, msk, &myp);
+        if (lane < k) {
+            s_e[lane] = myid;
+            s_p[lane] = myp;
+        }
+    } else if (wave == 1 && b == 0) {  // the caller's logits and dispatch tables
+        if (lane < E) a.ra.logits[lane] = lg[lane];
+        if (64 + lane < E) a.ra.logits[64 + lane] = lg[64 + lane];
+        topk_dispatch_wave<SMALL_GROUP_MAX_E / 64>(a.ra, a.o, lg, nullptr);
+    }
+    __syncthreads();
+
+    // ---- gate/up: tile b + grp * G of the (slot, row tile) list on waves 4 grp .. 4 grp + 3
+    {
+        const int grp = wave >> 2, lw = wave & 3, mat = lw >> 1, kw = lw & 1;
+        const int t = b + grp * NB;
+        const bool active = t < ng;
+        const int slot = active ? t / a.G.nrt : 0, rt = active ? t - slot * a.G.nrt : 0;
+        const int e = s_e[slot];
+        const ActLds A{xq, xs, nullptr, d};
+        const QMat& W = mat ? a.U : a.G;
+        const int nu = active ? n_units<TG>(a.G.nkb) : 0;
+        float acc[1] = {0.0f};
+        kloop_d<TG, DP_DEPTH>(
+            W, e, rt, kw, nu, 2, m, h, [] {},
+            [&](const typename Fmt<TG>::Raw& c, int u) { unit_accum<TG, 1>(c, A, u, h, 1, a.G.nkb, acc); });
+        acc[0] += __shfl_xor(acc[0], 32, 64);
+        if (h == 0) red[wave][m] = acc[0];
+        __syncthreads();
+        if (lw == 0 && active) {  // SwiGLU and h's Q8_0 block (as k_gemv_gateup), device-coherent
+            const float gv = red[wave][m] + red[wave + 1][m], uv = red[wave + 2][m] + red[wave + 3][m];
+            float2 sv;
+            const int q = q8_block_vals(gated(gv, uv, a.G.act), sv);
+            const uint32_t q1 = (uint32_t)__shfl_down(q, 1, 64), q2 = (uint32_t)__shfl_down(q, 2, 64),
+                           q3 = (uint32_t)__shfl_down(q, 3, 64);
+            const uint32_t word = ((uint32_t)q & 0xFFu) | ((q1 & 0xFFu) << 8) | ((q2 & 0xFFu) << 16) | (q3 << 24);
+            // every word carries the launch number, so neither store waits for the other
+            if (h == 0 && (m & 3) == 0)
+                __hip_atomic_store(a.hw + (size_t)slot * (a.hq.K / 4) + rt * 8 + (m >> 2),
+                                   ((uint64_t)a.epoch << 32) | word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0)
+                __hip_atomic_store(reinterpret_cast<uint64_t*>(a.hq.s + (size_t)slot * (a.hq.K / 32) + rt),
+                                   ((uint64_t)__float_as_uint(sv.y) << 32) | __float_as_uint(sv.x) | a.htag,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+
+    // ---- down: tiles b, b + G of the (slot, row tile) list on waves 0 .. DOWN_WAVES - 1 (the single-token
+    // down GEMV's unit split and wave-order sum, so the step is bit-identical to the separate launches)
+    static_assert(DOWN_WAVES <= DP_WAVES, "down waves");
+    for (int j = 0; j < 2; ++j) {
+        const int t = b + j * NB;
+        if (t >= nd) break;  // block-uniform
+        const int slot = t / a.D.nrt, rt = t - slot * a.D.nrt;
+        const int e = s_e[slot];
+        const float p = s_p[slot];
+        const int K = a.hq.K, KB = K / 32;
+        const ActLds A{smem, reinterpret_cast<const float2*>(smem + K), nullptr, K};
+        const int nu = wave < DOWN_WAVES ? n_units<TD>(a.D.nkb) : 0;
+        float acc[1] = {0.0f};
+        kloop_d<TD, DP_DEPTH>(
+            a.D, e, rt, wave, nu, DOWN_WAVES, m, h,
+            [&] {  // after the first two units' loads: read the slot's h until every word carries this launch's
+                   // number (the quant words) or tag (the scale words), then stage it
+                if (j) __syncthreads();  // the previous tile's LDS reads are done
+                constexpr int QPER = 16384 / 4 / DP_THREADS;  // d_ff <= 16384
+                const uint64_t* qw = a.hw + (size_t)slot * (K / 4);
+                const uint64_t* ss = reinterpret_cast<const uint64_t*>(a.hq.s + (size_t)slot * KB);
+                uint64_t qv[QPER], sv = 0;
+                for (int it = 0;; ++it) {
+                    bool ok = true;
+#pragma unroll
+                    for (int q = 0; q < QPER; ++q) {
+                        const int i = tid + q * DP_THREADS;
+                        qv[q] = i < K / 4 ? __hip_atomic_load(qw + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                          : (uint64_t)a.epoch << 32;
+                        ok = ok && (uint32_t)(qv[q] >> 32) == a.epoch;
+                    }
+                    if (tid < KB) {
+                        sv = __hip_atomic_load(ss + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        ok = ok && ((uint32_t)sv & DEC_HTAG_MASK) == a.htag;
+                    }
+                    if (__syncthreads_and(ok)) break;  // block-uniform
+                    if (it >= DEC_SPIN_LIMIT) {
+                        if (tid == 0) dec_fail(a.sync);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+#pragma unroll
+                for (int q = 0; q < QPER; ++q) {
+                    const int i = tid + q * DP_THREADS;
+                    if (i < K / 4) reinterpret_cast<uint32_t*>(smem)[i] = (uint32_t)qv[q];
+                }
+                if (tid < KB) reinterpret_cast<uint64_t*>(smem + K)[tid] = sv & ~(uint64_t)DEC_HTAG_MASK;
+                __syncthreads();
+            },
+            [&](const typename Fmt<TD>::Raw& c, int u) {
+                unit_accum<TD, 1>(c, A, u, h, 1, a.D.nkb, acc);
+            });
+        acc[0] += __shfl_xor(acc[0], 32, 64);
+        if (h == 0) red[wave][m] = acc[0];
+        __syncthreads();
+        if (wave == 0 && h == 0) {
+            float s = 0.0f;
+#pragma unroll
+            for (int w = 0; w < DOWN_WAVES; ++w) s += red[w][m];
+            const int row = rt * 32 + m;
+            if (!(a.D.valid_rows && row >= a.D.valid_rows)) atomicAdd(a.out + row, p * s);
+        }
+    }
+}
+
+bool decodep_fits(int gtype, int dtype, int d, int f, int E, int k, bool shared, bool fold, int gate_nrt,
+                  int down_nrt) {
+    const int nb = num_cus();
+    if (shared || !fold || k != 2 || !decode1_fits(gtype, dtype, d, f, E, k, 0, false) || E > nb ||
+        decodep_lds(d, f, E) > DP_LDS_MAX || down_nrt * k > 2 * nb)
+        return false;
+    // gate/up: at most DP_GROUPS tiles per block; a block zeroing output rows (its down tile of slot 0)
+    // also stores h of slot 1 afterwards, which the slot-1 down tile of those rows waits for
+    const int ng = gate_nrt * k;
+    if (ng > DP_GROUPS * nb) return false;
+    for (int b = 0; b < nb && b < down_nrt; ++b) {
+        bool s1 = false;
+        for (int j = 0; j < DP_GROUPS; ++j) s1 = s1 || (b + j * nb >= gate_nrt && b + j * nb < ng);
+        if (!s1) return false;
+    }
+    return true;
+}
+
+// One block per CU, every block resident at once (its LDS leaves room for no second one): a plain
+// launch.  (A cooperative launch, which checks the co-residency itself, measured ~15 us more per step.)
+int launch_decode_p(const Decode1Args& a, int gtype, int dtype, hipStream_t st) {
+    const size_t lds = decodep_lds(a.d, a.hq.K, a.E);
+    hipError_t err = hipErrorInvalidValue;
+    auto go = [&](auto kern) {
+        lds_optin(kern, lds);
+        hipLaunchKernelGGL(kern, dim3(num_cus()), dim3(DP_THREADS), lds, st, a);
+        err = hipGetLastError();
+    };
+#define JX_DECP(G, D) \
+    if (gtype == G && dtype == D) { go(k_decode_p<G, D>); return err == hipSuccess ? 0 : -1; }
+    JX_DECP(T_Q4_0, T_Q4_0)
+    JX_DECP(T_Q8_0, T_Q8_0)
+    JX_DECP(T_Q4_K, T_Q4_K)
+    JX_DECP(T_Q5_K, T_Q5_K)
+    JX_DECP(T_Q6_K, T_Q6_K)
+    JX_DECP(T_Q4_K, T_Q6_K)
+    JX_DECP(T_Q5_K, T_Q6_K)
+#undef JX_DECP
+    return -1;
 }
 
 void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp, int slots,

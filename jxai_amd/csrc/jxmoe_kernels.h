@@ -282,6 +282,7 @@ struct Decode1Args {
     const float* shgate = nullptr;  // [d] its fp32 gate row (sigmoid weight), or null (weight 1)
     ActQ8 hqs;                  //   [1][d_ff_shared] Q8_0 of its h
     float* ysh = nullptr;       //   [d] its output, for launch_combine
+    uint64_t* hw = nullptr;     // k_decode_p: [k][d_ff / 4] words of h, (epoch << 32) | four Q8_0 quants
 };
 // Whether k_decode1 is built for this shape: E router rows (+ the shared-expert gate row) <=
 // SMALL_GROUP_MAX_E, even k <= MAX_SLOTS_DEC, d % 32 == 0 and d <= 8192, d_ff and the shared d_ff
@@ -292,6 +293,14 @@ bool decode1_fits(int gtype, int dtype, int d, int f, int E, int k, int fs, bool
 // top-k and a shared gate/up of sgate_nrt (0: none).
 bool decode1_pays(int gate_nrt, int k, int sgate_nrt);
 void launch_decode1(const Decode1Args& a, int gtype, int dtype, hipStream_t st);
+// The same step as one grid of one 1024-thread block per CU (k_decode_p): every block routes the
+// token itself, streams an even share of the gate/up row tiles, then its down tiles once h's tagged
+// scale words say the slot is complete; top-2 with the folded combine and no shared expert, for
+// layers whose gate/up tiles outnumber the CUs (decode1_pays false).  Returns nonzero when the launch
+// fails.
+bool decodep_fits(int gtype, int dtype, int d, int f, int E, int k, bool shared, bool fold, int gate_nrt,
+                  int down_nrt);
+int launch_decode_p(const Decode1Args& a, int gtype, int dtype, hipStream_t st);
 
 // Q8_0 of rows x K fp32 (row-major, K % 32 == 0).
 void launch_quantize_q8(const float* x, int rows, int K, ActQ8 out, hipStream_t st);

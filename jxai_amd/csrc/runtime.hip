@@ -300,11 +300,14 @@ struct jx_moe_layer {
     // one-token steps in one launch (k_decode1): its device state, zeroed at creation, and the number
     // of such launches so far (JX_NO_FUSED=1 keeps the separate launches: A/B measurement)
     jx::DecodeSync* dsync = nullptr;
+    uint64_t* hw = nullptr;  // k_decode_p's h: [k][d_ff / 4] words of (launch number << 32 | four quants)
     uint32_t dec_epoch = 0;
     bool fused_decode = true;
     bool force_fused = false;  // JX_FUSED=1: also where the separate launches measured faster
     int smfma_min = 0;         // shared expert's GEMM threshold (JX_SMFMA_MIN overrides it: A/B)
     bool dec_used = false;     // the last forward took the fused launch
+    bool decp_used = false;    // ... in its one-block-per-CU form (k_decode_p)
+    int decp_mode = -1;        // JX_DECP=0 / 1: never / always that form where it fits (A/B measurement)
 };
 
 struct jx_qmatrix {
@@ -410,7 +413,7 @@ void free_layer(jx_moe_layer* L) {
     void* ptrs[] = {L->router, L->router_cm, L->bias, L->shgate, L->ffn_norm, L->post_norm, L->xn, L->x, L->out, L->probs, L->shscale, L->logits, L->ids,
                     L->counts, L->offs, L->act, L->n_act, L->pair_tok, L->pos_of, L->n_tiles, L->tiles,
                     L->slots, L->xq.q, L->xq.s, L->hq.q, L->hq.s, L->hqs.q, L->hqs.s, L->hf, L->hfs, L->y, L->ysh,
-                    L->xf, L->dsync};
+                    L->xf, L->dsync, L->hw};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     L->xh.release();
@@ -479,6 +482,17 @@ constexpr size_t LARGE_EXPERT_ELEMS = (size_t)1 << 25;  // d * d_ff per matrix
 // Whether a call takes the fused one-token launch (k_decode1), apart from stream capture: one token in
 // the GEMV regime, Q8_0 activations on both sides, a shared expert (if any) in the routed formats, a
 // shape the kernel is built for, and one where it measured faster (or JX_FUSED=1).
+// The one-block-per-CU form of the fused step (k_decode_p): top-2 with the folded combine, no shared
+// expert, a shape it is built for, and gate/up tiles too many for k_decode1's one block per CU
+// (decode1_pays false; measured Mixtral-shaped: see DESIGN.md), unless JX_DECP says otherwise.
+static bool decodep_ok(const jx_moe_layer* L, uint32_t flags) {
+    if (L->decp_mode == 0 || L->shared || L->k != 2 || (flags & JX_FWD_RESIDUAL) || !L->fold_combine) return false;
+    if (!jx::decodep_fits(L->gate.m.type, L->down.m.type, L->d, L->F, L->E, L->k, false, true, L->gate.m.nrt,
+                          L->down.m.nrt))
+        return false;
+    return L->decp_mode == 1 || !jx::decode1_pays(L->gate.m.nrt, L->k, 0);
+}
+
 bool decode1_wanted(const jx_moe_layer* L, int n, uint32_t flags) {
     if (n != 1 || !L->fused_decode || (flags & (JX_FWD_UNFUSED | JX_FWD_FORCE_MFMA))) return false;
     if (L->gu_f32 || L->down_f32 || L->up.m.type != L->gate.m.type) return false;
@@ -489,6 +503,7 @@ bool decode1_wanted(const jx_moe_layer* L, int n, uint32_t flags) {
     if (!jx::decode1_fits(L->gate.m.type, L->down.m.type, L->d, L->F, L->E, L->k, L->shared ? L->Fs : 0,
                           L->shgate != nullptr))
         return false;
+    if (decodep_ok(L, flags)) return true;
     return L->force_fused || jx::decode1_pays(L->gate.m.nrt, L->k, L->shared ? L->sgate.m.nrt : 0);
 }
 
@@ -562,6 +577,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     if (L->dec_used) {
         if (++L->dec_epoch == 0) {  // 2^32 launches: start the counts over
             HIPCHK(hipMemsetAsync(L->dsync, 0, sizeof(jx::DecodeSync), st));
+            HIPCHK(hipMemsetAsync(L->hw, 0, (size_t)L->k * L->F / 4 * sizeof(uint64_t), st));
             L->dec_epoch = 1;
         }
         jx::Decode1Args a;
@@ -595,7 +611,13 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
             a.hqs = L->hqs;
             a.ysh = L->ysh;
         }
-        {
+        L->decp_used = fold && decodep_ok(L, flags);
+        if (L->decp_used) {
+            a.hw = L->hw;
+            Launch l(L, "decode_fused_cu", st);
+            if (jx::launch_decode_p(a, L->gate.m.type, L->down.m.type, st) != 0)
+                return fail(JX_ERR_HIP, "fused one-token step: launch failed");
+        } else {
             Launch l(L, fold ? "decode_fused" : "decode_fused_y", st);
             jx::launch_decode1(a, L->gate.m.type, L->down.m.type, st);
         }
@@ -940,11 +962,15 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
     if (const char* f = std::getenv("JX_NO_FOLD")) L->fold_combine = std::strcmp(f, "0") == 0;
     if (const char* f = std::getenv("JX_NO_FUSED")) L->fused_decode = std::strcmp(f, "0") == 0;
     if (const char* f = std::getenv("JX_FUSED")) L->force_fused = std::strcmp(f, "0") != 0;
+    if (const char* f = std::getenv("JX_DECP")) L->decp_mode = std::strcmp(f, "0") != 0 ? 1 : 0;
     L->smfma_min = (L->shared && (L->sgate.m.type == jx::T_Q4_K || L->sgate.m.type == jx::T_Q6_K))
                        ? jx::MFMA_MIN_SHARED_TOKENS_KQ
                        : jx::MFMA_MIN_SHARED_TOKENS;
     if (const char* f = std::getenv("JX_SMFMA_MIN")) L->smfma_min = std::max(1, std::atoi(f));
     if ((r = dalloc(L->dsync, 1)) != JX_OK) return bail(r);
+    if ((r = dalloc(L->hw, (size_t)L->k * L->F / 4)) != JX_OK) return bail(r);
+    if (hipMemset(L->hw, 0, (size_t)L->k * L->F / 4 * sizeof(uint64_t)) != hipSuccess)
+        return bail(fail(JX_ERR_HIP, "decode state"));
     if (hipMemset(L->dsync, 0, sizeof(jx::DecodeSync)) != hipSuccess) return bail(fail(JX_ERR_HIP, "decode state"));
     *out = L;
     return JX_OK;

@@ -1,6 +1,7 @@
-"""GPU parity of the fused one-token step (k_decode1: router rows, gate/up, down and the folded
-combine in one launch whose blocks hand over through device-coherent words) against the separate
-launches (JX_FWD_UNFUSED).  Both run the same arithmetic in the same order, so the bar is bit-exact:
+"""GPU parity of the fused one-token steps (k_decode1: router rows, gate/up, down and the folded
+combine in one launch whose blocks hand over through device-coherent words; k_decode_p: the same
+step as one block per CU for layers with many gate/up tiles) against the separate launches
+(JX_FWD_UNFUSED).  Both run the same arithmetic in the same order, so the bar is bit-exact:
 outputs, router logits, ids, weights, counts and the Q8_0 of x.  The layer's launch count tags each
 launch's logits and h's scale words (blocks poll for the tag), so the cases run many fused steps in
 a row, interleaved with separate and multi-token calls, on one layer.  The layer outputs
@@ -66,7 +67,15 @@ def took_fused(L, x, residual):
     L.forward(x, residual=residual)
     names = set(L.profile_read())
     L.profile(False)
-    return bool(names & {"decode_fused", "decode_fused_y"})
+    return bool(names & {"decode_fused", "decode_fused_y", "decode_fused_cu"})
+
+
+def took_cu(L, x):
+    L.profile(True)
+    L.forward(x)
+    names = set(L.profile_read())
+    L.profile(False)
+    return "decode_fused_cu" in names
 
 
 def step(L, x, fused, residual):
@@ -128,4 +137,43 @@ def test_fused_steps_back_to_back(moe, name):
     assert same(L.forward(xa)[0], want_a)
     for buf in (da, db, oa, ob):
         buf.free()
+    L.close()
+
+
+# k_decode_p: one block per CU (every block routes the token itself; the down tiles start once h's
+# tagged scale words say their slot is complete); taken by itself on the Mixtral-shaped layers.  It
+# needs at least as many gate/up row tiles as CUs (d_ff >= 32 * 256 here), so the smaller shapes keep
+# Mixtral's d_ff at d_model 512, in each format it is built for (an F16 router on one).
+EXTRA.update({
+    "cu_q4_0": synth.LayerConfig("cu_q4_0", 512, 8, 2, 14336, F.Q4_0),
+    "cu_q8_0": synth.LayerConfig("cu_q8_0", 512, 8, 2, 14336, F.Q8_0, router_type=F.F16),
+    "cu_q5k": synth.LayerConfig("cu_q5k", 512, 8, 2, 14336, F.Q5_K),
+    "cu_q6k": synth.LayerConfig("cu_q6k", 512, 8, 2, 14336, F.Q6_K),
+})
+CU = ["cu_q4_0", "cu_q8_0", "cu_q5k", "cu_q6k", "mixtral", "mixtral_q6k"]
+
+
+@pytest.mark.parametrize("name", CU)
+def test_fused_cu_step_matches_separate_launches(moe, port, monkeypatch, name):
+    monkeypatch.setenv("JX_DECP", "1")
+    cfg, lw = layer(name)
+    L = moe.MoELayer.from_weights(lw)
+    xs = synth.make_tokens(cfg, 4, seed=31)
+    x2 = synth.make_tokens(cfg, 2, seed=37)
+    assert took_cu(L, xs[:1])
+    for i in range(4):
+        x = xs[i:i + 1]
+        say(f"{name} token {i}: one block per CU vs separate")
+        got = step(L, x, True, False)
+        want = step(L, x, False, False)
+        for g, w_, what in zip(got, want, ("out", "ids", "weights", "counts", "logits", "xq8")):
+            assert same(g, w_) if g.dtype != np.uint8 else np.array_equal(g, w_), f"token {i}: {what}"
+        if i == 1:
+            L.forward(x2)
+    x = xs[3:4]
+    out = L.forward(x)[0]
+    want, _, _, _ = port.moe_forward(lw, x, np.array([0], np.int32))
+    err = rel_err(out, want)
+    say(f"{name}: one-block-per-CU step vs oracle max rel err {err:.2e}")
+    assert err <= REL_TOL
     L.close()
