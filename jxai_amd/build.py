@@ -59,7 +59,7 @@ def _compile(src: str) -> str:
     return obj
 
 
-PROBES = [os.path.join(HERE, "probe", "mfma_rate.hip")]
+PROBES = [os.path.join(HERE, "probe", "mfma_rate.hip"), os.path.join(HERE, "probe", "hbm_stream.hip")]
 
 
 def build_probes() -> list[str]:

@@ -149,8 +149,9 @@ EXTRA.update({
     "cu_q8_0": synth.LayerConfig("cu_q8_0", 512, 8, 2, 14336, F.Q8_0, router_type=F.F16),
     "cu_q5k": synth.LayerConfig("cu_q5k", 512, 8, 2, 14336, F.Q5_K),
     "cu_q6k": synth.LayerConfig("cu_q6k", 512, 8, 2, 14336, F.Q6_K),
+    "cu_q4k": synth.LayerConfig("cu_q4k", 512, 8, 2, 14336, F.Q4_K),
 })
-CU = ["cu_q4_0", "cu_q8_0", "cu_q5k", "cu_q6k", "mixtral", "mixtral_q6k"]
+CU = ["cu_q4_0", "cu_q8_0", "cu_q5k", "cu_q6k", "cu_q4k", "mixtral", "mixtral_q6k"]
 
 
 @pytest.mark.parametrize("name", CU)
