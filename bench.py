@@ -311,16 +311,19 @@ def main():
     a_dec = algorithmic(cfg, nd, r_dec["counts"])
     # the dominant decode kernel: the one-launch step where the layer takes it (all of the layer's
     # bytes), else the gate/up GEMV (the gate and up matrices of the selected experts)
-    fused = next((kk for kk in ("decode_fused_cu", "decode_fused") if kk in r_dec["prof"]), None)
+    # (decode_fused_y: the one-launch step writing y for a separate combine, top-k above 2)
+    fused = next((kk for kk in ("decode_fused_cu", "decode_fused", "decode_fused_y") if kk in r_dec["prof"]), None)
     role = fused or "gateup_gemv"
-    dg_ms, dg_n = r_dec["prof"].get(role, (0.0, 1))
+    if role not in r_dec["prof"]:
+        raise RuntimeError(f"decode: no {role} launch among the profiled kernels {sorted(r_dec['prof'])}")
+    dg_ms, dg_n = r_dec["prof"][role]
     dg_avg = dg_ms / max(dg_n, 1) / 1e3
     dbytes = a_dec["bytes"] if fused else a_dec["gateup_bytes"]
     dec_med = float(np.median(r_dec["step_ms"])) / 1e3
     dec_roof = {"bound": "hbm",
-                "kernel": ("k_decode_p<Q4_K> (the whole one-token step, one block per CU)" if fused == "decode_fused_cu"
-                           else "k_decode1<Q4_K> (the whole one-token step)" if fused
-                           else "k_gemv_gateup<Q4_K> (gate+up dequant-GEMV + SwiGLU)"),
+                "kernel": ("k_decode_p (the whole one-token step, one block per CU)" if fused == "decode_fused_cu"
+                           else "k_decode1 (the whole one-token step)" if fused
+                           else "k_gemv_gateup (gate+up dequant-GEMV + SwiGLU)"),
                 "achieved": dbytes / dg_avg / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": dbytes / dg_avg / 1e9 / HBM_PEAK_GBS,
                 "traffic": measured_traffic(role, nd),
