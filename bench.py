@@ -7,9 +7,14 @@ activations already resident in HBM (weights uploaded beforehand, outside the
 timed region).  Headline workload: the Mixtral-8x7B-shaped Q4_K MoE layer
 (d_model 4096, 8 experts, top-2, d_ff 14336):
   * prefill: 2048 tokens (matrix-core regime)     -> `value` (tokens/s)
-  * decode : 1 token (dequant-GEMV regime)         -> the `decode` object
-and `configs`, every configured layer shape at its token counts, each with the
-algorithmic bytes and int8 ops of the pass and their roofline fractions.
+  * decode : 1 token (dequant-GEMV regime)         -> the `decode` object, with
+    successive steps on distinct copies of the layer (as a model's layers follow
+    one another) so that each step reads its experts from HBM; `decode_resident`
+    is the same step repeated on one layer (its experts stay in the 256 MB
+    last-level cache)
+and `configs`, every configured layer shape at its token counts (few-token
+points cycled over copies of the layer likewise), each with the algorithmic
+bytes and int8 ops of the pass and their roofline fractions.
 
 Timing: K steps back to back between two device synchronizations give `value`
 and `ms_per_step` (nothing else is enqueued in that region: a timing event costs
@@ -17,9 +22,10 @@ the GPU 3-5 us); a second pass with one HIP event after each step on the
 forward's stream gives the per-step median and p10/p90.  Before timing,
 the device-pointer asynchronous path (the one timed) is checked bit for bit
 against the host-pointer path.  Kernel durations for the rooflines come from a
-second pass with HIP events around every launch.  The prefill GEMMs run
-v_mfma_f32_32x32x16_f16 on exact integer-valued operands, so their roofline
-peak is the fp16 one; the fraction of the int8 peak is reported beside it.
+second pass with HIP events around every launch.  The prefill roofline is the
+fraction of the dense int8 peak (the path's products are int8 x int8 block
+sums); the GEMMs run v_mfma_f32_32x32x16_f16 on exact integer-valued operands,
+so the fraction of the fp16 peak is reported beside it.
 The reference's CPU path (its own quant.cpp/tier.cpp built in oracle/_ref,
 AVX2 dot order) is timed on a bounded token sample on the host cores.
 """
@@ -99,19 +105,24 @@ class Hip:
 
 
 def measured_traffic(role, tokens):
-    """Memory bytes per launch of the kernel timed as `role` (gateup_mfma, down_mfma, gateup_gemv,
-    down_gemv) at `tokens` tokens from the rocprofv3 --pmc summary: the L2's read and write requests
-    to memory times their sizes (exact on a plain device copy of known size), or None when no
-    summary covers it."""
+    """(bytes, note): memory bytes per launch of the kernel timed as `role` (gateup_mfma, down_mfma,
+    decode_fused_cu, ...) at `tokens` tokens from the rocprofv3 --pmc summary (the L2's read and write
+    requests to memory times their sizes, exact on a plain device copy of known size), or None with the
+    reason when no summary of the loaded build covers it.  The summary carries the jx_build_id() of the
+    library it measured; a summary of another build is refused."""
+    from jxai_amd._lib import lib
+    build = lib().jx_build_id().decode()
     try:
         with open(TRAFFIC_FILE) as f:
             t = json.load(f)
     except (OSError, ValueError):
-        return None
+        return None, "no traffic summary"
+    if t.get("build_id") != build:
+        return None, f"stale: the traffic summary measured build {t.get('build_id')}, this is build {build}"
     k = t.get("kernels", {}).get(f"{role}@{tokens}")
     if not k:
-        return None
-    return k["read_bytes"] + k["write_bytes"]
+        return None, f"the traffic summary has no {role}@{tokens}"
+    return k["read_bytes"] + k["write_bytes"], f"rocprofv3 --pmc TCC_EA0 requests x size, build {build}"
 
 
 def copy_calibration():
@@ -151,29 +162,39 @@ def pct(a, q):
     return float(np.percentile(np.asarray(a), q))
 
 
-def run_gpu(hip, L, cfg, n, steps, warmup, regime=None):
+def run_gpu(hip, Ls, cfg, n, steps, warmup, regime=None):
     """A bit-exact check of the timed path, warm-up, K timed steps, a pass with one timing event per
-    step (the per-step distribution), then a profiled pass."""
+    step (the per-step distribution), then a profiled pass.  Ls: one layer, or several copies of it
+    (the same weights uploaded to distinct HBM) that step i runs as Ls[i % len(Ls)], as a model's
+    layers follow one another: each step then reads its experts from HBM, not from the 256 MB
+    last-level cache that holds a single layer's few-token working set across steps."""
     from jxai_amd import moe
+    Ls = Ls if isinstance(Ls, (list, tuple)) else [Ls]
     x = synth.make_tokens(cfg, n)
     xb = moe.DeviceBuffer(x.nbytes).upload(x)
     ob = moe.DeviceBuffer(x.nbytes)
-    want, ids, w, counts = L.forward(x, regime=regime)  # host-pointer path; routing of this batch
-    L.forward_device(xb, n, ob, sync=False, regime=regime, stream=hip.stream)
-    hip.sync()
-    got = ob.download(np.empty_like(x))
-    if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
-        raise SystemExit(f"bench: the timed device path differs from the host path ({cfg.name}, n={n})")
-    # warm-up right before the timed region (the check above leaves the GPU idle for a while)
-    for _ in range(warmup):
+    want, ids, w, counts = Ls[0].forward(x, regime=regime)  # host-pointer path; routing of this batch
+    for L in Ls:
         L.forward_device(xb, n, ob, sync=False, regime=regime, stream=hip.stream)
+        hip.sync()
+        got = ob.download(np.empty_like(x))
+        if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
+            raise SystemExit(f"bench: the timed device path differs from the host path ({cfg.name}, n={n})")
+
+    def steps_of(k, after=None):
+        for i in range(k):
+            Ls[i % len(Ls)].forward_device(xb, n, ob, sync=False, regime=regime, stream=hip.stream)
+            if after:
+                after(i)
+
+    # warm-up right before the timed region (the check above leaves the GPU idle for a while)
+    steps_of(warmup)
     hip.sync()
     moe.lib().jx_device_synchronize()
     # timed region: K steps of the production path back to back between two device synchronizations,
     # nothing else in the stream (a timing event costs the GPU 3-5 us, a tenth of a decode step)
     t0 = time.perf_counter()
-    for _ in range(steps):
-        L.forward_device(xb, n, ob, sync=False, regime=regime, stream=hip.stream)
+    steps_of(steps)
     hip.sync()
     moe.lib().jx_device_synchronize()
     t1 = time.perf_counter()
@@ -181,22 +202,49 @@ def run_gpu(hip, L, cfg, n, steps, warmup, regime=None):
     # each interval includes one event's cost)
     evs = hip.events(steps + 1)
     hip.record(evs[0])
-    for i in range(steps):
-        L.forward_device(xb, n, ob, sync=False, regime=regime, stream=hip.stream)
-        hip.record(evs[i + 1])
+    steps_of(steps, lambda i: hip.record(evs[i + 1]))
     hip.sync()
     step_ms = [hip.elapsed_ms(evs[i], evs[i + 1]) for i in range(steps)]
     hip.free(evs)
     # kernel durations: the same steps again with HIP events around every launch
-    L.profile(True)
-    for _ in range(steps):
-        L.forward_device(xb, n, ob, sync=False, regime=regime, stream=hip.stream)
+    for L in Ls:
+        L.profile(True)
+    steps_of(steps)
     hip.sync()
-    prof = L.profile_read()
-    L.profile(False)
+    prof = {}
+    for L in Ls:
+        for k, (ms, cnt) in L.profile_read().items():
+            a = prof.setdefault(k, [0.0, 0])
+            a[0] += ms
+            a[1] += cnt
+        L.profile(False)
+    prof = {k: tuple(v) for k, v in prof.items()}
+    # each layer's fused one-token steps completed every wait (asynchronous calls report it here)
+    for L in Ls:
+        L.status(wait=True)
     xb.free()
     ob.free()
-    return dict(wall_s=(t1 - t0) / steps, step_ms=step_ms, prof=prof, counts=counts)
+    return dict(wall_s=(t1 - t0) / steps, step_ms=step_ms, prof=prof, counts=counts, copies=len(Ls))
+
+
+CYCLE_BYTES = 1.2e9  # the copies a few-token point cycles through hold at least this many step bytes
+MAX_COPIES = 16
+
+
+def copies_for(cfg, n):
+    """Copies of the layer a few-token point cycles through so that the bytes its steps read (cycled)
+    exceed the last-level cache several times over: 1 where one step already reads more than
+    CYCLE_BYTES, and for prefill batches (512 tokens and more), as for the headline prefill line."""
+    if n >= 512:
+        return 1
+    per_expert = 2 * F.matrix_bytes(cfg.wtype, cfg.d_ff, cfg.d_model) + F.matrix_bytes(cfg.down_t, cfg.d_model,
+                                                                                         cfg.d_ff)
+    step = min(cfg.n_experts, n * cfg.top_k) * per_expert + synth.shared_bytes(cfg)
+    return int(min(MAX_COPIES, max(1, -(-CYCLE_BYTES // step))))
+
+
+def layer_copies(moe, lw, count):
+    return [moe.MoELayer.from_weights(lw) for _ in range(count)]
 
 
 def step_stats(r):
@@ -211,7 +259,8 @@ def point_line(cfg, n, r):
     """tok/s, algorithmic work and roofline fractions of one configured point."""
     a = algorithmic(cfg, n, r["counts"])
     t = r["wall_s"]
-    return {"tokens": n, "tok_s": n / t, "step_ms": step_stats(r), "bytes": a["bytes"], "int8_ops": a["ops"],
+    return {"tokens": n, "tok_s": n / t, "step_ms": step_stats(r), "layer_copies_cycled": r["copies"],
+            "bytes": a["bytes"], "int8_ops": a["ops"],
             "distinct_experts": a["distinct"], "hbm_frac": a["bytes"] / t / 1e9 / HBM_PEAK_GBS,
             "int8_frac": a["ops"] / t / 1e12 / INT8_PEAK_TOPS,
             "roofline_frac": max(a["bytes"] / (HBM_PEAK_GBS * 1e9), a["ops"] / (INT8_PEAK_TOPS * 1e12)) / t,
@@ -292,69 +341,103 @@ def main():
     gu_ms, gu_n = r_pre["prof"].get("gateup_mfma", (0.0, 1))
     gu_avg = gu_ms / max(gu_n, 1) / 1e3
     gu_rate = a_pre["gateup_ops"] / gu_avg / 1e12
+    traffic, traffic_note = measured_traffic("gateup_mfma", n)
+    # the fraction of the int8 peak (the path's arithmetic is int8 x int8 block sums); the GEMM issues
+    # v_mfma_f32_32x32x16_f16 on exact integer-valued operands, so its fraction of the fp16 peak and of
+    # the issued matrix-core work are reported beside it
     pre_roof = {"bound": "mfma", "kernel": "k_wgemm<Q4_K, gate+up> (fp16 matrix-core grouped GEMM + SwiGLU)",
-                "achieved": gu_rate, "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": gu_rate / FP16_PEAK_TFLOPS,
-                "traffic": measured_traffic("gateup_mfma", n),
+                "achieved": gu_rate, "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                "ops": "algorithmic int8 ops (2 per multiply-accumulate, 2*n*k*2*d*F per launch) per second in "
+                       "units of 1e12, against the dense int8 peak of 5.0 POP/s",
+                "frac": gu_rate / INT8_PEAK_TOPS,
+                "traffic": traffic, "traffic_note": traffic_note,
                 "avg_launch_us": gu_avg * 1e6,
-                "int8_peak_frac": gu_rate / INT8_PEAK_TOPS,
+                "fp16_peak_frac": gu_rate / FP16_PEAK_TFLOPS,
                 "issued_fp16_frac": issued_per_algorithmic(cfg) * gu_rate / FP16_PEAK_TFLOPS,
                 "layer_int8_frac": a_pre["ops"] / s_pre / 1e12 / INT8_PEAK_TOPS}
 
     nd = args.decode_tokens
-    print(f"[bench] decode {nd} token(s)", file=sys.stderr, flush=True)
     dsteps = max(steps * 10, 50)
-    # decode steps run ~5% slower over the first few hundred (clock and cache warm-up after the
-    # prefill), so the untimed warm-up runs DECODE_WARMUP of them before the timed region
-    r_dec = run_gpu(hip, L, cfg, nd, dsteps, max(args.warmup * 4, DECODE_WARMUP), "gemv")
-    s_dec = r_dec["wall_s"]
-    a_dec = algorithmic(cfg, nd, r_dec["counts"])
-    # the dominant decode kernel: the one-launch step where the layer takes it (all of the layer's
-    # bytes), else the gate/up GEMV (the gate and up matrices of the selected experts)
-    # (decode_fused_y: the one-launch step writing y for a separate combine, top-k above 2)
-    fused = next((kk for kk in ("decode_fused_cu", "decode_fused", "decode_fused_y") if kk in r_dec["prof"]), None)
-    role = fused or "gateup_gemv"
-    if role not in r_dec["prof"]:
-        raise RuntimeError(f"decode: no {role} launch among the profiled kernels {sorted(r_dec['prof'])}")
-    dg_ms, dg_n = r_dec["prof"][role]
-    dg_avg = dg_ms / max(dg_n, 1) / 1e3
-    dbytes = a_dec["bytes"] if fused else a_dec["gateup_bytes"]
-    dec_med = float(np.median(r_dec["step_ms"])) / 1e3
-    dec_roof = {"bound": "hbm",
+    dwarm = max(args.warmup * 4, DECODE_WARMUP)
+
+    def decode_line(r, label):
+        s_dec = r["wall_s"]
+        a_dec = algorithmic(cfg, nd, r["counts"])
+        # the dominant decode kernel: the one-launch step where the layer takes it (all of the layer's
+        # bytes), else the gate/up GEMV (the gate and up matrices of the selected experts)
+        # (decode_fused_y: the one-launch step writing y for a separate combine, top-k above 2)
+        fused = next((kk for kk in ("decode_fused_cu", "decode_fused", "decode_fused_y") if kk in r["prof"]), None)
+        role = fused or "gateup_gemv"
+        if role not in r["prof"]:
+            raise RuntimeError(f"decode: no {role} launch among the profiled kernels {sorted(r['prof'])}")
+        dg_ms, dg_n = r["prof"][role]
+        dg_avg = dg_ms / max(dg_n, 1) / 1e3
+        dbytes = a_dec["bytes"] if fused else a_dec["gateup_bytes"]
+        dec_med = float(np.median(r["step_ms"])) / 1e3
+        tr, tr_note = measured_traffic(role, nd)
+        roof = {"bound": "hbm",
                 "kernel": ("k_decode_p (the whole one-token step, one block per CU)" if fused == "decode_fused_cu"
                            else "k_decode1 (the whole one-token step)" if fused
                            else "k_gemv_gateup (gate+up dequant-GEMV + SwiGLU)"),
                 "achieved": dbytes / dg_avg / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": dbytes / dg_avg / 1e9 / HBM_PEAK_GBS,
-                "traffic": measured_traffic(role, nd),
+                "traffic": tr, "traffic_note": tr_note,
                 "avg_launch_us": dg_avg * 1e6,
                 "layer_hbm_frac": a_dec["bytes"] / s_dec / 1e9 / HBM_PEAK_GBS,
                 "layer_hbm_frac_median_step": a_dec["bytes"] / dec_med / 1e9 / HBM_PEAK_GBS}
+        return {"value": nd / s_dec, "unit": "tok/s", "tokens": nd, "ms_per_step": s_dec * 1e3,
+                "layer_copies_cycled": r["copies"], "weights_from": label,
+                "step_ms": step_stats(r), "roofline": roof,
+                "kernels_us_per_step": {k: v[0] * 1e3 / dsteps for k, v in r["prof"].items()}}
+
+    # decode as a model runs it: successive steps on distinct copies of the layer, so every step reads
+    # its two experts from HBM (copies_for), then on one layer (its experts stay in the last-level cache)
+    ncop = copies_for(cfg, nd)
+    print(f"[bench] decode {nd} token(s), {ncop} copies of the layer in turn", file=sys.stderr, flush=True)
+    extra = layer_copies(moe, lw, ncop - 1)
+    r_cyc = run_gpu(hip, [L] + extra, cfg, nd, dsteps, dwarm, "gemv")
+    for Lc in extra:
+        Lc.close()
+    del extra
+    print(f"[bench] decode {nd} token(s), one layer", file=sys.stderr, flush=True)
+    # the untimed warm-up runs DECODE_WARMUP steps: decode steps run ~5% slower over the first few
+    # hundred after the prefill (clock and cache warm-up)
+    r_res = run_gpu(hip, L, cfg, nd, dsteps, dwarm, "gemv")
+    decode = decode_line(r_cyc, f"HBM: {ncop} copies of the layer, one per step in turn")
+    decode_res = decode_line(r_res, "one layer: its two experts stay in the 256 MB last-level cache across steps")
 
     cpu = None
     if not args.no_cpu:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         cpu = cpu_baseline(lw, cfg, n)
     L.close()
-    del lw
 
     configs = None
     if not args.no_configs:
         configs = {}
-        layers = {}
+        cur = None
         for name, tok in POINTS:
-            if name not in layers:
-                layers.clear()
+            if cur is None or cur[0] != name:
+                if cur is not None:
+                    for Lc in cur[3]:
+                        Lc.close()
                 c = synth.CONFIGS[name]
                 print(f"[bench] configs: {c.describe}", file=sys.stderr, flush=True)
-                layers[name] = (c, moe.MoELayer.from_weights(synth.make_layer(c)))
-            c, Lc = layers[name]
-            print(f"[bench] configs: {name} @ {tok}", file=sys.stderr, flush=True)
+                lwc = synth.make_layer(c)
+                cur = (name, c, lwc, [moe.MoELayer.from_weights(lwc)])
+            _, c, lwc, Lcs = cur
+            ncp = copies_for(c, tok)
+            if len(Lcs) < ncp:
+                Lcs.extend(layer_copies(moe, lwc, ncp - len(Lcs)))
+            print(f"[bench] configs: {name} @ {tok} ({ncp} copies in turn)", file=sys.stderr, flush=True)
             reps = steps if tok >= 512 else max(steps * 5, 50)
-            r = run_gpu(hip, Lc, c, tok, reps, args.warmup if tok >= 512 else max(args.warmup, DECODE_WARMUP))
+            r = run_gpu(hip, Lcs[:ncp], c, tok, reps,
+                        args.warmup if tok >= 512 else max(args.warmup, DECODE_WARMUP))
             configs[f"{name}@{tok}"] = point_line(c, tok, r)
-        for _, Lc in layers.values():
-            Lc.close()
+        if cur is not None:
+            for Lc in cur[3]:
+                Lc.close()
+    del lw
 
     line = {
         "metric": METRIC,
@@ -373,13 +456,13 @@ def main():
                    "n_experts": cfg.n_experts, "top_k": cfg.top_k, "d_ff": cfg.d_ff,
                    "weights": F.NAMES[cfg.wtype], "tokens": n},
         "step_ms": step_stats(r_pre),
-        "timed_path_check": "device-pointer async path == host path, bit for bit (every measured point)",
+        "timed_path_check": "device-pointer async path == host path, bit for bit (every measured point, every "
+                            "layer copy); jx_moe_layer_status clean after every pass",
         "roofline": pre_roof,
         "cpu_baseline": cpu,
         "kernels_ms_per_step": {k: v[0] / steps for k, v in r_pre["prof"].items()},
-        "decode": {"value": nd / s_dec, "unit": "tok/s", "tokens": nd, "ms_per_step": s_dec * 1e3,
-                   "step_ms": step_stats(r_dec), "roofline": dec_roof,
-                   "kernels_us_per_step": {k: v[0] * 1e3 / dsteps for k, v in r_dec["prof"].items()}},
+        "decode": decode,
+        "decode_resident": decode_res,
         "configs": configs,
     }
     print(json.dumps(line), flush=True)

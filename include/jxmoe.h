@@ -52,9 +52,16 @@ enum {
     JX_FWD_FORCE_MFMA = 1u << 3,  /* force the prefill (matrix-core GEMM) regime  */
     JX_FWD_RESIDUAL = 1u << 4,    /* x is the residual stream before ffn_norm: the
                                      whole FFN step of forward_token (see below)   */
-    JX_FWD_UNFUSED = 1u << 5      /* one-token steps as separate router, gate/up and
+    JX_FWD_UNFUSED = 1u << 5,     /* one-token steps as separate router, gate/up and
                                      down launches instead of the single fused
-                                     launch (same results; for comparison)          */
+                                     launch (same results).  Use it when kernels
+                                     of other streams or processes may hold the
+                                     GPU's CUs during the step (see below)          */
+    JX_FWD_TEST_GIVEUP = 1u << 6  /* test hook, no counterpart in the reference: a
+                                     fused one-token step's waits between its
+                                     blocks give up after a few polls (every kernel
+                                     still ends normally), to exercise the error
+                                     reporting below; its outputs are invalid       */
 };
 
 /* One MoE layer, as bound by bind_tensors (src/transformer.cpp:2142-2186).
@@ -127,6 +134,21 @@ void jx_moe_layer_destroy(jx_moe_layer* layer);
  *   out    = x + acc                          (2762-2764; out may alias x) */
 int jx_moe_forward(jx_moe_layer* layer, const float* x, int32_t n_tok, float* out, int32_t* topk_ids,
                    float* topk_w, int32_t* expert_counts, void* stream, uint32_t flags);
+/* One-token steps may run as one launch whose blocks hand data to one another
+ * (router rows -> gate/up -> down), which needs the launch's blocks resident
+ * together.  A kernel of another stream or process that holds CUs meanwhile
+ * delays the step; past a bound (2^18 polls, about a second) a wait gives up
+ * and that step's outputs are invalid.  The synchronous call then returns
+ * JX_ERR_HIP.  For an asynchronous call (JX_FWD_ASYNC) the failure is reported
+ * by jx_moe_layer_status, and by the layer's next jx_moe_forward, which then
+ * returns JX_ERR_HIP without doing any work; later calls run normally.
+ * JX_FWD_UNFUSED keeps the separate launches, which have no such window.
+ *
+ * jx_moe_layer_status: JX_OK, or JX_ERR_HIP if a fused step of this layer gave
+ * up a wait since the last report (the report clears it).  wait != 0 first
+ * synchronizes the stream of the layer's last forward.  No counterpart in the
+ * reference (its MoE block runs synchronously on the CPU). */
+int jx_moe_layer_status(jx_moe_layer* layer, int32_t wait);
 
 /* Router logits of the last forward, [n_tok][E] fp32, copied to host memory
  * (the reference's router_logits vector, src/transformer.cpp:2589-2594). */
@@ -254,6 +276,11 @@ int jx_dev_free(void* ptr);
 int jx_memcpy_htod(void* dst, const void* src, size_t bytes);
 int jx_memcpy_dtoh(void* dst, const void* src, size_t bytes);
 int jx_device_synchronize(void);
+
+/* Identity of the loaded build: the first 16 hex digits of the SHA-256 over
+ * the library's sources and this header, fixed at compile time.  Measurements
+ * recorded with one build carry it.  No counterpart in the reference. */
+const char* jx_build_id(void);
 
 /* Last error message of the calling thread ("" if none). */
 const char* jx_moe_last_error(void);

@@ -19,6 +19,7 @@ JX_FWD_FORCE_GEMV = 1 << 2
 JX_FWD_FORCE_MFMA = 1 << 3
 JX_FWD_RESIDUAL = 1 << 4
 JX_FWD_UNFUSED = 1 << 5
+JX_FWD_TEST_GIVEUP = 1 << 6  # test hook: the fused one-token step's waits give up (outputs invalid)
 
 JX_ACT_SILU = 0
 JX_ACT_GELU_TANH = 1
@@ -32,7 +33,8 @@ EXPORTS = [
     "jx_memcpy_dtoh", "jx_device_synchronize", "jx_moe_last_error", "jx_tier_record", "jx_tier_lfru_score",
     "jx_gguf_open", "jx_gguf_close", "jx_gguf_tensor_count", "jx_gguf_find_tensor", "jx_gguf_tensor_info",
     "jx_gguf_get_u32", "jx_gguf_get_f32", "jx_gguf_get_str", "jx_gguf_moe_layer_desc", "jx_gguf_last_error",
-    "jx_matmul_quant_f32_dev", "jx_matmul_qkv_quant_f32_dev",
+    "jx_matmul_quant_f32_dev", "jx_matmul_qkv_quant_f32_dev", "jx_moe_layer_status",
+    "jx_build_id",
 ]
 
 _fp = C.POINTER(C.c_float)
@@ -72,12 +74,14 @@ def lib() -> C.CDLL:
                       "(the MoE path has no CPU fallback)")
     L = C.CDLL(LIB_PATH)
     L.jx_moe_last_error.restype = C.c_char_p
+    L.jx_build_id.restype = C.c_char_p
     L.jx_moe_init.argtypes = [C.c_int32]
     L.jx_moe_layer_create.argtypes = [C.POINTER(LayerDesc), C.POINTER(_vp)]
     L.jx_moe_layer_destroy.argtypes = [_vp]
     L.jx_moe_layer_destroy.restype = None
     L.jx_moe_forward.argtypes = [_vp, _vp, C.c_int32, _vp, _vp, _vp, _vp, _vp, C.c_uint32]
     L.jx_moe_last_logits.argtypes = [_vp, _vp, C.c_int32]
+    L.jx_moe_layer_status.argtypes = [_vp, C.c_int32]
     L.jx_moe_last_xq8.argtypes = [_vp, _vp, C.c_int32]
     L.jx_moe_profile.argtypes = [_vp, C.c_int32]
     L.jx_moe_profile_read.argtypes = [_vp, C.c_char_p, C.c_size_t, C.POINTER(C.c_double), C.POINTER(C.c_int64),

@@ -14,6 +14,7 @@ links jxai_amd/libjxmoe.so.  Flags that matter for parity:
 from __future__ import annotations
 
 import concurrent.futures as cf
+import hashlib
 import os
 import shutil
 import subprocess
@@ -23,6 +24,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libjxmoe.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "jxmoe.h")
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc" if os.path.exists("/opt/rocm/bin/hipcc") else "hipcc")
@@ -44,12 +46,25 @@ def sources() -> list[str]:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 
 
-def _compile(src: str) -> str:
+def source_id() -> str:
+    """First 16 hex digits of the SHA-256 over every source under csrc and include/jxmoe.h (names and
+    bytes): compiled in as jx_build_id(), so a measurement recorded with one build can be told apart
+    from another."""
+    h = hashlib.sha256()
+    for path in sources() + sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")) + [HEADER]:
+        h.update(os.path.basename(path).encode() + b"\0")
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def _compile(src: str, sid: str) -> str:
     obj = os.path.join(OBJ, os.path.basename(src).rsplit(".", 1)[0] + ".o")
+    define = f'-DJX_SOURCE_SHA="{sid}"'
     if src.endswith(".cpp"):
-        cmd = [CXX, *HOST_CFLAGS, "-c", src, "-o", obj]
+        cmd = [CXX, *HOST_CFLAGS, define, "-c", src, "-o", obj]
     else:
-        cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
+        cmd = [HIPCC, *CFLAGS, define, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     msgs = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:
@@ -59,35 +74,19 @@ def _compile(src: str) -> str:
     return obj
 
 
-PROBES = [os.path.join(HERE, "probe", "mfma_rate.hip"), os.path.join(HERE, "probe", "hbm_stream.hip")]
-
-
-def build_probes() -> list[str]:
-    """Standalone measurement programs (jxai_amd/probe/*.hip -> executables beside them)."""
-    out = []
-    for src in PROBES:
-        exe = src[:-4]
-        cmd = [HIPCC, *[f for f in CFLAGS if f != "-fPIC"], src, "-o", exe]
-        r = subprocess.run(cmd, capture_output=True, text=True)
-        if r.returncode != 0:
-            raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}{r.stderr}")
-        out.append(exe)
-    return out
-
-
 def build(verbose: bool = True) -> str:
     if shutil.which(HIPCC) is None and not os.path.exists(HIPCC):
         raise RuntimeError("hipcc not found: the MoE path needs ROCm's hipcc to build")
     os.makedirs(OBJ, exist_ok=True)
     srcs = sources()
+    sid = source_id()
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
+        objs = list(ex.map(lambda src: _compile(src, sid), srcs))
     tmp = LIB + ".tmp"
     subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-o", tmp, *objs], check=True)
     os.replace(tmp, LIB)
-    probes = build_probes()
     if verbose:
-        print(f"built {LIB}, " + ", ".join(os.path.relpath(p, HERE) for p in probes))
+        print(f"built {LIB} (source id {sid})")
     return LIB
 
 

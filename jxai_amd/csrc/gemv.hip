@@ -1349,10 +1349,12 @@ static void down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, 
 // device-scope atomic loads and stores only (a device-scope fence writes back the whole L2 on this
 // part).  Calls on one layer must be stream-ordered.
 constexpr int DEC_THREADS = 512;
-constexpr int DEC_SPIN_LIMIT = 1 << 18;  // polls (each a device-coherent round trip) before giving up
 
-__device__ __forceinline__ void dec_fail(DecodeSync* s) {
-    __hip_atomic_store(&s->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// A wait that gave up: the device word, and the host-visible one the runtime checks on the layer's next
+// call whatever its flags (so an asynchronous caller learns of it too).
+__device__ __forceinline__ void dec_fail(const Decode1Args& a) {
+    __hip_atomic_store(&a.sync->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (a.herr) __hip_atomic_store(a.herr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // Wave 0: wait until the first n logit words carry this launch's tag, then put the logits in lg
@@ -1370,9 +1372,9 @@ __device__ void dec_wait_logits(const Decode1Args& a, int n, float* lg) {
             w1 = __hip_atomic_load(a.sync->tag + 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             ok = ok && (uint32_t)(w1 >> 32) == a.epoch;
         }
-        const bool all = __all(ok);
-        if (all || it >= DEC_SPIN_LIMIT) {
-            if (!all && lane == 0) dec_fail(a.sync);
+        const bool all = __all(ok && !a.giveup_test);
+        if (all || it >= (int)a.spin_limit) {
+            if (!all && lane == 0) dec_fail(a);
             if (lane < n) lg[lane] = __uint_as_float((uint32_t)w0);
             if (64 + lane < n) lg[64 + lane] = __uint_as_float((uint32_t)w1);
             return;
@@ -1457,10 +1459,10 @@ k_decode1(Decode1Args a) {
                 uint64_t sv = 0;
                 for (int it = 0;; ++it) {
                     if (tid < KB) sv = __hip_atomic_load(ss + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    const bool ok = tid >= KB || ((uint32_t)sv & DEC_HTAG_MASK) == a.htag;
+                    const bool ok = (tid >= KB || ((uint32_t)sv & DEC_HTAG_MASK) == a.htag) && !a.giveup_test;
                     if (__syncthreads_and(ok)) break;  // block-uniform
-                    if (it >= DEC_SPIN_LIMIT) {
-                        if (tid == 0) dec_fail(a.sync);
+                    if (it >= (int)a.spin_limit) {
+                        if (tid == 0) dec_fail(a);
                         break;
                     }
                     __builtin_amdgcn_s_sleep(1);
@@ -1676,13 +1678,13 @@ void launch_decode1(const Decode1Args& a, int gtype, int dtype, hipStream_t st) 
 // Layers whose gate/up row tiles outnumber the CUs several times (Mixtral-shaped: 896 tiles on 256
 // CUs; k_decode1 leaves its down blocks to the CUs its gate/up blocks free, unevenly) as one grid of
 // one 1024-thread block per CU:
-//   route    the last E blocks run one router row each (the row and the token chain-major in LDS, the
+//   route    the first E blocks run one router row each (the row and the token chain-major in LDS, the
 //            vec_dot_f32 chains of k_route_small) and publish the logit as a tagged word; every block
 //            forms the Q8_0 of x in LDS meanwhile, then selects the experts from the logits (the same
 //            selection in every block).  Block 0 writes the logits, the Q8_0 of x and the dispatch
 //            tables for the caller; each block first zeroes the output rows of its first-slot down
 //            tile (the folded combine adds into them).
-//   gate/up  (slot, row tile) tiles b, b + G, b + 2G, b + 3G of the G blocks, one per group of four
+//   gate/up  (slot, row tile) tiles G-1-b, 2G-1-b, 3G-1-b, 4G-1-b of the G blocks, one per group of four
 //            waves (the 4-wave single-token GEMV), so every CU streams about the same bytes.  h's
 //            Q8_0 quants go out as 64-bit words carrying the launch number, its scales with the
 //            launch's tag in their low mantissa bits, so no store waits for another.
@@ -1690,10 +1692,11 @@ void launch_decode1(const Decode1Args& a, int gtype, int dtype, hipStream_t st) 
 //            GEMV's unit split and wave-order sum): the first weight units in flight, then h read
 //            until every word of the slot carries this launch's number or tag, and p * y added into
 //            the output (two adds onto an exact zero per element).
-// The step is bit-identical to the separate launches.  Every block waits on others, so the grid must
-// be resident at once: one block per CU (its LDS leaves no room for a second) and a grid of one block
-// per CU; every wait is bounded anyway (giving up sets sync->err, which the synchronous forward
-// reports).  The zeroing of a row is ordered before the block's own slot-1 h stores, which the other
+// The step is bit-identical to the separate launches.  Every down tile waits on h from blocks across
+// the grid, so the grid must be resident at once: one block per CU (its LDS leaves no room for a
+// second) and a grid of one block per CU.  A kernel of another stream or process holding CUs delays
+// the step; every wait is bounded, and giving up sets sync->err and the host-visible herr, which the
+// runtime reports on the synchronous call, on jx_moe_layer_status and on the layer's next forward.  The zeroing of a row is ordered before the block's own slot-1 h stores, which the other
 // down tile of that row waits for (decodep_fits checks the tile layout gives every zeroing block one).
 // Measured Mixtral-shaped, host clock over 300 queued steps: 42.2 us per step against 46.3 us for the
 // separate launches (route, gate/up GEMV, down GEMV).
@@ -1713,6 +1716,10 @@ __host__ __device__ inline size_t decodep_xoff(int d, int f, int E) {
     const size_t r = decodep_route_bytes(d, E), hb = act_lds_bytes(1, f, false);
     return r > hb ? r : hb;
 }
+
+// Gate/up tile of group g of block b among nb: the list runs from the last block down, so the first
+// blocks (the router rows) hold the fewest tiles.
+__host__ __device__ inline int decodep_gu_tile(int b, int g, int nb) { return nb - 1 - b + g * nb; }
 
 // Dynamic LDS of k_decode_p: the router staging or the down projection's h, then the Q8_0 of x, and at
 // least 96 KB so that no CU holds two of the blocks (each waits on the others).
@@ -1742,7 +1749,9 @@ k_decode_p(Decode1Args a) {
                                __HIP_MEMORY_SCOPE_AGENT);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // complete before the block's h stores (the barriers below)
-    const int rr = NB - 1 - b;  // router row of this block: the last E blocks hold the fewest gate/up tiles
+    // router row of this block: the first E blocks, which the dispatcher starts first, so the routing
+    // never waits on a block that has not started; they hold the fewest gate/up tiles (decodep_gu_tile)
+    const int rr = b;
     if (rr < E) {  // router row rr against the token, chain-major in LDS (as k_decode1's router blocks)
         float* lds = reinterpret_cast<float*>(smem);
         const int S = rs_stride(d), RS = 16 * S;
@@ -1823,10 +1832,10 @@ k_decode_p(Decode1Args a) {
     }
     __syncthreads();
 
-    // ---- gate/up: tile b + grp * G of the (slot, row tile) list on waves 4 grp .. 4 grp + 3
+    // ---- gate/up: tile decodep_gu_tile(b, grp) of the (slot, row tile) list on waves 4 grp .. 4 grp + 3
     {
         const int grp = wave >> 2, lw = wave & 3, mat = lw >> 1, kw = lw & 1;
-        const int t = b + grp * NB;
+        const int t = decodep_gu_tile(b, grp, NB);
         const bool active = t < ng;
         const int slot = active ? t / a.G.nrt : 0, rt = active ? t - slot * a.G.nrt : 0;
         const int e = s_e[slot];
@@ -1893,9 +1902,9 @@ k_decode_p(Decode1Args a) {
                         sv = __hip_atomic_load(ss + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         ok = ok && ((uint32_t)sv & DEC_HTAG_MASK) == a.htag;
                     }
-                    if (__syncthreads_and(ok)) break;  // block-uniform
-                    if (it >= DEC_SPIN_LIMIT) {
-                        if (tid == 0) dec_fail(a.sync);
+                    if (__syncthreads_and(ok && !a.giveup_test)) break;  // block-uniform
+                    if (it >= (int)a.spin_limit) {
+                        if (tid == 0) dec_fail(a);
                         break;
                     }
                     __builtin_amdgcn_s_sleep(1);
@@ -1936,7 +1945,10 @@ bool decodep_fits(int gtype, int dtype, int d, int f, int E, int k, bool shared,
     if (ng > DP_GROUPS * nb) return false;
     for (int b = 0; b < nb && b < down_nrt; ++b) {
         bool s1 = false;
-        for (int j = 0; j < DP_GROUPS; ++j) s1 = s1 || (b + j * nb >= gate_nrt && b + j * nb < ng);
+        for (int j = 0; j < DP_GROUPS; ++j) {
+            const int t = decodep_gu_tile(b, j, nb);
+            s1 = s1 || (t >= gate_nrt && t < ng);
+        }
         if (!s1) return false;
     }
     return true;

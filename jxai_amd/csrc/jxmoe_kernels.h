@@ -283,6 +283,9 @@ struct Decode1Args {
     ActQ8 hqs;                  //   [1][d_ff_shared] Q8_0 of its h
     float* ysh = nullptr;       //   [d] its output, for launch_combine
     uint64_t* hw = nullptr;     // k_decode_p: [k][d_ff / 4] words of h, (epoch << 32) | four Q8_0 quants
+    uint32_t* herr = nullptr;   // host-visible word set (system scope) when a bounded wait gives up
+    uint32_t spin_limit = 0;    // polls before a wait gives up
+    uint32_t giveup_test = 0;   // nonzero: every wait treats its words as not yet published (error-path test)
 };
 // Whether k_decode1 is built for this shape: E router rows (+ the shared-expert gate row) <=
 // SMALL_GROUP_MAX_E, even k <= MAX_SLOTS_DEC, d % 32 == 0 and d <= 8192, d_ff and the shared d_ff

@@ -301,6 +301,13 @@ struct jx_moe_layer {
     // of such launches so far (JX_NO_FUSED=1 keeps the separate launches: A/B measurement)
     jx::DecodeSync* dsync = nullptr;
     uint64_t* hw = nullptr;  // k_decode_p's h: [k][d_ff / 4] words of (launch number << 32 | four quants)
+    // pinned host word the fused launches set when a bounded wait between their blocks gives up (their
+    // outputs are then invalid); read on the synchronous path, by jx_moe_layer_status and at the entry
+    // of every forward, so asynchronous callers learn of it too
+    uint32_t* herr = nullptr;
+    uint32_t* herr_dev = nullptr;
+    uint32_t spin_limit = 1u << 18;  // polls (each a device-coherent round trip) before a wait gives up
+    hipStream_t last_st = nullptr;   // stream of the last forward (jx_moe_layer_status waits on it)
     uint32_t dec_epoch = 0;
     bool fused_decode = true;
     bool force_fused = false;  // JX_FUSED=1: also where the separate launches measured faster
@@ -394,6 +401,8 @@ int ensure_workspace(jx_moe_layer* L, int n) {
     if (L->shared) {
         WS(L->hqs.q, (size_t)cap * L->Fs);
         WS(L->hqs.s, (size_t)cap * L->Fs / 32);
+        // the fused step's shared down tiles poll these scale words for the launch's tag, as for hq.s
+        HIPCHK(hipMemset(L->hqs.s, 0, (size_t)cap * L->Fs / 32 * sizeof(float2)));
         L->hqs.K = L->Fs;
         WS(L->ysh, (size_t)cap * L->d);
         const size_t fspad = ((size_t)L->Fs + 255) / 256 * 256;
@@ -416,6 +425,7 @@ void free_layer(jx_moe_layer* L) {
                     L->xf, L->dsync, L->hw};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
+    if (L->herr) (void)hipHostFree(L->herr);
     L->xh.release();
     L->hh.release();
     L->hhs.release();
@@ -602,6 +612,9 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         a.sync = L->dsync;
         a.epoch = L->dec_epoch;
         a.htag = 1u + L->dec_epoch % 8191u;  // never 0, the low bits of every untagged scale
+        a.herr = L->herr_dev;
+        a.giveup_test = (flags & JX_FWD_TEST_GIVEUP) ? 1u : 0u;
+        a.spin_limit = a.giveup_test ? 64u : L->spin_limit;
         if (L->shared) {
             a.sh = 1;
             a.SG = L->sgate.m;
@@ -915,7 +928,10 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
     if ((r = upload_matrix(D->down_type, L->E, L->d, L->F, D->down_exps, L->down, st, true)) != JX_OK) return bail(r);
     if (L->shared) {
         if ((r = upload_matrix(D->sh_gate_type, 1, L->Fs, L->d, D->sh_gate, L->sgate, st, true)) != JX_OK) return bail(r);
-        L->sgate.m.act = D->activation;
+        // The shared expert is always SwiGLU: src/transformer.cpp:2741-2745 calls matmul_swiglu_quant_f32
+        // without hp_.use_gelu (default false, include/quant.h:361); GELU-tanh reaches only the routed
+        // experts (2721-2724).
+        L->sgate.m.act = jx::ACT_SILU;
         if ((r = upload_matrix(D->sh_up_type, 1, L->Fs, L->d, D->sh_up, L->sup, st, true)) != JX_OK) return bail(r);
         if ((r = upload_matrix(D->sh_down_type, 1, L->d, L->Fs, D->sh_down, L->sdown, st, true)) != JX_OK) return bail(r);
         if (D->sh_gate_inp) {
@@ -972,12 +988,37 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
     if (hipMemset(L->hw, 0, (size_t)L->k * L->F / 4 * sizeof(uint64_t)) != hipSuccess)
         return bail(fail(JX_ERR_HIP, "decode state"));
     if (hipMemset(L->dsync, 0, sizeof(jx::DecodeSync)) != hipSuccess) return bail(fail(JX_ERR_HIP, "decode state"));
+    if (hipHostMalloc(reinterpret_cast<void**>(&L->herr), sizeof(uint32_t), hipHostMallocMapped | hipHostMallocCoherent) !=
+            hipSuccess ||
+        hipHostGetDevicePointer(reinterpret_cast<void**>(&L->herr_dev), L->herr, 0) != hipSuccess)
+        return bail(fail(JX_ERR_HIP, "decode error word"));
+    __atomic_store_n(L->herr, 0u, __ATOMIC_RELEASE);
     *out = L;
     return JX_OK;
 }
 
 void jx_moe_layer_destroy(jx_moe_layer* L) {
     if (L) free_layer(L);
+}
+
+namespace {
+// A fused one-token launch of this layer gave up a wait between its blocks: its outputs were invalid.
+// Clear the error words (the launch count keeps going, so no later launch can match a word that launch
+// left) and report it.
+int take_fused_error(jx_moe_layer* L) {
+    if (!L->herr || __atomic_load_n(L->herr, __ATOMIC_ACQUIRE) == 0) return JX_OK;
+    __atomic_store_n(L->herr, 0u, __ATOMIC_RELEASE);
+    return fail(JX_ERR_HIP,
+                "fused one-token step: a wait between its blocks timed out (another kernel held the GPU's CUs); "
+                "the outputs of that step are invalid");
+}
+}  // namespace
+
+int jx_moe_layer_status(jx_moe_layer* L, int32_t wait) {
+    if (!L) return fail(JX_ERR_INVALID, "null layer");
+    HIPCHK(hipSetDevice(L->device));
+    if (wait) HIPCHK(hipStreamSynchronize(L->last_st ? L->last_st : L->own));
+    return take_fused_error(L);
 }
 
 int jx_moe_forward(jx_moe_layer* L, const float* x, int32_t n_tok, float* out, int32_t* topk_ids, float* topk_w,
@@ -993,9 +1034,12 @@ int jx_moe_forward(jx_moe_layer* L, const float* x, int32_t n_tok, float* out, i
     if ((int64_t)n_tok * L->k > INT_MAX / 2 || (int64_t)n_tok * L->d * 4 >= ((int64_t)1 << 32))
         return fail(JX_ERR_UNSUPPORTED, "n_tok too large for one call (split the batch)");
     HIPCHK(hipSetDevice(L->device));
-    int r = ensure_workspace(L, n_tok);
+    // a failure of an earlier fused step that the caller has not been told of (asynchronous calls)
+    int r = take_fused_error(L);
     if (r != JX_OK) return r;
+    if ((r = ensure_workspace(L, n_tok)) != JX_OK) return r;
     hipStream_t st = stream ? reinterpret_cast<hipStream_t>(stream) : L->own;
+    L->last_st = st;
     const bool dev = flags & JX_FWD_DEVICE_PTRS;
     const size_t xd = (size_t)n_tok * L->d;
     const float* xin = x;
@@ -1055,15 +1099,7 @@ int jx_moe_forward(jx_moe_layer* L, const float* x, int32_t n_tok, float* out, i
     if (!(flags & JX_FWD_ASYNC)) {
         HIPCHK(hipStreamSynchronize(st));
         if (L->prof.on && (r = resolve_profile(L)) != JX_OK) return r;
-        if (L->dec_used) {  // a bounded wait of the fused one-token launch gave up: start its state over
-            uint32_t err = 0;
-            HIPCHK(hipMemcpy(&err, &L->dsync->err, sizeof(err), hipMemcpyDeviceToHost));
-            if (err) {
-                HIPCHK(hipMemset(L->dsync, 0, sizeof(jx::DecodeSync)));
-                L->dec_epoch = 0;
-                return fail(JX_ERR_HIP, "fused one-token step: a wait between its blocks timed out");
-            }
-        }
+        if ((r = take_fused_error(L)) != JX_OK) return r;  // a bounded wait of a fused launch gave up
     }
     return JX_OK;
 }
@@ -1382,5 +1418,10 @@ int jx_device_synchronize(void) {
     HIPCHK(hipDeviceSynchronize());
     return JX_OK;
 }
+
+#ifndef JX_SOURCE_SHA
+#define JX_SOURCE_SHA "unknown"
+#endif
+const char* jx_build_id(void) { return JX_SOURCE_SHA; }
 
 }  // extern "C"

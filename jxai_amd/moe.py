@@ -18,7 +18,7 @@ import numpy as np
 
 from . import formats as F
 from ._lib import (JX_FWD_DEVICE_PTRS, JX_FWD_ASYNC, JX_FWD_FORCE_GEMV, JX_FWD_FORCE_MFMA, JX_FWD_RESIDUAL,  # noqa: F401
-                   JX_FWD_UNFUSED,
+                   JX_FWD_UNFUSED, JX_FWD_TEST_GIVEUP,
                    JxError, LayerDesc, check, lib)
 
 _inited = {}
@@ -140,13 +140,18 @@ class MoELayer:
         return out, ids, w, counts
 
     def forward_device(self, x: DeviceBuffer, n: int, out: DeviceBuffer, sync: bool = True, regime=None,
-                       stream=None, fused: bool = True) -> None:
+                       stream=None, fused: bool = True, extra_flags: int = 0) -> None:
         """MoE block over device-resident activations (no host copies), enqueued on `stream`
         (a hipStream_t as an integer; None: the layer's own stream)."""
-        flags = JX_FWD_DEVICE_PTRS | (0 if sync else JX_FWD_ASYNC) | (0 if fused else JX_FWD_UNFUSED)
+        flags = JX_FWD_DEVICE_PTRS | (0 if sync else JX_FWD_ASYNC) | (0 if fused else JX_FWD_UNFUSED) | extra_flags
         flags |= {None: 0, "gemv": JX_FWD_FORCE_GEMV, "mfma": JX_FWD_FORCE_MFMA}[regime]
         st = None if stream is None else C.c_void_p(stream)
         check(lib().jx_moe_forward(self.handle, x.ptr, n, out.ptr, None, None, None, st, flags), "jx_moe_forward")
+
+    def status(self, wait: bool = True) -> None:
+        """Raise JxError if a fused one-token step of this layer gave up a wait between its blocks since
+        the last report (jx_moe_layer_status; wait: synchronize the last forward's stream first)."""
+        check(lib().jx_moe_layer_status(self.handle, 1 if wait else 0), "jx_moe_layer_status")
 
     def last_logits(self, n: int) -> np.ndarray:
         out = np.empty((n, self.E), np.float32)

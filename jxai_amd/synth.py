@@ -188,6 +188,12 @@ CONFIGS = {
     # the toy layer with the gemma family's GELU-tanh gate (the reference's use_gelu)
     "toy_gelu": LayerConfig("toy_gelu", 512, 8, 2, 1024, F.Q4_0, act=1, decode_tokens=(1, 64),
                             describe="Toy MoE FFN d512 E8 top-2 F1024 Q4_0, GELU-tanh gate"),
+    # a GELU-tanh layer with a sigmoid-gated shared expert: the routed experts take GELU, the shared expert
+    # SiLU (the reference's shared-expert call never passes use_gelu)
+    "toy_gelu_sh": LayerConfig("toy_gelu_sh", 512, 8, 2, 1024, F.Q4_0, d_ff_shared=1024, shared_gate=True, act=1,
+                               decode_tokens=(1, 64),
+                               describe="Toy MoE FFN d512 E8 top-2 F1024 Q4_0, GELU-tanh gate, shared 1024 "
+                                        "(SiLU, sigmoid gate)"),
     # the toy layer in its residual-stream form: ffn_norm before, post_ffw_norm and the residual add after
     "toy_norm": LayerConfig("toy_norm", 512, 8, 2, 1024, F.Q4_0, norms=True, decode_tokens=(1, 64),
                             describe="Toy MoE FFN d512 E8 top-2 F1024 Q4_0 with ffn_norm / post_ffw_norm"),

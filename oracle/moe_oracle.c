@@ -902,7 +902,7 @@ void jxo_rms_norm(float* out, const float* x, const float* weight, int64_t size,
 /* One token through the MoE block (src/transformer.cpp:2589-2757, residual
  * excluded): routed experts in descending-logit order, accum += p * down
  * (contracted to an fma by the reference build), then the shared expert
- * scaled by sigmoid(vec_dot_f32(gate_inp, x)) or 1. */
+ * (always SiLU-gated, 2741-2745) scaled by sigmoid(vec_dot_f32(gate_inp, x)) or 1. */
 static void moe_token(const jxo_moe_desc* L, const float* x, float* out, int32_t* ids, float* probs,
                       float* logits, int32_t order, float* h, float* y) {
     const int32_t E = L->n_experts, d = L->d_model, Fd = L->d_ff, k = L->top_k;
@@ -924,8 +924,10 @@ static void moe_token(const jxo_moe_desc* L, const float* x, float* out, int32_t
     }
     if (L->d_ff_shared > 0 && L->sh_gate && L->sh_up && L->sh_down) {
         const int32_t Fs = L->d_ff_shared;
+        /* always SiLU: the shared expert's call (transformer.cpp:2741-2745) leaves use_gelu at its
+         * default, false (quant.h:361), whatever the layer's activation */
         jxo_matmul_swiglu_quant_f32(L->sh_gate_type, L->sh_gate, L->sh_up_type, L->sh_up, x, h, Fs, d,
-                                    L->activation, order);
+                                    0, order);
         jxo_matmul_quant_f32(L->sh_down_type, L->sh_down, h, y, d, Fs, order);
         float sh = 1.0f;
         if (L->sh_gate_inp) {

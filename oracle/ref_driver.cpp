@@ -209,7 +209,7 @@ int32_t jxr_moe_forward(const jxo_moe_desc* L, const float* x, int32_t n_tok,
             std::vector<float> sh_buf(sh_dim, 0.0f);
             moe::matmul_swiglu_quant_f32(static_cast<GGMLType>(L->sh_gate_type), L->sh_gate,
                                          static_cast<GGMLType>(L->sh_up_type), L->sh_up,
-                                         xn, sh_buf.data(), sh_dim, d, L->activation != 0);
+                                         xn, sh_buf.data(), sh_dim, d);  // use_gelu left at false, as 2741-2745
             moe::matmul_quant_f32(static_cast<GGMLType>(L->sh_down_type), L->sh_down,
                                   sh_buf.data(), down_buf.data(), d, sh_dim);
             float sh_scale = 1.0f;

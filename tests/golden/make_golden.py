@@ -58,6 +58,12 @@ F3_CASES = [
     ("dsv2lite_q50", 1, [0]),
     ("dsv2lite_q50", 32, ("tiles", 16, 16)),
 ]
+# a GELU layer with a sigmoid-gated shared expert (GELU on the routed experts only, SiLU on the shared one):
+# 64 tokens take the routed GEMMs (32-pair tiles) and the shared expert's 16-token GEMV
+GELU_SH_CASES = [
+    ("toy_gelu_sh", 1, [0]),
+    ("toy_gelu_sh", 64, ("tiles", 32, 16)),
+]
 # the residual-stream form (rms_norm before, post_ffw_norm and the residual add after the block)
 RESID_CASES = [
     ("toy_norm", 1, [0]),
@@ -316,6 +322,11 @@ def main() -> None:
         for name, n, rows in RESID_CASES:
             print(make_case(ref, name, n, rows, tag="_resid", residual=True))
         return
+    if "--gelu-sh" in sys.argv:  # only the GELU + shared-expert cases
+        ref = Oracle("reference", avx512=False)
+        for name, n, rows in GELU_SH_CASES:
+            print(make_case(ref, name, n, rows))
+        return
     if "--avx512-child" in sys.argv:
         ref = Oracle("reference", avx512=True)
         print(make_case(ref, "toy", 1, [0], tag="_avx512"))
@@ -325,6 +336,8 @@ def main() -> None:
     print(make_units(ref))
     print(make_gguf_case(ref))
     for name, n, rows in CASES:
+        print(make_case(ref, name, n, rows))
+    for name, n, rows in GELU_SH_CASES:
         print(make_case(ref, name, n, rows))
     for name, n, rows in RESID_CASES:
         print(make_case(ref, name, n, rows, tag="_resid", residual=True))

@@ -99,7 +99,8 @@ def test_matmul_swiglu_quant_f32(moe, port, qt, rows, cols, use_gelu):
 
 # ------------------------------------------------------------------ layer vs the golden vectors
 GOLDEN_CASES = ["toy_n1", "qwen15moe_n1", "qwen15moe_n64", "mixtral_n1", "mixtral_n512", "mixtral_n2048",
-                "qwen3moe_n2048", "dsv2lite_n32", "toy_gelu_n1", "toy_gelu_n64", "toy_norm_n1_resid",
+                "qwen3moe_n2048", "dsv2lite_n32", "toy_gelu_n1", "toy_gelu_n64", "toy_gelu_sh_n1", "toy_gelu_sh_n64",
+                "toy_norm_n1_resid",
                 "toy_norm_n64_resid"]
 
 
@@ -148,7 +149,10 @@ def test_layer_vs_golden(moe, case):
                                            # GELU-tanh gate in every gate/up epilogue
                                            ("toy_gelu", 1, None), ("toy_gelu", 40, "gemv"), ("toy_gelu", 300, "mfma"),
                                            ("toy_gelu", 24, None), ("gelu_q4k", 1, None), ("gelu_q4k", 2, "gemv"),
-                                           ("gelu_q4k", 20, "gemv"), ("gelu_q4k", 200, "mfma")])
+                                           ("gelu_q4k", 20, "gemv"), ("gelu_q4k", 200, "mfma"),
+                                           # GELU routed experts beside a SiLU shared expert, every shared form
+                                           ("toy_gelu_sh", 2, "gemv"), ("toy_gelu_sh", 40, None),
+                                           ("toy_gelu_sh", 300, "mfma")])
 def test_layer_regimes_vs_oracle(moe, port, name, n, regime):
     say(f"{name} n={n} regime={regime}")
     cfg, lw = layer(name)

@@ -34,7 +34,7 @@ EXTRA = {
     "toy_sh_nogate": synth.LayerConfig("toy_sh_nogate", 512, 8, 2, 1024, F.Q8_0, d_ff_shared=544),
 }
 
-FUSED = ["toy", "toy_gelu", "toy_f16r", "toy_q5k", "toy_q6k", "toy_k4", "qwen3moe", "gelu_q4k", "qwen15_norm",
+FUSED = ["toy", "toy_gelu", "toy_gelu_sh", "toy_f16r", "toy_q5k", "toy_q6k", "toy_k4", "qwen3moe", "gelu_q4k", "qwen15_norm",
          "toy_sh_nogate", "toy_bf16r_sh", "qwen15moe", "mixtral_norm", "mixtral", "mixtral_q6k"]
 
 
@@ -178,3 +178,68 @@ def test_fused_cu_step_matches_separate_launches(moe, port, monkeypatch, name):
     say(f"{name}: one-block-per-CU step vs oracle max rel err {err:.2e}")
     assert err <= REL_TOL
     L.close()
+
+
+# ------------------------------------------------------------------ a wait that gives up is reported
+@pytest.mark.parametrize("name,cu", [("toy", False), ("qwen15moe", False), ("cu_q4k", True)])
+def test_fused_giveup_is_reported(moe, monkeypatch, name, cu):
+    """JX_FWD_TEST_GIVEUP makes every wait of the fused launch give up after a few polls (the kernels
+    end normally; the outputs are invalid).  The failure must reach the caller on every path: the
+    synchronous call returns an error; after an asynchronous call, jx_moe_layer_status reports it once,
+    and otherwise the layer's next forward does, without running.  The step after a report is
+    bit-identical to the separate launches (the launch count goes on, so nothing left by the failed
+    launch can pass a later wait)."""
+    if cu:
+        monkeypatch.setenv("JX_DECP", "1")
+    cfg, lw = layer(name)
+    L = moe.MoELayer.from_weights(lw)
+    xs = synth.make_tokens(cfg, 2, seed=53)
+    x = xs[:1]
+    assert (took_cu(L, x) if cu else took_fused(L, x, False))
+    want = L.forward(x, fused=False)[0]
+    dx = moe.DeviceBuffer(x.nbytes).upload(x)
+    do = moe.DeviceBuffer(x.nbytes)
+    giveup = moe.JX_FWD_TEST_GIVEUP
+
+    def fused_ok():
+        L.forward_device(dx, 1, do)
+        return same(do.download(np.empty_like(x)), want)
+
+    say(f"{name}: synchronous step whose waits give up")
+    with pytest.raises(moe.JxError, match="timed out"):
+        L.forward_device(dx, 1, do, extra_flags=giveup)
+    assert fused_ok()
+    say(f"{name}: asynchronous step whose waits give up, then jx_moe_layer_status")
+    L.forward_device(dx, 1, do, sync=False, extra_flags=giveup)
+    with pytest.raises(moe.JxError, match="timed out"):
+        L.status(wait=True)
+    L.status(wait=True)  # reported once
+    assert fused_ok()
+    say(f"{name}: asynchronous step whose waits give up, then the next forward")
+    L.forward_device(dx, 1, do, sync=False, extra_flags=giveup)
+    moe.lib().jx_device_synchronize()
+    with pytest.raises(moe.JxError, match="timed out"):
+        L.forward(xs[1:2])
+    assert fused_ok()
+    assert same(L.forward(x)[0], want)
+    dx.free()
+    do.free()
+    L.close()
+
+
+def test_fused_shared_first_step_after_recreate(moe):
+    """A layer with a shared expert, created where a destroyed layer of the same shape ran fused steps:
+    its first fused step must not take the old layer's tagged h scale words (the shared h's scale words
+    start untagged), so it equals the separate launches bit for bit."""
+    cfg, lw = layer("qwen15_norm")
+    cfg2 = synth.LayerConfig("qwen15_norm2", cfg.d_model, cfg.n_experts, cfg.top_k, cfg.d_ff, cfg.wtype,
+                             d_ff_shared=cfg.d_ff_shared, shared_gate=True)
+    lw2 = synth.make_layer(cfg2, seed=77)
+    x = synth.make_tokens(cfg, 1, seed=59)
+    for rnd in range(3):
+        say(f"recreate round {rnd}")
+        L = moe.MoELayer.from_weights(lw if rnd % 2 == 0 else lw2)
+        first = L.forward(x)[0]
+        assert took_fused(L, x, False)
+        assert same(first, L.forward(x, fused=False)[0])
+        L.close()

@@ -451,7 +451,7 @@ F3_GOLDEN_CASES = ["toy_q5k_n1", "toy_q5k_n64", "toy_q6k_n1", "toy_q6k_n64", "to
 ROUTER16_GOLDEN_CASES = ["toy_f16r_n1", "toy_f16r_n64", "toy_bf16r_sh_n1", "toy_bf16r_sh_n64"]
 GOLDEN_CASES = F3_GOLDEN_CASES + ROUTER16_GOLDEN_CASES + ["toy_n1", "qwen15moe_n1", "qwen15moe_n64", "mixtral_n1", "mixtral_n512",
                 "mixtral_n2048", "qwen3moe_n2048", "dsv2lite_n32", "toy_gelu_n1", "toy_gelu_n64",
-                "toy_norm_n1_resid", "toy_norm_n64_resid"]
+                "toy_gelu_sh_n1", "toy_gelu_sh_n64", "toy_norm_n1_resid", "toy_norm_n64_resid"]
 
 
 def _layer(name, n):
@@ -533,7 +533,7 @@ def _block_float64(port, lw, x, ids, probs):
             Fs = cfg.d_ff_shared
             g = deq_matrix(t, lw.sh_gate, Fs, d) @ xa
             u = deq_matrix(t, lw.sh_up, Fs, d) @ xa
-            h = ((_gelu64(g) if cfg.act else g / (1 + np.exp(-g))) * u).astype(np.float32)
+            h = (g / (1 + np.exp(-g)) * u).astype(np.float32)  # SiLU whatever cfg.act (transformer.cpp:2741-2745)
             sh = 1.0
             if lw.sh_gate_inp is not None:
                 sh = 1 / (1 + np.exp(-(lw.sh_gate_inp.astype(np.float64) @ x[i].astype(np.float64))))
@@ -541,7 +541,8 @@ def _block_float64(port, lw, x, ids, probs):
     return out
 
 
-@pytest.mark.parametrize("name,n", [("toy", 3), ("dsv2lite", 2), ("qwen15moe", 2), ("toy_gelu", 3), ("toy_q5k", 3),
+@pytest.mark.parametrize("name,n", [("toy", 3), ("dsv2lite", 2), ("qwen15moe", 2), ("toy_gelu", 3), ("toy_gelu_sh", 3),
+                                    ("toy_q5k", 3),
                                     ("toy_q6k", 3), ("toy_q50", 3), ("dsv2lite_q50", 2)])
 def test_moe_block_float64_restatement(port, name, n):
     cfg, lw, x = _layer(name, 64 if name == "qwen15moe" else n)
@@ -556,3 +557,30 @@ def test_moe_block_float64_restatement(port, name, n):
     ref64 = _block_float64(port, lw, x, ids, w)
     rel = np.abs(out - ref64).max(axis=1) / np.abs(ref64).max(axis=1)
     assert rel.max() < 2e-4, rel
+
+
+def test_shared_expert_is_silu_in_gelu_layer(port):
+    """A GELU-tanh layer's shared expert is SwiGLU: transformer.cpp:2741-2745 calls matmul_swiglu_quant_f32
+    without use_gelu (default false, quant.h:361); only the routed experts take the layer's GELU (2721-2724).
+    The block output must equal the routed-only output plus fma(sigmoid(gate), down(SiLU h)), and must not
+    equal the same sum with GELU h, which differs here by far more than the bar."""
+    cfg, lw, x = _layer("toy_gelu_sh", 4)
+    from dataclasses import replace
+    import copy
+    routed_cfg = replace(cfg, d_ff_shared=0, shared_gate=False)
+    routed_lw = copy.copy(lw)
+    routed_lw.cfg, routed_lw.sh_gate, routed_lw.sh_up, routed_lw.sh_down, routed_lw.sh_gate_inp = \
+        routed_cfg, None, None, None, None
+    full = port.moe_forward(lw, x)[0]
+    routed = port.moe_forward(routed_lw, x)[0]
+    d, Fs = cfg.d_model, cfg.d_ff_shared
+    for t in range(x.shape[0]):
+        sh = np.float32(1.0) / (np.float32(1.0) + np.exp(-np.float32(port.vec_dot_f32(lw.sh_gate_inp, x[t]))))
+        ys = {}
+        for gelu in (False, True):
+            h = port.matmul_swiglu_quant_f32(cfg.wtype, lw.sh_gate, cfg.wtype, lw.sh_up, x[t], Fs, d, use_gelu=gelu)
+            y = port.matmul_quant_f32(cfg.sh_down_t, lw.sh_down, h, d, Fs)
+            ys[gelu] = (sh.astype(np.float64) * y + routed[t]).astype(np.float32)
+        assert np.array_equal(full[t].view(np.uint32), ys[False].view(np.uint32))
+        gap = np.abs(ys[True] - ys[False]).max() / np.abs(ys[False]).max()
+        assert gap > 1e-3, gap

@@ -70,3 +70,68 @@ def test_noalloc_refuses_wide_matrix(moe):
     rc = lib.jx_matmul_quant_f32_noalloc(m.handle, C.c_void_p(1), C.c_void_p(1), None)  # refused before any use
     assert rc == 2 and b"no-allocation scratch" in lib.jx_moe_last_error()
     m.close()
+
+
+def _hip():
+    h = C.CDLL("libamdhip64.so")
+    h.hipStreamCreate.argtypes = [C.POINTER(C.c_void_p)]
+    h.hipStreamDestroy.argtypes = [C.c_void_p]
+    h.hipStreamSynchronize.argtypes = [C.c_void_p]
+    h.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+    h.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+    h.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]
+    h.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+    h.hipGraphExecDestroy.argtypes = [C.c_void_p]
+    h.hipGraphDestroy.argtypes = [C.c_void_p]
+    h.hipMemGetInfo.argtypes = [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+    return h
+
+
+def test_noalloc_graph_capture_and_no_allocation(moe):
+    """Captured into a HIP graph (global capture mode, where an allocation inside the call would be an
+    error), replayed with new inputs and eager calls between the replays: every replay equals the eager
+    call on the same input bit for bit.  Free device memory is unchanged across 200 calls."""
+    h = _hip()
+    lib = moe.lib()
+    qt, rows, cols = F.Q4_K, 256, 4096
+    W = synth.quant_matrix(synth.sub_seed("noalloc", "graph_w"), qt, rows, cols)
+    m = moe.QMatrix(qt, W, rows, cols)
+    xs = [synth.normal_f32(synth.sub_seed("noalloc", f"graph_x{i}"), cols, 1.0) for i in range(4)]
+    xb = moe.DeviceBuffer(cols * 4).upload(xs[0])
+    ob = moe.DeviceBuffer(rows * 4)
+    eb = moe.DeviceBuffer(rows * 4)
+    st = C.c_void_p()
+    assert h.hipStreamCreate(C.byref(st)) == 0
+    say("noalloc: capture into a graph")
+    assert h.hipStreamBeginCapture(st, 0) == 0  # hipStreamCaptureModeGlobal
+    rc = lib.jx_matmul_quant_f32_noalloc(m.handle, xb.ptr, ob.ptr, st)
+    g = C.c_void_p()
+    assert h.hipStreamEndCapture(st, C.byref(g)) == 0
+    assert rc == 0, lib.jx_moe_last_error()
+    ex = C.c_void_p()
+    assert h.hipGraphInstantiate(C.byref(ex), g, None, None, 0) == 0
+    for i, x in enumerate(xs):
+        say(f"noalloc: replay {i}")
+        xb.upload(x)
+        assert lib.jx_matmul_quant_f32_noalloc(m.handle, xb.ptr, eb.ptr, st) == 0  # eager, same input
+        assert h.hipStreamSynchronize(st) == 0
+        want = eb.download(np.empty(rows, np.float32))
+        assert h.hipGraphLaunch(ex, st) == 0
+        assert h.hipStreamSynchronize(st) == 0
+        got = ob.download(np.empty(rows, np.float32))
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"replay {i}"
+    h.hipGraphExecDestroy(ex)
+    h.hipGraphDestroy(g)
+    say("noalloc: free memory across 200 calls")
+    free0, free1, total = C.c_size_t(), C.c_size_t(), C.c_size_t()
+    assert h.hipStreamSynchronize(st) == 0
+    assert h.hipMemGetInfo(C.byref(free0), C.byref(total)) == 0
+    for _ in range(200):
+        assert lib.jx_matmul_quant_f32_noalloc(m.handle, xb.ptr, ob.ptr, st) == 0
+    assert h.hipStreamSynchronize(st) == 0
+    assert h.hipMemGetInfo(C.byref(free1), C.byref(total)) == 0
+    assert free1.value == free0.value
+    h.hipStreamDestroy(st)
+    for b in (xb, ob, eb):
+        b.free()
+    m.close()
