@@ -27,6 +27,7 @@
 //         bits (fp32 activations only)
 //   Q8_0  four 32-blocks: lanes of half h take half h of each
 #include <algorithm>
+#include <vector>
 
 #include "jxmoe_device.h"
 #include "jxmoe_dispatch.h"
@@ -174,6 +175,12 @@ struct Fmt<T_Q6_K> {
         c.d = *reinterpret_cast<const uint16_t*>((ok ? W.ex + e * W.ex_es + t * 64 : W.pad_ex) + m * 2);
     }
 };
+
+// Activation elements one GEMV unit covers.
+template <int TYPE>
+__host__ __device__ constexpr int dp_unit_elems() {
+    return (TYPE == T_Q5_K || TYPE == T_Q6_K) ? 128 : (TYPE == T_Q4_K ? 256 : 32 * Fmt<TYPE>::BPU);
+}
 
 template <int TYPE>
 __host__ __device__ constexpr int n_units(int nkb) {
@@ -1705,6 +1712,8 @@ constexpr int DP_THREADS = 1024, DP_WAVES = DP_THREADS / 64, DP_GROUPS = DP_WAVE
 // (more requests in flight slow the stream); likewise four gate/up groups streaming at once against two
 // (42.2 / 42.2 us) or one (51 us), and 16 down waves against 8 (42.4 / 42.2 us).
 constexpr int DP_DEPTH = 2;
+constexpr int DP_HDEPTH = 3;         // units of h words in flight per poller wave
+constexpr int DP_MAX_UNITS = 16384 / 128;  // down units of a d_ff <= 16384 (128-element units at most)
 constexpr size_t DP_LDS_MAX = 156 * 1024;
 
 __host__ __device__ inline size_t decodep_route_bytes(int d, int E) {
@@ -1717,9 +1726,32 @@ __host__ __device__ inline size_t decodep_xoff(int d, int f, int E) {
     return r > hb ? r : hb;
 }
 
-// Gate/up tile of group g of block b among nb: the list runs from the last block down, so the first
-// blocks (the router rows) hold the fewest tiles.
-__host__ __device__ inline int decodep_gu_tile(int b, int g, int nb) { return nb - 1 - b + g * nb; }
+// Gate/up tile (slot * nrt + row tile) of group g of block b among nb, or -1: top-2, so 2 nrt tiles,
+// q = 2 nrt / nb per block and one more on the last r = 2 nrt % nb blocks.  The tiles form a list in
+// row-tile order (both slots of a row tile side by side); its first positions go to the blocks with q
+// tiles, which are done first, round-robin over them, so the low row tiles -- the low K of h, which every
+// down wave consumes first -- are ready first.  The router rows sit on the first blocks, among those with
+// fewer tiles.  Within a position pair (both slots of a row tile) the slots alternate with the group, so
+// each block streams both slots (decodep_fits relies on it).  -1 where the layout does not hold
+// (decodep_fits then refuses the shape).
+__host__ __device__ inline int decodep_gu_tile(int b, int g, int nb, int nrt) {
+    const int T = 2 * nrt, q = T / nb, r = T % nb, n0 = nb - r;
+    int p, pl, C;
+    if (b < n0) {
+        if (g >= q) return -1;
+        C = n0;
+        pl = g * n0 + b;
+        p = pl;
+    } else {
+        if (g > q) return -1;
+        C = r;
+        pl = g * r + (b - n0);
+        p = n0 * q + pl;
+    }
+    if ((n0 * q) % 2) return -1;  // a position pair would straddle the two classes
+    const int rt = p / 2, sl = (p + (C % 2 == 0 ? pl / C : 0)) % 2;
+    return sl * nrt + rt;
+}
 
 // Dynamic LDS of k_decode_p: the router staging or the down projection's h, then the Q8_0 of x, and at
 // least 96 KB so that no CU holds two of the blocks (each waits on the others).
@@ -1735,8 +1767,10 @@ k_decode_p(Decode1Args a) {
     __shared__ float red[DP_WAVES][32];
     __shared__ int s_e[MAX_SLOTS_DEC];
     __shared__ float s_p[MAX_SLOTS_DEC];
+    __shared__ int hflag[DP_MAX_UNITS];  // per down unit: h staged in LDS (the tile's value, 0 before)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 31, h = lane >> 5;
     const int E = a.E, d = a.d, k = a.k, NB = gridDim.x, b = blockIdx.x;
+    if (tid < DP_MAX_UNITS) hflag[tid] = 0;  // before the block's first barrier
     const int ng = a.G.nrt * k, nd = a.D.nrt * k;
     int8_t* xq = smem + decodep_xoff(d, a.hq.K, E);  // Q8_0 of x: quants [d], then (scale, sum) [d / 32]
     float2* xs = reinterpret_cast<float2*>(xq + d);
@@ -1750,7 +1784,7 @@ k_decode_p(Decode1Args a) {
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // complete before the block's h stores (the barriers below)
     // router row of this block: the first E blocks, which the dispatcher starts first, so the routing
-    // never waits on a block that has not started; they hold the fewest gate/up tiles (decodep_gu_tile)
+    // never waits on a block that has not started; they are among those with fewer gate/up tiles
     const int rr = b;
     if (rr < E) {  // router row rr against the token, chain-major in LDS (as k_decode1's router blocks)
         float* lds = reinterpret_cast<float*>(smem);
@@ -1835,8 +1869,8 @@ k_decode_p(Decode1Args a) {
     // ---- gate/up: tile decodep_gu_tile(b, grp) of the (slot, row tile) list on waves 4 grp .. 4 grp + 3
     {
         const int grp = wave >> 2, lw = wave & 3, mat = lw >> 1, kw = lw & 1;
-        const int t = decodep_gu_tile(b, grp, NB);
-        const bool active = t < ng;
+        const int t = decodep_gu_tile(b, grp, NB, a.G.nrt);
+        const bool active = t >= 0 && t < ng;
         const int slot = active ? t / a.G.nrt : 0, rt = active ? t - slot * a.G.nrt : 0;
         const int e = s_e[slot];
         const ActLds A{xq, xs, nullptr, d};
@@ -1868,8 +1902,16 @@ k_decode_p(Decode1Args a) {
     }
 
     // ---- down: tiles b, b + G of the (slot, row tile) list on waves 0 .. DOWN_WAVES - 1 (the single-token
-    // down GEMV's unit split and wave-order sum, so the step is bit-identical to the separate launches)
-    static_assert(DOWN_WAVES <= DP_WAVES, "down waves");
+    // down GEMV's unit split and wave-order sum, so the step is bit-identical to the separate launches).
+    // h is taken unit by unit as it is published: waves DOWN_WAVES .. 2 DOWN_WAVES - 1 each serve one down
+    // wave, reading the h words of its units' K ranges (DP_HDEPTH units ahead) until every word carries
+    // this launch's number (quants) or tag (scales), staging them into the LDS copy of h and raising the
+    // unit's LDS flag; the down wave streams its weight units (DP_DEPTH ahead) and consumes each once its
+    // flag is up, in ascending order as before.  The low K of h is published first (decodep_gu_tile), so
+    // the down streams start while the last gate/up tiles are still running.
+    static_assert(2 * DOWN_WAVES <= DP_WAVES, "a poller wave per down wave");
+    constexpr int UE = dp_unit_elems<TD>();  // h elements per down unit
+    static_assert(UE / 4 <= 64 && UE % 32 == 0, "one h word per lane");
     for (int j = 0; j < 2; ++j) {
         const int t = b + j * NB;
         if (t >= nd) break;  // block-uniform
@@ -1878,50 +1920,82 @@ k_decode_p(Decode1Args a) {
         const float p = s_p[slot];
         const int K = a.hq.K, KB = K / 32;
         const ActLds A{smem, reinterpret_cast<const float2*>(smem + K), nullptr, K};
-        const int nu = wave < DOWN_WAVES ? n_units<TD>(a.D.nkb) : 0;
+        const int nu = n_units<TD>(a.D.nkb);
+        const int flag = j + 1;  // this tile's value of a unit's LDS flag
+        if (j) __syncthreads();  // the previous tile's reduction has read red and its h
         float acc[1] = {0.0f};
-        kloop_d<TD, DP_DEPTH>(
-            a.D, e, rt, wave, nu, DOWN_WAVES, m, h,
-            [&] {  // after the first two units' loads: read the slot's h until every word carries this launch's
-                   // number (the quant words) or tag (the scale words), then stage it
-                if (j) __syncthreads();  // the previous tile's LDS reads are done
-                constexpr int QPER = 16384 / 4 / DP_THREADS;  // d_ff <= 16384
-                const uint64_t* qw = a.hw + (size_t)slot * (K / 4);
-                const uint64_t* ss = reinterpret_cast<const uint64_t*>(a.hq.s + (size_t)slot * KB);
-                uint64_t qv[QPER], sv = 0;
-                for (int it = 0;; ++it) {
-                    bool ok = true;
+        if (wave < DOWN_WAVES) {
+            // the down wave: weight units wave, wave + DOWN_WAVES, ... with DP_DEPTH in flight
+            typename Fmt<TD>::Raw r[DP_DEPTH];
 #pragma unroll
-                    for (int q = 0; q < QPER; ++q) {
-                        const int i = tid + q * DP_THREADS;
-                        qv[q] = i < K / 4 ? __hip_atomic_load(qw + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                          : (uint64_t)a.epoch << 32;
-                        ok = ok && (uint32_t)(qv[q] >> 32) == a.epoch;
-                    }
-                    if (tid < KB) {
-                        sv = __hip_atomic_load(ss + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        ok = ok && ((uint32_t)sv & DEC_HTAG_MASK) == a.htag;
-                    }
-                    if (__syncthreads_and(ok && !a.giveup_test)) break;  // block-uniform
-                    if (it >= (int)a.spin_limit) {
-                        if (tid == 0) dec_fail(a);
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(1);
-                }
+            for (int i = 0; i < DP_DEPTH; ++i) {
+                const int u = wave + i * DOWN_WAVES;
+                Fmt<TD>::load(r[i], a.D, e, rt, u, m, h, u < nu);
+            }
+            for (int u = wave; u < nu; u += DP_DEPTH * DOWN_WAVES) {
 #pragma unroll
-                for (int q = 0; q < QPER; ++q) {
-                    const int i = tid + q * DP_THREADS;
-                    if (i < K / 4) reinterpret_cast<uint32_t*>(smem)[i] = (uint32_t)qv[q];
+                for (int i = 0; i < DP_DEPTH; ++i) {
+                    const int ui = u + i * DOWN_WAVES;
+                    if (ui >= nu) break;  // wave-uniform
+                    // its h is staged once the flag is up (the poller raises it on giving up too)
+                    for (int it = 0; __hip_atomic_load(hflag + ui, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != flag;
+                         ++it) {
+                        if (it >= 64 * (int)a.spin_limit) {  // a backstop: the poller bounds the wait
+                            if (lane == 0) dec_fail(a);
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(1);
+                    }
+                    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                    unit_accum<TD, 1>(r[i], A, ui, h, 1, a.D.nkb, acc);
+                    const int un = ui + DP_DEPTH * DOWN_WAVES;
+                    Fmt<TD>::load(r[i], a.D, e, rt, un, m, h, un < nu);
                 }
-                if (tid < KB) reinterpret_cast<uint64_t*>(smem + K)[tid] = sv & ~(uint64_t)DEC_HTAG_MASK;
-                __syncthreads();
-            },
-            [&](const typename Fmt<TD>::Raw& c, int u) {
-                unit_accum<TD, 1>(c, A, u, h, 1, a.D.nkb, acc);
-            });
+            }
+        } else if (wave < 2 * DOWN_WAVES) {
+            // the poller of down wave pw: its units' h words, DP_HDEPTH units ahead
+            const int pw = wave - DOWN_WAVES;
+            const uint64_t* qw = a.hw + (size_t)slot * (K / 4);
+            const uint64_t* ss = reinterpret_cast<const uint64_t*>(a.hq.s + (size_t)slot * KB);
+            // this lane's words of unit u: quant word u * UE / 4 + lane, scale word u * UE / 32 + lane
+            // (words outside the unit or past K read as published)
+            auto hload = [&](int u, uint64_t& hv, uint64_t& sv) {
+                const int w = u * (UE / 4) + lane, sw = u * (UE / 32) + lane;
+                const bool in = u < nu;
+                hv = (in && lane < UE / 4 && w < K / 4) ? __hip_atomic_load(qw + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                                        : (uint64_t)a.epoch << 32;
+                sv = (in && lane < UE / 32 && sw < KB) ? __hip_atomic_load(ss + sw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                                       : (uint64_t)a.htag;
+            };
+            uint64_t hv[DP_HDEPTH], sv[DP_HDEPTH];
+#pragma unroll
+            for (int i = 0; i < DP_HDEPTH; ++i) hload(pw + i * DOWN_WAVES, hv[i], sv[i]);
+            for (int u = pw; u < nu; u += DP_HDEPTH * DOWN_WAVES) {
+#pragma unroll
+                for (int i = 0; i < DP_HDEPTH; ++i) {
+                    const int ui = u + i * DOWN_WAVES;
+                    if (ui >= nu) break;  // wave-uniform
+                    for (int it = 0;; ++it) {
+                        const bool ok = (uint32_t)(hv[i] >> 32) == a.epoch && ((uint32_t)sv[i] & DEC_HTAG_MASK) == a.htag;
+                        if (__all(ok && !a.giveup_test)) break;
+                        if (it >= (int)a.spin_limit) {
+                            if (lane == 0) dec_fail(a);
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(1);
+                        hload(ui, hv[i], sv[i]);
+                    }
+                    const int w = ui * (UE / 4) + lane, sw = ui * (UE / 32) + lane;
+                    if (lane < UE / 4 && w < K / 4) reinterpret_cast<uint32_t*>(smem)[w] = (uint32_t)hv[i];
+                    if (lane < UE / 32 && sw < KB) reinterpret_cast<uint64_t*>(smem + K)[sw] = sv[i] & ~(uint64_t)DEC_HTAG_MASK;
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // h of the unit is in LDS before its flag
+                    if (lane == 0) __hip_atomic_store(hflag + ui, flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    hload(ui + DP_HDEPTH * DOWN_WAVES, hv[i], sv[i]);
+                }
+            }
+        }
         acc[0] += __shfl_xor(acc[0], 32, 64);
-        if (h == 0) red[wave][m] = acc[0];
+        if (h == 0 && wave < DOWN_WAVES) red[wave][m] = acc[0];
         __syncthreads();
         if (wave == 0 && h == 0) {
             float s = 0.0f;
@@ -1943,10 +2017,20 @@ bool decodep_fits(int gtype, int dtype, int d, int f, int E, int k, bool shared,
     // also stores h of slot 1 afterwards, which the slot-1 down tile of those rows waits for
     const int ng = gate_nrt * k;
     if (ng > DP_GROUPS * nb) return false;
+    // every tile on exactly one (block, group)
+    std::vector<int> seen(ng, 0);
+    for (int b = 0; b < nb; ++b)
+        for (int j = 0; j < DP_GROUPS; ++j) {
+            const int t = decodep_gu_tile(b, j, nb, gate_nrt);
+            if (t >= ng) return false;
+            if (t >= 0) ++seen[t];
+        }
+    for (int c : seen)
+        if (c != 1) return false;
     for (int b = 0; b < nb && b < down_nrt; ++b) {
         bool s1 = false;
         for (int j = 0; j < DP_GROUPS; ++j) {
-            const int t = decodep_gu_tile(b, j, nb);
+            const int t = decodep_gu_tile(b, j, nb, gate_nrt);
             s1 = s1 || (t >= gate_nrt && t < ng);
         }
         if (!s1) return false;

@@ -11,6 +11,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -41,6 +42,17 @@ int fail(int code, const std::string& msg) {
     g_err = msg;
     return code;
 }
+
+// One-block-per-CU fused steps (k_decode_p) need every block of the launch resident at once, so two of
+// them running at the same time on one GPU (different layers or streams of this process) could each
+// hold CUs the other waits for.  The stream of the last such launch that may still be running (an
+// asynchronous call's) is kept per device; a launch on another stream while it is set first
+// synchronizes the device.  Launches on one stream, and synchronous calls, add nothing.
+struct FusedOrder {
+    std::mutex mu;
+    hipStream_t pending[MAX_DEVICES] = {};
+};
+FusedOrder g_fused_order;
 
 #define HIPCHK(expr)                                                                              \
     do {                                                                                          \
@@ -418,6 +430,13 @@ int ensure_workspace(jx_moe_layer* L, int n) {
 
 void free_layer(jx_moe_layer* L) {
     (void)hipSetDevice(L->device);
+    if (L->own) {  // its stream goes away: no later launch may compare against it
+        std::lock_guard<std::mutex> lk(g_fused_order.mu);
+        if (g_fused_order.pending[L->device] == L->own) {
+            (void)hipStreamSynchronize(L->own);
+            g_fused_order.pending[L->device] = nullptr;
+        }
+    }
     for (auto* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown}) m->release();
     void* ptrs[] = {L->router, L->router_cm, L->bias, L->shgate, L->ffn_norm, L->post_norm, L->xn, L->x, L->out, L->probs, L->shscale, L->logits, L->ids,
                     L->counts, L->offs, L->act, L->n_act, L->pair_tok, L->pos_of, L->n_tiles, L->tiles,
@@ -627,6 +646,12 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         L->decp_used = fold && decodep_ok(L, flags);
         if (L->decp_used) {
             a.hw = L->hw;
+            {
+                std::lock_guard<std::mutex> lk(g_fused_order.mu);
+                hipStream_t& pending = g_fused_order.pending[L->device];
+                if (pending && pending != st) HIPCHK(hipDeviceSynchronize());  // it may still be running
+                pending = st;
+            }
             Launch l(L, "decode_fused_cu", st);
             if (jx::launch_decode_p(a, L->gate.m.type, L->down.m.type, st) != 0)
                 return fail(JX_ERR_HIP, "fused one-token step: launch failed");
@@ -1099,6 +1124,10 @@ int jx_moe_forward(jx_moe_layer* L, const float* x, int32_t n_tok, float* out, i
     if (!(flags & JX_FWD_ASYNC)) {
         HIPCHK(hipStreamSynchronize(st));
         if (L->prof.on && (r = resolve_profile(L)) != JX_OK) return r;
+        if (L->decp_used) {  // this call's one-block-per-CU launch is done
+            std::lock_guard<std::mutex> lk(g_fused_order.mu);
+            if (g_fused_order.pending[L->device] == st) g_fused_order.pending[L->device] = nullptr;
+        }
         if ((r = take_fused_error(L)) != JX_OK) return r;  // a bounded wait of a fused launch gave up
     }
     return JX_OK;

@@ -243,3 +243,31 @@ def test_fused_shared_first_step_after_recreate(moe):
         assert took_fused(L, x, False)
         assert same(first, L.forward(x, fused=False)[0])
         L.close()
+
+
+def test_fused_cu_steps_on_several_streams(moe, monkeypatch):
+    """One-block-per-CU steps of three layers queued asynchronously, each on the layer's own stream: two of
+    them running at once could each hold CUs the other waits for, so the library orders them across
+    streams.  Every step completes its waits (jx_moe_layer_status) and the outputs equal the separate
+    launches bit for bit."""
+    monkeypatch.setenv("JX_DECP", "1")
+    cfg, lw = layer("cu_q4k")
+    Ls = [moe.MoELayer.from_weights(lw) for _ in range(3)]
+    x = synth.make_tokens(cfg, 1, seed=71)
+    assert took_cu(Ls[0], x)
+    want = Ls[0].forward(x, fused=False)[0]
+    dx = moe.DeviceBuffer(x.nbytes).upload(x)
+    outs = [moe.DeviceBuffer(x.nbytes) for _ in Ls]
+    say("three layers, 300 steps, each on its own stream")
+    for i in range(300):
+        j = i % 3
+        Ls[j].forward_device(dx, 1, outs[j], sync=False)
+    moe.lib().jx_device_synchronize()
+    for L, o in zip(Ls, outs):
+        L.status(wait=True)
+        assert same(o.download(np.empty_like(x)), want)
+    dx.free()
+    for o in outs:
+        o.free()
+    for L in Ls:
+        L.close()
