@@ -1075,27 +1075,48 @@ k_gemv_mx(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_l
     for (int tb0 = 0; tb0 < cnt; tb0 += MX_NT) {
         const int nt = min(MX_NT, cnt - tb0);
         if (tb0) __syncthreads();  // the previous pass is done with msc and red
+        // the first two units' weights go out first: they need only the expert, while the activations wait
+        // on the token list (the pair table) and the scales on both
+        Raw wa, wb;
+        uint4 aa[BPU], ab[BPU];
+        X::load(wa, W, e, rt, kw, m, h, kw < nu);
+        X::load(wb, W, e, rt, kw + HW, m, h, kw + HW < nu);
         auto src = [&](int i) -> size_t {
             return GATEUP ? (size_t)token_of(grp, rec, tb0 + i) : (size_t)(p0 + tb0 + i);
         };
-        for (int i = tid; i < KB * MX_NT; i += WAVES * 64) {
-            const int b = i / MX_NT, t = i - b * MX_NT;
-            float2 v = make_float2(0.0f, 0.0f);
-            if (t < nt) {
-                const float2 sv = act.s[src(t) * KB + b];
-                // Q4_K / Q5_K: scale * sum (min term); Q4_0: sum
-                v = make_float2(sv.x, (TYPE == T_Q4_K || TYPE == T_Q5_K) ? sv.x * sv.y : sv.y);
-            }
-            msc[i] = v;
-        }
         const bool hi8 = nt > 8;  // tokens 8.. present: D registers 4-7 carry results
         // A row of this lane: token m; lanes past the pass's tokens read token 0 (their D rows are dropped)
         const int8_t* arow = act.q + src(m < nt ? m : 0) * (size_t)K + 16 * h;
         float acc[MX_NT / 2];
 #pragma unroll
         for (int r = 0; r < MX_NT / 2; ++r) acc[r] = 0.0f;
-        Raw wa, wb;
-        uint4 aa[BPU], ab[BPU];
+        auto lda = [&](uint4(&a)[BPU], int u) {
+#pragma unroll
+            for (int j = 0; j < BPU; ++j)  // in bounds past the end too (their results are never used)
+                a[j] = ld16(arow + (size_t)min(u * BPU + j, KB - 1) * 32);
+        };
+        // two units in flight per wave, as the GEMV's K loop: their activations go out before the scales
+        // are staged
+        int u = kw;
+        lda(aa, u);
+        lda(ab, u + HW);
+        // the tokens' (scale, sum) per block into LDS, MX_STAGE loads in flight per thread
+        constexpr int MX_STAGE = 2;
+        for (int i0 = tid; i0 < KB * MX_NT; i0 += MX_STAGE * WAVES * 64) {
+            float2 v[MX_STAGE];
+#pragma unroll
+            for (int q = 0; q < MX_STAGE; ++q) {
+                const int i = i0 + q * WAVES * 64, b = i / MX_NT, t = i - b * MX_NT;
+                v[q] = (i < KB * MX_NT && t < nt) ? act.s[src(t) * KB + b] : make_float2(0.0f, 0.0f);
+            }
+#pragma unroll
+            for (int q = 0; q < MX_STAGE; ++q) {
+                const int i = i0 + q * WAVES * 64;
+                // Q4_K / Q5_K: scale * sum (min term); Q4_0: sum
+                if (i < KB * MX_NT)
+                    msc[i] = make_float2(v[q].x, (TYPE == T_Q4_K || TYPE == T_Q5_K) ? v[q].x * v[q].y : v[q].y);
+            }
+        }
         auto ld = [&](Raw& w, uint4(&a)[BPU], int u) {
             X::load(w, W, e, rt, u, m, h, u < nu);
 #pragma unroll
@@ -1145,10 +1166,6 @@ k_gemv_mx(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_l
                 }
             }
         };
-        // two units in flight per wave, as the GEMV's K loop
-        int u = kw;
-        ld(wa, aa, u);
-        ld(wb, ab, u + HW);
         __syncthreads();  // msc staged
         for (; u < nu; u += 2 * HW) {
             accum(wa, aa, u);
@@ -1160,23 +1177,23 @@ k_gemv_mx(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_l
 #pragma unroll
         for (int r = 0; r < MX_NT / 2; ++r) red[wave][r][lane] = acc[r];
         __syncthreads();
-        if (wave == 0) {
+        // result register r holds tokens 4h + r (r < 4) and 8 + 4h + r - 4 (r >= 4): only the registers whose
+        // lane-half-0 token exists carry results; each is finished by one wave, the waves in turn
+        const int nr = nt > 8 ? 4 + min(4, nt - 8) : min(4, nt);
+        for (int r = wave; r < nr; r += WAVES) {  // wave-uniform
+            const int t = (r < 4 ? 4 * h + r : 8 + 4 * h + (r - 4));
+            float v0 = 0.0f, v1 = 0.0f;
 #pragma unroll
-            for (int r = 0; r < MX_NT / 2; ++r) {
-                const int t = (r < 4 ? 4 * h + r : 8 + 4 * h + (r - 4));
-                float v0 = 0.0f, v1 = 0.0f;
+            for (int w = 0; w < HW; ++w) v0 += red[w][r][lane];
+            const size_t row = (size_t)(p0 + tb0 + t);
+            if constexpr (GATEUP) {
 #pragma unroll
-                for (int w = 0; w < HW; ++w) v0 += red[w][r][lane];
-                const size_t row = (size_t)(p0 + tb0 + t);
-                if constexpr (GATEUP) {
-#pragma unroll
-                    for (int w = 0; w < HW; ++w) v1 += red[HW + w][r][lane];
-                    const float hv = gated(v0, v1, W0.act);
-                    store_q8_block(hv, m, t < nt && hq.q != nullptr, hq, row, rt);
-                    if (hf && t < nt) hf[row * (size_t)hf_ld + rt * 32 + m] = hv;
-                } else {
-                    if (t < nt) y[row * W0.rows + rt * 32 + m] = v0;
-                }
+                for (int w = 0; w < HW; ++w) v1 += red[HW + w][r][lane];
+                const float hv = gated(v0, v1, W0.act);
+                store_q8_block(hv, m, t < nt && hq.q != nullptr, hq, row, rt);
+                if (hf && t < nt) hf[row * (size_t)hf_ld + rt * 32 + m] = hv;
+            } else {
+                if (t < nt) y[row * W0.rows + rt * 32 + m] = v0;
             }
         }
     }
