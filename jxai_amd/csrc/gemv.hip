@@ -1199,6 +1199,209 @@ k_gemv_mx(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_l
     }
 }
 
+// Several row tiles per block (k_gemv_mxt): gate + up (+ SwiGLU + Q8_0 of h) or down for up to MX_NT
+// tokens per pass of MR row tiles of one expert, as k_gemv_mx computes them.  A block stages its group's
+// tokens once per pass for all its tiles; each wave walks its units (kw, kw + HW, ...) in order and, per
+// unit, takes the unit's products for every tile against the same activation operands, reloading each
+// tile's weight registers with that tile's next unit right after its products: MR units in flight per
+// wave, and the activations read once per unit.  (One tile per block leaves a ~74 KB Q4_K gate/up tile
+// behind a serial prologue of dependent loads -- slot record, token list, scales -- and an epilogue:
+// blocks lived ~15 us for a few us of streaming.)  Launches with many (group, tile) items take it;
+// launches with few (a dense shared expert) keep one tile per block, whose blocks fill more CUs.
+// Measured at 32 tokens, weights from HBM: DeepSeek-V2-Lite-shaped routed Q4_K gate/up 89.5 -> 62.2 us
+// (three tiles), Mixtral-shaped 184.6 -> 125.6 us; Qwen1.5-shaped Q4_0 at 64 tokens 85.8 -> 81.5 us and
+// its down 43.5 -> 39.2 us (two tiles).  Q6_K and Q8_0 gate/up stay at one tile (Q8_0: 55.0 us against
+// 59.3 at two tiles, Qwen3-shaped 32 tokens).
+constexpr int MX_MR_MIN_ITEMS = 1024;
+template <int TYPE, bool GATEUP>
+constexpr int mx_mr_max() {
+    return (TYPE == T_Q6_K || (TYPE == T_Q8_0 && GATEUP)) ? 1 : (TYPE == T_Q4_K || TYPE == T_Q5_K) ? 3 : 2;
+}
+// Static LDS of one k_gemv_mxt block: the MR tiles' per-wave partial sums.
+template <int WAVES, int MR>
+constexpr size_t mx_red_bytes() { return (size_t)MR * WAVES * (MX_NT / 2) * 64 * sizeof(float); }
+
+template <int TYPE, bool GATEUP, int WAVES, int MR>
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
+k_gemv_mxt(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_ld, float* y, SmallTail tail) {
+    using X = Mx<TYPE>;
+    using Raw = typename X::Raw;
+    constexpr int BPU = X::BPU;
+    constexpr int HW = GATEUP ? WAVES / 2 : WAVES;  // waves per matrix
+    extern __shared__ __align__(16) float2 msc[];   // [block][MX_NT]: (scale, sum) of each token
+    __shared__ float red[MR][WAVES][MX_NT / 2][64];
+    static_assert(sizeof(red) == mx_red_bytes<WAVES, MR>(), "red");
+    // grid: chunks of MR row tiles fastest over the slots, then (gate/up) the one tail block
+    if (GATEUP && tail.on && blockIdx.x == gridDim.x - 1) {  // the extra block: dispatch tables only
+        small_tail(tail, threadIdx.x);
+        return;
+    }
+    const int nch = (W0.nrt + MR - 1) / MR;
+    const int rt0 = (int)(blockIdx.x % nch) * MR, nj = min(MR, W0.nrt - rt0);  // tiles rt0 .. rt0 + nj - 1
+    const int4 rec = group_of(grp, blockIdx.x / nch);
+    const int e = rec.x, p0 = rec.y, cnt = rec.z;
+    if (cnt == 0) return;
+    const int tid = threadIdx.x, lane = tid & 63, m = lane & 31, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar unit loop and branches
+    const int kw = wave % HW;
+    const QMat& W = (GATEUP && wave >= HW) ? W1 : W0;
+    const int K = act.K, KB = K / 32;
+    const int nu = X::units(W0);
+    // one pass of up to MX_NT tokens; HI8: tokens 8.. present (D registers 4-7 carry results), a
+    // compile-time switch (as a runtime one it branched around single LDS reads and moves)
+    auto pass = [&](int tb0, int nt, auto hi8c) {
+        constexpr bool HI8 = decltype(hi8c)::value;
+        // every tile's first unit goes out first: the weights need only the expert, while the activations
+        // wait on the token list (the pair table) and the scales on both (tiles past the matrix load the
+        // last one; their results are dropped)
+        Raw w[MR];
+#pragma unroll
+        for (int j = 0; j < MR; ++j) X::load(w[j], W, e, min(rt0 + j, W0.nrt - 1), kw, m, h, kw < nu);
+        uint4 aa[BPU], ab[BPU];
+        auto src = [&](int i) -> size_t {
+            return GATEUP ? (size_t)token_of(grp, rec, tb0 + i) : (size_t)(p0 + tb0 + i);
+        };
+        // A row of this lane: token m; lanes past the pass's tokens read token 0 (their D rows are dropped)
+        const int8_t* arow = act.q + src(m < nt ? m : 0) * (size_t)K + 16 * h;
+        float acc[MR][MX_NT / 2];
+#pragma unroll
+        for (int j = 0; j < MR; ++j)
+#pragma unroll
+            for (int r = 0; r < MX_NT / 2; ++r) acc[j][r] = 0.0f;
+        auto lda = [&](uint4(&a)[BPU], int u) {
+#pragma unroll
+            for (int j = 0; j < BPU; ++j)  // in bounds past the end too (their results are never used)
+                a[j] = ld16(arow + (size_t)min(u * BPU + j, KB - 1) * 32);
+        };
+        // the first two units' activations go out before the scales are staged
+        int u = kw;
+        lda(aa, u);
+        lda(ab, u + HW);
+        // the tokens' (scale, sum) per block into LDS, MX_STAGE loads in flight per thread
+        constexpr int MX_STAGE = 2;
+        for (int i0 = tid; i0 < KB * MX_NT; i0 += MX_STAGE * WAVES * 64) {
+            float2 v[MX_STAGE];
+#pragma unroll
+            for (int q = 0; q < MX_STAGE; ++q) {
+                const int i = i0 + q * WAVES * 64, b = i / MX_NT, t = i - b * MX_NT;
+                v[q] = (i < KB * MX_NT && t < nt) ? act.s[src(t) * KB + b] : make_float2(0.0f, 0.0f);
+            }
+#pragma unroll
+            for (int q = 0; q < MX_STAGE; ++q) {
+                const int i = i0 + q * WAVES * 64;
+                // Q4_K / Q5_K: scale * sum (min term); Q4_0: sum
+                if (i < KB * MX_NT)
+                    msc[i] = make_float2(v[q].x, (TYPE == T_Q4_K || TYPE == T_Q5_K) ? v[q].x * v[q].y : v[q].y);
+            }
+        }
+        // one unit of one tile: per 32-block, the integer block sums of the pass's tokens on the matrix core,
+        // scaled into ac; block j + 1's products issue before block j's scaling, and nothing moves across a
+        // block (unhindered, the scheduler hoists every product of the tiles' units ahead of the scaling,
+        // 16 result registers each, and spills)
+        auto mfma = [&](const Raw& wr, const uint4(&a)[BPU], int j, v16i_t& D, v16i_t& D2) {
+            const uint4 bw = X::bop(wr, j, h);
+            if constexpr (TYPE == T_Q6_K) {
+                const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+                D = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i_t, a[j]),
+                                                          __builtin_bit_cast(v4i_t, h ? z : bw), v16i_t{}, 0, 0, 0);
+                D2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i_t, a[j]),
+                                                           __builtin_bit_cast(v4i_t, h ? bw : z), v16i_t{}, 0, 0, 0);
+            } else {
+                D = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i_t, a[j]),
+                                                          __builtin_bit_cast(v4i_t, bw), v16i_t{}, 0, 0, 0);
+            }
+        };
+        auto accum = [&](const Raw& wr, const uint4(&a)[BPU], int u, float(&ac)[MX_NT / 2]) {
+            // the unit's blocks in range: K-quant units are whole super-blocks; the others end at KB
+            const int nbk = is_kquant(TYPE) ? BPU : min(BPU, KB - u * BPU);  // wave-uniform
+            v16i_t D[2], D2[2];
+            mfma(wr, a, 0, D[0], D2[0]);
+#pragma unroll
+            for (int j = 0; j < BPU; ++j) {
+                if (j >= nbk) break;
+                if (j + 1 < BPU && j + 1 < nbk) mfma(wr, a, j + 1, D[(j + 1) & 1], D2[(j + 1) & 1]);
+                const v16i_t& Dj = D[j & 1];
+                const v16i_t& D2j = D2[j & 1];
+                const int b = u * BPU + j;
+                float rs, rmin;
+                X::scales(wr, j, rs, rmin);
+                // tokens of registers 0-3: 4h..4h+3, of 4-7: 8+4h..11+4h (only when the pass has them)
+                const float4* sp = reinterpret_cast<const float4*>(msc + b * MX_NT + 4 * h);
+                const float4 s0 = sp[0], s1 = sp[1];
+                const float4 s2 = HI8 ? sp[4] : s0, s3 = HI8 ? sp[5] : s1;
+                const float sx[8] = {s0.x, s0.z, s1.x, s1.z, s2.x, s2.z, s3.x, s3.z};
+                const float sy[8] = {s0.y, s0.w, s1.y, s1.w, s2.y, s2.w, s3.y, s3.w};
+#pragma unroll
+                for (int r = 0; r < MX_NT / 2; ++r) {
+                    if (r >= 4 && !HI8) break;
+                    if constexpr (TYPE == T_Q4_K || TYPE == T_Q5_K) {
+                        ac[r] = __builtin_fmaf(rs * sx[r], (float)Dj[r], ac[r]);
+                        ac[r] = __builtin_fmaf(rmin, sy[r], ac[r]);
+                    } else if constexpr (TYPE == T_Q6_K) {  // D = 4 sum((q6 - 32) y) per sub-block, exact
+                        const int isum = sbyte(wr.sc, 2 * j) * (Dj[r] >> 2) + sbyte(wr.sc, 2 * j + 1) * (D2j[r] >> 2);
+                        ac[r] = __builtin_fmaf(rs * sx[r], (float)isum, ac[r]);
+                    } else if constexpr (TYPE == T_Q4_0) {
+                        const int isum = Dj[r] - 8 * (int)sy[r];  // weights are nibble - 8; sy exact (|sum| < 2^12)
+                        ac[r] = __builtin_fmaf(rs * sx[r], (float)isum, ac[r]);
+                    } else {
+                        ac[r] = __builtin_fmaf(rs * sx[r], (float)Dj[r], ac[r]);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        // unit u's products for every tile, each tile's registers reloaded with its next unit right after
+        // (past the last unit: the padding)
+        auto unit = [&](const uint4(&a)[BPU], int u) {
+#pragma unroll
+            for (int j = 0; j < MR; ++j) {
+                accum(w[j], a, u, acc[j]);
+                X::load(w[j], W, e, min(rt0 + j, W0.nrt - 1), u + HW, m, h, u + HW < nu);
+            }
+        };
+        __syncthreads();  // msc staged
+        for (; u < nu; u += 2 * HW) {
+            unit(aa, u);
+            lda(aa, u + 2 * HW);
+            if (u + HW >= nu) break;
+            unit(ab, u + HW);
+            lda(ab, u + 3 * HW);
+        }
+#pragma unroll
+        for (int j = 0; j < MR; ++j)
+#pragma unroll
+            for (int r = 0; r < MX_NT / 2; ++r) red[j][wave][r][lane] = acc[j][r];
+        __syncthreads();
+        // result register r holds tokens 4h + r (r < 4) and 8 + 4h + r - 4 (r >= 4): only the registers whose
+        // lane-half-0 token exists carry results; each (tile, register) is finished by one wave, the waves
+        // in turn
+        const int nr = nt > 8 ? 4 + min(4, nt - 8) : min(4, nt);
+        for (int q = wave; q < nj * nr; q += WAVES) {  // wave-uniform
+            const int j = q / nr, r = q - j * nr, rt = rt0 + j;
+            const int t = (r < 4 ? 4 * h + r : 8 + 4 * h + (r - 4));
+            float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+            for (int w = 0; w < HW; ++w) v0 += red[j][w][r][lane];
+            const size_t row = (size_t)(p0 + tb0 + t);
+            if constexpr (GATEUP) {
+#pragma unroll
+                for (int w = 0; w < HW; ++w) v1 += red[j][HW + w][r][lane];
+                const float hv = gated(v0, v1, W0.act);
+                store_q8_block(hv, m, t < nt && hq.q != nullptr, hq, row, rt);
+                if (hf && t < nt) hf[row * (size_t)hf_ld + rt * 32 + m] = hv;
+            } else {
+                if (t < nt) y[row * W0.rows + rt * 32 + m] = v0;
+            }
+        }
+    };
+    for (int tb0 = 0; tb0 < cnt; tb0 += MX_NT) {
+        const int nt = min(MX_NT, cnt - tb0);
+        if (tb0) __syncthreads();  // the previous pass is done with msc and red
+        if (nt > 8) pass(tb0, nt, std::integral_constant<bool, true>{});
+        else pass(tb0, nt, std::integral_constant<bool, false>{});
+    }
+}
+
 #ifndef JX_GEMV_GATEUP_WAVES
 #define JX_GEMV_GATEUP_WAVES 4
 #endif
@@ -1289,9 +1492,19 @@ static void gateup_q8(const QMat& g, const QMat& u, const ActQ8& xq, const Group
                            nullptr, 0, grp, hq, hf, hf_ld, tail);
     } else {  // several tokens per expert: the matrix-core form
         const size_t lds = (size_t)(xq.K / 32) * MX_NT * sizeof(float2);
-        lds_optin(k_gemv_mx<TYPE, true, GATEUP_WAVES>, lds);
-        hipLaunchKernelGGL((k_gemv_mx<TYPE, true, GATEUP_WAVES>), grid, dim3(GATEUP_WAVES * 64), lds, st, g, u, xq,
-                           grp, hq, hf, hf_ld, nullptr, tail);
+        auto go = [&](auto kern, int mr) {
+            lds_optin(kern, lds);
+            const dim3 mg((g.nrt + mr - 1) / mr * slots + (tail.on ? 1 : 0));
+            hipLaunchKernelGGL(kern, mg, dim3(GATEUP_WAVES * 64), lds, st, g, u, xq, grp, hq, hf, hf_ld, nullptr, tail);
+        };
+        constexpr int MR = mx_mr_max<TYPE, true>();
+        if constexpr (MR > 1) {
+            if (g.nrt * slots >= MX_MR_MIN_ITEMS) {
+                go(k_gemv_mxt<TYPE, true, GATEUP_WAVES, MR>, MR);
+                return;
+            }
+        }
+        go(k_gemv_mx<TYPE, true, GATEUP_WAVES>, 1);
     }
 }
 
@@ -1327,13 +1540,26 @@ static void down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, 
             // the CUs (one dense matrix, few tokens); measured: Qwen1.5-shaped 64 tokens routed down
             // 75 -> 44 us, Qwen3-shaped 32 tokens 62 -> 33 us
             const size_t lds = (size_t)(K / 32) * MX_NT * sizeof(float2);
-            auto go = [&](auto kern, int waves) {
+            auto go = [&](auto kern, int mr, int waves) {
                 lds_optin(kern, lds);
-                hipLaunchKernelGGL(kern, grid, dim3(waves * 64), lds, st, dn, dn, hq, grp, ActQ8{}, nullptr, 0, y,
-                                   SmallTail{});
+                hipLaunchKernelGGL(kern, dim3((dn.nrt + mr - 1) / mr * slots), dim3(waves * 64), lds, st, dn, dn, hq,
+                                   grp, ActQ8{}, nullptr, 0, y, SmallTail{});
             };
-            if (2 * (int)grid.x < num_cus()) go(k_gemv_mx<TYPE, false, 8>, 8);
-            else go(k_gemv_mx<TYPE, false, 4>, 4);
+            // and 8-wave blocks where two 4-wave blocks' LDS would not fit one CU (long K: the staged scales
+            // plus the tiles' partial sums)
+            constexpr int MR = mx_mr_max<TYPE, false>();
+            if constexpr (MR > 1) {
+                if (dn.nrt * slots >= MX_MR_MIN_ITEMS) {
+                    const bool lds2 = 2 * (lds + mx_red_bytes<4, MR>()) <= (size_t)160 * 1024;
+                    if (2 * ((dn.nrt + MR - 1) / MR) * slots < num_cus() || !lds2)
+                        go(k_gemv_mxt<TYPE, false, 8, MR>, MR, 8);
+                    else
+                        go(k_gemv_mxt<TYPE, false, 4, MR>, MR, 4);
+                    return;
+                }
+            }
+            if (2 * (int)grid.x < num_cus()) go(k_gemv_mx<TYPE, false, 8>, 1, 8);
+            else go(k_gemv_mx<TYPE, false, 4>, 1, 4);
         }
     } else {
         const size_t lds = act_lds_bytes(4, K, F32ACT);
