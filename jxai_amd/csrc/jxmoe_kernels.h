@@ -212,9 +212,12 @@ void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_l
 void launch_mfma_gateup(const QMat& g, const QMat& u, const ActH& xin, const Groups& grp, int tiles_ub,
                         const ActQ8& hq, float* hf, hipStream_t st);
 // KS > 1: the K range split over KS workgroups per item (whole super-blocks each), part q of the
-// output at y + q * ystride (the combine adds the parts in order).
+// output at y + q * ystride (the combine adds the parts in order).  small: few pairs per expert (the
+// 64-pair tile form at four workgroups per CU).
 void launch_mfma_down(const QMat& dn, const ActH& hin, const Groups& grp, int tiles_ub, float* y, hipStream_t st,
-                      int KS = 1, size_t ystride = 0);
+                      int KS = 1, size_t ystride = 0, bool small = false);
+// Down GEMM in the small form up to this many (token, slot) pairs per expert on average.
+constexpr int MFMA_DOWN_SMALL_MAX_PPE = 16;
 // K-split of the down GEMM for a K of K: two parts from MFMA_DOWN_KSPLIT_MIN_K on (twice the
 // workgroups, finer rounds; measured Mixtral-shaped, K 14336: 2048 tokens 634 -> 575 us, 256 tokens
 // 155 -> 133 us; at K 768 - 1408 the per-workgroup overhead makes it slower).

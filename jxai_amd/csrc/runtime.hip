@@ -778,7 +778,8 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         }
         Launch l(L, "down_mfma", st);
         ks = jx::mfma_down_ksplit(L->hh.a.K);
-        jx::launch_mfma_down(L->down.m, L->hh.a, grp, tiles_ub, L->y, st, ks, L->ystride);
+        jx::launch_mfma_down(L->down.m, L->hh.a, grp, tiles_ub, L->y, st, ks, L->ystride,
+                             nk <= jx::MFMA_DOWN_SMALL_MAX_PPE * E);
     } else {
         jx::CombineOut comb;
         if (fold) {
