@@ -680,13 +680,11 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
             jx::launch_q8_to_acth(L->xq, n, L->xh.a, st);
         }
     } else {
-        {
-            Launch l(L, "route", st);
-            jx::launch_route(ra, st);
-        }
-        Launch l(L, "dispatch", st);
-        jx::launch_dispatch(L->ids, nk, E, k, dout, st);
+        Launch l(L, "route", st);
+        jx::launch_route(ra, st);
     }
+    // the dispatch tables (many-token path) follow the shared expert's fork: it needs only x's forms
+    const bool dispatch_later = !small_logits && !jx::route_small_fits(n, d, E);
     jx::Groups grp;
     grp.counts = L->counts;
     grp.offs = L->offs;
@@ -744,6 +742,10 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
                                  ss);
         }
         HIPCHK(hipEventRecord(L->ev_join, ss));
+    }
+    if (dispatch_later) {
+        Launch l(L, "dispatch", st);
+        jx::launch_dispatch(L->ids, nk, E, k, dout, st);
     }
     const float* gxf = L->gu_f32 ? L->xf : nullptr;
     if (mfma_gu) {
