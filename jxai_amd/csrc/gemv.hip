@@ -1215,7 +1215,7 @@ k_gemv_mx(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_l
 constexpr int MX_MR_MIN_ITEMS = 1024;
 template <int TYPE, bool GATEUP>
 constexpr int mx_mr_max() {
-    return (TYPE == T_Q6_K || (TYPE == T_Q8_0 && GATEUP)) ? 1 : (TYPE == T_Q4_K || TYPE == T_Q5_K) ? 3 : 2;
+    return (TYPE == T_Q6_K || (TYPE == T_Q8_0 && GATEUP)) ? 1 : (TYPE == T_Q4_K || TYPE == T_Q5_K || (TYPE == T_Q4_0 && GATEUP)) ? 3 : 2;
 }
 // Static LDS of one k_gemv_mxt block: the MR tiles' per-wave partial sums.
 template <int WAVES, int MR>
