@@ -580,12 +580,14 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
     const bool small_logits = !mfma && !smfma && n <= jx::ROUTE_SMALL_MAX_N && E <= jx::SMALL_GROUP_MAX_E &&
                               jx::route_small_fits(n, d, E);
     // GEMV form: one token; groups of 4 on the VALU (few tokens per expert); or 16 per weight pass on
-    // the int8 matrix cores, which streams faster once experts see ~1.5 tokens on average (Q8_0, whose
-    // VALU form is slower, from 0.5): measured on every configured shape (Qwen1.5-shaped 32 tokens
-    // 164 -> 131 us, DeepSeek-V2-Lite-shaped 16 tokens 137 -> 116 us against the VALU form)
+    // the int8 matrix cores, which streams faster once experts see one token on average (Mixtral-sized
+    // experts: 1.5; Q8_0, whose VALU form is slower: 0.5): measured on every configured shape
+    // (Qwen1.5-shaped 16 / 32 tokens 127 / 164 -> 112 / 131 us, DeepSeek-V2-Lite-shaped 12 / 16 tokens
+    // 127 / 137 -> 117 / 116 us against the VALU form; Mixtral-shaped 4 tokens 144 us VALU, 154 us MFMA)
     const bool q8w = L->gate.m.type == jx::T_Q8_0;
+    const bool large = (size_t)d * L->F >= LARGE_EXPERT_ELEMS;
     auto gemv_tb = [&](int tokens_per_expert_x2) {  // twice the average tokens per expert
-        return n == 1 ? 1 : (tokens_per_expert_x2 >= (q8w ? 1 : 3) ? 16 : 4);
+        return n == 1 ? 1 : (tokens_per_expert_x2 >= (q8w ? 1 : large ? 3 : 2) ? 16 : 4);
     };
     const int tb = gemv_tb(2 * nk / E);
     // fp32 h (no Q8_0 form at d_ff) takes the matrix-core down GEMM from 2 tokens on (every dispatch path
