@@ -1261,6 +1261,10 @@ k_gemv_mxt(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_
         auto src = [&](int i) -> size_t {
             return GATEUP ? (size_t)token_of(grp, rec, tb0 + i) : (size_t)(p0 + tb0 + i);
         };
+        // the token lookups of both the staging (below) and the A rows go out together
+        static_assert((WAVES * 64) % MX_NT == 0, "one token per thread");
+        const int tk = tid % MX_NT;
+        const size_t srow = tk < nt ? src(tk) * (size_t)KB : 0;
         // A row of this lane: token m; lanes past the pass's tokens read token 0 (their D rows are dropped)
         const int8_t* arow = act.q + src(m < nt ? m : 0) * (size_t)K + 16 * h;
         float acc[MR][MX_NT / 2];
@@ -1277,14 +1281,17 @@ k_gemv_mxt(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_
         int u = kw;
         lda(aa, u);
         lda(ab, u + HW);
-        // the tokens' (scale, sum) per block into LDS, MX_STAGE loads in flight per thread
-        constexpr int MX_STAGE = 2;
+        // the tokens' (scale, sum) per block into LDS, entry 16 b + t: a thread's entries all belong to its
+        // token t = tid % 16 (the thread count is a multiple of 16), whose row was looked up once above, and
+        // MX_STAGE scale loads are in flight per thread (one round at K <= 4096 for 4 waves: the token
+        // list and the scales are two dependent round trips, not one per entry group)
+        constexpr int MX_STAGE = 4;
         for (int i0 = tid; i0 < KB * MX_NT; i0 += MX_STAGE * WAVES * 64) {
             float2 v[MX_STAGE];
 #pragma unroll
             for (int q = 0; q < MX_STAGE; ++q) {
-                const int i = i0 + q * WAVES * 64, b = i / MX_NT, t = i - b * MX_NT;
-                v[q] = (i < KB * MX_NT && t < nt) ? act.s[src(t) * KB + b] : make_float2(0.0f, 0.0f);
+                const int i = i0 + q * WAVES * 64, b = i / MX_NT;
+                v[q] = (i < KB * MX_NT && tk < nt) ? act.s[srow + b] : make_float2(0.0f, 0.0f);
             }
 #pragma unroll
             for (int q = 0; q < MX_STAGE; ++q) {
