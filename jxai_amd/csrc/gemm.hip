@@ -1132,13 +1132,13 @@ struct Shape {
     static constexpr int RC = GATEUP ? JX_GEMM_GU_RC : JX_DOWN_RC;
 };
 
-// Down over few pairs per expert (batched decode; mostly fp32-activation downs, which have no GEMV form
-// on the matrix cores): 64-pair tile parts and two pair tiles per wave (half the MFMAs and staging of
-// the 128-pair form for a tile of a few pairs), 40 KB of LDS per workgroup, and as many workgroups per
-// CU as the registers allow without spills: 3 (Q6_K: 4; Q5_0: 2, whose 3-wave build spills), so the
-// ~1000 workgroups of a 64-expert layer run in about one round with more weight loads in flight.
-// Measured DeepSeek-V2-Lite-shaped, weights from HBM: Q4_K (fp32 activations) 32 tokens 63.6 -> 49.1
-// us, 8 tokens 49.3 -> 30.1 us; Q5_0 at 32 tokens 71.6 -> 50.9 us.
+// Down over fewer pairs per expert (batched decode, where fp32-activation downs have no GEMV form on the
+// matrix cores, and prefill up to ~256 pairs per expert): 64-pair tile parts (partial tiles waste half
+// as much) and two pair tiles per wave, 40 KB of LDS per workgroup, and as many workgroups per CU as the
+// registers allow without spills: 3 (Q6_K: 4; Q5_0: 2, whose 3-wave build spills), so more weight loads
+// are in flight.  Measured DeepSeek-V2-Lite-shaped, weights from HBM: Q4_K (fp32 activations) 32
+// tokens 63.6 -> 49.1 us, 8 tokens 49.3 -> 30.1 us; Q5_0 at 32 tokens 71.6 -> 50.9 us (prefill:
+// MFMA_DOWN_SMALL_MAX_PPE).
 template <int TYPE>
 struct ShapeSmallDown {
     static constexpr int WPE = TYPE == T_Q6_K ? 4 : TYPE == T_Q5_0 ? 2 : 3;

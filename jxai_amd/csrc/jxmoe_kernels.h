@@ -213,11 +213,14 @@ void launch_mfma_gateup(const QMat& g, const QMat& u, const ActH& xin, const Gro
                         const ActQ8& hq, float* hf, hipStream_t st);
 // KS > 1: the K range split over KS workgroups per item (whole super-blocks each), part q of the
 // output at y + q * ystride (the combine adds the parts in order).  small: few pairs per expert (the
-// 64-pair tile form at four workgroups per CU).
+// 64-pair tile form at more workgroups per CU).
 void launch_mfma_down(const QMat& dn, const ActH& hin, const Groups& grp, int tiles_ub, float* y, hipStream_t st,
                       int KS = 1, size_t ystride = 0, bool small = false);
-// Down GEMM in the small form up to this many (token, slot) pairs per expert on average.
-constexpr int MFMA_DOWN_SMALL_MAX_PPE = 16;
+// Down GEMM in the small form up to this many (token, slot) pairs per expert on average (measured:
+// Mixtral-shaped 512 tokens, 128 per expert, 239 -> 202 us; Qwen3-shaped 2048 tokens with Zipf-skewed
+// routing 143 -> 124 us; DeepSeek-V2-Lite-shaped 2048 tokens 130 -> 122 us; Mixtral-shaped 2048 tokens,
+// 512 per expert, 566 us in the 128-pair form against 590 in the small one).
+constexpr int MFMA_DOWN_SMALL_MAX_PPE = 256;
 // K-split of the down GEMM for a K of K: two parts from MFMA_DOWN_KSPLIT_MIN_K on (twice the
 // workgroups, finer rounds; measured Mixtral-shaped, K 14336: 2048 tokens 634 -> 575 us, 256 tokens
 // 155 -> 133 us; at K 768 - 1408 the per-workgroup overhead makes it slower).
