@@ -911,7 +911,7 @@ k_gemv_down(QMat D, ActQ8 hq, const float* hf, int hf_ld, Groups grp, float* y, 
 // quants (lane (t, g): token t, half g; tokens past the group give zeros).  Lane (m, g) receives
 // D[token 8(r/4) + 4g + r%4][row m] in register r, r < 8.  Each sum is scaled in fp32 by its row's
 // weight scale and its token's activation scale: the integer block sums and scale products of
-// vec_dot_*_q8_0 (src/quant.cpp:3307-3573); the Q4_0 -8 offset is applied to the integer sum; only
+// vec_dot_*_q8_0 (src/quant.cpp:3307-3573); Q4_0's -8 offset is in the weight operand (q - 8); only
 // the fp32 summation order differs.  The weights are read once per MX_NT tokens instead of once per
 // 4, and the scaling is a few instructions per (row, token, block) instead of the GEMV's per-token
 // dot products.  The tokens' (scale, sum) pairs are staged in LDS per pass; quants and weights
@@ -1010,7 +1010,8 @@ struct Mx<T_Q8_0> {
 };
 
 // Q4_0: four blocks per unit; both lane halves load a row's whole block (16 bytes) and take the low
-// (elements 0..15) or high (16..31) nibbles.
+// (elements 0..15) or high (16..31) nibbles, as the signed bytes q - 8 (so the block sum is the
+// reference's integer sum with no correction).
 template <>
 struct Mx<T_Q4_0> {
     static constexpr int BPU = 4;
@@ -1028,11 +1029,14 @@ struct Mx<T_Q4_0> {
             c.d[i] = *reinterpret_cast<const uint16_t*>(v ? sb + ((b0 + i) * 32 + m) * 2 : W.pad_sc + m * 2);
         }
     }
+    // nibble n (bytes of 0..15) -> n - 8 per byte: bit 7 set before subtracting 8 stops the borrows
+    // (0x80 + n - 8 >= 0x78), and clearing it again gives (n - 8) mod 256
+    __device__ static uint32_t s8(uint32_t n) { return ((n ^ 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
     __device__ static uint4 bop(const Raw& c, int j, int h) {
         const uint4 v = c.q[j];
         const int sh = h * 4;
-        return make_uint4((v.x >> sh) & 0x0F0F0F0Fu, (v.y >> sh) & 0x0F0F0F0Fu, (v.z >> sh) & 0x0F0F0F0Fu,
-                          (v.w >> sh) & 0x0F0F0F0Fu);
+        return make_uint4(s8((v.x >> sh) & 0x0F0F0F0Fu), s8((v.y >> sh) & 0x0F0F0F0Fu), s8((v.z >> sh) & 0x0F0F0F0Fu),
+                          s8((v.w >> sh) & 0x0F0F0F0Fu));
     }
     __device__ static void scales(const Raw& c, int j, float& rs, float& rmin) {
         rs = f16_to_f32(c.d[j] & 0xFFFFu);
@@ -1112,7 +1116,7 @@ k_gemv_mx(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_l
 #pragma unroll
             for (int q = 0; q < MX_STAGE; ++q) {
                 const int i = i0 + q * WAVES * 64;
-                // Q4_K / Q5_K: scale * sum (min term); Q4_0: sum
+                // Q4_K / Q5_K: scale * sum (min term); the others do not read the sum
                 if (i < KB * MX_NT)
                     msc[i] = make_float2(v[q].x, (TYPE == T_Q4_K || TYPE == T_Q5_K) ? v[q].x * v[q].y : v[q].y);
             }
@@ -1156,9 +1160,6 @@ k_gemv_mx(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_l
                         acc[r] = __builtin_fmaf(rmin, sy[r], acc[r]);
                     } else if constexpr (TYPE == T_Q6_K) {  // D = 4 sum((q6 - 32) y) per sub-block, exact
                         const int isum = sbyte(w.sc, 2 * j) * (D[r] >> 2) + sbyte(w.sc, 2 * j + 1) * (D2[r] >> 2);
-                        acc[r] = __builtin_fmaf(rs * sx[r], (float)isum, acc[r]);
-                    } else if constexpr (TYPE == T_Q4_0) {
-                        const int isum = D[r] - 8 * (int)sy[r];  // weights are nibble - 8; sy exact (|sum| < 2^12)
                         acc[r] = __builtin_fmaf(rs * sx[r], (float)isum, acc[r]);
                     } else {
                         acc[r] = __builtin_fmaf(rs * sx[r], (float)D[r], acc[r]);
@@ -1296,7 +1297,7 @@ k_gemv_mxt(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_
 #pragma unroll
             for (int q = 0; q < MX_STAGE; ++q) {
                 const int i = i0 + q * WAVES * 64;
-                // Q4_K / Q5_K: scale * sum (min term); Q4_0: sum
+                // Q4_K / Q5_K: scale * sum (min term); the others do not read the sum
                 if (i < KB * MX_NT)
                     msc[i] = make_float2(v[q].x, (TYPE == T_Q4_K || TYPE == T_Q5_K) ? v[q].x * v[q].y : v[q].y);
             }
@@ -1346,9 +1347,6 @@ k_gemv_mxt(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_
                         ac[r] = __builtin_fmaf(rmin, sy[r], ac[r]);
                     } else if constexpr (TYPE == T_Q6_K) {  // D = 4 sum((q6 - 32) y) per sub-block, exact
                         const int isum = sbyte(wr.sc, 2 * j) * (Dj[r] >> 2) + sbyte(wr.sc, 2 * j + 1) * (D2j[r] >> 2);
-                        ac[r] = __builtin_fmaf(rs * sx[r], (float)isum, ac[r]);
-                    } else if constexpr (TYPE == T_Q4_0) {
-                        const int isum = Dj[r] - 8 * (int)sy[r];  // weights are nibble - 8; sy exact (|sum| < 2^12)
                         ac[r] = __builtin_fmaf(rs * sx[r], (float)isum, ac[r]);
                     } else {
                         ac[r] = __builtin_fmaf(rs * sx[r], (float)Dj[r], ac[r]);
