@@ -946,6 +946,32 @@ struct Mx<T_Q4_K> {
         rs = f16_to_f32(c.hd.x) * (float)sc;
         rmin = -f16_to_f32(c.hd.x >> 16) * (float)mn;
     }
+    // all eight at once, four bytes per operation: scales 0-3 and mins 0-3 are the low six bits of
+    // scale bytes 0-3 and 4-7; scale (min) 4 + i takes the low (high) nibble of byte 8 + i and, as bits
+    // 4-5, the top two bits of byte i (4 + i) -- the same values as scales(), in the same products
+    struct Scl {
+        float rs[8], rmin[8];
+    };
+    __device__ static Scl prep(const Raw& c) {
+        const uint32_t y = c.hd.y, z = c.hd.z, w = c.hd.w;
+        const uint32_t sc0 = y & 0x3F3F3F3Fu, mn0 = z & 0x3F3F3F3Fu;
+        const uint32_t sc1 = (w & 0x0F0F0F0Fu) | ((y >> 2) & 0x30303030u);
+        const uint32_t mn1 = ((w >> 4) & 0x0F0F0F0Fu) | ((z >> 2) & 0x30303030u);
+        const float d = f16_to_f32(c.hd.x), dm = f16_to_f32(c.hd.x >> 16);
+        Scl s;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            s.rs[i] = d * (float)((sc0 >> (8 * i)) & 0xFFu);
+            s.rs[4 + i] = d * (float)((sc1 >> (8 * i)) & 0xFFu);
+            s.rmin[i] = -dm * (float)((mn0 >> (8 * i)) & 0xFFu);
+            s.rmin[4 + i] = -dm * (float)((mn1 >> (8 * i)) & 0xFFu);
+        }
+        return s;
+    }
+    __device__ static void scale(const Scl& s, const Raw&, int j, float& rs, float& rmin) {
+        rs = s.rs[j];
+        rmin = s.rmin[j];
+    }
 };
 
 // Q5_K: as Q4_K with the fifth bits (values 0..31, exact in int8).
@@ -969,6 +995,9 @@ struct Mx<T_Q5_K> {
         rs = f16_to_f32(c.hd.x) * (float)(c.s ? a1 : a0);
         rmin = -f16_to_f32(c.hd.x >> 16) * (float)(c.s ? b1 : b0);
     }
+    struct Scl {};
+    __device__ static Scl prep(const Raw&) { return Scl{}; }
+    __device__ static void scale(const Scl&, const Raw& c, int j, float& rs, float& rmin) { scales(c, j, rs, rmin); }
 };
 
 // Q6_K: lane (m, h) holds sub-block 2j + h of block j (the GEMV's split, half super-block units)
@@ -991,6 +1020,9 @@ struct Mx<T_Q6_K> {
         rs = f16_to_f32(c.d & 0xFFFFu);
         rmin = 0.0f;
     }
+    struct Scl {};
+    __device__ static Scl prep(const Raw&) { return Scl{}; }
+    __device__ static void scale(const Scl&, const Raw& c, int j, float& rs, float& rmin) { scales(c, j, rs, rmin); }
 };
 
 // Q8_0: four blocks per unit, the GEMV layout (lane half h holds half h of each block).
@@ -1007,6 +1039,9 @@ struct Mx<T_Q8_0> {
         rs = f16_to_f32(c.d[j] & 0xFFFFu);
         rmin = 0.0f;
     }
+    struct Scl {};
+    __device__ static Scl prep(const Raw&) { return Scl{}; }
+    __device__ static void scale(const Scl&, const Raw& c, int j, float& rs, float& rmin) { scales(c, j, rs, rmin); }
 };
 
 // Q4_0: four blocks per unit; both lane halves load a row's whole block (16 bytes) and take the low
@@ -1042,6 +1077,9 @@ struct Mx<T_Q4_0> {
         rs = f16_to_f32(c.d[j] & 0xFFFFu);
         rmin = 0.0f;
     }
+    struct Scl {};
+    __device__ static Scl prep(const Raw&) { return Scl{}; }
+    __device__ static void scale(const Scl&, const Raw& c, int j, float& rs, float& rmin) { scales(c, j, rs, rmin); }
 };
 
 // Gate + up (+ SwiGLU + Q8_0 of h) or down for up to MX_NT tokens per pass of one expert's row tile.
@@ -1128,6 +1166,7 @@ k_gemv_mx(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_l
                 a[j] = ld16(arow + (size_t)min(u * BPU + j, KB - 1) * 32);
         };
         auto accum = [&](const Raw& w, const uint4(&a)[BPU], int u) {
+            const auto scl = X::prep(w);
 #pragma unroll
             for (int j = 0; j < BPU; ++j) {
                 const int b = u * BPU + j;
@@ -1145,7 +1184,7 @@ k_gemv_mx(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_l
                                                               __builtin_bit_cast(v4i_t, bw), v16i_t{}, 0, 0, 0);
                 }
                 float rs, rmin;
-                X::scales(w, j, rs, rmin);
+                X::scale(scl, w, j, rs, rmin);
                 // tokens of registers 0-3: 4h..4h+3, of 4-7: 8+4h..11+4h (only when the pass has them)
                 const float4* sp = reinterpret_cast<const float4*>(msc + b * MX_NT + 4 * h);
                 const float4 s0 = sp[0], s1 = sp[1];
@@ -1320,6 +1359,7 @@ k_gemv_mxt(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_
             }
         };
         auto accum = [&](const Raw& wr, const uint4(&a)[BPU], int u, float(&ac)[MX_NT / 2]) {
+            const auto scl = X::prep(wr);
             // the unit's blocks in range: K-quant units are whole super-blocks; the others end at KB
             const int nbk = is_kquant(TYPE) ? BPU : min(BPU, KB - u * BPU);  // wave-uniform
             v16i_t D[2], D2[2];
@@ -1332,7 +1372,7 @@ k_gemv_mxt(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_
                 const v16i_t& D2j = D2[j & 1];
                 const int b = u * BPU + j;
                 float rs, rmin;
-                X::scales(wr, j, rs, rmin);
+                X::scale(scl, wr, j, rs, rmin);
                 // tokens of registers 0-3: 4h..4h+3, of 4-7: 8+4h..11+4h (only when the pass has them)
                 const float4* sp = reinterpret_cast<const float4*>(msc + b * MX_NT + 4 * h);
                 const float4 s0 = sp[0], s1 = sp[1];
