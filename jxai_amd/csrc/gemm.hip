@@ -54,10 +54,7 @@
 
 namespace jx {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef __bf16 b8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h2v __attribute__((ext_vector_type(2)));
-typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int HB = 4;  // 32-blocks per staged half-unit
 
@@ -98,24 +95,6 @@ __device__ __forceinline__ void dma16(const void* src, void* base) {
 }
 __device__ __forceinline__ void dma4(const void* src, void* base) {
     __builtin_amdgcn_global_load_lds(src, (lds_ptr)base, 4, 0, 0);
-}
-
-__device__ __forceinline__ h2v as_h2(uint32_t v) { return __builtin_bit_cast(h2v, v); }
-
-// 8 bytes (w0, w1) of small unsigned integers v (after mask/flip) -> 8 fp16
-// c1 * (1024 + v) + c0, exact: the perm builds fp16 bit patterns 0x64vv =
-// 1024 + vv and one fused fp16 fma removes the bias.
-__device__ __forceinline__ h8 cvt8(uint32_t w0, uint32_t w1, uint32_t mask, uint32_t flip, h2v c1, h2v c0) {
-    const uint32_t a = (w0 & mask) ^ flip, b = (w1 & mask) ^ flip;
-    const h2v x0 = as_h2(__builtin_amdgcn_perm(0x64646464u, a, 0x04010400u));
-    const h2v x1 = as_h2(__builtin_amdgcn_perm(0x64646464u, a, 0x04030402u));
-    const h2v x2 = as_h2(__builtin_amdgcn_perm(0x64646464u, b, 0x04010400u));
-    const h2v x3 = as_h2(__builtin_amdgcn_perm(0x64646464u, b, 0x04030402u));
-    const h2v y0 = __builtin_elementwise_fma(x0, c1, c0);
-    const h2v y1 = __builtin_elementwise_fma(x1, c1, c0);
-    const h2v y2 = __builtin_elementwise_fma(x2, c1, c0);
-    const h2v y3 = __builtin_elementwise_fma(x3, c1, c0);
-    return h8{y0.x, y0.y, y1.x, y1.y, y2.x, y2.y, y3.x, y3.y};
 }
 
 __device__ __forceinline__ h2v splat(float v) {
@@ -329,8 +308,6 @@ struct WRaw {  // Q4_0 / Q5_0 / Q8_0: 16 bytes per 32-block, row n's fp16 block 
     }
 };
 
-// Four bits -> bit 0 of four bytes (disjoint shifted copies, no carries).
-__device__ __forceinline__ uint32_t spread4(uint32_t x) { return ((x & 0xFu) * 0x00204081u) & 0x01010101u; }
 
 template <bool V>
 struct Parity {

@@ -1447,6 +1447,214 @@ k_gemv_mxt(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_
     }
 }
 
+// ---------------------------------------------------------------- fp32-activation down, several tokens
+// A down projection whose h has no Q8_0 form (Q5_0, or a K-quant whose d_ff is not a multiple of 256)
+// takes the reference's fp32-activation dots (vec_dot_quant_f32, src/quant.cpp:3269-3305).  With a few
+// tokens per expert (batched decode) it ran on the down GEMM's 64-pair tiles.  Here, as in k_gemv_mxt:
+// MR row tiles of one expert per block, the pass's tokens staged once, each wave walking its units with
+// one unit per tile in flight.  The tokens' operand is h's matrix-core hi form (fp16(h * 2^-E), E per
+// token, k_f32_to_acth: relative error <= 2^-12 per value, as the down GEMM's), staged in LDS; the
+// weights enter two v_mfma_f32_32x32x16_f16 per 32-block as exact small integers (Q4_K q, Q5_0 q - 16),
+// and each block's fp32 sums are scaled by the row's block scale (Q4_K: plus the min term from the
+// block's exact fp32 sum of h * 2^-E); 2^E at the end.
+template <int TYPE>
+struct Mh;
+
+template <>
+struct Mh<T_Q4_K> {  // super-block units, the GEMV layout of Mx<T_Q4_K>
+    using X = Mx<T_Q4_K>;
+    using Raw = X::Raw;
+    using Scl = X::Scl;
+    static constexpr int BPU = X::BPU;
+    static constexpr bool MIN = true;
+    static constexpr float C0 = -1024.0f;  // operand q
+    __device__ static int units(const QMat& W) { return X::units(W); }
+    __device__ static void load(Raw& c, const QMat& W, int e, int rt, int u, int m, int h, bool ok) {
+        X::load(c, W, e, rt, u, m, h, ok);
+    }
+    __device__ static uint4 bop(const Raw& c, int j, int h) { return X::bop(c, j, h); }
+    __device__ static Scl prep(const Raw& c) { return X::prep(c); }
+    __device__ static void scale(const Scl& s, const Raw& c, int j, float& rs, float& rmin) { X::scale(s, c, j, rs, rmin); }
+};
+
+template <>
+struct Mh<T_Q5_0> {  // four blocks per unit; both lane halves load a row's whole block and take their half
+    struct Raw {
+        uint4 q[4];
+        uint32_t d[4];
+        uint32_t qh[4];
+    };
+    struct Scl {};
+    static constexpr int BPU = 4;
+    static constexpr bool MIN = false;
+    static constexpr float C0 = -1040.0f;  // operand q5 - 16
+    __device__ static int units(const QMat& W) { return (W.nkb + BPU - 1) / BPU; }
+    __device__ static void load(Raw& c, const QMat& W, int e, int rt, int u, int m, int, bool ok) {
+        const uint8_t* qb = W.qs + e * W.qs_es;
+        const uint8_t* sb = W.sc + e * W.sc_es;
+        const uint8_t* xb = W.ex + e * W.ex_es;
+        const size_t b0 = (size_t)rt * W.nkb + (size_t)u * BPU;
+        const int left = W.nkb - u * BPU;
+#pragma unroll
+        for (int i = 0; i < BPU; ++i) {
+            const bool v = ok && i < left;
+            const size_t t = (b0 + i) * 32 + m;
+            c.q[i] = ld_stream16(v ? qb + t * 16 : W.pad_qs + m * 16);
+            c.d[i] = *reinterpret_cast<const uint16_t*>(v ? sb + t * 2 : W.pad_sc + m * 2);
+            c.qh[i] = *reinterpret_cast<const uint32_t*>(v ? xb + t * 4 : W.pad_ex + m * 4);
+        }
+    }
+    // elements 16h .. 16h + 15: nibble half h of the 16 quant bytes, fifth bits 16h .. 16h + 15
+    // (dequantize_row_q5_0, src/quant.cpp:1585-1600)
+    __device__ static uint4 bop(const Raw& c, int j, int h) {
+        const uint4 v = c.q[j];
+        const uint32_t hb = c.qh[j] >> (16 * h);
+        const int sh = 4 * h;
+        return make_uint4(((v.x >> sh) & 0x0F0F0F0Fu) | (spread4(hb) << 4), ((v.y >> sh) & 0x0F0F0F0Fu) | (spread4(hb >> 4) << 4),
+                          ((v.z >> sh) & 0x0F0F0F0Fu) | (spread4(hb >> 8) << 4),
+                          ((v.w >> sh) & 0x0F0F0F0Fu) | (spread4(hb >> 12) << 4));
+    }
+    __device__ static Scl prep(const Raw&) { return Scl{}; }
+    __device__ static void scale(const Scl&, const Raw& c, int j, float& rs, float& rmin) {
+        rs = f16_to_f32(c.d[j] & 0xFFFFu);
+        rmin = 0.0f;
+    }
+};
+
+// Row tiles per block and waves per block of the fp32-activation multi-token down.
+template <int TYPE>
+constexpr int mxh_mr() { return TYPE == T_Q5_0 ? 2 : 3; }  // Q5_0: three units of 24 registers spill
+constexpr int MXH_WAVES = 4;
+// Dynamic LDS of one block: the staged tokens (fp16 rows of K + 8) and, for K-quants, the blocks' sums.
+__host__ __device__ inline size_t mxh_lds(int K, bool kq) {
+    return (size_t)MX_NT * (K + 8) * 2 + (kq ? (size_t)(K / 32) * MX_NT * sizeof(float) : 0);
+}
+
+template <int TYPE, int WAVES, int MR>
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
+k_gemv_mxh(QMat W, ActH hin, Groups grp, float* y) {
+    using X = Mh<TYPE>;
+    using Raw = typename X::Raw;
+    constexpr int BPU = X::BPU;
+    constexpr int NTH = WAVES * 64;
+    extern __shared__ __align__(16) uint8_t mxh_lds_base[];
+    __shared__ float red[MR][WAVES][MX_NT / 2][64];
+    __shared__ float spe[MX_NT];
+    const int nch = (W.nrt + MR - 1) / MR;
+    const int rt0 = (int)(blockIdx.x % nch) * MR, nj = min(MR, W.nrt - rt0);  // tiles rt0 .. rt0 + nj - 1
+    const int4 rec = group_of(grp, blockIdx.x / nch);
+    const int e = rec.x, p0 = rec.y, cnt = rec.z;
+    if (cnt == 0) return;
+    const int tid = threadIdx.x, lane = tid & 63, m = lane & 31, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int K = hin.K, KB = K / 32, KH = hin.KH, AS = K + 8;
+    _Float16* As = reinterpret_cast<_Float16*>(mxh_lds_base);                    // [MX_NT][AS]: h * 2^-E
+    float* Ss = reinterpret_cast<float*>(mxh_lds_base + (size_t)MX_NT * AS * 2);  // [KB][MX_NT]: sums
+    const int nu = X::units(W);
+    const h2v c1 = h2v{(_Float16)1.0f, (_Float16)1.0f}, c0 = h2v{(_Float16)X::C0, (_Float16)X::C0};
+    auto pass = [&](int tb0, int nt, auto hi8c) {
+        constexpr bool HI8 = decltype(hi8c)::value;
+        // every tile's first unit goes out first
+        Raw w[MR];
+#pragma unroll
+        for (int j = 0; j < MR; ++j) X::load(w[j], W, e, min(rt0 + j, W.nrt - 1), wave, m, h, wave < nu);
+        // the tokens' rows of the hi form (zero rows past the pass), four 16-byte loads in flight per thread
+        const size_t row0 = (size_t)(p0 + tb0);
+        const int c8 = K / 8;
+        for (int i0 = tid; i0 < MX_NT * c8; i0 += 4 * NTH) {
+            uint4 v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int i = i0 + q * NTH, t = i / c8, k = 8 * (i - t * c8);
+                v[q] = (i < MX_NT * c8 && t < nt)
+                           ? *reinterpret_cast<const uint4*>(hin.hl + (row0 + t) * (size_t)KH * 256 + (k >> 7) * 256 + (k & 127))
+                           : make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int i = i0 + q * NTH, t = i / c8, k = 8 * (i - t * c8);
+                if (i < MX_NT * c8) *reinterpret_cast<uint4*>(As + t * AS + k) = v[q];
+            }
+        }
+        if (tid < MX_NT) spe[tid] = tid < nt ? hin.pe[(row0 + tid) * KH] : 0.0f;
+        if constexpr (X::MIN) {
+            // each block's fp32 sum of h * 2^-E from its three exact bf16 pieces
+            for (int i = tid; i < KB * MX_NT; i += NTH) {
+                const int b = i / MX_NT, t = i - b * MX_NT;
+                float s = 0.0f;
+                if (t < nt) {
+                    const uint16_t* xp = hin.xm + (row0 + t) * (size_t)hin.KU * 24 + (b >> 3) * 24 + (b & 7);
+                    s = (__uint_as_float((uint32_t)xp[0] << 16) + __uint_as_float((uint32_t)xp[8] << 16)) +
+                        __uint_as_float((uint32_t)xp[16] << 16);
+                }
+                Ss[i] = s;
+            }
+        }
+        __syncthreads();
+        float acc[MR][MX_NT / 2];
+#pragma unroll
+        for (int j = 0; j < MR; ++j)
+#pragma unroll
+            for (int r = 0; r < MX_NT / 2; ++r) acc[j][r] = 0.0f;
+        // A rows: token m % 16 (rows 16-31 repeat 0-15; their D rows are not used)
+        const _Float16* arow = As + (m & 15) * AS + 16 * h;
+        for (int u = wave; u < nu; u += WAVES) {
+#pragma unroll
+            for (int j = 0; j < MR; ++j) {
+                const auto scl = X::prep(w[j]);
+#pragma unroll
+                for (int jb = 0; jb < BPU; ++jb) {
+                    const int b = u * BPU + jb;
+                    if (!is_kquant(TYPE) && b >= KB) break;  // wave-uniform
+                    const uint4 bw = X::bop(w[j], jb, h);
+                    const h8 b0 = cvt8(bw.x, bw.y, 0xFFFFFFFFu, 0u, c1, c0), b1 = cvt8(bw.z, bw.w, 0xFFFFFFFFu, 0u, c1, c0);
+                    const h8 a0 = *reinterpret_cast<const h8*>(arow + b * 32), a1 = *reinterpret_cast<const h8*>(arow + b * 32 + 8);
+                    v16f D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, v16f{}, 0, 0, 0);
+                    D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, D, 0, 0, 0);
+                    float rs, rmin;
+                    X::scale(scl, w[j], jb, rs, rmin);
+                    // tokens of registers 0-3: 4h..4h+3, of 4-7: 8+4h..11+4h
+                    float sy[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                    if constexpr (X::MIN) {
+                        const float4 s0 = *reinterpret_cast<const float4*>(Ss + b * MX_NT + 4 * h);
+                        const float4 s1 = HI8 ? *reinterpret_cast<const float4*>(Ss + b * MX_NT + 8 + 4 * h) : s0;
+                        sy[0] = s0.x; sy[1] = s0.y; sy[2] = s0.z; sy[3] = s0.w;
+                        sy[4] = s1.x; sy[5] = s1.y; sy[6] = s1.z; sy[7] = s1.w;
+                    }
+#pragma unroll
+                    for (int r = 0; r < MX_NT / 2; ++r) {
+                        if (r >= 4 && !HI8) break;
+                        acc[j][r] = __builtin_fmaf(rs, D[r], acc[j][r]);
+                        if constexpr (X::MIN) acc[j][r] = __builtin_fmaf(rmin, sy[r], acc[j][r]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);  // one block's products at a time (16 result registers)
+                }
+                X::load(w[j], W, e, min(rt0 + j, W.nrt - 1), u + WAVES, m, h, u + WAVES < nu);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < MR; ++j)
+#pragma unroll
+            for (int r = 0; r < MX_NT / 2; ++r) red[j][wave][r][lane] = acc[j][r];
+        __syncthreads();
+        const int nr = nt > 8 ? 4 + min(4, nt - 8) : min(4, nt);
+        for (int q = wave; q < nj * nr; q += WAVES) {  // wave-uniform
+            const int j = q / nr, r = q - j * nr, rt = rt0 + j;
+            const int t = (r < 4 ? 4 * h + r : 8 + 4 * h + (r - 4));
+            float v0 = 0.0f;
+#pragma unroll
+            for (int w2 = 0; w2 < WAVES; ++w2) v0 += red[j][w2][r][lane];
+            if (t < nt) y[(row0 + t) * W.rows + rt * 32 + m] = v0 * spe[t];
+        }
+    };
+    for (int tb0 = 0; tb0 < cnt; tb0 += MX_NT) {
+        const int nt = min(MX_NT, cnt - tb0);
+        if (tb0) __syncthreads();  // the previous pass is done with the staged tokens, spe and red
+        if (nt > 8) pass(tb0, nt, std::integral_constant<bool, true>{});
+        else pass(tb0, nt, std::integral_constant<bool, false>{});
+    }
+}
+
 #ifndef JX_GEMV_GATEUP_WAVES
 #define JX_GEMV_GATEUP_WAVES 4
 #endif
@@ -2379,6 +2587,35 @@ void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_l
         case T_Q4_K: down_t<T_Q4_K, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
         case T_Q5_K: down_t<T_Q5_K, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
         case T_Q6_K: down_t<T_Q6_K, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
+        default: break;
+    }
+}
+
+template <int TYPE>
+static size_t mxh_lds_total(int K) {
+    constexpr int MR = mxh_mr<TYPE>();
+    return mxh_lds(K, is_kquant(TYPE)) + (size_t)MR * MXH_WAVES * (MX_NT / 2) * 64 * sizeof(float) + MX_NT * sizeof(float);
+}
+
+bool gemv_down_f16_fits(int type, int K) {
+    if (K % 128 != 0) return false;
+    switch (type) {
+        case T_Q4_K: return mxh_lds_total<T_Q4_K>(K) <= (size_t)160 * 1024;
+        case T_Q5_0: return mxh_lds_total<T_Q5_0>(K) <= (size_t)160 * 1024;
+        default: return false;
+    }
+}
+
+void launch_gemv_down_f16(const QMat& dn, const ActH& hh, const Groups& grp, int slots, float* y, hipStream_t st) {
+    const int K = hh.K;
+    auto go = [&](auto kern, int mr, bool kq) {
+        const size_t lds = mxh_lds(K, kq);
+        lds_optin(kern, lds);
+        hipLaunchKernelGGL(kern, dim3((dn.nrt + mr - 1) / mr * slots), dim3(MXH_WAVES * 64), lds, st, dn, hh, grp, y);
+    };
+    switch (dn.type) {
+        case T_Q4_K: go(k_gemv_mxh<T_Q4_K, MXH_WAVES, mxh_mr<T_Q4_K>()>, mxh_mr<T_Q4_K>(), true); break;
+        case T_Q5_0: go(k_gemv_mxh<T_Q5_0, MXH_WAVES, mxh_mr<T_Q5_0>()>, mxh_mr<T_Q5_0>(), false); break;
         default: break;
     }
 }

@@ -206,6 +206,10 @@ int gemv_max_k(bool gateup, int tb, bool f32);
 // Decode regime: down projection over Q8_0 (hq) or fp32 (hf) activations into y[pair][d].
 void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp,
                       int slots, int tb, float* y, hipStream_t st, const CombineOut& comb = CombineOut{});
+// Decode regime, fp32 h (no Q8_0 form): the down projection on fp16 matrix cores over h's hi form (hh,
+// k_f32_to_acth), a few tokens per expert; built for Q4_K and Q5_0 where the staged tokens fit the LDS.
+bool gemv_down_f16_fits(int type, int K);
+void launch_gemv_down_f16(const QMat& dn, const ActH& hh, const Groups& grp, int slots, float* y, hipStream_t st);
 // Prefill regime: matrix-core grouped GEMMs over the dispatch tile table.
 // gate/up writes SwiGLU(h) as Q8_0 (hq.q != null; the down GEMM takes it after
 // launch_q8_to_acth) and/or fp32 (hf != null).

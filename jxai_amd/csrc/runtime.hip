@@ -781,10 +781,16 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
             else
                 jx::launch_q8_to_acth(L->hq, nk, L->hh.a, st, false);
         }
-        Launch l(L, "down_mfma", st);
-        ks = jx::mfma_down_ksplit(L->hh.a.K);
-        jx::launch_mfma_down(L->down.m, L->hh.a, grp, tiles_ub, L->y, st, ks, L->ystride,
-                             nk <= jx::MFMA_DOWN_SMALL_MAX_PPE * E);
+        // fp32 h at a few tokens per expert: the multi-token down on the fp16 matrix cores where built
+        if (!mfma && L->down_f32 && jx::gemv_down_f16_fits(L->down.m.type, L->hh.a.K)) {
+            Launch l(L, "down_gemv_f16", st);
+            jx::launch_gemv_down_f16(L->down.m, L->hh.a, grp, slots, L->y, st);
+        } else {
+            Launch l(L, "down_mfma", st);
+            ks = jx::mfma_down_ksplit(L->hh.a.K);
+            jx::launch_mfma_down(L->down.m, L->hh.a, grp, tiles_ub, L->y, st, ks, L->ystride,
+                                 nk <= jx::MFMA_DOWN_SMALL_MAX_PPE * E);
+        }
     } else {
         jx::CombineOut comb;
         if (fold) {
