@@ -154,8 +154,10 @@ def algorithmic(cfg, n, counts):
     nbytes = distinct * (gu_bytes + dn_bytes) + synth.shared_bytes(cfg)
     nbytes += E * d * 4 + (d * 4 if cfg.shared_gate else 0) + n * d * 4 * 2
     ops = 2 * n * cfg.top_k * 3 * d * Fd + 2 * n * 3 * d * cfg.d_ff_shared
+    sh_gu = 2 * F.matrix_bytes(t, cfg.d_ff_shared, d) if cfg.d_ff_shared else 0
     return dict(bytes=nbytes, ops=ops, distinct=distinct, gateup_bytes=distinct * gu_bytes,
-                gateup_ops=2 * n * cfg.top_k * 2 * d * Fd, down_bytes=distinct * dn_bytes)
+                gateup_ops=2 * n * cfg.top_k * 2 * d * Fd, down_bytes=distinct * dn_bytes,
+                shared_gateup_bytes=sh_gu)
 
 
 def pct(a, q):
@@ -364,21 +366,24 @@ def main():
         s_dec = r["wall_s"]
         a_dec = algorithmic(cfg, nd, r["counts"])
         # the dominant decode kernel: the one-launch step where the layer takes it (all of the layer's
-        # bytes), else the gate/up GEMV (the gate and up matrices of the selected experts)
+        # bytes), else the gate/up GEMV (the gate and up matrices of the selected experts, and of the
+        # shared expert where its blocks join the launch: gateup_gemv_shared)
         # (decode_fused_y: the one-launch step writing y for a separate combine, top-k above 2)
         fused = next((kk for kk in ("decode_fused_cu", "decode_fused", "decode_fused_y") if kk in r["prof"]), None)
-        role = fused or "gateup_gemv"
+        role = fused or ("gateup_gemv_shared" if "gateup_gemv_shared" in r["prof"] else "gateup_gemv")
         if role not in r["prof"]:
             raise RuntimeError(f"decode: no {role} launch among the profiled kernels {sorted(r['prof'])}")
         dg_ms, dg_n = r["prof"][role]
         dg_avg = dg_ms / max(dg_n, 1) / 1e3
-        dbytes = a_dec["bytes"] if fused else a_dec["gateup_bytes"]
+        dbytes = (a_dec["bytes"] if fused else
+                  a_dec["gateup_bytes"] + (a_dec["shared_gateup_bytes"] if role == "gateup_gemv_shared" else 0))
         dec_med = float(np.median(r["step_ms"])) / 1e3
         tr, tr_note = measured_traffic(role, nd)
         roof = {"bound": "hbm",
                 "kernel": ("k_decode_p (the whole one-token step, one block per CU)" if fused == "decode_fused_cu"
                            else "k_decode1 (the whole one-token step)" if fused
-                           else "k_gemv_gateup (gate+up dequant-GEMV + SwiGLU)"),
+                           else "k_gemv_mxt (routed and shared gate+up GEMV + SwiGLU, one launch)"
+                           if role == "gateup_gemv_shared" else "k_gemv_gateup (gate+up dequant-GEMV + SwiGLU)"),
                 "achieved": dbytes / dg_avg / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": dbytes / dg_avg / 1e9 / HBM_PEAK_GBS,
                 "traffic": tr, "traffic_note": tr_note,

@@ -1263,7 +1263,8 @@ constexpr size_t mx_red_bytes() { return (size_t)MR * WAVES * (MX_NT / 2) * 64 *
 
 template <int TYPE, bool GATEUP, int WAVES, int MR>
 __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
-k_gemv_mxt(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_ld, float* y, SmallTail tail) {
+k_gemv_mxt(QMat W0r, QMat W1r, ActQ8 actr, Groups grpr, ActQ8 hqr, float* hfr, int hf_ldr, float* yr, SmallTail tail,
+           SharedPart sh) {
     using X = Mx<TYPE>;
     using Raw = typename X::Raw;
     constexpr int BPU = X::BPU;
@@ -1271,14 +1272,35 @@ k_gemv_mxt(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_
     extern __shared__ __align__(16) float2 msc[];   // [block][MX_NT]: (scale, sum) of each token
     __shared__ float red[MR][WAVES][MX_NT / 2][64];
     static_assert(sizeof(red) == mx_red_bytes<WAVES, MR>(), "red");
-    // grid: chunks of MR row tiles fastest over the slots, then (gate/up) the one tail block
+    // grid: chunks of MR row tiles fastest over the slots, then the shared expert's blocks (chunks fastest
+    // over its token groups, then its K parts), then (gate/up) the one tail block
     if (GATEUP && tail.on && blockIdx.x == gridDim.x - 1) {  // the extra block: dispatch tables only
         small_tail(tail, threadIdx.x);
         return;
     }
+    const bool shb = sh.slots > 0 && (int)blockIdx.x >= sh.blocks0;  // block-uniform
+    // the shared blocks' matrices: the routed ones with the shared bases (expert 0), rows and K (selecting
+    // whole structs by reference made the Q4_K gate/up spill ~1900 VGPRs)
+    QMat W0 = W0r, W1 = W1r;
+    if (shb) {
+        W0.qs = sh.g.qs;
+        W0.sc = sh.g.sc;
+        W0.ex = sh.g.ex;
+        W0.nrt = sh.g.nrt;
+        W0.rows = sh.g.rows;
+        W0.nkb = sh.g.nkb;
+        W0.act = sh.g.act;
+        W1.qs = sh.u.qs;
+        W1.sc = sh.u.sc;
+        W1.ex = sh.u.ex;
+    }
+    const ActQ8& act = (shb && !GATEUP) ? sh.hq : actr;
+    const Groups& grp = shb ? sh.grp : grpr;
+    const int bi = shb ? (int)blockIdx.x - sh.blocks0 : (int)blockIdx.x;
     const int nch = (W0.nrt + MR - 1) / MR;
-    const int rt0 = (int)(blockIdx.x % nch) * MR, nj = min(MR, W0.nrt - rt0);  // tiles rt0 .. rt0 + nj - 1
-    const int4 rec = group_of(grp, blockIdx.x / nch);
+    const int rt0 = (bi % nch) * MR, nj = min(MR, W0.nrt - rt0);  // tiles rt0 .. rt0 + nj - 1
+    const int gi = bi / nch, slot = shb ? gi % sh.slots : gi, kp = shb ? gi / sh.slots : 0;
+    const int4 rec = group_of(grp, slot);
     const int e = rec.x, p0 = rec.y, cnt = rec.z;
     if (cnt == 0) return;
     const int tid = threadIdx.x, lane = tid & 63, m = lane & 31, h = lane >> 5;
@@ -1286,7 +1308,14 @@ k_gemv_mxt(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_
     const int kw = wave % HW;
     const QMat& W = (GATEUP && wave >= HW) ? W1 : W0;
     const int K = act.K, KB = K / 32;
-    const int nu = X::units(W0);
+    // units ulo .. nu - 1 (a shared down's K part p: the p-th range of upp units), blocks kb0 .. kb1 - 1
+    const int nua = X::units(W0), upp = (nua + sh.kparts - 1) / sh.kparts;
+    const int ulo = (shb && !GATEUP) ? kp * upp : 0, nu = (shb && !GATEUP) ? min(nua, ulo + upp) : nua;
+    const int kb0 = ulo * BPU, kb1 = min(KB, nu * BPU);
+    ActQ8 hq = shb ? sh.hq : hqr;
+    float* const hf = shb ? sh.hf : hfr;
+    const int hf_ld = shb ? sh.hf_ld : hf_ldr;
+    float* const y = shb ? sh.y + (size_t)kp * sh.grp.n_tok * W0.rows : yr;
     // one pass of up to MX_NT tokens; HI8: tokens 8.. present (D registers 4-7 carry results), a
     // compile-time switch (as a runtime one it branched around single LDS reads and moves)
     auto pass = [&](int tb0, int nt, auto hi8c) {
@@ -1296,7 +1325,7 @@ k_gemv_mxt(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_
         // last one; their results are dropped)
         Raw w[MR];
 #pragma unroll
-        for (int j = 0; j < MR; ++j) X::load(w[j], W, e, min(rt0 + j, W0.nrt - 1), kw, m, h, kw < nu);
+        for (int j = 0; j < MR; ++j) X::load(w[j], W, e, min(rt0 + j, W0.nrt - 1), ulo + kw, m, h, ulo + kw < nu);
         uint4 aa[BPU], ab[BPU];
         auto src = [&](int i) -> size_t {
             return GATEUP ? (size_t)token_of(grp, rec, tb0 + i) : (size_t)(p0 + tb0 + i);
@@ -1318,26 +1347,27 @@ k_gemv_mxt(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_
                 a[j] = ld16(arow + (size_t)min(u * BPU + j, KB - 1) * 32);
         };
         // the first two units' activations go out before the scales are staged
-        int u = kw;
+        int u = ulo + kw;
         lda(aa, u);
         lda(ab, u + HW);
-        // the tokens' (scale, sum) per block into LDS, entry 16 b + t: a thread's entries all belong to its
-        // token t = tid % 16 (the thread count is a multiple of 16), whose row was looked up once above, and
-        // MX_STAGE scale loads are in flight per thread (one round at K <= 4096 for 4 waves: the token
-        // list and the scales are two dependent round trips, not one per entry group)
+        // the tokens' (scale, sum) of blocks kb0 .. kb1 - 1 into LDS, entry 16 (b - kb0) + t: a thread's
+        // entries all belong to its token t = tid % 16 (the thread count is a multiple of 16), whose row was
+        // looked up once above, and MX_STAGE scale loads are in flight per thread (one round at K <= 4096
+        // for 4 waves: the token list and the scales are two dependent round trips, not one per entry group)
         constexpr int MX_STAGE = 4;
-        for (int i0 = tid; i0 < KB * MX_NT; i0 += MX_STAGE * WAVES * 64) {
+        const int nsc = (kb1 - kb0) * MX_NT;
+        for (int i0 = tid; i0 < nsc; i0 += MX_STAGE * WAVES * 64) {
             float2 v[MX_STAGE];
 #pragma unroll
             for (int q = 0; q < MX_STAGE; ++q) {
-                const int i = i0 + q * WAVES * 64, b = i / MX_NT;
-                v[q] = (i < KB * MX_NT && tk < nt) ? act.s[srow + b] : make_float2(0.0f, 0.0f);
+                const int i = i0 + q * WAVES * 64, b = kb0 + i / MX_NT;
+                v[q] = (i < nsc && tk < nt) ? act.s[srow + b] : make_float2(0.0f, 0.0f);
             }
 #pragma unroll
             for (int q = 0; q < MX_STAGE; ++q) {
                 const int i = i0 + q * WAVES * 64;
                 // Q4_K / Q5_K: scale * sum (min term); the others do not read the sum
-                if (i < KB * MX_NT)
+                if (i < nsc)
                     msc[i] = make_float2(v[q].x, (TYPE == T_Q4_K || TYPE == T_Q5_K) ? v[q].x * v[q].y : v[q].y);
             }
         }
@@ -1374,7 +1404,7 @@ k_gemv_mxt(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_
                 float rs, rmin;
                 X::scale(scl, wr, j, rs, rmin);
                 // tokens of registers 0-3: 4h..4h+3, of 4-7: 8+4h..11+4h (only when the pass has them)
-                const float4* sp = reinterpret_cast<const float4*>(msc + b * MX_NT + 4 * h);
+                const float4* sp = reinterpret_cast<const float4*>(msc + (b - kb0) * MX_NT + 4 * h);
                 const float4 s0 = sp[0], s1 = sp[1];
                 const float4 s2 = HI8 ? sp[4] : s0, s3 = HI8 ? sp[5] : s1;
                 const float sx[8] = {s0.x, s0.z, s1.x, s1.z, s2.x, s2.z, s3.x, s3.z};
@@ -1699,12 +1729,12 @@ static int num_cus() {
 }
 
 template <int TYPE>
-static void gateup_q8(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots, int tb, ActQ8 hq,
-                      float* hf, int hf_ld, dim3 grid, hipStream_t st, const SmallTail& tail);
+static bool gateup_q8(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots, int tb, ActQ8 hq,
+                      float* hf, int hf_ld, dim3 grid, hipStream_t st, const SmallTail& tail, SharedPart* sh);
 
 template <int TYPE>
-static void gateup_t(const QMat& g, const QMat& u, const ActQ8& xq, const float* xf, int xf_ld, const Groups& grp,
-                     int slots, int tb, ActQ8 hq, float* hf, hipStream_t st, const SmallTail& tail) {
+static bool gateup_t(const QMat& g, const QMat& u, const ActQ8& xq, const float* xf, int xf_ld, const Groups& grp,
+                     int slots, int tb, ActQ8 hq, float* hf, hipStream_t st, const SmallTail& tail, SharedPart* sh) {
     dim3 grid(g.nrt * slots + (tail.on ? 1 : 0));
     const int hf_ld = ((g.rows + 255) / 256) * 256;
     if (xf) {  // fp32 activations: one token, or groups of 4
@@ -1717,15 +1747,16 @@ static void gateup_t(const QMat& g, const QMat& u, const ActQ8& xq, const float*
         };
         if (rows == 1) go(k_gemv_gateup<TYPE, 1, GATEUP_WAVES, 2, true>);
         else go(k_gemv_gateup<TYPE, 4, GATEUP_WAVES, 2, true>);
-        return;
+        return false;
     }
-    if constexpr (TYPE != T_Q5_0) gateup_q8<TYPE>(g, u, xq, grp, slots, tb, hq, hf, hf_ld, grid, st, tail);
+    if constexpr (TYPE != T_Q5_0) return gateup_q8<TYPE>(g, u, xq, grp, slots, tb, hq, hf, hf_ld, grid, st, tail, sh);
+    return false;
 }
 
 // The Q8_0-activation forms (not for Q5_0).
 template <int TYPE>
-static void gateup_q8(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots, int tb, ActQ8 hq,
-                      float* hf, int hf_ld, dim3 grid, hipStream_t st, const SmallTail& tail) {
+static bool gateup_q8(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots, int tb, ActQ8 hq,
+                      float* hf, int hf_ld, dim3 grid, hipStream_t st, const SmallTail& tail, SharedPart* sh) {
     if (tb <= 1) {
         const size_t lds = act_lds_bytes(1, xq.K, false);
         // every block resident at 3 waves per SIMD: the spill-free build (measured: Qwen3-shaped 32.6 -> 31.0 us,
@@ -1745,49 +1776,63 @@ static void gateup_q8(const QMat& g, const QMat& u, const ActQ8& xq, const Group
                            nullptr, 0, grp, hq, hf, hf_ld, tail);
     } else {  // several tokens per expert: the matrix-core form
         const size_t lds = (size_t)(xq.K / 32) * MX_NT * sizeof(float2);
-        auto go = [&](auto kern, int mr, int waves) {
-            lds_optin(kern, lds);
-            const dim3 mg((g.nrt + mr - 1) / mr * slots + (tail.on ? 1 : 0));
-            hipLaunchKernelGGL(kern, mg, dim3(waves * 64), lds, st, g, u, xq, grp, hq, hf, hf_ld, nullptr, tail);
-        };
         constexpr int MR = mx_mr_max<TYPE, true>();
         if constexpr (MR > 1) {
             if (g.nrt * slots >= MX_MR_MIN_ITEMS) {
+                // the shared expert's blocks join where it has this launch's weight format and every block
+                // stays in one resident round
+                const bool shm = sh && sh->slots > 0 && sh->g.type == TYPE && sh->u.type == TYPE && sh->g.nkb == g.nkb &&
+                                 sh->u.nkb == g.nkb && sh->g.nrt == sh->u.nrt &&
+                                 gemv_gateup_joins(TYPE, g.nrt, slots, tb, sh->g.nrt, sh->slots);
+                SharedPart sp = shm ? *sh : SharedPart{};
+                const int rb = (g.nrt + MR - 1) / MR * slots;
+                sp.blocks0 = rb;
+                sp.kparts = 1;
+                const int nb = rb + (shm ? (sp.g.nrt + MR - 1) / MR * sp.slots : 0);
+                auto go = [&](auto kern, int waves) {
+                    lds_optin(kern, lds);
+                    hipLaunchKernelGGL(kern, dim3(nb + (tail.on ? 1 : 0)), dim3(waves * 64), lds, st, g, u, xq, grp, hq,
+                                       hf, hf_ld, nullptr, tail, sp);
+                };
                 // 2-wave blocks (a gate and an up wave, twice the units each, four blocks per CU) where
                 // that puts every block in one resident round: no second round of block prologues and
                 // no tail (measured from HBM: DeepSeek-V2-Lite-shaped 32 tokens 140 -> 130 us,
                 // Qwen1.5-shaped 64 tokens 152 -> 146 us; Mixtral-shaped 32 tokens, 1200 blocks, 213 us
                 // at 4 waves against 236 at 2)
-                if ((g.nrt + MR - 1) / MR * slots <= 4 * num_cus())
-                    go(k_gemv_mxt<TYPE, true, 2, MR>, MR, 2);
+                if (nb <= 4 * num_cus())
+                    go(k_gemv_mxt<TYPE, true, 2, MR>, 2);
                 else
-                    go(k_gemv_mxt<TYPE, true, GATEUP_WAVES, MR>, MR, GATEUP_WAVES);
-                return;
+                    go(k_gemv_mxt<TYPE, true, GATEUP_WAVES, MR>, GATEUP_WAVES);
+                return shm;
             }
         }
-        go(k_gemv_mx<TYPE, true, GATEUP_WAVES>, 1, GATEUP_WAVES);
+        lds_optin(k_gemv_mx<TYPE, true, GATEUP_WAVES>, lds);
+        hipLaunchKernelGGL((k_gemv_mx<TYPE, true, GATEUP_WAVES>), dim3(g.nrt * slots + (tail.on ? 1 : 0)),
+                           dim3(GATEUP_WAVES * 64), lds, st, g, u, xq, grp, hq, hf, hf_ld, nullptr, tail);
     }
+    return false;
 }
 
-void launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots, int tb,
-                        ActQ8 hq, float* hf, hipStream_t st, const SmallTail* tail, const float* xf, int xf_ld) {
+bool launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots, int tb,
+                        ActQ8 hq, float* hf, hipStream_t st, const SmallTail* tail, const float* xf, int xf_ld,
+                        SharedPart* sh) {
     const SmallTail t = tail ? *tail : SmallTail{};
     switch (g.type) {
-        case T_Q4_0: gateup_t<T_Q4_0>(g, u, xq, xf, xf_ld, grp, slots, tb, hq, hf, st, t); break;
-        case T_Q8_0: gateup_t<T_Q8_0>(g, u, xq, xf, xf_ld, grp, slots, tb, hq, hf, st, t); break;
-        case T_Q4_K: gateup_t<T_Q4_K>(g, u, xq, xf, xf_ld, grp, slots, tb, hq, hf, st, t); break;
-        case T_Q5_K: gateup_t<T_Q5_K>(g, u, xq, xf, xf_ld, grp, slots, tb, hq, hf, st, t); break;
-        case T_Q6_K: gateup_t<T_Q6_K>(g, u, xq, xf, xf_ld, grp, slots, tb, hq, hf, st, t); break;
+        case T_Q4_0: return gateup_t<T_Q4_0>(g, u, xq, xf, xf_ld, grp, slots, tb, hq, hf, st, t, sh);
+        case T_Q8_0: return gateup_t<T_Q8_0>(g, u, xq, xf, xf_ld, grp, slots, tb, hq, hf, st, t, sh);
+        case T_Q4_K: return gateup_t<T_Q4_K>(g, u, xq, xf, xf_ld, grp, slots, tb, hq, hf, st, t, sh);
+        case T_Q5_K: return gateup_t<T_Q5_K>(g, u, xq, xf, xf_ld, grp, slots, tb, hq, hf, st, t, sh);
+        case T_Q6_K: return gateup_t<T_Q6_K>(g, u, xq, xf, xf_ld, grp, slots, tb, hq, hf, st, t, sh);
         case T_Q5_0:  // fp32 activations only
-            if (xf) gateup_t<T_Q5_0>(g, u, xq, xf, xf_ld, grp, slots, tb, hq, hf, st, t);
-            break;
-        default: break;
+            if (xf) return gateup_t<T_Q5_0>(g, u, xq, xf, xf_ld, grp, slots, tb, hq, hf, st, t, sh);
+            return false;
+        default: return false;
     }
 }
 
 template <int TYPE, bool F32ACT>
-static void down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp, int slots,
-                   int tb, float* y, hipStream_t st, const CombineOut& comb) {
+static bool down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp, int slots,
+                   int tb, float* y, hipStream_t st, const CombineOut& comb, SharedPart* sh) {
     dim3 grid(dn.nrt * slots);
     const int K = F32ACT ? hf_ld : hq.K;
     if (tb <= 1) {
@@ -1800,27 +1845,46 @@ static void down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, 
             // 4-wave blocks (more of them resident per CU) unless the grid is too small to fill half
             // the CUs (one dense matrix, few tokens); measured: Qwen1.5-shaped 64 tokens routed down
             // 75 -> 44 us, Qwen3-shaped 32 tokens 62 -> 33 us
-            const size_t lds = (size_t)(K / 32) * MX_NT * sizeof(float2);
-            auto go = [&](auto kern, int mr, int waves) {
-                lds_optin(kern, lds);
-                hipLaunchKernelGGL(kern, dim3((dn.nrt + mr - 1) / mr * slots), dim3(waves * 64), lds, st, dn, dn, hq,
-                                   grp, ActQ8{}, nullptr, 0, y, SmallTail{});
-            };
+            size_t lds = (size_t)(K / 32) * MX_NT * sizeof(float2);
             // and 8-wave blocks where two 4-wave blocks' LDS would not fit one CU (long K: the staged scales
             // plus the tiles' partial sums)
             constexpr int MR = mx_mr_max<TYPE, false>();
             if constexpr (MR > 1) {
                 if (dn.nrt * slots >= MX_MR_MIN_ITEMS) {
+                    // the shared down's blocks join (its K in parts of at most a routed block's units) where it
+                    // has this launch's weight format and Q8_0 h
+                    const bool shm = sh && sh->slots > 0 && sh->g.type == TYPE && sh->hq.q != nullptr &&
+                                     sh->g.rows == dn.rows && sh->hq.K == sh->g.cols;
+                    SharedPart sp = shm ? *sh : SharedPart{};
+                    const int rb = (dn.nrt + MR - 1) / MR * slots;
+                    sp.blocks0 = rb;
+                    if (!shm) sp.kparts = 1;
+                    if (shm) {
+                        constexpr int BPU = Mx<TYPE>::BPU;
+                        const int ub = (sp.hq.K / 32 + BPU - 1) / BPU, upp = (ub + sp.kparts - 1) / sp.kparts;
+                        lds = std::max(lds, (size_t)upp * BPU * MX_NT * sizeof(float2));
+                    }
+                    const int nb = rb + (shm ? (sp.g.nrt + MR - 1) / MR * sp.slots * sp.kparts : 0);
+                    auto go = [&](auto kern, int waves) {
+                        lds_optin(kern, lds);
+                        hipLaunchKernelGGL(kern, dim3(nb), dim3(waves * 64), lds, st, dn, dn, hq, grp, ActQ8{}, nullptr, 0,
+                                           y, SmallTail{}, sp);
+                    };
                     const bool lds2 = 2 * (lds + mx_red_bytes<4, MR>()) <= (size_t)160 * 1024;
-                    if (2 * ((dn.nrt + MR - 1) / MR) * slots < num_cus() || !lds2)
-                        go(k_gemv_mxt<TYPE, false, 8, MR>, MR, 8);
+                    if (2 * nb < num_cus() || !lds2)
+                        go(k_gemv_mxt<TYPE, false, 8, MR>, 8);
                     else
-                        go(k_gemv_mxt<TYPE, false, 4, MR>, MR, 4);
-                    return;
+                        go(k_gemv_mxt<TYPE, false, 4, MR>, 4);
+                    return shm;
                 }
             }
-            if (2 * (int)grid.x < num_cus()) go(k_gemv_mx<TYPE, false, 8>, 1, 8);
-            else go(k_gemv_mx<TYPE, false, 4>, 1, 4);
+            auto go = [&](auto kern, int waves) {
+                lds_optin(kern, lds);
+                hipLaunchKernelGGL(kern, grid, dim3(waves * 64), lds, st, dn, dn, hq, grp, ActQ8{}, nullptr, 0, y,
+                                   SmallTail{});
+            };
+            if (2 * (int)grid.x < num_cus()) go(k_gemv_mx<TYPE, false, 8>, 8);
+            else go(k_gemv_mx<TYPE, false, 4>, 4);
         }
     } else {
         const size_t lds = act_lds_bytes(4, K, F32ACT);
@@ -1828,6 +1892,7 @@ static void down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, 
         hipLaunchKernelGGL((k_gemv_down<TYPE, 4, DOWN_WAVES, F32ACT>), grid, dim3(DOWN_WAVES * 64), lds, st, dn, hq,
                            hf, hf_ld, grp, y, comb);
     }
+    return false;
 }
 
 // ---------------------------------------------------------------- one-token step in one launch
@@ -2565,30 +2630,69 @@ int launch_decode_p(const Decode1Args& a, int gtype, int dtype, hipStream_t st) 
     return -1;
 }
 
-void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp, int slots,
-                      int tb, float* y, hipStream_t st, const CombineOut& comb) {
+bool launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp, int slots,
+                      int tb, float* y, hipStream_t st, const CombineOut& comb, SharedPart* sh) {
     // the folded combine is written for the single-token and four-token GEMVs (the few-token path)
     const CombineOut c = tb <= 4 ? comb : CombineOut{};
     if (hf) {  // fp32 activations
         switch (dn.type) {
-            case T_Q4_0: down_t<T_Q4_0, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
-            case T_Q5_0: down_t<T_Q5_0, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
-            case T_Q8_0: down_t<T_Q8_0, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
-            case T_Q4_K: down_t<T_Q4_K, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
-            case T_Q5_K: down_t<T_Q5_K, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
-            case T_Q6_K: down_t<T_Q6_K, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
-            default: break;
+            case T_Q4_0: return down_t<T_Q4_0, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c, nullptr);
+            case T_Q5_0: return down_t<T_Q5_0, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c, nullptr);
+            case T_Q8_0: return down_t<T_Q8_0, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c, nullptr);
+            case T_Q4_K: return down_t<T_Q4_K, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c, nullptr);
+            case T_Q5_K: return down_t<T_Q5_K, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c, nullptr);
+            case T_Q6_K: return down_t<T_Q6_K, true>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c, nullptr);
+            default: return false;
         }
-        return;
     }
     switch (dn.type) {
-        case T_Q4_0: down_t<T_Q4_0, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
-        case T_Q8_0: down_t<T_Q8_0, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
-        case T_Q4_K: down_t<T_Q4_K, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
-        case T_Q5_K: down_t<T_Q5_K, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
-        case T_Q6_K: down_t<T_Q6_K, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c); break;
-        default: break;
+        case T_Q4_0: return down_t<T_Q4_0, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c, sh);
+        case T_Q8_0: return down_t<T_Q8_0, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c, sh);
+        case T_Q4_K: return down_t<T_Q4_K, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c, sh);
+        case T_Q5_K: return down_t<T_Q5_K, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c, sh);
+        case T_Q6_K: return down_t<T_Q6_K, false>(dn, hq, hf, hf_ld, grp, slots, tb, y, st, c, sh);
+        default: return false;
     }
+}
+
+bool gemv_gateup_joins(int type, int nrt, int slots, int tb, int snrt, int sslots) {
+    if (!gemv_mxt_takes(type, true, nrt, slots, tb)) return false;
+    int mr = 1;
+    switch (type) {
+        case T_Q4_0: mr = mx_mr_max<T_Q4_0, true>(); break;
+        case T_Q8_0: mr = mx_mr_max<T_Q8_0, true>(); break;
+        case T_Q4_K: mr = mx_mr_max<T_Q4_K, true>(); break;
+        case T_Q5_K: mr = mx_mr_max<T_Q5_K, true>(); break;
+        case T_Q6_K: mr = mx_mr_max<T_Q6_K, true>(); break;
+        default: return false;
+    }
+    return (nrt + mr - 1) / mr * slots + (snrt + mr - 1) / mr * sslots <= 4 * num_cus();
+}
+
+bool gemv_mxt_takes(int type, bool gateup, int nrt, int slots, int tb) {
+    if (tb <= 4 || nrt * slots < MX_MR_MIN_ITEMS) return false;
+    switch (type) {
+        case T_Q4_0: return (gateup ? mx_mr_max<T_Q4_0, true>() : mx_mr_max<T_Q4_0, false>()) > 1;
+        case T_Q8_0: return (gateup ? mx_mr_max<T_Q8_0, true>() : mx_mr_max<T_Q8_0, false>()) > 1;
+        case T_Q4_K: return (gateup ? mx_mr_max<T_Q4_K, true>() : mx_mr_max<T_Q4_K, false>()) > 1;
+        case T_Q5_K: return (gateup ? mx_mr_max<T_Q5_K, true>() : mx_mr_max<T_Q5_K, false>()) > 1;
+        case T_Q6_K: return (gateup ? mx_mr_max<T_Q6_K, true>() : mx_mr_max<T_Q6_K, false>()) > 1;
+        default: return false;
+    }
+}
+
+int shared_down_kparts(int type, int K, int Ks) {
+    int bpu = 0;
+    switch (type) {
+        case T_Q4_0: bpu = Mx<T_Q4_0>::BPU; break;
+        case T_Q8_0: bpu = Mx<T_Q8_0>::BPU; break;
+        case T_Q4_K: bpu = Mx<T_Q4_K>::BPU; break;
+        case T_Q5_K: bpu = Mx<T_Q5_K>::BPU; break;
+        case T_Q6_K: bpu = Mx<T_Q6_K>::BPU; break;
+        default: return 1;
+    }
+    const int u = (K / 32 + bpu - 1) / bpu, us = (Ks / 32 + bpu - 1) / bpu;
+    return std::max(1, std::min(SHARED_KPARTS_MAX, (us + u - 1) / std::max(1, u)));
 }
 
 template <int TYPE>

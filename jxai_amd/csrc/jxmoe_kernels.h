@@ -193,19 +193,52 @@ int chain_stride(int d);
 void chain_rows(const float* rows, int nrows, int d, float* out);
 void launch_dispatch(const int* ids, int nk, int E, int top_k, const DispatchOut& o, hipStream_t st);
 
+// A dense shared expert's blocks appended to a routed multi-token GEMV launch (k_gemv_mxt): its own
+// matrices and outputs over groups of 16 tokens, so its few long-lived blocks run among the routed
+// ones instead of beside them from a second stream.  Gate/up: g and u, h into hq (and fp32 hf when its
+// down takes fp32 h).  Down: g is the shared down over the Q8_0 h in hq; its K is cut into `kparts`
+// ranges of whole units, part p writing y + p * n * rows, which the combine adds in part order.
+struct SharedPart {
+    QMat g, u;
+    Groups grp;           // identity groups of `chunk` = 16 tokens
+    int slots = 0;        // token groups
+    ActQ8 hq;
+    float* hf = nullptr;
+    int hf_ld = 0;
+    float* y = nullptr;
+    int kparts = 1;
+    int blocks0 = 0;      // set by the launcher: the routed blocks ahead of the shared ones
+};
+// The K parts of a shared down of Ks columns appended to a routed down of K columns: as many as make
+// a shared block's unit range no longer than a routed block's (at most SHARED_KPARTS_MAX).
+constexpr int SHARED_KPARTS_MAX = 8;
+int shared_down_kparts(int type, int K, int Ks);
+// Whether a GEMV launch of nrt row tiles over `slots` groups at `tb` tokens per group takes the multi-tile
+// matrix-core form (k_gemv_mxt) for this weight format, with Q8_0 activations.
+bool gemv_mxt_takes(int type, bool gateup, int nrt, int slots, int tb);
+// Whether a shared gate/up of snrt row tiles over sslots token groups joins that launch: the multi-tile
+// form, and the routed and shared blocks together within one resident round of 2-wave blocks (past it
+// the launch takes 4-wave blocks or a second round, which measured slower than the shared expert on
+// its own stream: Qwen1.5-shaped 64 tokens 141 -> 144 us, DeepSeek-V2-Lite-shaped 32 tokens 132 -> 142 us).
+bool gemv_gateup_joins(int type, int nrt, int slots, int tb, int snrt, int sslots);
+
 // Decode regime: gate+up dequant-GEMV with SwiGLU and Q8_0 re-quantization.
 // Output rows are sorted pairs (routed) or tokens (shared).  With xf, the
 // fp32-activation dots over rows of xf_ld floats (zero-padded to whole K-units;
-// one token or groups of 4) instead of the Q8_0 form xq.
-void launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots,
+// one token or groups of 4) instead of the Q8_0 form xq.  With sh, the shared expert's blocks join the
+// launch where it takes the multi-tile matrix-core form with the same weight format (returns whether
+// they did; otherwise the caller launches the shared expert itself).
+bool launch_gemv_gateup(const QMat& g, const QMat& u, const ActQ8& xq, const Groups& grp, int slots,
                         int tb, ActQ8 hq, float* hf, hipStream_t st, const SmallTail* tail = nullptr,
-                        const float* xf = nullptr, int xf_ld = 0);
+                        const float* xf = nullptr, int xf_ld = 0, SharedPart* sh = nullptr);
 // Largest K the GEMVs accept for token groups of `tb` rows (gate/up or down,
 // Q8_0 or fp32 activations).
 int gemv_max_k(bool gateup, int tb, bool f32);
 // Decode regime: down projection over Q8_0 (hq) or fp32 (hf) activations into y[pair][d].
-void launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp,
-                      int slots, int tb, float* y, hipStream_t st, const CombineOut& comb = CombineOut{});
+// With sh, the shared down's blocks as for launch_gemv_gateup.
+bool launch_gemv_down(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, const Groups& grp,
+                      int slots, int tb, float* y, hipStream_t st, const CombineOut& comb = CombineOut{},
+                      SharedPart* sh = nullptr);
 // Decode regime, fp32 h (no Q8_0 form): the down projection on fp16 matrix cores over h's hi form (hh,
 // k_f32_to_acth), a few tokens per expert; built for Q4_K and Q5_0 where the staged tokens fit the LDS.
 bool gemv_down_f16_fits(int type, int K);
@@ -242,7 +275,8 @@ void launch_min_table(const QMat& m, uint8_t* mn, hipStream_t st);
 // (resid[t] +) rms_norm(acc[t], post_w, eps) (post_ffw_norm, transformer.cpp:2758-2764).
 void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
                     const float* shscale, float* out, hipStream_t st, const float* resid = nullptr,
-                    const float* post_w = nullptr, float eps = 0.0f, const float* y2 = nullptr);
+                    const float* post_w = nullptr, float eps = 0.0f, const float* y2 = nullptr,
+                    int shparts = 1);  // ysh in shparts K parts of n * d floats, added in part order
 // MoETransformerEngine::rms_norm (transformer.cpp:67-73) of rows x d floats: out = x * inv * w.
 void launch_rms_norm(const float* x, const float* w, int rows, int d, float eps, float* out, hipStream_t st);
 

@@ -1169,7 +1169,7 @@ void launch_rms_norm(const float* x, const float* w, int rows, int d, float eps,
 template <int KU>  // slots whose loads go out together (the fma order stays the selection order)
 __global__ void __launch_bounds__(256)
 k_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
-          const float* shscale, const float* resid, float* out, const float* y2) {
+          const float* shscale, const float* resid, float* out, const float* y2, int shparts) {
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;  // float4 index
     const int d4 = d / 4;
     if (idx >= (size_t)n * d4) return;
@@ -1206,7 +1206,11 @@ k_combine(int n, int d, int k, const float* probs, const int* pos_of, const floa
     }
     if (ysh) {
         const float w = shscale[t];
-        const float4 v = *reinterpret_cast<const float4*>(ysh + (size_t)t * d + i);
+        float4 v = *reinterpret_cast<const float4*>(ysh + (size_t)t * d + i);
+        for (int q = 1; q < shparts; ++q) {  // the K parts of a shared down, in part order
+            const float4 b = *reinterpret_cast<const float4*>(ysh + ((size_t)q * n + t) * d + i);
+            v = make_float4(v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w);
+        }
         acc.x = __builtin_fmaf(w, v.x, acc.x);
         acc.y = __builtin_fmaf(w, v.y, acc.y);
         acc.z = __builtin_fmaf(w, v.z, acc.z);
@@ -1224,8 +1228,9 @@ k_combine(int n, int d, int k, const float* probs, const int* pos_of, const floa
 // add (2762-2764): out = resid + rms_norm(acc, post_w).  acc as k_combine
 // computes it, staged chain-major for the exact vec_dot_f32 order of the norm.
 __global__ void __launch_bounds__(256)
-k_combine_norm(int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
-               const float* shscale, const float* post_w, float eps, const float* resid, float* out, const float* y2) {
+k_combine_norm(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
+               const float* shscale, const float* post_w, float eps, const float* resid, float* out, const float* y2,
+               int shparts) {
     extern __shared__ float as[];  // chain-major acc row
     __shared__ float inv_s;
     const int t = blockIdx.x, tid = threadIdx.x, S = d / 16 + 1;
@@ -1236,7 +1241,11 @@ k_combine_norm(int d, int k, const float* probs, const int* pos_of, const float*
             const size_t o = (size_t)pos_of[(size_t)t * k + s] * d + i;
             acc = __builtin_fmaf(w, y2 ? y[o] + y2[o] : y[o], acc);
         }
-        if (ysh) acc = __builtin_fmaf(shscale[t], ysh[(size_t)t * d + i], acc);
+        if (ysh) {
+            float v = ysh[(size_t)t * d + i];
+            for (int q = 1; q < shparts; ++q) v += ysh[((size_t)q * n + t) * d + i];
+            acc = __builtin_fmaf(shscale[t], v, acc);
+        }
         as[(i & 15) * S + (i >> 4)] = acc;
     }
     __syncthreads();
@@ -1254,27 +1263,27 @@ k_combine_norm(int d, int k, const float* probs, const int* pos_of, const float*
 
 void launch_combine(int n, int d, int k, const float* probs, const int* pos_of, const float* y, const float* ysh,
                     const float* shscale, float* out, hipStream_t st, const float* resid, const float* post_w,
-                    float eps, const float* y2) {
+                    float eps, const float* y2, int shparts) {
     if (post_w) {
         const size_t lds = (size_t)16 * (d / 16 + 1) * sizeof(float);
         if (lds > 65536)
             (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_combine_norm),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        hipLaunchKernelGGL(k_combine_norm, dim3((unsigned)n), dim3(256), lds, st, d, k, probs, pos_of, y, ysh, shscale,
-                           post_w, eps, resid, out, y2);
+        hipLaunchKernelGGL(k_combine_norm, dim3((unsigned)n), dim3(256), lds, st, n, d, k, probs, pos_of, y, ysh,
+                           shscale, post_w, eps, resid, out, y2, shparts);
         return;
     }
     const size_t tot = (size_t)n * (d / 4);
     const dim3 grid((unsigned)((tot + 255) / 256));
     if (k <= 2)
         hipLaunchKernelGGL(k_combine<2>, grid, dim3(256), 0, st, n, d, k, probs, pos_of, y, ysh, shscale, resid, out,
-                           y2);
+                           y2, shparts);
     else if (k <= 4)
         hipLaunchKernelGGL(k_combine<4>, grid, dim3(256), 0, st, n, d, k, probs, pos_of, y, ysh, shscale, resid, out,
-                           y2);
+                           y2, shparts);
     else
         hipLaunchKernelGGL(k_combine<8>, grid, dim3(256), 0, st, n, d, k, probs, pos_of, y, ysh, shscale, resid, out,
-                           y2);
+                           y2, shparts);
 }
 
 // Q8_0 of `rows` rows of K fp32 values (quantize_row_q8_0, src/quant.cpp:1029-1045),

@@ -321,6 +321,7 @@ struct jx_moe_layer {
     uint32_t spin_limit = 1u << 18;  // polls (each a device-coherent round trip) before a wait gives up
     hipStream_t last_st = nullptr;   // stream of the last forward (jx_moe_layer_status waits on it)
     uint32_t dec_epoch = 0;
+    int shparts_cap = 1;  // K parts of the shared down's output the workspace holds (ysh)
     bool fused_decode = true;
     bool force_fused = false;  // JX_FUSED=1: also where the separate launches measured faster
     int smfma_min = 0;         // shared expert's GEMM threshold (JX_SMFMA_MIN overrides it: A/B)
@@ -416,7 +417,9 @@ int ensure_workspace(jx_moe_layer* L, int n) {
         // the fused step's shared down tiles poll these scale words for the launch's tag, as for hq.s
         HIPCHK(hipMemset(L->hqs.s, 0, (size_t)cap * L->Fs / 32 * sizeof(float2)));
         L->hqs.K = L->Fs;
-        WS(L->ysh, (size_t)cap * L->d);
+        // the shared down's output, in K parts where its blocks join the routed down launch
+        L->shparts_cap = L->sdown.m.type == L->down.m.type ? jx::shared_down_kparts(L->down.m.type, L->F, L->Fs) : 1;
+        WS(L->ysh, (size_t)L->shparts_cap * cap * L->d);
         const size_t fspad = ((size_t)L->Fs + 255) / 256 * 256;
         if (L->sdown_f32) {
             WS(L->hfs, (size_t)cap * fspad);
@@ -707,22 +710,34 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         Launch l(L, "x_pad", st);
         jx::launch_copy_pad(xdev, d, L->dpad, L->xf, st, n);
     }
-    // shared expert on the side stream, concurrent with the routed gate/up
-    if (L->shared) {
-        HIPCHK(hipEventRecord(L->ev_fork, st));
-        HIPCHK(hipStreamWaitEvent(L->side, L->ev_fork, 0));
-        hipStream_t ss = L->side;
-        jx::Groups sg;
-        sg.identity = 1;
-        sg.n_tok = n;
-        sg.top_k = 1;
-        // the GEMVs' 16-token form: one group per 16 tokens, so the dense expert's row tiles spread
-        // over n / 16 times as many blocks as one group of all tokens (which each block streams pass
-        // by pass)
-        const int sslots = tbs == 16 ? (n + 15) / 16 : 1;
-        if (tbs == 16) sg.chunk = 16;
-        const size_t fspad = ((size_t)L->Fs + 255) / 256 * 256;
-        const int st_ub = (n + jx::MFMA_BN - 1) / jx::MFMA_BN;
+    jx::Groups sg;  // the shared expert's groups: every token
+    sg.identity = 1;
+    sg.n_tok = n;
+    sg.top_k = 1;
+    // the GEMVs' 16-token form: one group per 16 tokens, so the dense expert's row tiles spread
+    // over n / 16 times as many blocks as one group of all tokens (which each block streams pass
+    // by pass)
+    const int sslots = tbs == 16 ? (n + 15) / 16 : 1;
+    if (tbs == 16) sg.chunk = 16;
+    const size_t fspad = ((size_t)L->Fs + 255) / 256 * 256;
+    const int st_ub = (n + jx::MFMA_BN - 1) / jx::MFMA_BN;
+    // The shared expert's GEMV blocks join the routed multi-tile launches where both take that form in one
+    // weight format and the gate/up blocks stay in one resident round (the down also needs Q8_0 h on both
+    // sides): its few long-lived blocks then run among the routed ones instead of from a second stream
+    // beside them, which costs far more than its bytes (measured without the shared expert:
+    // Qwen1.5-shaped 64 tokens 148 -> 113 us per step, DeepSeek-V2-Lite-shaped 32 tokens 134 -> 111 us,
+    // for ~20 and ~10 MB of its weights; joined: Qwen1.5-shaped 16 / 32 tokens 111.5 / 123.6 ->
+    // 108.5 / 117.9 us).
+    // Only both launches together: with the down left on the side stream the joined gate/up measured
+    // slower (DeepSeek-V2-Lite-shaped, fp32 h: 16 / 32 tokens 112.4 / 130.1 -> 123.0 / 140.3 us).
+    const bool sh_dn = L->shared && !smfma && tbs == 16 && tb == 16 && !mfma_down && !L->down_f32 && !L->sdown_f32 &&
+                       L->sdown.m.type == L->down.m.type && L->shparts_cap > 1 &&
+                       jx::gemv_mxt_takes(L->down.m.type, false, L->down.m.nrt, slots, tb);
+    const bool sh_gu = sh_dn && !mfma_gu && !L->gu_f32 && !L->sgu_f32 && L->sgate.m.type == L->gate.m.type &&
+                       L->sup.m.type == L->up.m.type &&
+                       jx::gemv_gateup_joins(L->gate.m.type, L->gate.m.nrt, slots, tb, L->sgate.m.nrt, sslots);
+    int shparts = 1;  // K parts of the shared down's output (the combine adds them)
+    auto shared_gateup = [&](hipStream_t ss) {
         if (smfma_gu) {
             Launch l(L, "shared_gateup_mfma", ss);
             jx::launch_mfma_gateup(L->sgate.m, L->sup.m, L->xh.a, sg, st_ub, L->sdown_f32 ? jx::ActQ8{} : L->hqs,
@@ -732,6 +747,8 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
             jx::launch_gemv_gateup(L->sgate.m, L->sup.m, L->xq, sg, sslots, tbs, L->hqs, L->sdown_f32 ? L->hfs : nullptr, ss,
                                    nullptr, L->sgu_f32 ? L->xf : nullptr, L->dpad);
         }
+    };
+    auto shared_down = [&](hipStream_t ss) {
         if (smfma_dn) {
             Launch l(L, "shared_down", ss);
             if (L->sdown_f32)
@@ -744,7 +761,14 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
             jx::launch_gemv_down(L->sdown.m, L->hqs, L->sdown_f32 ? L->hfs : nullptr, (int)fspad, sg, sslots, tbs, L->ysh,
                                  ss);
         }
-        HIPCHK(hipEventRecord(L->ev_join, ss));
+    };
+    // otherwise the shared expert runs on the side stream, concurrent with the routed gate/up
+    if (L->shared && !sh_gu) {
+        HIPCHK(hipEventRecord(L->ev_fork, st));
+        HIPCHK(hipStreamWaitEvent(L->side, L->ev_fork, 0));
+        shared_gateup(L->side);
+        shared_down(L->side);
+        HIPCHK(hipEventRecord(L->ev_join, L->side));
     }
     if (dispatch_later) {
         Launch l(L, "dispatch", st);
@@ -767,11 +791,27 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         jx::launch_gemv_gateup(L->gate.m, L->up.m, L->xq, lg, slots, tb, L->hq, L->down_f32 ? L->hf : nullptr, st,
                                &tail, gxf, L->dpad);
     } else {
-        Launch l(L, "gateup_gemv", st);
-        jx::launch_gemv_gateup(L->gate.m, L->up.m, L->xq, grp, slots, tb, L->hq, L->down_f32 ? L->hf : nullptr, st,
-                               nullptr, gxf, L->dpad);
+        jx::SharedPart spg;
+        if (sh_gu) {
+            spg.g = L->sgate.m;
+            spg.u = L->sup.m;
+            spg.grp = sg;
+            spg.slots = sslots;
+            spg.hq = L->hqs;
+            spg.hf = L->sdown_f32 ? L->hfs : nullptr;
+            spg.hf_ld = (int)fspad;
+        }
+        bool joined = false;
+        {
+            Launch l(L, sh_gu ? "gateup_gemv_shared" : "gateup_gemv", st);
+            joined = jx::launch_gemv_gateup(L->gate.m, L->up.m, L->xq, grp, slots, tb, L->hq,
+                                            L->down_f32 ? L->hf : nullptr, st, nullptr, gxf, L->dpad,
+                                            sh_gu ? &spg : nullptr);
+        }
+        if (sh_gu && !joined) shared_gateup(st);  // (the launch took another form)
     }
-    if (L->shared) HIPCHK(hipStreamWaitEvent(st, L->ev_join, 0));
+    if (L->shared && !sh_gu) HIPCHK(hipStreamWaitEvent(st, L->ev_join, 0));
+
     int ks = 1;  // parts of the down GEMM's K (the combine adds them)
     if (mfma_down) {
         {
@@ -799,15 +839,30 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
             comb.ids = L->ids;
             comb.k = k;
         }
-        Launch l(L, fold ? "down_gemv_combine" : (L->down_f32 ? "down_gemv_f32" : "down_gemv"), st);
-        jx::launch_gemv_down(L->down.m, L->hq, L->down_f32 ? L->hf : nullptr, (int)fpad, grp, slots, tb, L->y, st,
-                             comb);
+        jx::SharedPart spd;
+        if (sh_gu) {
+            spd.g = L->sdown.m;
+            spd.grp = sg;
+            spd.slots = sslots;
+            spd.hq = L->hqs;
+            spd.y = L->ysh;
+            spd.kparts = std::min(L->shparts_cap, jx::shared_down_kparts(L->down.m.type, L->F, L->Fs));
+        }
+        bool joined = false;
+        {
+            Launch l(L, fold ? "down_gemv_combine" : (L->down_f32 ? "down_gemv_f32" : sh_gu ? "down_gemv_shared" : "down_gemv"),
+                     st);
+            joined = jx::launch_gemv_down(L->down.m, L->hq, L->down_f32 ? L->hf : nullptr, (int)fpad, grp, slots, tb, L->y,
+                                          st, comb, sh_gu ? &spd : nullptr);
+        }
+        if (sh_gu && !joined) shared_down(st);  // (the launch took another form)
+        if (joined) shparts = spd.kparts;
     }
     if (!fold) {
         Launch l(L, "combine", st);
         jx::launch_combine(n, d, k, L->probs, L->pos_of, L->y, L->shared ? L->ysh : nullptr, L->shscale, outdev, st,
                            resid ? xres : nullptr, resid ? L->post_norm : nullptr, L->eps,
-                           ks > 1 ? L->y + L->ystride : nullptr);
+                           ks > 1 ? L->y + L->ystride : nullptr, shparts);
     }
     HIPCHK(hipGetLastError());
     return JX_OK;

@@ -47,6 +47,12 @@ EXTRA = {
     "qwen15_norm": synth.LayerConfig("qwen15_norm", 512, 12, 4, 384, F.Q4_0, d_ff_shared=768, shared_gate=True,
                                      norms=True),
     "mixtral_norm": synth.LayerConfig("mixtral_norm", 4096, 8, 2, 1024, F.Q4_K, norms=True),
+    # a shared expert twice a routed one where both GEMVs take the multi-tile form: its blocks join the
+    # routed gate/up and down launches (the down's K in two parts); GELU routed experts beside the SiLU
+    # shared one (Q4_0, sigmoid gate), and Q4_K without a gate
+    "gelu_sh_mx": synth.LayerConfig("gelu_sh_mx", 1024, 32, 4, 1024, F.Q4_0, d_ff_shared=2048, shared_gate=True,
+                                    act=1),
+    "q4k_sh_mx": synth.LayerConfig("q4k_sh_mx", 1024, 32, 4, 1024, F.Q4_K, d_ff_shared=2048),
 }
 
 
@@ -152,7 +158,11 @@ def test_layer_vs_golden(moe, case):
                                            ("gelu_q4k", 20, "gemv"), ("gelu_q4k", 200, "mfma"),
                                            # GELU routed experts beside a SiLU shared expert, every shared form
                                            ("toy_gelu_sh", 2, "gemv"), ("toy_gelu_sh", 40, None),
-                                           ("toy_gelu_sh", 300, "mfma")])
+                                           ("toy_gelu_sh", 300, "mfma"),
+                                           # the shared expert's blocks in the routed launches: whole and
+                                           # partial 16-token groups
+                                           ("gelu_sh_mx", 64, None), ("gelu_sh_mx", 40, None),
+                                           ("q4k_sh_mx", 48, None), ("q4k_sh_mx", 37, None)])
 def test_layer_regimes_vs_oracle(moe, port, name, n, regime):
     say(f"{name} n={n} regime={regime}")
     cfg, lw = layer(name)
