@@ -1107,7 +1107,7 @@ k_gemv_mx(QMat W0, QMat W1, ActQ8 act, Groups grp, ActQ8 hq, float* hf, int hf_l
     const int rt = blockIdx.x % W0.nrt;
     const int4 rec = group_of(grp, blockIdx.x / W0.nrt);
     const int e = rec.x, p0 = rec.y, cnt = rec.z;
-    if (cnt == 0) return;
+    if (cnt == 0 || (grp.cold_max > 0 && cnt >= grp.cold_max)) return;  // (the GEMMs take that expert)
     const int tid = threadIdx.x, lane = tid & 63, m = lane & 31, h = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar unit loop and branches
     const int kw = wave % HW;
@@ -1302,7 +1302,7 @@ k_gemv_mxt(QMat W0r, QMat W1r, ActQ8 actr, Groups grpr, ActQ8 hqr, float* hfr, i
     const int gi = bi / nch, slot = shb ? gi % sh.slots : gi, kp = shb ? gi / sh.slots : 0;
     const int4 rec = group_of(grp, slot);
     const int e = rec.x, p0 = rec.y, cnt = rec.z;
-    if (cnt == 0) return;
+    if (cnt == 0 || (grp.cold_max > 0 && cnt >= grp.cold_max)) return;  // (the GEMMs take that expert)
     const int tid = threadIdx.x, lane = tid & 63, m = lane & 31, h = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar unit loop and branches
     const int kw = wave % HW;

@@ -121,6 +121,9 @@ struct Groups {
     // instead of reading dispatch tables (small_group in jxmoe_dispatch.h).
     const float* logits = nullptr;
     int n_experts = 0;
+    // > 0: the multi-token GEMVs take only the experts with fewer pairs than this (the GEMMs take the
+    // others: launch_dispatch's cold_max)
+    int cold_max = 0;
 };
 constexpr int SMALL_GROUP_MAX_E = 128;
 constexpr int MAX_SLOTS_DEC = 16;  // routed slots (top_k) of the fused one-token step
@@ -191,7 +194,10 @@ void launch_route(const RouteArgs& a, hipStream_t st);
 // (out holds nrows * 16 * chain_stride(d) floats).
 int chain_stride(int d);
 void chain_rows(const float* rows, int nrows, int d, float* out);
-void launch_dispatch(const int* ids, int nk, int E, int top_k, const DispatchOut& o, hipStream_t st);
+// With cold_max > 0 the tile table (and n_tiles) holds only the experts with at least cold_max pairs:
+// the matrix-core GEMMs take those, the GEMVs the others (Groups::cold_max).
+void launch_dispatch(const int* ids, int nk, int E, int top_k, const DispatchOut& o, hipStream_t st,
+                     int cold_max = 0);
 
 // A dense shared expert's blocks appended to a routed multi-token GEMV launch (k_gemv_mxt): its own
 // matrices and outputs over groups of 16 tokens, so its few long-lived blocks run among the routed

@@ -963,7 +963,7 @@ __device__ __forceinline__ int4 load_ids4(const int* ids, int f, int nk) {
 }
 
 __global__ void __launch_bounds__(DISPATCH_THREADS)
-k_dispatch(const int* ids, int nk, int E, int top_k, DispatchOut o) {
+k_dispatch(const int* ids, int nk, int E, int top_k, DispatchOut o, int cold_max) {
     extern __shared__ int hist[];
     __shared__ int red[3][DISPATCH_THREADS / 64];
     __shared__ int wtot[2][DISPATCH_THREADS / 64];
@@ -1012,12 +1012,13 @@ k_dispatch(const int* ids, int nk, int E, int top_k, DispatchOut o) {
         }
     }
     __syncthreads();
-    // pair offset, tile offset and active index of expert e: sums over the experts before it
+    // pair offset, tile offset and active index of expert e: sums over the experts before it (the tile
+    // list holds the experts of at least cold_max pairs only, when cold_max > 0: the others take the GEMVs)
     int off = 0, toff = 0, na = 0;
     for (int i = tid; i < e; i += DISPATCH_THREADS) {
         const int c = hist[i];
         off += c;
-        toff += (c + MFMA_BN - 1) / MFMA_BN;
+        toff += c >= cold_max ? (c + MFMA_BN - 1) / MFMA_BN : 0;
         na += c > 0;
     }
 #pragma unroll
@@ -1040,6 +1041,7 @@ k_dispatch(const int* ids, int nk, int E, int top_k, DispatchOut o) {
         na += red[2][w];
     }
     const int cnt = hist[e];
+    const int ntl = cnt >= cold_max ? (cnt + MFMA_BN - 1) / MFMA_BN : 0;  // this expert's tiles
     if (tid == 0) {
         o.counts[e] = cnt;
         o.offs[e] = off;
@@ -1048,10 +1050,10 @@ k_dispatch(const int* ids, int nk, int E, int top_k, DispatchOut o) {
         if (e == E - 1) {
             o.offs[E] = off + cnt;
             *o.n_act = na + (cnt > 0);
-            *o.n_tiles = toff + (cnt + MFMA_BN - 1) / MFMA_BN;
+            *o.n_tiles = toff + ntl;
         }
     }
-    for (int i = tid; i * MFMA_BN < cnt; i += DISPATCH_THREADS)
+    for (int i = tid; i < ntl; i += DISPATCH_THREADS)
         o.tiles[toff + i] = make_int4(e, off + i * MFMA_BN, min(MFMA_BN, cnt - i * MFMA_BN), 0);
     if (cnt == 0) return;  // block-uniform
     const uint64_t lt_mask = (1ull << lane) - 1ull;
@@ -1102,8 +1104,9 @@ k_dispatch(const int* ids, int nk, int E, int top_k, DispatchOut o) {
     }
 }
 
-void launch_dispatch(const int* ids, int nk, int E, int top_k, const DispatchOut& o, hipStream_t st) {
-    hipLaunchKernelGGL(k_dispatch, dim3(E), dim3(DISPATCH_THREADS), (size_t)E * sizeof(int), st, ids, nk, E, top_k, o);
+void launch_dispatch(const int* ids, int nk, int E, int top_k, const DispatchOut& o, hipStream_t st, int cold_max) {
+    hipLaunchKernelGGL(k_dispatch, dim3(E), dim3(DISPATCH_THREADS), (size_t)E * sizeof(int), st, ids, nk, E, top_k, o,
+                       cold_max);
 }
 
 // sum_i x[i] * x[i] over one row in vec_dot_f32's order (src/quant.cpp:2756-2778;

@@ -322,6 +322,7 @@ struct jx_moe_layer {
     hipStream_t last_st = nullptr;   // stream of the last forward (jx_moe_layer_status waits on it)
     uint32_t dec_epoch = 0;
     int shparts_cap = 1;  // K parts of the shared down's output the workspace holds (ysh)
+    int cold_pairs = 0;   // experts under this many pairs take the GEMVs in the matrix-core regime (0: none)
     bool fused_decode = true;
     bool force_fused = false;  // JX_FUSED=1: also where the separate launches measured faster
     int smfma_min = 0;         // shared expert's GEMM threshold (JX_SMFMA_MIN overrides it: A/B)
@@ -510,6 +511,14 @@ constexpr int MFMA_MIN_PAIRS_PER_EXPERT_Q4 = 12;
 constexpr int MFMA_MIN_PAIRS_PER_EXPERT_Q4_LARGE = 16;
 constexpr int MFMA_MIN_PAIRS_PER_EXPERT_Q8 = 4;
 constexpr size_t LARGE_EXPERT_ELEMS = (size_t)1 << 25;  // d * d_ff per matrix
+// The cold experts' GEMVs beside the GEMMs: layers of at least HYBRID_MIN_E experts, experts under
+// COLD_PAIRS pairs (JX_COLD_PAIRS overrides it, 0 turns the split off: A/B measurement).  Measured on
+// the Qwen3-shaped 2048-token step with Zipf routing (61 / 76 / 86 / 93 experts under 16 / 32 / 48 / 64
+// pairs): 624 us without the split, 600 / 609 / 621 / 637 us with these thresholds.  The GEMMs are
+// matrix-core bound on the head experts (the largest holds 1902 pairs), and the GEMV blocks share the
+// CUs with them.
+constexpr int HYBRID_MIN_E = 32;
+constexpr int COLD_PAIRS = 16;
 
 // Whether a call takes the fused one-token launch (k_decode1), apart from stream capture: one token in
 // the GEMV regime, Q8_0 activations on both sides, a shared expert (if any) in the routed formats, a
@@ -770,9 +779,31 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         shared_down(L->side);
         HIPCHK(hipEventRecord(L->ev_join, L->side));
     }
+    // Skewed routing over many experts in the matrix-core regime: the experts with fewer than COLD_PAIRS
+    // pairs take the multi-token GEMVs (weights streamed once per 16 tokens) on the side stream, beside
+    // the GEMMs over the others, instead of a mostly empty GEMM tile each.  The dispatch keeps them out of
+    // the tile table; the GEMV blocks of the others exit at once.
+    const bool hybrid = mfma && mfma_gu && mfma_down && !L->shared && dispatch_later && E >= HYBRID_MIN_E &&
+                        !L->gu_f32 && !L->down_f32 && !(flags & JX_FWD_FORCE_MFMA) &&
+                        jx::mfma_down_ksplit(L->hh.a.K) == 1 && L->cold_pairs > 0;
     if (dispatch_later) {
         Launch l(L, "dispatch", st);
-        jx::launch_dispatch(L->ids, nk, E, k, dout, st);
+        jx::launch_dispatch(L->ids, nk, E, k, dout, st, hybrid ? L->cold_pairs : 0);
+    }
+    if (hybrid) {
+        HIPCHK(hipEventRecord(L->ev_fork, st));
+        HIPCHK(hipStreamWaitEvent(L->side, L->ev_fork, 0));
+        jx::Groups cg = grp;
+        cg.cold_max = L->cold_pairs;
+        {
+            Launch l(L, "gateup_gemv_cold", L->side);
+            jx::launch_gemv_gateup(L->gate.m, L->up.m, L->xq, cg, slots, 16, L->hq, nullptr, L->side);
+        }
+        {
+            Launch l(L, "down_gemv_cold", L->side);
+            jx::launch_gemv_down(L->down.m, L->hq, nullptr, 0, cg, slots, 16, L->y, L->side);
+        }
+        HIPCHK(hipEventRecord(L->ev_join, L->side));
     }
     const float* gxf = L->gu_f32 ? L->xf : nullptr;
     if (mfma_gu) {
@@ -858,6 +889,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         if (sh_gu && !joined) shared_down(st);  // (the launch took another form)
         if (joined) shparts = spd.kparts;
     }
+    if (hybrid) HIPCHK(hipStreamWaitEvent(st, L->ev_join, 0));
     if (!fold) {
         Launch l(L, "combine", st);
         jx::launch_combine(n, d, k, L->probs, L->pos_of, L->y, L->shared ? L->ysh : nullptr, L->shscale, outdev, st,
@@ -1055,7 +1087,8 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
     }
     if ((r = ensure_workspace(L, 1)) != JX_OK) return bail(r);
     if (hipStreamCreate(&L->own) != hipSuccess) return bail(fail(JX_ERR_HIP, "stream create"));
-    if (L->shared && (hipStreamCreate(&L->side) != hipSuccess ||
+    // the side stream: the shared expert, or the cold experts' GEMVs beside the GEMMs
+    if ((hipStreamCreate(&L->side) != hipSuccess ||
                       hipEventCreateWithFlags(&L->ev_fork, hipEventDisableTiming) != hipSuccess ||
                       hipEventCreateWithFlags(&L->ev_join, hipEventDisableTiming) != hipSuccess))
         return bail(fail(JX_ERR_HIP, "shared-expert stream create"));
@@ -1071,6 +1104,8 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
     if (const char* f = std::getenv("JX_NO_FUSED")) L->fused_decode = std::strcmp(f, "0") == 0;
     if (const char* f = std::getenv("JX_FUSED")) L->force_fused = std::strcmp(f, "0") != 0;
     if (const char* f = std::getenv("JX_DECP")) L->decp_mode = std::strcmp(f, "0") != 0 ? 1 : 0;
+    L->cold_pairs = COLD_PAIRS;
+    if (const char* f = std::getenv("JX_COLD_PAIRS")) L->cold_pairs = std::max(0, std::atoi(f));
     L->smfma_min = (L->shared && (L->sgate.m.type == jx::T_Q4_K || L->sgate.m.type == jx::T_Q6_K))
                        ? jx::MFMA_MIN_SHARED_TOKENS_KQ
                        : jx::MFMA_MIN_SHARED_TOKENS;

@@ -162,7 +162,10 @@ def test_layer_vs_golden(moe, case):
                                            # the shared expert's blocks in the routed launches: whole and
                                            # partial 16-token groups
                                            ("gelu_sh_mx", 64, None), ("gelu_sh_mx", 40, None),
-                                           ("q4k_sh_mx", 48, None), ("q4k_sh_mx", 37, None)])
+                                           ("q4k_sh_mx", 48, None), ("q4k_sh_mx", 37, None),
+                                           # Zipf routing over 128 experts in the matrix-core regime: the
+                                           # experts under 32 pairs on the GEMVs beside the GEMMs
+                                           ("qwen3moe", 1024, None), ("qwen3moe", 2048, None)])
 def test_layer_regimes_vs_oracle(moe, port, name, n, regime):
     say(f"{name} n={n} regime={regime}")
     cfg, lw = layer(name)
@@ -179,6 +182,28 @@ def test_layer_regimes_vs_oracle(moe, port, name, n, regime):
     say(f"{name} n={n} regime={regime}: max rel err {err:.2e}")
     assert err <= REL_TOL
     L.close()
+
+
+@pytest.mark.parametrize("cold", ["0", "100000"])
+def test_cold_experts_split(moe, port, monkeypatch, cold):
+    """The matrix-core regime's split of the experts between the GEMMs and the GEMVs (JX_COLD_PAIRS, read
+    at layer creation): with no expert on the GEMVs and with every one of them there (an empty GEMM tile
+    table), routing exact and outputs within the bar."""
+    say(f"qwen3moe 1024 tokens, JX_COLD_PAIRS={cold}")
+    cfg, lw = layer("qwen3moe")
+    x = synth.make_tokens(cfg, 1024, seed=17)
+    monkeypatch.setenv("JX_COLD_PAIRS", cold)
+    L = moe.MoELayer.from_weights(lw)
+    out, ids, w, counts = L.forward(x)
+    L.close()
+    lg_o, ids_o, w_o = port.route(lw, x)
+    assert np.array_equal(ids, ids_o)
+    assert (counts < 32).any() and (counts >= 32).any()  # both kinds of expert at this size
+    sel = np.unique(np.linspace(0, 1023, 8).astype(np.int32))
+    want = port.moe_forward(lw, x, sel)[0]
+    err = rel_err(out[sel], want)
+    say(f"qwen3moe 1024 JX_COLD_PAIRS={cold}: max rel err {err:.2e}")
+    assert err <= REL_TOL
 
 
 @pytest.mark.parametrize("name", ["mixtral", "qwen3moe", "qwen15moe", "dsv2lite"])
