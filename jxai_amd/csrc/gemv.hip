@@ -1961,7 +1961,11 @@ __device__ void dec_wait_logits(const Decode1Args& a, int n, float* lg) {
 
 constexpr uint32_t DEC_HTAG_MASK = 0x1FFFu;  // low mantissa bits of h's stored scale
 
-template <int TG, int TD>
+// TSD: the shared down's format; DF32: the routed down takes fp32 h (no Q8_0 form at d_ff: its gate/up
+// blocks publish h as tagged 64-bit words (epoch << 32 | fp32 bits), and its down blocks read them
+// until every word carries this launch's number, as k_gemv_gateup / k_gemv_down<..., true> hand fp32 h
+// over in the separate launches).
+template <int TG, int TD, int TSD, bool DF32>
 __global__ void __launch_bounds__(DEC_THREADS) __attribute__((amdgpu_waves_per_eu(GEMV_WAVES_PER_SIMD(1))))
 k_decode1(Decode1Args a) {
     extern __shared__ __align__(16) int8_t smem[];
@@ -1984,7 +1988,8 @@ k_decode1(Decode1Args a) {
     // One gate/up row tile per half (waves 0-3, 4-7): expert e's rows 32 rt.. of Wg / Wu against the
     // Q8_0 of x in LDS; SwiGLU and h's Q8_0 block into row p0 of hout, device-coherently, the tagged
     // scale last.  An inactive half loads the pad and stores nothing (both halves meet every barrier).
-    auto gateup_tile = [&](const QMat& Wg, const QMat& Wu, int e, int rt, int p0, const ActQ8& hout, bool active) {
+    auto gateup_tile = [&](const QMat& Wg, const QMat& Wu, int e, int rt, int p0, const ActQ8& hout, bool active,
+                           uint64_t* hfw) {
         const int half = wave >> 2, lw = wave & 3, mat = lw >> 1, kw = lw & 1;
         const ActLds A{smem, reinterpret_cast<const float2*>(smem + d), nullptr, d};
         const QMat& W = mat ? Wu : Wg;
@@ -2005,6 +2010,13 @@ k_decode1(Decode1Args a) {
                 gv += red[4 * half + w][m];
                 uv += red[4 * half + 2 + w][m];
             }
+            if (DF32 && hfw) {  // fp32 h as tagged words, row p0 of d_ff values
+                if (h == 0)
+                    __hip_atomic_store(hfw + (size_t)p0 * hout.K + rt * 32 + m,
+                                       ((uint64_t)a.epoch << 32) | __float_as_uint(gated(gv, uv, Wg.act)), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                return;
+            }
             float2 sv;
             const int q = q8_block_vals(gated(gv, uv, Wg.act), sv);
             const uint32_t q1 = (uint32_t)__shfl_down(q, 1, 64), q2 = (uint32_t)__shfl_down(q, 2, 64),
@@ -2021,14 +2033,33 @@ k_decode1(Decode1Args a) {
         }
     };
 
+    // A down tile's lanes' partial sums: the 8 waves' sums in wave order, into y_out[row] or p * s added
+    // into the output (folded combine)
+    auto down_out = [&](const QMat& Wd, int rt, float* y_out, float p, float acc) {
+        acc += __shfl_xor(acc, 32, 64);
+        if (h == 0) red[wave][m] = acc;
+        __syncthreads();
+        if (wave == 0 && h == 0) {
+            float s = 0.0f;
+#pragma unroll
+            for (int w = 0; w < DEC_THREADS / 64; ++w) s += red[w][m];
+            const int row = rt * 32 + m;
+            if (!(Wd.valid_rows && row >= Wd.valid_rows)) {
+                if (y_out) y_out[row] = s;
+                else atomicAdd(a.out + row, p * s);
+            }
+        }
+    };
+
     // Down row tile rt of expert e of Wd against row p0 of hin (once every scale word of that row
     // carries this launch's tag): y_out[row] = s, or p * s added into the output (folded combine).
-    auto down_tile = [&](const QMat& Wd, int e, int rt, int p0, const ActQ8& hin, float* y_out, float p) {
+    auto down_tile = [&](auto tdc, const QMat& Wd, int e, int rt, int p0, const ActQ8& hin, float* y_out, float p) {
+        constexpr int T = decltype(tdc)::value;
         const int K = hin.K, KB = K / 32;
         const ActLds A{smem, reinterpret_cast<const float2*>(smem + K), nullptr, K};
-        const int nu = n_units<TD>(Wd.nkb);
+        const int nu = n_units<T>(Wd.nkb);
         float acc[1] = {0.0f};
-        kloop<TD, 1>(
+        kloop<T, 1>(
             Wd, Wd, e, rt, wave, nu, DEC_THREADS / 64, m, h,
             [&] {  // after the first two units' loads: wait for the tags, then stage h
                 const uint64_t* ss = reinterpret_cast<const uint64_t*>(hin.s + (size_t)p0 * KB);
@@ -2059,22 +2090,46 @@ k_decode1(Decode1Args a) {
                 if (tid < KB) reinterpret_cast<uint64_t*>(smem + K)[tid] = sv & ~(uint64_t)DEC_HTAG_MASK;
                 __syncthreads();
             },
-            [&](const typename Fmt<TD>::Raw& c, const typename Fmt<TD>::Raw&, int u) {
-                unit_accum<TD, 1>(c, A, u, h, 1, Wd.nkb, acc);
+            [&](const typename Fmt<T>::Raw& c, const typename Fmt<T>::Raw&, int u) {
+                unit_accum<T, 1>(c, A, u, h, 1, Wd.nkb, acc);
             });
-        acc[0] += __shfl_xor(acc[0], 32, 64);
-        if (h == 0) red[wave][m] = acc[0];
-        __syncthreads();
-        if (wave == 0 && h == 0) {
-            float s = 0.0f;
-#pragma unroll
-            for (int w = 0; w < DEC_THREADS / 64; ++w) s += red[w][m];
-            const int row = rt * 32 + m;
-            if (!(Wd.valid_rows && row >= Wd.valid_rows)) {
-                if (y_out) y_out[row] = s;
-                else atomicAdd(a.out + row, p * s);
-            }
-        }
+        down_out(Wd, rt, y_out, p, acc[0]);
+    };
+
+    // The same over fp32 h: row p0's tagged words, staged in LDS as floats zero-padded to a.hf_ld (whole
+    // K-units), against the fp32-activation dots of k_gemv_down<..., true>.
+    auto down_tile_f32 = [&](const QMat& Wd, int e, int rt, int p0, float* y_out, float p) {
+        const int F = a.hq.K, KP = a.hf_ld;
+        float* hl = reinterpret_cast<float*>(smem);
+        const ActLds A{nullptr, nullptr, hl, KP};
+        const int nu = n_units<TD>(Wd.nkb);
+        float acc[1] = {0.0f};
+        kloop<TD, 1>(
+            Wd, Wd, e, rt, wave, nu, DEC_THREADS / 64, m, h,
+            [&] {  // after the first two units' loads: every word of the row, once it carries the launch number
+                const uint64_t* hw = a.hfw + (size_t)p0 * F;
+                for (int it = 0;; ++it) {
+                    bool ok = true;
+                    for (int i = tid; i < F; i += DEC_THREADS) {
+                        const uint64_t w = __hip_atomic_load(hw + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        const bool t = (uint32_t)(w >> 32) == a.epoch;
+                        if (t) hl[i] = __uint_as_float((uint32_t)w);
+                        ok = ok && t;
+                    }
+                    if (__syncthreads_and(ok && !a.giveup_test)) break;  // block-uniform
+                    if (it >= (int)a.spin_limit) {
+                        if (tid == 0) dec_fail(a);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                for (int i = F + tid; i < KP; i += DEC_THREADS) hl[i] = 0.0f;
+                __syncthreads();
+            },
+            [&](const typename Fmt<TD>::Raw& c, const typename Fmt<TD>::Raw&, int u) {
+                unit_accum_f32<TD, 1>(c, A, u, h, 1, Wd.nkb, acc);
+            });
+        down_out(Wd, rt, y_out, p, acc[0]);
     };
 
     // Q8_0 of x into LDS (the gate/up blocks' activations), one 32-block per half-wave and step, as
@@ -2167,7 +2222,7 @@ k_decode1(Decode1Args a) {
         const int rt = 2 * (blk - b_sg) + (wave >> 2);
         quantize_x();
         __syncthreads();
-        gateup_tile(a.SG, a.SU, 0, rt < a.SG.nrt ? rt : 0, 0, a.hqs, rt < a.SG.nrt);
+        gateup_tile(a.SG, a.SU, 0, rt < a.SG.nrt ? rt : 0, 0, a.hqs, rt < a.SG.nrt, nullptr);
         return;
     }
 
@@ -2177,7 +2232,7 @@ k_decode1(Decode1Args a) {
         if (wave == 0) dec_wait_logits(a, E, lg);
         __syncthreads();  // the logits and the Q8_0 of x
         const int4 rec = small_group(grp, 2 * sp + (wave >> 2));
-        gateup_tile(a.G, a.U, rec.x, rt, rec.y, a.hq, true);
+        gateup_tile(a.G, a.U, rec.x, rt, rec.y, a.hq, true, DF32 ? a.hfw : nullptr);
         return;
     }
 
@@ -2201,19 +2256,29 @@ k_decode1(Decode1Args a) {
                 if (id == rec.x) p = pq;
             }
         }
-        down_tile(a.D, rec.x, rt, rec.y, a.hq, a.out ? nullptr : a.y + (size_t)rec.y * a.D.rows, p);
+        float* const yo = a.out ? nullptr : a.y + (size_t)rec.y * a.D.rows;
+        if constexpr (DF32)
+            down_tile_f32(a.D, rec.x, rt, rec.y, yo, p);
+        else
+            down_tile(std::integral_constant<int, TD>{}, a.D, rec.x, rt, rec.y, a.hq, yo, p);
         return;
     }
 
     // ---- shared down: row tile rt
-    down_tile(a.SD, 0, blk - b_sd, 0, a.hqs, a.ysh, 0.0f);
+    down_tile(std::integral_constant<int, TSD>{}, a.SD, 0, blk - b_sd, 0, a.hqs, a.ysh, 0.0f);
 }
 
 static bool fmt_q8(int t) { return t == T_Q4_0 || t == T_Q8_0 || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
 
-bool decode1_fits(int gtype, int dtype, int d, int f, int E, int k, int fs, bool shgate) {
-    // built: one format on both sides, or a K-quant gate/up with a Q6_K down (the _M mixes)
-    const bool built = fmt_q8(gtype) && (gtype == dtype || ((gtype == T_Q4_K || gtype == T_Q5_K) && dtype == T_Q6_K));
+bool decode1_fits(int gtype, int dtype, int d, int f, int E, int k, int fs, bool shgate, int sdtype, bool df32) {
+    // built: one format on both sides, or a K-quant gate/up with a Q6_K down (the _M mixes); with fp32 h at
+    // d_ff, a Q4_K gate/up with a Q4_K or Q5_0 down and a shared down of Q4_K or Q6_K (DeepSeek-V2-Lite-shaped
+    // Q4_K and Q4_K_M)
+    const bool q8 = !df32 && fmt_q8(gtype) && (gtype == dtype || ((gtype == T_Q4_K || gtype == T_Q5_K) && dtype == T_Q6_K)) &&
+                    (fs == 0 || sdtype == dtype);
+    const bool hf = df32 && gtype == T_Q4_K &&
+                    ((dtype == T_Q4_K && (fs == 0 || sdtype == T_Q4_K)) || (dtype == T_Q5_0 && (fs == 0 || sdtype == T_Q6_K)));
+    const bool built = q8 || hf;
     return built && E >= 1 && E + (shgate ? 1 : 0) <= SMALL_GROUP_MAX_E && k >= 2 && k % 2 == 0 && k <= MAX_SLOTS_DEC && k <= E &&
            d % 32 == 0 && d <= 8192 && f % 32 == 0 && f <= 16384 && fs % 32 == 0 && fs <= 16384;
 }
@@ -2228,25 +2293,29 @@ bool decode1_pays(int gate_nrt, int k, int sgate_nrt) {
     return gate_nrt * (k / 2) + (sgate_nrt + 1) / 2 <= num_cus();
 }
 
-void launch_decode1(const Decode1Args& a, int gtype, int dtype, hipStream_t st) {
+void launch_decode1(const Decode1Args& a, int gtype, int dtype, hipStream_t st, int sdtype, bool df32) {
     const dim3 grid(a.E + (a.shgate ? 1 : 0) + 1 + (a.sh ? (a.SG.nrt + 1) / 2 + a.SD.nrt : 0) +
                     a.G.nrt * (a.k / 2) + a.D.nrt * a.k);
-    // LDS: router row + token chain-major, or a gate/up's Q8_0 of x, or a down's Q8_0 of h
+    // LDS: router row + token chain-major, or a gate/up's Q8_0 of x, or a down's Q8_0 (or fp32) h
     const size_t lds = std::max({(size_t)2 * 16 * rs_stride(a.d) * sizeof(float), act_lds_bytes(1, a.d, false),
-                                 act_lds_bytes(1, a.hq.K, false), act_lds_bytes(1, a.sh ? a.hqs.K : 0, false)});
+                                 act_lds_bytes(1, a.hq.K, false), act_lds_bytes(1, a.sh ? a.hqs.K : 0, false),
+                                 df32 ? (size_t)a.hf_ld * sizeof(float) : (size_t)0});
     auto go = [&](auto kern) {
         lds_optin(kern, lds);
         hipLaunchKernelGGL(kern, grid, dim3(DEC_THREADS), lds, st, a);
     };
-#define JX_DEC1(G, D) \
-    if (gtype == G && dtype == D) return go(k_decode1<G, D>);
-    JX_DEC1(T_Q4_0, T_Q4_0)
-    JX_DEC1(T_Q8_0, T_Q8_0)
-    JX_DEC1(T_Q4_K, T_Q4_K)
-    JX_DEC1(T_Q5_K, T_Q5_K)
-    JX_DEC1(T_Q6_K, T_Q6_K)
-    JX_DEC1(T_Q4_K, T_Q6_K)
-    JX_DEC1(T_Q5_K, T_Q6_K)
+    if (!a.sh) sdtype = dtype == T_Q5_0 ? T_Q6_K : dtype;  // no shared blocks: any built instance
+#define JX_DEC1(G, D, SD, F32) \
+    if (gtype == G && dtype == D && sdtype == SD && df32 == F32) return go(k_decode1<G, D, SD, F32>);
+    JX_DEC1(T_Q4_0, T_Q4_0, T_Q4_0, false)
+    JX_DEC1(T_Q8_0, T_Q8_0, T_Q8_0, false)
+    JX_DEC1(T_Q4_K, T_Q4_K, T_Q4_K, false)
+    JX_DEC1(T_Q5_K, T_Q5_K, T_Q5_K, false)
+    JX_DEC1(T_Q6_K, T_Q6_K, T_Q6_K, false)
+    JX_DEC1(T_Q4_K, T_Q6_K, T_Q6_K, false)
+    JX_DEC1(T_Q5_K, T_Q6_K, T_Q6_K, false)
+    JX_DEC1(T_Q4_K, T_Q4_K, T_Q4_K, true)
+    JX_DEC1(T_Q4_K, T_Q5_0, T_Q6_K, true)
 #undef JX_DEC1
 }
 
@@ -2579,7 +2648,7 @@ k_decode_p(Decode1Args a) {
 bool decodep_fits(int gtype, int dtype, int d, int f, int E, int k, bool shared, bool fold, int gate_nrt,
                   int down_nrt) {
     const int nb = num_cus();
-    if (shared || !fold || k != 2 || !decode1_fits(gtype, dtype, d, f, E, k, 0, false) || E > nb ||
+    if (shared || !fold || k != 2 || !decode1_fits(gtype, dtype, d, f, E, k, 0, false, dtype, false) || E > nb ||
         decodep_lds(d, f, E) > DP_LDS_MAX || down_nrt * k > 2 * nb)
         return false;
     // gate/up: at most DP_GROUPS tiles per block; a block zeroing output rows (its down tile of slot 0)

@@ -333,6 +333,8 @@ struct Decode1Args {
     ActQ8 hqs;                  //   [1][d_ff_shared] Q8_0 of its h
     float* ysh = nullptr;       //   [d] its output, for launch_combine
     uint64_t* hw = nullptr;     // k_decode_p: [k][d_ff / 4] words of h, (epoch << 32) | four Q8_0 quants
+    uint64_t* hfw = nullptr;    // k_decode1 with fp32 h: [k][d_ff] words, (epoch << 32) | fp32 h
+    int hf_ld = 0;              //   h's zero-padded length for the down (whole K-units)
     uint32_t* herr = nullptr;   // host-visible word set (system scope) when a bounded wait gives up
     uint32_t spin_limit = 0;    // polls before a wait gives up
     uint32_t giveup_test = 0;   // nonzero: every wait treats its words as not yet published (error-path test)
@@ -341,11 +343,13 @@ struct Decode1Args {
 // SMALL_GROUP_MAX_E, even k <= MAX_SLOTS_DEC, d % 32 == 0 and d <= 8192, d_ff and the shared d_ff
 // (fs, 0: none) <= 16384, gate/up and down formats with Q8_0 activations (a shared expert: the same
 // formats as the routed ones).
-bool decode1_fits(int gtype, int dtype, int d, int f, int E, int k, int fs, bool shgate);
+// With df32 the routed down takes fp32 h (its d_ff has no Q8_0 form for the down's format); sdtype is the
+// shared down's format.
+bool decode1_fits(int gtype, int dtype, int d, int f, int E, int k, int fs, bool shgate, int sdtype, bool df32);
 // Whether the fused launch is the faster one for routed gate/up matrices of gate_nrt row tiles at
 // top-k and a shared gate/up of sgate_nrt (0: none).
 bool decode1_pays(int gate_nrt, int k, int sgate_nrt);
-void launch_decode1(const Decode1Args& a, int gtype, int dtype, hipStream_t st);
+void launch_decode1(const Decode1Args& a, int gtype, int dtype, hipStream_t st, int sdtype, bool df32);
 // The same step as one grid of one 1024-thread block per CU (k_decode_p): every block routes the
 // token itself, streams an even share of the gate/up row tiles, then its down tiles once h's tagged
 // scale words say the slot is complete; top-2 with the folded combine and no shared expert, for

@@ -313,6 +313,7 @@ struct jx_moe_layer {
     // of such launches so far (JX_NO_FUSED=1 keeps the separate launches: A/B measurement)
     jx::DecodeSync* dsync = nullptr;
     uint64_t* hw = nullptr;  // k_decode_p's h: [k][d_ff / 4] words of (launch number << 32 | four quants)
+    uint64_t* hfw = nullptr;  // k_decode1's fp32 h (fp32-activation downs): [k][d_ff] tagged words
     // pinned host word the fused launches set when a bounded wait between their blocks gives up (their
     // outputs are then invalid); read on the synchronous path, by jx_moe_layer_status and at the entry
     // of every forward, so asynchronous callers learn of it too
@@ -445,7 +446,7 @@ void free_layer(jx_moe_layer* L) {
     void* ptrs[] = {L->router, L->router_cm, L->bias, L->shgate, L->ffn_norm, L->post_norm, L->xn, L->x, L->out, L->probs, L->shscale, L->logits, L->ids,
                     L->counts, L->offs, L->act, L->n_act, L->pair_tok, L->pos_of, L->n_tiles, L->tiles,
                     L->slots, L->xq.q, L->xq.s, L->hq.q, L->hq.s, L->hqs.q, L->hqs.s, L->hf, L->hfs, L->y, L->ysh,
-                    L->xf, L->dsync, L->hw};
+                    L->xf, L->dsync, L->hw, L->hfw};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     if (L->herr) (void)hipHostFree(L->herr);
@@ -527,7 +528,8 @@ constexpr int COLD_PAIRS = 16;
 // expert, a shape it is built for, and gate/up tiles too many for k_decode1's one block per CU
 // (decode1_pays false; measured Mixtral-shaped: see DESIGN.md), unless JX_DECP says otherwise.
 static bool decodep_ok(const jx_moe_layer* L, uint32_t flags) {
-    if (L->decp_mode == 0 || L->shared || L->k != 2 || (flags & JX_FWD_RESIDUAL) || !L->fold_combine) return false;
+    if (L->decp_mode == 0 || L->shared || L->k != 2 || (flags & JX_FWD_RESIDUAL) || !L->fold_combine || L->down_f32)
+        return false;  // (k_decode_p hands h over in its Q8_0 form only)
     if (!jx::decodep_fits(L->gate.m.type, L->down.m.type, L->d, L->F, L->E, L->k, false, true, L->gate.m.nrt,
                           L->down.m.nrt))
         return false;
@@ -536,13 +538,13 @@ static bool decodep_ok(const jx_moe_layer* L, uint32_t flags) {
 
 bool decode1_wanted(const jx_moe_layer* L, int n, uint32_t flags) {
     if (n != 1 || !L->fused_decode || (flags & (JX_FWD_UNFUSED | JX_FWD_FORCE_MFMA))) return false;
-    if (L->gu_f32 || L->down_f32 || L->up.m.type != L->gate.m.type) return false;
+    if (L->gu_f32 || L->up.m.type != L->gate.m.type || (L->down_f32 && !L->hfw)) return false;
     if (L->shared && (L->sgu_f32 || L->sdown_f32 || L->sgate.m.type != L->gate.m.type ||
-                      L->sup.m.type != L->gate.m.type || L->sdown.m.type != L->down.m.type))
+                      L->sup.m.type != L->gate.m.type))
         return false;
     if (L->E > jx::SMALL_GROUP_MAX_E || !jx::route_small_fits(1, L->d, L->E)) return false;
     if (!jx::decode1_fits(L->gate.m.type, L->down.m.type, L->d, L->F, L->E, L->k, L->shared ? L->Fs : 0,
-                          L->shgate != nullptr))
+                          L->shgate != nullptr, L->shared ? L->sdown.m.type : L->down.m.type, L->down_f32))
         return false;
     if (decodep_ok(L, flags)) return true;
     return L->force_fused || jx::decode1_pays(L->gate.m.nrt, L->k, L->shared ? L->sgate.m.nrt : 0);
@@ -622,6 +624,7 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         if (++L->dec_epoch == 0) {  // 2^32 launches: start the counts over
             HIPCHK(hipMemsetAsync(L->dsync, 0, sizeof(jx::DecodeSync), st));
             HIPCHK(hipMemsetAsync(L->hw, 0, (size_t)L->k * L->F / 4 * sizeof(uint64_t), st));
+            if (L->hfw) HIPCHK(hipMemsetAsync(L->hfw, 0, (size_t)L->k * L->F * sizeof(uint64_t), st));
             L->dec_epoch = 1;
         }
         jx::Decode1Args a;
@@ -647,6 +650,8 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
         a.epoch = L->dec_epoch;
         a.htag = 1u + L->dec_epoch % 8191u;  // never 0, the low bits of every untagged scale
         a.herr = L->herr_dev;
+        a.hfw = L->hfw;
+        a.hf_ld = (int)(((size_t)L->F + 255) / 256 * 256);
         a.giveup_test = (flags & JX_FWD_TEST_GIVEUP) ? 1u : 0u;
         a.spin_limit = a.giveup_test ? 64u : L->spin_limit;
         if (L->shared) {
@@ -672,7 +677,8 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
                 return fail(JX_ERR_HIP, "fused one-token step: launch failed");
         } else {
             Launch l(L, fold ? "decode_fused" : "decode_fused_y", st);
-            jx::launch_decode1(a, L->gate.m.type, L->down.m.type, st);
+            jx::launch_decode1(a, L->gate.m.type, L->down.m.type, st, L->shared ? L->sdown.m.type : L->down.m.type,
+                               L->down_f32);
         }
         if (!fold) {
             Launch l(L, "combine", st);
@@ -1112,6 +1118,11 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
     if (const char* f = std::getenv("JX_SMFMA_MIN")) L->smfma_min = std::max(1, std::atoi(f));
     if ((r = dalloc(L->dsync, 1)) != JX_OK) return bail(r);
     if ((r = dalloc(L->hw, (size_t)L->k * L->F / 4)) != JX_OK) return bail(r);
+    if (L->down_f32) {
+        if ((r = dalloc(L->hfw, (size_t)L->k * L->F)) != JX_OK) return bail(r);
+        if (hipMemset(L->hfw, 0, (size_t)L->k * L->F * sizeof(uint64_t)) != hipSuccess)
+            return bail(fail(JX_ERR_HIP, "decode state"));
+    }
     if (hipMemset(L->hw, 0, (size_t)L->k * L->F / 4 * sizeof(uint64_t)) != hipSuccess)
         return bail(fail(JX_ERR_HIP, "decode state"));
     if (hipMemset(L->dsync, 0, sizeof(jx::DecodeSync)) != hipSuccess) return bail(fail(JX_ERR_HIP, "decode state"));

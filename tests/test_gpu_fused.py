@@ -32,10 +32,16 @@ EXTRA = {
     # a shared expert without a gate (weight 1) and of an odd row-tile count (17: one shared gate/up
     # block runs a single tile)
     "toy_sh_nogate": synth.LayerConfig("toy_sh_nogate", 512, 8, 2, 1024, F.Q8_0, d_ff_shared=544),
+    # fp32 h at d_ff = 1408 (no Q8_0 form for a K-quant or Q5_0 down): h as tagged fp32 words, the folded
+    # combine (top-2, no shared expert)
+    "toy_f32dn_q4k": synth.LayerConfig("toy_f32dn_q4k", 512, 8, 2, 1408, F.Q4_K),
+    "toy_f32dn_q50": synth.LayerConfig("toy_f32dn_q50", 512, 8, 2, 1408, F.Q4_K, down_wtype=F.Q5_0),
 }
 
 FUSED = ["toy", "toy_gelu", "toy_gelu_sh", "toy_f16r", "toy_q5k", "toy_q6k", "toy_k4", "qwen3moe", "gelu_q4k", "qwen15_norm",
-         "toy_sh_nogate", "toy_bf16r_sh", "qwen15moe", "mixtral_norm", "mixtral", "mixtral_q6k"]
+         "toy_sh_nogate", "toy_bf16r_sh", "qwen15moe", "mixtral_norm", "mixtral", "mixtral_q6k",
+         # fp32-activation routed downs, with shared experts of the routed or another down format
+         "toy_f32dn_q4k", "toy_f32dn_q50", "dsv2lite", "dsv2lite_q50"]
 
 
 @pytest.fixture(scope="module")
@@ -110,7 +116,7 @@ def test_fused_step_matches_separate_launches(moe, port, name):
     L.close()
 
 
-@pytest.mark.parametrize("name", ["toy", "qwen15moe", "mixtral"])
+@pytest.mark.parametrize("name", ["toy", "qwen15moe", "mixtral", "dsv2lite_q50"])
 def test_fused_steps_back_to_back(moe, name):
     """Hundreds of fused launches queued without host synchronization (the launch count, and with
     it the tags of the logits and of h's scales, advances every step), then the last outputs against
@@ -181,7 +187,7 @@ def test_fused_cu_step_matches_separate_launches(moe, port, monkeypatch, name):
 
 
 # ------------------------------------------------------------------ a wait that gives up is reported
-@pytest.mark.parametrize("name,cu", [("toy", False), ("qwen15moe", False), ("cu_q4k", True)])
+@pytest.mark.parametrize("name,cu", [("toy", False), ("qwen15moe", False), ("cu_q4k", True), ("dsv2lite_q50", False)])
 def test_fused_giveup_is_reported(moe, monkeypatch, name, cu):
     """JX_FWD_TEST_GIVEUP makes every wait of the fused launch give up after a few polls (the kernels
     end normally; the outputs are invalid).  The failure must reach the caller on every path: the
