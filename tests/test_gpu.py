@@ -53,6 +53,7 @@ EXTRA = {
     "gelu_sh_mx": synth.LayerConfig("gelu_sh_mx", 1024, 32, 4, 1024, F.Q4_0, d_ff_shared=2048, shared_gate=True,
                                     act=1),
     "q4k_sh_mx": synth.LayerConfig("q4k_sh_mx", 1024, 32, 4, 1024, F.Q4_K, d_ff_shared=2048),
+    "q4k_sh_mx_norm": synth.LayerConfig("q4k_sh_mx_norm", 1024, 32, 4, 1024, F.Q4_K, d_ff_shared=2048, norms=True),
 }
 
 
@@ -366,7 +367,7 @@ def test_decode_two_tokens_same_experts(moe, port, name):
     L.close()
 
 
-@pytest.mark.parametrize("name", ["dsv2lite", "toy"])
+@pytest.mark.parametrize("name", ["dsv2lite", "toy", "gelu_sh_mx"])
 def test_graph_replays_match_eager(moe, monkeypatch, name):
     """Captured-graph replays, interleaved with eager launches and syncs, equal the eager result bit for bit
     (layers with a shared expert replay graphs by default; the toy layer is forced to)."""
@@ -588,7 +589,10 @@ def test_gguf_toy_layer_on_gpu(moe, tmp_path):
                                            ("toy_norm", 300, "mfma"), ("qwen15_norm", 1, None),
                                            ("qwen15_norm", 70, None), ("qwen15_norm", 700, None),
                                            ("mixtral_norm", 1, None), ("mixtral_norm", 2, None),
-                                           ("mixtral_norm", 200, "mfma")])
+                                           ("mixtral_norm", 200, "mfma"),
+                                           # the shared expert's blocks in the routed launches, its down's
+                                           # K parts added before post_ffw_norm
+                                           ("q4k_sh_mx_norm", 48, None)])
 def test_residual_form_vs_oracle(moe, port, name, n, regime):
     """JX_FWD_RESIDUAL: rms_norm(x, ffn_norm) feeds the router (routing exact), the combine applies
     post_ffw_norm and adds x, against the oracle's forward_token FFN step."""
