@@ -1064,17 +1064,19 @@ struct Mx<T_Q4_0> {
             c.d[i] = *reinterpret_cast<const uint16_t*>(v ? sb + ((b0 + i) * 32 + m) * 2 : W.pad_sc + m * 2);
         }
     }
-    // nibble n (bytes of 0..15) -> n - 8 per byte: bit 7 set before subtracting 8 stops the borrows
-    // (0x80 + n - 8 >= 0x78), and clearing it again gives (n - 8) mod 256
-    __device__ static uint32_t s8(uint32_t n) { return ((n ^ 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
+    // nibble n of half h -> the signed byte 16 (n - 8): the nibble moved to the byte's high half (h = 0
+    // shifts the low nibbles up, h = 1 masks the high ones in place), and flipping bit 7 subtracts 128
+    // without a borrow into the next byte: three operations per word instead of the four of n - 8.  The
+    // block sums come out 16 times the exact ones (|16 sum| < 2^20, exact in fp32), and the scale below
+    // carries the exact 1/16.
+    __device__ static uint32_t s16(uint32_t v, int sh) { return ((v << sh) & 0xF0F0F0F0u) ^ 0x80808080u; }
     __device__ static uint4 bop(const Raw& c, int j, int h) {
         const uint4 v = c.q[j];
-        const int sh = h * 4;
-        return make_uint4(s8((v.x >> sh) & 0x0F0F0F0Fu), s8((v.y >> sh) & 0x0F0F0F0Fu), s8((v.z >> sh) & 0x0F0F0F0Fu),
-                          s8((v.w >> sh) & 0x0F0F0F0Fu));
+        const int sh = 4 - h * 4;
+        return make_uint4(s16(v.x, sh), s16(v.y, sh), s16(v.z, sh), s16(v.w, sh));
     }
     __device__ static void scales(const Raw& c, int j, float& rs, float& rmin) {
-        rs = f16_to_f32(c.d[j] & 0xFFFFu);
+        rs = f16_to_f32(c.d[j] & 0xFFFFu) * 0.0625f;
         rmin = 0.0f;
     }
     struct Scl {};
