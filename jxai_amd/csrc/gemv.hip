@@ -1852,7 +1852,8 @@ static bool down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, 
             // plus the tiles' partial sums)
             constexpr int MR = mx_mr_max<TYPE, false>();
             if constexpr (MR > 1) {
-                if (dn.nrt * slots >= MX_MR_MIN_ITEMS) {
+                // (slots 0 with sh: the shared down alone, its K in parts)
+                if (dn.nrt * slots >= MX_MR_MIN_ITEMS || (sh && slots == 0)) {
                     // the shared down's blocks join (its K in parts of at most a routed block's units) where it
                     // has this launch's weight format and Q8_0 h
                     const bool shm = sh && sh->slots > 0 && sh->g.type == TYPE && sh->hq.q != nullptr &&

@@ -324,6 +324,7 @@ struct jx_moe_layer {
     uint32_t dec_epoch = 0;
     int shparts_cap = 1;  // K parts of the shared down's output the workspace holds (ysh)
     int cold_pairs = 0;   // experts under this many pairs take the GEMVs in the matrix-core regime (0: none)
+    bool sh_ksplit = true;  // JX_SH_KSPLIT=0: the standalone shared down in one part (A/B measurement)
     bool fused_decode = true;
     bool force_fused = false;  // JX_FUSED=1: also where the separate launches measured faster
     int smfma_min = 0;         // shared expert's GEMM threshold (JX_SMFMA_MIN overrides it: A/B)
@@ -752,6 +753,10 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
                        L->sup.m.type == L->up.m.type &&
                        jx::gemv_gateup_joins(L->gate.m.type, L->gate.m.nrt, slots, tb, L->sgate.m.nrt, sslots);
     int shparts = 1;  // K parts of the shared down's output (the combine adds them)
+    // A standalone shared down of at least 4 routed K's (Qwen1.5-shaped: 5632 against 1408) in K parts;
+    // measured per step, weights from HBM: 48 / 64 tokens 133.6 / 138.8 -> 127.2 / 137.3 us.  Two parts
+    // (DeepSeek-V2-Lite-shaped 2816 against 1408) measured slower: 32 tokens 132.5 -> 135.7 us.
+    const bool sh_ksplit = L->shared && !smfma_dn && tbs == 16 && !L->sdown_f32 && L->shparts_cap >= 4 && L->sh_ksplit;
     auto shared_gateup = [&](hipStream_t ss) {
         if (smfma_gu) {
             Launch l(L, "shared_gateup_mfma", ss);
@@ -771,6 +776,22 @@ int run_forward(jx_moe_layer* L, const float* xdev, int n, float* outdev, hipStr
             else
                 jx::launch_q8_to_acth(L->hqs, n, L->hhs.a, ss, false);
             jx::launch_mfma_down(L->sdown.m, L->hhs.a, sg, st_ub, L->ysh, ss);
+        } else if (sh_ksplit) {
+            // the dense shared down's long K in parts, each block a routed block's share of units (the
+            // combine adds the parts), so it is done before the routed gate/up that the routed down
+            // waits on with it
+            jx::SharedPart sp;
+            sp.g = L->sdown.m;
+            sp.grp = sg;
+            sp.slots = sslots;
+            sp.hq = L->hqs;
+            sp.y = L->ysh;
+            sp.kparts = L->shparts_cap;
+            Launch l(L, "shared_down_kparts", ss);
+            if (jx::launch_gemv_down(L->sdown.m, L->hqs, nullptr, 0, sg, 0, tbs, L->ysh, ss, jx::CombineOut{}, &sp))
+                shparts = sp.kparts;
+            else
+                jx::launch_gemv_down(L->sdown.m, L->hqs, nullptr, 0, sg, sslots, tbs, L->ysh, ss);
         } else {
             Launch l(L, "shared_down", ss);
             jx::launch_gemv_down(L->sdown.m, L->hqs, L->sdown_f32 ? L->hfs : nullptr, (int)fspad, sg, sslots, tbs, L->ysh,
@@ -1111,6 +1132,7 @@ int jx_moe_layer_create(const jx_moe_layer_desc* D, jx_moe_layer** out) {
     if (const char* f = std::getenv("JX_FUSED")) L->force_fused = std::strcmp(f, "0") != 0;
     if (const char* f = std::getenv("JX_DECP")) L->decp_mode = std::strcmp(f, "0") != 0 ? 1 : 0;
     L->cold_pairs = COLD_PAIRS;
+    if (const char* f = std::getenv("JX_SH_KSPLIT")) L->sh_ksplit = std::strcmp(f, "0") != 0;
     if (const char* f = std::getenv("JX_COLD_PAIRS")) L->cold_pairs = std::max(0, std::atoi(f));
     L->smfma_min = (L->shared && (L->sgate.m.type == jx::T_Q4_K || L->sgate.m.type == jx::T_Q6_K))
                        ? jx::MFMA_MIN_SHARED_TOKENS_KQ
