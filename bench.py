@@ -322,8 +322,8 @@ def main():
         copy_calibration()
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (experts would shard by "
-              "expert parallelism, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: there is no multi-GPU path (the experts would shard by expert "
+              "parallelism, whole experts per GPU); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     steps = max(args.steps, 1)
 

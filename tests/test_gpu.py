@@ -1,6 +1,6 @@
 """GPU parity of the HIP MoE path against the oracle and the golden vectors.
 
-Bar (BASELINE north star): expert ids, top-k order and per-expert counts
+Bar: expert ids, top-k order and per-expert counts
 bit-exact; Q8_0 activations bit-exact; layer outputs within max relative error
 1e-3 per token (||y_gpu - y_ref||_inf / ||y_ref||_inf) of the reference CPU
 path; softmax weights within 2e-6 relative (the GPU's expf and glibc's may
