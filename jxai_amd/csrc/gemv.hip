@@ -1318,10 +1318,14 @@ k_gemv_mxt(QMat W0r, QMat W1r, ActQ8 actr, Groups grpr, ActQ8 hqr, float* hfr, i
     float* const hf = shb ? sh.hf : hfr;
     const int hf_ld = shb ? sh.hf_ld : hf_ldr;
     float* const y = shb ? sh.y + (size_t)kp * sh.grp.n_tok * W0.rows : yr;
-    // one pass of up to MX_NT tokens; HI8: tokens 8.. present (D registers 4-7 carry results), a
-    // compile-time switch (as a runtime one it branched around single LDS reads and moves)
-    auto pass = [&](int tb0, int nt, auto hi8c) {
-        constexpr bool HI8 = decltype(hi8c)::value;
+    // one pass of up to MX_NT tokens.  R: result registers per lane, a compile-time switch (as a runtime
+    // one it branched around single LDS reads and moves).  Token t of the pass sits in A row
+    // 4 (t / R) + t % R for R <= 4 (8: rows t), so that lane-half h holds tokens hR .. hR + R - 1 in
+    // D registers 0 .. R - 1: passes of at most 2 / 4 tokens scale 1 / 2 registers per block, not 4
+    auto pass = [&](int tb0, int nt, auto rc) {
+        constexpr int R = decltype(rc)::value;
+        constexpr bool HI8 = R == 8;
+        constexpr int NREG = R == 8 ? 8 : R;
         // every tile's first unit goes out first: the weights need only the expert, while the activations
         // wait on the token list (the pair table) and the scales on both (tiles past the matrix load the
         // last one; their results are dropped)
@@ -1336,8 +1340,10 @@ k_gemv_mxt(QMat W0r, QMat W1r, ActQ8 actr, Groups grpr, ActQ8 hqr, float* hfr, i
         static_assert((WAVES * 64) % MX_NT == 0, "one token per thread");
         const int tk = tid % MX_NT;
         const size_t srow = tk < nt ? src(tk) * (size_t)KB : 0;
-        // A row of this lane: token m; lanes past the pass's tokens read token 0 (their D rows are dropped)
-        const int8_t* arow = act.q + src(m < nt ? m : 0) * (size_t)K + 16 * h;
+        // A row m of this lane: its token (rows that hold none, and tokens past the pass, read token 0:
+        // their D rows are dropped)
+        const int ta = R >= 4 ? m : ((m & 3) < R && m < 8 ? (m >> 2) * R + (m & 3) : 0);
+        const int8_t* arow = act.q + src(ta < nt ? ta : 0) * (size_t)K + 16 * h;
         float acc[MR][MX_NT / 2];
 #pragma unroll
         for (int j = 0; j < MR; ++j)
@@ -1405,15 +1411,33 @@ k_gemv_mxt(QMat W0r, QMat W1r, ActQ8 actr, Groups grpr, ActQ8 hqr, float* hfr, i
                 const int b = u * BPU + j;
                 float rs, rmin;
                 X::scale(scl, wr, j, rs, rmin);
-                // tokens of registers 0-3: 4h..4h+3, of 4-7: 8+4h..11+4h (only when the pass has them)
-                const float4* sp = reinterpret_cast<const float4*>(msc + (b - kb0) * MX_NT + 4 * h);
-                const float4 s0 = sp[0], s1 = sp[1];
-                const float4 s2 = HI8 ? sp[4] : s0, s3 = HI8 ? sp[5] : s1;
-                const float sx[8] = {s0.x, s0.z, s1.x, s1.z, s2.x, s2.z, s3.x, s3.z};
-                const float sy[8] = {s0.y, s0.w, s1.y, s1.w, s2.y, s2.w, s3.y, s3.w};
+                // tokens of registers 0-3: 4h..4h+3, of 4-7: 8+4h..11+4h (R = 8); hR..hR+R-1 (R <= 4)
+                float sx[8], sy[8];
+                if constexpr (R >= 4) {
+                    const float4* sp = reinterpret_cast<const float4*>(msc + (b - kb0) * MX_NT + 4 * h);
+                    const float4 s0 = sp[0], s1 = sp[1];
+                    const float4 s2 = HI8 ? sp[4] : s0, s3 = HI8 ? sp[5] : s1;
+                    const float ux[8] = {s0.x, s0.z, s1.x, s1.z, s2.x, s2.z, s3.x, s3.z};
+                    const float uy[8] = {s0.y, s0.w, s1.y, s1.w, s2.y, s2.w, s3.y, s3.w};
+#pragma unroll
+                    for (int r = 0; r < 8; ++r) {
+                        sx[r] = ux[r];
+                        sy[r] = uy[r];
+                    }
+                } else if constexpr (R == 2) {
+                    const float4 s0 = *reinterpret_cast<const float4*>(msc + (b - kb0) * MX_NT + 2 * h);
+                    sx[0] = s0.x;
+                    sy[0] = s0.y;
+                    sx[1] = s0.z;
+                    sy[1] = s0.w;
+                } else {
+                    const float2 s0 = msc[(b - kb0) * MX_NT + h];
+                    sx[0] = s0.x;
+                    sy[0] = s0.y;
+                }
 #pragma unroll
                 for (int r = 0; r < MX_NT / 2; ++r) {
-                    if (r >= 4 && !HI8) break;
+                    if (r >= NREG) break;
                     if constexpr (TYPE == T_Q4_K || TYPE == T_Q5_K) {
                         ac[r] = __builtin_fmaf(rs * sx[r], (float)Dj[r], ac[r]);
                         ac[r] = __builtin_fmaf(rmin, sy[r], ac[r]);
@@ -1447,15 +1471,15 @@ k_gemv_mxt(QMat W0r, QMat W1r, ActQ8 actr, Groups grpr, ActQ8 hqr, float* hfr, i
 #pragma unroll
         for (int j = 0; j < MR; ++j)
 #pragma unroll
-            for (int r = 0; r < MX_NT / 2; ++r) red[j][wave][r][lane] = acc[j][r];
+            for (int r = 0; r < NREG; ++r) red[j][wave][r][lane] = acc[j][r];
         __syncthreads();
-        // result register r holds tokens 4h + r (r < 4) and 8 + 4h + r - 4 (r >= 4): only the registers whose
-        // lane-half-0 token exists carry results; each (tile, register) is finished by one wave, the waves
-        // in turn
-        const int nr = nt > 8 ? 4 + min(4, nt - 8) : min(4, nt);
+        // result register r holds tokens 4h + r (r < 4) and 8 + 4h + r - 4 (r >= 4) (R = 8), hR + r (R <= 4):
+        // only the registers whose lane-half-0 token exists carry results; each (tile, register) is finished
+        // by one wave, the waves in turn
+        const int nr = R == 8 ? 4 + min(4, nt - 8) : min(R, nt);
         for (int q = wave; q < nj * nr; q += WAVES) {  // wave-uniform
             const int j = q / nr, r = q - j * nr, rt = rt0 + j;
-            const int t = (r < 4 ? 4 * h + r : 8 + 4 * h + (r - 4));
+            const int t = R == 8 ? (r < 4 ? 4 * h + r : 8 + 4 * h + (r - 4)) : h * R + r;
             float v0 = 0.0f, v1 = 0.0f;
 #pragma unroll
             for (int w = 0; w < HW; ++w) v0 += red[j][w][r][lane];
@@ -1474,8 +1498,17 @@ k_gemv_mxt(QMat W0r, QMat W1r, ActQ8 actr, Groups grpr, ActQ8 hqr, float* hfr, i
     for (int tb0 = 0; tb0 < cnt; tb0 += MX_NT) {
         const int nt = min(MX_NT, cnt - tb0);
         if (tb0) __syncthreads();  // the previous pass is done with msc and red
-        if (nt > 8) pass(tb0, nt, std::integral_constant<bool, true>{});
-        else pass(tb0, nt, std::integral_constant<bool, false>{});
+        if (nt > 8) {
+            pass(tb0, nt, std::integral_constant<int, 8>{});
+        } else if constexpr (TYPE == T_Q4_0) {
+            // (Qwen1.5-shaped 16 / 64 tokens 106.4 / 137.2 -> 104.1 / 135.4 us; with the other formats'
+            // passes the Q4_K gate/up spilled and ran slower, Q8_0 gained nothing)
+            if (nt > 4) pass(tb0, nt, std::integral_constant<int, 4>{});
+            else if (nt > 2) pass(tb0, nt, std::integral_constant<int, 2>{});
+            else pass(tb0, nt, std::integral_constant<int, 1>{});
+        } else {
+            pass(tb0, nt, std::integral_constant<int, 4>{});
+        }
     }
 }
 
