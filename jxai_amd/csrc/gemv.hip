@@ -1396,45 +1396,60 @@ k_gemv_mxt(QMat W0r, QMat W1r, ActQ8 actr, Groups grpr, ActQ8 hqr, float* hfr, i
                                                           __builtin_bit_cast(v4i_t, bw), v16i_t{}, 0, 0, 0);
             }
         };
+        // the tokens' (scale, sum) of block b for the pass's result registers: registers 0-3 hold tokens
+        // 4h..4h+3, 4-7 hold 8+4h..11+4h (R = 8); hR..hR+R-1 (R <= 4)
+        auto ldsx = [&](int b, float(&sx)[8], float(&sy)[8]) {
+            if constexpr (R >= 4) {
+                const float4* sp = reinterpret_cast<const float4*>(msc + (b - kb0) * MX_NT + 4 * h);
+                const float4 s0 = sp[0], s1 = sp[1];
+                const float4 s2 = HI8 ? sp[4] : s0, s3 = HI8 ? sp[5] : s1;
+                const float ux[8] = {s0.x, s0.z, s1.x, s1.z, s2.x, s2.z, s3.x, s3.z};
+                const float uy[8] = {s0.y, s0.w, s1.y, s1.w, s2.y, s2.w, s3.y, s3.w};
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    sx[r] = ux[r];
+                    sy[r] = uy[r];
+                }
+            } else if constexpr (R == 2) {
+                const float4 s0 = *reinterpret_cast<const float4*>(msc + (b - kb0) * MX_NT + 2 * h);
+                sx[0] = s0.x;
+                sy[0] = s0.y;
+                sx[1] = s0.z;
+                sy[1] = s0.w;
+            } else {
+                const float2 s0 = msc[(b - kb0) * MX_NT + h];
+                sx[0] = s0.x;
+                sy[0] = s0.y;
+            }
+        };
         auto accum = [&](const Raw& wr, const uint4(&a)[BPU], int u, float(&ac)[MX_NT / 2]) {
             const auto scl = X::prep(wr);
             // the unit's blocks in range: K-quant units are whole super-blocks; the others end at KB
             const int nbk = is_kquant(TYPE) ? BPU : min(BPU, KB - u * BPU);  // wave-uniform
+            // PIPE: block j + 1's product and its tokens' scales go out before block j's scaling, so that
+            // neither the matrix core's latency nor the LDS read sits between one block's scaling and the
+            // next (left to itself, the scheduler issued the product after the scaling).  Not Q4_K, whose
+            // gate/up then spilled.
+            constexpr bool PIPE = TYPE != T_Q4_K;
             v16i_t D[2], D2[2];
+            float sxb[2][8], syb[2][8];
             mfma(wr, a, 0, D[0], D2[0]);
+            if constexpr (PIPE) ldsx(u * BPU, sxb[0], syb[0]);
 #pragma unroll
             for (int j = 0; j < BPU; ++j) {
                 if (j >= nbk) break;
-                if (j + 1 < BPU && j + 1 < nbk) mfma(wr, a, j + 1, D[(j + 1) & 1], D2[(j + 1) & 1]);
+                if (j + 1 < BPU && j + 1 < nbk) {
+                    mfma(wr, a, j + 1, D[(j + 1) & 1], D2[(j + 1) & 1]);
+                    if constexpr (PIPE) ldsx(u * BPU + j + 1, sxb[(j + 1) & 1], syb[(j + 1) & 1]);
+                }
+                if constexpr (PIPE) __builtin_amdgcn_sched_barrier(0);
+                else ldsx(u * BPU + j, sxb[j & 1], syb[j & 1]);
                 const v16i_t& Dj = D[j & 1];
                 const v16i_t& D2j = D2[j & 1];
-                const int b = u * BPU + j;
+                const float(&sx)[8] = sxb[j & 1];
+                const float(&sy)[8] = syb[j & 1];
                 float rs, rmin;
                 X::scale(scl, wr, j, rs, rmin);
-                // tokens of registers 0-3: 4h..4h+3, of 4-7: 8+4h..11+4h (R = 8); hR..hR+R-1 (R <= 4)
-                float sx[8], sy[8];
-                if constexpr (R >= 4) {
-                    const float4* sp = reinterpret_cast<const float4*>(msc + (b - kb0) * MX_NT + 4 * h);
-                    const float4 s0 = sp[0], s1 = sp[1];
-                    const float4 s2 = HI8 ? sp[4] : s0, s3 = HI8 ? sp[5] : s1;
-                    const float ux[8] = {s0.x, s0.z, s1.x, s1.z, s2.x, s2.z, s3.x, s3.z};
-                    const float uy[8] = {s0.y, s0.w, s1.y, s1.w, s2.y, s2.w, s3.y, s3.w};
-#pragma unroll
-                    for (int r = 0; r < 8; ++r) {
-                        sx[r] = ux[r];
-                        sy[r] = uy[r];
-                    }
-                } else if constexpr (R == 2) {
-                    const float4 s0 = *reinterpret_cast<const float4*>(msc + (b - kb0) * MX_NT + 2 * h);
-                    sx[0] = s0.x;
-                    sy[0] = s0.y;
-                    sx[1] = s0.z;
-                    sy[1] = s0.w;
-                } else {
-                    const float2 s0 = msc[(b - kb0) * MX_NT + h];
-                    sx[0] = s0.x;
-                    sy[0] = s0.y;
-                }
 #pragma unroll
                 for (int r = 0; r < MX_NT / 2; ++r) {
                     if (r >= NREG) break;
