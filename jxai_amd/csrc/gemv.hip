@@ -1922,10 +1922,21 @@ static bool down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, 
                                            y, SmallTail{}, sp);
                     };
                     const bool lds2 = 2 * (lds + mx_red_bytes<4, MR>()) <= (size_t)160 * 1024;
-                    if (2 * nb < num_cus() || !lds2)
+                    // Fewer waves per block where the CU's LDS holds the extra blocks: the same waves per CU, each
+                    // with more of its block's units behind one round trip for the first (Q4_0: one wave,
+                    // Qwen1.5-shaped 48 / 64 tokens 125.1 / 133.8 -> 119.2 / 129.1 us per step; Q8_0: two,
+                    // Qwen3-shaped 32 tokens 100.0 -> 98.0 us, one wave measured 104.6)
+                    const bool lds_w1 = 8 * (lds + mx_red_bytes<1, MR>()) <= (size_t)160 * 1024;
+                    const bool lds_w2 = 4 * (lds + mx_red_bytes<2, MR>()) <= (size_t)160 * 1024;
+                    if (2 * nb < num_cus() || !lds2) {
                         go(k_gemv_mxt<TYPE, false, 8, MR>, 8);
-                    else
+                    } else if constexpr (TYPE == T_Q4_0 || TYPE == T_Q8_0) {
+                        constexpr int FW = TYPE == T_Q4_0 ? 1 : 2;
+                        if (FW == 1 ? lds_w1 : lds_w2) go(k_gemv_mxt<TYPE, false, FW, MR>, FW);
+                        else go(k_gemv_mxt<TYPE, false, 4, MR>, 4);
+                    } else {
                         go(k_gemv_mxt<TYPE, false, 4, MR>, 4);
+                    }
                     return shm;
                 }
             }
