@@ -1606,11 +1606,13 @@ template <int TYPE>
 constexpr int mxh_mr() { return TYPE == T_Q5_0 ? 2 : 3; }  // Q5_0: three units of 24 registers spill
 constexpr int MXH_WAVES = 4;
 // Dynamic LDS of one block: the staged tokens (fp16 rows of K + 8) and, for K-quants, the blocks' sums.
-__host__ __device__ inline size_t mxh_lds(int K, bool kq) {
-    return (size_t)MX_NT * (K + 8) * 2 + (kq ? (size_t)(K / 32) * MX_NT * sizeof(float) : 0);
+__host__ __device__ inline size_t mxh_lds(int K, bool kq, int ntp = MX_NT) {
+    return (size_t)ntp * (K + 8) * 2 + (kq ? (size_t)(K / 32) * ntp * sizeof(float) : 0);
 }
 
-template <int TYPE, int WAVES, int MR>
+// NTP: tokens per pass, 16 or 8 (8: half the staged rows and no registers for tokens 8-15, so the build fits
+// 3 waves per SIMD; groups of more tokens take more passes)
+template <int TYPE, int WAVES, int MR, int NTP>
 __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
 k_gemv_mxh(QMat W, ActH hin, Groups grp, float* y) {
     using X = Mh<TYPE>;
@@ -1628,8 +1630,8 @@ k_gemv_mxh(QMat W, ActH hin, Groups grp, float* y) {
     const int tid = threadIdx.x, lane = tid & 63, m = lane & 31, h = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = hin.K, KB = K / 32, KH = hin.KH, AS = K + 8;
-    _Float16* As = reinterpret_cast<_Float16*>(mxh_lds_base);                    // [MX_NT][AS]: h * 2^-E
-    float* Ss = reinterpret_cast<float*>(mxh_lds_base + (size_t)MX_NT * AS * 2);  // [KB][MX_NT]: sums
+    _Float16* As = reinterpret_cast<_Float16*>(mxh_lds_base);                  // [NTP][AS]: h * 2^-E
+    float* Ss = reinterpret_cast<float*>(mxh_lds_base + (size_t)NTP * AS * 2);  // [KB][NTP]: sums
     const int nu = X::units(W);
     const h2v c1 = h2v{(_Float16)1.0f, (_Float16)1.0f}, c0 = h2v{(_Float16)X::C0, (_Float16)X::C0};
     auto pass = [&](int tb0, int nt, auto hi8c) {
@@ -1641,26 +1643,26 @@ k_gemv_mxh(QMat W, ActH hin, Groups grp, float* y) {
         // the tokens' rows of the hi form (zero rows past the pass), four 16-byte loads in flight per thread
         const size_t row0 = (size_t)(p0 + tb0);
         const int c8 = K / 8;
-        for (int i0 = tid; i0 < MX_NT * c8; i0 += 4 * NTH) {
+        for (int i0 = tid; i0 < NTP * c8; i0 += 4 * NTH) {
             uint4 v[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int i = i0 + q * NTH, t = i / c8, k = 8 * (i - t * c8);
-                v[q] = (i < MX_NT * c8 && t < nt)
+                v[q] = (i < NTP * c8 && t < nt)
                            ? *reinterpret_cast<const uint4*>(hin.hl + (row0 + t) * (size_t)KH * 256 + (k >> 7) * 256 + (k & 127))
                            : make_uint4(0u, 0u, 0u, 0u);
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int i = i0 + q * NTH, t = i / c8, k = 8 * (i - t * c8);
-                if (i < MX_NT * c8) *reinterpret_cast<uint4*>(As + t * AS + k) = v[q];
+                if (i < NTP * c8) *reinterpret_cast<uint4*>(As + t * AS + k) = v[q];
             }
         }
         if (tid < MX_NT) spe[tid] = tid < nt ? hin.pe[(row0 + tid) * KH] : 0.0f;
         if constexpr (X::MIN) {
             // each block's fp32 sum of h * 2^-E from its three exact bf16 pieces
-            for (int i = tid; i < KB * MX_NT; i += NTH) {
-                const int b = i / MX_NT, t = i - b * MX_NT;
+            for (int i = tid; i < KB * NTP; i += NTH) {
+                const int b = i / NTP, t = i - b * NTP;
                 float s = 0.0f;
                 if (t < nt) {
                     const uint16_t* xp = hin.xm + (row0 + t) * (size_t)hin.KU * 24 + (b >> 3) * 24 + (b & 7);
@@ -1676,8 +1678,8 @@ k_gemv_mxh(QMat W, ActH hin, Groups grp, float* y) {
         for (int j = 0; j < MR; ++j)
 #pragma unroll
             for (int r = 0; r < MX_NT / 2; ++r) acc[j][r] = 0.0f;
-        // A rows: token m % 16 (rows 16-31 repeat 0-15; their D rows are not used)
-        const _Float16* arow = As + (m & 15) * AS + 16 * h;
+        // A rows: token m % NTP (rows NTP-31 repeat 0..NTP-1; their D rows are not used)
+        const _Float16* arow = As + (m & (NTP - 1)) * AS + 16 * h;
         for (int u = wave; u < nu; u += WAVES) {
 #pragma unroll
             for (int j = 0; j < MR; ++j) {
@@ -1696,8 +1698,8 @@ k_gemv_mxh(QMat W, ActH hin, Groups grp, float* y) {
                     // tokens of registers 0-3: 4h..4h+3, of 4-7: 8+4h..11+4h
                     float sy[8] = {0, 0, 0, 0, 0, 0, 0, 0};
                     if constexpr (X::MIN) {
-                        const float4 s0 = *reinterpret_cast<const float4*>(Ss + b * MX_NT + 4 * h);
-                        const float4 s1 = HI8 ? *reinterpret_cast<const float4*>(Ss + b * MX_NT + 8 + 4 * h) : s0;
+                        const float4 s0 = *reinterpret_cast<const float4*>(Ss + b * NTP + 4 * h);
+                        const float4 s1 = HI8 ? *reinterpret_cast<const float4*>(Ss + b * NTP + 8 + 4 * h) : s0;
                         sy[0] = s0.x; sy[1] = s0.y; sy[2] = s0.z; sy[3] = s0.w;
                         sy[4] = s1.x; sy[5] = s1.y; sy[6] = s1.z; sy[7] = s1.w;
                     }
@@ -1727,11 +1729,15 @@ k_gemv_mxh(QMat W, ActH hin, Groups grp, float* y) {
             if (t < nt) y[(row0 + t) * W.rows + rt * 32 + m] = v0 * spe[t];
         }
     };
-    for (int tb0 = 0; tb0 < cnt; tb0 += MX_NT) {
-        const int nt = min(MX_NT, cnt - tb0);
+    for (int tb0 = 0; tb0 < cnt; tb0 += NTP) {
+        const int nt = min(NTP, cnt - tb0);
         if (tb0) __syncthreads();  // the previous pass is done with the staged tokens, spe and red
-        if (nt > 8) pass(tb0, nt, std::integral_constant<bool, true>{});
-        else pass(tb0, nt, std::integral_constant<bool, false>{});
+        if constexpr (NTP > 8) {
+            if (nt > 8) pass(tb0, nt, std::integral_constant<bool, true>{});
+            else pass(tb0, nt, std::integral_constant<bool, false>{});
+        } else {
+            pass(tb0, nt, std::integral_constant<bool, false>{});
+        }
     }
 }
 
@@ -2843,14 +2849,30 @@ bool gemv_down_f16_fits(int type, int K) {
 
 void launch_gemv_down_f16(const QMat& dn, const ActH& hh, const Groups& grp, int slots, float* y, hipStream_t st) {
     const int K = hh.K;
-    auto go = [&](auto kern, int mr, bool kq) {
-        const size_t lds = mxh_lds(K, kq);
-        lds_optin(kern, lds);
-        hipLaunchKernelGGL(kern, dim3((dn.nrt + mr - 1) / mr * slots), dim3(MXH_WAVES * 64), lds, st, dn, hh, grp, y);
+    // 8-token passes up to 4 pairs per expert slot on average (DeepSeek-V2-Lite-shaped 16 / 32 tokens
+    // 112.9 / 131.4 -> 109.1 / 123.8 us per step, Q4_K_M mix at 32 tokens 132.6 -> 124.5 us); beyond, the
+    // groups' second passes cost more (64 / 96 tokens 149.8 / 193.4 -> 151.5 / 203.6 us)
+    const int ntp = (size_t)grp.n_tok * grp.top_k <= (size_t)4 * slots ? 8 : MX_NT;
+    auto go = [&](auto k8, auto k16, int mr, bool kq) {
+        const size_t lds = mxh_lds(K, kq, ntp);
+        const dim3 grid((dn.nrt + mr - 1) / mr * slots), blk(MXH_WAVES * 64);
+        if (ntp == 8) {
+            lds_optin(k8, lds);
+            hipLaunchKernelGGL(k8, grid, blk, lds, st, dn, hh, grp, y);
+        } else {
+            lds_optin(k16, lds);
+            hipLaunchKernelGGL(k16, grid, blk, lds, st, dn, hh, grp, y);
+        }
     };
     switch (dn.type) {
-        case T_Q4_K: go(k_gemv_mxh<T_Q4_K, MXH_WAVES, mxh_mr<T_Q4_K>()>, mxh_mr<T_Q4_K>(), true); break;
-        case T_Q5_0: go(k_gemv_mxh<T_Q5_0, MXH_WAVES, mxh_mr<T_Q5_0>()>, mxh_mr<T_Q5_0>(), false); break;
+        case T_Q4_K:
+            go(k_gemv_mxh<T_Q4_K, MXH_WAVES, mxh_mr<T_Q4_K>(), 8>, k_gemv_mxh<T_Q4_K, MXH_WAVES, mxh_mr<T_Q4_K>(), MX_NT>,
+               mxh_mr<T_Q4_K>(), true);
+            break;
+        case T_Q5_0:
+            go(k_gemv_mxh<T_Q5_0, MXH_WAVES, mxh_mr<T_Q5_0>(), 8>, k_gemv_mxh<T_Q5_0, MXH_WAVES, mxh_mr<T_Q5_0>(), MX_NT>,
+               mxh_mr<T_Q5_0>(), false);
+            break;
         default: break;
     }
 }

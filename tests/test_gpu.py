@@ -207,6 +207,28 @@ def test_cold_experts_split(moe, port, monkeypatch, cold):
     assert err <= REL_TOL
 
 
+@pytest.mark.parametrize("down", [F.Q4_K, F.Q5_0])
+def test_fp16_down_passes_of_8(moe, port, down):
+    """The multi-token down over fp32 h (d_ff 1408: no Q8_0 form of h for these formats) takes passes of 8
+    tokens where the launch averages at most 4 pairs per expert slot; under Zipf routing some experts then
+    hold more than 8 tokens and take several passes.  Routing exact, every token within the bar."""
+    cfg = synth.LayerConfig(f"zipf_f32dn_{down}", 512, 32, 4, 1408, F.Q4_K, down_wtype=down, zipf_gamma=1.2)
+    lw = synth.make_layer(cfg)
+    L = moe.MoELayer.from_weights(lw)
+    n = 24
+    say(f"{cfg.name} n={n} gemv")
+    x = synth.make_tokens(cfg, n, seed=3)
+    out, ids, w, counts = L.forward(x, regime="gemv")
+    L.close()
+    nk = n * cfg.top_k
+    assert nk <= 4 * min(cfg.n_experts, nk) and counts.max() > 8, counts  # the case under test
+    lg_o, ids_o, w_o = port.route(lw, x)
+    assert np.array_equal(ids, ids_o)
+    err = rel_err(out, port.moe_forward(lw, x, np.arange(n, dtype=np.int32))[0])
+    say(f"{cfg.name}: max count {counts.max()}, max rel err {err:.2e}")
+    assert err <= REL_TOL
+
+
 @pytest.mark.parametrize("name", ["mixtral", "qwen3moe", "qwen15moe", "dsv2lite"])
 def test_odd_token_counts(moe, port, name):
     """The library's own regime choice at token counts that fill no tile, group or block evenly."""
