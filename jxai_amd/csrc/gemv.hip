@@ -1919,7 +1919,9 @@ static bool down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, 
                     if (shm) {
                         constexpr int BPU = Mx<TYPE>::BPU;
                         const int ub = (sp.hq.K / 32 + BPU - 1) / BPU, upp = (ub + sp.kparts - 1) / sp.kparts;
-                        lds = std::max(lds, (size_t)upp * BPU * MX_NT * sizeof(float2));
+                        // a K part stages only its own blocks' token scales; with no routed blocks that is all
+                        const size_t lp = (size_t)upp * BPU * MX_NT * sizeof(float2);
+                        lds = rb == 0 ? lp : std::max(lds, lp);
                     }
                     const int nb = rb + (shm ? (sp.g.nrt + MR - 1) / MR * sp.slots * sp.kparts : 0);
                     auto go = [&](auto kern, int waves) {
@@ -1936,9 +1938,12 @@ static bool down_t(const QMat& dn, const ActQ8& hq, const float* hf, int hf_ld, 
                     const bool lds_w2 = 4 * (lds + mx_red_bytes<2, MR>()) <= (size_t)160 * 1024;
                     if (2 * nb < num_cus() || !lds2) {
                         go(k_gemv_mxt<TYPE, false, 8, MR>, 8);
-                    } else if constexpr (TYPE == T_Q4_0 || TYPE == T_Q8_0) {
-                        constexpr int FW = TYPE == T_Q4_0 ? 1 : 2;
-                        if (FW == 1 ? lds_w1 : lds_w2) go(k_gemv_mxt<TYPE, false, FW, MR>, FW);
+                    } else if constexpr (TYPE == T_Q4_0) {
+                        if (lds_w1) go(k_gemv_mxt<TYPE, false, 1, MR>, 1);
+                        else if (lds_w2) go(k_gemv_mxt<TYPE, false, 2, MR>, 2);
+                        else go(k_gemv_mxt<TYPE, false, 4, MR>, 4);
+                    } else if constexpr (TYPE == T_Q8_0) {
+                        if (lds_w2) go(k_gemv_mxt<TYPE, false, 2, MR>, 2);
                         else go(k_gemv_mxt<TYPE, false, 4, MR>, 4);
                     } else {
                         go(k_gemv_mxt<TYPE, false, 4, MR>, 4);
